@@ -1,0 +1,197 @@
+"""Benchmark of the ELARA sparse-update hot path on one MI355X.
+
+Step (the headline, BASELINE metric "sparse-Adam+replay rows/s at d=128"): config C2's 262,144 logged rows at
+D=128 (c ~ U{1,2,3} gradients each, steps with gaps U{1..50}) are materialised by exact replay (init + c Adam steps,
+elr_replay_rows) and then take this step's row-sparse Adam update with a fresh gradient (elr_adam_rows) -- the
+executor's path for logged rows (srm2/elara.py:485, 514).  Inputs are resident in HBM before timing starts.
+value = rows per second over the K timed steps.
+
+roofline: the dominant kernel (replay) -- algorithmic bytes per launch / its mean duration from HIP events
+recorded on the launch stream; peak 8 TB/s.  cpu_baseline: the CPU oracle's replay + Adam (a C port of the
+reference CPU path, same thread split) on a bounded sample, timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode headline|copy] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = 'sparse-Adam+replay rows/s at d=128; achieved HBM GB/s vs ~8 TB/s peak'
+HBM_PEAK_GBS = 8000.0
+
+
+def replay_bytes(n, K, D, nlog):
+    """Algorithmic bytes of one replay launch: per row id 8 + offs 8 + steps 4K + cnt 4 + write 12D; per log
+    entry 4D."""
+    return n * (8 + 8 + 4 * K + 4 + 12 * D) + nlog * 4 * D
+
+
+def adam_bytes(n, D, idx_bytes=8):
+    """Algorithmic bytes of one Adam launch: read w,m,v,g + write w,m,v (28D) + the slot id, per row."""
+    return n * (28 * D + idx_bytes)
+
+
+def cpu_sample_baseline(w, D, K, seed, bound, table_np, threads, pass_s=2.5):
+    """Time the oracle's replay + Adam (kind 'port': the C restatement of the reference CPU path with its
+    contiguous-chunk thread split) on a bounded sample of the workload.  The sample starts at 16,384 rows and
+    grows up to the whole step; each of 1 warm-up + 3 timed passes repeats the sample step for >= pass_s seconds
+    (about 10 s of CPU work in all); the median pass rate is reported."""
+    from elara_amd import synth
+    from oracle import oracle as O
+    n = min(w.n, 16_384)
+    rng = np.random.default_rng(5)
+    while True:
+        rows, cnt, steps, offs = w.rows[:n], w.cnt[:n], w.steps[:n], w.offs[:n]
+        nlog = int(cnt.sum())
+        logs = w.logs[:nlog]
+        g = synth.grads(rng, n, D)
+        idx = np.arange(n, dtype=np.int64)
+        sc = O.adam_scalars(*synth.ADAM, w.max_step + 1)
+
+        def once():
+            out = O.replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table_np, nthreads=threads)
+            O.cpu_adam(out, idx, g, sc, threads)
+
+        t0 = time.perf_counter(); once(); dt = time.perf_counter() - t0
+        if dt >= 0.5 or n >= w.n:
+            break
+        n = min(w.n, n * 4)
+    reps = max(1, int(np.ceil(pass_s / max(dt, 1e-6))))
+    rates = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            once()
+        rates.append(n * reps / (time.perf_counter() - t0))
+    rate = float(np.median(rates))
+    per_row = (replay_bytes(n, K, D, int(w.cnt[:n].sum())) + adam_bytes(n, D)) / n
+    return {'value': rate, 'unit': 'rows/s', 'cores': threads, 'kind': 'port',
+            'sample': f'oracle replay (K=3) + cpu_adam of the first {n} of the {w.n} C2 rows at D={D}, repeated '
+                      f'{reps}x per pass, {threads} threads, median of 3 passes after 1 warm-up',
+            'gbs': rate * per_row / 1e9, 'host_cpu': _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def headline(args):
+    import torch
+    from elara_amd import synth
+    from elara_amd.gpu_ops import ScalarTable, replay_rows
+    from elara_amd.ops import gpu_adam
+
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    D, K, seed = 128, 3, 0
+    bound = synth.bound_for(D)
+    w = synth.ReplayLog(n=262_144, D=D, K=K, seed=0)
+    n, nlog = w.n, int(w.cnt.sum())
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    rows, logs, offs, steps, cnt = t(w.rows), t(w.logs), t(w.offs), t(w.steps), t(w.cnt)
+    table = ScalarTable(*synth.ADAM, w.max_step + 1, dev)
+    out = torch.empty(n, 3, D, device=dev)
+    slots = torch.arange(n, device=dev)
+    grad = t(synth.grads(np.random.default_rng(1), n, D))
+    step_t = w.max_step + 1
+    stream = torch.cuda.current_stream(dev)
+
+    def one_step(ev=None):
+        if ev: ev[0].record(stream)
+        replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=out)
+        if ev: ev[1].record(stream)
+        gpu_adam(out, slots, grad, *synth.ADAM, step_t)
+        if ev: ev[2].record(stream)
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one_step(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    rep_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
+    adam_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    rb, ab = replay_bytes(n, K, D, nlog), adam_bytes(n, D)
+    rep_gbs = rb / (rep_ms * 1e-3) / 1e9
+    res = {
+        'metric': METRIC, 'value': n * args.steps / elapsed, 'unit': 'rows/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': elapsed / args.steps * 1e3, 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32', 'data': 'synthetic',
+        'config': {'workload': 'C2 exact replay (262,144 rows x d=128, k~U{1,2,3}, gaps U{1..50}) + one '
+                               'row-sparse Adam step on the materialised rows', 'rows_per_step': n, 'dim': D,
+                   'kmax': K, 'log_entries': nlog, 'parallelism': 'single GPU'},
+        'roofline': {'bound': 'hbm', 'kernel': 'elr::k_replay_v4<3>', 'achieved': rep_gbs, 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': rep_gbs / HBM_PEAK_GBS, 'traffic': _traffic('replay_c2'),
+                     'algorithmic_bytes_per_launch': rb, 'mean_launch_ms': rep_ms},
+        'kernels': {'replay': {'ms': rep_ms, 'GBps': rep_gbs, 'bytes': rb},
+                    'adam': {'ms': adam_ms, 'GBps': ab / (adam_ms * 1e-3) / 1e9, 'bytes': ab,
+                             'frac': ab / (adam_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}},
+        'step_GBps': (rb + ab) / (elapsed / args.steps) / 1e9,
+    }
+    if not args.no_cpu:
+        res['cpu_baseline'] = cpu_sample_baseline(w, D, K, seed, bound, table.t.cpu().numpy(),
+                                                  threads=min(16, os.cpu_count() or 1))
+    return res
+
+
+def _traffic(name):
+    """HBM bytes per launch measured by rocprofv3 PMC passes (committed under profiles/), or None."""
+    p = ROOT / 'profiles' / f'traffic_{name}.json'
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get('bytes_per_launch')
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def copy_calibration(args):
+    """A plain device copy of known size (PMC calibration of FETCH_SIZE / WRITE_SIZE)."""
+    import torch
+    dev = torch.device('cuda:0')
+    nbytes = 1 << 30
+    a = torch.ones(nbytes // 4, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(args.steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    return {'mode': 'copy', 'bytes_read_per_launch': nbytes, 'bytes_written_per_launch': nbytes,
+            'launches': args.steps}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--mode', default='headline', choices=['headline', 'copy'])
+    ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU only: this build has no multi-GPU path (the sharding design is '
+              'described in DESIGN.md); run with --gpus 1', file=sys.stderr)
+        sys.exit(2)
+    res = copy_calibration(args) if args.mode == 'copy' else headline(args)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,70 @@
+"""ctypes binding of libelara_amd.so (the C-ABI declared in include/elara_amd.h).
+
+PyTorch supplies device memory and streams; the kernels are the library's.  There is no fallback: if the
+library is missing, every op raises.  torch is imported before the library is loaded so that the library binds
+to the HIP runtime torch already loaded (same soname), and torch's streams are valid handles for it.
+"""
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / 'libelara_amd.so'
+
+_lib = None
+_lock = threading.Lock()
+
+c_i64, c_i32, c_u32, c_f32, c_f64, c_vp = (ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_float,
+                                           ctypes.c_double, ctypes.c_void_p)
+c_f32p = ctypes.POINTER(ctypes.c_float)
+
+# name -> (restype, argtypes); must match include/elara_amd.h
+SIGNATURES = {
+    'elr_error_string': (ctypes.c_char_p, [ctypes.c_int]),
+    'elr_version': (ctypes.c_int, []),
+    'elr_adam_scalars': (None, [c_f64, c_f64, c_f64, c_f64, c_i64, c_f32p]),
+    'elr_scalar_table': (ctypes.c_int, [c_f64, c_f64, c_f64, c_f64, c_i64, c_vp]),
+    'elr_adam_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_f32p, c_vp]),
+    'elr_init_rows': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_u32, c_f32, c_vp]),
+    'elr_replay_rows': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_u32,
+                                       c_f32, c_vp, c_i64, c_vp]),
+}
+
+
+def lib():
+    """The loaded library; raises RuntimeError if it has not been built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(f'{LIB_PATH} is missing: build it with `python -c "import __graft_entry__ as g; '
+                                       f'g.build()"` (no CPU fallback exists)')
+                L = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in SIGNATURES.items():
+                    f = getattr(L, name)
+                    f.restype = res
+                    f.argtypes = args
+                _lib = L
+    return _lib
+
+
+def check(rc, what):
+    """Raise RuntimeError for a nonzero C-ABI return code (the reference raises through TORCH_CHECK)."""
+    if rc != 0:
+        msg = lib().elr_error_string(rc).decode()
+        raise RuntimeError(f'{what} failed ({rc}): {msg}')
+
+
+def stream_of(t):
+    """Raw hipStream_t of torch's current stream on t's device."""
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def scalars8(vals):
+    return (ctypes.c_float * 8)(*vals)

@@ -1,0 +1,122 @@
+// Shared device code of the elara_amd HIP kernels (gfx950, wave64).
+//
+// Bit-exactness rules for every fp32 expression in this library:
+//   - no contraction into FMA (the build passes -ffp-contract=off; the pragma below enforces it per file);
+//   - division and square root correctly rounded (-fhip-fp32-correctly-rounded-divide-sqrt; plain '/' and
+//     __builtin_sqrtf, never the native/approximate intrinsics);
+//   - fp32 denormals kept (no -fgpu-flush-denormals-to-zero).
+// Under those rules each statement below is one IEEE-754 binary32 operation rounded to nearest even, which is
+// what the reference's CPU Adam computes (srm2/csrc/srm2_cpu.cpp:22-34, built with -ffp-contract=off).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+#include "../../include/elara_amd.h"
+
+namespace elr {
+
+struct AdamScalars {
+  float lr, b1, omb1, b2, omb2, bc1, bc2, eps;
+};
+
+// One Adam update of one element, in the reference's operation order (srm2/csrc/srm2_cpu.cpp:26-32).
+__device__ __forceinline__ void adam_elem(float& w, float& m, float& v, float g, const AdamScalars& s) {
+  float mj = s.b1 * m;
+  float t1 = s.omb1 * g;
+  mj = mj + t1;
+  float vj = s.b2 * v;
+  float t2 = s.omb2 * g;
+  t2 = t2 * g;
+  vj = vj + t2;
+  float mh = mj / s.bc1;
+  float vh = vj / s.bc2;
+  float den = __builtin_sqrtf(vh);
+  den = den + s.eps;
+  float num = s.lr * mh;
+  float up = num / den;
+  w = w - up;
+  m = mj;
+  v = vj;
+}
+
+__device__ __forceinline__ void adam_vec4(float4& w, float4& m, float4& v, const float4& g, const AdamScalars& s) {
+  adam_elem(w.x, m.x, v.x, g.x, s);
+  adam_elem(w.y, m.y, v.y, g.y, s);
+  adam_elem(w.z, m.z, v.z, g.z, s);
+  adam_elem(w.w, m.w, v.w, g.w, s);
+}
+
+// MurmurHash3 32-bit finalizer (fmix32), as srm2/gpu_ops.py:15-23 applies it to uint32 values.
+__device__ __forceinline__ uint32_t fmix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85EBCA6Bu;
+  x ^= x >> 13;
+  x *= 0xC2B2AE35u;
+  x ^= x >> 16;
+  return x;
+}
+
+// Per-row part of the counter hash: fmix32(u32(r >> 32) + seed)  (srm2/gpu_ops.py:33).
+__device__ __forceinline__ uint32_t init_row_key(int64_t r, uint32_t seed) {
+  return fmix32((uint32_t)((uint64_t)r >> 32) + seed);
+}
+
+// Initial weight of element j of row r (srm2/gpu_ops.py:33-36):
+//   key = u32(r*D + j) ^ rowkey;  h = fmix32(key ^ seed);  u = f32(h >> 8) * 2^-24;  w0 = (u*2 - 1) * bound.
+// u*2 and u*2-1 are exact in fp32; the product with bound is the only rounding.
+__device__ __forceinline__ float init_elem(uint32_t rlo_times_d_plus_j, uint32_t rowkey, uint32_t seed, float bound) {
+  uint32_t h = fmix32((rlo_times_d_plus_j ^ rowkey) ^ seed);
+  float u = (float)(h >> 8) * (1.0f / 16777216.0f);
+  float t = u * 2.0f;
+  t = t - 1.0f;
+  return t * bound;
+}
+
+// Four consecutive initial weights starting at element j0 (j0 % 4 == 0).
+__device__ __forceinline__ float4 init_vec4(int64_t r, int64_t D, int64_t j0, uint32_t rowkey, uint32_t seed,
+                                            float bound) {
+  uint32_t base = (uint32_t)((uint64_t)r * (uint64_t)D + (uint64_t)j0);
+  float4 w;
+  w.x = init_elem(base + 0u, rowkey, seed, bound);
+  w.y = init_elem(base + 1u, rowkey, seed, bound);
+  w.z = init_elem(base + 2u, rowkey, seed, bound);
+  w.w = init_elem(base + 3u, rowkey, seed, bound);
+  return w;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load marked non-temporal (data read once, e.g. gradients and log entries).
+__device__ __forceinline__ float4 ldg_stream(const float4* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Lanes of a 64-wide wave that share one row when a row holds `nchunk` 16-byte chunks: the smallest power of two
+// >= nchunk, capped at 64 (a lane then loops over nchunk/64 chunks).
+inline int lanes_per_row_log2(int64_t nchunk) {
+  int l = 0;
+  while ((1 << l) < nchunk && l < 6) ++l;
+  return l;
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Grid size for a grid-stride loop over `units` work units of `per_block` units per block: enough blocks to
+// cover the work, capped at a few full waves of the 256-CU chip so very large calls still loop.
+inline unsigned grid_for(int64_t units, int64_t per_block, int64_t cap_blocks = 256 * 64) {
+  int64_t b = (units + per_block - 1) / per_block;
+  if (b < 1) b = 1;
+  if (b > cap_blocks) b = cap_blocks;
+  return (unsigned)b;
+}
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? ELR_OK : (int)e;
+}
+
+}  // namespace elr

@@ -1,0 +1,211 @@
+// Counter-hash row initialisation and exact replay of short gradient logs (HBM-bound, no MFMA).
+//
+// init   replaces srm2/gpu_ops.py:26-48:  out[i] = (w0(rows[i]), 0, 0)
+// replay replaces srm2/gpu_ops.py:51-99:  out[i] = init(rows[i]); then for k < cnt[i], one Adam step with the
+//        scalars of logical step steps[i,k] and the gradient logs[offs[i]+k].  The Adam arithmetic is
+//        elr::adam_elem, so replay(init, log) is bitwise equal to eager Adam applied at those steps.
+//
+// Launch shape as in adam.hip: 2^lg lanes per row, one 16-byte chunk per lane per pass.  A replayed row's
+// K (<= 8) gradient chunks are all loaded into registers before the first update, so the c log reads of a row
+// are in flight together; the initial weights are computed in registers while they arrive, and the row is
+// written once (w, m, v).  Scalars come from the per-step table (32 bytes per step, cache resident).
+#include "elr_common.h"
+
+namespace elr {
+
+__global__ __launch_bounds__(256) void k_init_rows_v4(float* __restrict__ out, const int64_t* __restrict__ rows,
+                                                      int64_t n, int nchunk, int lg, uint32_t seed, float bound) {
+  const int lane = threadIdx.x & 63;
+  const int l = lane & ((1 << lg) - 1);
+  const int64_t rpw = 64 >> lg;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int64_t D = 4 * (int64_t)nchunk;
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t i = wave * rpw + (lane >> lg); i < n; i += nwave * rpw) {
+    const int64_t r = rows[i];
+    const uint32_t rk = init_row_key(r, seed);
+    float4* dst = reinterpret_cast<float4*>(out) + i * 3 * (int64_t)nchunk;
+    for (int c = l; c < nchunk; c += (1 << lg)) {
+      dst[c] = init_vec4(r, D, 4 * (int64_t)c, rk, seed, bound);
+      dst[nchunk + c] = zero;
+      dst[2 * nchunk + c] = zero;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_init_rows_scalar(float* __restrict__ out, const int64_t* __restrict__ rows,
+                                                          int64_t n, int64_t D, uint32_t seed, float bound) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t i = wave; i < n; i += nwave) {
+    const int64_t r = rows[i];
+    const uint32_t rk = init_row_key(r, seed);
+    float* dst = out + i * 3 * D;
+    for (int64_t j = lane; j < D; j += 64) {
+      dst[j] = init_elem((uint32_t)((uint64_t)r * (uint64_t)D + (uint64_t)j), rk, seed, bound);
+      dst[D + j] = 0.f;
+      dst[2 * D + j] = 0.f;
+    }
+  }
+}
+
+__device__ __forceinline__ AdamScalars load_scalars(const float* __restrict__ table, int64_t step) {
+  const float4* t = reinterpret_cast<const float4*>(table + step * 8);
+  const float4 a = t[0], b = t[1];
+  return AdamScalars{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+}
+
+// Row i is valid when every used step indexes the table and every used log entry exists.
+template <int K>
+__device__ __forceinline__ bool replay_row_inputs(const int32_t* __restrict__ steps, int64_t i, int c, int64_t o,
+                                                  int64_t nlogs, int64_t table_rows, int32_t (&st)[K]) {
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    st[k] = 0;
+    if (k < c) {
+      st[k] = steps[i * K + k];
+      ok = ok && st[k] >= 0 && st[k] < table_rows && o + k >= 0 && o + k < nlogs;
+    }
+  }
+  return ok;
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void k_replay_v4(float* __restrict__ out, const int64_t* __restrict__ rows,
+                                                   const float* __restrict__ logs, int64_t nlogs,
+                                                   const int64_t* __restrict__ offs,
+                                                   const int32_t* __restrict__ steps, const int32_t* __restrict__ cnt,
+                                                   int64_t n, int nchunk, int lg, uint32_t seed, float bound,
+                                                   const float* __restrict__ table, int64_t table_rows) {
+  const int lane = threadIdx.x & 63;
+  const int l = lane & ((1 << lg) - 1);
+  const int64_t rpw = 64 >> lg;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  const int64_t D = 4 * (int64_t)nchunk;
+  const float4* lg4 = reinterpret_cast<const float4*>(logs);
+  const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t i = wave * rpw + (lane >> lg); i < n; i += nwave * rpw) {
+    const int64_t r = rows[i];
+    const int c = cnt[i];
+    const int64_t o = offs[i];
+    int32_t st[K];
+    if (!replay_row_inputs<K>(steps, i, c, o, nlogs, table_rows, st)) continue;
+    const uint32_t rk = init_row_key(r, seed);
+    float4* dst = reinterpret_cast<float4*>(out) + i * 3 * (int64_t)nchunk;
+    for (int ch = l; ch < nchunk; ch += (1 << lg)) {
+      float4 g[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if (k < c) g[k] = ldg_stream(lg4 + (o + k) * (int64_t)nchunk + ch);
+      float4 w = init_vec4(r, D, 4 * (int64_t)ch, rk, seed, bound);
+      float4 m = zero, v = zero;
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if (k < c) adam_vec4(w, m, v, g[k], load_scalars(table, st[k]));
+      dst[ch] = w;
+      dst[nchunk + ch] = m;
+      dst[2 * nchunk + ch] = v;
+    }
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void k_replay_scalar(float* __restrict__ out, const int64_t* __restrict__ rows,
+                                                       const float* __restrict__ logs, int64_t nlogs,
+                                                       const int64_t* __restrict__ offs,
+                                                       const int32_t* __restrict__ steps,
+                                                       const int32_t* __restrict__ cnt, int64_t n, int64_t D,
+                                                       uint32_t seed, float bound, const float* __restrict__ table,
+                                                       int64_t table_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
+  for (int64_t i = wave; i < n; i += nwave) {
+    const int64_t r = rows[i];
+    const int c = cnt[i];
+    const int64_t o = offs[i];
+    int32_t st[K];
+    if (!replay_row_inputs<K>(steps, i, c, o, nlogs, table_rows, st)) continue;
+    const uint32_t rk = init_row_key(r, seed);
+    float* dst = out + i * 3 * D;
+    for (int64_t j = lane; j < D; j += 64) {
+      float w = init_elem((uint32_t)((uint64_t)r * (uint64_t)D + (uint64_t)j), rk, seed, bound), m = 0.f, v = 0.f;
+      for (int k = 0; k < K; ++k) {
+        if (k >= c) break;
+        const float* t = table + (int64_t)st[k] * 8;
+        const AdamScalars s{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
+        adam_elem(w, m, v, logs[(o + k) * D + j], s);
+      }
+      dst[j] = w;
+      dst[D + j] = m;
+      dst[2 * D + j] = v;
+    }
+  }
+}
+
+template <int K>
+static int launch_replay(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
+                         const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, uint32_t seed, float bound,
+                         const float* table, int64_t table_rows, hipStream_t st) {
+  if (D % 4 == 0 && D / 4 <= INT32_MAX && aligned16(out) && aligned16(logs) && aligned16(table)) {
+    const int64_t nchunk = D / 4;
+    const int lg = lanes_per_row_log2(nchunk);
+    const int64_t rpw = 64 >> lg;
+    k_replay_v4<K><<<grid_for((n + rpw - 1) / rpw, 4), 256, 0, st>>>(out, rows, logs, nlogs, offs, steps, cnt, n,
+                                                                     (int)nchunk, lg, seed, bound, table,
+                                                                     table_rows);
+  } else {
+    k_replay_scalar<K><<<grid_for(n, 4), 256, 0, st>>>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound,
+                                                       table, table_rows);
+  }
+  return launch_status();
+}
+
+}  // namespace elr
+
+extern "C" int elr_init_rows(float* out, const int64_t* rows, int64_t n, int64_t D, uint32_t seed, float bound,
+                             void* stream) {
+  if (n < 0 || D <= 0) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!out || !rows) return ELR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  if (D % 4 == 0 && D / 4 <= INT32_MAX && elr::aligned16(out)) {
+    const int64_t nchunk = D / 4;
+    const int lg = elr::lanes_per_row_log2(nchunk);
+    const int64_t rpw = 64 >> lg;
+    elr::k_init_rows_v4<<<elr::grid_for((n + rpw - 1) / rpw, 4), 256, 0, st>>>(out, rows, n, (int)nchunk, lg, seed,
+                                                                                bound);
+  } else {
+    elr::k_init_rows_scalar<<<elr::grid_for(n, 4), 256, 0, st>>>(out, rows, n, D, seed, bound);
+  }
+  return elr::launch_status();
+}
+
+extern "C" int elr_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
+                               const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed,
+                               float bound, const float* table, int64_t table_rows, void* stream) {
+  if (n < 0 || D <= 0 || nlogs < 0 || table_rows < 0) return ELR_EINVAL;
+  if (K < 1 || K > 8) return ELR_EUNSUPPORTED;
+  if (n == 0) return ELR_OK;
+  if (!out || !rows || !offs || !steps || !cnt || !table || (nlogs > 0 && !logs)) return ELR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  switch (K) {
+#define ELR_REPLAY_CASE(KK) \
+  case KK:                  \
+    return elr::launch_replay<KK>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound, table, table_rows, st);
+    ELR_REPLAY_CASE(1)
+    ELR_REPLAY_CASE(2)
+    ELR_REPLAY_CASE(3)
+    ELR_REPLAY_CASE(4)
+    ELR_REPLAY_CASE(5)
+    ELR_REPLAY_CASE(6)
+    ELR_REPLAY_CASE(7)
+    ELR_REPLAY_CASE(8)
+#undef ELR_REPLAY_CASE
+  }
+  return ELR_EUNSUPPORTED;
+}

@@ -1,0 +1,62 @@
+"""Row-sparse Adam on HBM-resident (w, m, v) records -- drop-in for srm2/ops.py (gpu_adam, ext().adam_scalars).
+
+    gpu_adam(pool, slots, grad, lr, b1, b2, eps, step)       srm2/ops.py:59-67
+    ext().adam_scalars(lr, b1, b2, eps, step) -> [8 floats]  srm2/csrc/srm2_cpu.cpp:255-257
+
+The update runs in the HIP kernel behind elr_adam_rows (elara_amd/csrc/adam.hip) on torch's current stream;
+there is no other implementation in the product path.
+"""
+import torch
+
+from . import _lib
+
+
+def adam_scalars(lr, b1, b2, eps, step):
+    """The 8 fp32 Adam scalars of logical step `step` (fp64 arithmetic rounded to fp32), as a list of floats."""
+    out = (_lib.c_f32 * 8)()
+    _lib.lib().elr_adam_scalars(float(lr), float(b1), float(b2), float(eps), int(step), out)
+    return list(out)
+
+
+class _Ext:
+    """Mirror of the reference's `ext()` module for the functions on this path."""
+
+    adam_scalars = staticmethod(adam_scalars)
+
+
+_ext = _Ext()
+
+
+def ext():
+    """Counterpart of srm2/ops.py:19-26 ext(): the native helpers (here: adam_scalars)."""
+    _lib.lib()
+    return _ext
+
+
+def _check_state(pool, name='pool'):
+    if not (pool.is_cuda and pool.dtype == torch.float32 and pool.dim() == 3 and pool.shape[1] == 3
+            and pool.is_contiguous()):
+        raise RuntimeError(f'{name} must be a contiguous cuda float32 tensor of shape [C,3,D], got '
+                           f'{tuple(pool.shape)} {pool.dtype} {pool.device}')
+
+
+def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
+    """pool [C,3,D] cuda float32 (updated in place); slots int32/int64 [n] (unique rows of pool); grad [n,D]
+    (row i -> slots[i]).  srm2/ops.py:59-67."""
+    n = slots.numel()
+    if n == 0:
+        return
+    _check_state(pool)
+    D = pool.shape[2]
+    if slots.dtype not in (torch.int32, torch.int64) or not slots.is_cuda or slots.device != pool.device:
+        raise RuntimeError(f'slots must be a cuda int32/int64 tensor on {pool.device}')
+    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.device == pool.device and grad.numel() == n * D):
+        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {pool.device}')
+    slots = slots.contiguous()
+    grad = grad.contiguous()
+    s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
+    L = _lib.lib()
+    with torch.cuda.device(pool.device):
+        rc = L.elr_adam_rows(_lib.ptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
+                             _lib.ptr(grad), n, D, s, _lib.stream_of(pool))
+    _lib.check(rc, 'elr_adam_rows')

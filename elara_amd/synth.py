@@ -1,0 +1,47 @@
+"""Synthetic inputs of the benchmark configurations (host numpy; callers copy what they need to HBM).
+
+Common settings: Adam lr=1e-3, b1=0.9, b2=0.999, eps=1e-8; gradients N(0, sigma=1e-3) drawn in fp64 and rounded to
+fp32; RNG numpy.random.default_rng(seed).
+"""
+import numpy as np
+
+ADAM = (1e-3, 0.9, 0.999, 1e-8)
+
+
+def bound_for(D):
+    """fp32(1/sqrt(D)), the init bound of the configs."""
+    return float(np.float32(1.0 / np.sqrt(D)))
+
+
+def grads(rng, n, D, sigma=1e-3):
+    return (rng.standard_normal((n, D)) * sigma).astype(np.float32)
+
+
+class ReplayLog:
+    """Config C2 shape: n rows, each with c ~ U{1..K} logged gradients at strictly increasing steps (gaps U{1..50}).
+
+    rows int64 [n]; cnt int32 [n]; steps int32 [n,K] (0 for unused slots); offs int64 [n] (exclusive cumsum of cnt);
+    logs fp32 [sum(cnt), D] (row i's entries contiguous at offs[i]); max_step = largest logged step.
+    """
+
+    def __init__(self, n=262_144, D=128, K=3, seed=0, rows=None, max_gap=50, cmin=1):
+        rng = np.random.default_rng(seed)
+        self.n, self.D, self.K = n, D, K
+        self.rows = np.arange(n, dtype=np.int64) if rows is None else np.asarray(rows, dtype=np.int64)
+        self.cnt = rng.integers(cmin, K + 1, n).astype(np.int32)
+        st = np.cumsum(rng.integers(1, max_gap + 1, (n, K)), 1)
+        st[np.arange(K)[None, :] >= self.cnt[:, None]] = 0
+        self.steps = st.astype(np.int32)
+        self.offs = (np.cumsum(self.cnt, dtype=np.int64) - self.cnt).astype(np.int64)
+        self.logs = grads(rng, int(self.cnt.sum()), D)
+        self.max_step = int(self.steps.max()) if n else 0
+
+    def entries_of_step(self, t):
+        """(row index i, log entry index) of every row whose log holds step t."""
+        i, k = np.nonzero(self.steps == t)
+        return i.astype(np.int64), (self.offs[i] + k).astype(np.int64)
+
+
+def unique_rows(rng, R, n):
+    """n distinct row ids from [0, R), uniform without replacement, unsorted."""
+    return rng.choice(R, n, replace=False).astype(np.int64)

@@ -1,0 +1,86 @@
+/*
+ * elara_amd — C-ABI of the MI355X (gfx950) sparse-update path of ELARA.
+ *
+ * Conventions
+ *   - extern "C", plain pointers and int64 sizes; no C++ types or exceptions cross the boundary.
+ *   - All memory is owned by the caller.  Device pointers point to HBM; host pointers are marked "host".
+ *   - Every entry point that touches the GPU takes an explicit hipStream_t (passed as void*, so this header
+ *     needs no HIP include) and is asynchronous on that stream; nothing uses the legacy default stream.
+ *   - Return value: ELR_OK (0) on success, a negative ELR_E* code for an invalid argument detected on the
+ *     host, or a positive hipError_t from the launch.  elr_error_string() describes a code.
+ *   - The library keeps no mutable global state (re-entrant; callable from several host threads).
+ *   - Device-side index checks: a row whose index (slot, log offset, step) is out of range is skipped and left
+ *     unwritten instead of faulting.  The reference leaves such inputs undefined; callers must not rely on it.
+ *
+ * Layouts (the reference's, srm2/ops.py:47, srm2/csrc/srm2_cpu.cpp:36):
+ *   state  fp32 [C, 3, D]   interleaved record (w, m, v) per row, row stride 12*D bytes
+ *   grad   fp32 [n, D]      row i belongs to slots[i]
+ *   logs   fp32 [L, D]      gradient-log entries; row i of a replay owns logs[offs[i] .. offs[i]+cnt[i])
+ *   table  fp32 [S, 8]      Adam scalars per logical step (lr, b1, 1-b1, b2, 1-b2, 1-b1^t, 1-b2^t, eps)
+ */
+#ifndef ELARA_AMD_H
+#define ELARA_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ELR_OK 0
+#define ELR_EINVAL (-1)      /* null pointer, negative size or inconsistent shape */
+#define ELR_EUNSUPPORTED (-2) /* valid for the reference but outside this build's limits (e.g. K > 8) */
+#define ELR_ECAPACITY (-3)   /* caller-provided scratch or output too small */
+
+/* Text for a return code (static storage). */
+const char* elr_error_string(int code);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int elr_version(void);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Adam scalars for logical step `step` (host only).
+ * Replaces: srm2/csrc/srm2_cpu.cpp:13-20 make_scalars and its binding adam_scalars (srm2_cpu.cpp:255-257),
+ * called from srm2/ops.py:64 and srm2/gpu_ops.py:86.  out = (lr, b1, 1-b1, b2, 1-b2, 1-b1^t, 1-b2^t, eps),
+ * each computed in fp64 and rounded to fp32.
+ * ------------------------------------------------------------------------------------------------------- */
+void elr_adam_scalars(double lr, double b1, double b2, double eps, int64_t step, float out[8]);
+
+/* Fill a host table [max_step+1, 8]: row 0 zeros, row t = elr_adam_scalars(t).
+ * Replaces: srm2/gpu_ops.py:82-88 ScalarTable (host part; the caller copies it to HBM). */
+int elr_scalar_table(double lr, double b1, double b2, double eps, int64_t max_step, float* table_host);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Row-sparse Adam, in place.
+ * Replaces: srm2/ops.py:42-67 gpu_adam / _adam_rows.  For i < n: Adam(state[slots[i]], grad[i]) with the
+ * scalars sc (host array, from elr_adam_scalars).  Slots must be unique within a call (as in the reference).
+ *   state  device fp32 [C,3,D];  slots device int32 (idx64 = 0) or int64 (idx64 = 1) [n];  grad device [n,D].
+ * ------------------------------------------------------------------------------------------------------- */
+int elr_adam_rows(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n, int64_t D,
+                  const float sc[8], void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Counter-hash initial state.
+ * Replaces: srm2/gpu_ops.py:41-48 init_rows / _init_rows (hash gpu_ops.py:15-23).  out[i] = (w0(rows[i]), 0, 0)
+ * with w0[j] = ((h >> 8) * 2^-24 * 2 - 1) * bound, h = fmix32(u32(r*D + j) ^ fmix32(u32(r >> 32) + seed) ^ seed).
+ *   out device fp32 [n,3,D];  rows device int64 [n];  seed = low 32 bits of the reference's seed;
+ *   bound = the reference's bound rounded to fp32.
+ * ------------------------------------------------------------------------------------------------------- */
+int elr_init_rows(float* out, const int64_t* rows, int64_t n, int64_t D, uint32_t seed, float bound, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Exact replay of logged gradients.
+ * Replaces: srm2/gpu_ops.py:91-99 replay_rows / _replay (gpu_ops.py:51-79).  out[i] = init(rows[i]) followed by
+ * Adam with gradient logs[offs[i] + k] and scalars table[steps[i*K + k]] for k < cnt[i].  1 <= K <= 8.
+ *   out device fp32 [n,3,D]; rows int64 [n]; logs fp32 [nlogs,D]; offs int64 [n]; steps int32 [n,K];
+ *   cnt int32 [n]; table fp32 [table_rows, 8].  All device pointers.
+ * ------------------------------------------------------------------------------------------------------- */
+int elr_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
+                    const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed, float bound,
+                    const float* table, int64_t table_rows, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ELARA_AMD_H */

@@ -1,0 +1,67 @@
+"""The C-ABI library: it loads, exports every symbol include/elara_amd.h declares, and its host-only entry points
+and argument checks behave as documented.  CPU only (no call here reaches the GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from elara_amd import _lib
+from oracle import oracle as O
+
+HEADERS = sorted((Path(__file__).resolve().parents[1] / 'include').glob('*.h'))
+
+
+def declared():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r'/\*.*?\*/', '', h.read_text(), flags=re.S)
+        names |= set(re.findall(r'\b(elr_\w+)\s*\(', text))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) <= set(_lib.SIGNATURES), 'binding lacks a signature for a declared entry point'
+
+
+def test_version_and_errors():
+    L = _lib.lib()
+    assert L.elr_version() >= 100
+    assert b'invalid' in L.elr_error_string(-1)
+    with pytest.raises(RuntimeError):
+        _lib.check(-1, 'x')
+
+
+def test_scalars_and_table_match_oracle():
+    from elara_amd.ops import adam_scalars
+    for hp in [(1e-3, 0.9, 0.999, 1e-8), (5e-2, 0.5, 0.9, 1e-3)]:
+        for t in range(0, 3000, 7):
+            a = np.array(adam_scalars(*hp, t), np.float32)
+            assert np.array_equal(a.view(np.uint32), O.adam_scalars(*hp, t).view(np.uint32))
+        tab = np.empty((201, 8), np.float32)
+        assert _lib.lib().elr_scalar_table(*hp, 200, tab.ctypes.data_as(ctypes.c_void_p)) == 0
+        assert np.array_equal(tab.view(np.uint32), O.scalar_table(*hp, 200).view(np.uint32))
+
+
+def test_host_argument_checks_return_codes():
+    L = _lib.lib()
+    s = _lib.scalars8([0.0] * 8)
+    assert L.elr_adam_rows(None, 0, None, 0, None, -1, 4, s, None) == -1
+    assert L.elr_adam_rows(None, 0, None, 0, None, 0, 4, s, None) == 0          # n == 0: no-op
+    assert L.elr_adam_rows(None, 0, None, 0, None, 5, 4, s, None) == -1         # null pointers
+    assert L.elr_init_rows(None, None, 3, 0, 0, 1.0, None) == -1
+    assert L.elr_replay_rows(None, None, None, 0, None, None, None, 1, 4, 9, 0, 1.0, None, 0, None) == -2
+    assert L.elr_replay_rows(None, None, None, 0, None, None, None, 0, 4, 3, 0, 1.0, None, 0, None) == 0
+
+
+def test_ops_raise_without_gpu_tensors():
+    import torch
+    from elara_amd.ops import gpu_adam
+    with pytest.raises(RuntimeError):
+        gpu_adam(torch.zeros(4, 3, 8), torch.tensor([0]), torch.zeros(1, 8), 1e-3, 0.9, 0.999, 1e-8, 1)
