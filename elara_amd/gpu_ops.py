@@ -52,7 +52,7 @@ def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None
     if out is None:
         out = torch.empty(n, 3, D, device=rows.device)
     if n:
-        t = table.t if hasattr(table, 't') else table
+        t = table if isinstance(table, torch.Tensor) else table.t
         dev = rows.device
         if not (out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and out.numel() >= n * 3 * D):
             raise RuntimeError(f'out must be a contiguous cuda float32 tensor with at least {n}x3x{D} elements')

@@ -50,14 +50,15 @@ def test_adam_matches_oracle(dev, D, idx):
 
 
 def test_adam_matches_triton_golden(dev, golden):
+    from elara_amd import _lib
     for ci in range(4):
+        # every device buffer is held by a name until the launch has completed
         st = torch.from_numpy(golden[f'adam{ci}_state'].copy()).to(dev)
+        slots = torch.from_numpy(golden[f'adam{ci}_slots']).to(dev)
+        grad = torch.from_numpy(golden[f'adam{ci}_grad']).to(dev)
         s = golden[f'adam{ci}_scalars']
-        from elara_amd import _lib
-        rc = _lib.lib().elr_adam_rows(_lib.ptr(st), st.shape[0], _lib.ptr(torch.from_numpy(golden[f'adam{ci}_slots']).to(dev)),
-                                      1, _lib.ptr(torch.from_numpy(golden[f'adam{ci}_grad']).to(dev)),
-                                      golden[f'adam{ci}_slots'].size, st.shape[2], _lib.scalars8(s.tolist()),
-                                      _lib.stream_of(st))
+        rc = _lib.lib().elr_adam_rows(_lib.ptr(st), st.shape[0], _lib.ptr(slots), 1, _lib.ptr(grad), slots.numel(),
+                                      st.shape[2], _lib.scalars8(s.tolist()), _lib.stream_of(st))
         assert rc == 0
         torch.cuda.synchronize()
         assert same(st, golden[f'adam{ci}_out']), ci
