@@ -5,12 +5,14 @@ library is missing, every op raises.  torch is imported before the library is lo
 to the HIP runtime torch already loaded (same soname), and torch's streams are valid handles for it.
 """
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / 'libelara_amd.so'
+# ELARA_AMD_LIB may name another build of the same library (e.g. a tuning variant); default: the in-tree build.
+LIB_PATH = Path(os.environ.get('ELARA_AMD_LIB') or (Path(__file__).resolve().parent / 'libelara_amd.so'))
 
 _lib = None
 _lock = threading.Lock()

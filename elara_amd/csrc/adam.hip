@@ -3,11 +3,11 @@
 // Replaces srm2/ops.py:42-67 (_adam_rows / gpu_adam).  Per element the arithmetic is elr::adam_elem, the
 // reference's CPU operation order (srm2/csrc/srm2_cpu.cpp:22-34), so results are bitwise those of cpu_adam.
 //
-// Launch shape: a row of D floats is D/4 16-byte chunks; 2^lg lanes of a wave share one row (lg from
-// lanes_per_row_log2), so a wave updates 64 >> lg rows at a time with one global_load_dwordx4 per lane for each
-// of w, m, v, g and one global_store_dwordx4 for each of w, m, v.  The gradient is read once, with a
-// non-temporal load.  A grid-stride loop over row groups keeps the grid bounded for very large calls.
-#include "elr_common.h"
+// Launch shapes.  D in {64,128,256,512}: one wave per row (elr_rowio.h), U rows per wave, slot ids read as scalars.
+// Other D divisible by 4: 2^lg lanes share one row (lg from lanes_per_row_log2), one 16-byte chunk per lane per
+// pass, a grid-stride loop over row groups.  Otherwise one float per lane.  The gradient is read once, with a
+// non-temporal load.
+#include "elr_rowio.h"
 
 #include <cmath>
 
@@ -64,9 +64,72 @@ __global__ __launch_bounds__(256) void k_adam_rows_scalar(float* __restrict__ st
   }
 }
 
+// Wave-per-row variant for D = 64*VPL: the slot of each row is a wave-uniform (scalar) load; the U rows of a wave
+// issue all their w, m, v, g loads before the first update.  No loop (see init_replay.hip): one row group per
+// wave, large calls split into several launches on the host.
+#ifndef ELR_ADAM_U
+#define ELR_ADAM_U 2
+#endif
+
+template <int VPL, typename Idx, int U>
+__global__ __launch_bounds__(256) void k_adam_rows_wpr(float* __restrict__ state, int64_t C,
+                                                       const Idx* __restrict__ slots, const float* __restrict__ grad,
+                                                       int64_t n, AdamScalars s) {
+  constexpr int64_t D = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t i0 = wave_id() * U;
+  int64_t sl[U];
+  RowFrag<VPL> w[U], m[U], v[U], g[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + u;
+    sl[u] = i < n ? (int64_t)slots[i] : -1;
+    if (sl[u] >= C) sl[u] = -1;
+    if (sl[u] >= 0) {
+      const float* rec = state + sl[u] * 3 * D + lane * VPL;
+      w[u] = frag_load<VPL, false>(rec);
+      m[u] = frag_load<VPL, false>(rec + D);
+      v[u] = frag_load<VPL, false>(rec + 2 * D);
+      g[u] = frag_load<VPL, true>(grad + i * D + lane * VPL);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (sl[u] < 0) continue;
+    frag_adam<VPL>(w[u], m[u], v[u], g[u], s);
+    float* rec = state + sl[u] * 3 * D + lane * VPL;
+    frag_store<VPL>(rec, w[u]);
+    frag_store<VPL>(rec + D, m[u]);
+    frag_store<VPL>(rec + 2 * D, v[u]);
+  }
+}
+
+template <int VPL, typename Idx>
+static void launch_adam_wpr(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n,
+                            const AdamScalars& s, hipStream_t st) {
+  constexpr int U = ELR_ADAM_U;
+  constexpr int64_t D = 64 * VPL;
+  constexpr int64_t per = wpr_rows_per_launch(U);
+  for (int64_t a = 0; a < n; a += per) {
+    const int64_t m = n - a < per ? n - a : per;
+    k_adam_rows_wpr<VPL, Idx, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(state, C, slots + a,
+                                                                                               grad + a * D, m, s);
+  }
+}
+
 template <typename Idx>
 static int launch_adam(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n, int64_t D,
                        const AdamScalars& s, hipStream_t st) {
+  const int vpl = wpr_vpl(D);
+  if (vpl && aligned16(state) && aligned16(grad)) {
+    switch (vpl) {
+      case 1: launch_adam_wpr<1, Idx>(state, C, slots, grad, n, s, st); break;
+      case 2: launch_adam_wpr<2, Idx>(state, C, slots, grad, n, s, st); break;
+      case 4: launch_adam_wpr<4, Idx>(state, C, slots, grad, n, s, st); break;
+      default: launch_adam_wpr<8, Idx>(state, C, slots, grad, n, s, st); break;
+    }
+    return launch_status();
+  }
   if (D % 4 == 0 && D / 4 <= INT32_MAX && aligned16(state) && aligned16(grad)) {
     const int64_t nchunk = D / 4;
     const int lg = lanes_per_row_log2(nchunk);

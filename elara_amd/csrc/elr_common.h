@@ -105,8 +105,16 @@ inline int lanes_per_row_log2(int64_t nchunk) {
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Wave-per-row kernels launch one wave per group of rows (no loop iteration in practice): on gfx9 stores count in
+// vmcnt, so a second grid-stride iteration would wait for the first iteration's stores before its loads.  The
+// grid-stride loop remains only as a fallback past this many blocks (gridDim.x * 256 stays below 2^31).
+constexpr int64_t kOneShotBlocks = int64_t(1) << 22;
+
+// Rows per launch of a loop-free wave-per-row kernel with U rows per wave and 4 waves per block.
+constexpr int64_t wpr_rows_per_launch(int U) { return kOneShotBlocks * 4 * U; }
+
 // Grid size for a grid-stride loop over `units` work units of `per_block` units per block: enough blocks to
-// cover the work, capped at a few full waves of the 256-CU chip so very large calls still loop.
+// cover the work, capped (by default at a few full waves of the 256-CU chip) so very large calls loop.
 inline unsigned grid_for(int64_t units, int64_t per_block, int64_t cap_blocks = 256 * 64) {
   int64_t b = (units + per_block - 1) / per_block;
   if (b < 1) b = 1;

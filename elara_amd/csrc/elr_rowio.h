@@ -1,0 +1,117 @@
+// Wave-per-row access helpers: a row of D = 64*VPL floats is spread over the 64 lanes of one wavefront, lane l
+// holding the VPL consecutive floats [l*VPL, l*VPL + VPL).  One wave therefore reads or writes a whole row with a
+// single coalesced vector instruction (VPL = 1, 2, 4: dword, dwordx2, dwordx4; VPL = 8: two dwordx4).
+//
+// Why a wave per row: every per-row quantity (row id, slot, log offset, count, logical steps, Adam scalars) is
+// then uniform across the wave.  Reading it through a readfirstlane'd index lets the compiler use scalar loads
+// (s_load, through the scalar cache) and scalar branches, so the vector pipe only moves the D-wide payload.
+#pragma once
+
+#include "elr_common.h"
+
+namespace elr {
+
+template <int VPL>
+struct RowFrag {
+  float v[VPL];
+};
+
+template <int VPL, bool NT>
+__device__ __forceinline__ RowFrag<VPL> frag_load(const float* __restrict__ p) {
+  RowFrag<VPL> r;
+  if constexpr (VPL == 1) {
+    r.v[0] = NT ? __builtin_nontemporal_load(p) : *p;
+  } else if constexpr (VPL == 2) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 t = NT ? __builtin_nontemporal_load(reinterpret_cast<const f2*>(p)) : *reinterpret_cast<const f2*>(p);
+    r.v[0] = t.x;
+    r.v[1] = t.y;
+  } else {
+    static_assert(VPL % 4 == 0, "VPL must be 1, 2 or a multiple of 4");
+#pragma unroll
+    for (int q = 0; q < VPL / 4; ++q) {
+      const f32x4 t = NT ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + q)
+                         : reinterpret_cast<const f32x4*>(p)[q];
+      r.v[4 * q + 0] = t.x;
+      r.v[4 * q + 1] = t.y;
+      r.v[4 * q + 2] = t.z;
+      r.v[4 * q + 3] = t.w;
+    }
+  }
+  return r;
+}
+
+template <int VPL>
+__device__ __forceinline__ void frag_store(float* __restrict__ p, const RowFrag<VPL>& r) {
+  if constexpr (VPL == 1) {
+    *p = r.v[0];
+  } else if constexpr (VPL == 2) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    f2 t;
+    t.x = r.v[0];
+    t.y = r.v[1];
+    *reinterpret_cast<f2*>(p) = t;
+  } else {
+#pragma unroll
+    for (int q = 0; q < VPL / 4; ++q) {
+      f32x4 t;
+      t.x = r.v[4 * q + 0];
+      t.y = r.v[4 * q + 1];
+      t.z = r.v[4 * q + 2];
+      t.w = r.v[4 * q + 3];
+      reinterpret_cast<f32x4*>(p)[q] = t;
+    }
+  }
+}
+
+template <int VPL>
+__device__ __forceinline__ void frag_adam(RowFrag<VPL>& w, RowFrag<VPL>& m, RowFrag<VPL>& v, const RowFrag<VPL>& g,
+                                          const AdamScalars& s) {
+#pragma unroll
+  for (int e = 0; e < VPL; ++e) adam_elem(w.v[e], m.v[e], v.v[e], g.v[e], s);
+}
+
+// Initial weights of the lane's fragment of row r (D = 64*VPL): elements j = lane*VPL + e.
+template <int VPL>
+__device__ __forceinline__ RowFrag<VPL> frag_init(int64_t r, int lane, uint32_t seed, float bound) {
+  constexpr uint32_t D = 64u * VPL;
+  const uint32_t rk = init_row_key(r, seed);
+  const uint32_t base = (uint32_t)((uint64_t)r * (uint64_t)D) + (uint32_t)(lane * VPL);
+  RowFrag<VPL> w;
+#pragma unroll
+  for (int e = 0; e < VPL; ++e) w.v[e] = init_elem(base + (uint32_t)e, rk, seed, bound);
+  return w;
+}
+
+template <int VPL>
+__device__ __forceinline__ RowFrag<VPL> frag_zero() {
+  RowFrag<VPL> z;
+#pragma unroll
+  for (int e = 0; e < VPL; ++e) z.v[e] = 0.0f;
+  return z;
+}
+
+// Scalars of one table row, read through the scalar cache when `step` is wave-uniform.
+__device__ __forceinline__ AdamScalars table_scalars(const float* __restrict__ table, int64_t step) {
+  const float* t = table + step * 8;
+  return AdamScalars{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
+}
+
+// Index of this wave in the grid and the number of waves, both wave-uniform (SGPR) values.
+__device__ __forceinline__ int64_t wave_id() {
+  return (int64_t)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
+}
+__device__ __forceinline__ int64_t wave_count() { return (int64_t)gridDim.x * (blockDim.x >> 6); }
+
+// VPL for D if the wave-per-row kernels handle it (D = 64, 128, 256, 512), else 0.
+inline int wpr_vpl(int64_t D) {
+  switch (D) {
+    case 64: return 1;
+    case 128: return 2;
+    case 256: return 4;
+    case 512: return 8;
+    default: return 0;
+  }
+}
+
+}  // namespace elr

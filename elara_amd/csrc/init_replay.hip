@@ -5,14 +5,18 @@
 //        scalars of logical step steps[i,k] and the gradient logs[offs[i]+k].  The Adam arithmetic is
 //        elr::adam_elem, so replay(init, log) is bitwise equal to eager Adam applied at those steps.
 //
-// Launch shape as in adam.hip: 2^lg lanes per row, one 16-byte chunk per lane per pass.  A replayed row's
-// K (<= 8) gradient chunks are all loaded into registers before the first update, so the c log reads of a row
-// are in flight together; the initial weights are computed in registers while they arrive, and the row is
-// written once (w, m, v).  Scalars come from the per-step table (32 bytes per step, cache resident).
-#include "elr_common.h"
+// D in {64, 128, 256, 512}: wave-per-row kernels (elr_rowio.h).  A wave owns U rows; their ids, counts, log offsets
+// and steps are scalar loads, all their log-entry loads are issued before the first update, the Adam scalars of each
+// step come through the scalar cache, the initial weights are computed in registers while the loads are in
+// flight, and each record is written once.  The kernels have no loop: a loop back-edge makes the compiler guard the
+// next iteration's loads with vmcnt(0) waits that also drain this iteration's stores, so very large calls are split
+// into several launches on the host instead.
+// Other D: the generic kernels below (2^lg lanes per row with 16-byte chunks, or one float per lane).
+#include "elr_rowio.h"
 
 namespace elr {
 
+// ---- generic kernels (any D) --------------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_init_rows_v4(float* __restrict__ out, const int64_t* __restrict__ rows,
                                                       int64_t n, int nchunk, int lg, uint32_t seed, float bound) {
   const int lane = threadIdx.x & 63;
@@ -147,10 +151,130 @@ __global__ __launch_bounds__(256) void k_replay_scalar(float* __restrict__ out, 
   }
 }
 
+// ---- wave-per-row kernels (D = 64*VPL) ------------------------------------------------------------------------------
+#ifndef ELR_REPLAY_U
+#define ELR_REPLAY_U 2
+#endif
+#ifndef ELR_INIT_U
+#define ELR_INIT_U 2
+#endif
+
+template <int VPL, int U>
+__global__ __launch_bounds__(256) void k_init_rows_wpr(float* __restrict__ out, const int64_t* __restrict__ rows,
+                                                       int64_t n, uint32_t seed, float bound) {
+  constexpr int64_t D = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  const RowFrag<VPL> z = frag_zero<VPL>();
+  const int64_t i0 = wave_id() * U;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + u;
+    if (i < n) {
+      float* dst = out + i * 3 * D + lane * VPL;
+      frag_store<VPL>(dst, frag_init<VPL>(rows[i], lane, seed, bound));
+      frag_store<VPL>(dst + D, z);
+      frag_store<VPL>(dst + 2 * D, z);
+    }
+  }
+}
+
+template <int VPL, int K, int U>
+__global__ __launch_bounds__(256) void k_replay_wpr(float* __restrict__ out, const int64_t* __restrict__ rows,
+                                                    const float* __restrict__ logs, int64_t nlogs,
+                                                    const int64_t* __restrict__ offs,
+                                                    const int32_t* __restrict__ steps,
+                                                    const int32_t* __restrict__ cnt, int64_t n, uint32_t seed,
+                                                    float bound, const float* __restrict__ table, int64_t table_rows) {
+  constexpr int64_t D = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t i0 = wave_id() * U;
+  int64_t r[U], o[U];
+  int c[U];
+  int32_t st[U][K];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = i0 + u;
+    c[u] = -1;  // -1: past the end, or invalid inputs (the row is skipped)
+    r[u] = 0;
+    o[u] = 0;
+    if (i < n) {
+      r[u] = rows[i];
+      o[u] = offs[i];
+      const int ci = cnt[i];
+      const int cc = ci < 0 ? 0 : (ci > K ? K : ci);
+      // every used step indexes the table and every used log entry exists (branch-free)
+      int bad = (o[u] < 0) | (o[u] + cc > nlogs);
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        st[u][k] = steps[i * K + k];
+        bad |= (k < cc) & ((st[u][k] < 0) | (st[u][k] >= table_rows));
+      }
+      c[u] = bad ? -1 : cc;
+    }
+  }
+  RowFrag<VPL> g[U][K];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (k < c[u]) g[u][k] = frag_load<VPL, true>(logs + (o[u] + k) * D + lane * VPL);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (c[u] < 0) continue;
+    RowFrag<VPL> w = frag_init<VPL>(r[u], lane, seed, bound), m = frag_zero<VPL>(), v = frag_zero<VPL>();
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (k < c[u]) frag_adam<VPL>(w, m, v, g[u][k], table_scalars(table, st[u][k]));
+    float* dst = out + (i0 + u) * 3 * D + lane * VPL;
+    frag_store<VPL>(dst, w);
+    frag_store<VPL>(dst + D, m);
+    frag_store<VPL>(dst + 2 * D, v);
+  }
+}
+
+template <int VPL, int K>
+static void launch_replay_wpr(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
+                              const int32_t* steps, const int32_t* cnt, int64_t n, uint32_t seed, float bound,
+                              const float* table, int64_t table_rows, hipStream_t st) {
+  constexpr int U = ELR_REPLAY_U;
+  constexpr int64_t D = 64 * VPL;
+  constexpr int64_t per = wpr_rows_per_launch(U);
+  for (int64_t a = 0; a < n; a += per) {
+    const int64_t m = n - a < per ? n - a : per;
+    k_replay_wpr<VPL, K, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(
+        out + a * 3 * D, rows + a, logs, nlogs, offs + a, steps + a * K, cnt + a, m, seed, bound, table, table_rows);
+  }
+}
+
+template <int VPL>
+static void launch_init_wpr(float* out, const int64_t* rows, int64_t n, uint32_t seed, float bound, hipStream_t st) {
+  constexpr int U = ELR_INIT_U;
+  constexpr int64_t D = 64 * VPL;
+  constexpr int64_t per = wpr_rows_per_launch(U);
+  for (int64_t a = 0; a < n; a += per) {
+    const int64_t m = n - a < per ? n - a : per;
+    k_init_rows_wpr<VPL, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(out + a * 3 * D, rows + a,
+                                                                                          m, seed, bound);
+  }
+}
+
 template <int K>
 static int launch_replay(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                          const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, uint32_t seed, float bound,
                          const float* table, int64_t table_rows, hipStream_t st) {
+  const int vpl = wpr_vpl(D);
+  if (K <= 4 && vpl && aligned16(out) && aligned16(logs)) {
+#define ELR_WPR_REPLAY(V) \
+  launch_replay_wpr<V, K>(out, rows, logs, nlogs, offs, steps, cnt, n, seed, bound, table, table_rows, st)
+    switch (vpl) {
+      case 1: ELR_WPR_REPLAY(1); break;
+      case 2: ELR_WPR_REPLAY(2); break;
+      case 4: ELR_WPR_REPLAY(4); break;
+      default: ELR_WPR_REPLAY(8); break;
+    }
+#undef ELR_WPR_REPLAY
+    return launch_status();
+  }
   if (D % 4 == 0 && D / 4 <= INT32_MAX && aligned16(out) && aligned16(logs) && aligned16(table)) {
     const int64_t nchunk = D / 4;
     const int lg = lanes_per_row_log2(nchunk);
@@ -173,7 +297,15 @@ extern "C" int elr_init_rows(float* out, const int64_t* rows, int64_t n, int64_t
   if (n == 0) return ELR_OK;
   if (!out || !rows) return ELR_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-  if (D % 4 == 0 && D / 4 <= INT32_MAX && elr::aligned16(out)) {
+  const int vpl = elr::wpr_vpl(D);
+  if (vpl && elr::aligned16(out)) {
+    switch (vpl) {
+      case 1: elr::launch_init_wpr<1>(out, rows, n, seed, bound, st); break;
+      case 2: elr::launch_init_wpr<2>(out, rows, n, seed, bound, st); break;
+      case 4: elr::launch_init_wpr<4>(out, rows, n, seed, bound, st); break;
+      default: elr::launch_init_wpr<8>(out, rows, n, seed, bound, st); break;
+    }
+  } else if (D % 4 == 0 && D / 4 <= INT32_MAX && elr::aligned16(out)) {
     const int64_t nchunk = D / 4;
     const int lg = elr::lanes_per_row_log2(nchunk);
     const int64_t rpw = 64 >> lg;
