@@ -138,8 +138,8 @@ def headline(args):
         'config': {'workload': 'C2 exact replay (262,144 rows x d=128, k~U{1,2,3}, gaps U{1..50}) + one '
                                'row-sparse Adam step on the materialised rows', 'rows_per_step': n, 'dim': D,
                    'kmax': K, 'log_entries': nlog, 'parallelism': 'single GPU'},
-        'roofline': {'bound': 'hbm', 'kernel': 'elr::k_replay_v4<3>', 'achieved': rep_gbs, 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': rep_gbs / HBM_PEAK_GBS, 'traffic': _traffic('replay_c2'),
+        'roofline': {'bound': 'hbm', 'kernel': 'elr::k_replay_wpr<2, 3, 2>', 'achieved': rep_gbs, 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': rep_gbs / HBM_PEAK_GBS, 'traffic': _traffic('elr::k_replay_wpr<2, 3, 2>'),
                      'algorithmic_bytes_per_launch': rb, 'mean_launch_ms': rep_ms},
         'kernels': {'replay': {'ms': rep_ms, 'GBps': rep_gbs, 'bytes': rb},
                     'adam': {'ms': adam_ms, 'GBps': ab / (adam_ms * 1e-3) / 1e9, 'bytes': ab,
@@ -152,14 +152,18 @@ def headline(args):
     return res
 
 
-def _traffic(name):
-    """HBM bytes per launch measured by rocprofv3 PMC passes (committed under profiles/), or None."""
-    p = ROOT / 'profiles' / f'traffic_{name}.json'
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get('bytes_per_launch')
-        except (ValueError, OSError):
-            return None
+def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, each
+    scaled by the same counter's reading for a copy kernel of known size), or None if absent."""
+    p = ROOT / 'profiles' / profile
+    if not p.exists():
+        return None
+    cur = None
+    for line in p.read_text().splitlines():
+        if line.startswith('kernel: '):
+            cur = line[len('kernel: '):].strip()
+        elif line.startswith('bytes_per_launch = ') and cur and cur in kernel:
+            return int(float(line.split('=', 1)[1]))
     return None
 
 

@@ -1,0 +1,107 @@
+"""Summaries of rocprofv3 result databases (rocpd SQLite, the default output of rocprofv3 in ROCm 7.x).
+
+Counterpart of the reference's torch.profiler summary (srm2/profsum.py:10-25), for rocprofv3 runs:
+
+    python -m elara_amd.profsum stats  <run>_results.db            per-kernel calls / total / mean / share
+    python -m elara_amd.profsum pmc    <run>_results.db            per-kernel mean of each PMC counter per dispatch
+    python -m elara_amd.profsum traffic --kernel SUBSTR \
+        --fetch F.db --write W.db --copy-fetch CF.db --copy-write CW.db --copy-bytes N
+                                                                   HBM bytes per launch of one kernel, with
+                                                                   FETCH_SIZE / WRITE_SIZE (KiB per dispatch)
+                                                                   scaled by what the same counters read for a
+                                                                   plain copy kernel of N bytes read and written
+
+Only the standard library is used, so the summaries can be made on any host from the .db files.
+"""
+import argparse
+import sqlite3
+import sys
+
+
+def _rows(db, sql):
+    con = sqlite3.connect(db)
+    try:
+        return con.execute(sql).fetchall()
+    finally:
+        con.close()
+
+
+def kernel_stats(db):
+    """[(name, calls, total_us, mean_us, pct)] from the top_kernels view (durations in microseconds)."""
+    return [(n, int(c), float(t), float(a), float(p))
+            for n, c, t, a, p in _rows(db, 'select name, total_calls, total_duration, average, percentage '
+                                           'from top_kernels order by total_duration desc')]
+
+
+def pmc_means(db):
+    """{(kernel name, counter): (dispatches, mean value per dispatch)}."""
+    out = {}
+    for n, cn, cnt, avg in _rows(db, 'select name, counter_name, count(*), avg(counter_value) from pmc_events '
+                                     'group by name, counter_name'):
+        out[(n, cn)] = (int(cnt), float(avg))
+    return out
+
+
+def _pick(means, counter, substr):
+    hits = [(k, v) for k, v in means.items() if k[1] == counter and substr in k[0]]
+    if len(hits) != 1:
+        raise SystemExit(f'{counter}: expected one kernel matching {substr!r}, found {[k[0] for k, _ in hits]}')
+    return hits[0][1][1]
+
+
+def short(name, width=72):
+    return name if len(name) <= width else name[:width - 3] + '...'
+
+
+def cmd_stats(a):
+    print(f'| kernel | calls | total us | mean us | % |\n|---|---:|---:|---:|---:|')
+    for n, c, t, m, p in kernel_stats(a.db):
+        print(f'| `{short(n)}` | {c} | {t:.1f} | {m:.2f} | {p:.1f} |')
+
+
+def cmd_pmc(a):
+    print('| kernel | counter | dispatches | mean per dispatch |\n|---|---|---:|---:|')
+    for (n, cn), (cnt, avg) in sorted(pmc_means(a.db).items()):
+        print(f'| `{short(n)}` | {cn} | {cnt} | {avg:.2f} |')
+
+
+def cmd_traffic(a):
+    f_kib = _pick(pmc_means(a.fetch), 'FETCH_SIZE', a.kernel)
+    w_kib = _pick(pmc_means(a.write), 'WRITE_SIZE', a.kernel)
+    cf_kib = _pick(pmc_means(a.copy_fetch), 'FETCH_SIZE', a.copy_kernel)
+    cw_kib = _pick(pmc_means(a.copy_write), 'WRITE_SIZE', a.copy_kernel)
+    f_scale = a.copy_bytes / (cf_kib * 1024.0)
+    w_scale = a.copy_bytes / (cw_kib * 1024.0)
+    rd = f_kib * 1024.0 * f_scale
+    wr = w_kib * 1024.0 * w_scale
+    print(f'kernel: {a.kernel}')
+    print(f'FETCH_SIZE_KiB_per_dispatch = {f_kib:.2f}')
+    print(f'WRITE_SIZE_KiB_per_dispatch = {w_kib:.2f}')
+    print(f'copy_bytes = {a.copy_bytes}')
+    print(f'copy_FETCH_SIZE_KiB = {cf_kib:.2f}   fetch_scale = {f_scale:.4f}')
+    print(f'copy_WRITE_SIZE_KiB = {cw_kib:.2f}   write_scale = {w_scale:.4f}')
+    print(f'read_bytes_per_launch = {rd:.0f}')
+    print(f'write_bytes_per_launch = {wr:.0f}')
+    print(f'bytes_per_launch = {rd + wr:.0f}')
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = ap.add_subparsers(dest='cmd', required=True)
+    s = sub.add_parser('stats'); s.add_argument('db'); s.set_defaults(fn=cmd_stats)
+    p = sub.add_parser('pmc'); p.add_argument('db'); p.set_defaults(fn=cmd_pmc)
+    t = sub.add_parser('traffic')
+    t.add_argument('--kernel', required=True)
+    t.add_argument('--fetch', required=True)
+    t.add_argument('--write', required=True)
+    t.add_argument('--copy-fetch', required=True)
+    t.add_argument('--copy-write', required=True)
+    t.add_argument('--copy-kernel', default='copyBuffer')
+    t.add_argument('--copy-bytes', type=int, default=1 << 30)
+    t.set_defaults(fn=cmd_traffic)
+    a = ap.parse_args(argv)
+    a.fn(a)
+
+
+if __name__ == '__main__':
+    sys.exit(main())
