@@ -31,7 +31,25 @@ SIGNATURES = {
     'elr_init_rows': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_u32, c_f32, c_vp]),
     'elr_replay_rows': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_u32,
                                        c_f32, c_vp, c_i64, c_vp]),
+    'elr_dir_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_dir_a': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64] + [c_vp] * 9
+                  + [c_vp, c_i64, c_vp]),
+    'elr_dir_b': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64,
+                                 c_vp]),
 }
+
+DIR_FIELDS = ('code', 'loc', 'ent', 'lstep', 'lfree', 'n_lfree', 'log_top', 'mat_top', 'live', 'adm_c0', 'rj',
+              'pstep', 'kthr', 'toff', 'slot_of', 'slot_row', 'rok')
+
+
+class DirState(ctypes.Structure):
+    """elr_dir_state: the 17 device pointers of the directory (srm2/csrc/elara_dir.cpp:8-10) and T."""
+    _fields_ = [(n, c_vp) for n in DIR_FIELDS] + [('T', c_i64)]
+
+
+class DirParams(ctypes.Structure):
+    """elr_dir_params: the reference's pv = (R, K, Lcap, n0, Cdyn, MAT, trash, evl) (elara_dir.cpp:11)."""
+    _fields_ = [(n, c_i64) for n in ('R', 'K', 'Lcap', 'n0', 'Cdyn', 'MAT', 'trash', 'evl')]
 
 
 def lib():

@@ -1,0 +1,499 @@
+// ELARA state directory on the GPU: row codes (I / L_c / M), log-entry ids and steps, sync-free allocators.
+//
+// Replaces srm2/csrc/elara_dir.cpp:13-110 (elara_dir_a / elara_dir_b, the reference's default directory
+// implementation) with the same results and the same allocation order ("cpp" order):
+//   call A:  replay inputs of L rows; resident-history recording of hits; eviction representation
+//            (back to L: log ids for the resident history, MAT trash slot; to M: MAT slot, release host logs)
+//   call B:  appends (stay L, one log id each), then compactions (to M: MAT slot, release all logs)
+// Allocation ranks are exclusive prefix counts in row-major (item, k) order: the log allocator pops the free stack
+// top-down and then bumps log_top (elara_dir.cpp:13-21), MAT slots bump mat_top (elara_dir.cpp:36-44), releases
+// push onto the free stack at n_lfree + rank (elara_dir.cpp:23-34).
+//
+// The device counters n_lfree, log_top, mat_top, live stay in HBM; nothing is read back to the host.  Grid-wide
+// ranks come from a three-step scan: per-block counts, one single-block scan that also advances the counters
+// (keeping their old values in scratch), then an apply pass.  Stack pops and pushes are separate launches,
+// because a push may reuse a stack position that another block still has to pop.
+//
+// Trash conventions are the reference's (srm2/elara.py:119-123): loc/ent row R, pstep row Cdyn, MAT slot `trash`.
+// The reference scatters values of invalid entries into lstep[Lcap] and lfree[Lcap] (which value lands there is
+// unspecified on a GPU); this implementation does not write those two trash elements.
+//
+// Index safety: every gathered or scattered index is checked against its array's extent; an item whose slot, row
+// or entry id is out of range is treated as carrying nothing (no writes).  The reference leaves such inputs
+// undefined.
+#include "elr_common.h"
+
+namespace elr {
+
+constexpr int kDirBlock = 256;
+constexpr int kScanBlock = 1024;
+
+// Old counter values kept by the scan step for the apply steps.
+struct DirHdr {
+  int64_t nf0;   // n_lfree before this call's log allocation
+  int64_t top0;  // log_top before it
+  int64_t mt0;   // mat_top before this call's MAT allocation
+  int64_t nf1;   // n_lfree after the log allocation (push base of the releases)
+};
+
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(v, d, 64);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// Exclusive prefix of v[c] over the threads of the block (kDirBlock threads) and the block totals.
+template <int NCH>
+__device__ __forceinline__ void block_excl_scan(const int (&v)[NCH], int (&ex)[NCH], int (&tot)[NCH]) {
+  __shared__ int wsum[NCH][kDirBlock / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    inc[c] = wave_incl_scan(v[c]);
+    if (lane == 63) wsum[c][w] = inc[c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    int base = 0, t = 0;
+#pragma unroll
+    for (int q = 0; q < kDirBlock / 64; ++q) {
+      const int x = wsum[c][q];
+      base += q < w ? x : 0;
+      t += x;
+    }
+    ex[c] = base + inc[c] - v[c];
+    tot[c] = t;
+  }
+}
+
+__device__ __forceinline__ bool in_range(int64_t x, int64_t hi) { return x >= 0 && x < hi; }
+
+// searchsorted(toff, row, right=True) - 1, with ATen's wrap of index -1 to T-1 (elara_dir.cpp:46-48, 75).
+__device__ __forceinline__ int64_t table_of(const int64_t* __restrict__ toff, int64_t T, int64_t row) {
+  int64_t lo = 0, hi = T;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (toff[mid] <= row) lo = mid + 1; else hi = mid;
+  }
+  const int64_t t = lo - 1;
+  return t < 0 ? t + T : t;
+}
+
+// Log id of allocation rank `rank` (elara_dir.cpp:15-17): free stack top-down first, then the bump pointer.
+__device__ __forceinline__ int64_t log_id_of_rank(const int32_t* __restrict__ lfree, int64_t Lcap, int64_t nf0,
+                                                  int64_t top0, int64_t rank) {
+  if (rank < nf0) {
+    const int64_t fi = nf0 - 1 - rank;
+    return in_range(fi, Lcap + 1) ? (int64_t)lfree[fi] : -1;
+  }
+  return top0 + rank - nf0;
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// A1: replay inputs of L rows (elara_dir.cpp:56-59) and resident-history recording of hits (elara_dir.cpp:60-71).
+// Threads [0, nL*K) take one (row, k) entry each; threads [nL*K, nL*K + nh) take one hit slot each.  The two parts
+// touch disjoint arrays (ent/lstep are read; pstep/rj/rok are written), and hit slots are unique.
+__global__ __launch_bounds__(kDirBlock) void k_dir_lsteps_hits(elr_dir_state st, elr_dir_params p,
+                                                               const int64_t* __restrict__ hs, int64_t nh,
+                                                               const int64_t* __restrict__ L_row,
+                                                               const int32_t* __restrict__ L_cnt, int64_t nL,
+                                                               int32_t s, int32_t* __restrict__ L_steps,
+                                                               int32_t* __restrict__ L_ids,
+                                                               int64_t* __restrict__ hrec_dyn,
+                                                               int64_t* __restrict__ hrec_j) {
+  const int64_t t = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+  const int64_t K = p.K, nLK = nL * K;
+  if (t < nLK) {
+    const int64_t i = t / K, k = t - i * K;
+    const int64_t row = L_row[i];
+    int32_t e = -1;
+    if (in_range(row, p.R + 1)) e = st.ent[row * K + k];
+    L_steps[t] = (e >= 0 && e <= p.Lcap) ? st.lstep[e] : 0;
+    L_ids[t] = k < (int64_t)L_cnt[i] ? e : -1;
+    return;
+  }
+  const int64_t i = t - nLK;
+  if (i >= nh) return;
+  const int64_t sl = hs[i];
+  const int64_t C = p.n0 + p.Cdyn;
+  if (!in_range(sl, C)) {
+    hrec_dyn[i] = p.Cdyn;
+    hrec_j[i] = 0;
+    return;
+  }
+  const bool dyn = sl >= p.n0;
+  const int64_t c0 = st.adm_c0[sl], j = st.rj[sl];
+  const bool ok = st.rok[sl] != 0;
+  const bool rec = p.evl && dyn && ok && (c0 + j < K);
+  const int64_t hd = rec ? sl - p.n0 : p.Cdyn, hj = rec ? j : 0;
+  hrec_dyn[i] = hd;
+  hrec_j[i] = hj;
+  if (in_range(hj, K)) st.pstep[hd * K + hj] = s;  // non-recorded hits write the trash row (Cdyn, 0), as the reference
+  st.rj[sl] = (int8_t)(j + (rec ? 1 : 0));
+  st.rok[sl] = (int8_t)(ok && !(dyn && !rec));
+}
+
+// Per-item quantities of an eviction (elara_dir.cpp:73-77, 80, 89, 92).
+struct EvCounts {
+  int nalloc;  // log ids for the resident history (rows going back to L): k < j
+  int nmat;    // 1 if the row goes to M and has no MAT slot yet
+  int nrel;    // host-log entries released (rows going to M): k < max(c0, 0) with ent >= 0
+};
+
+__device__ __forceinline__ EvCounts ev_counts(const elr_dir_state& st, const elr_dir_params& p, int64_t row, bool rep,
+                                              int64_t c0, int64_t j) {
+  EvCounts c{0, 0, 0};
+  if (!in_range(row, p.R)) return c;
+  const int64_t K = p.K;
+  if (rep) {
+    c.nalloc = (int)(j < 0 ? 0 : (j > K ? K : j));
+  } else {
+    c.nmat = st.loc[row] < 0 ? 1 : 0;
+    const int64_t cnt = c0 > 0 ? c0 : 0;
+    for (int64_t k = 0; k < K && k < cnt; ++k) c.nrel += st.ent[row * K + k] >= 0 ? 1 : 0;
+  }
+  return c;
+}
+
+// A2: eviction representation and per-block allocation counts (elara_dir.cpp:73-78).
+__global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st, elr_dir_params p,
+                                                               const int64_t* __restrict__ ev_slot, int64_t nev,
+                                                               int64_t* __restrict__ ev_row, uint8_t* __restrict__ rep,
+                                                               int64_t* __restrict__ ev_dyn,
+                                                               int64_t* __restrict__ bsum, int64_t nblk) {
+  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+  int v[3] = {0, 0, 0};
+  if (i < nev) {
+    const int64_t sl = ev_slot[i];
+    const int64_t C = p.n0 + p.Cdyn;
+    int64_t row = -1, c0 = -1, j = 0;
+    bool rp = false;
+    if (in_range(sl, C)) {
+      row = st.slot_row[sl];
+      c0 = st.adm_c0[sl];
+      j = st.rj[sl];
+      if (p.evl && in_range(row, p.R))
+        rp = st.rok[sl] != 0 && (c0 + j) <= (int64_t)st.kthr[table_of(st.toff, st.T, row)];
+      if (in_range(row, p.R)) st.slot_of[row] = -1;
+      st.slot_row[sl] = -1;
+    }
+    ev_row[i] = row;
+    rep[i] = rp ? 1 : 0;
+    ev_dyn[i] = sl - p.n0;
+    const EvCounts c = ev_counts(st, p, row, rp, c0, j);
+    v[0] = c.nalloc;
+    v[1] = c.nmat;
+    v[2] = c.nrel;
+  }
+  int ex[3], tot[3];
+  block_excl_scan<3>(v, ex, tot);
+  if (threadIdx.x == 0)
+    for (int c = 0; c < 3; ++c) bsum[c * nblk + blockIdx.x] = tot[c];
+}
+
+// Single-block exclusive scan of the per-block counts of `nch` channels (in place) and the counter update.
+// Channel roles: mode 0 (call A): 0 = log allocations, 1 = MAT allocations, 2 = releases.
+//                mode 1 (call B): 0 = MAT allocations, 1 = releases; `nappend` log allocations (rank = item).
+// Counter arithmetic of elara_dir.cpp:18-19 (alloc), 31 (release), 42 (MAT), in the reference's order: log
+// allocation, MAT allocation, release.
+__global__ __launch_bounds__(kScanBlock) void k_dir_scan(elr_dir_state st, int mode, int64_t nappend,
+                                                         int64_t* __restrict__ bsum, int64_t nblk, int nch,
+                                                         DirHdr* __restrict__ hdr) {
+  __shared__ int64_t wtot[kScanBlock / 64];
+  __shared__ int64_t chan_tot[3];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int c = 0; c < nch; ++c) {
+    int64_t carry = 0;
+    for (int64_t b0 = 0; b0 < nblk; b0 += kScanBlock) {
+      const int64_t b = b0 + threadIdx.x;
+      const int64_t x = b < nblk ? bsum[c * nblk + b] : 0;
+      int64_t inc = x;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int64_t t = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += t;
+      }
+      if (lane == 63) wtot[w] = inc;
+      __syncthreads();
+      int64_t base = 0, all = 0;
+      for (int q = 0; q < kScanBlock / 64; ++q) {
+        base += q < w ? wtot[q] : 0;
+        all += wtot[q];
+      }
+      if (b < nblk) bsum[c * nblk + b] = carry + base + inc - x;
+      carry += all;
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) chan_tot[c] = carry;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int64_t nalloc = mode == 0 ? chan_tot[0] : nappend;
+    const int64_t nmat = mode == 0 ? chan_tot[1] : (nch > 0 ? chan_tot[0] : 0);
+    const int64_t nrel = mode == 0 ? chan_tot[2] : (nch > 1 ? chan_tot[1] : 0);
+    DirHdr h;
+    h.nf0 = *st.n_lfree;
+    h.top0 = *st.log_top;
+    h.mt0 = *st.mat_top;
+    const int64_t used = nalloc < h.nf0 ? nalloc : h.nf0;
+    h.nf1 = h.nf0 - used;
+    *st.log_top = h.top0 + nalloc - used;
+    *st.mat_top = h.mt0 + nmat;
+    *st.n_lfree = h.nf1 + nrel;
+    *st.live = *st.live + nalloc - nrel;
+    *hdr = h;
+  }
+}
+
+// A4: apply the eviction representation (elara_dir.cpp:79-93 except the stack pushes): log ids of rows going back
+// to L (ent, lstep), MAT slots (loc, evf_slots), codes; records each item's release rank for A5.
+__global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st, elr_dir_params p,
+                                                               const int64_t* __restrict__ ev_slot, int64_t nev,
+                                                               const int64_t* __restrict__ ev_row,
+                                                               const uint8_t* __restrict__ rep,
+                                                               const int64_t* __restrict__ ev_dyn,
+                                                               int64_t* __restrict__ evl_ids,
+                                                               int64_t* __restrict__ evf_slots,
+                                                               const int64_t* __restrict__ boff, int64_t nblk,
+                                                               const DirHdr* __restrict__ hdr,
+                                                               int64_t* __restrict__ rel_rank) {
+  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+  const int64_t K = p.K;
+  int64_t row = -1, c0 = -1, j = 0;
+  bool rp = false;
+  EvCounts c{0, 0, 0};
+  if (i < nev) {
+    const int64_t sl = ev_slot[i];
+    row = ev_row[i];
+    rp = rep[i] != 0;
+    if (in_range(sl, p.n0 + p.Cdyn)) {
+      c0 = st.adm_c0[sl];
+      j = st.rj[sl];
+    }
+    c = ev_counts(st, p, row, rp, c0, j);
+  }
+  int v[3] = {c.nalloc, c.nmat, c.nrel}, ex[3], tot[3];
+  block_excl_scan<3>(v, ex, tot);
+  if (i >= nev) return;
+  const DirHdr h = *hdr;
+  // log ids for the resident history: ent[row, max(c0,0) + k] = id, lstep[id] = pstep[dyn, k]  (k < j)
+  const int64_t rA = boff[0 * nblk + blockIdx.x] + ex[0];
+  int64_t dyn = ev_dyn[i];
+  if (!in_range(dyn, p.Cdyn)) dyn = p.Cdyn;
+  const int64_t kb = c0 > 0 ? c0 : 0;
+  for (int64_t k = 0; k < K; ++k) {
+    int64_t id = -1;
+    if (k < c.nalloc) {
+      id = log_id_of_rank(st.lfree, p.Lcap, h.nf0, h.top0, rA + k);
+      if (kb + k < K) st.ent[row * K + kb + k] = (int32_t)id;
+      if (in_range(id, p.Lcap)) st.lstep[id] = st.pstep[dyn * K + k];
+    }
+    evl_ids[i * K + k] = id;
+  }
+  // MAT slot for rows going to M (elara_dir.cpp:36-44, 89-90); rows going back to L get the trash slot
+  int64_t slot = -1;
+  if (in_range(row, p.R)) {
+    const int64_t cur = st.loc[row];
+    slot = c.nmat ? h.mt0 + boff[1 * nblk + blockIdx.x] + ex[1] : cur;
+    if (c.nmat) st.loc[row] = (int32_t)slot;
+    const int64_t tj = c0 + j;
+    st.code[row] = rp ? (int8_t)(tj < 127 ? tj : 127) : (int8_t)p.MAT;
+  }
+  evf_slots[i] = rp ? p.trash : slot;
+  rel_rank[i] = boff[2 * nblk + blockIdx.x] + ex[2];
+}
+
+// Push the released entries of rows[i] (k < cnt, ent >= 0; `rank` = item's first push rank) and clear them
+// (elara_dir.cpp:25-33).
+__device__ __forceinline__ void release_row(const elr_dir_state& st, const elr_dir_params& p, int64_t row,
+                                            int64_t cnt, int64_t push_at) {
+  const int64_t K = p.K;
+  int64_t q = 0;
+  for (int64_t k = 0; k < K && k < cnt; ++k) {
+    const int32_t e = st.ent[row * K + k];
+    if (e >= 0) {
+      const int64_t dst = push_at + q++;
+      if (in_range(dst, p.Lcap)) st.lfree[dst] = e;
+      st.ent[row * K + k] = -1;
+    }
+  }
+}
+
+// A5: releases of rows going to M (after every pop of this call).
+__global__ __launch_bounds__(kDirBlock) void k_dir_evict_release(elr_dir_state st, elr_dir_params p,
+                                                                 const int64_t* __restrict__ ev_slot, int64_t nev,
+                                                                 const int64_t* __restrict__ ev_row,
+                                                                 const uint8_t* __restrict__ rep,
+                                                                 const int64_t* __restrict__ rel_rank,
+                                                                 const DirHdr* __restrict__ hdr) {
+  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+  if (i >= nev || rep[i]) return;
+  const int64_t row = ev_row[i], sl = ev_slot[i];
+  if (!in_range(row, p.R) || !in_range(sl, p.n0 + p.Cdyn)) return;
+  const int64_t c0 = st.adm_c0[sl];
+  release_row(st, p, row, c0 > 0 ? c0 : 0, hdr->nf1 + rel_rank[i]);
+}
+
+// B1: appends (elara_dir.cpp:102-106; log id of append i has rank i) and per-block counts of the compactions
+// (MAT slots needed, entries released).  Appended and compacted rows are disjoint.
+__global__ __launch_bounds__(kDirBlock) void k_dir_b_count(elr_dir_state st, elr_dir_params p,
+                                                           const int64_t* __restrict__ a_rows,
+                                                           const int64_t* __restrict__ a_k, int64_t na,
+                                                           const int64_t* __restrict__ c_rows,
+                                                           const int64_t* __restrict__ c_cnt, int64_t nc, int32_t s,
+                                                           int64_t* __restrict__ a_ids, int64_t* __restrict__ bsum,
+                                                           int64_t nblk_c, int64_t nblk_a) {
+  const int64_t K = p.K;
+  if ((int64_t)blockIdx.x < nblk_a) {
+    const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+    if (i >= na) return;
+    const int64_t id = log_id_of_rank(st.lfree, p.Lcap, *st.n_lfree, *st.log_top, i);
+    a_ids[i] = id;
+    const int64_t row = a_rows[i], k = a_k[i];
+    if (in_range(row, p.R) && in_range(k, K)) {
+      st.ent[row * K + k] = (int32_t)id;
+      st.code[row] = (int8_t)(k + 1);
+    }
+    if (in_range(id, p.Lcap)) st.lstep[id] = s;
+    return;
+  }
+  const int64_t b = (int64_t)blockIdx.x - nblk_a;
+  const int64_t i = b * kDirBlock + threadIdx.x;
+  int v[2] = {0, 0};
+  if (i < nc) {
+    const int64_t row = c_rows[i];
+    if (in_range(row, p.R)) {
+      v[0] = st.loc[row] < 0 ? 1 : 0;
+      const int64_t cnt = c_cnt[i];
+      for (int64_t k = 0; k < K && k < cnt; ++k) v[1] += st.ent[row * K + k] >= 0 ? 1 : 0;
+    }
+  }
+  int ex[2], tot[2];
+  block_excl_scan<2>(v, ex, tot);
+  if (threadIdx.x == 0) {
+    bsum[0 * nblk_c + b] = tot[0];
+    bsum[1 * nblk_c + b] = tot[1];
+  }
+}
+
+// B3: compactions (elara_dir.cpp:107-108): MAT slot, release of all logs, code = MAT.
+__global__ __launch_bounds__(kDirBlock) void k_dir_b_compact(elr_dir_state st, elr_dir_params p,
+                                                             const int64_t* __restrict__ c_rows,
+                                                             const int64_t* __restrict__ c_cnt, int64_t nc,
+                                                             int64_t* __restrict__ c_slots,
+                                                             const int64_t* __restrict__ boff, int64_t nblk,
+                                                             const DirHdr* __restrict__ hdr) {
+  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+  const int64_t K = p.K;
+  int64_t row = -1, cnt = 0, cur = -1;
+  int v[2] = {0, 0};
+  if (i < nc) {
+    row = c_rows[i];
+    cnt = c_cnt[i];
+    if (in_range(row, p.R)) {
+      cur = st.loc[row];
+      v[0] = cur < 0 ? 1 : 0;
+      for (int64_t k = 0; k < K && k < cnt; ++k) v[1] += st.ent[row * K + k] >= 0 ? 1 : 0;
+    }
+  }
+  int ex[2], tot[2];
+  block_excl_scan<2>(v, ex, tot);
+  if (i >= nc) return;
+  if (!in_range(row, p.R)) {
+    c_slots[i] = -1;
+    return;
+  }
+  const DirHdr h = *hdr;
+  const int64_t slot = v[0] ? h.mt0 + boff[0 * nblk + blockIdx.x] + ex[0] : cur;
+  if (v[0]) st.loc[row] = (int32_t)slot;
+  c_slots[i] = slot;
+  release_row(st, p, row, cnt, h.nf1 + boff[1 * nblk + blockIdx.x] + ex[1]);
+  st.code[row] = (int8_t)p.MAT;
+}
+
+inline int64_t nblocks(int64_t n) { return (n + kDirBlock - 1) / kDirBlock; }
+inline int64_t align8(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+// Scratch layout: [DirHdr][bsum: nch * nblk int64][per-item release ranks: nev int64]
+inline int64_t dir_a_scratch(int64_t nev) { return align8(sizeof(DirHdr)) + align8(3 * nblocks(nev) * 8) + nev * 8; }
+inline int64_t dir_b_scratch(int64_t nc) { return align8(sizeof(DirHdr)) + align8(2 * nblocks(nc) * 8); }
+
+inline bool params_ok(const elr_dir_state* st, const elr_dir_params* p) {
+  return st && p && p->K >= 1 && p->K <= 126 && p->R >= 0 && p->Lcap >= 0 && p->n0 >= 0 && p->Cdyn >= 0 &&
+         st->code && st->loc && st->ent && st->lstep && st->lfree && st->n_lfree && st->log_top && st->mat_top &&
+         st->live && st->adm_c0 && st->rj && st->pstep && st->kthr && st->toff && st->slot_of && st->slot_row &&
+         st->rok && st->T >= 1;
+}
+
+}  // namespace elr
+
+extern "C" int64_t elr_dir_scratch_bytes(int64_t nev, int64_t nc) {
+  if (nev < 0 || nc < 0) return ELR_EINVAL;
+  const int64_t a = elr::dir_a_scratch(nev), b = elr::dir_b_scratch(nc);
+  return a > b ? a : b;
+}
+
+extern "C" int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const int64_t* hs, int64_t nh,
+                         const int64_t* L_row, const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot, int64_t nev,
+                         int64_t s, int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j,
+                         int64_t* ev_row, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn,
+                         void* scratch, int64_t scratch_bytes, void* stream) {
+  using namespace elr;
+  if (!params_ok(st, p) || nh < 0 || nL < 0 || nev < 0) return ELR_EINVAL;
+  if ((nh && (!hs || !hrec_dyn || !hrec_j)) || (nL && (!L_row || !L_cnt || !L_steps || !L_ids)) ||
+      (nev && (!ev_slot || !ev_row || !rep || !evl_ids || !evf_slots || !ev_dyn)))
+    return ELR_EINVAL;
+  if (nev && (!scratch || scratch_bytes < dir_a_scratch(nev))) return ELR_ECAPACITY;
+  hipStream_t strm = (hipStream_t)stream;
+  const elr_dir_state S = *st;
+  const elr_dir_params P = *p;
+  const int32_t s32 = (int32_t)s;
+  const int64_t n1 = nL * P.K + nh;
+  if (n1) {
+    k_dir_lsteps_hits<<<(unsigned)nblocks(n1), kDirBlock, 0, strm>>>(S, P, hs, nh, L_row, L_cnt, nL, s32, L_steps,
+                                                                     L_ids, hrec_dyn, hrec_j);
+  }
+  if (nev) {
+    char* base = (char*)scratch;
+    DirHdr* hdr = (DirHdr*)base;
+    const int64_t nblk = nblocks(nev);
+    int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
+    int64_t* rel_rank = (int64_t*)(base + align8(sizeof(DirHdr)) + align8(3 * nblk * 8));
+    k_dir_evict_count<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row, rep, ev_dyn, bsum, nblk);
+    k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 0, 0, bsum, nblk, 3, hdr);
+    k_dir_evict_apply<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row, rep, ev_dyn, evl_ids,
+                                                              evf_slots, bsum, nblk, hdr, rel_rank);
+    k_dir_evict_release<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row, rep, rel_rank, hdr);
+  }
+  return launch_status();
+}
+
+extern "C" int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,
+                         int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s,
+                         int64_t* a_ids, int64_t* c_slots, void* scratch, int64_t scratch_bytes, void* stream) {
+  using namespace elr;
+  if (!params_ok(st, p) || na < 0 || nc < 0) return ELR_EINVAL;
+  if ((na && (!a_rows || !a_k || !a_ids)) || (nc && (!c_rows || !c_cnt || !c_slots))) return ELR_EINVAL;
+  if (na == 0 && nc == 0) return ELR_OK;
+  if (!scratch || scratch_bytes < dir_b_scratch(nc)) return ELR_ECAPACITY;
+  hipStream_t strm = (hipStream_t)stream;
+  const elr_dir_state S = *st;
+  const elr_dir_params P = *p;
+  char* base = (char*)scratch;
+  DirHdr* hdr = (DirHdr*)base;
+  const int64_t nblk_c = nblocks(nc), nblk_a = nblocks(na);
+  int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
+  k_dir_b_count<<<(unsigned)(nblk_a + nblk_c), kDirBlock, 0, strm>>>(S, P, a_rows, a_k, na, c_rows, c_cnt, nc,
+                                                                     (int32_t)s, a_ids, bsum, nblk_c, nblk_a);
+  k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 1, na, bsum, nblk_c, 2, hdr);
+  if (nc) {
+    k_dir_b_compact<<<(unsigned)nblk_c, kDirBlock, 0, strm>>>(S, P, c_rows, c_cnt, nc, c_slots, bsum, nblk_c, hdr);
+  }
+  return launch_status();
+}

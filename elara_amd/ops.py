@@ -2,6 +2,7 @@
 
     gpu_adam(pool, slots, grad, lr, b1, b2, eps, step)       srm2/ops.py:59-67
     ext().adam_scalars(lr, b1, b2, eps, step) -> [8 floats]  srm2/csrc/srm2_cpu.cpp:255-257
+    dir_ext().elara_dir_a / elara_dir_b                      srm2/ops.py:32-39 (defined in elara_amd.elara_dir)
 
 The update runs in the HIP kernel behind elr_adam_rows (elara_amd/csrc/adam.hip) on torch's current stream;
 there is no other implementation in the product path.
@@ -9,6 +10,7 @@ there is no other implementation in the product path.
 import torch
 
 from . import _lib
+from .elara_dir import dir_ext  # noqa: F401  (the reference exposes dir_ext from ops)
 
 
 def adam_scalars(lr, b1, b2, eps, step):

@@ -79,6 +79,60 @@ int elr_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t 
                     const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed, float bound,
                     const float* table, int64_t table_rows, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * State directory.
+ * Replaces: srm2/csrc/elara_dir.cpp (state layout 8-11; elara_dir_a 50-96; elara_dir_b 98-110), the reference's
+ * default directory implementation, with the same results and allocation order.  All pointers in the two
+ * structs are device pointers (the structs themselves are host memory, read at the call).  Row codes: 0 = I,
+ * 1..K = L_c, MAT = K + 1 = M.  Trash: loc/ent row R, lstep/lfree index Lcap, pstep row Cdyn.
+ * ------------------------------------------------------------------------------------------------------- */
+typedef struct elr_dir_state {
+  int8_t* code;         /* [R]          row codes */
+  int32_t* loc;         /* [R+1]        MAT slot of each row (-1: none) */
+  int32_t* ent;         /* [(R+1)*K]    log-entry ids of each row (-1: none) */
+  int32_t* lstep;       /* [Lcap+1]     logical step of each log entry */
+  int32_t* lfree;       /* [Lcap+1]     free stack of log ids */
+  int64_t* n_lfree;     /* [1]          free-stack depth */
+  int64_t* log_top;     /* [1]          bump pointer of the log arena */
+  int64_t* mat_top;     /* [1]          bump pointer of the MAT arena */
+  int64_t* live;        /* [1]          live log entries */
+  int8_t* adm_c0;       /* [C]          host log entries of the slot's row at admission (-1: admitted from M) */
+  int8_t* rj;           /* [C]          gradients recorded while resident */
+  int32_t* pstep;       /* [Cdyn+1, K]  steps of the resident history */
+  const int8_t* kthr;   /* [T]          per-table materialisation threshold */
+  const int64_t* toff;  /* [T]          first row of each table (ascending) */
+  int32_t* slot_of;     /* [R]          pool slot of each row (-1: not resident) */
+  int64_t* slot_row;    /* [C]          row held by each pool slot (-1: empty) */
+  int8_t* rok;          /* [C]          resident history still representable as logs */
+  int64_t T;            /* number of tables */
+} elr_dir_state;
+
+/* The reference's parameter vector pv (elara_dir.cpp:11, srm2/elara.py:277): C = n0 + Cdyn pool slots. */
+typedef struct elr_dir_params {
+  int64_t R, K, Lcap, n0, Cdyn, MAT, trash, evl;
+} elr_dir_params;
+
+/* Bytes of device scratch elr_dir_a (nev evictions) and elr_dir_b (nc compactions) need (max of both), or a
+ * negative code. */
+int64_t elr_dir_scratch_bytes(int64_t nev, int64_t nc);
+
+/* Call A (elara_dir.cpp:50-96): replay inputs of the L rows L_row [nL] (counts L_cnt int32 [nL]) ->
+ * L_steps int32 [nL,K], L_ids int32 [nL,K]; resident-history recording of the hit slots hs [nh] -> hrec_dyn,
+ * hrec_j int64 [nh]; eviction of the pool slots ev_slot [nev] -> ev_row int64 [nev], rep uint8 [nev] (1: back to
+ * L), evl_ids int64 [nev,K], evf_slots int64 [nev], ev_dyn int64 [nev].  Mutates the directory.  Inputs hs,
+ * L_row, ev_slot int64.  `scratch` (device, >= elr_dir_scratch_bytes(nev, 0) bytes) is needed when nev > 0. */
+int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const int64_t* hs, int64_t nh, const int64_t* L_row,
+              const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot, int64_t nev, int64_t s, int32_t* L_steps,
+              int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, int64_t* ev_row, uint8_t* rep, int64_t* evl_ids,
+              int64_t* evf_slots, int64_t* ev_dyn, void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Call B (elara_dir.cpp:98-110): appends of rows a_rows [na] at entry a_k [na] -> a_ids int64 [na]; compactions of
+ * rows c_rows [nc] with c_cnt [nc] logged entries -> c_slots int64 [nc].  All inputs int64.  Mutates the
+ * directory.  `scratch` (device, >= elr_dir_scratch_bytes(0, nc) bytes) is needed when na + nc > 0. */
+int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k, int64_t na,
+              const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids, int64_t* c_slots,
+              void* scratch, int64_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,153 @@
+"""State directory (srm2/csrc/elara_dir.cpp elara_dir_a / elara_dir_b): the C oracle against the reference's own
+build (oracle/_ref, CPU tensors) and the HIP path (elr_dir_a / elr_dir_b through the C-ABI) against both.
+
+Every step compares all 9 + 2 outputs and the whole directory (17 arrays) bitwise, except the two trash elements
+lstep[Lcap] and lfree[Lcap], whose contents the reference leaves unspecified.  Each run also checks the invariants
+of srm2/train.py:474-477 (dir_check) and a few more (no id both live and free, codes match entry counts).
+"""
+import numpy as np
+import pytest
+
+from dirsim import (OracleImpl, Sim, TorchImpl, check_invariants, comparable_state, diff_outputs, diff_states)
+from oracle import oracle as O
+from oracle import ref
+
+needs_ref = pytest.mark.skipif(ref.dir() is None, reason='oracle/_ref not built (needs /root/reference)')
+
+CONFIGS = {
+    'default': dict(seed=1),
+    'k4_no_static': dict(seed=2, K=4, R=3000, C=500, n0=0, batch=400),
+    'evl_off': dict(seed=3, evl=False),
+    'k1_one_table': dict(seed=4, K=1, T=1, kthr=[1]),
+    'tight_pool': dict(seed=5, R=1500, C=120, n0=10, batch=300),
+}
+
+
+def run(sim, impls, steps):
+    """Drive `steps` plan steps; assert every implementation equals the first one after each call."""
+    for s in range(1, steps + 1):
+        outs = sim.step(s, impls)
+        va = comparable_state(impls[0].view(), sim)
+        for m, o in zip(impls[1:], outs[1:]):
+            d = diff_states(va, comparable_state(m.view(), sim))
+            ba, bb = diff_outputs(outs[0][0], o[0]), diff_outputs(outs[0][1], o[1])
+            assert not (d or ba or bb), f'step {s}: {type(m).__name__} differs: state {d}, outputs A {ba}, B {bb}'
+        check_invariants(impls[0].view(), sim)
+    return impls
+
+
+@needs_ref
+@pytest.mark.parametrize('name', sorted(CONFIGS))
+def test_oracle_matches_reference_directory(name):
+    sim = Sim(**CONFIGS[name])
+    st0 = sim.initial_state()
+    run(sim, [TorchImpl(sim, st0, ref.dir()), OracleImpl(sim, st0)], 60)
+
+
+def test_oracle_allocators_by_hand():
+    """Hand-worked allocation sequence: bump, release onto the stack, pops top-down (elara_dir.cpp:13-34)."""
+    R, C, K = 10, 4, 3
+    st = O.DirState(R, C, K, 0, np.array([0], np.int64), np.array([3], np.int8), log_cap=20)
+    pv = st.params(True)
+    # appends: rows 2, 5, 7 at k = 0 -> ids 0, 1, 2 (bump), code 1
+    a_ids, c_slots = O.dir_b(st, pv, [2, 5, 7], [0, 0, 0], [], [], 4)
+    assert a_ids.tolist() == [0, 1, 2] and st.log_top[0] == 3 and st.live[0] == 3 and st.n_lfree[0] == 0
+    assert st.code[[2, 5, 7]].tolist() == [1, 1, 1] and st.lstep[:3].tolist() == [4, 4, 4]
+    # compact rows 5 and 2 (1 entry each): MAT slots 0, 1; ids 1, 0 pushed in that order
+    a_ids, c_slots = O.dir_b(st, pv, [], [], [5, 2], [1, 1], 5)
+    assert c_slots.tolist() == [0, 1] and st.mat_top[0] == 2
+    assert st.lfree[:2].tolist() == [1, 0] and st.n_lfree[0] == 2 and st.live[0] == 1
+    assert st.code[[5, 2]].tolist() == [4, 4] and st.ent[5 * K] == -1 and st.ent[2 * K] == -1
+    # three appends: pop 0 (top), then 1, then bump 3
+    a_ids, _ = O.dir_b(st, pv, [1, 3, 4], [0, 0, 0], [], [], 6)
+    assert a_ids.tolist() == [0, 1, 3] and st.n_lfree[0] == 0 and st.log_top[0] == 4 and st.live[0] == 4
+    # compacting row 2 again keeps its MAT slot
+    _, c_slots = O.dir_b(st, pv, [], [], [2], [0], 7)
+    assert c_slots.tolist() == [1] and st.mat_top[0] == 2
+
+
+# ------------------------------------------------------------------------------------------------------------- GPU
+def gpu_impl(sim, st0, dev):
+    from elara_amd.elara_dir import dir_ext
+    return TorchImpl(sim, st0, dir_ext(), device=dev)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('name', sorted(CONFIGS))
+def test_gpu_directory_matches_oracle_and_reference(dev, name):
+    print(f'[gpu-test] directory {name}', flush=True)
+    sim = Sim(**CONFIGS[name])
+    st0 = sim.initial_state()
+    impls = [OracleImpl(sim, st0), gpu_impl(sim, st0, dev)]
+    if ref.dir() is not None:
+        impls.append(TorchImpl(sim, st0, ref.dir()))
+    run(sim, impls, 60)
+
+
+@pytest.mark.gpu
+def test_gpu_directory_large_multiblock(dev):
+    """Thousands of items per call: block offsets across many blocks of the grid-wide scans."""
+    print('[gpu-test] directory large', flush=True)
+    sim = Sim(seed=11, R=400_000, C=60_000, n0=5_000, K=3, T=6, batch=40_000, vocab_skew=0.9)
+    st0 = sim.initial_state()
+    run(sim, [OracleImpl(sim, st0), gpu_impl(sim, st0, dev)], 12)
+
+
+@pytest.mark.gpu
+def test_gpu_dir_b_scan_beyond_one_scan_block(dev):
+    """300,000 compactions in one call (more than 1024 blocks: the single-block scan loops over chunks with a
+    carry), then 200,000 appends that pop the whole free stack and continue with the bump pointer."""
+    import torch
+    from elara_amd.elara_dir import dir_ext
+    print('[gpu-test] dir_b large scan', flush=True)
+    rng = np.random.default_rng(12)
+    R, K, C = 1_200_000, 3, 8
+    st = O.DirState(R, C, K, 0, np.array([0], np.int64), np.array([3], np.int8))
+    pv = st.params(True)
+    perm = rng.permutation(R).astype(np.int64)
+    logged, fresh = perm[:700_000], perm[700_000:900_000]
+    cnt = rng.integers(1, 4, logged.size)
+    for k in range(3):                                  # rows get 1..3 log entries (oracle only)
+        sel = logged[cnt > k]
+        O.dir_b(st, pv, sel, np.full(sel.size, k, np.int64), [], [], 1 + k)
+    crow = logged[:300_000]
+    ccnt = np.where(rng.random(crow.size) < 0.1, cnt[:300_000], 0).astype(np.int64)
+    pre = crow[::2]                                     # half of them already hold a MAT slot
+    st.loc[pre] = np.arange(pre.size, dtype=np.int32)
+    st.mat_top[0] = pre.size
+    gst = [torch.from_numpy(getattr(st, f).copy()).to(dev) for f in O.DIR_FIELDS]
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    e = np.empty(0, np.int64)
+    calls = [(e, e, crow, ccnt), (fresh, np.zeros(fresh.size, np.int64), e, e)]
+    for s, (ar, ak, cr, cc) in enumerate(calls, start=10):
+        want = O.dir_b(st, pv, ar, ak, cr, cc, s)
+        got = dir_ext().elara_dir_b(gst, list(pv), T(ar), T(ak), T(cr), T(cc), s)
+        torch.cuda.synchronize()
+        for w, g in zip(want, got):
+            assert np.array_equal(w, g.cpu().numpy())
+        for i, f in enumerate(O.DIR_FIELDS):
+            a, b = getattr(st, f).reshape(-1), gst[i].cpu().numpy().reshape(-1)
+            if f in ('lstep', 'lfree'):
+                a, b = a[:-1], b[:-1]
+            assert np.array_equal(a, b), (s, f)
+    assert 0 < st.n_lfree[0] or st.log_top[0] > 0
+
+
+@pytest.mark.gpu
+def test_gpu_directory_empty_calls(dev):
+    import torch
+    from elara_amd.elara_dir import dir_ext
+    sim = Sim(seed=13)
+    st0 = sim.initial_state()
+    g = gpu_impl(sim, st0, dev)
+    before = comparable_state(g.view(), sim)
+    z = torch.empty(0, dtype=torch.int64, device=dev)
+    out = dir_ext().elara_dir_a(g.st, list(sim.pv), z, z, z.to(torch.int32), z, 3)
+    assert [tuple(o.shape) for o in out] == [(0, 3), (0, 3), (0,), (0,), (0,), (0,), (0, 3), (0,), (0,)]
+    assert [o.dtype for o in out] == [torch.int32, torch.int32] + [torch.int64] * 3 + [torch.bool] + [torch.int64] * 3
+    a_ids, c_slots = dir_ext().elara_dir_b(g.st, list(sim.pv), z, z, z, z, 3)
+    assert a_ids.numel() == 0 and c_slots.numel() == 0
+    torch.cuda.synchronize()
+    assert not diff_states(before, comparable_state(g.view(), sim))
+    with pytest.raises(RuntimeError):
+        dir_ext().elara_dir_a(g.st[:16], list(sim.pv), z, z, z.to(torch.int32), z, 3)
