@@ -32,6 +32,10 @@ SIGNATURES = {
     'elr_replay_rows': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_u32,
                                        c_f32, c_vp, c_i64, c_vp]),
     'elr_dir_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_dedup_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_unique': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
+    'elr_segment_sum': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    'elr_adam_dedup': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_f32p, c_vp, c_i64, c_vp]),
     'elr_dir_a': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64] + [c_vp] * 9
                   + [c_vp, c_i64, c_vp]),
     'elr_dir_b': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64,

@@ -1,0 +1,527 @@
+// Batch dedup and duplicate-id gradient reduction in a fixed order, optionally fused with row-sparse Adam
+// (HBM-bound; no MFMA).
+//
+// Replaces the step before Adam on every batch: torch.unique(ids, return_inverse=True) (srm2/train.py:352) and
+// aten.embedding_dense_backward (srm2/train.py:429), and gives config C3 its fused form (dedup, fixed-order
+// segment sum, Adam on each unique row).
+//
+// Sort.  Stable LSD radix sort of (id, occurrence index) pairs, 8-bit digits, ceil(key_bits / 8) passes, keys held
+// as uint32 when key_bits <= 32.  Each pass is three launches: per-tile digit histograms (tiles of 4096 keys), one
+// block per digit scanning that digit's per-tile counts, and a scatter in which each key's rank among equal digits
+// of its tile comes from wave ballots (peer mask of the 8 digit bits), per-wave counts in LDS and a running count
+// over the tile's 16 rounds, so equal keys keep their occurrence order.
+//
+// Segments.  Sorted position i starts a segment when its key differs from position i-1; a scan of those heads
+// gives every position its unique index (the inverse) and every unique id its first position.
+//
+// Summation order (this build's definition; the reference's order is ATen's and no reference test pins it):
+// the occurrences of one id, in ascending occurrence index, are cut into chunks of 64; each chunk is summed left
+// to right starting from its first gradient, and the chunk sums are added left to right starting from chunk 0.
+// For an id with at most 64 occurrences this is the plain left-to-right sum.  The result depends only on that id's
+// own occurrence list, and chunks of long (Zipf-hot) segments are summed in parallel by different waves.
+#include "elr_rowio.h"
+#include "elr_scan.h"
+
+namespace elr {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int64_t kSortTile = (int64_t)kSortThreads * kSortItems;
+constexpr int kRadixBins = 256;
+constexpr int kSegChunk = 64;
+constexpr int kSegBlock = 256;
+
+static_assert(kSortThreads == kRadixBins, "one histogram bin per sort thread");
+
+template <typename Key>
+__device__ __forceinline__ uint32_t digit_of(Key k, int shift) {
+  return (uint32_t)((k >> shift) & (Key)(kRadixBins - 1));
+}
+
+// Per-tile digit histogram, digit-major: hist[d * nblk + tile].
+template <typename Src, typename Key>
+__global__ __launch_bounds__(kSortThreads) void k_radix_hist(const Src* __restrict__ src, int64_t n, int shift,
+                                                             int64_t* __restrict__ hist, int64_t nblk) {
+  __shared__ int h[kRadixBins];
+  h[threadIdx.x] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  for (int r = 0; r < kSortItems; ++r) {
+    const int64_t pos = base + (int64_t)r * kSortThreads + threadIdx.x;
+    if (pos < n) atomicAdd(&h[digit_of((Key)src[pos], shift)], 1);
+  }
+  __syncthreads();
+  hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
+}
+
+// One block per digit: exclusive scan of that digit's per-tile counts (in place) and the digit's total.
+__global__ __launch_bounds__(kScanBlock) void k_radix_hist_scan(int64_t* __restrict__ hist, int64_t ntile,
+                                                                int64_t* __restrict__ dtot) {
+  scan_channels_block(hist + (int64_t)blockIdx.x * ntile, ntile, 1, dtot + blockIdx.x);
+}
+
+// One block: exclusive scan of per-block counts in place, total to *tot.
+__global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict__ bsum, int64_t n,
+                                                            int64_t* __restrict__ tot) {
+  scan_channels_block(bsum, n, 1, tot);
+}
+
+// Stable scatter of one pass.  FIRST: the source keys are the caller's int64 ids and the values are their
+// positions.
+template <typename Src, typename Key, bool FIRST>
+__global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __restrict__ src_keys,
+                                                                const int32_t* __restrict__ src_vals, int64_t n,
+                                                                int shift, const int64_t* __restrict__ offs,
+                                                                const int64_t* __restrict__ dtot, int64_t nblk,
+                                                                Key* __restrict__ dst_keys,
+                                                                int32_t* __restrict__ dst_vals) {
+  constexpr int NW = kSortThreads / 64;
+  __shared__ int64_t bo[kRadixBins];
+  __shared__ int run[kRadixBins];
+  __shared__ int wc[NW][kRadixBins];
+  const int t = threadIdx.x, w = t >> 6;
+  {
+    // digit bases: exclusive scan of the 256 digit totals (n < 2^31, so they fit in int)
+    int v[1] = {(int)dtot[t]}, ex[1], tot[1];
+    block_excl_scan<kSortThreads, 1>(v, ex, tot);
+    bo[t] = (int64_t)ex[0] + offs[(int64_t)t * nblk + blockIdx.x];
+  }
+  run[t] = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) wc[q][t] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  for (int r = 0; r < kSortItems; ++r) {
+    const int64_t pos = base + (int64_t)r * kSortThreads + t;
+    const bool valid = pos < n;
+    const Key k = valid ? (Key)src_keys[pos] : (Key)0;
+    const int32_t v = valid ? (FIRST ? (int32_t)pos : src_vals[pos]) : 0;
+    const uint32_t d = digit_of(k, shift);
+    uint64_t m = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t bal = __ballot(bit);
+      m &= bit ? bal : ~bal;
+    }
+    const int lr = __popcll(m & lanemask_lt());
+    if (valid && lr == 0) wc[w][d] = __popcll(m);
+    __syncthreads();
+    if (valid) {
+      int rank = run[d] + lr;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) rank += q < w ? wc[q][d] : 0;
+      const int64_t dst = bo[d] + rank;
+      if (dst >= 0 && dst < n) {
+        dst_keys[dst] = k;
+        dst_vals[dst] = v;
+      }
+    }
+    __syncthreads();
+    int add = 0;
+#pragma unroll
+    for (int q = 0; q < NW; ++q) {
+      add += wc[q][t];
+      wc[q][t] = 0;
+    }
+    run[t] += add;
+    __syncthreads();
+  }
+}
+
+// Segment kernels take kSegItems consecutive positions per thread (blocked), kSegTile per block.
+constexpr int kSegItems = 16;
+constexpr int64_t kSegTile = (int64_t)kSegBlock * kSegItems;
+
+template <typename Key>
+__device__ __forceinline__ int is_head(const Key* __restrict__ sk, int64_t i, int64_t n) {
+  return i < n && (i == 0 || sk[i] != sk[i - 1]) ? 1 : 0;
+}
+
+// Segment heads: per-block head counts.
+template <typename Key>
+__global__ __launch_bounds__(kSegBlock) void k_seg_count(const Key* __restrict__ sk, int64_t n,
+                                                         int64_t* __restrict__ bsum) {
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  int v[1] = {0}, ex[1], tot[1];
+  for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + r, n);
+  block_excl_scan<kSegBlock, 1>(v, ex, tot);
+  if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
+}
+
+// Segment heads: unique ids, segment starts (seg_start[U] = n) and the inverse.
+template <typename Key>
+__global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__ sk, const int32_t* __restrict__ sv,
+                                                         int64_t n, const int64_t* __restrict__ boff,
+                                                         const int64_t* __restrict__ d_U,
+                                                         int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
+                                                         int64_t* __restrict__ inverse) {
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  int v[1] = {0}, ex[1], tot[1];
+  for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + r, n);
+  block_excl_scan<kSegBlock, 1>(v, ex, tot);
+  int64_t u = boff[blockIdx.x] + ex[0] - 1;   // segment of the position before this thread's first
+  for (int r = 0; r < kSegItems; ++r) {
+    const int64_t i = base + r;
+    if (i >= n) break;
+    const int f = is_head(sk, i, n);
+    u += f;
+    if (f) {
+      uniq[u] = (int64_t)sk[i];
+      seg_start[u] = i;
+    }
+    if (inverse) {
+      const int32_t o = sv[i];
+      if (o >= 0 && o < n) inverse[o] = u;
+    }
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0) seg_start[*d_U] = n;
+}
+
+__device__ __forceinline__ int extra_chunks(const int64_t* __restrict__ seg_start, int64_t u, int64_t U) {
+  return u < U ? (int)((seg_start[u + 1] - seg_start[u] - 1) / kSegChunk) : 0;
+}
+
+// Extra chunks (beyond the first) of each segment: per-block counts.
+__global__ __launch_bounds__(kSegBlock) void k_chunk_count(const int64_t* __restrict__ seg_start,
+                                                           const int64_t* __restrict__ d_U,
+                                                           int64_t* __restrict__ bsum) {
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  const int64_t U = *d_U;
+  int v[1] = {0}, ex[1], tot[1];
+  for (int r = 0; r < kSegItems; ++r) v[0] += extra_chunks(seg_start, base + r, U);
+  block_excl_scan<kSegBlock, 1>(v, ex, tot);
+  if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
+}
+
+// chunk_off[u] = first work item of segment u's extra chunks; chunk_seg[item] = u.
+__global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __restrict__ seg_start,
+                                                           const int64_t* __restrict__ d_U,
+                                                           const int64_t* __restrict__ boff,
+                                                           int32_t* __restrict__ chunk_off,
+                                                           int32_t* __restrict__ chunk_seg) {
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  const int64_t U = *d_U;
+  int v[1] = {0}, ex[1], tot[1];
+  for (int r = 0; r < kSegItems; ++r) v[0] += extra_chunks(seg_start, base + r, U);
+  block_excl_scan<kSegBlock, 1>(v, ex, tot);
+  int64_t off = boff[blockIdx.x] + ex[0];
+  for (int r = 0; r < kSegItems; ++r) {
+    const int64_t u = base + r;
+    if (u >= U) break;
+    const int e = extra_chunks(seg_start, u, U);
+    chunk_off[u] = (int32_t)off;
+    for (int c = 0; c < e; ++c) chunk_seg[off + c] = (int32_t)u;
+    off += e;
+  }
+}
+
+// Left-to-right sum of the gradients at sorted positions [p0, p1) (p1 - p0 <= 64), this lane's NQ elements
+// j = lane + 64 q (< D).  Occurrence indices are loaded once per wave and broadcast with readlane.
+template <int NQ>
+__device__ __forceinline__ void chunk_sum(const float* __restrict__ grad, int64_t D, const int32_t* __restrict__ sv,
+                                          int64_t p0, int64_t p1, float (&acc)[NQ]) {
+  const int lane = threadIdx.x & 63;
+  const int len = (int)(p1 - p0);
+  const int32_t my = lane < len ? sv[p0 + lane] : 0;
+  constexpr int UN = 8;
+  for (int k0 = 0; k0 < len; k0 += UN) {
+    float g[UN][NQ];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int k = k0 + u;
+      if (k < len) {
+        const int64_t o = (int64_t)__builtin_amdgcn_readlane(my, k);
+        const float* row = grad + o * D;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          const int64_t j = lane + 64 * q;
+          g[u][q] = j < D ? __builtin_nontemporal_load(row + j) : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int k = k0 + u;
+      if (k < len) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) acc[q] = k == 0 ? g[u][q] : acc[q] + g[u][q];
+      }
+    }
+  }
+}
+
+// Sums of the extra chunks, one wave per chunk (grid-stride over the E work items).
+template <int NQ>
+__global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ grad, int64_t D,
+                                                      const int32_t* __restrict__ sv,
+                                                      const int64_t* __restrict__ seg_start,
+                                                      const int32_t* __restrict__ chunk_off,
+                                                      const int32_t* __restrict__ chunk_seg,
+                                                      const int64_t* __restrict__ d_E, float* __restrict__ parts) {
+  const int lane = threadIdx.x & 63;
+  const int64_t E = *d_E;
+  for (int64_t wi = wave_id(); wi < E; wi += wave_count()) {
+    const int64_t u = chunk_seg[wi];
+    const int64_t c = wi - chunk_off[u] + 1;
+    const int64_t p0 = seg_start[u] + c * kSegChunk;
+    int64_t p1 = p0 + kSegChunk;
+    const int64_t e = seg_start[u + 1];
+    if (p1 > e) p1 = e;
+    float acc[NQ];
+    chunk_sum<NQ>(grad, D, sv, p0, p1, acc);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int64_t j = lane + 64 * q;
+      if (j < D) parts[wi * D + j] = acc[q];
+    }
+  }
+}
+
+// Final per-segment sum (chunk 0 summed here, then the extra chunks' partials in order), then either written to
+// out[uniq[u]] (MODE 0) or applied as an Adam step to state[uniq[u]] (MODE 1).  One wave per segment.
+template <int NQ, int MODE>
+__global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ grad, int64_t D,
+                                                   const int32_t* __restrict__ sv,
+                                                   const int64_t* __restrict__ seg_start,
+                                                   const int64_t* __restrict__ uniq,
+                                                   const int32_t* __restrict__ chunk_off,
+                                                   const float* __restrict__ parts, const int64_t* __restrict__ d_U,
+                                                   float* __restrict__ out, int64_t nrows, AdamScalars s) {
+  const int lane = threadIdx.x & 63;
+  const int64_t U = *d_U;
+  for (int64_t u = wave_id(); u < U; u += wave_count()) {
+    const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
+    const int64_t L = s1 - s0;
+    const int64_t row = uniq[u];
+    float acc[NQ];
+    chunk_sum<NQ>(grad, D, sv, s0, L < kSegChunk ? s1 : s0 + kSegChunk, acc);
+    const int64_t extra = (L - 1) / kSegChunk;
+    const int64_t pb = extra ? (int64_t)chunk_off[u] : 0;
+    for (int64_t c = 0; c < extra; ++c) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int64_t j = lane + 64 * q;
+        if (j < D) acc[q] = acc[q] + parts[(pb + c) * D + j];
+      }
+    }
+    if (row < 0 || row >= nrows) continue;
+    if (MODE == 0) {
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int64_t j = lane + 64 * q;
+        if (j < D) out[row * D + j] = acc[q];
+      }
+    } else {
+      float* rec = out + row * 3 * D;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int64_t j = lane + 64 * q;
+        if (j < D) {
+          float w = rec[j], m = rec[D + j], v = rec[2 * D + j];
+          adam_elem(w, m, v, acc[q], s);
+          rec[j] = w;
+          rec[D + j] = m;
+          rec[2 * D + j] = v;
+        }
+      }
+    }
+  }
+}
+
+// ---- host side -------------------------------------------------------------------------------------------------
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+// Scratch carve-up for n occurrences of width D.
+struct DedupScratch {
+  void* keys[2];
+  int32_t* vals[2];
+  int64_t* hist;      // [256 * ntile]
+  int64_t* dtot;      // [256] digit totals
+  int64_t* bsum;      // [n / kSegTile + 1]
+  int64_t* d_tot;     // [2]: U, E
+  int64_t* uniq;      // [n]
+  int64_t* seg_start; // [n + 1]
+  int32_t* chunk_off; // [n]
+  int32_t* chunk_seg; // [n / 64 + 1]
+  float* parts;       // [(n / 64 + 1) * D]
+};
+
+inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void* base) {
+  const int64_t ntile = cdiv(n, kSortTile), nblk = cdiv(n, kSegTile), nch = n / kSegChunk + 1;
+  int64_t o = 0;
+  char* b = (char*)base;
+  auto take = [&](int64_t bytes) {
+    void* p = b ? (void*)(b + o) : nullptr;
+    o += al256(bytes);
+    return p;
+  };
+  DedupScratch s;
+  s.keys[0] = take(n * 8);
+  s.keys[1] = take(n * 8);
+  s.vals[0] = (int32_t*)take(n * 4);
+  s.vals[1] = (int32_t*)take(n * 4);
+  s.hist = (int64_t*)take(kRadixBins * ntile * 8);
+  s.dtot = (int64_t*)take(kRadixBins * 8);
+  s.bsum = (int64_t*)take(nblk * 8);
+  s.d_tot = (int64_t*)take(2 * 8);
+  s.uniq = (int64_t*)take(n * 8);
+  s.seg_start = (int64_t*)take((n + 1) * 8);
+  s.chunk_off = (int32_t*)take(n * 4);
+  s.chunk_seg = (int32_t*)take(nch * 4);
+  s.parts = (float*)take(nch * D * 4);
+  if (out) *out = s;
+  return o;
+}
+
+// Sort (ids, positions) by id; returns which buffer holds the result.
+template <typename Key>
+static int radix_sort(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, hipStream_t st) {
+  const int64_t ntile = cdiv(n, kSortTile);
+  const int passes = (key_bits + 7) / 8;
+  Key* kb[2] = {(Key*)S.keys[0], (Key*)S.keys[1]};
+  int cur = 0;
+  for (int p = 0; p < passes; ++p) {
+    const int shift = 8 * p;
+    const int nxt = p == 0 ? 0 : cur ^ 1;
+    if (p == 0) {
+      k_radix_hist<int64_t, Key><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
+      k_radix_hist_scan<<<kRadixBins, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
+      k_radix_scatter<int64_t, Key, true><<<(unsigned)ntile, kSortThreads, 0, st>>>(
+          ids, nullptr, n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
+    } else {
+      k_radix_hist<Key, Key><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
+      k_radix_hist_scan<<<kRadixBins, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
+      k_radix_scatter<Key, Key, false><<<(unsigned)ntile, kSortThreads, 0, st>>>(
+          kb[cur], S.vals[cur], n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
+    }
+    cur = nxt;
+  }
+  return cur;
+}
+
+// Sort, segment heads (uniq / seg_start / inverse, U in d_tot[0]) and the extra-chunk plan (E in d_tot[1]).
+template <typename Key>
+static int dedup_core(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, int64_t* uniq_out,
+                      int64_t* inverse, hipStream_t st) {
+  const int cur = radix_sort<Key>(ids, n, key_bits, S, st);
+  const Key* sk = (const Key*)S.keys[cur];
+  const int32_t* sv = S.vals[cur];
+  const int64_t nblk = cdiv(n, kSegTile);
+  int64_t* uniq = uniq_out ? uniq_out : S.uniq;
+  k_seg_count<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
+  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot);
+  k_seg_apply<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start, inverse);
+  return cur;
+}
+
+static void chunk_plan(int64_t n, DedupScratch& S, hipStream_t st) {
+  const int64_t nblk = cdiv(n, kSegTile);
+  k_chunk_count<<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum);
+  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1);
+  k_chunk_apply<<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.chunk_off, S.chunk_seg);
+}
+
+// Grid of a grid-stride wave loop: enough blocks to fill the chip several times over, at most one wave per item.
+inline unsigned wave_grid(int64_t items) {
+  int64_t b = cdiv(items, 4);
+  const int64_t cap = 256 * 16;
+  if (b > cap) b = cap;
+  if (b < 1) b = 1;
+  return (unsigned)b;
+}
+
+template <int NQ, int MODE>
+static void seg_reduce(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
+                       int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+  k_seg_partials<NQ><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
+                                                                    S.chunk_seg, S.d_tot + 1, S.parts);
+  k_seg_final<NQ, MODE><<<wave_grid(n), 256, 0, st>>>(grad, D, sv, S.seg_start, uniq, S.chunk_off, S.parts, S.d_tot,
+                                                       out, nrows, s);
+}
+
+template <int MODE>
+static int seg_reduce_d(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
+                        int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+  const int64_t nq = cdiv(D, 64);
+  switch (nq) {
+    case 1: seg_reduce<1, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    case 2: seg_reduce<2, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    case 3:
+    case 4: seg_reduce<4, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    case 5: case 6: case 7:
+    case 8: seg_reduce<8, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    default: return ELR_EUNSUPPORTED;
+  }
+  return ELR_OK;
+}
+
+inline int bits_for(int64_t bound) {  // smallest b with bound <= 2^b (keys in [0, bound))
+  int b = 1;
+  while (b < 63 && (int64_t(1) << b) < bound) ++b;
+  return b;
+}
+
+inline bool dedup_sizes_ok(int64_t n) { return n >= 0 && n < (int64_t(1) << 31); }
+
+}  // namespace elr
+
+extern "C" int64_t elr_dedup_scratch_bytes(int64_t n, int64_t D) {
+  if (!elr::dedup_sizes_ok(n) || D < 0) return ELR_EINVAL;
+  return elr::dedup_scratch_bytes(n, D < 1 ? 1 : D, nullptr, nullptr);
+}
+
+extern "C" int elr_unique(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, int64_t* inverse,
+                          int64_t* n_unique, void* scratch, int64_t scratch_bytes, void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || key_bits < 1 || key_bits > 64) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!ids || !uniq || !n_unique || !scratch) return ELR_EINVAL;
+  DedupScratch S;
+  if (scratch_bytes < dedup_scratch_bytes(n, 1, &S, scratch)) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  if (key_bits <= 32) dedup_core<uint32_t>(ids, n, key_bits, S, uniq, inverse, st);
+  else dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, st);
+  hipError_t e = hipMemcpyAsync(n_unique, S.d_tot, sizeof(int64_t), hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) return (int)e;
+  return launch_status();
+}
+
+extern "C" int elr_segment_sum(const float* grad, const int64_t* idx, int64_t n, int64_t D, int64_t num_rows,
+                               float* out, void* scratch, int64_t scratch_bytes, void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || D < 1 || num_rows < 0) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!grad || !idx || !out || !scratch) return ELR_EINVAL;
+  if (D > 512) return ELR_EUNSUPPORTED;
+  DedupScratch S;
+  if (scratch_bytes < dedup_scratch_bytes(n, D, &S, scratch)) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  const int kb = bits_for(num_rows);
+  const int cur = kb <= 32 ? dedup_core<uint32_t>(idx, n, kb, S, nullptr, nullptr, st)
+                           : dedup_core<uint64_t>(idx, n, kb, S, nullptr, nullptr, st);
+  chunk_plan(n, S, st);
+  const AdamScalars none{};
+  const int rc = seg_reduce_d<0>(grad, D, S.vals[cur], S, S.uniq, n, out, num_rows, none, st);
+  return rc != ELR_OK ? rc : launch_status();
+}
+
+extern "C" int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
+                              const float sc[8], void* scratch, int64_t scratch_bytes, void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || D < 1 || C < 0 || !sc) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!state || !ids || !grad || !scratch) return ELR_EINVAL;
+  if (D > 512) return ELR_EUNSUPPORTED;
+  DedupScratch S;
+  if (scratch_bytes < dedup_scratch_bytes(n, D, &S, scratch)) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  const AdamScalars s = {sc[0], sc[1], sc[2], sc[3], sc[4], sc[5], sc[6], sc[7]};
+  const int kb = bits_for(C);
+  const int cur = kb <= 32 ? dedup_core<uint32_t>(ids, n, kb, S, nullptr, nullptr, st)
+                           : dedup_core<uint64_t>(ids, n, kb, S, nullptr, nullptr, st);
+  chunk_plan(n, S, st);
+  const int rc = seg_reduce_d<1>(grad, D, S.vals[cur], S, S.uniq, n, state, C, s, st);
+  return rc != ELR_OK ? rc : launch_status();
+}

@@ -21,12 +21,11 @@
 // Index safety: every gathered or scattered index is checked against its array's extent; an item whose slot, row
 // or entry id is out of range is treated as carrying nothing (no writes).  The reference leaves such inputs
 // undefined.
-#include "elr_common.h"
+#include "elr_scan.h"
 
 namespace elr {
 
 constexpr int kDirBlock = 256;
-constexpr int kScanBlock = 1024;
 
 // Old counter values kept by the scan step for the apply steps.
 struct DirHdr {
@@ -36,40 +35,9 @@ struct DirHdr {
   int64_t nf1;   // n_lfree after the log allocation (push base of the releases)
 };
 
-__device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int t = __shfl_up(v, d, 64);
-    if (lane >= d) v += t;
-  }
-  return v;
-}
-
-// Exclusive prefix of v[c] over the threads of the block (kDirBlock threads) and the block totals.
 template <int NCH>
-__device__ __forceinline__ void block_excl_scan(const int (&v)[NCH], int (&ex)[NCH], int (&tot)[NCH]) {
-  __shared__ int wsum[NCH][kDirBlock / 64];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int inc[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    inc[c] = wave_incl_scan(v[c]);
-    if (lane == 63) wsum[c][w] = inc[c];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    int base = 0, t = 0;
-#pragma unroll
-    for (int q = 0; q < kDirBlock / 64; ++q) {
-      const int x = wsum[c][q];
-      base += q < w ? x : 0;
-      t += x;
-    }
-    ex[c] = base + inc[c] - v[c];
-    tot[c] = t;
-  }
+__device__ __forceinline__ void dir_block_scan(const int (&v)[NCH], int (&ex)[NCH], int (&tot)[NCH]) {
+  block_excl_scan<kDirBlock, NCH>(v, ex, tot);
 }
 
 __device__ __forceinline__ bool in_range(int64_t x, int64_t hi) { return x >= 0 && x < hi; }
@@ -192,7 +160,7 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st,
     v[2] = c.nrel;
   }
   int ex[3], tot[3];
-  block_excl_scan<3>(v, ex, tot);
+  dir_block_scan<3>(v, ex, tot);
   if (threadIdx.x == 0)
     for (int c = 0; c < 3; ++c) bsum[c * nblk + blockIdx.x] = tot[c];
 }
@@ -205,33 +173,10 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st,
 __global__ __launch_bounds__(kScanBlock) void k_dir_scan(elr_dir_state st, int mode, int64_t nappend,
                                                          int64_t* __restrict__ bsum, int64_t nblk, int nch,
                                                          DirHdr* __restrict__ hdr) {
-  __shared__ int64_t wtot[kScanBlock / 64];
   __shared__ int64_t chan_tot[3];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int c = 0; c < nch; ++c) {
-    int64_t carry = 0;
-    for (int64_t b0 = 0; b0 < nblk; b0 += kScanBlock) {
-      const int64_t b = b0 + threadIdx.x;
-      const int64_t x = b < nblk ? bsum[c * nblk + b] : 0;
-      int64_t inc = x;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int64_t t = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += t;
-      }
-      if (lane == 63) wtot[w] = inc;
-      __syncthreads();
-      int64_t base = 0, all = 0;
-      for (int q = 0; q < kScanBlock / 64; ++q) {
-        base += q < w ? wtot[q] : 0;
-        all += wtot[q];
-      }
-      if (b < nblk) bsum[c * nblk + b] = carry + base + inc - x;
-      carry += all;
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) chan_tot[c] = carry;
-  }
+  if (threadIdx.x < 3) chan_tot[threadIdx.x] = 0;
+  __syncthreads();
+  scan_channels_block(bsum, nblk, nch, chan_tot);
   __syncthreads();
   if (threadIdx.x == 0) {
     const int64_t nalloc = mode == 0 ? chan_tot[0] : nappend;
@@ -279,7 +224,7 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st,
     c = ev_counts(st, p, row, rp, c0, j);
   }
   int v[3] = {c.nalloc, c.nmat, c.nrel}, ex[3], tot[3];
-  block_excl_scan<3>(v, ex, tot);
+  dir_block_scan<3>(v, ex, tot);
   if (i >= nev) return;
   const DirHdr h = *hdr;
   // log ids for the resident history: ent[row, max(c0,0) + k] = id, lstep[id] = pstep[dyn, k]  (k < j)
@@ -375,7 +320,7 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_b_count(elr_dir_state st, elr
     }
   }
   int ex[2], tot[2];
-  block_excl_scan<2>(v, ex, tot);
+  dir_block_scan<2>(v, ex, tot);
   if (threadIdx.x == 0) {
     bsum[0 * nblk_c + b] = tot[0];
     bsum[1 * nblk_c + b] = tot[1];
@@ -403,7 +348,7 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_b_compact(elr_dir_state st, e
     }
   }
   int ex[2], tot[2];
-  block_excl_scan<2>(v, ex, tot);
+  dir_block_scan<2>(v, ex, tot);
   if (i >= nc) return;
   if (!in_range(row, p.R)) {
     c_slots[i] = -1;

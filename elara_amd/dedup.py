@@ -1,0 +1,109 @@
+"""Batch dedup and duplicate-id gradient reduction on the GPU -- the step before Adam on every batch.
+
+    unique(ids) -> (u, inv)                       torch.unique(ids, return_inverse=True), srm2/train.py:352
+    embedding_dense_backward(grad, inv, num_weights, padding_idx=-1, scale_grad_by_freq=False) -> [num_weights, D]
+                                                  aten.embedding_dense_backward as srm2/train.py:429 calls it
+    adam_dedup(pool, ids, grad, lr, b1, b2, eps, step)
+                                                  dedup + fixed-order segment sum + row-sparse Adam on pool[id]
+                                                  (config C3: one Adam step per unique id of a batch)
+
+Summation order of duplicate ids (this build's definition; the reference's belongs to ATen and is pinned by no
+reference test): per id, the occurrences in ascending occurrence index are cut into chunks of 64, each chunk is
+summed left to right, and the chunk sums are added left to right.  All three run as HIP kernels
+(elara_amd/csrc/dedup.hip) on torch's current stream.
+"""
+import torch
+
+from . import _lib
+from .ops import _check_state, adam_scalars
+
+I64 = torch.int64
+
+
+def _scratch(dev, n, D):
+    nbytes = int(_lib.lib().elr_dedup_scratch_bytes(int(n), int(D)))
+    if nbytes < 0:
+        _lib.check(nbytes, 'elr_dedup_scratch_bytes')
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev), nbytes
+
+
+def _ids(ids, name='ids'):
+    if not ids.is_cuda:
+        raise RuntimeError(f'{name} must be a cuda tensor')
+    if ids.dtype not in (torch.int32, torch.int64):
+        raise RuntimeError(f'{name} must be int32 or int64')
+    return ids.reshape(-1).to(I64).contiguous()
+
+
+def _bits(bound):
+    b = 1
+    while b < 63 and (1 << b) < bound:
+        b += 1
+    return b
+
+
+def unique(ids):
+    """Sorted unique values of `ids` (int32/int64, >= 0) and the inverse, as torch.unique(ids, sorted=True,
+    return_inverse=True) returns them (int64).  Synchronises once to size the output, as torch.unique does."""
+    flat = _ids(ids)
+    n = flat.numel()
+    dev = flat.device
+    inv = torch.empty(ids.shape, dtype=I64, device=dev)
+    if n == 0:
+        return torch.empty(0, dtype=I64, device=dev), inv
+    lo, hi = torch.aminmax(flat)
+    lo, hi = int(lo), int(hi)
+    if lo < 0:
+        raise RuntimeError('unique: ids must be non-negative')
+    u = torch.empty(n, dtype=I64, device=dev)
+    nu = torch.empty(1, dtype=I64, device=dev)
+    scratch, nbytes = _scratch(dev, n, 1)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_unique(_lib.ptr(flat), n, _bits(hi + 1), _lib.ptr(u), _lib.ptr(inv), _lib.ptr(nu),
+                                   _lib.ptr(scratch), nbytes, _lib.stream_of(flat))
+    _lib.check(rc, 'elr_unique')
+    return u[:int(nu)], inv
+
+
+def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1, scale_grad_by_freq=False):
+    """[num_weights, D] per-row sums of grad_output [n, D] over indices [n] (rows without an index are zero), in
+    this build's fixed summation order.  Supports the reference's call (padding_idx=-1, no frequency scaling)."""
+    if padding_idx != -1 or scale_grad_by_freq:
+        raise RuntimeError('embedding_dense_backward: only padding_idx=-1 and scale_grad_by_freq=False are supported')
+    idx = _ids(indices, 'indices')
+    n = idx.numel()
+    D = grad_output.shape[-1]
+    if not (grad_output.is_cuda and grad_output.dtype == torch.float32 and grad_output.numel() == n * D):
+        raise RuntimeError(f'grad_output must be a cuda float32 tensor with {n}x{D} elements')
+    dev = idx.device
+    out = torch.zeros(int(num_weights), D, dtype=torch.float32, device=dev)
+    if n == 0:
+        return out
+    g = grad_output.reshape(n, D).contiguous()
+    scratch, nbytes = _scratch(dev, n, D)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_segment_sum(_lib.ptr(g), _lib.ptr(idx), n, D, int(num_weights), _lib.ptr(out),
+                                        _lib.ptr(scratch), nbytes, _lib.stream_of(g))
+    _lib.check(rc, 'elr_segment_sum')
+    return out
+
+
+def adam_dedup(pool, ids, grad, lr, b1, b2, eps, step):
+    """pool [C,3,D] cuda float32 (updated in place); ids int32/int64 [n] rows of pool, repeats allowed; grad [n,D]
+    (row i belongs to ids[i]).  Each unique id gets one Adam step with the sum of its gradients."""
+    idx = _ids(ids)
+    n = idx.numel()
+    if n == 0:
+        return
+    _check_state(pool)
+    D = pool.shape[2]
+    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.numel() == n * D):
+        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements')
+    g = grad.reshape(n, D).contiguous()
+    dev = pool.device
+    scratch, nbytes = _scratch(dev, n, D)
+    s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_adam_dedup(_lib.ptr(pool), pool.shape[0], _lib.ptr(idx), _lib.ptr(g), n, D, s,
+                                       _lib.ptr(scratch), nbytes, _lib.stream_of(pool))
+    _lib.check(rc, 'elr_adam_dedup')

@@ -45,3 +45,46 @@ class ReplayLog:
 def unique_rows(rng, R, n):
     """n distinct row ids from [0, R), uniform without replacement, unsorted."""
     return rng.choice(R, n, replace=False).astype(np.int64)
+
+
+class ZipfFields:
+    """Row ids of a batch of `fields` categorical fields with bounded Zipf(alpha) popularity (configs C3-C5).
+
+    Field f has vocabulary vocab[f] and rows [offset[f], offset[f] + vocab[f]) of the table.  A rank k in
+    [0, vocab) is drawn by inverting the CDF of the continuous power law x^-alpha on [1, vocab + 1) and flooring
+    (a bounded Zipf up to discretisation); it is mapped to a row through a per-field bijection of [0, vocab),
+    k -> (a_f * k + b_f) mod vocab with gcd(a_f, vocab) = 1, so every field has its own hot rows.  draw() returns
+    int64 ids [batch * fields] in (sample, field) order: occurrence index = sample * fields + field.
+    """
+
+    def __init__(self, vocab, alpha, seed=0, offsets=None):
+        import math
+        self.vocab = np.asarray(vocab, dtype=np.int64)
+        self.F = self.vocab.size
+        self.alpha = float(alpha)
+        self.offsets = (np.concatenate([[0], np.cumsum(self.vocab)[:-1]]) if offsets is None
+                        else np.asarray(offsets, dtype=np.int64))
+        rng = np.random.default_rng(seed)
+        self.a = np.empty(self.F, np.int64)
+        self.b = np.empty(self.F, np.int64)
+        for f, V in enumerate(self.vocab.tolist()):
+            while True:
+                a = int(rng.integers(1, max(2, V)))
+                if math.gcd(a, V) == 1:
+                    break
+            self.a[f], self.b[f] = a, int(rng.integers(0, V))
+
+    def ranks(self, rng, batch):
+        """[batch, F] ranks in [0, vocab_f)."""
+        u = rng.random((batch, self.F))
+        e = 1.0 - self.alpha
+        top = (self.vocab.astype(np.float64) + 1.0) ** e - 1.0
+        x = (1.0 + u * top[None, :]) ** (1.0 / e)
+        return np.minimum(np.floor(x).astype(np.int64) - 1, self.vocab[None, :] - 1)
+
+    def draw(self, rng, batch):
+        k = self.ranks(rng, batch)
+        # (a*k + b) mod V without int64 overflow for V < 2^31: a, k < V
+        ids = (self.a[None, :].astype(object) * k.astype(object) + self.b[None, :]) % self.vocab[None, :] \
+            if self.vocab.max() >= (1 << 31) else (self.a[None, :] * k + self.b[None, :]) % self.vocab[None, :]
+        return (np.asarray(ids, dtype=np.int64) + self.offsets[None, :]).reshape(-1)

@@ -133,6 +133,35 @@ int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a
               const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids, int64_t* c_slots,
               void* scratch, int64_t scratch_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Batch dedup and duplicate-id gradient reduction.
+ * Summation order (this build's definition; the reference's is ATen's embedding backward and no reference test
+ * pins it): per id, occurrences in ascending occurrence index are cut into chunks of 64; each chunk is summed left
+ * to right from its first gradient, and the chunk sums are added left to right from the first chunk.  n < 2^31.
+ * ------------------------------------------------------------------------------------------------------- */
+
+/* Bytes of device scratch elr_unique / elr_segment_sum / elr_adam_dedup need for n occurrences of width D
+ * (D = 1 for elr_unique), or a negative code. */
+int64_t elr_dedup_scratch_bytes(int64_t n, int64_t D);
+
+/* Replaces: torch.unique(ids, return_inverse=True) at srm2/train.py:352.  ids int64 [n] in [0, 2^key_bits)
+ * -> uniq int64 [>= U] ascending (first U valid), inverse int64 [n] (uniq[inverse[i]] == ids[i]; may be NULL),
+ * n_unique int64 [1] = U.  All device pointers; nothing is read back to the host. */
+int elr_unique(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, int64_t* inverse, int64_t* n_unique,
+               void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Replaces: aten.embedding_dense_backward(grad, inv, num_rows, -1, False) at srm2/train.py:429.  out[k] = sum of
+ * grad[i] (fp32 [n, D]) over i with idx[i] == k (idx int64 [n] in [0, num_rows)), in the order above; rows of out
+ * without an index are not written (the caller zero-fills).  D <= 512. */
+int elr_segment_sum(const float* grad, const int64_t* idx, int64_t n, int64_t D, int64_t num_rows, float* out,
+                    void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Duplicate-id row-sparse Adam (config C3; the dedup of srm2/train.py:352 and 429 followed by srm2/ops.py:59-67
+ * gpu_adam on the unique rows): state fp32 [C,3,D]; ids int64 [n] in [0, C), repeats allowed; grad fp32 [n,D].
+ * Each unique id gets one Adam step (scalars sc) with the sum of its gradients.  D <= 512. */
+int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
+                   const float sc[8], void* scratch, int64_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

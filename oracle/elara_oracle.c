@@ -185,9 +185,13 @@ int orc_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t 
  * (srm2/train.py:352 torch.unique(..., return_inverse=True) and train.py:429 embedding_dense_backward).
  * Unique ids come out ascending (torch.unique's definition).  The summation order of the reference's
  * embedding backward belongs to ATen and is pinned by no reference test, so this build fixes its own order:
- * for each id, start from the gradient of its first occurrence (lowest occurrence index) and add the others
- * left to right in ascending occurrence index.  Returns the number of unique ids.
+ * the occurrences of one id, in ascending occurrence index, are cut into chunks of ORC_SEG_CHUNK; each chunk is
+ * summed left to right starting from its first gradient, and the chunk sums are added left to right starting
+ * from the first chunk (for at most ORC_SEG_CHUNK occurrences: the plain left-to-right sum).  Returns the number
+ * of unique ids.
  * ------------------------------------------------------------------------------------------------------- */
+#define ORC_SEG_CHUNK 64
+
 static const int64_t* g_sort_ids;
 static int cmp_occ(const void* a, const void* b) {
   int64_t i = *(const int64_t*)a, j = *(const int64_t*)b;
@@ -199,24 +203,33 @@ static int cmp_occ(const void* a, const void* b) {
 int64_t orc_segment_sum(const int64_t* ids, const float* grad, int64_t nocc, int64_t D, int64_t* uniq,
                         float* gsum, int64_t* inverse) {
   int64_t* ord = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nocc > 0 ? nocc : 1));
+  float* part = (float*)malloc(sizeof(float) * (size_t)(D > 0 ? D : 1));
   for (int64_t i = 0; i < nocc; ++i) ord[i] = i;
   g_sort_ids = ids;
   qsort(ord, (size_t)nocc, sizeof(int64_t), cmp_occ);
   int64_t u = -1;
-  for (int64_t q = 0; q < nocc; ++q) {
-    int64_t i = ord[q];
-    const float* g = grad + i * D;
-    if (q == 0 || ids[i] != ids[ord[q - 1]]) {
-      ++u;
-      uniq[u] = ids[i];
-      memcpy(gsum + u * D, g, sizeof(float) * (size_t)D);
-    } else {
-      float* s = gsum + u * D;
-      for (int64_t j = 0; j < D; ++j) s[j] = s[j] + g[j];
+  for (int64_t q0 = 0; q0 < nocc;) {
+    int64_t q1 = q0 + 1;
+    while (q1 < nocc && ids[ord[q1]] == ids[ord[q0]]) ++q1;
+    ++u;
+    uniq[u] = ids[ord[q0]];
+    float* s = gsum + u * D;
+    for (int64_t c0 = q0; c0 < q1; c0 += ORC_SEG_CHUNK) {
+      const int64_t c1 = c0 + ORC_SEG_CHUNK < q1 ? c0 + ORC_SEG_CHUNK : q1;
+      memcpy(part, grad + ord[c0] * D, sizeof(float) * (size_t)D);
+      for (int64_t q = c0 + 1; q < c1; ++q) {
+        const float* g = grad + ord[q] * D;
+        for (int64_t j = 0; j < D; ++j) part[j] = part[j] + g[j];
+      }
+      if (c0 == q0) memcpy(s, part, sizeof(float) * (size_t)D);
+      else for (int64_t j = 0; j < D; ++j) s[j] = s[j] + part[j];
     }
-    if (inverse) inverse[i] = u;
+    if (inverse)
+      for (int64_t q = q0; q < q1; ++q) inverse[ord[q]] = u;
+    q0 = q1;
   }
   free(ord);
+  free(part);
   return u + 1;
 }
 

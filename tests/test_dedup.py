@@ -1,0 +1,225 @@
+"""Batch dedup and duplicate-id gradient reduction (srm2/train.py:352 torch.unique, train.py:429
+embedding_dense_backward) and the fused duplicate-id Adam of config C3.
+
+The reference's summation order belongs to ATen and is pinned by no reference test ("parity unpinned"); this
+build defines the order (per id, ascending occurrence index, chunks of 64 summed left to right, chunk sums added
+left to right).  The CPU tests pin the oracle's restatement of that order by properties that a wrong order or a
+dropped term fails; the GPU tests hold the HIP path to the oracle bitwise.
+"""
+import numpy as np
+import pytest
+import torch
+
+from elara_amd import synth
+from oracle import oracle as O
+
+HP = synth.ADAM
+
+
+def bits(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def lr_sum(rows):
+    """Plain left-to-right float32 sum of rows[0], rows[1], ... starting from rows[0]."""
+    acc = rows[0].astype(np.float32).copy()
+    for r in rows[1:]:
+        acc = (acc + r).astype(np.float32)
+    return acc
+
+
+# ------------------------------------------------------------------------------------------------------------ CPU
+def test_oracle_segment_sum_short_segments_are_left_to_right():
+    rng = np.random.default_rng(0)
+    ids = rng.integers(0, 300, 5000).astype(np.int64)          # every id occurs well under 64 times
+    g = (rng.standard_normal((5000, 16)) * 10.0 ** rng.integers(-6, 3, (5000, 1))).astype(np.float32)
+    u, s, inv = O.segment_sum(ids, g)
+    assert np.array_equal(u, np.unique(ids)) and np.array_equal(u[inv], ids)
+    for q, i in enumerate(u):
+        assert np.array_equal(bits(s[q]), bits(lr_sum(g[ids == i])))
+
+
+def test_oracle_segment_sum_chunked_order_for_long_segments():
+    """An id with 200 occurrences: chunks [0,64), [64,128), [128,192), [192,200) summed left to right, then the
+    four chunk sums left to right.  Values are chosen so that the plain left-to-right sum differs."""
+    rng = np.random.default_rng(1)
+    n = 200
+    ids = np.full(n, 7, np.int64)
+    g = np.zeros((n, 4), np.float32)
+    g[:, 0] = rng.standard_normal(n).astype(np.float32) * np.float32(1e-3)
+    g[0, 1], g[1:, 1] = np.float32(1.0), np.float32(2.0 ** -24)  # left to right drops every small term; chunked keeps some
+    g[:, 2] = (rng.standard_normal(n) * 1e4).astype(np.float32)
+    g[:, 3] = np.float32(-0.0)
+    _, s, _ = O.segment_sum(ids, g)
+    parts = [lr_sum(g[c:c + 64]) for c in range(0, n, 64)]
+    want = lr_sum(np.stack(parts))
+    assert np.array_equal(bits(s[0]), bits(want))
+    assert s[0, 1] != lr_sum(g)[1]                               # the order is observable
+    assert bits(s[0])[3] == bits(np.float32(-0.0))               # -0 + -0 stays -0: sums start from the first term
+
+
+def test_oracle_segment_sum_depends_only_on_each_ids_occurrence_order():
+    """Interleaving other ids differently does not change an id's sum (order = its own occurrence order)."""
+    rng = np.random.default_rng(2)
+    a = (rng.standard_normal((150, 8)) * 1e3).astype(np.float32)
+    b = (rng.standard_normal((90, 8))).astype(np.float32)
+    x_ids = np.concatenate([np.full(150, 3), np.full(90, 9)]).astype(np.int64)
+    x_g = np.concatenate([a, b])
+    perm = rng.permutation(240)
+    # keep each id's own relative order: stable sort of the permuted positions per id
+    order = np.concatenate([np.sort(perm[:150]), np.sort(perm[150:])])
+    y_ids = np.empty(240, np.int64)
+    y_g = np.empty_like(x_g)
+    y_ids[order] = x_ids
+    y_g[order] = x_g
+    ux, sx, _ = O.segment_sum(x_ids, x_g)
+    uy, sy, _ = O.segment_sum(y_ids, y_g)
+    assert np.array_equal(ux, uy) and np.array_equal(bits(sx), bits(sy))
+
+
+def test_oracle_segment_sum_matches_torch_unique_and_totals():
+    rng = np.random.default_rng(3)
+    z = synth.ZipfFields([5000] * 4, 1.05, seed=3, offsets=[0] * 4)
+    ids = z.draw(rng, 3000)
+    g = rng.standard_normal((ids.size, 8)).astype(np.float32)
+    u, s, inv = O.segment_sum(ids, g)
+    tu, tinv = torch.unique(torch.from_numpy(ids), return_inverse=True)
+    assert np.array_equal(tu.numpy(), u) and np.array_equal(tinv.numpy(), inv)
+    # the per-id sums add up to the column totals (fp64 check; tolerance for the fp32 roundings)
+    assert np.allclose(s.astype(np.float64).sum(0), g.astype(np.float64).sum(0), rtol=1e-4, atol=1e-2)
+
+
+def test_zipf_fields_shape_and_range():
+    z = synth.ZipfFields([1000, 50, 7], 1.1, seed=4)
+    ids = z.draw(np.random.default_rng(4), 2000).reshape(2000, 3)
+    assert ids[:, 0].max() < 1000 and ids[:, 1].min() >= 1000 and ids[:, 1].max() < 1050
+    assert ids[:, 2].min() >= 1050 and ids[:, 2].max() < 1057
+    # rank 0 (the hottest) is the most frequent row of a field
+    r = z.ranks(np.random.default_rng(5), 20000)[:, 0]
+    assert np.bincount(r).argmax() == 0
+
+
+# ------------------------------------------------------------------------------------------------------------ GPU
+def zipf_case(seed, n_samples, fields, vocab, alpha, D, scale=1e-3):
+    rng = np.random.default_rng(seed)
+    z = synth.ZipfFields([vocab] * fields, alpha, seed=seed, offsets=[0] * fields)
+    ids = z.draw(rng, n_samples)
+    g = (rng.standard_normal((ids.size, D)) * scale).astype(np.float32)
+    return ids, g
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', ['zipf', 'big_ids', 'one_id', 'distinct', 'single'])
+def test_gpu_unique_matches_torch(dev, case):
+    from elara_amd.dedup import unique
+    rng = np.random.default_rng(10)
+    ids = {'zipf': lambda: zipf_case(10, 20000, 26, 100000, 1.05, 1)[0],
+           'big_ids': lambda: rng.integers(0, 2**40, 50000) // 7 * 7,
+           'one_id': lambda: np.full(70000, 123456789, np.int64),
+           'distinct': lambda: rng.permutation(300000),
+           'single': lambda: np.array([5])}[case]().astype(np.int64)
+    print(f'[gpu-test] unique {case} n={ids.size}', flush=True)
+    u, inv = unique(torch.from_numpy(ids).to(dev))
+    tu, tinv = torch.unique(torch.from_numpy(ids), return_inverse=True)
+    assert torch.equal(u.cpu(), tu) and torch.equal(inv.cpu(), tinv)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('D', [128, 64, 30, 200])
+def test_gpu_embedding_backward_matches_oracle(dev, D):
+    from elara_amd.dedup import embedding_dense_backward
+    print(f'[gpu-test] segment sum D={D}', flush=True)
+    ids, g = zipf_case(11, 8000, 26, 50000, 1.05, D, scale=1.0)
+    u, s, inv = O.segment_sum(ids, g)
+    # the reference's call: indices are the inverse (unique positions), num_weights = U
+    out = embedding_dense_backward(torch.from_numpy(g).to(dev), torch.from_numpy(inv).to(dev), u.size)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(s))
+    # raw ids as indices, with rows never indexed left zero
+    out2 = embedding_dense_backward(torch.from_numpy(g).to(dev), torch.from_numpy(ids).to(dev), 50000)
+    want = np.zeros((50000, D), np.float32)
+    want[u] = s
+    assert np.array_equal(bits(out2.cpu().numpy()), bits(want))
+
+
+@pytest.mark.gpu
+def test_gpu_segment_sum_very_long_segment(dev):
+    """One id with 100,000 occurrences (1,563 chunks) next to short ones."""
+    from elara_amd.dedup import embedding_dense_backward
+    print('[gpu-test] segment sum long', flush=True)
+    rng = np.random.default_rng(12)
+    ids = np.concatenate([np.full(100000, 3), rng.integers(0, 1000, 20000)])[rng.permutation(120000)].astype(np.int64)
+    g = rng.standard_normal((ids.size, 128)).astype(np.float32)
+    u, s, _ = O.segment_sum(ids, g)
+    out = embedding_dense_backward(torch.from_numpy(g).to(dev), torch.from_numpy(ids).to(dev), 1000)
+    torch.cuda.synchronize()
+    want = np.zeros((1000, 128), np.float32)
+    want[u] = s
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('D,idx', [(128, torch.int64), (64, torch.int32), (96, torch.int64)])
+def test_gpu_adam_dedup_matches_oracle(dev, D, idx):
+    from elara_amd.dedup import adam_dedup
+    print(f'[gpu-test] adam_dedup D={D}', flush=True)
+    R = 200000
+    rng = np.random.default_rng(13)
+    state = np.zeros((R, 3, D), np.float32)
+    state[:, 0] = (rng.standard_normal((R, D)) * 0.05).astype(np.float32)
+    gpu = torch.from_numpy(state).to(dev)
+    for t in range(1, 4):
+        ids, g = zipf_case(100 + t, 4000, 26, R, 1.05, D)
+        u, s, _ = O.segment_sum(ids, g)
+        O.cpu_adam(state, u, s, O.adam_scalars(*HP, t), 8)
+        adam_dedup(gpu, torch.from_numpy(ids).to(dev, idx), torch.from_numpy(g).to(dev), *HP, t)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(gpu.cpu().numpy()), bits(state))
+
+
+@pytest.mark.gpu
+def test_gpu_dedup_edge_cases(dev):
+    from elara_amd.dedup import adam_dedup, embedding_dense_backward, unique
+    z = torch.empty(0, dtype=torch.int64, device=dev)
+    u, inv = unique(z)
+    assert u.numel() == 0 and inv.numel() == 0
+    assert embedding_dense_backward(torch.empty(0, 8, device=dev), z, 5).abs().sum().item() == 0
+    pool = torch.randn(10, 3, 8, device=dev)
+    ref = pool.clone()
+    adam_dedup(pool, z, torch.empty(0, 8, device=dev), *HP, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, ref)
+    # ids out of range are skipped by the kernel's check (undefined in the reference)
+    adam_dedup(pool, torch.tensor([3, 3, 10, 1 << 20], device=dev), torch.ones(4, 8, device=dev), *HP, 1)
+    torch.cuda.synchronize()
+    changed = (pool != ref).any(dim=2).any(dim=1).nonzero().flatten().tolist()
+    assert changed == [3]
+    with pytest.raises(RuntimeError):
+        unique(torch.tensor([-1, 2], device=dev))
+
+
+@pytest.mark.gpu
+def test_gpu_c3_full_size_two_steps(dev):
+    """Config C3 at full size: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step; touched rows bitwise
+    equal to the oracle (segment sum + cpu_adam on a compact copy of the touched rows)."""
+    from elara_amd.dedup import adam_dedup
+    from elara_amd.gpu_ops import init_rows
+    print('[gpu-test] C3 full size', flush=True)
+    R, D, B, F = 10_000_000, 128, 131_072, 26
+    z = synth.ZipfFields([R] * F, 1.05, seed=0, offsets=[0] * F)
+    rng = np.random.default_rng(0)
+    table = init_rows(torch.arange(R, device=dev), D, 0, synth.bound_for(D))
+    batches = []
+    for t in (1, 2):
+        ids = z.draw(rng, B)
+        g = torch.randn(ids.size, D, device=dev, generator=torch.Generator(dev).manual_seed(t)) * 1e-3
+        batches.append((ids, g))
+    touched = np.unique(np.concatenate([b[0] for b in batches]))
+    tt = torch.from_numpy(touched).to(dev)
+    compact = table[tt].cpu().numpy()
+    for t, (ids, g) in enumerate(batches, start=1):
+        adam_dedup(table, torch.from_numpy(ids).to(dev), g, *HP, t)
+        u, s, _ = O.segment_sum(ids, g.cpu().numpy())
+        O.cpu_adam(compact, np.searchsorted(touched, u).astype(np.int64), s, O.adam_scalars(*HP, t), 16)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(table[tt].cpu().numpy()), bits(compact))
