@@ -33,6 +33,7 @@ SIGNATURES = {
                                        c_f32, c_vp, c_i64, c_vp]),
     'elr_dir_scratch_bytes': (c_i64, [c_i64, c_i64]),
     'elr_dedup_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_copy_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     'elr_unique': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_segment_sum': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'elr_adam_dedup': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_f32p, c_vp, c_i64, c_vp]),

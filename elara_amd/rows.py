@@ -1,0 +1,56 @@
+"""Row copies in HBM: gradient-log appends and the executor's row gathers and scatters.
+
+    log_append(logs, ids, g)            logs[ids] = g          srm2/elara.py:569-570 (host cpu_scatter into the log
+                                                               arena; the arena is in HBM here), and the
+                                                               resident-history record glog.index_put_((dyn, j), g)
+                                                               (srm2/elara.py:501, 524) with ids = dyn * K + j
+    copy_rows(dst, dst_idx, src, src_idx)
+                                        dst[dst_idx] = src[src_idx] (None = all rows in order)
+
+Both run the HIP kernel behind elr_copy_rows (elara_amd/csrc/rows.hip) on torch's current stream.  Rows are the
+trailing dimensions flattened (a [C,3,D] state has rows of 3*D floats).
+"""
+import torch
+
+from . import _lib
+
+
+def _rows2d(t, name):
+    if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.dim() >= 1):
+        raise RuntimeError(f'{name} must be a contiguous cuda float32 tensor')
+    n = t.shape[0]
+    return n, (t.numel() // n if n else 0)
+
+
+def _index(idx, dev, name):
+    if idx is None:
+        return None
+    if not (idx.is_cuda and idx.device == dev and idx.dtype in (torch.int32, torch.int64)):
+        raise RuntimeError(f'{name} must be a cuda int32/int64 tensor on {dev}')
+    return idx.reshape(-1).to(torch.int64).contiguous()
+
+
+def copy_rows(dst, dst_idx, src, src_idx=None):
+    """dst[dst_idx[i]] = src[src_idx[i]] for every i (rows of the same width); indices out of range are skipped."""
+    nd, wd = _rows2d(dst, 'dst')
+    ns, ws = _rows2d(src, 'src')
+    di, si = _index(dst_idx, dst.device, 'dst_idx'), _index(src_idx, dst.device, 'src_idx')
+    n = di.numel() if di is not None else (si.numel() if si is not None else ns)
+    if si is not None and di is not None and si.numel() != n:
+        raise RuntimeError('dst_idx and src_idx must have the same length')
+    if si is None and n > ns:
+        raise RuntimeError(f'src has {ns} rows, {n} needed')
+    if n == 0:
+        return dst
+    if wd != ws:
+        raise RuntimeError(f'row widths differ: {wd} vs {ws}')
+    with torch.cuda.device(dst.device):
+        rc = _lib.lib().elr_copy_rows(_lib.ptr(dst), nd, _lib.ptr(di), _lib.ptr(src), ns, _lib.ptr(si), n, wd,
+                                      _lib.stream_of(dst))
+    _lib.check(rc, 'elr_copy_rows')
+    return dst
+
+
+def log_append(logs, ids, g):
+    """logs[ids[i]] = g[i]: append gradient rows to the log arena at their allocated log ids."""
+    return copy_rows(logs, ids, g, None)

@@ -88,3 +88,26 @@ class ZipfFields:
         ids = (self.a[None, :].astype(object) * k.astype(object) + self.b[None, :]) % self.vocab[None, :] \
             if self.vocab.max() >= (1 << 31) else (self.a[None, :] * k + self.b[None, :]) % self.vocab[None, :]
         return (np.asarray(ids, dtype=np.int64) + self.offsets[None, :]).reshape(-1)
+
+
+class C5Tables:
+    """Config C5: `T` tables with vocabularies round(exp(U(ln lo, ln hi))), one Zipf(alpha) field per table
+    (ZipfFields), rows of table t at toff[t] + [0, vocab_t)."""
+
+    def __init__(self, T=26, lo=1e3, hi=4e7, alpha=1.1, seed=0):
+        rng = np.random.default_rng(seed)
+        self.vocab = np.round(np.exp(rng.uniform(np.log(lo), np.log(hi), T))).astype(np.int64)
+        self.toff = np.concatenate([[0], np.cumsum(self.vocab)[:-1]]).astype(np.int64)
+        self.R = int(self.vocab.sum())
+        self.fields = ZipfFields(self.vocab, alpha, seed=seed + 1, offsets=self.toff)
+
+    def batch(self, rng, B):
+        return self.fields.draw(rng, B)
+
+    def static_rows(self, rng, B, n_static, n_batches=20):
+        """The n_static most frequent rows over n_batches profiling batches (ties: lower row first), sorted
+        ascending -- the reference's static hot set (srm2/train.py:262-270) on synthetic data."""
+        ids = np.concatenate([self.batch(rng, B) for _ in range(n_batches)])
+        u, c = np.unique(ids, return_counts=True)
+        top = np.lexsort((u, -c))[:n_static]
+        return np.sort(u[top]).astype(np.int64)

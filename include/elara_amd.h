@@ -162,6 +162,16 @@ int elr_segment_sum(const float* grad, const int64_t* idx, int64_t n, int64_t D,
 int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
                    const float sc[8], void* scratch, int64_t scratch_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * Row copies: dst[dst_idx[i]] = src[src_idx[i]], i < n, rows of W floats (NULL index = identity).
+ * Replaces: the gradient-log append logs[A_ids] = g (srm2/elara.py:569-570 with srm2/csrc/srm2_cpu.cpp:167-180
+ * cs_append semantics; here the log arena is in HBM), the resident-history record glog.index_put_((dyn, j), g)
+ * (srm2/elara.py:501, 524) and the executor's index_select / index_copy_ of rows (srm2/elara.py:480-488,
+ * 506-531).  Rows with an index outside [0, dst_rows) / [0, src_rows) are skipped.  Device pointers.
+ * ------------------------------------------------------------------------------------------------------- */
+int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
+                  const int64_t* src_idx, int64_t n, int64_t W, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

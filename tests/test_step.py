@@ -1,0 +1,118 @@
+"""The whole ELARA step with HBM-resident arenas (config C5; elara_amd.step, the counterpart of srm2/elara.py's
+planner and executor): the HIP kernels against the CPU oracle driving the identical step.
+
+Both runs see the same batches and occurrence gradients; the planner logic is shared (torch ops on each device),
+the hot-path kernels differ (HIP vs oracle/elara_oracle.c).  After the run the directory, the pool, the resident
+histories, the MAT and log arenas and the eval-style weights of every touched row (srm2/elara.py:582-604) must be
+bitwise equal.  Trash rows (whose contents the reference leaves unspecified) are excluded.
+"""
+import numpy as np
+import pytest
+import torch
+
+from elara_amd import synth
+from oracle_backend import OracleBackend
+
+HP = synth.ADAM
+
+
+def make(cfg, device, backend=None):
+    from elara_amd.step import ElaraStep
+    return ElaraStep(cfg['toff'], cfg['R'], cfg['D'], cfg['C'], static_rows=cfg['static'], K=3, kthr=3,
+                     evl=cfg.get('evl', True), L=cfg.get('L', 8), depth=3, st_mode=cfg.get('st', 'T'),
+                     seed=42, bound=cfg['bound'], hp=HP, max_step=cfg['steps'] + 2, log_cap=cfg['log_cap'],
+                     mat_cap=cfg['mat_cap'], device=device, backend=backend)
+
+
+def config(T, lo, hi, B, steps, C, n_static, D=128, seed=0, **kw):
+    tabs = synth.C5Tables(T=T, lo=lo, hi=hi, alpha=1.1, seed=seed)
+    rng = np.random.default_rng(seed + 7)
+    static = tabs.static_rows(rng, B, n_static, n_batches=10) if n_static else None
+    batches = [torch.from_numpy(tabs.batch(rng, B)) for _ in range(steps)]
+    O = B * T
+    cfg = dict(toff=tabs.toff, R=tabs.R, D=D, C=C, static=static, steps=steps, bound=synth.bound_for(D),
+               log_cap=steps * O + 16, mat_cap=min(tabs.R + 1, steps * O + 16), batches=batches, seed=seed)
+    cfg.update(kw)
+    return cfg
+
+
+def grads_fn(cfg, device):
+    D = cfg['D']
+
+    def g(j):
+        gen = torch.Generator().manual_seed(1000 + j)
+        return (torch.randn(cfg['batches'][j].numel(), D, generator=gen, dtype=torch.float64) * 1e-3).float()
+    return g
+
+
+def compare(a, b, cfg):
+    """Assert the two steps' states are equal; returns the number of touched rows compared."""
+    def eq(x, y, what):
+        x, y = x.detach().cpu(), y.detach().cpu()
+        if x.dtype == torch.float32:
+            x, y = x.view(torch.int32), y.view(torch.int32)
+        assert x.shape == y.shape and torch.equal(x, y), what
+    for name in ('code', 'loc', 'ent', 'n_lfree', 'log_top', 'mat_top', 'live', 'adm_c0', 'rj', 'pstep', 'slot_of',
+                 'slot_row', 'rok'):
+        eq(getattr(a, name), getattr(b, name), name)
+    eq(a.lstep[:-1], b.lstep[:-1], 'lstep')
+    eq(a.lfree[:-1], b.lfree[:-1], 'lfree')
+    eq(a.pool, b.pool, 'pool')
+    eq(a.glog[:-1], b.glog[:-1], 'glog')
+    mt, lt = int(a.mat_top), int(a.log_top)
+    eq(a.mat[:min(mt, a.R)], b.mat[:min(mt, b.R)], 'MAT arena')
+    eq(a.logs[:lt], b.logs[:lt], 'log arena')
+    rows = torch.unique(torch.cat(cfg['batches']))
+    eq(a.eval_weights(rows.to(a.d), full=True), b.eval_weights(rows.to(b.d), full=True), 'eval weights')
+    return rows.numel()
+
+
+def test_step_runs_on_cpu_with_oracle_backend():
+    """The step itself on CPU tensors with the oracle kernels: invariants of srm2/train.py:474-477 hold and every
+    class of rows occurs."""
+    from elara_amd.step import run
+    cfg = config(T=5, lo=100, hi=3000, B=300, steps=40, C=700, n_static=400)
+    st = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
+    run(st, cfg['batches'], grads_fn(cfg, 'cpu'))
+    K = st.K
+    ent = st.ent[:st.R * K].view(st.R, K)
+    assert int(st.live) == int((ent >= 0).sum()) and int(st.live) + int(st.n_lfree) == int(st.log_top)
+    s = st.stats
+    assert s['hits'] and s['adm'] and s['ev'] and s['compactions'] and s['appends'] and s['F'], s
+    # rows that reached M hold MAT slots; codes are I, L_1..L_K or M only
+    assert torch.all(st.loc[:st.R][st.code == st.MAT][st.slot_of[st.code == st.MAT] < 0] >= 0)
+    assert int(st.code.min()) >= 0 and int(st.code.max()) <= st.MAT
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S'])
+def test_gpu_step_matches_oracle_step(dev, name):
+    from elara_amd.step import run
+    print(f'[gpu-test] elara step {name}', flush=True)
+    kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}}[name]
+    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, C=2500, n_static=1500, **kw)
+    g = make(cfg, dev)
+    c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
+    gf = grads_fn(cfg, None)
+    run(g, cfg['batches'], gf)
+    run(c, cfg['batches'], gf)
+    torch.cuda.synchronize()
+    assert compare(g, c, cfg) > 0
+    assert g.stats == c.stats
+
+
+@pytest.mark.gpu
+def test_gpu_step_c5_full_shape(dev):
+    """Config C5 shapes: 26 tables (vocab log-uniform in [1e3, 4e7], ~75M rows), batch 16,384 x 26 Zipf(1.1),
+    D = 128, pool 337,626 (321,242 static hot rows), K = 3, evl on; 12 steps, HIP vs oracle bitwise."""
+    from elara_amd.step import run
+    print('[gpu-test] elara step C5 full shape', flush=True)
+    cfg = config(T=26, lo=1e3, hi=4e7, B=16384, steps=12, C=337_626, n_static=337_626 - 16_384)
+    g = make(cfg, dev)
+    c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2, nthreads=16))
+    gf = grads_fn(cfg, None)
+    run(g, cfg['batches'], gf)
+    run(c, cfg['batches'], gf)
+    torch.cuda.synchronize()
+    assert compare(g, c, cfg) > 100_000
+    assert g.stats == c.stats
