@@ -167,6 +167,146 @@ def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
     return None
 
 
+def _timed_steps(step_fn, steps, warmup):
+    """Run warmup + steps calls of step_fn(i); the timed steps are bracketed by device synchronisation.  Returns
+    (seconds for the timed steps, per-step ms from events on the current stream)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        step_fn(i)
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        step_fn(warmup + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    return el, [a.elapsed_time(b) for a, b in ev]
+
+
+def _line(metric, value, unit, args, steps, warmup, el, config, gbytes_per_step, dtype='f32', extra=None):
+    gbs = gbytes_per_step * steps / el
+    res = {'metric': metric, 'value': value, 'unit': unit, 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
+           'ms_per_step': el / steps * 1e3, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
+           'dtype': dtype, 'data': 'synthetic', 'config': config,
+           'step_GBps': gbs, 'step_frac_of_hbm_peak': gbs / HBM_PEAK_GBS}
+    if extra:
+        res.update(extra)
+    return res
+
+
+def mode_c1(args):
+    """Config C1: 1,048,576 x 64 table, 65,536 unique rows per step (uniform, unsorted), t = 1..10."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.gpu_ops import init_rows
+    from elara_amd.ops import gpu_adam
+    dev = torch.device('cuda:0')
+    R, D, n = 1 << 20, 64, 65_536
+    table = init_rows(torch.arange(R, device=dev), D, 0, synth.bound_for(D))
+    rng = np.random.default_rng(0)
+    ids = [torch.from_numpy(synth.unique_rows(rng, R, n)).to(dev) for _ in range(10)]
+    gs = [torch.from_numpy(synth.grads(rng, n, D)).to(dev) for _ in range(10)]
+    steps, warmup = 10, 2
+    el, ms = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 10], *synth.ADAM, i + 1), steps, warmup)
+    return _line('C1 row-sparse Adam rows/s (d=64)', n * steps / el, 'rows/s', args, steps, warmup, el,
+                 {'workload': 'C1 row-sparse Adam: 1,048,576 x 64 fp32 table, 65,536 unique rows per step',
+                  'rows_per_step': n, 'dim': D}, adam_bytes(n, D) / 1e9,
+                 extra={'mean_launch_ms': float(np.mean(ms))})
+
+
+def mode_c3(args):
+    """Config C3: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step with duplicates: dedup, fixed-order
+    segment sum and Adam on the unique rows (elr_adam_dedup).  Four resident batches are cycled."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.dedup import adam_dedup
+    from elara_amd.gpu_ops import init_rows
+    dev = torch.device('cuda:0')
+    R, D, B, F = 10_000_000, 128, 131_072, 26
+    table = init_rows(torch.arange(R, device=dev), D, 0, synth.bound_for(D))
+    z = synth.ZipfFields([R] * F, 1.05, seed=0, offsets=[0] * F)
+    rng = np.random.default_rng(0)
+    host = [z.draw(rng, B) for _ in range(4)]
+    U = [int(np.unique(h).size) for h in host]
+    ids = [torch.from_numpy(h).to(dev) for h in host]
+    gen = torch.Generator(dev).manual_seed(0)
+    gs = [torch.randn(B * F, D, device=dev, generator=gen) * 1e-3 for _ in range(4)]
+    steps, warmup = args.steps_c3, 3
+    el, ms = _timed_steps(lambda i: adam_dedup(table, ids[i % 4], gs[i % 4], *synth.ADAM, i + 1), steps, warmup)
+    O = B * F
+    Umean = float(np.mean(U))
+    byts = (O * (4 * D + 8) + Umean * (28 * D + 8)) / 1e9
+    return _line('C3 duplicate-id sparse Adam occurrences/s (d=128)', O * steps / el, 'occurrences/s', args, steps,
+                 warmup, el, {'workload': 'C3 duplicate-id Adam: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) '
+                                          'ids per step, dedup + fixed-order segment sum + Adam',
+                              'occurrences_per_step': O, 'unique_rows_per_step': Umean, 'dim': D}, byts,
+                 extra={'unique_rows_per_s': Umean * steps / el, 'mean_step_ms_events': float(np.mean(ms))})
+
+
+def mode_c4(args):
+    """Config C4: 50,000,000 x 256 table (153.6 GB resident), 262,144 unique Zipf(1.1) ids per step, 50 steps."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.gpu_ops import init_rows
+    from elara_amd.ops import gpu_adam
+    dev = torch.device('cuda:0')
+    R, D, n = 50_000_000, 256, 262_144
+    table = torch.empty(R, 3, D, device=dev)
+    for a in range(0, R, 1 << 23):
+        rows = torch.arange(a, min(R, a + (1 << 23)), device=dev)
+        init_rows(rows, D, 0, synth.bound_for(D), out=table[a:a + rows.numel()])
+    z = synth.ZipfFields([R], 1.1, seed=4, offsets=[0])
+    rng = np.random.default_rng(4)
+    ids = [torch.from_numpy(synth.unique_zipf(rng, z, n)).to(dev) for _ in range(10)]
+    gen = torch.Generator(dev).manual_seed(4)
+    gs = [torch.randn(n, D, device=dev, generator=gen) * 1e-3 for _ in range(4)]
+    steps, warmup = 50, 3
+    el, ms = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 4], *synth.ADAM, i + 1), steps, warmup)
+    return _line('C4 large-row sparse Adam rows/s (d=256, 153.6 GB table)', n * steps / el, 'rows/s', args, steps,
+                 warmup, el, {'workload': 'C4 large-row stress: 50,000,000 x 256 fp32 table (w, m, v: 153.6 GB in '
+                                          'HBM), 262,144 unique Zipf(1.1) rows per step', 'rows_per_step': n,
+                              'dim': D}, adam_bytes(n, D) / 1e9,
+                 extra={'mean_launch_ms': float(np.mean(ms))})
+
+
+def mode_c5(args):
+    """Config C5: the whole ELARA step (elara_amd.step) with HBM-resident arenas: 26 tables (vocab log-uniform in
+    [1e3, 4e7]), batch 16,384 x 26 Zipf(1.1), D = 128, pool 337,626 with 321,242 static hot rows, K = 3, evl on,
+    200 steps.  Occurrence gradients: 8 resident buffers cycled."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.step import ElaraStep, run
+    dev = torch.device('cuda:0')
+    B, D, steps = 16_384, 128, args.steps_c5
+    tabs = synth.C5Tables(T=26, lo=1e3, hi=4e7, alpha=1.1, seed=0)
+    rng = np.random.default_rng(7)
+    C = 337_626
+    static = tabs.static_rows(rng, B, C - 16_384, n_batches=10)
+    batches = [torch.from_numpy(tabs.batch(rng, B)).to(dev) for _ in range(steps)]
+    O = B * 26
+    st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
+                   seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=steps + 2, log_cap=steps * O + 16,
+                   mat_cap=steps * O // 2, device=dev)
+    gen = torch.Generator(dev).manual_seed(5)
+    gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run(st, batches, lambda j: gs[j % 8])
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    s = st.stats
+    uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
+    return _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, 0, el,
+                 {'workload': 'C5 full ELARA step, HBM-resident arenas: 26 tables (R=%d), batch 16,384 x 26 '
+                              'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % tabs.R,
+                  'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, 0.0,
+                 extra={'steps_per_s': steps / el, 'stats': s, 'note': 'step_GBps not reported for C5 (mixed '
+                        'kernels; per-kernel bytes in profiles/)'})
+
+
 def copy_calibration(args):
     """A plain device copy of known size (PMC calibration of FETCH_SIZE / WRITE_SIZE)."""
     import torch
@@ -186,15 +326,24 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=50)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--mode', default='headline', choices=['headline', 'copy'])
+    ap.add_argument('--mode', default='headline', choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'all'])
+    ap.add_argument('--steps-c3', type=int, default=100)
+    ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path (the sharding design is '
               'described in DESIGN.md); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
-    res = copy_calibration(args) if args.mode == 'copy' else headline(args)
-    print(json.dumps(res), flush=True)
+    fns = {'headline': headline, 'copy': copy_calibration, 'c1': mode_c1, 'c3': mode_c3, 'c4': mode_c4,
+           'c5': mode_c5}
+    for m in (['headline', 'c1', 'c3', 'c4', 'c5'] if args.mode == 'all' else [args.mode]):
+        res = fns[m](args)
+        print(json.dumps(res, default=float), flush=True)
+        import gc
+        import torch
+        gc.collect()
+        torch.cuda.empty_cache()
 
 
 if __name__ == '__main__':

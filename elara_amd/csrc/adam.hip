@@ -163,12 +163,21 @@ extern "C" int elr_scalar_table(double lr, double b1, double b2, double eps, int
   return ELR_OK;
 }
 
+extern "C" int elr_scalar_recip(const float* table_host, int64_t table_rows, double* recip_host) {
+  if (table_rows < 0 || (table_rows && (!table_host || !recip_host))) return ELR_EINVAL;
+  for (int64_t t = 0; t < table_rows; ++t) {
+    recip_host[2 * t] = 1.0 / (double)table_host[8 * t + 5];
+    recip_host[2 * t + 1] = 1.0 / (double)table_host[8 * t + 6];
+  }
+  return ELR_OK;
+}
+
 extern "C" int elr_adam_rows(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n,
                              int64_t D, const float sc[8], void* stream) {
   if (n < 0 || D <= 0 || C < 0 || !sc) return ELR_EINVAL;
   if (n == 0) return ELR_OK;
   if (!state || !slots || !grad) return ELR_EINVAL;
-  const elr::AdamScalars s = {sc[0], sc[1], sc[2], sc[3], sc[4], sc[5], sc[6], sc[7]};
+  const elr::AdamScalars s = elr::make_scalars(sc);
   hipStream_t st = (hipStream_t)stream;
   if (idx64) return elr::launch_adam(state, C, (const int64_t*)slots, grad, n, D, s, st);
   return elr::launch_adam(state, C, (const int32_t*)slots, grad, n, D, s, st);

@@ -329,6 +329,97 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
   }
 }
 
+// Wave-per-row form of k_seg_final for D = 64*VPL (lane l holds floats [l*VPL, l*VPL + VPL)): no loop, each
+// wave owns kSegPerWave consecutive segments starting at u_base + wave * kSegPerWave; waves past U exit.  The
+// segment bounds, the row id and (MODE 1) its w, m, v are loaded before the gradients, the first chunk's
+// occurrence indices with one vector load, then every gradient row of the chunk; the Adam update follows.
+constexpr int kSegPerWave = 2;
+
+template <int VPL, int MODE>
+__global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__ grad,
+                                                       const int32_t* __restrict__ sv,
+                                                       const int64_t* __restrict__ seg_start,
+                                                       const int64_t* __restrict__ uniq,
+                                                       const int32_t* __restrict__ chunk_off,
+                                                       const float* __restrict__ parts,
+                                                       const int64_t* __restrict__ d_U, int64_t u_base,
+                                                       float* __restrict__ out, int64_t nrows, AdamScalars s) {
+  constexpr int64_t D = 64 * VPL;
+  constexpr int SW = kSegPerWave;
+  const int lane = threadIdx.x & 63;
+  const int64_t U = *d_U;
+  const int64_t u0 = u_base + wave_id() * SW;
+  if (u0 >= U) return;
+  int64_t s0[SW], len[SW], row[SW];
+  bool ok[SW];
+  RowFrag<VPL> w[SW], m[SW], v[SW];
+#pragma unroll
+  for (int q = 0; q < SW; ++q) {
+    const int64_t u = u0 + q;
+    ok[q] = u < U;
+    s0[q] = ok[q] ? seg_start[u] : 0;
+    len[q] = ok[q] ? seg_start[u + 1] - s0[q] : 0;
+    row[q] = ok[q] ? uniq[u] : -1;
+    ok[q] = ok[q] && row[q] >= 0 && row[q] < nrows;
+    if (MODE == 1 && ok[q]) {
+      const float* rec = out + row[q] * 3 * D + lane * VPL;
+      w[q] = frag_load<VPL, false>(rec);
+      m[q] = frag_load<VPL, false>(rec + D);
+      v[q] = frag_load<VPL, false>(rec + 2 * D);
+    }
+  }
+  int32_t my[SW];
+#pragma unroll
+  for (int q = 0; q < SW; ++q) {
+    const int64_t l0 = len[q] < kSegChunk ? len[q] : kSegChunk;
+    my[q] = (ok[q] && lane < l0) ? sv[s0[q] + lane] : 0;
+  }
+  RowFrag<VPL> acc[SW];
+#pragma unroll
+  for (int q = 0; q < SW; ++q) {
+    if (!ok[q]) continue;
+    const int l0 = (int)(len[q] < kSegChunk ? len[q] : kSegChunk);
+    constexpr int UN = 8;
+    for (int k0 = 0; k0 < l0; k0 += UN) {
+      RowFrag<VPL> g[UN];
+#pragma unroll
+      for (int e = 0; e < UN; ++e)
+        if (k0 + e < l0) {
+          const int64_t o = (int64_t)__builtin_amdgcn_readlane(my[q], k0 + e);
+          g[e] = frag_load<VPL, true>(grad + o * D + lane * VPL);
+        }
+#pragma unroll
+      for (int e = 0; e < UN; ++e)
+        if (k0 + e < l0) {
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) acc[q].v[j] = (k0 + e == 0) ? g[e].v[j] : acc[q].v[j] + g[e].v[j];
+        }
+    }
+    const int64_t extra = (len[q] - 1) / kSegChunk;
+    if (extra) {
+      const int64_t pb = (int64_t)chunk_off[u0 + q];
+      for (int64_t c = 0; c < extra; ++c) {
+        const RowFrag<VPL> pc = frag_load<VPL, false>(parts + (pb + c) * D + lane * VPL);
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) acc[q].v[j] = acc[q].v[j] + pc.v[j];
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < SW; ++q) {
+    if (!ok[q]) continue;
+    if (MODE == 0) {
+      frag_store<VPL>(out + row[q] * D + lane * VPL, acc[q]);
+    } else {
+      frag_adam<VPL>(w[q], m[q], v[q], acc[q], s);
+      float* rec = out + row[q] * 3 * D + lane * VPL;
+      frag_store<VPL>(rec, w[q]);
+      frag_store<VPL>(rec + D, m[q]);
+      frag_store<VPL>(rec + 2 * D, v[q]);
+    }
+  }
+}
+
 // ---- host side -------------------------------------------------------------------------------------------------
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
@@ -441,9 +532,33 @@ static void seg_reduce(const float* grad, int64_t D, const int32_t* sv, DedupScr
                                                        out, nrows, s);
 }
 
+template <int VPL, int MODE>
+static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S, const int64_t* uniq, int64_t n,
+                           float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+  constexpr int64_t D = 64 * VPL;
+  k_seg_partials<VPL><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
+                                                                     S.chunk_seg, S.d_tot + 1, S.parts);
+  // one launch per range of at most 2^22 blocks (4 waves of kSegPerWave segments each); U <= n
+  const int64_t per = kOneShotBlocks * 4 * kSegPerWave;
+  for (int64_t a = 0; a < n; a += per) {
+    const int64_t m = n - a < per ? n - a : per;
+    k_seg_final_wpr<VPL, MODE><<<(unsigned)cdiv(m, 4 * kSegPerWave), 256, 0, st>>>(
+        grad, sv, S.seg_start, uniq, S.chunk_off, S.parts, S.d_tot, a, out, nrows, s);
+  }
+}
+
 template <int MODE>
 static int seg_reduce_d(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
                         int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+  if (aligned16(grad) && aligned16(out)) {
+    switch (D) {
+      case 64: seg_reduce_wpr<1, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
+      case 128: seg_reduce_wpr<2, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
+      case 256: seg_reduce_wpr<4, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
+      case 512: seg_reduce_wpr<8, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
+      default: break;
+    }
+  }
   const int64_t nq = cdiv(D, 64);
   switch (nq) {
     case 1: seg_reduce<1, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
@@ -517,7 +632,7 @@ extern "C" int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const
   DedupScratch S;
   if (scratch_bytes < dedup_scratch_bytes(n, D, &S, scratch)) return ELR_ECAPACITY;
   hipStream_t st = (hipStream_t)stream;
-  const AdamScalars s = {sc[0], sc[1], sc[2], sc[3], sc[4], sc[5], sc[6], sc[7]};
+  const AdamScalars s = make_scalars(sc);
   const int kb = bits_for(C);
   const int cur = kb <= 32 ? dedup_core<uint32_t>(ids, n, kb, S, nullptr, nullptr, st)
                            : dedup_core<uint64_t>(ids, n, kb, S, nullptr, nullptr, st);

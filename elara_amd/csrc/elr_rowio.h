@@ -91,10 +91,22 @@ __device__ __forceinline__ RowFrag<VPL> frag_zero() {
   return z;
 }
 
-// Scalars of one table row, read through the scalar cache when `step` is wave-uniform.
-__device__ __forceinline__ AdamScalars table_scalars(const float* __restrict__ table, int64_t step) {
+// Scalars of one table row, read through the scalar cache when `step` is wave-uniform.  recip [S, 2] holds
+// RN_f64(1/bc1), RN_f64(1/bc2) per row (elr_scalar_recip).
+__device__ __forceinline__ AdamScalars table_scalars(const float* __restrict__ table,
+                                                     const double* __restrict__ recip, int64_t step) {
   const float* t = table + step * 8;
-  return AdamScalars{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
+  return AdamScalars{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], recip[2 * step], recip[2 * step + 1]};
+}
+
+// The same without a reciprocal table (recip may be NULL): the reciprocals are then computed here with the
+// correctly rounded double division.
+__device__ __forceinline__ AdamScalars table_scalars_any(const float* __restrict__ table,
+                                                         const double* __restrict__ recip, int64_t step) {
+  const float* t = table + step * 8;
+  const double r1 = recip ? recip[2 * step] : 1.0 / (double)t[5];
+  const double r2 = recip ? recip[2 * step + 1] : 1.0 / (double)t[6];
+  return AdamScalars{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7], r1, r2};
 }
 
 // Index of this wave in the grid and the number of waves, both wave-uniform (SGPR) values.

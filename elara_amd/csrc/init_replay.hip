@@ -11,7 +11,8 @@
 // flight, and each record is written once.  The kernels have no loop: a loop back-edge makes the compiler guard the
 // next iteration's loads with vmcnt(0) waits that also drain this iteration's stores, so very large calls are split
 // into several launches on the host instead.
-// Other D: the generic kernels below (2^lg lanes per row with 16-byte chunks, or one float per lane).
+// Other D, or no reciprocal table: the generic kernels below (2^lg lanes per row with 16-byte chunks, or one float
+// per lane).
 #include "elr_rowio.h"
 
 namespace elr {
@@ -55,10 +56,13 @@ __global__ __launch_bounds__(256) void k_init_rows_scalar(float* __restrict__ ou
   }
 }
 
-__device__ __forceinline__ AdamScalars load_scalars(const float* __restrict__ table, int64_t step) {
+__device__ __forceinline__ AdamScalars load_scalars(const float* __restrict__ table, const double* __restrict__ recip,
+                                                    int64_t step) {
   const float4* t = reinterpret_cast<const float4*>(table + step * 8);
   const float4 a = t[0], b = t[1];
-  return AdamScalars{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  const double r1 = recip ? recip[2 * step] : 1.0 / (double)b.y;
+  const double r2 = recip ? recip[2 * step + 1] : 1.0 / (double)b.z;
+  return AdamScalars{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, r1, r2};
 }
 
 // Row i is valid when every used step indexes the table and every used log entry exists.
@@ -83,7 +87,8 @@ __global__ __launch_bounds__(256) void k_replay_v4(float* __restrict__ out, cons
                                                    const int64_t* __restrict__ offs,
                                                    const int32_t* __restrict__ steps, const int32_t* __restrict__ cnt,
                                                    int64_t n, int nchunk, int lg, uint32_t seed, float bound,
-                                                   const float* __restrict__ table, int64_t table_rows) {
+                                                   const float* __restrict__ table, const double* __restrict__ recip,
+                                                   int64_t table_rows) {
   const int lane = threadIdx.x & 63;
   const int l = lane & ((1 << lg) - 1);
   const int64_t rpw = 64 >> lg;
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(256) void k_replay_v4(float* __restrict__ out, cons
       float4 m = zero, v = zero;
 #pragma unroll
       for (int k = 0; k < K; ++k)
-        if (k < c) adam_vec4(w, m, v, g[k], load_scalars(table, st[k]));
+        if (k < c) adam_vec4(w, m, v, g[k], load_scalars(table, recip, st[k]));
       dst[ch] = w;
       dst[nchunk + ch] = m;
       dst[2 * nchunk + ch] = v;
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(256) void k_replay_scalar(float* __restrict__ out, 
                                                        const int32_t* __restrict__ steps,
                                                        const int32_t* __restrict__ cnt, int64_t n, int64_t D,
                                                        uint32_t seed, float bound, const float* __restrict__ table,
-                                                       int64_t table_rows) {
+                                                       const double* __restrict__ recip, int64_t table_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
@@ -140,9 +145,7 @@ __global__ __launch_bounds__(256) void k_replay_scalar(float* __restrict__ out, 
       float w = init_elem((uint32_t)((uint64_t)r * (uint64_t)D + (uint64_t)j), rk, seed, bound), m = 0.f, v = 0.f;
       for (int k = 0; k < K; ++k) {
         if (k >= c) break;
-        const float* t = table + (int64_t)st[k] * 8;
-        const AdamScalars s{t[0], t[1], t[2], t[3], t[4], t[5], t[6], t[7]};
-        adam_elem(w, m, v, logs[(o + k) * D + j], s);
+        adam_elem(w, m, v, logs[(o + k) * D + j], table_scalars_any(table, recip, st[k]));
       }
       dst[j] = w;
       dst[D + j] = m;
@@ -184,7 +187,8 @@ __global__ __launch_bounds__(256) void k_replay_wpr(float* __restrict__ out, con
                                                     const int64_t* __restrict__ offs,
                                                     const int32_t* __restrict__ steps,
                                                     const int32_t* __restrict__ cnt, int64_t n, uint32_t seed,
-                                                    float bound, const float* __restrict__ table, int64_t table_rows) {
+                                                    float bound, const float* __restrict__ table,
+                                                    const double* __restrict__ recip, int64_t table_rows) {
   constexpr int64_t D = 64 * VPL;
   const int lane = threadIdx.x & 63;
   const int64_t i0 = wave_id() * U;
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(256) void k_replay_wpr(float* __restrict__ out, con
     RowFrag<VPL> w = frag_init<VPL>(r[u], lane, seed, bound), m = frag_zero<VPL>(), v = frag_zero<VPL>();
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      if (k < c[u]) frag_adam<VPL>(w, m, v, g[u][k], table_scalars(table, st[u][k]));
+      if (k < c[u]) frag_adam<VPL>(w, m, v, g[u][k], table_scalars(table, recip, st[u][k]));
     float* dst = out + (i0 + u) * 3 * D + lane * VPL;
     frag_store<VPL>(dst, w);
     frag_store<VPL>(dst + D, m);
@@ -235,14 +239,15 @@ __global__ __launch_bounds__(256) void k_replay_wpr(float* __restrict__ out, con
 template <int VPL, int K>
 static void launch_replay_wpr(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                               const int32_t* steps, const int32_t* cnt, int64_t n, uint32_t seed, float bound,
-                              const float* table, int64_t table_rows, hipStream_t st) {
+                              const float* table, const double* recip, int64_t table_rows, hipStream_t st) {
   constexpr int U = ELR_REPLAY_U;
   constexpr int64_t D = 64 * VPL;
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
     k_replay_wpr<VPL, K, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(
-        out + a * 3 * D, rows + a, logs, nlogs, offs + a, steps + a * K, cnt + a, m, seed, bound, table, table_rows);
+        out + a * 3 * D, rows + a, logs, nlogs, offs + a, steps + a * K, cnt + a, m, seed, bound, table, recip,
+        table_rows);
   }
 }
 
@@ -261,11 +266,11 @@ static void launch_init_wpr(float* out, const int64_t* rows, int64_t n, uint32_t
 template <int K>
 static int launch_replay(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                          const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, uint32_t seed, float bound,
-                         const float* table, int64_t table_rows, hipStream_t st) {
+                         const float* table, const double* recip, int64_t table_rows, hipStream_t st) {
   const int vpl = wpr_vpl(D);
-  if (K <= 4 && vpl && aligned16(out) && aligned16(logs)) {
+  if (K <= 4 && vpl && recip && aligned16(out) && aligned16(logs)) {
 #define ELR_WPR_REPLAY(V) \
-  launch_replay_wpr<V, K>(out, rows, logs, nlogs, offs, steps, cnt, n, seed, bound, table, table_rows, st)
+  launch_replay_wpr<V, K>(out, rows, logs, nlogs, offs, steps, cnt, n, seed, bound, table, recip, table_rows, st)
     switch (vpl) {
       case 1: ELR_WPR_REPLAY(1); break;
       case 2: ELR_WPR_REPLAY(2); break;
@@ -280,11 +285,11 @@ static int launch_replay(float* out, const int64_t* rows, const float* logs, int
     const int lg = lanes_per_row_log2(nchunk);
     const int64_t rpw = 64 >> lg;
     k_replay_v4<K><<<grid_for((n + rpw - 1) / rpw, 4), 256, 0, st>>>(out, rows, logs, nlogs, offs, steps, cnt, n,
-                                                                     (int)nchunk, lg, seed, bound, table,
+                                                                     (int)nchunk, lg, seed, bound, table, recip,
                                                                      table_rows);
   } else {
     k_replay_scalar<K><<<grid_for(n, 4), 256, 0, st>>>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound,
-                                                       table, table_rows);
+                                                       table, recip, table_rows);
   }
   return launch_status();
 }
@@ -319,7 +324,8 @@ extern "C" int elr_init_rows(float* out, const int64_t* rows, int64_t n, int64_t
 
 extern "C" int elr_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                                const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed,
-                               float bound, const float* table, int64_t table_rows, void* stream) {
+                               float bound, const float* table, const double* recip, int64_t table_rows,
+                               void* stream) {
   if (n < 0 || D <= 0 || nlogs < 0 || table_rows < 0) return ELR_EINVAL;
   if (K < 1 || K > 8) return ELR_EUNSUPPORTED;
   if (n == 0) return ELR_OK;
@@ -328,7 +334,8 @@ extern "C" int elr_replay_rows(float* out, const int64_t* rows, const float* log
   switch (K) {
 #define ELR_REPLAY_CASE(KK) \
   case KK:                  \
-    return elr::launch_replay<KK>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound, table, table_rows, st);
+    return elr::launch_replay<KK>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound, table, recip, \
+                                  table_rows, st);
     ELR_REPLAY_CASE(1)
     ELR_REPLAY_CASE(2)
     ELR_REPLAY_CASE(3)

@@ -1,0 +1,52 @@
+// Exhaustive check of this library's fp32 division by a step-constant divisor.
+//
+// The Adam kernels compute the correctly rounded quotient a / b for the two per-step divisors b = 1 - b1^t and
+// b = 1 - b2^t as RN_f32((double)a * y) with y = RN_f64(1 / b).  Why that is exact for every finite a: the double
+// product is within 2^-51 |a/b| of a/b, while a quotient of two floats lies at least 2^-49 |a/b| away from every
+// midpoint between consecutive floats (normal and subnormal results alike), so rounding the product to float
+// gives the float nearest to a/b.  This kernel confirms it on the GPU for one divisor over all 2^32 bit patterns
+// of a, against the compiler's correctly rounded fp32 division (NaN results compare equal when both are NaN).
+#include "elr_common.h"
+
+namespace elr {
+
+constexpr int kCheckThreads = 256;
+constexpr int kCheckPerThread = 16;
+
+__global__ __launch_bounds__(kCheckThreads) void k_check_div(float b, double y, uint64_t base,
+                                                             unsigned long long* __restrict__ bad,
+                                                             unsigned int* __restrict__ first_bad) {
+  const uint64_t t0 = base + ((uint64_t)blockIdx.x * kCheckThreads + threadIdx.x) * kCheckPerThread;
+  int nbad = 0;
+  uint32_t firstv = 0xFFFFFFFFu;
+  for (int k = 0; k < kCheckPerThread; ++k) {
+    const uint64_t ab = t0 + k;
+    if (ab > 0xFFFFFFFFull) break;
+    const float a = __uint_as_float((uint32_t)ab);
+    const float want = a / b;
+    const float got = div_by_recip(a, y);
+    const bool same = __float_as_uint(want) == __float_as_uint(got) || (want != want && got != got);
+    if (!same) {
+      ++nbad;
+      if ((uint32_t)ab < firstv) firstv = (uint32_t)ab;
+    }
+  }
+  if (nbad) {
+    atomicAdd(bad, (unsigned long long)nbad);
+    atomicMin(first_bad, firstv);
+  }
+}
+
+}  // namespace elr
+
+extern "C" int elr_selfcheck_div(float b, unsigned long long* mismatches, unsigned int* first_bad, void* stream) {
+  using namespace elr;
+  if (!mismatches || !first_bad) return ELR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const double y = 1.0 / (double)b;
+  const uint64_t per_block = (uint64_t)kCheckThreads * kCheckPerThread;
+  const uint64_t blocks_per_launch = 1ull << 18;
+  for (uint64_t base = 0; base < (1ull << 32); base += blocks_per_launch * per_block)
+    k_check_div<<<(unsigned)blocks_per_launch, kCheckThreads, 0, st>>>(b, y, base, mismatches, first_bad);
+  return launch_status();
+}

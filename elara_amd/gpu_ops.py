@@ -35,14 +35,22 @@ def init_rows(rows, D, seed, bound, out=None):
     return out
 
 
+def _recip_host(t_host):
+    r = torch.empty(t_host.shape[0], 2, dtype=torch.float64)
+    _lib.check(_lib.lib().elr_scalar_recip(_lib.ptr(t_host), t_host.shape[0], _lib.ptr(r)), 'elr_scalar_recip')
+    return r
+
+
 class ScalarTable:
-    """Per-logical-step Adam scalars [max_step+1, 8] fp32 in HBM; row 0 is zeros, row t = adam_scalars(t)."""
+    """Per-logical-step Adam scalars [max_step+1, 8] fp32 in HBM; row 0 is zeros, row t = adam_scalars(t).
+    Also holds r [max_step+1, 2] fp64 = (1/bc1, 1/bc2) per row, correctly rounded, for the replay kernel."""
 
     def __init__(self, lr, b1, b2, eps, max_step, device):
         host = torch.empty(int(max_step) + 1, 8, dtype=torch.float32)
         _lib.check(_lib.lib().elr_scalar_table(float(lr), float(b1), float(b2), float(eps), int(max_step),
                                                _lib.ptr(host)), 'elr_scalar_table')
         self.t = host.to(device)
+        self.r = _recip_host(host).to(device)
 
 
 def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None):
@@ -53,6 +61,7 @@ def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None
         out = torch.empty(n, 3, D, device=rows.device)
     if n:
         t = table if isinstance(table, torch.Tensor) else table.t
+        r = None if isinstance(table, torch.Tensor) else getattr(table, 'r', None)
         dev = rows.device
         if not (out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and out.numel() >= n * 3 * D):
             raise RuntimeError(f'out must be a contiguous cuda float32 tensor with at least {n}x3x{D} elements')
@@ -68,10 +77,12 @@ def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None
         steps = steps.to(torch.int32).contiguous()
         cnt = cnt.to(torch.int32).contiguous()
         t = t.contiguous()
+        if r is None or r.shape != (t.shape[0], 2) or r.device != t.device:
+            r = _recip_host(t.cpu().contiguous()).to(dev)   # a bare [S, 8] table: reciprocals computed here
         with torch.cuda.device(dev):
             rc = _lib.lib().elr_replay_rows(_lib.ptr(out), _lib.ptr(rows), _lib.ptr(logs), logs.numel() // D,
                                             _lib.ptr(offs), _lib.ptr(steps), _lib.ptr(cnt), n, int(D), int(K),
-                                            _seed32(seed), float(bound), _lib.ptr(t), t.shape[0],
+                                            _seed32(seed), float(bound), _lib.ptr(t), _lib.ptr(r), t.shape[0],
                                             _lib.stream_of(rows))
         _lib.check(rc, 'elr_replay_rows')
     return out

@@ -132,7 +132,7 @@ class ElaraStep:
         self.mat = torch.empty(self.mat_cap, 3, D, device=d)
         self.logs = torch.empty(self.log_cap + 1, D, device=d)
         self._c8 = [torch.tensor(v, dtype=I8, device=d) for v in range(10)]
-        self.stats = {k: 0 for k in ('adm', 'ev', 'ev_to_logs', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
+        self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs')}
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
@@ -176,12 +176,14 @@ class ElaraStep:
                 j = torch.searchsorted(un, u).clamp(max=un.numel() - 1)
                 in_next |= un[j] == u
         admit = ~hit & (self.last_seen[u] > s)
-        protect = self.pinned.clone()
+        # slots of rows needed by the next batches (srm2/elara.py:227-229); rows without a slot mark a trash element
+        # (a plain store, where counting them into slot 0 would serialise on one address)
+        prot = torch.zeros(C + 1, dtype=torch.bool, device=d)
+        prot[:C] = self.pinned
         for un in u_nexts:
             sn = self.slot_of[un].long()
-            m = torch.zeros(C, dtype=I32, device=d)
-            m.scatter_add_(0, sn.clamp(min=0), (sn >= 0).to(I32))
-            protect |= m > 0
+            prot[torch.where(sn >= 0, sn, torch.full_like(sn, C))] = True
+        protect = prot[:C]
         dl = self.dyn_slots
         exp = ~protect[dl] & (self.last_seen[self.slot_row[dl]] <= s)
         c = self.code[u]

@@ -111,3 +111,16 @@ class C5Tables:
         u, c = np.unique(ids, return_counts=True)
         top = np.lexsort((u, -c))[:n_static]
         return np.sort(u[top]).astype(np.int64)
+
+
+def unique_zipf(rng, fields, n_unique, draw=1 << 20):
+    """Config C4: draw ids from `fields` (one ZipfFields field) until n_unique distinct ids are collected; returns
+    them in first-appearance order (int64 [n_unique])."""
+    seen = np.empty(0, np.int64)
+    while seen.size < n_unique:
+        ids = fields.draw(rng, draw)
+        allv = np.concatenate([seen, ids])
+        _, first = np.unique(allv, return_index=True)
+        first.sort()
+        seen = allv[first]
+    return seen[:n_unique]

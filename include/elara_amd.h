@@ -50,6 +50,11 @@ void elr_adam_scalars(double lr, double b1, double b2, double eps, int64_t step,
  * Replaces: srm2/gpu_ops.py:82-88 ScalarTable (host part; the caller copies it to HBM). */
 int elr_scalar_table(double lr, double b1, double b2, double eps, int64_t max_step, float* table_host);
 
+/* Fill a host array [table_rows, 2] with RN_f64(1 / bc1), RN_f64(1 / bc2) of each table row (columns 5 and 6;
+ * row 0's zeros give inf).  elr_replay_rows uses them for its divisions by the bias corrections (no counterpart in
+ * the reference: the reciprocals only make those correctly rounded divisions cheaper). */
+int elr_scalar_recip(const float* table_host, int64_t table_rows, double* recip_host);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Row-sparse Adam, in place.
  * Replaces: srm2/ops.py:42-67 gpu_adam / _adam_rows.  For i < n: Adam(state[slots[i]], grad[i]) with the
@@ -73,11 +78,12 @@ int elr_init_rows(float* out, const int64_t* rows, int64_t n, int64_t D, uint32_
  * Replaces: srm2/gpu_ops.py:91-99 replay_rows / _replay (gpu_ops.py:51-79).  out[i] = init(rows[i]) followed by
  * Adam with gradient logs[offs[i] + k] and scalars table[steps[i*K + k]] for k < cnt[i].  1 <= K <= 8.
  *   out device fp32 [n,3,D]; rows int64 [n]; logs fp32 [nlogs,D]; offs int64 [n]; steps int32 [n,K];
- *   cnt int32 [n]; table fp32 [table_rows, 8].  All device pointers.
+ *   cnt int32 [n]; table fp32 [table_rows, 8]; recip fp64 [table_rows, 2] from elr_scalar_recip (copied to the
+ *   device), or NULL (then the kernel computes the reciprocals itself, at some cost).  All device pointers.
  * ------------------------------------------------------------------------------------------------------- */
 int elr_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                     const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed, float bound,
-                    const float* table, int64_t table_rows, void* stream);
+                    const float* table, const double* recip, int64_t table_rows, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * State directory.
@@ -171,6 +177,15 @@ int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* gra
  * ------------------------------------------------------------------------------------------------------- */
 int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
                   const int64_t* src_idx, int64_t n, int64_t W, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Exhaustive check of the step-constant division (no counterpart in the reference).  The Adam kernels compute
+ * a / b for b = 1 - b1^t and b = 1 - b2^t as RN_f32((double)a * RN_f64(1/b)); for all 2^32 float bit patterns a
+ * this compares that with the correctly rounded fp32 quotient a / b, adds the number of mismatches to
+ * *mismatches (device uint64, caller zeroes it) and the lowest mismatching pattern to *first_bad (device uint32
+ * atomic min; caller sets it to 0xFFFFFFFF).  Asynchronous; a few milliseconds.
+ * ------------------------------------------------------------------------------------------------------- */
+int elr_selfcheck_div(float b, unsigned long long* mismatches, unsigned int* first_bad, void* stream);
 
 #ifdef __cplusplus
 }

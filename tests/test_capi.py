@@ -49,6 +49,17 @@ def test_scalars_and_table_match_oracle():
         assert np.array_equal(tab.view(np.uint32), O.scalar_table(*hp, 200).view(np.uint32))
 
 
+def test_scalar_recip_is_the_correctly_rounded_double_reciprocal():
+    tab = O.scalar_table(1e-3, 0.9, 0.999, 1e-8, 3000)
+    r = np.empty((tab.shape[0], 2), np.float64)
+    assert _lib.lib().elr_scalar_recip(tab.ctypes.data_as(ctypes.c_void_p), tab.shape[0],
+                                       r.ctypes.data_as(ctypes.c_void_p)) == 0
+    with np.errstate(divide='ignore'):
+        want = 1.0 / tab[:, 5:7].astype(np.float64)
+    assert np.array_equal(r, want)
+    assert np.isinf(r[0]).all()
+
+
 def test_host_argument_checks_return_codes():
     L = _lib.lib()
     s = _lib.scalars8([0.0] * 8)
@@ -56,8 +67,8 @@ def test_host_argument_checks_return_codes():
     assert L.elr_adam_rows(None, 0, None, 0, None, 0, 4, s, None) == 0          # n == 0: no-op
     assert L.elr_adam_rows(None, 0, None, 0, None, 5, 4, s, None) == -1         # null pointers
     assert L.elr_init_rows(None, None, 3, 0, 0, 1.0, None) == -1
-    assert L.elr_replay_rows(None, None, None, 0, None, None, None, 1, 4, 9, 0, 1.0, None, 0, None) == -2
-    assert L.elr_replay_rows(None, None, None, 0, None, None, None, 0, 4, 3, 0, 1.0, None, 0, None) == 0
+    assert L.elr_replay_rows(None, None, None, 0, None, None, None, 1, 4, 9, 0, 1.0, None, None, 0, None) == -2
+    assert L.elr_replay_rows(None, None, None, 0, None, None, None, 0, 4, 3, 0, 1.0, None, None, 0, None) == 0
 
 
 def test_ops_raise_without_gpu_tensors():

@@ -221,3 +221,41 @@ def test_replay_edge_cases(dev):
                     torch.zeros(10, 9, dtype=torch.int32, device=dev), torch.zeros(10, dtype=torch.int32, device=dev),
                     64, 9, 5, 0.1, table)
     assert adam_scalars(*HP, 3) == O.adam_scalars(*HP, 3).tolist()
+
+
+def test_replay_without_reciprocal_table(dev):
+    """elr_replay_rows with recip = NULL (a C caller without elr_scalar_recip): the kernels compute the
+    reciprocals themselves; results are the same bits."""
+    from elara_amd import _lib
+    w = synth.ReplayLog(n=3000, D=128, K=3, seed=3, rows=np.arange(3000, dtype=np.int64) * 977 + 2**33)
+    table = ScalarTable(*HP, w.max_step + 1, dev)
+    d = {k: torch.from_numpy(np.ascontiguousarray(getattr(w, k))).to(dev) for k in ('rows', 'logs', 'offs', 'steps',
+                                                                                      'cnt')}
+    out = torch.empty(w.n, 3, 128, device=dev)
+    rc = _lib.lib().elr_replay_rows(_lib.ptr(out), _lib.ptr(d['rows']), _lib.ptr(d['logs']), d['logs'].shape[0],
+                                    _lib.ptr(d['offs']), _lib.ptr(d['steps']), _lib.ptr(d['cnt']), w.n, 128, 3, 11,
+                                    0.05, _lib.ptr(table.t), None, table.t.shape[0], _lib.stream_of(out))
+    _lib.check(rc, 'elr_replay_rows')
+    torch.cuda.synchronize()
+    ref = O.replay_rows(w.rows, w.logs, w.offs, w.steps, w.cnt, 128, 3, 11, 0.05, table.t.cpu().numpy())
+    assert same(out, ref)
+
+
+@pytest.mark.parametrize('D', [128, 64])
+def test_replay_extreme_gradients(dev, D):
+    """Logged gradients whose squares underflow into fp32 subnormals, zeros (incl. -0), and huge values: the
+    replayed state is bitwise the oracle's."""
+    rng = np.random.default_rng(21)
+    n, K = 900, 3
+    mags = np.array([0.0, 1e-38, 1e-30, 1e-23, 3e-19, 1e-10, 1.0, 1e10, 1e18], np.float64)
+    cnt = np.full(n, K, np.int32)
+    steps = np.tile(np.array([1, 2, 7], np.int32), (n, 1))
+    logs = (rng.standard_normal((n * K, D)) * np.repeat(mags, n * K // mags.size)[:, None]).astype(np.float32)
+    logs[::17] = -0.0
+    rows = rng.integers(0, 2**40, n).astype(np.int64)
+    offs = (np.arange(n) * K).astype(np.int64)
+    table = ScalarTable(*HP, 10, dev)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    out = replay_rows(t(rows), t(logs), t(offs), t(steps), t(cnt), D, K, 5, 0.03, table)
+    torch.cuda.synchronize()
+    assert same(out, O.replay_rows(rows, logs, offs, steps, cnt, D, K, 5, 0.03, table.t.cpu().numpy()))
