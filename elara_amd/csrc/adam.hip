@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void k_adam_rows_scalar(float* __restrict__ st
 // issue all their w, m, v, g loads before the first update.  No loop (see init_replay.hip): one row group per
 // wave, large calls split into several launches on the host.
 #ifndef ELR_ADAM_U
-#define ELR_ADAM_U 2
+#define ELR_ADAM_U 1
 #endif
 
 template <int VPL, typename Idx, int U>

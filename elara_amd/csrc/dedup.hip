@@ -149,13 +149,14 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_count(const Key* __restrict__
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
 
-// Segment heads: unique ids, segment starts (seg_start[U] = n) and the inverse.
+// Segment heads: unique ids, segment starts (seg_start[U] = n), each segment's first occurrence index and the
+// inverse.
 template <typename Key>
 __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__ sk, const int32_t* __restrict__ sv,
                                                          int64_t n, const int64_t* __restrict__ boff,
                                                          const int64_t* __restrict__ d_U,
                                                          int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
-                                                         int64_t* __restrict__ inverse) {
+                                                         int32_t* __restrict__ seg_occ0, int64_t* __restrict__ inverse) {
   const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
   int v[1] = {0}, ex[1], tot[1];
   for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + r, n);
@@ -169,6 +170,7 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__
     if (f) {
       uniq[u] = (int64_t)sk[i];
       seg_start[u] = i;
+      seg_occ0[u] = sv[i];
     }
     if (inverse) {
       const int32_t o = sv[i];
@@ -330,15 +332,20 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
 }
 
 // Wave-per-row form of k_seg_final for D = 64*VPL (lane l holds floats [l*VPL, l*VPL + VPL)): no loop, each
-// wave owns kSegPerWave consecutive segments starting at u_base + wave * kSegPerWave; waves past U exit.  The
-// segment bounds, the row id and (MODE 1) its w, m, v are loaded before the gradients, the first chunk's
-// occurrence indices with one vector load, then every gradient row of the chunk; the Adam update follows.
-constexpr int kSegPerWave = 2;
+// wave owns kSegPerWave consecutive segments starting at u_base + wave * kSegPerWave; waves past U exit.  All
+// per-segment metadata (bounds, row id, first occurrence) are scalar loads issued together, then the first
+// gradient row, the row's w, m, v (MODE 1) and the chunk's remaining occurrence indices load in parallel: a
+// one-occurrence segment -- the common case -- costs two dependent memory round trips.
+#ifndef ELR_SEG_SW
+#define ELR_SEG_SW 2
+#endif
+constexpr int kSegPerWave = ELR_SEG_SW;
 
 template <int VPL, int MODE>
 __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__ grad,
                                                        const int32_t* __restrict__ sv,
                                                        const int64_t* __restrict__ seg_start,
+                                                       const int32_t* __restrict__ seg_occ0,
                                                        const int64_t* __restrict__ uniq,
                                                        const int32_t* __restrict__ chunk_off,
                                                        const float* __restrict__ parts,
@@ -350,9 +357,8 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
   const int64_t U = *d_U;
   const int64_t u0 = u_base + wave_id() * SW;
   if (u0 >= U) return;
-  int64_t s0[SW], len[SW], row[SW];
+  int64_t s0[SW], len[SW], row[SW], o0[SW];
   bool ok[SW];
-  RowFrag<VPL> w[SW], m[SW], v[SW];
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
     const int64_t u = u0 + q;
@@ -360,27 +366,30 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
     s0[q] = ok[q] ? seg_start[u] : 0;
     len[q] = ok[q] ? seg_start[u + 1] - s0[q] : 0;
     row[q] = ok[q] ? uniq[u] : -1;
+    o0[q] = ok[q] ? (int64_t)seg_occ0[u] : 0;
     ok[q] = ok[q] && row[q] >= 0 && row[q] < nrows;
-    if (MODE == 1 && ok[q]) {
+  }
+  RowFrag<VPL> w[SW], m[SW], v[SW], acc[SW];
+  int32_t my[SW];
+#pragma unroll
+  for (int q = 0; q < SW; ++q) {
+    if (!ok[q]) continue;
+    acc[q] = frag_load<VPL, true>(grad + o0[q] * D + lane * VPL);
+    if (MODE == 1) {
       const float* rec = out + row[q] * 3 * D + lane * VPL;
       w[q] = frag_load<VPL, false>(rec);
       m[q] = frag_load<VPL, false>(rec + D);
       v[q] = frag_load<VPL, false>(rec + 2 * D);
     }
-  }
-  int32_t my[SW];
-#pragma unroll
-  for (int q = 0; q < SW; ++q) {
     const int64_t l0 = len[q] < kSegChunk ? len[q] : kSegChunk;
-    my[q] = (ok[q] && lane < l0) ? sv[s0[q] + lane] : 0;
+    my[q] = (lane >= 1 && lane < l0) ? sv[s0[q] + lane] : 0;
   }
-  RowFrag<VPL> acc[SW];
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
     if (!ok[q]) continue;
     const int l0 = (int)(len[q] < kSegChunk ? len[q] : kSegChunk);
     constexpr int UN = 8;
-    for (int k0 = 0; k0 < l0; k0 += UN) {
+    for (int k0 = 1; k0 < l0; k0 += UN) {
       RowFrag<VPL> g[UN];
 #pragma unroll
       for (int e = 0; e < UN; ++e)
@@ -392,7 +401,7 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
       for (int e = 0; e < UN; ++e)
         if (k0 + e < l0) {
 #pragma unroll
-          for (int j = 0; j < VPL; ++j) acc[q].v[j] = (k0 + e == 0) ? g[e].v[j] : acc[q].v[j] + g[e].v[j];
+          for (int j = 0; j < VPL; ++j) acc[q].v[j] = acc[q].v[j] + g[e].v[j];
         }
     }
     const int64_t extra = (len[q] - 1) / kSegChunk;
@@ -434,6 +443,7 @@ struct DedupScratch {
   int64_t* d_tot;     // [2]: U, E
   int64_t* uniq;      // [n]
   int64_t* seg_start; // [n + 1]
+  int32_t* seg_occ0;  // [n] first occurrence index of each segment
   int32_t* chunk_off; // [n]
   int32_t* chunk_seg; // [n / 64 + 1]
   float* parts;       // [(n / 64 + 1) * D]
@@ -459,6 +469,7 @@ inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void
   s.d_tot = (int64_t*)take(2 * 8);
   s.uniq = (int64_t*)take(n * 8);
   s.seg_start = (int64_t*)take((n + 1) * 8);
+  s.seg_occ0 = (int32_t*)take(n * 4);
   s.chunk_off = (int32_t*)take(n * 4);
   s.chunk_seg = (int32_t*)take(nch * 4);
   s.parts = (float*)take(nch * D * 4);
@@ -503,7 +514,8 @@ static int dedup_core(const int64_t* ids, int64_t n, int key_bits, DedupScratch&
   int64_t* uniq = uniq_out ? uniq_out : S.uniq;
   k_seg_count<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
   k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot);
-  k_seg_apply<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start, inverse);
+  k_seg_apply<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start, S.seg_occ0,
+                                                         inverse);
   return cur;
 }
 
@@ -543,7 +555,7 @@ static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
     k_seg_final_wpr<VPL, MODE><<<(unsigned)cdiv(m, 4 * kSegPerWave), 256, 0, st>>>(
-        grad, sv, S.seg_start, uniq, S.chunk_off, S.parts, S.d_tot, a, out, nrows, s);
+        grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a, out, nrows, s);
   }
 }
 

@@ -39,9 +39,30 @@ inline AdamScalars make_scalars(const float sc[8]) {
 // over all 2^32 values of a by elr_selfcheck_div.
 __device__ __forceinline__ float div_by_recip(float a, double y) { return (float)((double)a * y); }
 
+// Correctly rounded fp32 square root.  The compiler's IEEE sequence wraps a core -- the hardware estimate s and a
+// choice among s - 1 ulp, s, s + 1 ulp by the signs of the residuals x - s'*s -- in a rescaling of small inputs and
+// a special-case selection for 0, inf and NaN.  For a normal x >= 2^-96 neither wrapper changes anything, so when
+// every lane of the wave has such an x (a wave-uniform branch) the core alone is used; otherwise the full
+// sequence.  Checked over all 2^32 inputs by elr_selfcheck_sqrt.
+__device__ __forceinline__ float sqrt_core(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float sm = __uint_as_float(__float_as_uint(s) - 1u);
+  const float sp = __uint_as_float(__float_as_uint(s) + 1u);
+  const float rm = __builtin_fmaf(-sm, s, x);
+  const float rp = __builtin_fmaf(-sp, s, x);
+  const float r = rm <= 0.0f ? sm : s;
+  return rp > 0.0f ? sp : r;
+}
+
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const bool core_ok = __builtin_isnormal(x) && x >= 0x1.0p-96f;
+  if (__all(core_ok)) return sqrt_core(x);
+  return __builtin_sqrtf(x);
+}
+
 // One Adam update of one element, in the reference's operation order (srm2/csrc/srm2_cpu.cpp:26-32).  Each
 // statement is one correctly rounded fp32 operation; the two divisions by the step's bias corrections use
-// div_by_recip, the division by den is the general correctly rounded one.
+// div_by_recip, the square root sqrt_rn, the division by den the general correctly rounded one.
 __device__ __forceinline__ void adam_elem(float& w, float& m, float& v, float g, const AdamScalars& s) {
   float mj = s.b1 * m;
   float t1 = s.omb1 * g;
@@ -52,7 +73,7 @@ __device__ __forceinline__ void adam_elem(float& w, float& m, float& v, float g,
   vj = vj + t2;
   float mh = div_by_recip(mj, s.r1);
   float vh = div_by_recip(vj, s.r2);
-  float den = __builtin_sqrtf(vh);
+  float den = sqrt_rn(vh);
   den = den + s.eps;
   float num = s.lr * mh;
   float up = num / den;

@@ -1,4 +1,5 @@
-// Exhaustive check of this library's fp32 division by a step-constant divisor.
+// Exhaustive checks of this library's fp32 arithmetic shortcuts: the division by a step-constant divisor and the
+// square root (sqrt_rn).
 //
 // The Adam kernels compute the correctly rounded quotient a / b for the two per-step divisors b = 1 - b1^t and
 // b = 1 - b2^t as RN_f32((double)a * y) with y = RN_f64(1 / b).  Why that is exact for every finite a: the double
@@ -37,7 +38,40 @@ __global__ __launch_bounds__(kCheckThreads) void k_check_div(float b, double y, 
   }
 }
 
+// sqrt_rn against the compiler's correctly rounded fp32 square root, for all 2^32 bit patterns x (consecutive
+// patterns share a wave, so waves with special or small values take sqrt_rn's full path and the others its core).
+__global__ __launch_bounds__(kCheckThreads) void k_check_sqrt(uint64_t base, unsigned long long* __restrict__ bad,
+                                                              unsigned int* __restrict__ first_bad) {
+  const uint64_t t0 = base + ((uint64_t)blockIdx.x * kCheckThreads + threadIdx.x);
+  int nbad = 0;
+  uint32_t firstv = 0xFFFFFFFFu;
+  const uint64_t stride = (uint64_t)gridDim.x * kCheckThreads;
+  for (uint64_t xb = t0; xb <= 0xFFFFFFFFull; xb += stride) {
+    const float x = __uint_as_float((uint32_t)xb);
+    const float want = __builtin_sqrtf(x);
+    const float got = sqrt_rn(x);
+    const bool same = __float_as_uint(want) == __float_as_uint(got) || (want != want && got != got);
+    if (!same) {
+      ++nbad;
+      if ((uint32_t)xb < firstv) firstv = (uint32_t)xb;
+    }
+  }
+  if (nbad) {
+    atomicAdd(bad, (unsigned long long)nbad);
+    atomicMin(first_bad, firstv);
+  }
+}
+
 }  // namespace elr
+
+extern "C" int elr_selfcheck_sqrt(unsigned long long* mismatches, unsigned int* first_bad, void* stream) {
+  using namespace elr;
+  if (!mismatches || !first_bad) return ELR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint64_t blocks = 1ull << 18;                               // 2^26 threads, 64 patterns each
+  k_check_sqrt<<<(unsigned)blocks, kCheckThreads, 0, st>>>(0, mismatches, first_bad);
+  return launch_status();
+}
 
 extern "C" int elr_selfcheck_div(float b, unsigned long long* mismatches, unsigned int* first_bad, void* stream) {
   using namespace elr;

@@ -187,6 +187,10 @@ int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const fl
  * ------------------------------------------------------------------------------------------------------- */
 int elr_selfcheck_div(float b, unsigned long long* mismatches, unsigned int* first_bad, void* stream);
 
+/* The same for the square root (no counterpart in the reference): the Adam kernels' fp32 square root against the
+ * correctly rounded one, for all 2^32 bit patterns x. */
+int elr_selfcheck_sqrt(unsigned long long* mismatches, unsigned int* first_bad, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,4 +1,4 @@
-"""Exhaustive GPU check of the division by a step-constant divisor (elr_selfcheck_div): for each divisor b of the
+"""Exhaustive GPU checks of the arithmetic shortcuts.  elr_selfcheck_div: for each divisor b of the
 scalar table (1 - b1^t, 1 - b2^t) and a few others, RN_f32((double)a * RN_f64(1/b)) equals the correctly rounded
 fp32 quotient a / b for all 2^32 bit patterns of a."""
 import numpy as np
@@ -34,3 +34,13 @@ def test_gpu_division_by_reciprocal_is_exact_for_all_floats(dev):
     torch.cuda.synchronize()
     fails = [(b, int(n), int(f) & 0xFFFFFFFF) for b, n, f in zip(ds, bad.tolist(), first.tolist()) if n]
     assert not fails, fails
+
+
+def test_gpu_sqrt_is_correctly_rounded_for_all_floats(dev):
+    from elara_amd import _lib
+    print('[gpu-test] selfcheck sqrt: 2^32 inputs', flush=True)
+    bad = torch.zeros(1, dtype=torch.int64, device=dev)
+    first = torch.full((1,), -1, dtype=torch.int32, device=dev)
+    _lib.check(_lib.lib().elr_selfcheck_sqrt(_lib.ptr(bad), _lib.ptr(first), _lib.stream_of(bad)), 'elr_selfcheck_sqrt')
+    torch.cuda.synchronize()
+    assert int(bad) == 0, f'{int(bad)} mismatches, first at 0x{int(first) & 0xFFFFFFFF:08x}'
