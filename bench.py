@@ -308,17 +308,21 @@ def mode_c5(args):
 
 
 def copy_calibration(args):
-    """A plain device copy of known size (PMC calibration of FETCH_SIZE / WRITE_SIZE)."""
+    """A plain device copy of known size: the PMC calibration of FETCH_SIZE / WRITE_SIZE, and the copy bandwidth
+    (read + write bytes over the mean launch time, HIP events) as the practical ceiling of a streaming kernel."""
     import torch
     dev = torch.device('cuda:0')
     nbytes = 1 << 30
     a = torch.ones(nbytes // 4, device=dev)
     b = torch.empty_like(a)
-    for _ in range(args.steps):
+    for _ in range(3):
         b.copy_(a)
-    torch.cuda.synchronize()
+    el, ms = _timed_steps(lambda i: b.copy_(a), args.steps, 0)
+    mean_ms = float(np.mean(ms))
     return {'mode': 'copy', 'bytes_read_per_launch': nbytes, 'bytes_written_per_launch': nbytes,
-            'launches': args.steps}
+            'launches': args.steps + 3, 'mean_launch_ms': mean_ms,
+            'copy_GBps': 2 * nbytes / (mean_ms * 1e-3) / 1e9,
+            'copy_frac_of_hbm_peak': 2 * nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
 def main():

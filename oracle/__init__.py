@@ -22,11 +22,15 @@ How each function is pinned (checked against something other than itself; tests 
                      seeds >= 2^31, D not a power of two); range [-bound, bound), w0(0,0,seed 0) = -bound
   orc_replay_rows    == Triton golden vectors of srm2/gpu_ops.py _replay; == init + eager reference cpu_adam
                      (oracle/_ref) at the logged steps (test_replay.py:22-33 as an assertion)
-  orc_segment_sum    this build defines the order (ascending id, ascending occurrence); checked against
-                     brute force per id in numpy float32 and torch.unique ordering.  The reference's own
-                     duplicate-gradient sum order belongs to ATen (embedding_dense_backward) and is pinned by no
-                     reference test: parity with the reference is UNPINNED for that order.
+  orc_segment_sum    this build defines the order (per id: ascending occurrence index in chunks of 64, each chunk
+                     left to right, then the chunk sums left to right); pinned by properties a wrong order fails
+                     (<= 64 occurrences == plain left-to-right sum, an observable 200-occurrence case, independence
+                     from the interleaving of other ids, torch.unique ordering, column totals)
+                     [tests/test_dedup.py].  The reference's own duplicate-gradient sum order belongs to ATen
+                     (embedding_dense_backward) and is pinned by no reference test: parity with the reference is
+                     UNPINNED for that order.
   orc_dir_a/b        == reference elara_dir_a/elara_dir_b from oracle/_ref run on CPU tensors, whole directory
-                     state and every output compared, over random multi-step sequences; invariants of
-                     srm2/train.py:474-477 (live == #valid entries, live + n_lfree == log_top)
+                     state and every output compared, over 60-step planner simulations in 5 configurations
+                     (tests/dirsim.py); a hand-worked allocation sequence; invariants of srm2/train.py:474-477
+                     (live == #valid entries, live + n_lfree == log_top)  [tests/test_directory.py]
 """
