@@ -1,9 +1,10 @@
-"""The hot-path kernels of elara_amd.step.ElaraStep implemented by the CPU oracle (test helper): the same step,
-on CPU tensors, with every kernel replaced by its oracle restatement (oracle/elara_oracle.c)."""
+"""The hot-path kernels of elara_amd.step.ElaraStep implemented by the CPU oracle -- TEST INFRASTRUCTURE ONLY (used
+by tests/ and __graft_entry__.smoke()): the same step, on CPU tensors, with every kernel replaced by its oracle
+restatement (oracle/elara_oracle.c)."""
 import numpy as np
 import torch
 
-from oracle import oracle as O
+from . import oracle as O
 
 DT = dict(code=np.int8, loc=np.int32, ent=np.int32, lstep=np.int32, lfree=np.int32)
 

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from elara_amd import synth
-from oracle_backend import OracleBackend
+from oracle.backend import OracleBackend
 
 HP = synth.ADAM
 
