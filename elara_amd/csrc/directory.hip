@@ -129,9 +129,13 @@ __device__ __forceinline__ EvCounts ev_counts(const elr_dir_state& st, const elr
   return c;
 }
 
-// A2: eviction representation and per-block allocation counts (elara_dir.cpp:73-78).
+// A2: eviction representation and per-block allocation counts (elara_dir.cpp:73-78).  With ev_row_in (the
+// Directory.evict form, srm2/elara_kernels.py:152-171) the caller supplies the evicted rows and their thresholds
+// and has already cleared slot_of / slot_row; otherwise the rows come from slot_row and are unmapped here.
 __global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st, elr_dir_params p,
                                                                const int64_t* __restrict__ ev_slot, int64_t nev,
+                                                               const int64_t* __restrict__ ev_row_in,
+                                                               const int8_t* __restrict__ thr_in,
                                                                int64_t* __restrict__ ev_row, uint8_t* __restrict__ rep,
                                                                int64_t* __restrict__ ev_dyn,
                                                                int64_t* __restrict__ bsum, int64_t nblk) {
@@ -143,15 +147,19 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st,
     int64_t row = -1, c0 = -1, j = 0;
     bool rp = false;
     if (in_range(sl, C)) {
-      row = st.slot_row[sl];
+      row = ev_row_in ? ev_row_in[i] : st.slot_row[sl];
       c0 = st.adm_c0[sl];
       j = st.rj[sl];
-      if (p.evl && in_range(row, p.R))
-        rp = st.rok[sl] != 0 && (c0 + j) <= (int64_t)st.kthr[table_of(st.toff, st.T, row)];
-      if (in_range(row, p.R)) st.slot_of[row] = -1;
-      st.slot_row[sl] = -1;
+      if (p.evl && in_range(row, p.R)) {
+        const int64_t th = thr_in ? (int64_t)thr_in[i] : (int64_t)st.kthr[table_of(st.toff, st.T, row)];
+        rp = st.rok[sl] != 0 && (c0 + j) <= th;
+      }
+      if (!ev_row_in) {
+        if (in_range(row, p.R)) st.slot_of[row] = -1;
+        st.slot_row[sl] = -1;
+      }
     }
-    ev_row[i] = row;
+    if (!ev_row_in) ev_row[i] = row;
     rep[i] = rp ? 1 : 0;
     ev_dyn[i] = sl - p.n0;
     const EvCounts c = ev_counts(st, p, row, rp, c0, j);
@@ -378,6 +386,29 @@ inline bool params_ok(const elr_dir_state* st, const elr_dir_params* p) {
 
 }  // namespace elr
 
+namespace elr {
+
+// The eviction part of call A (A2..A5) over nev slots; rows come from ev_row_in when given (then ev_row_out is
+// not written and may be NULL).
+static void launch_evict(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
+                         const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
+                         int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, void* scratch, hipStream_t strm) {
+  char* base = (char*)scratch;
+  DirHdr* hdr = (DirHdr*)base;
+  const int64_t nblk = nblocks(nev);
+  int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
+  int64_t* rel_rank = (int64_t*)(base + align8(sizeof(DirHdr)) + align8(3 * nblk * 8));
+  const int64_t* rows = ev_row_in ? ev_row_in : ev_row_out;
+  k_dir_evict_count<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep,
+                                                            ev_dyn, bsum, nblk);
+  k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 0, 0, bsum, nblk, 3, hdr);
+  k_dir_evict_apply<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, rows, rep, ev_dyn, evl_ids,
+                                                            evf_slots, bsum, nblk, hdr, rel_rank);
+  k_dir_evict_release<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, rows, rep, rel_rank, hdr);
+}
+
+}  // namespace elr
+
 extern "C" int64_t elr_dir_scratch_bytes(int64_t nev, int64_t nc) {
   if (nev < 0 || nc < 0) return ELR_EINVAL;
   const int64_t a = elr::dir_a_scratch(nev), b = elr::dir_b_scratch(nc);
@@ -404,18 +435,21 @@ extern "C" int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const
     k_dir_lsteps_hits<<<(unsigned)nblocks(n1), kDirBlock, 0, strm>>>(S, P, hs, nh, L_row, L_cnt, nL, s32, L_steps,
                                                                      L_ids, hrec_dyn, hrec_j);
   }
-  if (nev) {
-    char* base = (char*)scratch;
-    DirHdr* hdr = (DirHdr*)base;
-    const int64_t nblk = nblocks(nev);
-    int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
-    int64_t* rel_rank = (int64_t*)(base + align8(sizeof(DirHdr)) + align8(3 * nblk * 8));
-    k_dir_evict_count<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row, rep, ev_dyn, bsum, nblk);
-    k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 0, 0, bsum, nblk, 3, hdr);
-    k_dir_evict_apply<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row, rep, ev_dyn, evl_ids,
-                                                              evf_slots, bsum, nblk, hdr, rel_rank);
-    k_dir_evict_release<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row, rep, rel_rank, hdr);
-  }
+  if (nev) launch_evict(S, P, ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids, evf_slots, ev_dyn, scratch, strm);
+  return launch_status();
+}
+
+extern "C" int elr_dir_evict(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot,
+                             const int64_t* ev_row, const int8_t* thr, int64_t nev, uint8_t* rep, int64_t* evl_ids,
+                             int64_t* evf_slots, int64_t* ev_dyn, void* scratch, int64_t scratch_bytes,
+                             void* stream) {
+  using namespace elr;
+  if (!params_ok(st, p) || nev < 0) return ELR_EINVAL;
+  if (nev == 0) return ELR_OK;
+  if (!ev_slot || !ev_row || !thr || !rep || !evl_ids || !evf_slots || !ev_dyn) return ELR_EINVAL;
+  if (!scratch || scratch_bytes < dir_a_scratch(nev)) return ELR_ECAPACITY;
+  launch_evict(*st, *p, ev_slot, nev, ev_row, thr, nullptr, rep, evl_ids, evf_slots, ev_dyn, scratch,
+               (hipStream_t)stream);
   return launch_status();
 }
 

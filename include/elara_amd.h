@@ -132,6 +132,14 @@ int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const int64_t* h
               int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, int64_t* ev_row, uint8_t* rep, int64_t* evl_ids,
               int64_t* evf_slots, int64_t* ev_dyn, void* scratch, int64_t scratch_bytes, void* stream);
 
+/* The eviction part of call A in the form of srm2/elara_kernels.py:152-171 Directory.evict: the caller has unmapped
+ * the evicted slots (slot_of / slot_row) itself and passes their rows ev_row int64 [nev] and thresholds thr int8
+ * [nev] (kthr of each row's table).  Outputs as elr_dir_a's rep, evl_ids, evf_slots, ev_dyn.  Allocation order:
+ * this build's (the one of elr_dir_a: the released host logs of rows going to M are pushed at once). */
+int elr_dir_evict(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot, const int64_t* ev_row,
+                  const int8_t* thr, int64_t nev, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots,
+                  int64_t* ev_dyn, void* scratch, int64_t scratch_bytes, void* stream);
+
 /* Call B (elara_dir.cpp:98-110): appends of rows a_rows [na] at entry a_k [na] -> a_ids int64 [na]; compactions of
  * rows c_rows [nc] with c_cnt [nc] logged entries -> c_slots int64 [nc].  All inputs int64.  Mutates the
  * directory.  `scratch` (device, >= elr_dir_scratch_bytes(0, nc) bytes) is needed when na + nc > 0. */

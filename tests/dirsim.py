@@ -242,3 +242,48 @@ def check_invariants(view, sim):
     assert np.array_equal(nent[isL & nonres], code[isL & nonres].astype(np.int64))
     # M rows have a MAT slot
     assert np.all(np.asarray(view['loc'])[:sim.R][code == sim.MAT] >= 0)
+
+
+class FacadeImpl(TorchImpl):
+    """The directory driven through the elara_kernels-style front end (hits / lsteps / Directory), in the call
+    sequence of the reference planner's fused path (srm2/elara.py:281-283, 292-293, 312-318, 376-378)."""
+
+    class _Planner:
+        pass
+
+    def __init__(self, sim, st, device):
+        from elara_amd import elara_kernels
+        super().__init__(sim, st, None, device)
+        self.ek = elara_kernels
+        pl = self._Planner()
+        for f, t in zip(O.DIR_FIELDS, self.st):
+            setattr(pl, f, t)
+        pl.R, pl.Kmax, pl.log_cap, pl.n0, pl.Cdyn = sim.R, sim.K, sim.Lcap, sim.n0, sim.Cdyn
+        pl.MAT, pl.mat_trash, pl.evict_logs = sim.MAT, sim.R, sim.evl
+        self.pl = pl
+        self.dirk = elara_kernels.Directory(pl)
+
+    def dir_a(self, hs, L_row, L_cnt, ev_slot, s):
+        torch, pl, K = self.torch, self.pl, self.sim.K
+        L_steps, L_ids = self.ek.lsteps(pl, self.t(L_row, torch.int64), self.t(L_cnt, torch.int32))
+        hd, hj = self.ek.hits(pl, self.t(hs, torch.int64), int(s))
+        ev_slot = self.t(ev_slot, torch.int64)
+        ev_row = pl.slot_row[ev_slot]
+        if ev_slot.numel():
+            pl.slot_of[ev_row] = -1
+            pl.slot_row[ev_slot] = -1
+        thr = pl.kthr[torch.searchsorted(pl.toff, ev_row, right=True) - 1] if ev_slot.numel() else \
+            torch.empty(0, dtype=torch.int8, device=self.dev)
+        rep, evl_ids, evf, self.rel_ev = self.dirk.evict(ev_slot, ev_row, thr)
+        out = [L_steps, L_ids.to(torch.int32), hd, hj, ev_row, rep.to(torch.bool), evl_ids, evf,
+               ev_slot - self.sim.n0]
+        assert L_ids.dtype == torch.int64 and L_ids.shape == (L_row.size, K)
+        return [o.cpu().numpy() for o in out]
+
+    def dir_b(self, a_rows, a_k, c_rows, c_cnt, s):
+        torch = self.torch
+        c_rows_t, c_cnt_t = self.t(c_rows, torch.int64), self.t(c_cnt, torch.int64)
+        a_ids = self.dirk.appends(self.t(a_rows, torch.int64), self.t(a_k, torch.int64), int(s))
+        c_slots = self.dirk.compact(c_rows_t, c_cnt_t)
+        self.dirk.release([self.rel_ev, (c_rows_t, c_cnt_t)])
+        return [a_ids.cpu().numpy(), c_slots.cpu().numpy()]

@@ -8,7 +8,8 @@ of srm2/train.py:474-477 (dir_check) and a few more (no id both live and free, c
 import numpy as np
 import pytest
 
-from dirsim import (OracleImpl, Sim, TorchImpl, check_invariants, comparable_state, diff_outputs, diff_states)
+from dirsim import (FacadeImpl, OracleImpl, Sim, TorchImpl, check_invariants, comparable_state, diff_outputs,
+                    diff_states)
 from oracle import oracle as O
 from oracle import ref
 
@@ -82,6 +83,18 @@ def test_gpu_directory_matches_oracle_and_reference(dev, name):
     if ref.dir() is not None:
         impls.append(TorchImpl(sim, st0, ref.dir()))
     run(sim, impls, 60)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('name', ['default', 'k4_no_static', 'evl_off'])
+def test_gpu_directory_facade_matches_oracle(dev, name):
+    """The elara_kernels-style front end (hits / lsteps / Directory.evict / appends / compact / release), driven in
+    the reference planner's fused-path call sequence, gives the same outputs and states as the oracle (this build
+    uses the cpp allocation order behind both front ends)."""
+    print(f'[gpu-test] directory facade {name}', flush=True)
+    sim = Sim(**CONFIGS[name])
+    st0 = sim.initial_state()
+    run(sim, [OracleImpl(sim, st0), FacadeImpl(sim, st0, dev)], 60)
 
 
 @pytest.mark.gpu
