@@ -81,7 +81,8 @@ def test_gpu_directory_matches_oracle_and_reference(dev, name):
     st0 = sim.initial_state()
     impls = [OracleImpl(sim, st0), gpu_impl(sim, st0, dev)]
     if ref.dir() is not None:
-        impls.append(TorchImpl(sim, st0, ref.dir()))
+        # the reference's own elara_dir.cpp, on CPU tensors and on the same GPU (ATen dispatches to HIP kernels)
+        impls += [TorchImpl(sim, st0, ref.dir()), TorchImpl(sim, st0, ref.dir(), device=dev)]
     run(sim, impls, 60)
 
 
