@@ -31,13 +31,25 @@ inline AdamScalars make_scalars(const float sc[8]) {
 }
 
 // Correctly rounded fp32 quotient a / b from y = RN_f64(1 / b): RN_f32((double)a * y).  The double product is
-// within (2^-53 + 2^-53 + 2^-106) |a/b| < 2^-51 |a/b| of a/b.  A quotient of two floats is never a midpoint
-// between consecutive floats and lies at least 2^-49 |a/b| from every such midpoint (write the distance as
-// |a - mu*b| / |b| and bound the numerator by the granularity of a and of mu*b), for normal and subnormal results
-// alike, so rounding the product to float yields RN_f32(a / b) for every finite a (and inf/NaN propagate as in the
-// division).  Three instructions instead of the eleven of the general correctly rounded fp32 division; checked
-// over all 2^32 values of a by elr_selfcheck_div.
+// within (2^-53 + 2^-53 + 2^-106) |a/b| < 2^-51 |a/b| of a/b.  Write the distance from a/b to a midpoint mu between
+// consecutive floats as |a - mu*b| / |b| and bound the numerator below by the granularity of a and of mu*b: when
+// it is not zero, the distance exceeds the product's error, for normal and subnormal results alike.  It is zero
+// only if a/b is itself a midpoint, which needs a subnormal quotient and b an even integer other than a power of
+// two; the divisors here are bias corrections in (0, 1], so rounding the product to float yields RN_f32(a / b) for
+// every finite a (and inf/NaN propagate as in the division).  Three instructions instead of the eleven of the
+// general correctly rounded fp32 division; checked over all 2^32 values of a by elr_selfcheck_div.
 __device__ __forceinline__ float div_by_recip(float a, double y) { return (float)((double)a * y); }
+
+// True on every active lane: a wave-uniform condition for choosing between a fast and a general code path.
+__device__ __forceinline__ bool wave_all(bool p) {
+  return __builtin_amdgcn_ballot_w64(p) == __builtin_amdgcn_read_exec();
+}
+
+// Lanes (as a wave mask) whose x lies in [lo, hi): two compares, each ballot taken on a single compare so that the
+// mask is the compare's result itself.  NaN is in no range.
+__device__ __forceinline__ uint64_t lanes_in(float x, float lo, float hi) {
+  return __builtin_amdgcn_ballot_w64(x >= lo) & __builtin_amdgcn_ballot_w64(x < hi);
+}
 
 // Correctly rounded fp32 square root.  The compiler's IEEE sequence wraps a core -- the hardware estimate s and a
 // choice among s - 1 ulp, s, s + 1 ulp by the signs of the residuals x - s'*s -- in a rescaling of small inputs and
@@ -54,15 +66,49 @@ __device__ __forceinline__ float sqrt_core(float x) {
   return rp > 0.0f ? sp : r;
 }
 
+// x is finite, normal and >= 2^-96; then 2^-48 <= sqrt(x) < 2^64.
+__device__ __forceinline__ bool sqrt_core_ok(float x) { return x >= 0x1.0p-96f && x < __builtin_inff(); }
+__device__ __forceinline__ uint64_t sqrt_core_lanes(float x) { return lanes_in(x, 0x1.0p-96f, __builtin_inff()); }
+
 __device__ __forceinline__ float sqrt_rn(float x) {
-  const bool core_ok = __builtin_isnormal(x) && x >= 0x1.0p-96f;
-  if (__all(core_ok)) return sqrt_core(x);
+  if (sqrt_core_lanes(x) == __builtin_amdgcn_read_exec()) return sqrt_core(x);
   return __builtin_sqrtf(x);
 }
 
+// Correctly rounded fp32 division n / d for operands in a range.  The compiler's IEEE sequence is a scaling step
+// (v_div_scale on d and on n), the Newton-refined reciprocal r, the quotient n*r, two remainder corrections (the
+// last one, v_div_fmas, rescales when the scaling step asked for it) and a fixup (v_div_fixup) that handles zero,
+// infinite and NaN operands and results out of range.  For 2^-48 <= d < 2^65 and 2^-60 <= |n| < 2^40 the scaling
+// step changes neither operand and asks for no rescale (d and n/d are normal, 1/d is normal, the exponents differ
+// by less than 96, n is far from the denormal range), and the fixup returns the quotient as it is (no special
+// operand, a normal quotient whose sign is sign(n)).  There the core below -- the same instructions without
+// scaling and fixup -- gives the same bits as n / d.  Checked over all 2^32 values of n for a set of d by
+// elr_selfcheck_quot.
+__device__ __forceinline__ bool quot_num_ok(float n) {  // 2^-60 <= |n| < 2^40
+  return __builtin_fabsf(n) >= 0x1.0p-60f && __builtin_fabsf(n) < 0x1.0p40f;
+}
+__device__ __forceinline__ uint64_t quot_num_lanes(float n) { return lanes_in(__builtin_fabsf(n), 0x1.0p-60f, 0x1.0p40f); }
+__device__ __forceinline__ bool quot_den_ok(float d) { return d >= 0x1.0p-48f && d < 0x1.0p65f; }
+__device__ __forceinline__ float div_core(float n, float d) {
+  float r = __builtin_amdgcn_rcpf(d);
+  const float e = __builtin_fmaf(-d, r, 1.0f);
+  r = __builtin_fmaf(e, r, r);
+  float q = n * r;
+  float rem = __builtin_fmaf(-d, q, n);
+  q = __builtin_fmaf(rem, r, q);
+  rem = __builtin_fmaf(-d, q, n);
+  return __builtin_fmaf(rem, r, q);
+}
+
+// eps in [+0, 2^60] (a test of the bit pattern, done on the scalar unit for a wave-uniform eps).  With
+// sqrt_core_ok(vh) it puts den = sqrt(vh) + eps in [2^-48, 2^65), the range of div_core.
+__device__ __forceinline__ bool eps_ok(float eps) { return __float_as_uint(eps) <= 0x5D800000u; }
+
 // One Adam update of one element, in the reference's operation order (srm2/csrc/srm2_cpu.cpp:26-32).  Each
 // statement is one correctly rounded fp32 operation; the two divisions by the step's bias corrections use
-// div_by_recip, the square root sqrt_rn, the division by den the general correctly rounded one.
+// div_by_recip.  When every lane of the wave has vh and num in range (and eps is), the square root and the
+// division by den take their cores sqrt_core and div_core; otherwise the compiler's general sequences.  Both
+// branches give the same bits.
 __device__ __forceinline__ void adam_elem(float& w, float& m, float& v, float g, const AdamScalars& s) {
   float mj = s.b1 * m;
   float t1 = s.omb1 * g;
@@ -73,10 +119,17 @@ __device__ __forceinline__ void adam_elem(float& w, float& m, float& v, float g,
   vj = vj + t2;
   float mh = div_by_recip(mj, s.r1);
   float vh = div_by_recip(vj, s.r2);
-  float den = sqrt_rn(vh);
-  den = den + s.eps;
   float num = s.lr * mh;
-  float up = num / den;
+  float up;
+  if (eps_ok(s.eps) && (sqrt_core_lanes(vh) & quot_num_lanes(num)) == __builtin_amdgcn_read_exec()) {
+    float den = sqrt_core(vh);
+    den = den + s.eps;
+    up = div_core(num, den);
+  } else {
+    float den = __builtin_sqrtf(vh);
+    den = den + s.eps;
+    up = num / den;
+  }
   w = w - up;
   m = mj;
   v = vj;
@@ -106,12 +159,12 @@ __device__ __forceinline__ uint32_t init_row_key(int64_t r, uint32_t seed) {
 
 // Initial weight of element j of row r (srm2/gpu_ops.py:33-36):
 //   key = u32(r*D + j) ^ rowkey;  h = fmix32(key ^ seed);  u = f32(h >> 8) * 2^-24;  w0 = (u*2 - 1) * bound.
-// u*2 and u*2-1 are exact in fp32; the product with bound is the only rounding.
+// With k = h >> 8 < 2^24, f32(k), u = k*2^-24 and u*2 = k*2^-23 are exact, and so is u*2 - 1 = (k - 2^23)*2^-23
+// (|k - 2^23| <= 2^23 fits the significand); one fma(f32(k), 2^-23, -1) computes that exact value.  The product with
+// bound is the only rounding.
 __device__ __forceinline__ float init_elem(uint32_t rlo_times_d_plus_j, uint32_t rowkey, uint32_t seed, float bound) {
   uint32_t h = fmix32((rlo_times_d_plus_j ^ rowkey) ^ seed);
-  float u = (float)(h >> 8) * (1.0f / 16777216.0f);
-  float t = u * 2.0f;
-  t = t - 1.0f;
+  const float t = __builtin_fmaf((float)(h >> 8), 0x1.0p-23f, -1.0f);
   return t * bound;
 }
 

@@ -41,16 +41,19 @@ __device__ __forceinline__ RowFrag<VPL> frag_load(const float* __restrict__ p) {
   return r;
 }
 
+// Stores are marked non-temporal: every row written here (updated Adam state, replayed rows, fresh rows) is read
+// again only by a later kernel, after far more than the caches hold has streamed through.  Measured on the C2 Adam
+// step (d=128): 158 us with ordinary stores, 140 us with non-temporal ones.
 template <int VPL>
 __device__ __forceinline__ void frag_store(float* __restrict__ p, const RowFrag<VPL>& r) {
   if constexpr (VPL == 1) {
-    *p = r.v[0];
+    __builtin_nontemporal_store(r.v[0], p);
   } else if constexpr (VPL == 2) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     f2 t;
     t.x = r.v[0];
     t.y = r.v[1];
-    *reinterpret_cast<f2*>(p) = t;
+    __builtin_nontemporal_store(t, reinterpret_cast<f2*>(p));
   } else {
 #pragma unroll
     for (int q = 0; q < VPL / 4; ++q) {
@@ -59,7 +62,7 @@ __device__ __forceinline__ void frag_store(float* __restrict__ p, const RowFrag<
       t.y = r.v[4 * q + 1];
       t.z = r.v[4 * q + 2];
       t.w = r.v[4 * q + 3];
-      reinterpret_cast<f32x4*>(p)[q] = t;
+      __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p) + q);
     }
   }
 }

@@ -1,5 +1,5 @@
-// Exhaustive checks of this library's fp32 arithmetic shortcuts: the division by a step-constant divisor and the
-// square root (sqrt_rn).
+// Exhaustive checks of this library's fp32 arithmetic shortcuts: the division by a step-constant divisor, the
+// square root (sqrt_rn) and the division core (div_core).
 //
 // The Adam kernels compute the correctly rounded quotient a / b for the two per-step divisors b = 1 - b1^t and
 // b = 1 - b2^t as RN_f32((double)a * y) with y = RN_f64(1 / b).  Why that is exact for every finite a: the double
@@ -62,6 +62,35 @@ __global__ __launch_bounds__(kCheckThreads) void k_check_sqrt(uint64_t base, uns
   }
 }
 
+// div_core(n, d) against the compiler's correctly rounded fp32 division n / d, for one d in div_core's range and
+// every bit pattern n in it (quot_num_ok); `tested` counts the patterns compared.
+__global__ __launch_bounds__(kCheckThreads) void k_check_quot(float d, uint64_t base,
+                                                              unsigned long long* __restrict__ bad,
+                                                              unsigned long long* __restrict__ tested,
+                                                              unsigned int* __restrict__ first_bad) {
+  const uint64_t t0 = base + ((uint64_t)blockIdx.x * kCheckThreads + threadIdx.x) * kCheckPerThread;
+  int nbad = 0, ntested = 0;
+  uint32_t firstv = 0xFFFFFFFFu;
+  for (int k = 0; k < kCheckPerThread; ++k) {
+    const uint64_t nb = t0 + k;
+    if (nb > 0xFFFFFFFFull) break;
+    const float n = __uint_as_float((uint32_t)nb);
+    if (!quot_num_ok(n)) continue;
+    ++ntested;
+    const float want = n / d;
+    const float got = div_core(n, d);
+    if (__float_as_uint(want) != __float_as_uint(got)) {
+      ++nbad;
+      if ((uint32_t)nb < firstv) firstv = (uint32_t)nb;
+    }
+  }
+  if (ntested) atomicAdd(tested, (unsigned long long)ntested);
+  if (nbad) {
+    atomicAdd(bad, (unsigned long long)nbad);
+    atomicMin(first_bad, firstv);
+  }
+}
+
 }  // namespace elr
 
 extern "C" int elr_selfcheck_sqrt(unsigned long long* mismatches, unsigned int* first_bad, void* stream) {
@@ -82,5 +111,18 @@ extern "C" int elr_selfcheck_div(float b, unsigned long long* mismatches, unsign
   const uint64_t blocks_per_launch = 1ull << 18;
   for (uint64_t base = 0; base < (1ull << 32); base += blocks_per_launch * per_block)
     k_check_div<<<(unsigned)blocks_per_launch, kCheckThreads, 0, st>>>(b, y, base, mismatches, first_bad);
+  return launch_status();
+}
+
+extern "C" int elr_selfcheck_quot(float d, unsigned long long* mismatches, unsigned long long* tested,
+                                  unsigned int* first_bad, void* stream) {
+  using namespace elr;
+  if (!mismatches || !tested || !first_bad) return ELR_EINVAL;
+  if (!(d >= 0x1.0p-48f && d < 0x1.0p65f)) return ELR_EINVAL;  // the range of div_core's denominators
+  hipStream_t st = (hipStream_t)stream;
+  const uint64_t per_block = (uint64_t)kCheckThreads * kCheckPerThread;
+  const uint64_t blocks_per_launch = 1ull << 18;
+  for (uint64_t base = 0; base < (1ull << 32); base += blocks_per_launch * per_block)
+    k_check_quot<<<(unsigned)blocks_per_launch, kCheckThreads, 0, st>>>(d, base, mismatches, tested, first_bad);
   return launch_status();
 }

@@ -199,6 +199,12 @@ int elr_selfcheck_div(float b, unsigned long long* mismatches, unsigned int* fir
  * correctly rounded one, for all 2^32 bit patterns x. */
 int elr_selfcheck_sqrt(unsigned long long* mismatches, unsigned int* first_bad, void* stream);
 
+/* The same for the division by den (no counterpart in the reference): the Adam kernels' fast fp32 division core
+ * against the correctly rounded division n / d, for one d in [2^-48, 2^65) (else ELR_EINVAL) and every bit pattern
+ * n with 2^-60 <= |n| < 2^40; *tested (device uint64, caller zeroes it) receives the number of n compared. */
+int elr_selfcheck_quot(float d, unsigned long long* mismatches, unsigned long long* tested, unsigned int* first_bad,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif
