@@ -46,6 +46,8 @@ SIGNATURES = {
     'elr_dir_evict': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_dir_b': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64,
                                  c_vp]),
+    'elr_plan_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_plan_classify': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
 }
 
 DIR_FIELDS = ('code', 'loc', 'ent', 'lstep', 'lfree', 'n_lfree', 'log_top', 'mat_top', 'live', 'adm_c0', 'rj',
@@ -60,6 +62,21 @@ class DirState(ctypes.Structure):
 class DirParams(ctypes.Structure):
     """elr_dir_params: the reference's pv = (R, K, Lcap, n0, Cdyn, MAT, trash, evl) (elara_dir.cpp:11)."""
     _fields_ = [(n, c_i64) for n in ('R', 'K', 'Lcap', 'n0', 'Cdyn', 'MAT', 'trash', 'evl')]
+
+
+class PlanIn(ctypes.Structure):
+    """elr_plan_in: inputs of the planner classification (srm2/elara.py:214-267)."""
+    _fields_ = [('u', c_vp), ('n', c_i64), ('next', c_vp * 4), ('n_next', c_i64 * 4), ('nnext', ctypes.c_int),
+                ('slot_of', c_vp), ('last_seen', c_vp), ('code', c_vp), ('kthr', c_vp), ('toff', c_vp), ('T', c_i64),
+                ('dyn', c_vp), ('nd', c_i64), ('slot_row', c_vp), ('mat_top', c_vp), ('log_top', c_vp),
+                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int)]
+
+
+class PlanOut(ctypes.Structure):
+    """elr_plan_out: per-position classes, flags, slots and codes, the class order, the dynamic-slot partition and
+    the host counts."""
+    _fields_ = [('cls', c_vp), ('flags', c_vp), ('sl', c_vp), ('c', c_vp), ('order', c_vp), ('dyn_out', c_vp),
+                ('counts', c_vp)]
 
 
 def lib():

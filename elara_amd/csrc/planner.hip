@@ -1,0 +1,240 @@
+// Planner classification of one ELARA step (srm2/elara.py:214-267, the part before the class counts go to the host):
+// three launches in place of the reference planner's chain of elementwise torch ops, bincount and stable argsorts.
+//
+//   unique rows u[i] of the batch: slot sl = slot_of[u], hit = sl >= 0, admit = !hit && last_seen[u] > s,
+//     in_next = u appears in one of the next batches, c = code[u], app = c < kthr[table_of(u)], and the class
+//       hit -> HIT;  c == 0 (N) -> admit ? NADM : app ? NAPP : NCMP;  1 <= c <= K (L) -> LADM / LAPP / LCMP;
+//       otherwise (M) -> admit ? FADM : want_T ? FNADM : S                              (elara.py:244-258)
+//   dynamic pool slots d = dyn[j] (row r = slot_row[d]): protected when r appears in one of the next batches
+//     (the slot holds a row the pipeline needs, elara.py:227-229), expired when last_seen[r] <= s (the row's TTL is
+//     over, elara.py:231-233); class 0 = expired and unprotected, 1 = unprotected (preemptible), 2 = protected.
+//
+// Outputs: the positions of u sorted stably by class (`order`), the dynamic slots partitioned stably by class
+// ([class 0 | class 1 | class 2] and [class 0 | classes 1, 2 in dyn order], so that the evicted and kept slots of
+// both the plain and the preempting plan are contiguous slices), per-position flags, slots and codes, and a small
+// block of counts for the host: 10 class counts, the 3 dynamic-slot counts, mat_top and log_top.
+//
+// A dynamic slot is protected in the reference when slot_of[un] == d for a row un of the next batches; every
+// occupied dynamic slot satisfies slot_of[slot_row[d]] == d, so the test here is the membership of slot_row[d] in
+// the (ascending, unique) next batches, by binary search.
+#include "elr_scan.h"
+
+namespace elr {
+
+constexpr int kPlanBlock = 256;
+constexpr int kNumCls = 10;     // HIT, NADM, NAPP, NCMP, LADM, LAPP, LCMP, FADM, FNADM, S
+constexpr int kDynCh = 4;       // expired, preemptible, protected, not expired (= preemptible + protected)
+
+enum : int { kHit = 0, kNAdm, kNApp, kNCmp, kLAdm, kLApp, kLCmp, kFAdm, kFNAdm, kS };
+
+__device__ __forceinline__ bool sorted_has(const int64_t* __restrict__ a, int64_t n, int64_t x) {
+  int64_t lo = 0, hi = n;   // first index with a[idx] >= x
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (a[mid] < x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo < n && a[lo] == x;
+}
+
+__device__ __forceinline__ bool in_next(const elr_plan_in& p, int64_t r) {
+  bool f = false;
+  for (int k = 0; k < p.nnext; ++k) f = f || sorted_has(p.next[k], p.n_next[k], r);
+  return f;
+}
+
+// Table of row r: the last t with toff[t] <= r (searchsorted(toff, r, right=True) - 1, srm2/elara_dir.cpp:46-48).
+__device__ __forceinline__ int64_t table_of(const int64_t* __restrict__ toff, int64_t T, int64_t r) {
+  int64_t lo = 0, hi = T;   // first index with toff[idx] > r
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (toff[mid] <= r) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo - 1;
+}
+
+struct RowClass {
+  int cls, flags, sl, c;
+};
+
+__device__ __forceinline__ RowClass classify_row(const elr_plan_in& p, int64_t r) {
+  RowClass o;
+  o.sl = p.slot_of[r];
+  const bool hit = o.sl >= 0;
+  const bool admit = !hit && (int64_t)p.last_seen[r] > p.s;
+  const bool nxt = in_next(p, r);
+  o.c = p.code[r];
+  const int64_t t = table_of(p.toff, p.T, r);
+  const int thr = (t >= 0 && t < p.T) ? (int)p.kthr[t] : 0;
+  const bool isN = o.c == 0, isL = o.c >= 1 && o.c <= p.K, app = o.c < thr;
+  int k;
+  if (hit) k = kHit;
+  else if (isN) k = admit ? kNAdm : (app ? kNApp : kNCmp);
+  else if (isL) k = admit ? kLAdm : (app ? kLApp : kLCmp);
+  else if (admit || p.want_t) k = admit ? kFAdm : kFNAdm;
+  else k = kS;
+  o.cls = k;
+  o.flags = (hit ? ELR_PLAN_HIT : 0) | (isN ? ELR_PLAN_N : 0) | (isL ? ELR_PLAN_L : 0) | (app ? ELR_PLAN_APP : 0) |
+            (admit ? ELR_PLAN_ADMIT : 0) | (nxt ? ELR_PLAN_NEXT : 0);
+  return o;
+}
+
+__device__ __forceinline__ int dyn_class(const elr_plan_in& p, int64_t d) {
+  const int64_t r = p.slot_row[d];
+  const bool prot = r >= 0 && in_next(p, r);
+  if (prot) return 2;
+  const bool expired = r < 0 || (int64_t)p.last_seen[r] <= p.s;
+  return expired ? 0 : 1;
+}
+
+// Wave ranks and block counts of NCH classes: for element class k (or -1 for none) the rank among the block's
+// earlier elements of the same class (stable: thread order), and every class's block total in tot.
+template <int NCH>
+__device__ __forceinline__ int block_class_rank(int k, int (&tot)[NCH]) {
+  constexpr int NW = kPlanBlock / 64;
+  __shared__ int wc[NW][NCH];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int rank_w = 0;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    const uint64_t m = __builtin_amdgcn_ballot_w64(k == q);
+    if (k == q) rank_w = __builtin_popcountll(m & lanemask_lt());
+    if (lane == 0) wc[w][q] = __builtin_popcountll(m);
+  }
+  __syncthreads();
+  int before = 0;
+#pragma unroll
+  for (int q = 0; q < NCH; ++q) {
+    int t = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const int x = wc[v][q];
+      if (q == k && v < w) before += x;
+      t += x;
+    }
+    tot[q] = t;
+  }
+  return before + rank_w;
+}
+
+// Pass 1: classify and count per block.  Blocks [0, nbu) take the unique rows, blocks [nbu, nbu + nbd) the dynamic
+// slots.  Block counts go channel-major: bu[c * nbu + b], bd[c * nbd + b].
+__global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
+                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd) {
+  const int64_t b = blockIdx.x;
+  if (b < nbu) {
+    const int64_t i = b * kPlanBlock + threadIdx.x;
+    int k = -1;
+    if (i < p.n) {
+      const RowClass rc = classify_row(p, p.u[i]);
+      k = rc.cls;
+      o.cls[i] = (int8_t)rc.cls;
+      o.flags[i] = (uint8_t)rc.flags;
+      o.sl[i] = rc.sl;
+      o.c[i] = (int8_t)rc.c;
+    }
+    int tot[kNumCls];
+    block_class_rank<kNumCls>(k, tot);
+    if (threadIdx.x < kNumCls) bu[threadIdx.x * nbu + b] = tot[threadIdx.x];
+  } else {
+    const int64_t bb = b - nbu;
+    const int64_t j = bb * kPlanBlock + threadIdx.x;
+    const int k = j < p.nd ? dyn_class(p, p.dyn[j]) : -1;
+    int tot[3];
+    block_class_rank<3>(k, tot);
+    if (threadIdx.x == 0) {
+      bd[0 * nbd + bb] = tot[0];
+      bd[1 * nbd + bb] = tot[1];
+      bd[2 * nbd + bb] = tot[2];
+      bd[3 * nbd + bb] = tot[1] + tot[2];
+    }
+  }
+}
+
+// Pass 2 (one block): block offsets per class; class totals and the host counts.
+__global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
+                                                          int64_t* __restrict__ bu, int64_t* __restrict__ bd,
+                                                          int64_t* __restrict__ tot) {
+  scan_channels_block(bu, nbu, kNumCls, tot);
+  scan_channels_block(bd, nbd, kDynCh, tot + kNumCls);
+  __syncthreads();
+  if (threadIdx.x < kNumCls) o.counts[threadIdx.x] = tot[threadIdx.x];
+  if (threadIdx.x < 3) o.counts[kNumCls + threadIdx.x] = tot[kNumCls + threadIdx.x];
+  if (threadIdx.x == 0) {
+    o.counts[13] = p.mat_top ? *p.mat_top : 0;
+    o.counts[14] = p.log_top ? *p.log_top : 0;
+    o.counts[15] = 0;
+  }
+}
+
+// Pass 3: stable scatter by class.
+__global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
+                                                             const int64_t* __restrict__ bu,
+                                                             const int64_t* __restrict__ bd,
+                                                             const int64_t* __restrict__ tot) {
+  const int64_t b = blockIdx.x;
+  if (b < nbu) {
+    const int64_t i = b * kPlanBlock + threadIdx.x;
+    const int k = i < p.n ? (int)o.cls[i] : -1;
+    int t[kNumCls];
+    const int r = block_class_rank<kNumCls>(k, t);
+    if (k >= 0) {
+      int64_t base = 0;
+      for (int q = 0; q < k; ++q) base += tot[q];
+      o.order[base + bu[(int64_t)k * nbu + b] + r] = i;
+    }
+  } else {
+    const int64_t bb = b - nbu;
+    const int64_t j = bb * kPlanBlock + threadIdx.x;
+    const int k = j < p.nd ? dyn_class(p, p.dyn[j]) : -1;
+    int t3[3];
+    const int r3 = block_class_rank<3>(k, t3);
+    int t2[2];
+    const int r2 = block_class_rank<2>(k < 0 ? -1 : (k == 0 ? 0 : 1), t2);
+    if (k >= 0) {
+      const int64_t* dt = tot + kNumCls;   // expired, preemptible, protected, not expired
+      const int64_t base3 = k == 0 ? 0 : (k == 1 ? dt[0] : dt[0] + dt[1]);
+      const int64_t d = p.dyn[j];
+      o.dyn_out[base3 + bd[(int64_t)k * nbd + bb] + r3] = d;
+      const int64_t pos2 = k == 0 ? bd[0 * nbd + bb] + r2 : dt[0] + bd[3 * nbd + bb] + r2;
+      o.dyn_out[p.nd + pos2] = d;
+    }
+  }
+}
+
+inline int64_t plan_blocks(int64_t m) { return (m + kPlanBlock - 1) / kPlanBlock; }
+
+}  // namespace elr
+
+extern "C" int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd) {
+  using namespace elr;
+  if (n < 0 || nd < 0) return -1;
+  const int64_t nbu = plan_blocks(n), nbd = plan_blocks(nd);
+  return ((kNumCls * nbu + kDynCh * nbd + kNumCls + kDynCh) * 8 + 255) & ~int64_t(255);
+}
+
+extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
+                                 void* stream) {
+  using namespace elr;
+  if (!in || !out) return ELR_EINVAL;
+  const elr_plan_in& p = *in;
+  const elr_plan_out& o = *out;
+  if (p.n < 0 || p.nd < 0 || p.n >= (int64_t(1) << 31) || p.nd >= (int64_t(1) << 31)) return ELR_EINVAL;
+  if (p.nnext < 0 || p.nnext > 4 || p.T < 1 || p.K < 1 || !p.toff || !p.kthr || !o.counts) return ELR_EINVAL;
+  for (int k = 0; k < p.nnext; ++k)
+    if (p.n_next[k] < 0 || (p.n_next[k] > 0 && !p.next[k])) return ELR_EINVAL;
+  if (p.n > 0 && (!p.u || !p.slot_of || !p.last_seen || !p.code || !o.cls || !o.flags || !o.sl || !o.c || !o.order))
+    return ELR_EINVAL;
+  if (p.nd > 0 && (!p.dyn || !p.slot_row || !p.last_seen || !o.dyn_out)) return ELR_EINVAL;
+  if (!scratch || scratch_bytes < elr_plan_scratch_bytes(p.n, p.nd)) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nbu = plan_blocks(p.n), nbd = plan_blocks(p.nd);
+  int64_t* bu = (int64_t*)scratch;
+  int64_t* bd = bu + kNumCls * nbu;
+  int64_t* tot = bd + kDynCh * nbd;
+  if (nbu + nbd > 0) k_plan_count<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd);
+  k_plan_scan<<<1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
+  if (nbu + nbd > 0) k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
+  return launch_status();
+}

@@ -1,0 +1,87 @@
+"""Planner classification of one ELARA step on the GPU (elr_plan_classify): srm2/elara.py:214-267.
+
+plan_classify(...) returns the per-position class, flags, slot and code of the batch's unique rows, their positions
+sorted stably by class, the dynamic pool slots partitioned into expired / preemptible / protected, and a device
+block of counts for the host (one small read, the plan's only synchronisation in the common case).
+"""
+import ctypes
+from collections import namedtuple
+
+import torch
+
+from . import _lib
+
+I8, I32, I64 = torch.int8, torch.int32, torch.int64
+# classes (srm2/elara.py:31-32)
+C_HIT, C_NADM, C_NAPP, C_NCMP, C_LADM, C_LAPP, C_LCMP, C_FADM, C_FNADM, C_S = range(10)
+F_HIT, F_N, F_L, F_APP, F_ADMIT, F_NEXT = 1, 2, 4, 8, 16, 32
+# counts[16]: 10 class counts, then these
+CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP = 10, 11, 12, 13, 14
+
+PlanClass = namedtuple('PlanClass', 'cls flags sl c order dyn_out counts')
+
+
+def _dev_i64(t, dev):
+    return t.to(device=dev, dtype=I64).contiguous()
+
+
+def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t):
+    """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
+
+    u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
+    them: slot_of int32 [R], last_seen int32 [R], code int8 [R], kthr int8 [T], toff int64 [T], slot_row int64 [C],
+    mat_top / log_top int64 [1].  Returns PlanClass(cls int8 [n], flags uint8 [n], sl int32 [n], c int8 [n],
+    order int64 [n], dyn_out int64 [2 nd], counts int64 [16] on the device)."""
+    dev = u.device
+    if dev.type != 'cuda':
+        raise RuntimeError('plan_classify: tensors must be on a GPU')
+    u = _dev_i64(u, dev)
+    nexts = [_dev_i64(x, dev) for x in u_nexts if x.numel()]
+    if len(nexts) > 4:
+        raise RuntimeError('plan_classify: at most 4 next batches')
+    for t, dt, name in ((slot_of, I32, 'slot_of'), (last_seen, I32, 'last_seen'), (code, I8, 'code'),
+                        (kthr, I8, 'kthr'), (toff, I64, 'toff'), (slot_row, I64, 'slot_row'),
+                        (mat_top, I64, 'mat_top'), (log_top, I64, 'log_top')):
+        if t.dtype != dt or t.device != dev or not t.is_contiguous():
+            raise RuntimeError(f'plan_classify: {name} must be a contiguous {dt} tensor on {dev}')
+    dyn = _dev_i64(dyn, dev)
+    n, nd = u.numel(), dyn.numel()
+    out = PlanClass(torch.empty(n, dtype=I8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev),
+                    torch.empty(n, dtype=I32, device=dev), torch.empty(n, dtype=I8, device=dev),
+                    torch.empty(n, dtype=I64, device=dev), torch.empty(2 * nd, dtype=I64, device=dev),
+                    torch.empty(16, dtype=I64, device=dev))
+    p = _lib.ptr
+    pin = _lib.PlanIn()
+    pin.u, pin.n = u.data_ptr(), n
+    for k, x in enumerate(nexts):
+        pin.next[k] = x.data_ptr()
+        pin.n_next[k] = x.numel()
+    pin.nnext = len(nexts)
+    pin.slot_of, pin.last_seen, pin.code = slot_of.data_ptr(), last_seen.data_ptr(), code.data_ptr()
+    pin.kthr, pin.toff, pin.T = kthr.data_ptr(), toff.data_ptr(), toff.numel()
+    pin.dyn, pin.nd, pin.slot_row = dyn.data_ptr(), nd, slot_row.data_ptr()
+    pin.mat_top, pin.log_top = mat_top.data_ptr(), log_top.data_ptr()
+    pin.s, pin.K, pin.want_t = int(s), int(K), int(bool(want_t))
+    pout = _lib.PlanOut(*[t.data_ptr() for t in out])
+    nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
+    scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,
+                                          _lib.stream_of(u))
+    _lib.check(rc, 'elr_plan_classify')
+    return out
+
+
+def classify_from_flags(flags, admit, want_t):
+    """Classes from the flags of plan_classify with a changed admission mask (the planner's overflow path,
+    srm2/elara.py:244-258 applied to the un-admitted rows)."""
+    dev = flags.device
+    f = flags.to(torch.int32)
+    hit, isN, isL, app = (f & F_HIT) != 0, (f & F_N) != 0, (f & F_L) != 0, (f & F_APP) != 0
+    t8 = lambda v: torch.tensor(v, dtype=I8, device=dev)  # noqa: E731
+    cls = torch.full(flags.shape, C_S, dtype=I8, device=dev)
+    wantT = torch.full(flags.shape, bool(want_t), dtype=torch.bool, device=dev)
+    cls = torch.where(~isN & ~isL & (admit | wantT), torch.where(admit, t8(C_FADM), t8(C_FNADM)), cls)
+    cls = torch.where(isL, torch.where(admit, t8(C_LADM), torch.where(app, t8(C_LAPP), t8(C_LCMP))), cls)
+    cls = torch.where(isN, torch.where(admit, t8(C_NADM), torch.where(app, t8(C_NAPP), t8(C_NCMP))), cls)
+    return torch.where(hit, t8(C_HIT), cls)

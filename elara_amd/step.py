@@ -24,6 +24,8 @@ from .dedup import embedding_dense_backward, unique
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import gpu_adam
+from .planner import (CNT_EXP, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
+                      plan_classify)
 from .rows import copy_rows
 
 I8, I32, I64 = torch.int8, torch.int32, torch.int64
@@ -42,6 +44,9 @@ class HipBackend:
 
     def unique(self, ids):
         return unique(ids)
+
+    def plan_classify(self, *args):
+        return plan_classify(*args)
 
     def segsum(self, g_occ, inv, U):
         return embedding_dense_backward(g_occ, inv, U)
@@ -131,7 +136,6 @@ class ElaraStep:
         self.glog = torch.zeros(self.Cdyn + 1, K, D, device=d)
         self.mat = torch.empty(self.mat_cap, 3, D, device=d)
         self.logs = torch.empty(self.log_cap + 1, D, device=d)
-        self._c8 = [torch.tensor(v, dtype=I8, device=d) for v in range(10)]
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs')}
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
@@ -161,76 +165,47 @@ class ElaraStep:
         self.stats['syncs'] += 1
         return torch.stack([t.reshape(()).to(I64) for t in ts]).tolist()
 
-    def table_of(self, rows):
-        return torch.searchsorted(self.toff, rows, right=True) - 1
+    def _host_list(self, t):
+        self.stats['syncs'] += 1
+        return t.tolist()
 
     # ---- plan (srm2/elara.py:209-414, cpp directory path) ----
     def plan(self, s, u, u_nexts):
         d, K, C = self.d, self.K, self.C
         n = u.numel()
-        sl = self.slot_of[u]
-        hit = sl >= 0
-        in_next = torch.zeros(n, dtype=torch.bool, device=d)
-        for un in u_nexts:
-            if un.numel():
-                j = torch.searchsorted(un, u).clamp(max=un.numel() - 1)
-                in_next |= un[j] == u
-        admit = ~hit & (self.last_seen[u] > s)
-        # slots of rows needed by the next batches (srm2/elara.py:227-229); rows without a slot mark a trash element
-        # (a plain store, where counting them into slot 0 would serialise on one address)
-        prot = torch.zeros(C + 1, dtype=torch.bool, device=d)
-        prot[:C] = self.pinned
-        for un in u_nexts:
-            sn = self.slot_of[un].long()
-            prot[torch.where(sn >= 0, sn, torch.full_like(sn, C))] = True
-        protect = prot[:C]
-        dl = self.dyn_slots
-        exp = ~protect[dl] & (self.last_seen[self.slot_row[dl]] <= s)
-        c = self.code[u]
-        thr = self.kthr[self.table_of(u)]
-        isN = c == 0
-        isL = (c >= 1) & (c <= K)
-        app = c < thr
-        wantT = torch.full((n,), self.st_mode == 'T', dtype=torch.bool, device=d)
-        t8 = self._c8.__getitem__
-
-        def classify(admit):
-            cls = torch.full((n,), C_S, dtype=I8, device=d)
-            cls = torch.where(~isN & ~isL & (admit | wantT), torch.where(admit, t8(C_FADM), t8(C_FNADM)), cls)
-            cls = torch.where(isL, torch.where(admit, t8(C_LADM), torch.where(app, t8(C_LAPP), t8(C_LCMP))), cls)
-            cls = torch.where(isN, torch.where(admit, t8(C_NADM), torch.where(app, t8(C_NAPP), t8(C_NCMP))), cls)
-            return torch.where(hit, t8(C_HIT), cls)
-
-        cls = classify(admit)
-        vals = self._host(exp.sum(), self.mat_top, self.log_top, *torch.bincount(cls.long(), minlength=10))
-        n_exp, mat_top, log_top, counts = vals[0], vals[1], vals[2], vals[3:]
+        # classes, class order, expired / preemptible / protected dynamic slots, counts (srm2/elara.py:214-267)
+        pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
+                                   self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
+                                   self.st_mode == 'T')
+        vals = self._host_list(pc.counts)
+        counts = vals[:10]
+        n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]
         if mat_top > self.mat_cap - 1 or log_top > self.log_cap:
             raise RuntimeError(f'arena capacity exceeded (MAT {mat_top}/{self.mat_cap}, logs {log_top}/{self.log_cap})')
+        sl, c, order = pc.sl, pc.c, pc.order
         n_adm = counts[C_NADM] + counts[C_LADM] + counts[C_FADM]
-        o = torch.argsort((~exp).to(I8), stable=True)
-        ev_slot, keep_dyn = dl[o[:n_exp]], dl[o[n_exp:]]
+        nd = self.dyn_slots.numel()
         need = n_adm - (self.n_free + n_exp)
-        if need > 0 and keep_dyn.numel():   # preempt residents not needed within the pipeline window
-            pre = ~protect[keep_dyn]
-            n_pre, = self._host(pre.sum())
-            take = min(need, n_pre)
-            if take:
-                o2 = torch.argsort((~pre).to(I8), stable=True)
-                ev_slot = torch.cat([ev_slot, keep_dyn[o2[:take]]])
-                keep_dyn = keep_dyn[o2[take:]]
-                n_exp += take
-                need -= take
-                self.stats['preempt'] += take
+        take = min(need, n_pre) if need > 0 and nd > n_exp else 0
+        if take:   # preempt residents not needed within the pipeline window
+            ev_slot, keep_dyn = pc.dyn_out[:n_exp + take], pc.dyn_out[n_exp + take:nd]
+            n_exp += take
+            need -= take
+            self.stats['preempt'] += take
+        else:
+            ev_slot, keep_dyn = pc.dyn_out[:n_exp], pc.dyn_out[nd + n_exp:]
         if need > 0:   # overflow: un-admit (non-carry first) and recount
+            admit = (pc.flags & F_ADMIT) != 0
+            in_next = (pc.flags & F_NEXT) != 0
             pri = (~admit).to(I32) * 4 + admit.to(I32) * (2 - 2 * in_next.to(I32))
             oo = torch.argsort(pri, stable=True)
             drop = oo[n_adm - need:n_adm]
             admit[drop] = False
             self.stats['overflow'] += need
             n_adm -= need
-            cls = classify(admit)
+            cls = classify_from_flags(pc.flags, admit, self.st_mode == 'T')
             counts = self._host(*torch.bincount(cls.long(), minlength=10))
-        order = torch.argsort(cls, stable=True)
+            order = torch.argsort(cls, stable=True)
         b_ = [0]
         for x in counts:
             b_.append(b_[-1] + x)

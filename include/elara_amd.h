@@ -177,6 +177,60 @@ int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* gra
                    const float sc[8], void* scratch, int64_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Planner classification of one step: srm2/elara.py:214-267 (ELARAPlanner.plan up to the class counts) -- the
+ * per-row class of the batch's unique rows, the stable class order, the expired / preemptible / protected split of
+ * the dynamic pool slots, and the counts the host needs, in three launches.
+ *
+ * Classes (srm2/elara.py:31-32): 0 HIT, 1 N admitted, 2 N append, 3 N compact, 4 L admitted, 5 L append,
+ * 6 L compact, 7 F admitted, 8 F not admitted (transient), 9 S.  A row hits when slot_of[u] >= 0; a missing row is
+ * admitted when last_seen[u] > s; N rows have code 0, L rows 1..K, F/S rows code K+1; "append" when
+ * code < kthr[table]; F rows that are not admitted are transient with want_t, else S.
+ * ------------------------------------------------------------------------------------------------------- */
+#define ELR_PLAN_HIT 1
+#define ELR_PLAN_N 2
+#define ELR_PLAN_L 4
+#define ELR_PLAN_APP 8
+#define ELR_PLAN_ADMIT 16
+#define ELR_PLAN_NEXT 32   /* the row appears in one of the next batches */
+
+typedef struct elr_plan_in {
+  const int64_t* u;           /* [n] the batch's unique rows, ascending */
+  int64_t n;
+  const int64_t* next[4];     /* unique rows of the next batches, each ascending */
+  int64_t n_next[4];
+  int nnext;                  /* 0..4 */
+  const int32_t* slot_of;     /* [R] pool slot of each row or -1 */
+  const int32_t* last_seen;   /* [R] last logical step each row is known to appear at */
+  const int8_t* code;         /* [R] row codes */
+  const int8_t* kthr;         /* [T] */
+  const int64_t* toff;        /* [T] first row of each table */
+  int64_t T;
+  const int64_t* dyn;         /* [nd] occupied dynamic pool slots */
+  int64_t nd;
+  const int64_t* slot_row;    /* [C] row held by each slot or -1 */
+  const int64_t* mat_top;     /* device counters copied into counts[13], counts[14] (may be NULL) */
+  const int64_t* log_top;
+  int64_t s;                  /* logical step */
+  int K;
+  int want_t;                 /* transient updates of non-admitted F rows (st_mode 'T') */
+} elr_plan_in;
+
+typedef struct elr_plan_out {
+  int8_t* cls;                /* [n] class of each position */
+  uint8_t* flags;             /* [n] ELR_PLAN_* bits */
+  int32_t* sl;                /* [n] slot_of[u] */
+  int8_t* c;                  /* [n] code[u] */
+  int64_t* order;             /* [n] positions sorted stably by class */
+  int64_t* dyn_out;           /* [2 nd]: slots as [expired | preemptible | protected], then [expired | the rest],
+                                 each part in dyn order */
+  int64_t* counts;            /* [16] device: 10 class counts, expired, preemptible, protected, mat_top, log_top, 0 */
+} elr_plan_out;
+
+int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd);
+int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Row copies: dst[dst_idx[i]] = src[src_idx[i]], i < n, rows of W floats (NULL index = identity).
  * Replaces: the gradient-log append logs[A_ids] = g (srm2/elara.py:569-570 with srm2/csrc/srm2_cpu.cpp:167-180
  * cs_append semantics; here the log arena is in HBM), the resident-history record glog.index_put_((dyn, j), g)

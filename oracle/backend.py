@@ -17,6 +17,55 @@ class OracleBackend:
     def unique(self, ids):
         return torch.unique(ids, return_inverse=True)
 
+    def plan_classify(self, u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s,
+                      K, want_t):
+        """Restatement of the planner's classification (srm2/elara.py:214-267) with torch ops on CPU tensors:
+        slot lookup and hits (:219-220), next-batch membership (:223-226), admission by TTL (:221), protection of
+        the slots the next batches need through a scatter of their slots (:227-229), expiry of unprotected
+        dynamic slots (:231-233), class per row (:244-258) and the stable class orders (:242, 260-267).  Returns
+        what elara_amd.planner.plan_classify returns."""
+        from elara_amd.planner import PlanClass
+        n = u.numel()
+        sl = slot_of[u]
+        hit = sl >= 0
+        in_next = torch.zeros(n, dtype=torch.bool)
+        for un in u_nexts:
+            if un.numel():
+                j = torch.searchsorted(un, u).clamp(max=un.numel() - 1)
+                in_next |= un[j] == u
+        admit = ~hit & (last_seen[u].long() > s)
+        C = slot_row.numel()
+        prot = torch.zeros(C + 1, dtype=torch.bool)
+        for un in u_nexts:
+            sn = slot_of[un].long()
+            prot[torch.where(sn >= 0, sn, torch.full_like(sn, C))] = True
+        dyn = dyn.long()
+        unprot = ~prot[dyn]
+        exp = unprot & (last_seen[slot_row[dyn]].long() <= s)
+        pre = unprot & ~exp
+        c = code[u]
+        thr = kthr[torch.searchsorted(toff, u, right=True) - 1]
+        isN = c == 0
+        isL = (c >= 1) & (c <= K)
+        app = c < thr
+        t8 = lambda v: torch.tensor(v, dtype=torch.int8)  # noqa: E731
+        cls = torch.full((n,), 9, dtype=torch.int8)
+        wantT = torch.full((n,), bool(want_t), dtype=torch.bool)
+        cls = torch.where(~isN & ~isL & (admit | wantT), torch.where(admit, t8(7), t8(8)), cls)
+        cls = torch.where(isL, torch.where(admit, t8(4), torch.where(app, t8(5), t8(6))), cls)
+        cls = torch.where(isN, torch.where(admit, t8(1), torch.where(app, t8(2), t8(3))), cls)
+        cls = torch.where(hit, t8(0), cls)
+        flags = (hit.to(torch.uint8) | (isN.to(torch.uint8) << 1) | (isL.to(torch.uint8) << 2) |
+                 (app.to(torch.uint8) << 3) | (admit.to(torch.uint8) << 4) | (in_next.to(torch.uint8) << 5))
+        order = torch.argsort(cls, stable=True)
+        dcls = torch.where(exp, 0, torch.where(pre, 1, 2)).to(torch.int8)
+        dyn_out = torch.cat([dyn[torch.argsort(dcls, stable=True)], dyn[torch.argsort((~exp).to(torch.int8),
+                                                                                      stable=True)]])
+        counts = torch.cat([torch.bincount(cls.long(), minlength=10),
+                            torch.stack([exp.sum(), pre.sum(), (dcls == 2).sum()]),
+                            mat_top.reshape(1), log_top.reshape(1), torch.zeros(1, dtype=torch.int64)])
+        return PlanClass(cls, flags, sl, c, order, dyn_out, counts)
+
     def segsum(self, g_occ, inv, U):
         out = np.zeros((U, self.D), np.float32)
         if inv.numel():

@@ -1,8 +1,9 @@
 """The whole ELARA step with HBM-resident arenas (config C5; elara_amd.step, the counterpart of srm2/elara.py's
 planner and executor): the HIP kernels against the CPU oracle driving the identical step.
 
-Both runs see the same batches and occurrence gradients; the planner logic is shared (torch ops on each device),
-the hot-path kernels differ (HIP vs oracle/elara_oracle.c).  After the run the directory, the pool, the resident
+Both runs see the same batches and occurrence gradients; the planner's glue is shared (torch ops on each device),
+the hot-path kernels and the planner classification differ (HIP vs oracle/elara_oracle.c and the torch
+restatement in oracle/backend.py).  After the run the directory, the pool, the resident
 histories, the MAT and log arenas and the eval-style weights of every touched row (srm2/elara.py:582-604) must be
 bitwise equal.  Trash rows (whose contents the reference leaves unspecified) are excluded.
 """
@@ -85,12 +86,12 @@ def test_step_runs_on_cpu_with_oracle_backend():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S'])
+@pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow'])
 def test_gpu_step_matches_oracle_step(dev, name):
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
-    kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}}[name]
-    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, C=2500, n_static=1500, **kw)
+    kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000}}[name]
+    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
     g = make(cfg, dev)
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
     gf = grads_fn(cfg, None)
@@ -116,3 +117,34 @@ def test_gpu_step_c5_full_shape(dev):
     torch.cuda.synchronize()
     assert compare(g, c, cfg) > 100_000
     assert g.stats == c.stats
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('name', ['small_evl', 'small_S'])
+def test_gpu_plan_classify_matches_oracle(dev, name):
+    """elr_plan_classify against the oracle's torch restatement of the planner classification, on every plan of
+    a run (states as the step produces them, including steps that preempt and overflow): every output bitwise."""
+    from elara_amd.planner import plan_classify
+    from elara_amd.step import run
+    print(f'[gpu-test] plan classify {name}', flush=True)
+    kw = {'small_evl': {}, 'small_S': {'st': 'S'}}[name]
+    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=30, C=2000, n_static=1500, **kw)
+    be = OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2)
+    calls = []
+    orig = be.plan_classify
+
+    def both(*args):
+        want = orig(*args)
+        g = [a.to(dev) if isinstance(a, torch.Tensor) else a for a in args]
+        g[1] = [x.to(dev) for x in args[1]]
+        got = plan_classify(*g)
+        for f in want._fields:
+            x, y = getattr(want, f), getattr(got, f).cpu()
+            assert x.dtype == y.dtype and torch.equal(x, y), (len(calls), f)
+        calls.append(int(want.counts[10]))
+        return want
+    be.plan_classify = both
+    st = make(cfg, 'cpu', be)
+    run(st, cfg['batches'], grads_fn(cfg, 'cpu'))
+    assert len(calls) == cfg['steps']
+    assert st.stats['preempt'] > 0 and st.stats['overflow'] > 0 and sum(calls) > 0, st.stats
