@@ -47,6 +47,12 @@ SIGNATURES = {
     'elr_dir_b': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64,
                                  c_vp]),
     'elr_plan_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_plan_admit': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_i64, c_i64, c_i64, c_i64, ctypes.c_int,
+                                      c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    'elr_assemble': (ctypes.c_int, [c_vp, c_vp]),
+    'elr_dedup_plan_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_dedup_plan': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
+    'elr_segment_sum_plan': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'elr_plan_classify': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
 }
 
@@ -75,8 +81,17 @@ class PlanIn(ctypes.Structure):
 class PlanOut(ctypes.Structure):
     """elr_plan_out: per-position classes, flags, slots and codes, the class order, the dynamic-slot partition and
     the host counts."""
-    _fields_ = [('cls', c_vp), ('flags', c_vp), ('sl', c_vp), ('c', c_vp), ('order', c_vp), ('dyn_out', c_vp),
-                ('counts', c_vp)]
+    _fields_ = [('cls', c_vp), ('flags', c_vp), ('sl', c_vp), ('c', c_vp), ('order', c_vp), ('rank', c_vp),
+                ('dyn_out', c_vp), ('counts', c_vp)]
+
+
+class AssembleArgs(ctypes.Structure):
+    """elr_assemble_args: the fused weight assembly of one step (srm2/elara.py:471-489)."""
+    _fields_ = [('work', c_vp), ('rows', c_vp), ('n', c_i64), ('D', c_i64), ('K', ctypes.c_int),
+                ('nseg', ctypes.c_int), ('seg_end', c_i64 * 16), ('seg_kind', ctypes.c_int * 16),
+                ('seg_aux', c_i64 * 16), ('seed', c_u32), ('bound', c_f32), ('L_ids', c_vp), ('L_steps', c_vp),
+                ('L_cnt', c_vp), ('nL', c_i64), ('logs', c_vp), ('nlogs', c_i64), ('table', c_vp), ('recip', c_vp),
+                ('table_rows', c_i64), ('mat', c_vp), ('mat_rows', c_i64), ('loc', c_vp), ('R', c_i64)]
 
 
 def lib():

@@ -23,7 +23,7 @@ __global__ __launch_bounds__(256) void k_adam_rows_v4(float* __restrict__ state,
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t i = wave * rpw + (lane >> lg); i < n; i += nwave * rpw) {
-    const int64_t slot = (int64_t)slots[i];
+    const int64_t slot = slots ? (int64_t)slots[i] : i;
     if (slot < 0 || slot >= C) continue;
     float4* rec = reinterpret_cast<float4*>(state) + slot * 3 * (int64_t)nchunk;
     const float4* g = reinterpret_cast<const float4*>(grad) + i * (int64_t)nchunk;
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void k_adam_rows_scalar(float* __restrict__ st
   const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   const int64_t nwave = ((int64_t)gridDim.x * blockDim.x) >> 6;
   for (int64_t i = wave; i < n; i += nwave) {
-    const int64_t slot = (int64_t)slots[i];
+    const int64_t slot = slots ? (int64_t)slots[i] : i;
     if (slot < 0 || slot >= C) continue;
     float* w = state + slot * 3 * D;
     const float* g = grad + i * D;
@@ -73,8 +73,8 @@ __global__ __launch_bounds__(256) void k_adam_rows_scalar(float* __restrict__ st
 
 template <int VPL, typename Idx, int U>
 __global__ __launch_bounds__(256) void k_adam_rows_wpr(float* __restrict__ state, int64_t C,
-                                                       const Idx* __restrict__ slots, const float* __restrict__ grad,
-                                                       int64_t n, AdamScalars s) {
+                                                       const Idx* __restrict__ slots, int64_t base,
+                                                       const float* __restrict__ grad, int64_t n, AdamScalars s) {
   constexpr int64_t D = 64 * VPL;
   const int lane = threadIdx.x & 63;
   const int64_t i0 = wave_id() * U;
@@ -83,7 +83,7 @@ __global__ __launch_bounds__(256) void k_adam_rows_wpr(float* __restrict__ state
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t i = i0 + u;
-    sl[u] = i < n ? (int64_t)slots[i] : -1;
+    sl[u] = i < n ? (slots ? (int64_t)slots[i] : base + i) : -1;
     if (sl[u] >= C) sl[u] = -1;
     if (sl[u] >= 0) {
       const float* rec = state + sl[u] * 3 * D + lane * VPL;
@@ -112,8 +112,8 @@ static void launch_adam_wpr(float* state, int64_t C, const Idx* slots, const flo
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
-    k_adam_rows_wpr<VPL, Idx, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(state, C, slots + a,
-                                                                                               grad + a * D, m, s);
+    k_adam_rows_wpr<VPL, Idx, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(
+        state, C, slots ? slots + a : nullptr, a, grad + a * D, m, s);
   }
 }
 
@@ -176,7 +176,7 @@ extern "C" int elr_adam_rows(float* state, int64_t C, const void* slots, int idx
                              int64_t D, const float sc[8], void* stream) {
   if (n < 0 || D <= 0 || C < 0 || !sc) return ELR_EINVAL;
   if (n == 0) return ELR_OK;
-  if (!state || !slots || !grad) return ELR_EINVAL;
+  if (!state || !grad) return ELR_EINVAL;   // slots == NULL: row i of grad updates state row i
   const elr::AdamScalars s = elr::make_scalars(sc);
   hipStream_t st = (hipStream_t)stream;
   if (idx64) return elr::launch_adam(state, C, (const int64_t*)slots, grad, n, D, s, st);

@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
   for (int64_t u = wave_id(); u < U; u += wave_count()) {
     const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
     const int64_t L = s1 - s0;
-    const int64_t row = uniq[u];
+    const int64_t row = uniq ? uniq[u] : u;   // NULL: segment u goes to row u
     float acc[NQ];
     chunk_sum<NQ>(grad, D, sv, s0, L < kSegChunk ? s1 : s0 + kSegChunk, acc);
     const int64_t extra = (L - 1) / kSegChunk;
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
     ok[q] = u < U;
     s0[q] = ok[q] ? seg_start[u] : 0;
     len[q] = ok[q] ? seg_start[u + 1] - s0[q] : 0;
-    row[q] = ok[q] ? uniq[u] : -1;
+    row[q] = ok[q] ? (uniq ? uniq[u] : u) : -1;   // NULL: segment u goes to row u
     o0[q] = ok[q] ? (int64_t)seg_occ0[u] : 0;
     ok[q] = ok[q] && row[q] >= 0 && row[q] < nrows;
   }
@@ -650,5 +650,52 @@ extern "C" int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const
                            : dedup_core<uint64_t>(ids, n, kb, S, nullptr, nullptr, st);
   chunk_plan(n, S, st);
   const int rc = seg_reduce_d<1>(grad, D, S.vals[cur], S, S.uniq, n, state, C, s, st);
+  return rc != ELR_OK ? rc : launch_status();
+}
+
+// ---- dedup plan: one sort per batch, reused by the segment sum -------------------------------------------------
+// elr_dedup_plan sorts the batch and finds its segments exactly as elr_unique does, and also lays out the extra
+// chunks; the scratch then holds the plan (sorted positions, segment starts, first occurrences, chunk plan, U).
+// elr_segment_sum_plan sums a gradient batch over that plan without sorting again.  The sorted result lives in the
+// scratch buffer that the last radix pass wrote: with p passes, buffer (p - 1) % 2.
+static int plan_result_buffer(int key_bits) { return ((key_bits + 7) / 8 - 1) % 2; }
+
+extern "C" int64_t elr_dedup_plan_bytes(int64_t n, int64_t D) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || D < 1) return ELR_EINVAL;
+  return dedup_scratch_bytes(n, D, nullptr, nullptr);
+}
+
+extern "C" int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, int64_t* inverse,
+                              int64_t* n_unique, void* plan, int64_t plan_bytes, int64_t D, void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || key_bits < 1 || key_bits > 64 || D < 1) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!ids || !uniq || !n_unique || !plan) return ELR_EINVAL;
+  DedupScratch S;
+  if (plan_bytes < dedup_scratch_bytes(n, D, &S, plan)) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  const int cur = key_bits <= 32 ? dedup_core<uint32_t>(ids, n, key_bits, S, uniq, inverse, st)
+                                 : dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, st);
+  if (cur != plan_result_buffer(key_bits)) return ELR_EINVAL;
+  chunk_plan(n, S, st);
+  hipError_t e = hipMemcpyAsync(n_unique, S.d_tot, sizeof(int64_t), hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) return (int)e;
+  return launch_status();
+}
+
+extern "C" int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                                    int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows,
+                                    void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || D < 1 || key_bits < 1 || key_bits > 64 || out_rows < 0) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!grad || !plan || !out) return ELR_EINVAL;
+  if (D > 512) return ELR_EUNSUPPORTED;
+  DedupScratch S;
+  if (plan_bytes < dedup_scratch_bytes(n, D, &S, const_cast<void*>(plan))) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  const AdamScalars none{};
+  const int rc = seg_reduce_d<0>(grad, D, S.vals[plan_result_buffer(key_bits)], S, perm, n, out, out_rows, none, st);
   return rc != ELR_OK ? rc : launch_status();
 }

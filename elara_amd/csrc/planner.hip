@@ -9,10 +9,11 @@
 //     (the slot holds a row the pipeline needs, elara.py:227-229), expired when last_seen[r] <= s (the row's TTL is
 //     over, elara.py:231-233); class 0 = expired and unprotected, 1 = unprotected (preemptible), 2 = protected.
 //
-// Outputs: the positions of u sorted stably by class (`order`), the dynamic slots partitioned stably by class
-// ([class 0 | class 1 | class 2] and [class 0 | classes 1, 2 in dyn order], so that the evicted and kept slots of
-// both the plain and the preempting plan are contiguous slices), per-position flags, slots and codes, and a small
-// block of counts for the host: 10 class counts, the 3 dynamic-slot counts, mat_top and log_top.
+// Outputs: the positions of u sorted stably by class rank (`order`, and its inverse `rank`), the dynamic slots
+// partitioned stably by class ([class 0 | class 1 | class 2] and [class 0 | classes 1, 2 in dyn order], so that the
+// evicted and kept slots of both the plain and the preempting plan are contiguous slices), per-position flags, slots
+// and codes, and a small block of counts for the host: 10 class counts, the 3 dynamic-slot counts, mat_top and
+// log_top.
 //
 // A dynamic slot is protected in the reference when slot_of[un] == d for a row un of the next batches; every
 // occupied dynamic slot satisfies slot_of[slot_row[d]] == d, so the test here is the membership of slot_row[d] in
@@ -26,6 +27,13 @@ constexpr int kNumCls = 10;     // HIT, NADM, NAPP, NCMP, LADM, LAPP, LCMP, FADM
 constexpr int kDynCh = 4;       // expired, preemptible, protected, not expired (= preemptible + protected)
 
 enum : int { kHit = 0, kNAdm, kNApp, kNCmp, kLAdm, kLApp, kLCmp, kFAdm, kFNAdm, kS };
+
+// Position of each class in `order` (the class rank): hits, then the admitted N, L and F rows, the N and L appends,
+// the N and L compactions, the transient F rows and the S rows.  Each group the executor treats alike -- the
+// admissions (ascending N, L, F as the reference concatenates them, srm2/elara.py:345-350), the appends and the
+// compactions (srm2/elara.py:379-386) -- is then one contiguous range.
+__constant__ int kRankOf[kNumCls] = {0, 1, 4, 6, 2, 5, 7, 3, 8, 9};
+__constant__ int kClsOfRank[kNumCls] = {kHit, kNAdm, kLAdm, kFAdm, kNApp, kLApp, kNCmp, kLCmp, kFNAdm, kS};
 
 __device__ __forceinline__ bool sorted_has(const int64_t* __restrict__ a, int64_t n, int64_t x) {
   int64_t lo = 0, hi = n;   // first index with a[idx] >= x
@@ -128,7 +136,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_pl
     int k = -1;
     if (i < p.n) {
       const RowClass rc = classify_row(p, p.u[i]);
-      k = rc.cls;
+      k = kRankOf[rc.cls];
       o.cls[i] = (int8_t)rc.cls;
       o.flags[i] = (uint8_t)rc.flags;
       o.sl[i] = rc.sl;
@@ -159,7 +167,7 @@ __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_pla
   scan_channels_block(bu, nbu, kNumCls, tot);
   scan_channels_block(bd, nbd, kDynCh, tot + kNumCls);
   __syncthreads();
-  if (threadIdx.x < kNumCls) o.counts[threadIdx.x] = tot[threadIdx.x];
+  if (threadIdx.x < kNumCls) o.counts[kClsOfRank[threadIdx.x]] = tot[threadIdx.x];
   if (threadIdx.x < 3) o.counts[kNumCls + threadIdx.x] = tot[kNumCls + threadIdx.x];
   if (threadIdx.x == 0) {
     o.counts[13] = p.mat_top ? *p.mat_top : 0;
@@ -176,13 +184,15 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
   const int64_t b = blockIdx.x;
   if (b < nbu) {
     const int64_t i = b * kPlanBlock + threadIdx.x;
-    const int k = i < p.n ? (int)o.cls[i] : -1;
+    const int k = i < p.n ? kRankOf[(int)o.cls[i]] : -1;
     int t[kNumCls];
     const int r = block_class_rank<kNumCls>(k, t);
     if (k >= 0) {
       int64_t base = 0;
       for (int q = 0; q < k; ++q) base += tot[q];
-      o.order[base + bu[(int64_t)k * nbu + b] + r] = i;
+      const int64_t pos = base + bu[(int64_t)k * nbu + b] + r;
+      o.order[pos] = i;
+      if (o.rank) o.rank[i] = pos;
     }
   } else {
     const int64_t bb = b - nbu;
@@ -204,6 +214,29 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
 }
 
 inline int64_t plan_blocks(int64_t m) { return (m + kPlanBlock - 1) / kPlanBlock; }
+
+// Admissions of one step (srm2/elara.py:352-367): row adm_rows[i] takes pool slot adm_slots[i]; the first lazy_n
+// rows are N/L rows (they keep their code as c0 and, with evl, start a resident history whose step 0 is s), the rest
+// are F rows (c0 = -1).
+__global__ __launch_bounds__(kPlanBlock) void k_plan_admit(const int64_t* __restrict__ adm_rows,
+                                                           const int64_t* __restrict__ adm_slots, int64_t n_adm,
+                                                           int64_t lazy_n, int evl, int64_t s, int64_t n0, int64_t C,
+                                                           int64_t R, int K, const int8_t* __restrict__ code,
+                                                           int32_t* __restrict__ slot_of, int64_t* __restrict__ slot_row,
+                                                           int8_t* __restrict__ adm_c0, int8_t* __restrict__ rj,
+                                                           int8_t* __restrict__ rok, int32_t* __restrict__ pstep) {
+  const int64_t i = (int64_t)blockIdx.x * kPlanBlock + threadIdx.x;
+  if (i >= n_adm) return;
+  const int64_t r = adm_rows[i], a = adm_slots[i];
+  if (r < 0 || r >= R || a < n0 || a >= C) return;
+  const bool il = i < lazy_n, lazy = il && evl;
+  slot_of[r] = (int32_t)a;
+  slot_row[a] = r;
+  adm_c0[a] = il ? code[r] : (int8_t)-1;
+  rj[a] = lazy ? 1 : 0;
+  rok[a] = lazy ? 1 : 0;
+  if (lazy) pstep[(a - n0) * K] = (int32_t)s;
+}
 
 }  // namespace elr
 
@@ -236,5 +269,20 @@ extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out,
   if (nbu + nbd > 0) k_plan_count<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd);
   k_plan_scan<<<1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
   if (nbu + nbd > 0) k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
+  return launch_status();
+}
+
+extern "C" int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots, int64_t n_adm, int64_t lazy_n, int evl,
+                              int64_t s, int64_t n0, int64_t C, int64_t R, int K, const int8_t* code, int32_t* slot_of,
+                              int64_t* slot_row, int8_t* adm_c0, int8_t* rj, int8_t* rok, int32_t* pstep,
+                              void* stream) {
+  using namespace elr;
+  if (n_adm < 0 || lazy_n < 0 || lazy_n > n_adm || n0 < 0 || n0 > C || K < 1 || R < 0) return ELR_EINVAL;
+  if (n_adm == 0) return ELR_OK;
+  if (!adm_rows || !adm_slots || !code || !slot_of || !slot_row || !adm_c0 || !rj || !rok || !pstep) return ELR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  k_plan_admit<<<(unsigned)plan_blocks(n_adm), kPlanBlock, 0, st>>>(adm_rows, adm_slots, n_adm, lazy_n, evl, s, n0, C,
+                                                                     R, K, code, slot_of, slot_row, adm_c0, rj, rok,
+                                                                     pstep);
   return launch_status();
 }

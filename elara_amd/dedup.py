@@ -1,6 +1,9 @@
 """Batch dedup and duplicate-id gradient reduction on the GPU -- the step before Adam on every batch.
 
     unique(ids) -> (u, inv)                       torch.unique(ids, return_inverse=True), srm2/train.py:352
+    unique_plan(ids, D) -> (u, plan); segment_sum_plan(grad, plan, out, perm)
+                                                  the same dedup sorted once per batch: the segment sum of the
+                                                  backward reuses the sort of the unique
     embedding_dense_backward(grad, inv, num_weights, padding_idx=-1, scale_grad_by_freq=False) -> [num_weights, D]
                                                   aten.embedding_dense_backward as srm2/train.py:429 calls it
     adam_dedup(pool, ids, grad, lr, b1, b2, eps, step)
@@ -42,27 +45,93 @@ def _bits(bound):
     return b
 
 
-def unique(ids):
+def _key_bits(flat, bound):
+    if bound is not None:
+        return _bits(int(bound))
+    lo, hi = torch.aminmax(flat)
+    lo, hi = int(lo), int(hi)
+    if lo < 0:
+        raise RuntimeError('unique: ids must be non-negative')
+    return _bits(hi + 1)
+
+
+def unique(ids, bound=None):
     """Sorted unique values of `ids` (int32/int64, >= 0) and the inverse, as torch.unique(ids, sorted=True,
-    return_inverse=True) returns them (int64).  Synchronises once to size the output, as torch.unique does."""
+    return_inverse=True) returns them (int64).  Synchronises once to size the output, as torch.unique does.  With
+    `bound` (every id < bound, the caller's guarantee) the key width comes from it instead of a min/max pass and
+    its synchronisation."""
     flat = _ids(ids)
     n = flat.numel()
     dev = flat.device
     inv = torch.empty(ids.shape, dtype=I64, device=dev)
     if n == 0:
         return torch.empty(0, dtype=I64, device=dev), inv
-    lo, hi = torch.aminmax(flat)
-    lo, hi = int(lo), int(hi)
-    if lo < 0:
-        raise RuntimeError('unique: ids must be non-negative')
+    kb = _key_bits(flat, bound)
     u = torch.empty(n, dtype=I64, device=dev)
     nu = torch.empty(1, dtype=I64, device=dev)
     scratch, nbytes = _scratch(dev, n, 1)
     with torch.cuda.device(dev):
-        rc = _lib.lib().elr_unique(_lib.ptr(flat), n, _bits(hi + 1), _lib.ptr(u), _lib.ptr(inv), _lib.ptr(nu),
+        rc = _lib.lib().elr_unique(_lib.ptr(flat), n, kb, _lib.ptr(u), _lib.ptr(inv), _lib.ptr(nu),
                                    _lib.ptr(scratch), nbytes, _lib.stream_of(flat))
     _lib.check(rc, 'elr_unique')
     return u[:int(nu)], inv
+
+
+class DedupPlan:
+    """One batch's sort and segment layout (elr_dedup_plan), kept for elr_segment_sum_plan."""
+    __slots__ = ('buf', 'nbytes', 'n', 'D', 'key_bits', 'U')
+
+
+def unique_plan(ids, D, bound=None):
+    """unique(ids) without the inverse, keeping the sort as a plan for segment_sum_plan over gradients of width D:
+    returns (u, plan)."""
+    flat = _ids(ids)
+    n = flat.numel()
+    dev = flat.device
+    plan = DedupPlan()
+    plan.n, plan.D, plan.U = n, int(D), 0
+    plan.buf, plan.nbytes, plan.key_bits = None, 0, 1
+    if n == 0:
+        return torch.empty(0, dtype=I64, device=dev), plan
+    plan.key_bits = _key_bits(flat, bound)
+    nbytes = int(_lib.lib().elr_dedup_plan_bytes(n, int(D)))
+    if nbytes < 0:
+        _lib.check(nbytes, 'elr_dedup_plan_bytes')
+    plan.buf, plan.nbytes = torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
+    u = torch.empty(n, dtype=I64, device=dev)
+    nu = torch.empty(1, dtype=I64, device=dev)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_dedup_plan(_lib.ptr(flat), n, plan.key_bits, _lib.ptr(u), None, _lib.ptr(nu),
+                                       _lib.ptr(plan.buf), nbytes, int(D), _lib.stream_of(flat))
+    _lib.check(rc, 'elr_dedup_plan')
+    plan.U = int(nu)
+    return u[:plan.U], plan
+
+
+def segment_sum_plan(grad, plan, out=None, perm=None):
+    """Per-segment sums of grad [n, D] over a unique_plan: segment u into row perm[u] (or u) of out [rows, D]
+    (allocated [U, D] when None), in the fixed summation order of embedding_dense_backward."""
+    n, D = plan.n, plan.D
+    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.numel() == n * D):
+        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements')
+    dev = grad.device
+    if out is None:
+        out = torch.empty(plan.U, D, dtype=torch.float32, device=dev)
+    if not (out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and out.dim() == 2
+            and out.shape[1] == D):
+        raise RuntimeError(f'out must be a contiguous cuda float32 tensor [rows, {D}]')
+    if perm is not None:
+        if perm.dtype != I64 or not perm.is_cuda or perm.numel() < plan.U:
+            raise RuntimeError('perm must be a cuda int64 tensor with one row per segment')
+        perm = perm.contiguous()
+    if n == 0:
+        return out
+    g = grad.reshape(n, D).contiguous()
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_segment_sum_plan(_lib.ptr(g), n, D, plan.key_bits, _lib.ptr(plan.buf), plan.nbytes,
+                                             _lib.ptr(perm), _lib.ptr(out), out.shape[0], _lib.stream_of(g))
+    _lib.check(rc, 'elr_segment_sum_plan')
+    return out
 
 
 def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1, scale_grad_by_freq=False):

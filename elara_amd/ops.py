@@ -62,3 +62,20 @@ def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
         rc = L.elr_adam_rows(_lib.ptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
                              _lib.ptr(grad), n, D, s, _lib.stream_of(pool))
     _lib.check(rc, 'elr_adam_rows')
+
+
+def adam_rows_dense(state, grad, lr, b1, b2, eps, step):
+    """state [n,3,D] cuda float32 (contiguous; updated in place) with grad [n,D], row i by row i (elr_adam_rows with
+    no slot list: the executor's contiguous work arrays)."""
+    n = state.shape[0]
+    if n == 0:
+        return
+    _check_state(state, 'state')
+    D = state.shape[2]
+    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.device == state.device and grad.numel() == n * D):
+        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {state.device}')
+    grad = grad.contiguous()
+    s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
+    with torch.cuda.device(state.device):
+        rc = _lib.lib().elr_adam_rows(_lib.ptr(state), n, None, 1, _lib.ptr(grad), n, D, s, _lib.stream_of(state))
+    _lib.check(rc, 'elr_adam_rows')

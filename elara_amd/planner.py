@@ -18,7 +18,7 @@ F_HIT, F_N, F_L, F_APP, F_ADMIT, F_NEXT = 1, 2, 4, 8, 16, 32
 # counts[16]: 10 class counts, then these
 CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP = 10, 11, 12, 13, 14
 
-PlanClass = namedtuple('PlanClass', 'cls flags sl c order dyn_out counts')
+PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts')
 
 
 def _dev_i64(t, dev):
@@ -31,7 +31,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
     them: slot_of int32 [R], last_seen int32 [R], code int8 [R], kthr int8 [T], toff int64 [T], slot_row int64 [C],
     mat_top / log_top int64 [1].  Returns PlanClass(cls int8 [n], flags uint8 [n], sl int32 [n], c int8 [n],
-    order int64 [n], dyn_out int64 [2 nd], counts int64 [16] on the device)."""
+    order int64 [n] (positions by class rank), rank int64 [n] (its inverse), dyn_out int64 [2 nd], counts int64 [16]
+    on the device)."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -48,8 +49,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     n, nd = u.numel(), dyn.numel()
     out = PlanClass(torch.empty(n, dtype=I8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev),
                     torch.empty(n, dtype=I32, device=dev), torch.empty(n, dtype=I8, device=dev),
-                    torch.empty(n, dtype=I64, device=dev), torch.empty(2 * nd, dtype=I64, device=dev),
-                    torch.empty(16, dtype=I64, device=dev))
+                    torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
+                    torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(16, dtype=I64, device=dev))
     p = _lib.ptr
     pin = _lib.PlanIn()
     pin.u, pin.n = u.data_ptr(), n
@@ -85,3 +86,26 @@ def classify_from_flags(flags, admit, want_t):
     cls = torch.where(isL, torch.where(admit, t8(C_LADM), torch.where(app, t8(C_LAPP), t8(C_LCMP))), cls)
     cls = torch.where(isN, torch.where(admit, t8(C_NADM), torch.where(app, t8(C_NAPP), t8(C_NCMP))), cls)
     return torch.where(hit, t8(C_HIT), cls)
+
+
+def plan_admit(adm_rows, adm_slots, lazy_n, evl, s, n0, C, R, K, code, slot_of, slot_row, adm_c0, rj, rok, pstep):
+    """Admissions of one step (elr_plan_admit, srm2/elara.py:352-367): row adm_rows[i] takes pool slot
+    adm_slots[i]; the first lazy_n rows are N/L rows."""
+    n = adm_rows.numel()
+    if adm_slots.numel() != n:
+        raise RuntimeError('plan_admit: one slot per admitted row')
+    if n == 0:
+        return
+    dev = code.device
+    rows = _dev_i64(adm_rows, dev)
+    slots = _dev_i64(adm_slots, dev)
+    for t, dt, name in ((code, I8, 'code'), (slot_of, I32, 'slot_of'), (slot_row, I64, 'slot_row'),
+                        (adm_c0, I8, 'adm_c0'), (rj, I8, 'rj'), (rok, I8, 'rok'), (pstep, I32, 'pstep')):
+        if t.dtype != dt or t.device != dev or not t.is_contiguous():
+            raise RuntimeError(f'plan_admit: {name} must be a contiguous {dt} tensor on {dev}')
+    p = _lib.ptr
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_plan_admit(p(rows), p(slots), n, int(lazy_n), int(bool(evl)), int(s), int(n0), int(C),
+                                       int(R), int(K), p(code), p(slot_of), p(slot_row), p(adm_c0), p(rj), p(rok),
+                                       p(pstep), _lib.stream_of(code))
+    _lib.check(rc, 'elr_plan_admit')

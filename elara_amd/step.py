@@ -13,25 +13,47 @@ compacted, log appends, transient Adam of M rows).  The dense model is not part 
 the per-occurrence gradients, which are reduced per unique row (dedup + fixed-order segment sum) as the reference's
 embedding backward does (srm2/train.py:352, 429).
 
-Planner classification uses torch ops on the device, as the reference's does, with one host synchronisation per
-plan for the class counts (elara.py:242).  The hot-path kernels come from a backend object (HipBackend: this
-library's HIP kernels), so the same step can be driven by another implementation of the kernels for comparison.
+Layout.  The planner sorts the batch's unique rows by class rank (hits; admitted N, L, F; appended N, L; compacted
+N, L; transient F; S), so each group the executor treats alike is one contiguous range: the fused assembly writes
+the non-resident rows' full states into one work array in that order, the segment sum writes the per-row gradients
+in that order, and the update is a few Adam calls and row copies over contiguous ranges.  The batch is sorted once
+(the dedup plan of `unique`), and the segment sum reuses that sort.
+
+Classification, admissions and assembly are HIP kernels; the remaining glue is a few torch ops per step.  The
+plan synchronises with the host once (class counts, elara.py:242), plus once more on the rare overflow path.  The
+hot-path kernels come from a backend object (HipBackend: this library's HIP kernels), so the same step can be
+driven by another implementation of the kernels (the oracle's) for comparison.
 """
 import torch
 
 from . import _lib  # noqa: F401  (the library must be present)
-from .dedup import embedding_dense_backward, unique
+from .assemble import assemble_rows
+from .dedup import segment_sum_plan, unique_plan
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
-from .ops import gpu_adam
+from .ops import adam_rows_dense, gpu_adam
 from .planner import (CNT_EXP, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
-                      plan_classify)
+                      plan_admit, plan_classify)
 from .rows import copy_rows
 
 I8, I32, I64 = torch.int8, torch.int32, torch.int64
 # classes (srm2/elara.py:31-32): hit, N admitted / append / compact, L admitted / append / compact, F admitted /
 # not admitted, S
 C_HIT, C_NADM, C_NAPP, C_NCMP, C_LADM, C_LAPP, C_LCMP, C_FADM, C_FNADM, C_S = range(10)
+# class ranks: the order of the planner's `order` (elr_plan_classify), which makes the admissions (N, L, F), the
+# appends (N, L) and the compactions (N, L) contiguous
+R_HIT, R_NADM, R_LADM, R_FADM, R_NAPP, R_LAPP, R_NCMP, R_LCMP, R_FN, R_S = range(10)
+RANK_CLASSES = (C_HIT, C_NADM, C_LADM, C_FADM, C_NAPP, C_LAPP, C_NCMP, C_LCMP, C_FNADM, C_S)
+ASM_INIT, ASM_REPLAY, ASM_GATHER = 0, 1, 2
+
+
+def rank_order(cls):
+    """Positions sorted stably by class rank, and the inverse (the planner's overflow path)."""
+    lut = torch.tensor([RANK_CLASSES.index(c) for c in range(10)], dtype=I8, device=cls.device)
+    order = torch.argsort(lut[cls.long()], stable=True)
+    rank = torch.empty_like(order)
+    rank[order] = torch.arange(order.numel(), device=cls.device)
+    return order, rank
 
 
 class HipBackend:
@@ -42,14 +64,24 @@ class HipBackend:
         self.table = ScalarTable(*hp, max_step, device)
         self.dx = dir_ext()
 
-    def unique(self, ids):
-        return unique(ids)
+    def unique(self, ids, bound=None):
+        return unique_plan(ids, self.D, bound)
 
     def plan_classify(self, *args):
         return plan_classify(*args)
 
-    def segsum(self, g_occ, inv, U):
-        return embedding_dense_backward(g_occ, inv, U)
+    def plan_admit(self, *args):
+        plan_admit(*args)
+
+    def segsum(self, g_occ, dplan, U, perm=None):
+        return segment_sum_plan(g_occ, dplan, torch.empty(U, self.D, device=g_occ.device), perm)
+
+    def assemble(self, rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K):
+        return assemble_rows(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K, self.D, self.seed, self.bound,
+                             self.table)
+
+    def adam_dense(self, state, grad, s):
+        adam_rows_dense(state, grad, *self.hp, s)
 
     def dir_a(self, st, pv, hs, L_row, L_cnt, ev_slot, s):
         return self.dx.elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s)
@@ -194,6 +226,7 @@ class ElaraStep:
             self.stats['preempt'] += take
         else:
             ev_slot, keep_dyn = pc.dyn_out[:n_exp], pc.dyn_out[nd + n_exp:]
+        rank = pc.rank
         if need > 0:   # overflow: un-admit (non-carry first) and recount
             admit = (pc.flags & F_ADMIT) != 0
             in_next = (pc.flags & F_NEXT) != 0
@@ -205,107 +238,86 @@ class ElaraStep:
             n_adm -= need
             cls = classify_from_flags(pc.flags, admit, self.st_mode == 'T')
             counts = self._host(*torch.bincount(cls.long(), minlength=10))
-            order = torch.argsort(cls, stable=True)
-        b_ = [0]
-        for x in counts:
-            b_.append(b_[-1] + x)
-        rng = lambda lo, hi: order[b_[lo]:b_[hi + 1]]  # noqa: E731
-        p = Plan()
-        p.s, p.u, p.n = s, u, n
-        hp_ = rng(C_HIT, C_HIT)
-        p.hit_pos, p.hit_slot = hp_, sl[hp_].long()
-        Npos, Lpos, Fpos, Spos = rng(C_NADM, C_NCMP), rng(C_LADM, C_LCMP), rng(C_FADM, C_FNADM), rng(C_S, C_S)
-        p.N_pos, p.N_row = Npos, u[Npos]
-        p.L_pos, p.L_row, p.L_cnt = Lpos, u[Lpos], c[Lpos].to(I32)
-        p.F_pos, p.F_row, p.S_pos, p.S_row = Fpos, u[Fpos], Spos, u[Spos]
+            order, rank = rank_order(cls)
+        # class-rank bounds: positions b[r] .. b[r+1] of `order` hold the rows of rank r
+        b = [0]
+        for cl in RANK_CLASSES:
+            b.append(b[-1] + counts[cl])
         nNa, nNp, nNc, nLa, nLp, nLc, nFa, nFn = counts[1:9]
+        p = Plan()
+        p.s, p.u, p.n, p.b, p.order, p.rank = s, u, n, b, order, rank
         p.counts = counts
+        u_ord = u[order]
+        c_ord = c[order]
+        p.u_ord = u_ord
+        p.hit_slot = sl[order[b[R_HIT]:b[R_HIT + 1]]].long()
+        rs = lambda r0, r1: slice(b[r0], b[r1 + 1])  # noqa: E731
+        # L rows in the reference's order (admitted, append, compact) for the directory's replay inputs
+        Ls = (rs(R_LADM, R_LADM), rs(R_LAPP, R_LAPP), rs(R_LCMP, R_LCMP))
+        p.L_row = torch.cat([u_ord[x] for x in Ls])
+        p.L_cnt = torch.cat([c_ord[x] for x in Ls]).to(I32)
+        p.nL = (nLa, nLp, nLc)
         st, pv = self.state_list(), self.params()
         (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots,
          p.ev_dyn) = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s)
         p.ev_slot = ev_slot
         nev = ev_slot.numel()
-        # admissions (srm2/elara.py:345-367)
+        # admissions (srm2/elara.py:345-367): admitted N, L, F rows take slots from the free stack's top
         pool_free = torch.cat([self.free, ev_slot])
         nf = self.n_free + nev
         adm_slots = pool_free[nf - n_adm:]
         self.free = pool_free[:nf - n_adm]
         self.n_free = nf - n_adm
-        adm_rows = torch.cat([p.N_row[:nNa], p.L_row[:nLa], p.F_row[:nFa]])
-        ar = lambda a_, b2: torch.arange(a_, b2, device=d)  # noqa: E731
-        ix = {'N_adm': ar(0, nNa), 'N_app': ar(nNa, nNa + nNp), 'N_cmp': ar(nNa + nNp, nNa + nNp + nNc),
-              'L_adm': ar(0, nLa), 'L_app': ar(nLa, nLa + nLp), 'L_cmp': ar(nLa + nLp, nLa + nLp + nLc),
-              'F_adm': ar(0, nFa), 'F_nadm': ar(nFa, nFa + nFn)}
-        ix['N_upd'] = torch.cat([ix['N_adm'], ix['N_cmp']])
-        ix['L_upd'] = torch.cat([ix['L_adm'], ix['L_cmp']])
-        ix['N_adm_slot'] = adm_slots[:nNa]
-        ix['L_adm_slot'] = adm_slots[nNa:nNa + nLa]
-        ix['F_adm_slot'] = adm_slots[nNa + nLa:]
-        p.ix = ix
-        p.L_off = torch.cumsum(p.L_cnt.long(), 0) - p.L_cnt.long()
+        p.adm_slots = adm_slots
         lazy_n = nNa + nLa
-        p.adm_rec_dyn = adm_slots[:lazy_n] - self.n0
-        if n_adm:
-            self.slot_of[adm_rows] = adm_slots.to(I32)
-            self.slot_row[adm_slots] = adm_rows
-            c_adm = self.code[adm_rows].to(I64)
-            isIL = torch.cat([torch.ones(lazy_n, dtype=torch.bool, device=d),
-                              torch.zeros(nFa, dtype=torch.bool, device=d)])
-            lazy_adm = isIL & self.evl
-            self.adm_c0[adm_slots] = torch.where(isIL, c_adm, torch.full_like(c_adm, -1)).to(I8)
-            self.rj[adm_slots] = lazy_adm.to(I8)
-            self.rok[adm_slots] = lazy_adm.to(I8)
-            if lazy_n and self.evl:
-                self.pstep[p.adm_rec_dyn, 0] = s
+        p.lazy_n = lazy_n
+        if lazy_n and self.evl:
+            p.adm_rec_dyn = adm_slots[:lazy_n] - self.n0
+        self.be.plan_admit(u_ord[rs(R_NADM, R_FADM)], adm_slots, lazy_n, self.evl, s, self.n0, self.C, self.R, K,
+                           self.code, self.slot_of, self.slot_row, self.adm_c0, self.rj, self.rok, self.pstep)
         self.dyn_slots = torch.cat([keep_dyn, adm_slots])
-        # non-resident lazy rows: append (stay L) or compact (to M)
-        p.a_rows = torch.cat([p.N_row[nNa:nNa + nNp], p.L_row[nLa:nLa + nLp]])
-        a_k = torch.cat([torch.zeros(nNp, dtype=I64, device=d), p.L_cnt[nLa:nLa + nLp].long()])
-        p.c_rows = torch.cat([p.N_row[nNa + nNp:], p.L_row[nLa + nLp:]])
-        c_cnt = torch.cat([torch.zeros(nNc, dtype=I64, device=d), p.L_cnt[nLa + nLp:].long()])
-        p.a_ids, p.c_slots = self.be.dir_b(st, pv, p.a_rows, a_k, p.c_rows, c_cnt, s)
-        p.F_slot = self.loc[p.F_row].to(I64)
-        p.S_slot = self.loc[p.S_row].to(I64)
+        # non-resident lazy rows: append (stay L, entry index = current count) or compact (to M)
+        p.a_ids, p.c_slots = self.be.dir_b(st, pv, u_ord[rs(R_NAPP, R_LAPP)], c_ord[rs(R_NAPP, R_LAPP)].long(),
+                                           u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)].long(), s)
+        p.FN_slot = self.loc[u_ord[rs(R_FN, R_FN)]].to(I64)
+        p.S_slot = self.loc[u_ord[rs(R_S, R_S)]].to(I64)
         st_ = self.stats
         st_['adm'] += n_adm
         st_['ev'] += nev
         st_['hits'] += counts[C_HIT]
-        st_['N'] += Npos.numel()
-        st_['L'] += Lpos.numel()
-        st_['F'] += Fpos.numel()
-        st_['S'] += Spos.numel()
+        st_['N'] += nNa + nNp + nNc
+        st_['L'] += nLa + nLp + nLc
+        st_['F'] += nFa + nFn
+        st_['S'] += counts[C_S]
         st_['compactions'] += nNc + nLc
         st_['appends'] += nNp + nLp
         return p
 
-    # ---- assemble (srm2/elara.py:471-489): states of the non-resident rows this step updates ----
+    # ---- assemble (srm2/elara.py:471-489): full states of the non-resident rows, one fused launch ----
     def assemble(self, p):
-        be, D, K = self.be, self.D, self.K
-        fullN = be.init_rows(p.N_row) if p.N_row.numel() else None
-        fullL = None
-        nL = p.L_row.numel()
-        if nL:
-            # the logged gradients of each L row, packed row by row (entry k of row i at L_off[i] + k)
-            kk = torch.arange(K, device=self.d)
-            valid = kk[None, :] < p.L_cnt.long()[:, None]
-            dst = torch.where(valid, p.L_off[:, None] + kk[None, :], torch.full_like(p.L_off[:, None], -1))
-            lg = torch.empty(nL * K, D, device=self.d)
-            be.copy_rows(lg, dst.reshape(-1), self.logs, p.L_ids.reshape(-1).to(I64))
-            fullL = be.replay(p.L_row, lg, p.L_off, p.L_steps, p.L_cnt, K)
-        ff = None
-        if p.F_row.numel():
-            ff = torch.empty(p.F_row.numel(), 3, D, device=self.d)
-            be.copy_rows(ff, None, self.mat, p.F_slot)
-        return fullN, fullL, ff
+        """Work array [b[R_S] - b[R_NADM], 3, D] in class-rank order: admitted N / L / F, appended N / L, compacted
+        N / L and transient F rows -- N rows by counter-hash init, L rows by replay of their log entries, F rows
+        from the MAT arena."""
+        b = p.b
+        w0 = b[R_NADM]
+        nLa, nLp, _ = p.nL
+        segs = [(b[r + 1] - w0, kind, aux) for r, kind, aux in (
+            (R_NADM, ASM_INIT, 0), (R_LADM, ASM_REPLAY, 0), (R_FADM, ASM_GATHER, 0), (R_NAPP, ASM_INIT, 0),
+            (R_LAPP, ASM_REPLAY, nLa), (R_NCMP, ASM_INIT, 0), (R_LCMP, ASM_REPLAY, nLa + nLp),
+            (R_FN, ASM_GATHER, 0))]
+        p.work = self.be.assemble(p.u_ord[w0:b[R_S]], segs, p.L_ids, p.L_steps, p.L_cnt, self.logs, self.mat,
+                                  self.loc, self.K)
 
     # ---- update (srm2/elara.py:491-542 and the host worker's writes 544-580, all in HBM) ----
-    def update(self, p, G, bufs):
-        be, s, D, K, ix = self.be, p.s, self.D, self.K, p.ix
-        fullN, fullL, ff = bufs
-        sel = lambda t, i: t.index_select(0, i)  # noqa: E731
+    def update(self, p, G):
+        """G [n, D]: the batch's per-row gradients in class-rank order (p.order)."""
+        be, s, D, K, b = self.be, p.s, self.D, self.K, p.b
         glog2 = self.glog.view(-1, D)
-        if p.hit_pos.numel():
-            gh = sel(G, p.hit_pos)
+        W, w0 = p.work, b[R_NADM]
+        rg = lambda r0, r1: G[b[r0]:b[r1 + 1]]  # noqa: E731
+        rw = lambda r0, r1: W[b[r0] - w0:b[r1 + 1] - w0]  # noqa: E731
+        if b[R_HIT + 1] > b[R_HIT]:
+            gh = rg(R_HIT, R_HIT)
             if self.evl:
                 be.copy_rows(glog2, p.hrec_dyn * K + p.hrec_j, gh)
             be.adam(self.pool, p.hit_slot, gh, s)
@@ -316,44 +328,33 @@ class ElaraStep:
             be.copy_rows(self.mat, p.evf_slots, self.pool, p.ev_slot)
             src = (p.ev_dyn.clamp(min=0, max=self.Cdyn)[:, None] * K + torch.arange(K, device=self.d)[None, :])
             be.copy_rows(self.logs, p.evl_ids.reshape(-1), glog2, src.reshape(-1))
-        adm_g = []
-        nNc = ix['N_cmp'].numel()
-        nNp = ix['N_app'].numel()
-        for X, full, pos in (('N', fullN, p.N_pos), ('L', fullL, p.L_pos)):
-            if full is None:
-                continue
-            up = ix[X + '_upd']
-            if up.numel():
-                be.adam(full, up, sel(G, sel(pos, up)), s)
-            if ix[X + '_adm'].numel():
-                be.copy_rows(self.pool, ix[X + '_adm_slot'], full, ix[X + '_adm'])
-                adm_g.append(sel(G, sel(pos, ix[X + '_adm'])))
-            if ix[X + '_cmp'].numel():
-                cs = p.c_slots[:nNc] if X == 'N' else p.c_slots[nNc:]
-                be.copy_rows(self.mat, cs, full, ix[X + '_cmp'])
-            if ix[X + '_app'].numel():
-                ai = p.a_ids[:nNp] if X == 'N' else p.a_ids[nNp:]
-                be.copy_rows(self.logs, ai, G, sel(pos, ix[X + '_app']))
-        if adm_g and self.evl:   # admission gradient = resident history entry 0
-            ag = torch.cat(adm_g) if len(adm_g) > 1 else adm_g[0]
-            be.copy_rows(glog2, p.adm_rec_dyn * K, ag)
-        if ff is not None:
-            be.adam(ff, torch.arange(p.F_row.numel(), device=self.d), sel(G, p.F_pos), s)
-            if ix['F_adm'].numel():
-                be.copy_rows(self.pool, ix['F_adm_slot'], ff, ix['F_adm'])
-            if ix['F_nadm'].numel():
-                be.copy_rows(self.mat, p.F_slot[ix['F_adm'].numel():], ff, ix['F_nadm'])
-        if p.S_row.numel():
-            be.adam(self.mat, p.S_slot, sel(G, p.S_pos), s)
+        # Adam on the admitted, compacted and transient work rows (appended rows only log their gradient)
+        if b[R_FADM + 1] > b[R_NADM]:
+            be.adam_dense(rw(R_NADM, R_FADM), rg(R_NADM, R_FADM), s)
+        if b[R_FN + 1] > b[R_NCMP]:
+            be.adam_dense(rw(R_NCMP, R_FN), rg(R_NCMP, R_FN), s)
+        if p.adm_slots.numel():
+            be.copy_rows(self.pool, p.adm_slots, rw(R_NADM, R_FADM))
+        if p.lazy_n and self.evl:   # admission gradient = resident history entry 0 of admitted N / L rows
+            be.copy_rows(glog2, p.adm_rec_dyn * K, rg(R_NADM, R_LADM))
+        if p.c_slots.numel():
+            be.copy_rows(self.mat, p.c_slots, rw(R_NCMP, R_LCMP))
+        if p.a_ids.numel():
+            be.copy_rows(self.logs, p.a_ids, rg(R_NAPP, R_LAPP))
+        if p.FN_slot.numel():
+            be.copy_rows(self.mat, p.FN_slot, rw(R_FN, R_FN))
+        if p.S_slot.numel():
+            be.adam(self.mat, p.S_slot, rg(R_S, R_S), s)
 
     # ---- one step from a batch's occurrence ids and gradients ----
-    def step(self, s, ids, g_occ, u, inv, u_nexts):
-        """Logical step s (1-based): ids int64 [O] (occurrences), g_occ [O, D] their gradients, (u, inv) the
-        batch's unique rows and inverse, u_nexts the unique rows of the next depth-1 batches."""
+    def step(self, s, ids, g_occ, u, dplan, u_nexts):
+        """Logical step s (1-based): ids int64 [O] (occurrences), g_occ [O, D] their gradients, u the batch's
+        unique rows and dplan its dedup plan (from be.unique), u_nexts the unique rows of the next depth-1
+        batches."""
         p = self.plan(s, u, u_nexts)
-        bufs = self.assemble(p)
-        G = self.be.segsum(g_occ, inv, u.numel())
-        self.update(p, G, bufs)
+        self.assemble(p)
+        G = self.be.segsum(g_occ, dplan, u.numel(), p.rank)
+        self.update(p, G)
         return p
 
     # ---- eval-style materialisation (srm2/elara.py:582-604) ----
@@ -398,12 +399,12 @@ def run(step, batches, grads, steps=None, on_step=None):
     assembles and updates.  batches[j]: int64 occurrence ids; grads(j) or grads[j]: [O_j, D] occurrence gradients.
     on_step(s, plan) is called after each step."""
     S = len(batches) if steps is None else steps
-    U, INV = {}, {}
+    U, PLANS = {}, {}
     dev = step.d
 
     def load(j):
-        u, inv = step.be.unique(batches[j].to(dev))
-        U[j], INV[j] = u, inv
+        u, dplan = step.be.unique(batches[j].to(dev), step.R)
+        U[j], PLANS[j] = u, dplan
         step.observe(j + 1, u)
 
     for j in range(min(S, step.L + 1)):
@@ -413,7 +414,7 @@ def run(step, batches, grads, steps=None, on_step=None):
             load(s + step.L + 1)
         u_nexts = [U[s + k] for k in range(1, step.depth) if s + k < S]
         g = grads(s) if callable(grads) else grads[s]
-        p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), INV.pop(s), u_nexts)
+        p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
         if on_step is not None:
             on_step(s + 1, p)
     step.check_capacity()

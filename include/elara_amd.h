@@ -60,6 +60,7 @@ int elr_scalar_recip(const float* table_host, int64_t table_rows, double* recip_
  * Replaces: srm2/ops.py:42-67 gpu_adam / _adam_rows.  For i < n: Adam(state[slots[i]], grad[i]) with the
  * scalars sc (host array, from elr_adam_scalars).  Slots must be unique within a call (as in the reference).
  *   state  device fp32 [C,3,D];  slots device int32 (idx64 = 0) or int64 (idx64 = 1) [n];  grad device [n,D].
+ *   slots == NULL (an extension): grad row i updates state row i (contiguous work arrays of the executor).
  * ------------------------------------------------------------------------------------------------------- */
 int elr_adam_rows(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n, int64_t D,
                   const float sc[8], void* stream);
@@ -176,13 +177,27 @@ int elr_segment_sum(const float* grad, const int64_t* idx, int64_t n, int64_t D,
 int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
                    const float sc[8], void* scratch, int64_t scratch_bytes, void* stream);
 
+/* Dedup plan (no counterpart in the reference; the reference sorts each batch twice, in torch.unique and in the
+ * embedding backward): elr_dedup_plan is elr_unique that keeps its sort -- sorted positions, segment starts, first
+ * occurrences, the chunk plan and U -- in `plan` (elr_dedup_plan_bytes(n, D) bytes, the width D of the gradients to
+ * be summed later).  elr_segment_sum_plan then sums a gradient batch grad [n, D] over that plan, segment u (the
+ * u-th smallest id) into out[perm ? perm[u] : u] (out_rows rows; rows out of range are skipped), in the same fixed
+ * order as elr_segment_sum.  key_bits must be the value given to elr_dedup_plan. */
+int64_t elr_dedup_plan_bytes(int64_t n, int64_t D);
+int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, int64_t* inverse, int64_t* n_unique,
+                   void* plan, int64_t plan_bytes, int64_t D, void* stream);
+int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan, int64_t plan_bytes,
+                         const int64_t* perm, float* out, int64_t out_rows, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Planner classification of one step: srm2/elara.py:214-267 (ELARAPlanner.plan up to the class counts) -- the
  * per-row class of the batch's unique rows, the stable class order, the expired / preemptible / protected split of
  * the dynamic pool slots, and the counts the host needs, in three launches.
  *
  * Classes (srm2/elara.py:31-32): 0 HIT, 1 N admitted, 2 N append, 3 N compact, 4 L admitted, 5 L append,
- * 6 L compact, 7 F admitted, 8 F not admitted (transient), 9 S.  A row hits when slot_of[u] >= 0; a missing row is
+ * 6 L compact, 7 F admitted, 8 F not admitted (transient), 9 S.  `order` sorts the positions stably by class rank:
+ * HIT, N admitted, L admitted, F admitted, N append, L append, N compact, L compact, F transient, S -- so the
+ * admissions, the appends and the compactions are contiguous ranges.  A row hits when slot_of[u] >= 0; a missing row is
  * admitted when last_seen[u] > s; N rows have code 0, L rows 1..K, F/S rows code K+1; "append" when
  * code < kthr[table]; F rows that are not admitted are transient with want_t, else S.
  * ------------------------------------------------------------------------------------------------------- */
@@ -220,7 +235,8 @@ typedef struct elr_plan_out {
   uint8_t* flags;             /* [n] ELR_PLAN_* bits */
   int32_t* sl;                /* [n] slot_of[u] */
   int8_t* c;                  /* [n] code[u] */
-  int64_t* order;             /* [n] positions sorted stably by class */
+  int64_t* order;             /* [n] positions sorted stably by class rank */
+  int64_t* rank;              /* [n] inverse of order (may be NULL) */
   int64_t* dyn_out;           /* [2 nd]: slots as [expired | preemptible | protected], then [expired | the rest],
                                  each part in dyn order */
   int64_t* counts;            /* [16] device: 10 class counts, expired, preemptible, protected, mat_top, log_top, 0 */
@@ -229,6 +245,60 @@ typedef struct elr_plan_out {
 int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd);
 int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
                       void* stream);
+
+/* Admissions of one step (srm2/elara.py:352-367): row adm_rows[i] takes dynamic pool slot adm_slots[i]
+ * (slot_of, slot_row); the first lazy_n rows are N/L rows (adm_c0 = their code; with evl their resident history
+ * starts: rj = rok = 1, pstep[slot - n0][0] = s), the others F rows (adm_c0 = -1, rj = rok = 0).  Rows or slots
+ * out of range are skipped. */
+int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots, int64_t n_adm, int64_t lazy_n, int evl,
+                   int64_t s, int64_t n0, int64_t C, int64_t R, int K, const int8_t* code, int32_t* slot_of,
+                   int64_t* slot_row, int8_t* adm_c0, int8_t* rj, int8_t* rok, int32_t* pstep, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Fused weight assembly: srm2/elara.py:471-489 (ELARAExecutor.assemble) -- the full states [n, 3, D] of the
+ * step's non-resident rows in one launch.  Work row k (row rows[k]) lies in segment g (positions
+ * [seg_end[g-1], seg_end[g])) of kind seg_kind[g]:
+ *   ELR_ASM_INIT    counter-hash initial state (as elr_init_rows);
+ *   ELR_ASM_REPLAY  initial state plus the row's logged Adam steps (as elr_replay_rows), entry q of L row
+ *                   j = seg_aux[g] + (k - seg_start) read from logs[L_ids[j*K + q]] at step L_steps[j*K + q] for
+ *                   q < L_cnt[j] (elr_dir_a's replay inputs);
+ *   ELR_ASM_GATHER  the state held in the MAT arena at mat[loc[row]].
+ * D in {64, 128, 256, 512}, K <= 4.  Rows with out-of-range inputs are skipped.
+ * ------------------------------------------------------------------------------------------------------- */
+#define ELR_ASM_INIT 0
+#define ELR_ASM_REPLAY 1
+#define ELR_ASM_GATHER 2
+#define ELR_ASM_MAX_SEG 16
+
+typedef struct elr_assemble_args {
+  float* work;                /* [n, 3, D] output */
+  const int64_t* rows;        /* [n] */
+  int64_t n;
+  int64_t D;
+  int K;
+  int nseg;
+  int64_t seg_end[ELR_ASM_MAX_SEG];
+  int seg_kind[ELR_ASM_MAX_SEG];
+  int64_t seg_aux[ELR_ASM_MAX_SEG];
+  uint32_t seed;              /* counter-hash init: seed (low 32 bits) and bound */
+  float bound;
+  const int32_t* L_ids;       /* [nL, K] log entry ids (-1 unused) */
+  const int32_t* L_steps;     /* [nL, K] logical steps */
+  const int32_t* L_cnt;       /* [nL] */
+  int64_t nL;
+  const float* logs;          /* [nlogs, D] log arena */
+  int64_t nlogs;
+  const float* table;         /* [table_rows, 8] Adam scalars per step */
+  const double* recip;        /* [table_rows, 2] elr_scalar_recip */
+  int64_t table_rows;
+  const float* mat;           /* [mat_rows, 3, D] MAT arena */
+  int64_t mat_rows;
+  const int32_t* loc;         /* [R + 1] MAT slot of each row */
+  int64_t R;
+} elr_assemble_args;
+
+int elr_assemble(const elr_assemble_args* args, void* stream);
+
 
 /* ---------------------------------------------------------------------------------------------------------
  * Row copies: dst[dst_idx[i]] = src[src_idx[i]], i < n, rows of W floats (NULL index = identity).

@@ -14,7 +14,8 @@ class OracleBackend:
         self.D, self.seed, self.bound, self.hp, self.nthreads = D, seed, bound, hp, nthreads
         self.table = O.scalar_table(*hp, max_step)
 
-    def unique(self, ids):
+    def unique(self, ids, bound=None):
+        """(u, plan): the plan of the oracle's dedup is the inverse (torch.unique, srm2/train.py:352)."""
         return torch.unique(ids, return_inverse=True)
 
     def plan_classify(self, u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s,
@@ -57,21 +58,79 @@ class OracleBackend:
         cls = torch.where(hit, t8(0), cls)
         flags = (hit.to(torch.uint8) | (isN.to(torch.uint8) << 1) | (isL.to(torch.uint8) << 2) |
                  (app.to(torch.uint8) << 3) | (admit.to(torch.uint8) << 4) | (in_next.to(torch.uint8) << 5))
-        order = torch.argsort(cls, stable=True)
+        # class ranks: hits; admitted N, L, F; appended N, L; compacted N, L; transient F; S
+        lut = torch.tensor([0, 1, 4, 6, 2, 5, 7, 3, 8, 9], dtype=torch.int8)
+        order = torch.argsort(lut[cls.long()], stable=True)
+        rank = torch.empty_like(order)
+        rank[order] = torch.arange(n)
         dcls = torch.where(exp, 0, torch.where(pre, 1, 2)).to(torch.int8)
         dyn_out = torch.cat([dyn[torch.argsort(dcls, stable=True)], dyn[torch.argsort((~exp).to(torch.int8),
                                                                                       stable=True)]])
         counts = torch.cat([torch.bincount(cls.long(), minlength=10),
                             torch.stack([exp.sum(), pre.sum(), (dcls == 2).sum()]),
                             mat_top.reshape(1), log_top.reshape(1), torch.zeros(1, dtype=torch.int64)])
-        return PlanClass(cls, flags, sl, c, order, dyn_out, counts)
+        return PlanClass(cls, flags, sl, c, order, rank, dyn_out, counts)
 
-    def segsum(self, g_occ, inv, U):
+    def segsum(self, g_occ, inv, U, perm=None):
+        """Per-unique-row gradient sums (orc_segment_sum's order), row u into perm[u] when perm is given."""
         out = np.zeros((U, self.D), np.float32)
         if inv.numel():
             u, s, _ = O.segment_sum(inv.numpy().astype(np.int64), np.ascontiguousarray(g_occ.numpy()))
             out[u] = s
+        if perm is not None:
+            res = np.zeros_like(out)
+            res[perm.numpy()] = out
+            out = res
         return torch.from_numpy(out)
+
+    def plan_admit(self, adm_rows, adm_slots, lazy_n, evl, s, n0, C, R, K, code, slot_of, slot_row, adm_c0, rj, rok,
+                   pstep):
+        """Admissions (srm2/elara.py:352-367) with torch ops on CPU tensors."""
+        n = adm_rows.numel()
+        if n == 0:
+            return
+        slot_of[adm_rows] = adm_slots.to(torch.int32)
+        slot_row[adm_slots] = adm_rows
+        c_adm = code[adm_rows].to(torch.int64)
+        isIL = torch.arange(n) < lazy_n
+        lazy = isIL & bool(evl)
+        adm_c0[adm_slots] = torch.where(isIL, c_adm, torch.full_like(c_adm, -1)).to(torch.int8)
+        rj[adm_slots] = lazy.to(torch.int8)
+        rok[adm_slots] = lazy.to(torch.int8)
+        if lazy_n and evl:
+            pstep[adm_slots[:lazy_n] - n0, 0] = s
+
+    def assemble(self, rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K):
+        """Full states of the work rows, segment by segment: oracle init (N), oracle replay of the log entries
+        packed row by row (L), copies from the MAT arena at loc[row] (F)."""
+        n = rows.numel()
+        work = np.empty((n, 3, self.D), np.float32)
+        lo = 0
+        for end, kind, aux in segs:
+            r = rows[lo:end].numpy()
+            m = end - lo
+            if m:
+                if kind == 0:
+                    work[lo:end] = O.init_rows(r, self.D, self.seed, self.bound)
+                elif kind == 1:
+                    cnt = L_cnt[aux:aux + m].numpy().astype(np.int32)
+                    ids = L_ids[aux:aux + m].numpy().astype(np.int64)
+                    steps = np.ascontiguousarray(L_steps[aux:aux + m].numpy().astype(np.int32))
+                    offs = np.concatenate([[0], np.cumsum(cnt)[:-1]]).astype(np.int64)
+                    kk = np.arange(K)[None, :]
+                    sel = ids[kk < cnt[:, None]]
+                    lg = np.ascontiguousarray(logs.numpy()[sel])
+                    work[lo:end] = O.replay_rows(r, lg, offs, steps, cnt, self.D, K, self.seed, self.bound,
+                                                 self.table, nthreads=self.nthreads)
+                else:
+                    work[lo:end] = mat.numpy()[loc.numpy()[r].astype(np.int64)]
+            lo = end
+        return torch.from_numpy(work)
+
+    def adam_dense(self, state, grad, s):
+        n = state.shape[0]
+        if n:
+            self.adam(state, torch.arange(n), grad, s)
 
     def _view(self, st, pv):
         v = object.__new__(O.DirState)
