@@ -143,6 +143,41 @@ def test_gpu_embedding_backward_matches_oracle(dev, D):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('D,case', [(128, 'zipf'), (64, 'long'), (30, 'zipf'), (128, 'big_ids')])
+def test_gpu_dedup_plan_matches_unique_and_backward(dev, D, case):
+    """unique_plan + segment_sum_plan (one sort reused by the sum) give torch.unique's rows and the oracle's sums,
+    into rows u or perm[u] (a permutation, and a scatter into a larger output)."""
+    from elara_amd.dedup import segment_sum_plan, unique_plan
+    print(f'[gpu-test] dedup plan D={D} {case}', flush=True)
+    rng = np.random.default_rng(13)
+    if case == 'zipf':
+        ids, g = zipf_case(14, 9000, 26, 60000, 1.05, D, scale=1.0)
+        bound = None
+    elif case == 'long':
+        ids = np.concatenate([np.full(5000, 77), rng.integers(0, 3000, 30000)])[rng.permutation(35000)].astype(np.int64)
+        g = rng.standard_normal((ids.size, D)).astype(np.float32)
+        bound = 3000
+    else:
+        ids = (rng.integers(0, 2**40, 40000) // 5 * 5).astype(np.int64)
+        g = rng.standard_normal((ids.size, D)).astype(np.float32)
+        bound = 2**40
+    u_ref, s_ref, _ = O.segment_sum(ids, g)
+    u, plan = unique_plan(torch.from_numpy(ids).to(dev), D, bound)
+    assert torch.equal(u.cpu(), torch.from_numpy(u_ref))
+    gd = torch.from_numpy(g).to(dev)
+    out = segment_sum_plan(gd, plan)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(s_ref))
+    perm = torch.from_numpy(rng.permutation(u_ref.size).astype(np.int64))
+    big = torch.zeros(u_ref.size + 5, D, device=dev)
+    segment_sum_plan(gd, plan, big, (perm + 3).to(dev))
+    want = np.zeros((u_ref.size + 5, D), np.float32)
+    want[perm.numpy() + 3] = s_ref
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(big.cpu().numpy()), bits(want))
+
+
+@pytest.mark.gpu
 def test_gpu_segment_sum_very_long_segment(dev):
     """One id with 100,000 occurrences (1,563 chunks) next to short ones."""
     from elara_amd.dedup import embedding_dense_backward

@@ -27,6 +27,23 @@ def step_banner(msg):
 
 
 # ------------------------------------------------------------------------------------------------ Adam
+@pytest.mark.parametrize('D', [128, 256, 30])
+def test_adam_dense_equals_identity_slots(dev, D):
+    """elr_adam_rows without a slot list (row i of grad -> state row i) equals the call with slots 0..n-1."""
+    from elara_amd.ops import adam_rows_dense
+    step_banner(f'adam dense D={D}')
+    g0 = torch.Generator().manual_seed(3)
+    n = 9_001
+    a = (torch.randn(n, 3, D, generator=g0) * 0.05).to(dev)
+    b = a.clone()
+    for step in (1, 2, 5):
+        grad = (torch.randn(n, D, generator=g0) * 1e-3).to(dev)
+        adam_rows_dense(a, grad, *HP, step)
+        gpu_adam(b, torch.arange(n, device=dev), grad, *HP, step)
+    torch.cuda.synchronize()
+    assert same(a, b)
+
+
 @pytest.mark.parametrize('D,idx', [(128, torch.int64), (128, torch.int32), (64, torch.int64), (256, torch.int64),
                                    (512, torch.int32), (30, torch.int64)])
 def test_adam_matches_oracle(dev, D, idx):

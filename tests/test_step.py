@@ -148,3 +148,62 @@ def test_gpu_plan_classify_matches_oracle(dev, name):
     run(st, cfg['batches'], grads_fn(cfg, 'cpu'))
     assert len(calls) == cfg['steps']
     assert st.stats['preempt'] > 0 and st.stats['overflow'] > 0 and sum(calls) > 0, st.stats
+
+
+@pytest.mark.gpu
+def test_gpu_assemble_and_admit_match_oracle(dev):
+    """elr_assemble (init / replay by entry id / MAT gather segments, including empty ones) and elr_plan_admit
+    against the oracle backend's restatements, on synthetic arenas."""
+    from elara_amd.step import HipBackend
+    print('[gpu-test] assemble + admit', flush=True)
+    rng = np.random.default_rng(21)
+    D, K, R, S = 128, 3, 5000, 40
+    hb = HipBackend(D, 42, synth.bound_for(D), HP, S, dev)
+    ob = OracleBackend(D, 42, synth.bound_for(D), HP, S)
+    logs = torch.from_numpy(rng.standard_normal((700, D)).astype(np.float32) * 1e-3)
+    mat = torch.from_numpy(rng.standard_normal((300, 3, D)).astype(np.float32))
+    loc = torch.full((R + 1,), -1, dtype=torch.int32)
+    nL = 90
+    L_cnt = torch.from_numpy(rng.integers(1, K + 1, nL).astype(np.int32))
+    L_ids = torch.full((nL, K), -1, dtype=torch.int32)
+    L_steps = torch.zeros((nL, K), dtype=torch.int32)
+    perm = rng.permutation(700)
+    q = 0
+    for i in range(nL):
+        c = int(L_cnt[i])
+        L_ids[i, :c] = torch.from_numpy(perm[q:q + c].astype(np.int32))
+        L_steps[i, :c] = torch.from_numpy(np.sort(rng.choice(np.arange(1, S), c, replace=False)).astype(np.int32))
+        q += c
+    sizes = [17, 30, 0, 25, 40, 11, 20, 9]        # NADM, LADM, FADM, NAPP, LAPP, NCMP, LCMP, FN
+    kinds = [0, 1, 2, 0, 1, 0, 1, 2]
+    rows = torch.from_numpy(rng.choice(R, sum(sizes), replace=False).astype(np.int64))
+    segs, end, aux = [], 0, 0
+    for m, kd in zip(sizes, kinds):
+        end += m
+        segs.append((end, kd, aux if kd == 1 else 0))
+        if kd == 1:
+            aux += m
+        if kd == 2:
+            r = rows[end - m:end]
+            loc[r] = torch.from_numpy(rng.choice(300, m, replace=False).astype(np.int32))
+    want = ob.assemble(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K)
+    got = hb.assemble(rows.to(dev), segs, L_ids.to(dev), L_steps.to(dev), L_cnt.to(dev), logs.to(dev),
+                      mat.to(dev), loc.to(dev), K)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().view(torch.int32), want.view(torch.int32))
+    # admissions: 60 rows into dynamic slots, the first 35 lazy (N/L)
+    C, n0 = 400, 100
+    code = torch.from_numpy(rng.integers(0, K + 2, R).astype(np.int8))
+    st = lambda: [torch.full((R,), -1, dtype=torch.int32), torch.full((C,), -1, dtype=torch.int64),  # noqa: E731
+                  torch.full((C,), -1, dtype=torch.int8), torch.zeros(C, dtype=torch.int8),
+                  torch.zeros(C, dtype=torch.int8), torch.zeros((C - n0 + 1, K), dtype=torch.int32)]
+    a_rows = torch.from_numpy(rng.choice(R, 60, replace=False).astype(np.int64))
+    a_slots = torch.from_numpy(rng.choice(np.arange(n0, C), 60, replace=False).astype(np.int64))
+    for evl in (True, False):
+        o = st()
+        ob.plan_admit(a_rows, a_slots, 35, evl, 7, n0, C, R, K, code, *o)
+        g = [t.to(dev) for t in st()]
+        hb.plan_admit(a_rows.to(dev), a_slots.to(dev), 35, evl, 7, n0, C, R, K, code.to(dev), *g)
+        torch.cuda.synchronize()
+        for x, y in zip(o, g):
+            assert torch.equal(x, y.cpu())
