@@ -274,32 +274,43 @@ def mode_c4(args):
 
 def mode_c5(args):
     """Config C5: the whole ELARA step (elara_amd.step) with HBM-resident arenas: 26 tables (vocab log-uniform in
-    [1e3, 4e7]), batch 16,384 x 26 Zipf(1.1), D = 128, pool 337,626 with 321,242 static hot rows, K = 3, evl on,
-    200 steps.  Occurrence gradients: 8 resident buffers cycled."""
+    [1e3, 4e7]), batch 16,384 x 26 Zipf(1.1), D = 128, pool 337,626 with 321,242 static hot rows, K = 3, evl on.
+    --warmup-c5 untimed steps (the pool fills, kernels load), then --steps-c5 timed steps.  Occurrence gradients:
+    8 resident buffers cycled."""
     import torch
     from elara_amd import synth
     from elara_amd.step import ElaraStep, run
     dev = torch.device('cuda:0')
-    B, D, steps = 16_384, 128, args.steps_c5
+    B, D, steps, W = 16_384, 128, args.steps_c5, args.warmup_c5
+    total = W + steps
     tabs = synth.C5Tables(T=26, lo=1e3, hi=4e7, alpha=1.1, seed=0)
     rng = np.random.default_rng(7)
     C = 337_626
     static = tabs.static_rows(rng, B, C - 16_384, n_batches=10)
-    batches = [torch.from_numpy(tabs.batch(rng, B)).to(dev) for _ in range(steps)]
+    batches = [torch.from_numpy(tabs.batch(rng, B)).to(dev) for _ in range(total)]
     O = B * 26
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
-                   seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=steps + 2, log_cap=steps * O + 16,
-                   mat_cap=steps * O // 2, device=dev)
+                   seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=total * O + 16,
+                   mat_cap=total * O // 2, device=dev)
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
+    mark = {}
+
+    def on_step(s, p):
+        if s == W:
+            torch.cuda.synchronize()
+            mark['stats'] = dict(st.stats)
+            mark['t0'] = time.perf_counter()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    run(st, batches, lambda j: gs[j % 8])
+    if W == 0:
+        mark['stats'] = dict(st.stats)
+        mark['t0'] = time.perf_counter()
+    run(st, batches, lambda j: gs[j % 8], on_step=on_step)
     torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    s = st.stats
+    el = time.perf_counter() - mark['t0']
+    s = {k: v - mark['stats'][k] for k, v in st.stats.items()}
     uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
-    return _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, 0, el,
+    return _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
                  {'workload': 'C5 full ELARA step, HBM-resident arenas: 26 tables (R=%d), batch 16,384 x 26 '
                               'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % tabs.R,
                   'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, 0.0,
@@ -333,6 +344,7 @@ def main():
     ap.add_argument('--mode', default='headline', choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'all'])
     ap.add_argument('--steps-c3', type=int, default=100)
     ap.add_argument('--steps-c5', type=int, default=200)
+    ap.add_argument('--warmup-c5', type=int, default=20)
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
