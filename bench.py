@@ -289,9 +289,14 @@ def mode_c5(args):
     static = tabs.static_rows(rng, B, C - 16_384, n_batches=10)
     batches = [torch.from_numpy(tabs.batch(rng, B)).to(dev) for _ in range(total)]
     O = B * 26
+    host = bool(args.host_arenas)
+    # arena capacities: every possible entry in HBM; in pinned host memory, the measured need with headroom
+    # (about 47k log entries and 7k MAT rows per step at this shape; check_capacity raises if exceeded)
+    log_cap = total * 80_000 + 1_000_000 if host else total * O + 16
+    mat_cap = total * 20_000 + 1_000_000 if host else total * O // 2
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
-                   seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=total * O + 16,
-                   mat_cap=total * O // 2, device=dev)
+                   seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=log_cap,
+                   mat_cap=mat_cap, device=dev, host_arenas=host)
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
     mark = {}
@@ -310,9 +315,12 @@ def mode_c5(args):
     el = time.perf_counter() - mark['t0']
     s = {k: v - mark['stats'][k] for k, v in st.stats.items()}
     uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
+    mt, lt = (int(x) for x in (st.mat_top, st.log_top))
+    where = 'pinned host arenas (capacity tier)' if host else 'HBM-resident arenas'
     return _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
-                 {'workload': 'C5 full ELARA step, HBM-resident arenas: 26 tables (R=%d), batch 16,384 x 26 '
-                              'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % tabs.R,
+                 {'workload': 'C5 full ELARA step, %s: 26 tables (R=%d), batch 16,384 x 26 '
+                              'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, tabs.R),
+                  'arenas': 'host' if host else 'hbm', 'mat_top': mt, 'log_top': lt,
                   'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, 0.0,
                  extra={'steps_per_s': steps / el, 'stats': s, 'note': 'step_GBps not reported for C5 (mixed '
                         'kernels; per-kernel bytes in profiles/)'})
@@ -345,6 +353,7 @@ def main():
     ap.add_argument('--steps-c3', type=int, default=100)
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=20)
+    ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:

@@ -25,6 +25,7 @@ c_f32p = ctypes.POINTER(ctypes.c_float)
 SIGNATURES = {
     'elr_error_string': (ctypes.c_char_p, [ctypes.c_int]),
     'elr_version': (ctypes.c_int, []),
+    'elr_host_device_ptr': (ctypes.c_int, [c_vp, ctypes.POINTER(c_vp)]),
     'elr_adam_scalars': (None, [c_f64, c_f64, c_f64, c_f64, c_i64, c_f32p]),
     'elr_scalar_table': (ctypes.c_int, [c_f64, c_f64, c_f64, c_f64, c_i64, c_vp]),
     'elr_adam_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_f32p, c_vp]),
@@ -126,6 +127,27 @@ def stream_of(t):
 
 def ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def is_arena(t):
+    """A float32 contiguous tensor the kernels can reach: in HBM, or in pinned host memory (the capacity tier)."""
+    return t.dtype == torch.float32 and t.is_contiguous() and (t.is_cuda or (t.device.type == 'cpu' and t.is_pinned()))
+
+
+def dptr(t):
+    """Device-visible address of t's data: a GPU tensor's own address, or for a pinned host tensor the address HIP
+    maps it to (elr_host_device_ptr; raises if the memory is not pinned and mapped)."""
+    if t is None:
+        return ctypes.c_void_p(0)
+    if t.is_cuda:
+        return ctypes.c_void_p(t.data_ptr())
+    if t.device.type == 'cpu' and t.is_pinned():
+        if t.numel() == 0:
+            return ctypes.c_void_p(0)
+        d = c_vp()
+        check(lib().elr_host_device_ptr(ctypes.c_void_p(t.data_ptr()), ctypes.byref(d)), 'elr_host_device_ptr')
+        return ctypes.c_void_p(d.value)
+    raise RuntimeError('tensor must be on the GPU or in pinned host memory')
 
 
 def scalars8(vals):

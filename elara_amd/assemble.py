@@ -18,8 +18,8 @@ MAX_SEG = 16
 def assemble_rows(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K, D, seed, bound, table):
     """rows int64 [n] (work order); segs: list of (end, kind, aux) with ascending ends, the last equal to n (aux:
     the first L row of a replay segment in L_ids / L_steps / L_cnt, elr_dir_a's int32 [nL, K] replay inputs);
-    logs [nlogs, D], mat [M, 3, D] float32, loc int32 [R + 1]; table: a gpu_ops.ScalarTable.  Returns the work
-    array [n, 3, D]."""
+    logs [nlogs, D], mat [M, 3, D] float32 (on the GPU or pinned host arenas), loc int32 [R + 1]; table: a
+    gpu_ops.ScalarTable.  Returns the work array [n, 3, D]."""
     dev = rows.device
     n = rows.numel()
     work = torch.empty(n, 3, D, dtype=torch.float32, device=dev)
@@ -30,8 +30,9 @@ def assemble_rows(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K, D, seed,
     rows = rows.to(I64).contiguous()
     L_ids, L_steps, L_cnt = (t.to(device=dev, dtype=I32).contiguous() for t in (L_ids, L_steps, L_cnt))
     for t, name in ((logs, 'logs'), (mat, 'mat')):
-        if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.shape[-1] == D):
-            raise RuntimeError(f'assemble_rows: {name} must be a contiguous cuda float32 tensor of width {D}')
+        if not (_lib.is_arena(t) and t.shape[-1] == D):
+            raise RuntimeError(f'assemble_rows: {name} must be a contiguous float32 tensor of width {D} on the GPU '
+                               f'or in pinned host memory')
     if loc.dtype != I32 or not loc.is_contiguous():
         raise RuntimeError('assemble_rows: loc must be a contiguous int32 tensor')
     a = _lib.AssembleArgs()
@@ -43,9 +44,9 @@ def assemble_rows(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K, D, seed,
         a.seg_end[g], a.seg_kind[g], a.seg_aux[g] = int(end), int(kind), int(aux)
     a.seed, a.bound = int(seed) & 0xFFFFFFFF, float(bound)
     a.L_ids, a.L_steps, a.L_cnt, a.nL = L_ids.data_ptr(), L_steps.data_ptr(), L_cnt.data_ptr(), L_cnt.numel()
-    a.logs, a.nlogs = logs.data_ptr(), logs.shape[0]
+    a.logs, a.nlogs = _lib.dptr(logs).value, logs.shape[0]
     a.table, a.recip, a.table_rows = table.t.data_ptr(), table.r.data_ptr(), table.t.shape[0]
-    a.mat, a.mat_rows = mat.data_ptr(), mat.shape[0]
+    a.mat, a.mat_rows = _lib.dptr(mat).value, mat.shape[0]
     a.loc, a.R = loc.data_ptr(), loc.numel() - 1
     with torch.cuda.device(dev):
         rc = _lib.lib().elr_assemble(ctypes.byref(a), _lib.stream_of(work))

@@ -44,23 +44,28 @@ def _check_state(pool, name='pool'):
 
 def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
     """pool [C,3,D] cuda float32 (updated in place); slots int32/int64 [n] (unique rows of pool); grad [n,D]
-    (row i -> slots[i]).  srm2/ops.py:59-67."""
+    (row i -> slots[i]).  srm2/ops.py:59-67.  pool may also be a pinned host arena (the capacity tier): the kernel
+    then updates it over the host link."""
     n = slots.numel()
     if n == 0:
         return
-    _check_state(pool)
+    if pool.is_cuda:
+        _check_state(pool)
+    elif not (_lib.is_arena(pool) and pool.dim() == 3 and pool.shape[1] == 3):
+        raise RuntimeError('pool must be a contiguous float32 [C,3,D] tensor on the GPU or in pinned host memory')
     D = pool.shape[2]
-    if slots.dtype not in (torch.int32, torch.int64) or not slots.is_cuda or slots.device != pool.device:
+    dev = slots.device
+    if slots.dtype not in (torch.int32, torch.int64) or not slots.is_cuda or (pool.is_cuda and dev != pool.device):
         raise RuntimeError(f'slots must be a cuda int32/int64 tensor on {pool.device}')
-    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.device == pool.device and grad.numel() == n * D):
-        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {pool.device}')
+    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.device == dev and grad.numel() == n * D):
+        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {dev}')
     slots = slots.contiguous()
     grad = grad.contiguous()
     s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
     L = _lib.lib()
-    with torch.cuda.device(pool.device):
-        rc = L.elr_adam_rows(_lib.ptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
-                             _lib.ptr(grad), n, D, s, _lib.stream_of(pool))
+    with torch.cuda.device(dev):
+        rc = L.elr_adam_rows(_lib.dptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
+                             _lib.ptr(grad), n, D, s, _lib.stream_of(grad))
     _lib.check(rc, 'elr_adam_rows')
 
 

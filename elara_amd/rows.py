@@ -1,4 +1,5 @@
-"""Row copies in HBM: gradient-log appends and the executor's row gathers and scatters.
+"""Row copies in HBM (or between HBM and pinned host arenas): gradient-log appends and the executor's row gathers
+and scatters.
 
     log_append(logs, ids, g)            logs[ids] = g          srm2/elara.py:569-570 (host cpu_scatter into the log
                                                                arena; the arena is in HBM here), and the
@@ -10,16 +11,25 @@
 Both run the HIP kernel behind elr_copy_rows (elara_amd/csrc/rows.hip) on torch's current stream.  Rows are the
 trailing dimensions flattened (a [C,3,D] state has rows of 3*D floats).
 """
+import ctypes
+
 import torch
 
 from . import _lib
 
 
 def _rows2d(t, name):
-    if not (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.dim() >= 1):
-        raise RuntimeError(f'{name} must be a contiguous cuda float32 tensor')
+    if not (_lib.is_arena(t) and t.dim() >= 1):
+        raise RuntimeError(f'{name} must be a contiguous float32 tensor on the GPU or in pinned host memory')
     n = t.shape[0]
     return n, (t.numel() // n if n else 0)
+
+
+def _device(*ts):
+    for t in ts:
+        if t is not None and t.is_cuda:
+            return t.device
+    raise RuntimeError('copy_rows: at least one of dst, src and the indices must be on the GPU')
 
 
 def _index(idx, dev, name):
@@ -34,7 +44,8 @@ def copy_rows(dst, dst_idx, src, src_idx=None):
     """dst[dst_idx[i]] = src[src_idx[i]] for every i (rows of the same width); indices out of range are skipped."""
     nd, wd = _rows2d(dst, 'dst')
     ns, ws = _rows2d(src, 'src')
-    di, si = _index(dst_idx, dst.device, 'dst_idx'), _index(src_idx, dst.device, 'src_idx')
+    dev = _device(dst, src, dst_idx, src_idx)
+    di, si = _index(dst_idx, dev, 'dst_idx'), _index(src_idx, dev, 'src_idx')
     n = di.numel() if di is not None else (si.numel() if si is not None else ns)
     if si is not None and di is not None and si.numel() != n:
         raise RuntimeError('dst_idx and src_idx must have the same length')
@@ -44,9 +55,9 @@ def copy_rows(dst, dst_idx, src, src_idx=None):
         return dst
     if wd != ws:
         raise RuntimeError(f'row widths differ: {wd} vs {ws}')
-    with torch.cuda.device(dst.device):
-        rc = _lib.lib().elr_copy_rows(_lib.ptr(dst), nd, _lib.ptr(di), _lib.ptr(src), ns, _lib.ptr(si), n, wd,
-                                      _lib.stream_of(dst))
+    with torch.cuda.device(dev):
+        rc = _lib.lib().elr_copy_rows(_lib.dptr(dst), nd, _lib.ptr(di), _lib.dptr(src), ns, _lib.ptr(si), n, wd,
+                                      ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
     _lib.check(rc, 'elr_copy_rows')
     return dst
 

@@ -113,12 +113,13 @@ class ElaraStep:
     (the `static` base, srm2/train.py:262-270) or None; K = Kmax; kthr: materialisation threshold per table (or one
     int); evl: residency-aware representation (evicted rows may return to L); L: TTL lookahead; depth: number of
     batches u_nexts covers plus one (srm2/train.py:366); st_mode 'T' (transient full-state updates on the GPU) or
-    'S' (materialised cold rows updated in the MAT arena); log_cap / mat_cap: arena capacities in rows.
+    'S' (materialised cold rows updated in the MAT arena); log_cap / mat_cap: arena capacities in rows;
+    host_arenas: keep the MAT and log arenas in pinned host memory (the capacity tier, srm2/elara.py:40-103).
     """
 
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
-                 backend=None):
+                 backend=None, host_arenas=False):
         d = torch.device(device)
         self.d, self.R, self.D, self.C, self.K, self.L, self.depth = d, R, D, C, K, L, depth
         self.MAT = K + 1
@@ -166,8 +167,12 @@ class ElaraStep:
         # ---- arenas (HBM) ----
         self.pool = torch.zeros(C, 3, D, device=d)
         self.glog = torch.zeros(self.Cdyn + 1, K, D, device=d)
-        self.mat = torch.empty(self.mat_cap, 3, D, device=d)
-        self.logs = torch.empty(self.log_cap + 1, D, device=d)
+        # the capacity tier: with host_arenas the MAT and log arenas live in pinned host memory, which the kernels
+        # read and write directly over the host link (no staging copies, no host-side arithmetic)
+        ad = dict(device='cpu', pin_memory=True) if host_arenas and d.type == 'cuda' else dict(device=d)
+        self.host_arenas = bool(host_arenas and d.type == 'cuda')
+        self.mat = torch.empty(self.mat_cap, 3, D, **ad)
+        self.logs = torch.empty(self.log_cap + 1, D, **ad)
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs')}
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool

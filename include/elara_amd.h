@@ -38,6 +38,13 @@ const char* elr_error_string(int code);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int elr_version(void);
 
+/* Device-visible address of pinned host memory (no counterpart in the reference, whose host arenas are reached
+ * through CPU gathers and staging copies): *dev receives the address the kernels use for host, or the HIP error is
+ * returned if the memory is not pinned and mapped.  Every entry point below accepts such addresses for its arena
+ * arguments (the MAT and log arenas of the capacity tier), which the kernels then read and write over the host
+ * link. */
+int elr_host_device_ptr(const void* host, void** dev);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Adam scalars for logical step `step` (host only).
  * Replaces: srm2/csrc/srm2_cpu.cpp:13-20 make_scalars and its binding adam_scalars (srm2_cpu.cpp:255-257),

@@ -76,3 +76,19 @@ def test_ops_raise_without_gpu_tensors():
     from elara_amd.ops import gpu_adam
     with pytest.raises(RuntimeError):
         gpu_adam(torch.zeros(4, 3, 8), torch.tensor([0]), torch.zeros(1, 8), 1e-3, 0.9, 0.999, 1e-8, 1)
+
+
+@pytest.mark.gpu
+def test_host_device_ptr_accepts_pinned_and_rejects_pageable(dev):
+    """elr_host_device_ptr maps pinned host memory and returns an error (no address) for pageable memory."""
+    import torch
+    pinned = torch.zeros(1024, pin_memory=True)
+    d = ctypes.c_void_p()
+    assert _lib.lib().elr_host_device_ptr(ctypes.c_void_p(pinned.data_ptr()), ctypes.byref(d)) == 0 and d.value
+    inner = ctypes.c_void_p()
+    assert _lib.lib().elr_host_device_ptr(ctypes.c_void_p(pinned[256:].data_ptr()), ctypes.byref(inner)) == 0
+    assert inner.value == d.value + 256 * 4
+    pageable = torch.zeros(1024)
+    bad = ctypes.c_void_p()
+    assert _lib.lib().elr_host_device_ptr(ctypes.c_void_p(pageable.data_ptr()), ctypes.byref(bad)) != 0
+    assert not bad.value

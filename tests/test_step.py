@@ -22,7 +22,7 @@ def make(cfg, device, backend=None):
     return ElaraStep(cfg['toff'], cfg['R'], cfg['D'], cfg['C'], static_rows=cfg['static'], K=3, kthr=3,
                      evl=cfg.get('evl', True), L=cfg.get('L', 8), depth=3, st_mode=cfg.get('st', 'T'),
                      seed=42, bound=cfg['bound'], hp=HP, max_step=cfg['steps'] + 2, log_cap=cfg['log_cap'],
-                     mat_cap=cfg['mat_cap'], device=device, backend=backend)
+                     mat_cap=cfg['mat_cap'], device=device, backend=backend, host_arenas=cfg.get('host', False))
 
 
 def config(T, lo, hi, B, steps, C, n_static, D=128, seed=0, **kw):
@@ -86,11 +86,15 @@ def test_step_runs_on_cpu_with_oracle_backend():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow'])
+@pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow', 'host_arenas',
+                                  'host_arenas_S'])
 def test_gpu_step_matches_oracle_step(dev, name):
+    """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
+    kernels over the host link."""
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
-    kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000}}[name]
+    kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
+          'host_arenas': {'host': True}, 'host_arenas_S': {'host': True, 'st': 'S'}}[name]
     cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
     g = make(cfg, dev)
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
