@@ -129,7 +129,9 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   }
 }
 
-// Segment kernels take kSegItems consecutive positions per thread (blocked), kSegTile per block.
+// Segment kernels take a tile of kSegTile positions per block, in kSegItems rounds of kSegBlock consecutive
+// positions (thread t takes position base + r * kSegBlock + t in round r: every load is coalesced).  Positions are
+// ranked in that order, round by round, with one block scan per round.
 constexpr int kSegItems = 16;
 constexpr int64_t kSegTile = (int64_t)kSegBlock * kSegItems;
 
@@ -142,9 +144,9 @@ __device__ __forceinline__ int is_head(const Key* __restrict__ sk, int64_t i, in
 template <typename Key>
 __global__ __launch_bounds__(kSegBlock) void k_seg_count(const Key* __restrict__ sk, int64_t n,
                                                          int64_t* __restrict__ bsum) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
   int v[1] = {0}, ex[1], tot[1];
-  for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + r, n);
+  for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + (int64_t)r * kSegBlock, n);
   block_excl_scan<kSegBlock, 1>(v, ex, tot);
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
@@ -157,25 +159,25 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__
                                                          const int64_t* __restrict__ d_U,
                                                          int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
                                                          int32_t* __restrict__ seg_occ0, int64_t* __restrict__ inverse) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
-  int v[1] = {0}, ex[1], tot[1];
-  for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + r, n);
-  block_excl_scan<kSegBlock, 1>(v, ex, tot);
-  int64_t u = boff[blockIdx.x] + ex[0] - 1;   // segment of the position before this thread's first
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
+  int64_t before = boff[blockIdx.x];   // heads in earlier positions of the tile's earlier rounds
   for (int r = 0; r < kSegItems; ++r) {
-    const int64_t i = base + r;
-    if (i >= n) break;
+    const int64_t i = base + (int64_t)r * kSegBlock;
     const int f = is_head(sk, i, n);
-    u += f;
-    if (f) {
-      uniq[u] = (int64_t)sk[i];
-      seg_start[u] = i;
-      seg_occ0[u] = sv[i];
-    }
-    if (inverse) {
+    int v[1] = {f}, ex[1], tot[1];
+    block_excl_scan<kSegBlock, 1>(v, ex, tot);
+    const int64_t u = before + ex[0] + f - 1;   // segment of position i
+    if (i < n) {
       const int32_t o = sv[i];
-      if (o >= 0 && o < n) inverse[o] = u;
+      if (f) {
+        uniq[u] = (int64_t)sk[i];
+        seg_start[u] = i;
+        seg_occ0[u] = o;
+      }
+      if (inverse && o >= 0 && o < n) inverse[o] = u;
     }
+    before += tot[0];
+    __syncthreads();   // block_excl_scan's LDS is reused by the next round
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) seg_start[*d_U] = n;
 }
@@ -188,10 +190,10 @@ __device__ __forceinline__ int extra_chunks(const int64_t* __restrict__ seg_star
 __global__ __launch_bounds__(kSegBlock) void k_chunk_count(const int64_t* __restrict__ seg_start,
                                                            const int64_t* __restrict__ d_U,
                                                            int64_t* __restrict__ bsum) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
   const int64_t U = *d_U;
   int v[1] = {0}, ex[1], tot[1];
-  for (int r = 0; r < kSegItems; ++r) v[0] += extra_chunks(seg_start, base + r, U);
+  for (int r = 0; r < kSegItems; ++r) v[0] += extra_chunks(seg_start, base + (int64_t)r * kSegBlock, U);
   block_excl_scan<kSegBlock, 1>(v, ex, tot);
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
@@ -202,19 +204,21 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __rest
                                                            const int64_t* __restrict__ boff,
                                                            int32_t* __restrict__ chunk_off,
                                                            int32_t* __restrict__ chunk_seg) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + (int64_t)threadIdx.x * kSegItems;
+  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
   const int64_t U = *d_U;
-  int v[1] = {0}, ex[1], tot[1];
-  for (int r = 0; r < kSegItems; ++r) v[0] += extra_chunks(seg_start, base + r, U);
-  block_excl_scan<kSegBlock, 1>(v, ex, tot);
-  int64_t off = boff[blockIdx.x] + ex[0];
+  int64_t before = boff[blockIdx.x];
   for (int r = 0; r < kSegItems; ++r) {
-    const int64_t u = base + r;
-    if (u >= U) break;
+    const int64_t u = base + (int64_t)r * kSegBlock;
     const int e = extra_chunks(seg_start, u, U);
-    chunk_off[u] = (int32_t)off;
-    for (int c = 0; c < e; ++c) chunk_seg[off + c] = (int32_t)u;
-    off += e;
+    int v[1] = {e}, ex[1], tot[1];
+    block_excl_scan<kSegBlock, 1>(v, ex, tot);
+    if (u < U) {
+      const int64_t off = before + ex[0];
+      chunk_off[u] = (int32_t)off;
+      for (int c = 0; c < e; ++c) chunk_seg[off + c] = (int32_t)u;
+    }
+    before += tot[0];
+    __syncthreads();
   }
 }
 

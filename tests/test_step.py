@@ -19,7 +19,8 @@ HP = synth.ADAM
 
 def make(cfg, device, backend=None):
     from elara_amd.step import ElaraStep
-    return ElaraStep(cfg['toff'], cfg['R'], cfg['D'], cfg['C'], static_rows=cfg['static'], K=3, kthr=3,
+    return ElaraStep(cfg['toff'], cfg['R'], cfg['D'], cfg['C'], static_rows=cfg['static'], K=cfg.get('K', 3),
+                     kthr=cfg.get('kthr', 3),
                      evl=cfg.get('evl', True), L=cfg.get('L', 8), depth=3, st_mode=cfg.get('st', 'T'),
                      seed=42, bound=cfg['bound'], hp=HP, max_step=cfg['steps'] + 2, log_cap=cfg['log_cap'],
                      mat_cap=cfg['mat_cap'], device=device, backend=backend, host_arenas=cfg.get('host', False))
@@ -87,14 +88,16 @@ def test_step_runs_on_cpu_with_oracle_backend():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow', 'host_arenas',
-                                  'host_arenas_S'])
+                                  'host_arenas_S', 'D64_K2', 'D256_K4', 'K1_kthr0'])
 def test_gpu_step_matches_oracle_step(dev, name):
     """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
     kernels over the host link."""
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
     kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
-          'host_arenas': {'host': True}, 'host_arenas_S': {'host': True, 'st': 'S'}}[name]
+          'host_arenas': {'host': True}, 'host_arenas_S': {'host': True, 'st': 'S'},
+          'D64_K2': {'D': 64, 'K': 2, 'kthr': 2}, 'D256_K4': {'D': 256, 'K': 4, 'kthr': 3},
+          'K1_kthr0': {'K': 1, 'kthr': 0}}[name]
     cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
     g = make(cfg, dev)
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
