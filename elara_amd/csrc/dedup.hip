@@ -67,7 +67,9 @@ __global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict_
 }
 
 // Stable scatter of one pass.  FIRST: the source keys are the caller's int64 ids and the values are their
-// positions.
+// positions.  Each item's rank among the tile's items of its digit comes from ballots (wave) and LDS counts (block);
+// the tile is then sorted by digit in LDS and written out run by run, so consecutive threads write consecutive
+// addresses of one digit's bucket instead of 64 scattered ones.
 template <typename Src, typename Key, bool FIRST>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __restrict__ src_keys,
                                                                 const int32_t* __restrict__ src_vals, int64_t n,
@@ -76,9 +78,12 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
                                                                 Key* __restrict__ dst_keys,
                                                                 int32_t* __restrict__ dst_vals) {
   constexpr int NW = kSortThreads / 64;
-  __shared__ int64_t bo[kRadixBins];
-  __shared__ int run[kRadixBins];
+  __shared__ int64_t bo[kRadixBins];   // global position of this tile's first item of digit d
+  __shared__ int run[kRadixBins];      // items of digit d in earlier rounds of the tile
+  __shared__ int lbase[kRadixBins];    // position of digit d's first item in the tile sorted by digit
   __shared__ int wc[NW][kRadixBins];
+  __shared__ Key lk[kSortTile];
+  __shared__ int32_t lv[kSortTile];
   const int t = threadIdx.x, w = t >> 6;
   {
     // digit bases: exclusive scan of the 256 digit totals (n < 2^31, so they fit in int)
@@ -91,11 +96,16 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   for (int q = 0; q < NW; ++q) wc[q][t] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  Key kk[kSortItems];
+  int32_t vv[kSortItems];
+  int rk[kSortItems];
+#pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t pos = base + (int64_t)r * kSortThreads + t;
     const bool valid = pos < n;
     const Key k = valid ? (Key)src_keys[pos] : (Key)0;
-    const int32_t v = valid ? (FIRST ? (int32_t)pos : src_vals[pos]) : 0;
+    kk[r] = k;
+    vv[r] = valid ? (FIRST ? (int32_t)pos : src_vals[pos]) : 0;
     const uint32_t d = digit_of(k, shift);
     uint64_t m = __ballot(valid);
 #pragma unroll
@@ -107,15 +117,12 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
     const int lr = __popcll(m & lanemask_lt());
     if (valid && lr == 0) wc[w][d] = __popcll(m);
     __syncthreads();
+    rk[r] = -1;
     if (valid) {
       int rank = run[d] + lr;
 #pragma unroll
       for (int q = 0; q < NW; ++q) rank += q < w ? wc[q][d] : 0;
-      const int64_t dst = bo[d] + rank;
-      if (dst >= 0 && dst < n) {
-        dst_keys[dst] = k;
-        dst_vals[dst] = v;
-      }
+      rk[r] = rank;
     }
     __syncthreads();
     int add = 0;
@@ -126,6 +133,33 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
     }
     run[t] += add;
     __syncthreads();
+  }
+  {
+    // the tile sorted by digit: digit d's items start at the exclusive scan of the tile's digit counts
+    int v[1] = {run[t]}, ex[1], tot[1];
+    block_excl_scan<kSortThreads, 1>(v, ex, tot);
+    lbase[t] = ex[0];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortItems; ++r) {
+    if (rk[r] >= 0) {
+      const int lp = lbase[digit_of(kk[r], shift)] + rk[r];
+      lk[lp] = kk[r];
+      lv[lp] = vv[r];
+    }
+  }
+  __syncthreads();
+  const int64_t rem = n - base;
+  const int nvalid = rem < kSortTile ? (int)rem : (int)kSortTile;
+  for (int j = t; j < nvalid; j += kSortThreads) {
+    const Key k = lk[j];
+    const uint32_t d = digit_of(k, shift);
+    const int64_t dst = bo[d] + (j - lbase[d]);
+    if (dst >= 0 && dst < n) {
+      dst_keys[dst] = k;
+      dst_vals[dst] = lv[j];
+    }
   }
 }
 
