@@ -85,6 +85,16 @@ class DedupPlan:
 def unique_plan(ids, D, bound=None):
     """unique(ids) without the inverse, keeping the sort as a plan for segment_sum_plan over gradients of width D:
     returns (u, plan)."""
+    u, plan, nu = unique_plan_async(ids, D, bound)
+    if nu is not None:
+        plan.U = int(nu)
+        u = u[:plan.U]
+    return u, plan
+
+
+def unique_plan_async(ids, D, bound=None):
+    """unique_plan without reading the unique count: returns (u_full, plan, nu) with u_full [n] whose first nu
+    entries are the unique ids, nu the count on the device (None when n == 0).  Set plan.U once nu is known."""
     flat = _ids(ids)
     n = flat.numel()
     dev = flat.device
@@ -92,7 +102,7 @@ def unique_plan(ids, D, bound=None):
     plan.n, plan.D, plan.U = n, int(D), 0
     plan.buf, plan.nbytes, plan.key_bits = None, 0, 1
     if n == 0:
-        return torch.empty(0, dtype=I64, device=dev), plan
+        return torch.empty(0, dtype=I64, device=dev), plan, None
     plan.key_bits = _key_bits(flat, bound)
     nbytes = int(_lib.lib().elr_dedup_plan_bytes(n, int(D)))
     if nbytes < 0:
@@ -104,8 +114,7 @@ def unique_plan(ids, D, bound=None):
         rc = _lib.lib().elr_dedup_plan(_lib.ptr(flat), n, plan.key_bits, _lib.ptr(u), None, _lib.ptr(nu),
                                        _lib.ptr(plan.buf), nbytes, int(D), _lib.stream_of(flat))
     _lib.check(rc, 'elr_dedup_plan')
-    plan.U = int(nu)
-    return u[:plan.U], plan
+    return u, plan, nu
 
 
 def segment_sum_plan(grad, plan, out=None, perm=None):

@@ -65,3 +65,16 @@ def copy_rows(dst, dst_idx, src, src_idx=None):
 def log_append(logs, ids, g):
     """logs[ids[i]] = g[i]: append gradient rows to the log arena at their allocated log ids."""
     return copy_rows(logs, ids, g, None)
+
+
+def mark_rows(rows, n_dev, value, out):
+    """out[rows[i]] = value for i < n_dev (a device int64 count; rows beyond it are ignored), with no
+    synchronisation: rows int64 [n_max] cuda, out int32 [R] cuda."""
+    if not (rows.is_cuda and rows.dtype == torch.int64 and out.is_cuda and out.dtype == torch.int32
+            and n_dev.is_cuda and n_dev.dtype == torch.int64 and out.is_contiguous()):
+        raise RuntimeError('mark_rows: rows int64, n_dev int64 and out int32 cuda tensors')
+    rows = rows.contiguous()
+    with torch.cuda.device(out.device):
+        rc = _lib.lib().elr_mark_rows(_lib.ptr(rows), _lib.ptr(n_dev), rows.numel(), int(value), _lib.ptr(out),
+                                      out.numel(), ctypes.c_void_p(torch.cuda.current_stream(out.device).cuda_stream))
+    _lib.check(rc, 'elr_mark_rows')

@@ -28,13 +28,13 @@ import torch
 
 from . import _lib  # noqa: F401  (the library must be present)
 from .assemble import assemble_rows
-from .dedup import segment_sum_plan, unique_plan
+from .dedup import segment_sum_plan, unique_plan, unique_plan_async
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
 from .planner import (CNT_EXP, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
                       plan_admit, plan_classify)
-from .rows import copy_rows
+from .rows import copy_rows, mark_rows
 
 I8, I32, I64 = torch.int8, torch.int32, torch.int64
 # classes (srm2/elara.py:31-32): hit, N admitted / append / compact, L admitted / append / compact, F admitted /
@@ -66,6 +66,12 @@ class HipBackend:
 
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
+
+    def unique_async(self, ids, bound=None):
+        return unique_plan_async(ids, self.D, bound)
+
+    def mark_rows(self, rows, n_dev, value, out):
+        mark_rows(rows, n_dev, value, out)
 
     def plan_classify(self, *args):
         return plan_classify(*args)
@@ -175,6 +181,7 @@ class ElaraStep:
         self.logs = torch.empty(self.log_cap + 1, D, **ad)
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs')}
+        self._deferred = []
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
@@ -194,17 +201,37 @@ class ElaraStep:
         if mt > self.mat_cap - 1 or lt > self.log_cap:
             raise RuntimeError(f'arena capacity exceeded (MAT {mt}/{self.mat_cap - 1}, logs {lt}/{self.log_cap})')
 
-    def observe(self, step, u):
-        """Record that rows u appear at logical step `step` (the TTL lookahead, srm2/elara.py:160-161)."""
-        self.last_seen[u] = step
+    def observe(self, step, u, n_dev=None):
+        """Record that rows u appear at logical step `step` (the TTL lookahead, srm2/elara.py:160-161); with n_dev
+        (a device count) only the first n_dev rows of u, without a synchronisation."""
+        if n_dev is None:
+            self.last_seen[u] = step
+        else:
+            self.be.mark_rows(u, n_dev, step, self.last_seen)
+
+    def defer_count(self, t, cb):
+        """Read the device int64 scalar t at the next host synchronisation and pass it to cb."""
+        self._deferred.append((t, cb))
+
+    def flush_deferred(self):
+        """One host synchronisation that resolves every deferred count (counted in stats like any other)."""
+        self._host_list(torch.zeros(0, dtype=I64, device=self.d))
 
     def _host(self, *ts):
         self.stats['syncs'] += 1
         return torch.stack([t.reshape(()).to(I64) for t in ts]).tolist()
 
     def _host_list(self, t):
+        """t.tolist() -- with any deferred device counts read in the same transfer (one synchronisation)."""
         self.stats['syncs'] += 1
-        return t.tolist()
+        if not self._deferred:
+            return t.tolist()
+        n = t.numel()
+        vals = torch.cat([t.reshape(-1).to(I64)] + [x.reshape(-1) for x, _ in self._deferred]).tolist()
+        for (_, cb), v in zip(self._deferred, vals[n:]):
+            cb(v)
+        self._deferred = []
+        return vals[:n]
 
     # ---- plan (srm2/elara.py:209-414, cpp directory path) ----
     def plan(self, s, u, u_nexts):
@@ -408,12 +435,23 @@ def run(step, batches, grads, steps=None, on_step=None):
     dev = step.d
 
     def load(j):
-        u, dplan = step.be.unique(batches[j].to(dev), step.R)
-        U[j], PLANS[j] = u, dplan
-        step.observe(j + 1, u)
+        # the batch's unique count is read at the next host synchronisation (the plan's), not here
+        u, dplan, nu = step.be.unique_async(batches[j].to(dev), step.R)
+        PLANS[j] = dplan
+        if nu is None:
+            U[j] = u
+            step.observe(j + 1, u)
+            return
+
+        def resolve(v, j=j, u=u, dplan=dplan):
+            U[j] = u[:v]
+            dplan.U = v
+        step.observe(j + 1, u, nu)
+        step.defer_count(nu, resolve)
 
     for j in range(min(S, step.L + 1)):
         load(j)
+    step.flush_deferred()
     for s in range(S):
         if s + step.L + 1 < S:
             load(s + step.L + 1)

@@ -317,6 +317,13 @@ int elr_assemble(const elr_assemble_args* args, void* stream);
 int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
                   const int64_t* src_idx, int64_t n, int64_t W, void* stream);
 
+/* out[rows[i]] = value for i < min(*n_dev, n_max), with the count read on the device (no counterpart in the
+ * reference, which reads the batch's unique count on the host first): the TTL lookahead's record of when rows
+ * appear next (srm2/elara.py:160-161) for a batch whose unique count the host reads later.  Rows out of range are
+ * skipped. */
+int elr_mark_rows(const int64_t* rows, const int64_t* n_dev, int64_t n_max, int32_t value, int32_t* out,
+                  int64_t out_rows, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Exhaustive check of the step-constant division (no counterpart in the reference).  The Adam kernels compute
  * a / b for b = 1 - b1^t and b = 1 - b2^t as RN_f32((double)a * RN_f64(1/b)); for all 2^32 float bit patterns a

@@ -18,6 +18,11 @@ class OracleBackend:
         """(u, plan): the plan of the oracle's dedup is the inverse (torch.unique, srm2/train.py:352)."""
         return torch.unique(ids, return_inverse=True)
 
+    def unique_async(self, ids, bound=None):
+        """(u, plan, None): the oracle's count is known at once."""
+        u, inv = torch.unique(ids, return_inverse=True)
+        return u, inv, None
+
     def plan_classify(self, u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s,
                       K, want_t):
         """Restatement of the planner's classification (srm2/elara.py:214-267) with torch ops on CPU tensors:
