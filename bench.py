@@ -357,8 +357,8 @@ def main():
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
-        print('bench.py measures one GPU only: this build has no multi-GPU path (the sharding design is '
-              'described in DESIGN.md); run with --gpus 1', file=sys.stderr)
+        print('bench.py measures one GPU only: this build has no multi-GPU path (rows would shard by owner, with '
+              'an all-to-all of occurrence gradients; not implemented); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     fns = {'headline': headline, 'copy': copy_calibration, 'c1': mode_c1, 'c3': mode_c3, 'c4': mode_c4,
            'c5': mode_c5}
