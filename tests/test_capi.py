@@ -71,6 +71,59 @@ def test_host_argument_checks_return_codes():
     assert L.elr_replay_rows(None, None, None, 0, None, None, None, 0, 4, 3, 0, 1.0, None, None, 0, None) == 0
 
 
+def test_planner_executor_dedup_argument_checks():
+    """The entry points of the planner, the fused executor and the dedup plan reject bad arguments on the host,
+    before any launch (none of these calls reaches the GPU)."""
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)          # never dereferenced: every call below returns before any launch
+    assert L.elr_plan_classify(None, None, None, 0, None) == -1
+    pin, pout = _lib.PlanIn(), _lib.PlanOut()
+    pin.n, pin.nd, pin.nnext, pin.T, pin.K = 0, 0, 0, 1, 3
+    pin.toff, pin.kthr, pout.counts = fake.value, fake.value, fake.value
+    assert L.elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), None, 0, None) == -3      # no scratch
+    for field, bad in (('n', -1), ('nnext', 5), ('T', 0), ('K', 0)):
+        q = _lib.PlanIn.from_buffer_copy(pin)
+        setattr(q, field, bad)
+        assert L.elr_plan_classify(ctypes.byref(q), ctypes.byref(pout), fake, 1 << 20, None) == -1, field
+    q = _lib.PlanIn.from_buffer_copy(pin)
+    q.n = 5                                                        # rows but no row pointers
+    assert L.elr_plan_classify(ctypes.byref(q), ctypes.byref(pout), fake, 1 << 20, None) == -1
+    assert L.elr_plan_scratch_bytes(-1, 0) == -1 and L.elr_plan_scratch_bytes(1000, 10) > 0
+    adm = [None] * 8
+    assert L.elr_plan_admit(None, None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == 0              # nothing to do
+    assert L.elr_plan_admit(None, None, 3, 4, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1             # lazy_n > n
+    assert L.elr_plan_admit(None, None, 3, 1, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1             # null pointers
+    a = _lib.AssembleArgs()
+    a.n, a.D, a.K, a.nseg = 0, 128, 3, 1
+    assert L.elr_assemble(None, None) == -1
+    assert L.elr_assemble(ctypes.byref(a), None) == 0                                               # n == 0
+    a.nseg = 0
+    assert L.elr_assemble(ctypes.byref(a), None) == -1
+    a.nseg, a.K = 1, 5
+    assert L.elr_assemble(ctypes.byref(a), None) == -2                                              # K > 4
+    a.K, a.n, a.work, a.rows = 3, 10, fake.value, fake.value
+    a.seg_end[0], a.seg_kind[0] = 9, 0
+    assert L.elr_assemble(ctypes.byref(a), None) == -1                                              # ends != n
+    a.seg_end[0], a.seg_kind[0] = 10, 3
+    assert L.elr_assemble(ctypes.byref(a), None) == -1                                              # unknown kind
+    a.seg_kind[0] = 1
+    assert L.elr_assemble(ctypes.byref(a), None) == -1                                              # replay, no logs
+    a.seg_kind[0] = 2
+    assert L.elr_assemble(ctypes.byref(a), None) == -1                                              # gather, no MAT
+    assert L.elr_dedup_plan_bytes(-1, 1) == -1 and L.elr_dedup_plan_bytes(10, 0) == -1
+    assert L.elr_dedup_plan(None, 0, 20, None, None, None, None, 0, 8, None) == 0                   # n == 0
+    assert L.elr_dedup_plan(fake, 10, 0, fake, None, fake, fake, 1 << 20, 8, None) == -1            # key bits
+    assert L.elr_dedup_plan(fake, 10, 20, fake, None, fake, fake, 1, 8, None) == -3                 # plan too small
+    assert L.elr_segment_sum_plan(fake, 10, 600, 20, fake, 1 << 30, None, fake, 10, None) == -2     # D > 512
+    assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1, None, fake, 10, None) == -3             # plan too small
+    assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1 << 20, None, fake, -1, None) == -1
+    assert L.elr_mark_rows(None, None, -1, 0, None, 0, None) == -1
+    assert L.elr_mark_rows(None, None, 0, 0, None, 0, None) == 0
+    assert L.elr_mark_rows(None, fake, 5, 0, fake, 10, None) == -1
+    d = ctypes.c_void_p()
+    assert L.elr_host_device_ptr(None, ctypes.byref(d)) == -1
+
+
 def test_ops_raise_without_gpu_tensors():
     import torch
     from elara_amd.ops import gpu_adam
