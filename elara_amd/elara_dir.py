@@ -20,9 +20,27 @@ I8, I32, I64 = torch.int8, torch.int32, torch.int64
 ST_DTYPES = (I8, I32, I32, I32, I32, I64, I64, I64, I64, I8, I8, I32, I8, I64, I32, I64, I8)
 
 
+_STATE_CACHE = {}
+
+
 def _state(st, pv):
+    """The validated DirState / DirParams of (st, pv).  A directory is called once or twice per step with the same
+    17 tensors, so the structures are kept per (tensor addresses and sizes, pv) and validated once."""
     if len(st) != 17 or len(pv) != 8:
         raise RuntimeError('st must hold the 17 directory tensors and pv the 8 parameters')
+    key = (tuple((t.data_ptr(), t.numel(), t.dtype, t.device, t.is_contiguous()) for t in st),
+           tuple(int(x) for x in pv))
+    hit = _STATE_CACHE.get(key)
+    if hit is not None:
+        return hit
+    res = _state_checked(st, pv)
+    if len(_STATE_CACHE) >= 16:
+        _STATE_CACHE.clear()
+    _STATE_CACHE[key] = res
+    return res
+
+
+def _state_checked(st, pv):
     R, K, Lcap, n0, Cdyn = (int(x) for x in pv[:5])
     C = n0 + Cdyn
     dev = st[0].device
