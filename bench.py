@@ -218,7 +218,7 @@ def mode_c1(args):
 
 
 def mode_c3(args):
-    """Config C3: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step with duplicates: dedup, fixed-order
+    """Config C3: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step with duplicates: dedup, ATen-order
     segment sum and Adam on the unique rows (elr_adam_dedup).  Four resident batches are cycled."""
     import torch
     from elara_amd import synth
@@ -241,7 +241,7 @@ def mode_c3(args):
     byts = (O * (4 * D + 8) + Umean * (28 * D + 8)) / 1e9
     return _line('C3 duplicate-id sparse Adam occurrences/s (d=128)', O * steps / el, 'occurrences/s', args, steps,
                  warmup, el, {'workload': 'C3 duplicate-id Adam: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) '
-                                          'ids per step, dedup + fixed-order segment sum + Adam',
+                                          'ids per step, dedup + segment sum in ATen order + Adam',
                               'occurrences_per_step': O, 'unique_rows_per_step': Umean, 'dim': D}, byts,
                  extra={'unique_rows_per_s': Umean * steps / el, 'mean_step_ms_events': float(np.mean(ms))})
 

@@ -14,11 +14,18 @@
 // Segments.  Sorted position i starts a segment when its key differs from position i-1; a scan of those heads
 // gives every position its unique index (the inverse) and every unique id its first position.
 //
-// Summation order (this build's definition; the reference's order is ATen's and no reference test pins it):
-// the occurrences of one id, in ascending occurrence index, are cut into chunks of 64; each chunk is summed left
-// to right starting from its first gradient, and the chunk sums are added left to right starting from chunk 0.
-// For an id with at most 64 occurrences this is the plain left-to-right sum.  The result depends only on that id's
-// own occurrence list, and chunks of long (Zipf-hot) segments are summed in parallel by different waves.
+// Summation order: ATen's, as torch.ops.aten.embedding_dense_backward computes it on this GPU
+// (aten/src/ATen/native/cuda/Embedding.cu embedding_dense_backward_cuda and EmbeddingBackwardKernel.cu, PyTorch
+// 2.10 / 2.11; third-party code the reference calls, restated here).  Every id's sum is ((0 + G1) + G2) + ..., G
+// the left-to-right sum of one group of that id's occurrences, taken in ascending occurrence index:
+//   n <= 3072 indices (embedding_backward_feature_kernel): a group is the id's occurrences inside one window of
+//       16 consecutive indices (the kernel's blockDim.y in ATen's ROCm build; 32 in its CUDA build);
+//   n >  3072 (embedding_backward_cuda_kernel on a stable sort): groups are the id's occurrences cut into runs of
+//       NROWS_PER_THREAD = 10 from its first.
+// ATen starts every group sum from zero as well; the total never is -0 (it starts at +0 and a rounded sum is -0
+// only when both terms are), so starting a group from its first gradient gives the same bits.  Long (Zipf-hot)
+// segments are cut into chunks of 6 groups summed in parallel by different waves (partial sums per group, added in
+// order by the segment's own wave).
 #include "elr_rowio.h"
 #include "elr_scan.h"
 
@@ -28,7 +35,11 @@ constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int64_t kSortTile = (int64_t)kSortThreads * kSortItems;
 constexpr int kRadixBins = 256;
-constexpr int kSegChunk = 64;
+constexpr int kAtenGroup = 10;                          // NROWS_PER_THREAD of ATen's sort path
+constexpr int kGroupsPerChunk = 6;
+constexpr int kSegChunk = kAtenGroup * kGroupsPerChunk;   // occurrences per parallel chunk (sort path)
+constexpr int64_t kAtenSmall = 3072;                      // ATen's windowed path up to this many indices
+constexpr int kAtenWinShift = 4;                          // its window: 16 indices
 constexpr int kSegBlock = 256;
 
 static_assert(kSortThreads == kRadixBins, "one histogram bin per sort thread");
@@ -256,22 +267,30 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __rest
   }
 }
 
-// Left-to-right sum of the gradients at sorted positions [p0, p1) (p1 - p0 <= 64), this lane's NQ elements
-// j = lane + 64 q (< D).  Occurrence indices are loaded once per wave and broadcast with readlane.
+// Does occurrence k of a segment (occurrence index o, previous one prev) start a new group?  Sort path
+// (win_shift == 0): every kAtenGroup occurrences; windowed path: when its index window differs from the previous
+// occurrence's.  Wave-uniform (all arguments are).
+__device__ __forceinline__ bool group_head(int64_t k, int32_t o, int32_t prev, int win_shift) {
+  return k == 0 || (win_shift ? (o >> win_shift) != (prev >> win_shift) : k % kAtenGroup == 0);
+}
+
+// Folds the gradients at sorted positions [p0, p1) (p1 - p0 <= 64), occurrences k0.. of their segment, into the
+// open group acc and the segment total tot (this lane's NQ elements j = lane + 64 q < D).  Occurrence indices are
+// loaded once per wave and broadcast with readlane; prev carries the previous occurrence index across calls.
 template <int NQ>
-__device__ __forceinline__ void chunk_sum(const float* __restrict__ grad, int64_t D, const int32_t* __restrict__ sv,
-                                          int64_t p0, int64_t p1, float (&acc)[NQ]) {
+__device__ __forceinline__ void fold_range(const float* __restrict__ grad, int64_t D, const int32_t* __restrict__ sv,
+                                           int64_t p0, int64_t p1, int64_t k0, int win_shift, int32_t& prev,
+                                           float (&acc)[NQ], float (&tot)[NQ]) {
   const int lane = threadIdx.x & 63;
   const int len = (int)(p1 - p0);
   const int32_t my = lane < len ? sv[p0 + lane] : 0;
   constexpr int UN = 8;
-  for (int k0 = 0; k0 < len; k0 += UN) {
+  for (int b0 = 0; b0 < len; b0 += UN) {
     float g[UN][NQ];
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int k = k0 + u;
-      if (k < len) {
-        const int64_t o = (int64_t)__builtin_amdgcn_readlane(my, k);
+      if (b0 + u < len) {
+        const int64_t o = (int64_t)__builtin_amdgcn_readlane(my, b0 + u);
         const float* row = grad + o * D;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
@@ -282,16 +301,28 @@ __device__ __forceinline__ void chunk_sum(const float* __restrict__ grad, int64_
     }
 #pragma unroll
     for (int u = 0; u < UN; ++u) {
-      const int k = k0 + u;
-      if (k < len) {
+      if (b0 + u < len) {
+        const int32_t o = __builtin_amdgcn_readlane(my, b0 + u);
+        const int64_t k = k0 + b0 + u;
+        if (group_head(k, o, prev, win_shift)) {
 #pragma unroll
-        for (int q = 0; q < NQ; ++q) acc[q] = k == 0 ? g[u][q] : acc[q] + g[u][q];
+          for (int q = 0; q < NQ; ++q) {
+            if (k) tot[q] = tot[q] + acc[q];
+            acc[q] = g[u][q];
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) acc[q] = acc[q] + g[u][q];
+        }
+        prev = o;
       }
     }
   }
 }
 
-// Sums of the extra chunks, one wave per chunk (grid-stride over the E work items).
+// Group sums of the extra chunks (sort path), one wave per chunk (grid-stride over the E work items): chunk wi's
+// group gi goes to parts row wi * kGroupsPerChunk + gi.  The rows of GB groups load together; the sums are stored
+// after the last load (a store in flight would hold up the wait for the next loads).
 template <int NQ>
 __global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ grad, int64_t D,
                                                       const int32_t* __restrict__ sv,
@@ -299,6 +330,9 @@ __global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ 
                                                       const int32_t* __restrict__ chunk_off,
                                                       const int32_t* __restrict__ chunk_seg,
                                                       const int64_t* __restrict__ d_E, float* __restrict__ parts) {
+  constexpr int GB = NQ == 1 ? 6 : (NQ == 2 ? 3 : 1);
+  constexpr int RB = GB * kAtenGroup;
+  static_assert(kGroupsPerChunk % GB == 0, "whole batches of groups per chunk");
   const int lane = threadIdx.x & 63;
   const int64_t E = *d_E;
   for (int64_t wi = wave_id(); wi < E; wi += wave_count()) {
@@ -308,18 +342,56 @@ __global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ 
     int64_t p1 = p0 + kSegChunk;
     const int64_t e = seg_start[u + 1];
     if (p1 > e) p1 = e;
-    float acc[NQ];
-    chunk_sum<NQ>(grad, D, sv, p0, p1, acc);
+    const int len = (int)(p1 - p0);
+    const int32_t my = lane < len ? sv[p0 + lane] : 0;
+    float acc[kGroupsPerChunk][NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
-      const int64_t j = lane + 64 * q;
-      if (j < D) parts[wi * D + j] = acc[q];
+    for (int b = 0; b < kGroupsPerChunk / GB; ++b) {
+      const int k0 = b * RB;
+      if (k0 >= len) break;
+      float g[RB][NQ];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (k0 + r < len) {
+          const int64_t o = (int64_t)__builtin_amdgcn_readlane(my, k0 + r);
+          const float* row = grad + o * D;
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+            const int64_t j = lane + 64 * q;
+            g[r][q] = j < D ? __builtin_nontemporal_load(row + j) : 0.0f;
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        if (k0 + r < len) {
+          const int gi = b * GB + r / kAtenGroup;
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) acc[gi][q] = r % kAtenGroup == 0 ? g[r][q] : acc[gi][q] + g[r][q];
+        }
+      }
+    }
+#pragma unroll
+    for (int gi = 0; gi < kGroupsPerChunk; ++gi) {
+      if (gi * kAtenGroup >= len) break;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int64_t j = lane + 64 * q;
+        if (j < D) parts[(wi * kGroupsPerChunk + gi) * D + j] = acc[gi][q];
+      }
     }
   }
 }
 
-// Final per-segment sum (chunk 0 summed here, then the extra chunks' partials in order), then either written to
-// out[uniq[u]] (MODE 0) or applied as an Adam step to state[uniq[u]] (MODE 1).  One wave per segment.
+// The group sums of a segment's extra chunks are consecutive parts rows from chunk_off[u] * kGroupsPerChunk (every
+// extra chunk but the last is full): ceil((L - kSegChunk) / kAtenGroup) of them.
+__device__ __forceinline__ int64_t seg_parts(int64_t L, int win_shift) {
+  return win_shift || L <= kSegChunk ? 0 : (L - kSegChunk + kAtenGroup - 1) / kAtenGroup;
+}
+
+// Final per-segment sum (the inline part -- the first chunk, or the whole segment on the windowed path -- then the
+// extra chunks' group sums in order), then either written to out[uniq[u]] (MODE 0) or applied as an Adam step to
+// state[uniq[u]] (MODE 1).  One wave per segment.
 template <int NQ, int MODE>
 __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ grad, int64_t D,
                                                    const int32_t* __restrict__ sv,
@@ -327,30 +399,50 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
                                                    const int64_t* __restrict__ uniq,
                                                    const int32_t* __restrict__ chunk_off,
                                                    const float* __restrict__ parts, const int64_t* __restrict__ d_U,
-                                                   float* __restrict__ out, int64_t nrows, AdamScalars s) {
+                                                   int win_shift, float* __restrict__ out, int64_t nrows,
+                                                   AdamScalars s) {
   const int lane = threadIdx.x & 63;
   const int64_t U = *d_U;
   for (int64_t u = wave_id(); u < U; u += wave_count()) {
     const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
     const int64_t L = s1 - s0;
     const int64_t row = uniq ? uniq[u] : u;   // NULL: segment u goes to row u
-    float acc[NQ];
-    chunk_sum<NQ>(grad, D, sv, s0, L < kSegChunk ? s1 : s0 + kSegChunk, acc);
-    const int64_t extra = (L - 1) / kSegChunk;
-    const int64_t pb = extra ? (int64_t)chunk_off[u] : 0;
-    for (int64_t c = 0; c < extra; ++c) {
+    const int64_t inl = win_shift ? L : (L < kSegChunk ? L : kSegChunk);
+    float acc[NQ], tot[NQ];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int64_t j = lane + 64 * q;
-        if (j < D) acc[q] = acc[q] + parts[(pb + c) * D + j];
-      }
+    for (int q = 0; q < NQ; ++q) acc[q] = tot[q] = 0.0f;
+    int32_t prev = 0;
+    for (int64_t b0 = 0; b0 < inl; b0 += 64)
+      fold_range<NQ>(grad, D, sv, s0 + b0, s0 + (inl - b0 < 64 ? inl : b0 + 64), b0, win_shift, prev, acc, tot);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) tot[q] = tot[q] + acc[q];
+    const int64_t np = seg_parts(L, win_shift);
+    const float* pr = np ? parts + (int64_t)chunk_off[u] * kGroupsPerChunk * D : parts;
+    constexpr int PB = 8;
+    for (int64_t c0 = 0; c0 < np; c0 += PB) {
+      float pc[PB][NQ];
+#pragma unroll
+      for (int e = 0; e < PB; ++e)
+        if (c0 + e < np) {
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+            const int64_t j = lane + 64 * q;
+            pc[e][q] = j < D ? pr[(c0 + e) * D + j] : 0.0f;
+          }
+        }
+#pragma unroll
+      for (int e = 0; e < PB; ++e)
+        if (c0 + e < np) {
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) tot[q] = tot[q] + pc[e][q];
+        }
     }
     if (row < 0 || row >= nrows) continue;
     if (MODE == 0) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         const int64_t j = lane + 64 * q;
-        if (j < D) out[row * D + j] = acc[q];
+        if (j < D) out[row * D + j] = tot[q];
       }
     } else {
       float* rec = out + row * 3 * D;
@@ -359,7 +451,7 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
         const int64_t j = lane + 64 * q;
         if (j < D) {
           float w = rec[j], m = rec[D + j], v = rec[2 * D + j];
-          adam_elem(w, m, v, acc[q], s);
+          adam_elem(w, m, v, tot[q], s);
           rec[j] = w;
           rec[D + j] = m;
           rec[2 * D + j] = v;
@@ -369,11 +461,11 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
   }
 }
 
-// Wave-per-row form of k_seg_final for D = 64*VPL (lane l holds floats [l*VPL, l*VPL + VPL)): no loop, each
-// wave owns kSegPerWave consecutive segments starting at u_base + wave * kSegPerWave; waves past U exit.  All
-// per-segment metadata (bounds, row id, first occurrence) are scalar loads issued together, then the first
-// gradient row, the row's w, m, v (MODE 1) and the chunk's remaining occurrence indices load in parallel: a
-// one-occurrence segment -- the common case -- costs two dependent memory round trips.
+// Wave-per-row form of k_seg_final for D = 64*VPL (lane l holds floats [l*VPL, l*VPL + VPL)): no grid-stride
+// loop, each wave owns kSegPerWave consecutive segments starting at u_base + wave * kSegPerWave; waves past U exit.
+// All per-segment metadata (bounds, row id, first occurrence) are scalar loads issued together, then the first
+// gradient row, the row's w, m, v (MODE 1) and the next 63 occurrence indices load in parallel: a one-occurrence
+// segment -- the common case -- costs two dependent memory round trips.
 #ifndef ELR_SEG_SW
 #define ELR_SEG_SW 2
 #endif
@@ -388,7 +480,8 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
                                                        const int32_t* __restrict__ chunk_off,
                                                        const float* __restrict__ parts,
                                                        const int64_t* __restrict__ d_U, int64_t u_base,
-                                                       float* __restrict__ out, int64_t nrows, AdamScalars s) {
+                                                       int win_shift, float* __restrict__ out, int64_t nrows,
+                                                       AdamScalars s) {
   constexpr int64_t D = 64 * VPL;
   constexpr int SW = kSegPerWave;
   const int lane = threadIdx.x & 63;
@@ -419,38 +512,66 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
       m[q] = frag_load<VPL, false>(rec + D);
       v[q] = frag_load<VPL, false>(rec + 2 * D);
     }
-    const int64_t l0 = len[q] < kSegChunk ? len[q] : kSegChunk;
-    my[q] = (lane >= 1 && lane < l0) ? sv[s0[q] + lane] : 0;
+    my[q] = (lane >= 1 && lane < len[q]) ? sv[s0[q] + lane] : 0;
   }
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
     if (!ok[q]) continue;
-    const int l0 = (int)(len[q] < kSegChunk ? len[q] : kSegChunk);
+    // occurrences [1, inl) fold here: the first chunk (sort path) or the whole segment (windowed path)
+    const int64_t inl = win_shift ? len[q] : (len[q] < kSegChunk ? len[q] : kSegChunk);
+    RowFrag<VPL> tot = frag_zero<VPL>();
+    int32_t prev = (int32_t)o0[q];
+    int32_t mb = my[q];
     constexpr int UN = 8;
-    for (int k0 = 1; k0 < l0; k0 += UN) {
-      RowFrag<VPL> g[UN];
+    for (int64_t b0 = 0; b0 < inl; b0 += 64) {
+      if (b0) mb = lane < inl - b0 ? sv[s0[q] + b0 + lane] : 0;
+      const int bl = (int)(inl - b0 < 64 ? inl - b0 : 64);
+      for (int k0 = b0 ? 0 : 1; k0 < bl; k0 += UN) {
+        RowFrag<VPL> g[UN];
 #pragma unroll
-      for (int e = 0; e < UN; ++e)
-        if (k0 + e < l0) {
-          const int64_t o = (int64_t)__builtin_amdgcn_readlane(my[q], k0 + e);
-          g[e] = frag_load<VPL, true>(grad + o * D + lane * VPL);
-        }
+        for (int e = 0; e < UN; ++e)
+          if (k0 + e < bl) {
+            const int64_t o = (int64_t)__builtin_amdgcn_readlane(mb, k0 + e);
+            g[e] = frag_load<VPL, true>(grad + o * D + lane * VPL);
+          }
 #pragma unroll
-      for (int e = 0; e < UN; ++e)
-        if (k0 + e < l0) {
+        for (int e = 0; e < UN; ++e)
+          if (k0 + e < bl) {
+            const int32_t o = __builtin_amdgcn_readlane(mb, k0 + e);
+            if (group_head(b0 + k0 + e, o, prev, win_shift)) {
 #pragma unroll
-          for (int j = 0; j < VPL; ++j) acc[q].v[j] = acc[q].v[j] + g[e].v[j];
-        }
-    }
-    const int64_t extra = (len[q] - 1) / kSegChunk;
-    if (extra) {
-      const int64_t pb = (int64_t)chunk_off[u0 + q];
-      for (int64_t c = 0; c < extra; ++c) {
-        const RowFrag<VPL> pc = frag_load<VPL, false>(parts + (pb + c) * D + lane * VPL);
+              for (int j = 0; j < VPL; ++j) {
+                tot.v[j] = tot.v[j] + acc[q].v[j];
+                acc[q].v[j] = g[e].v[j];
+              }
+            } else {
 #pragma unroll
-        for (int j = 0; j < VPL; ++j) acc[q].v[j] = acc[q].v[j] + pc.v[j];
+              for (int j = 0; j < VPL; ++j) acc[q].v[j] = acc[q].v[j] + g[e].v[j];
+            }
+            prev = o;
+          }
       }
     }
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) tot.v[j] = tot.v[j] + acc[q].v[j];
+    const int64_t np = seg_parts(len[q], win_shift);
+    if (np) {
+      const float* pr = parts + (int64_t)chunk_off[u0 + q] * kGroupsPerChunk * D + lane * VPL;
+      constexpr int PB = VPL <= 2 ? 16 : 32 / VPL;   // group sums loaded together, added in order
+      for (int64_t c0 = 0; c0 < np; c0 += PB) {
+        RowFrag<VPL> pc[PB];
+#pragma unroll
+        for (int e = 0; e < PB; ++e)
+          if (c0 + e < np) pc[e] = frag_load<VPL, false>(pr + (c0 + e) * D);
+#pragma unroll
+        for (int e = 0; e < PB; ++e)
+          if (c0 + e < np) {
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) tot.v[j] = tot.v[j] + pc[e].v[j];
+          }
+      }
+    }
+    acc[q] = tot;
   }
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
@@ -483,8 +604,8 @@ struct DedupScratch {
   int64_t* seg_start; // [n + 1]
   int32_t* seg_occ0;  // [n] first occurrence index of each segment
   int32_t* chunk_off; // [n]
-  int32_t* chunk_seg; // [n / 64 + 1]
-  float* parts;       // [(n / 64 + 1) * D]
+  int32_t* chunk_seg; // [n / kSegChunk + 1]
+  float* parts;       // [(n / kSegChunk + 1) * kGroupsPerChunk * D] group sums of the extra chunks
 };
 
 inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void* base) {
@@ -510,7 +631,7 @@ inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void
   s.seg_occ0 = (int32_t*)take(n * 4);
   s.chunk_off = (int32_t*)take(n * 4);
   s.chunk_seg = (int32_t*)take(nch * 4);
-  s.parts = (float*)take(nch * D * 4);
+  s.parts = (float*)take(nch * kGroupsPerChunk * D * 4);
   if (out) *out = s;
   return o;
 }
@@ -557,7 +678,11 @@ static int dedup_core(const int64_t* ids, int64_t n, int key_bits, DedupScratch&
   return cur;
 }
 
+// ATen's windowed order applies up to kAtenSmall indices: returns the window's shift there, 0 on the sort path.
+inline int win_shift_for(int64_t n) { return n <= kAtenSmall ? kAtenWinShift : 0; }
+
 static void chunk_plan(int64_t n, DedupScratch& S, hipStream_t st) {
+  if (win_shift_for(n)) return;   // the windowed path sums every segment in one wave: no extra chunks
   const int64_t nblk = cdiv(n, kSegTile);
   k_chunk_count<<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum);
   k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1);
@@ -576,24 +701,28 @@ inline unsigned wave_grid(int64_t items) {
 template <int NQ, int MODE>
 static void seg_reduce(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
                        int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
-  k_seg_partials<NQ><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
-                                                                    S.chunk_seg, S.d_tot + 1, S.parts);
+  const int ws = win_shift_for(n);
+  if (!ws)
+    k_seg_partials<NQ><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
+                                                                      S.chunk_seg, S.d_tot + 1, S.parts);
   k_seg_final<NQ, MODE><<<wave_grid(n), 256, 0, st>>>(grad, D, sv, S.seg_start, uniq, S.chunk_off, S.parts, S.d_tot,
-                                                       out, nrows, s);
+                                                       ws, out, nrows, s);
 }
 
 template <int VPL, int MODE>
 static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S, const int64_t* uniq, int64_t n,
                            float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
   constexpr int64_t D = 64 * VPL;
-  k_seg_partials<VPL><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
-                                                                     S.chunk_seg, S.d_tot + 1, S.parts);
+  const int ws = win_shift_for(n);
+  if (!ws)
+    k_seg_partials<VPL><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
+                                                                       S.chunk_seg, S.d_tot + 1, S.parts);
   // one launch per range of at most 2^22 blocks (4 waves of kSegPerWave segments each); U <= n
   const int64_t per = kOneShotBlocks * 4 * kSegPerWave;
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
     k_seg_final_wpr<VPL, MODE><<<(unsigned)cdiv(m, 4 * kSegPerWave), 256, 0, st>>>(
-        grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a, out, nrows, s);
+        grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a, ws, out, nrows, s);
   }
 }
 

@@ -7,13 +7,15 @@
     embedding_dense_backward(grad, inv, num_weights, padding_idx=-1, scale_grad_by_freq=False) -> [num_weights, D]
                                                   aten.embedding_dense_backward as srm2/train.py:429 calls it
     adam_dedup(pool, ids, grad, lr, b1, b2, eps, step)
-                                                  dedup + fixed-order segment sum + row-sparse Adam on pool[id]
+                                                  dedup + segment sum in ATen's order + row-sparse Adam on pool[id]
                                                   (config C3: one Adam step per unique id of a batch)
 
-Summation order of duplicate ids (this build's definition; the reference's belongs to ATen and is pinned by no
-reference test): per id, the occurrences in ascending occurrence index are cut into chunks of 64, each chunk is
-summed left to right, and the chunk sums are added left to right.  All three run as HIP kernels
-(elara_amd/csrc/dedup.hip) on torch's current stream.
+Summation order of duplicate ids: ATen's embedding_dense_backward as it runs on this GPU (third-party code the
+reference calls; aten/src/ATen/native/cuda/Embedding.cu, EmbeddingBackwardKernel.cu).  Up to 3072 indices, per
+window of 16 consecutive indices an id's gradients are summed left to right and the window sums are added into a
+zeroed row; above 3072, an id's occurrences in ascending index are cut into runs of 10, each run summed from zero,
+and the run sums added from zero.  Equal bits to torch.ops.aten.embedding_dense_backward on the same inputs.  All
+of it runs as HIP kernels (elara_amd/csrc/dedup.hip) on torch's current stream.
 """
 import torch
 
@@ -119,7 +121,7 @@ def unique_plan_async(ids, D, bound=None):
 
 def segment_sum_plan(grad, plan, out=None, perm=None):
     """Per-segment sums of grad [n, D] over a unique_plan: segment u into row perm[u] (or u) of out [rows, D]
-    (allocated [U, D] when None), in the fixed summation order of embedding_dense_backward."""
+    (allocated [U, D] when None), in embedding_dense_backward's summation order for n = plan.n indices."""
     n, D = plan.n, plan.D
     if not (grad.is_cuda and grad.dtype == torch.float32 and grad.numel() == n * D):
         raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements')
@@ -145,7 +147,7 @@ def segment_sum_plan(grad, plan, out=None, perm=None):
 
 def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1, scale_grad_by_freq=False):
     """[num_weights, D] per-row sums of grad_output [n, D] over indices [n] (rows without an index are zero), in
-    this build's fixed summation order.  Supports the reference's call (padding_idx=-1, no frequency scaling)."""
+    ATen's summation order.  Supports the reference's call (padding_idx=-1, no frequency scaling)."""
     if padding_idx != -1 or scale_grad_by_freq:
         raise RuntimeError('embedding_dense_backward: only padding_idx=-1 and scale_grad_by_freq=False are supported')
     idx = _ids(indices, 'indices')

@@ -10,7 +10,7 @@ Per step: plan (classify the batch's unique rows into hit / N / L / F / S classe
 directory call B), assemble (counter-hash init of N rows, replay of L rows from the log arena, gather of F rows
 from MAT), then update (Adam on hits, evictions to MAT or back to the log arena, Adam on N/L rows being admitted or
 compacted, log appends, transient Adam of M rows).  The dense model is not part of this path: the caller supplies
-the per-occurrence gradients, which are reduced per unique row (dedup + fixed-order segment sum) as the reference's
+the per-occurrence gradients, which are reduced per unique row (dedup + segment sum in ATen's order) as the reference's
 embedding backward does (srm2/train.py:352, 429).
 
 Layout.  The planner sorts the batch's unique rows by class rank (hits; admitted N, L, F; appended N, L; compacted

@@ -157,9 +157,10 @@ int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a
 
 /* ---------------------------------------------------------------------------------------------------------
  * Batch dedup and duplicate-id gradient reduction.
- * Summation order (this build's definition; the reference's is ATen's embedding backward and no reference test
- * pins it): per id, occurrences in ascending occurrence index are cut into chunks of 64; each chunk is summed left
- * to right from its first gradient, and the chunk sums are added left to right from the first chunk.  n < 2^31.
+ * Summation order: ATen's embedding_dense_backward on this GPU (aten/src/ATen/native/cuda/Embedding.cu,
+ * EmbeddingBackwardKernel.cu), equal bits.  n <= 3072: per window of 16 consecutive indices an id's gradients are
+ * summed left to right and the window sums added into a zeroed row; n > 3072: an id's occurrences in ascending
+ * index are cut into runs of 10, each run summed from zero, and the run sums added from zero.  n < 2^31.
  * ------------------------------------------------------------------------------------------------------- */
 
 /* Bytes of device scratch elr_unique / elr_segment_sum / elr_adam_dedup need for n occurrences of width D
@@ -188,8 +189,8 @@ int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* gra
  * embedding backward): elr_dedup_plan is elr_unique that keeps its sort -- sorted positions, segment starts, first
  * occurrences, the chunk plan and U -- in `plan` (elr_dedup_plan_bytes(n, D) bytes, the width D of the gradients to
  * be summed later).  elr_segment_sum_plan then sums a gradient batch grad [n, D] over that plan, segment u (the
- * u-th smallest id) into out[perm ? perm[u] : u] (out_rows rows; rows out of range are skipped), in the same fixed
- * order as elr_segment_sum.  key_bits must be the value given to elr_dedup_plan. */
+ * u-th smallest id) into out[perm ? perm[u] : u] (out_rows rows; rows out of range are skipped), in the same
+ * order as elr_segment_sum for n indices.  key_bits must be the value given to elr_dedup_plan. */
 int64_t elr_dedup_plan_bytes(int64_t n, int64_t D);
 int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, int64_t* inverse, int64_t* n_unique,
                    void* plan, int64_t plan_bytes, int64_t D, void* stream);

@@ -22,13 +22,11 @@ How each function is pinned (checked against something other than itself; tests 
                      seeds >= 2^31, D not a power of two); range [-bound, bound), w0(0,0,seed 0) = -bound
   orc_replay_rows    == Triton golden vectors of srm2/gpu_ops.py _replay; == init + eager reference cpu_adam
                      (oracle/_ref) at the logged steps (test_replay.py:22-33 as an assertion)
-  orc_segment_sum    this build defines the order (per id: ascending occurrence index in chunks of 64, each chunk
-                     left to right, then the chunk sums left to right); pinned by properties a wrong order fails
-                     (<= 64 occurrences == plain left-to-right sum, an observable 200-occurrence case, independence
-                     from the interleaving of other ids, torch.unique ordering, column totals)
-                     [tests/test_dedup.py].  The reference's own duplicate-gradient sum order belongs to ATen
-                     (embedding_dense_backward) and is pinned by no reference test: parity with the reference is
-                     UNPINNED for that order.
+  orc_segment_sum    == ATen's embedding_dense_backward (the op srm2/train.py:429 calls) run on the GPU, bitwise, on
+                     both of its paths: <= 3072 indices (windows of 16) and the sorted path (runs of 10 from zero),
+                     hot ids, all -0.0 ids (tests/golden/aten_segsum.npz, made by make_aten_segsum.py); properties
+                     of both orders that other window or run lengths fail; torch.unique ordering and inverse;
+                     column totals  [tests/test_dedup.py, tests/test_oracle.py]
   orc_dir_a/b        == reference elara_dir_a/elara_dir_b from oracle/_ref run on CPU tensors, whole directory
                      state and every output compared, over 60-step planner simulations in 5 configurations
                      (tests/dirsim.py); a hand-worked allocation sequence; invariants of srm2/train.py:474-477

@@ -183,14 +183,22 @@ int orc_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t 
 /* ---------------------------------------------------------------------------------------------------------
  * Duplicate-id reduction (dedup + per-id gradient sum), the step before Adam for a batch with repeated ids
  * (srm2/train.py:352 torch.unique(..., return_inverse=True) and train.py:429 embedding_dense_backward).
- * Unique ids come out ascending (torch.unique's definition).  The summation order of the reference's
- * embedding backward belongs to ATen and is pinned by no reference test, so this build fixes its own order:
- * the occurrences of one id, in ascending occurrence index, are cut into chunks of ORC_SEG_CHUNK; each chunk is
- * summed left to right starting from its first gradient, and the chunk sums are added left to right starting
- * from the first chunk (for at most ORC_SEG_CHUNK occurrences: the plain left-to-right sum).  Returns the number
- * of unique ids.
+ * Unique ids come out ascending (torch.unique's definition).  The sums follow ATen's
+ * embedding_dense_backward as its ROCm build runs on the GPU (PyTorch 2.10 / 2.11, third-party code the reference
+ * calls; aten/src/ATen/native/cuda/Embedding.cu embedding_dense_backward_cuda), restated kernel by kernel:
+ *  - at most ORC_ATEN_SMALL indices (embedding_backward_feature_kernel): the indices are taken in windows of
+ *    ORC_ATEN_WINDOW consecutive positions (the kernel's blockDim.y: 16 in the ROCm build, 32 in the CUDA build);
+ *    in a window the first position of each id sums that id's gradients of the window left to right, starting
+ *    from its own, and adds the sum into the id's output row, which starts at zero;
+ *  - more indices (EmbeddingBackwardKernel.cu embedding_backward_cuda_kernel): a stable sort of the indices
+ *    groups each id's occurrences in ascending position; they are cut into partial segments of
+ *    NROWS_PER_THREAD = 10 from the id's first, each summed from zero (compute_grad_weight), and an id's partial
+ *    sums are added from zero in order (sum_and_scatter).
+ * Returns the number of unique ids.
  * ------------------------------------------------------------------------------------------------------- */
-#define ORC_SEG_CHUNK 64
+#define ORC_ATEN_SMALL 3072
+#define ORC_ATEN_WINDOW 16
+#define ORC_ATEN_NROWS 10
 
 static const int64_t* g_sort_ids;
 static int cmp_occ(const void* a, const void* b) {
@@ -203,34 +211,61 @@ static int cmp_occ(const void* a, const void* b) {
 int64_t orc_segment_sum(const int64_t* ids, const float* grad, int64_t nocc, int64_t D, int64_t* uniq,
                         float* gsum, int64_t* inverse) {
   int64_t* ord = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nocc > 0 ? nocc : 1));
+  int64_t* inv = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nocc > 0 ? nocc : 1));
   float* part = (float*)malloc(sizeof(float) * (size_t)(D > 0 ? D : 1));
+  float* tot = (float*)malloc(sizeof(float) * (size_t)(D > 0 ? D : 1));
   for (int64_t i = 0; i < nocc; ++i) ord[i] = i;
   g_sort_ids = ids;
-  qsort(ord, (size_t)nocc, sizeof(int64_t), cmp_occ);
-  int64_t u = -1;
+  qsort(ord, (size_t)nocc, sizeof(int64_t), cmp_occ);   /* ties by position: a stable sort */
+  int64_t U = 0;
   for (int64_t q0 = 0; q0 < nocc;) {
     int64_t q1 = q0 + 1;
     while (q1 < nocc && ids[ord[q1]] == ids[ord[q0]]) ++q1;
-    ++u;
-    uniq[u] = ids[ord[q0]];
-    float* s = gsum + u * D;
-    for (int64_t c0 = q0; c0 < q1; c0 += ORC_SEG_CHUNK) {
-      const int64_t c1 = c0 + ORC_SEG_CHUNK < q1 ? c0 + ORC_SEG_CHUNK : q1;
-      memcpy(part, grad + ord[c0] * D, sizeof(float) * (size_t)D);
-      for (int64_t q = c0 + 1; q < c1; ++q) {
-        const float* g = grad + ord[q] * D;
-        for (int64_t j = 0; j < D; ++j) part[j] = part[j] + g[j];
+    uniq[U] = ids[ord[q0]];
+    for (int64_t q = q0; q < q1; ++q) inv[ord[q]] = U;
+    if (nocc > ORC_ATEN_SMALL) {
+      /* sort path: partial segments of ORC_ATEN_NROWS, each summed from zero; partial sums added from zero */
+      for (int64_t j = 0; j < D; ++j) tot[j] = 0.0f;
+      for (int64_t c0 = q0; c0 < q1; c0 += ORC_ATEN_NROWS) {
+        const int64_t c1 = c0 + ORC_ATEN_NROWS < q1 ? c0 + ORC_ATEN_NROWS : q1;
+        for (int64_t j = 0; j < D; ++j) part[j] = 0.0f;
+        for (int64_t q = c0; q < c1; ++q) {
+          const float* g = grad + ord[q] * D;
+          for (int64_t j = 0; j < D; ++j) part[j] = part[j] + g[j];
+        }
+        for (int64_t j = 0; j < D; ++j) tot[j] = tot[j] + part[j];
       }
-      if (c0 == q0) memcpy(s, part, sizeof(float) * (size_t)D);
-      else for (int64_t j = 0; j < D; ++j) s[j] = s[j] + part[j];
+      memcpy(gsum + U * D, tot, sizeof(float) * (size_t)D);
     }
-    if (inverse)
-      for (int64_t q = q0; q < q1; ++q) inverse[ord[q]] = u;
+    ++U;
     q0 = q1;
   }
+  if (nocc <= ORC_ATEN_SMALL) {
+    /* windowed path, window by window in position order */
+    for (int64_t u = 0; u < U * D; ++u) gsum[u] = 0.0f;
+    for (int64_t w0 = 0; w0 < nocc; w0 += ORC_ATEN_WINDOW) {
+      const int64_t w1 = w0 + ORC_ATEN_WINDOW < nocc ? w0 + ORC_ATEN_WINDOW : nocc;
+      for (int64_t p = w0; p < w1; ++p) {
+        int leader = 1;
+        for (int64_t q = w0; q < p; ++q) leader &= ids[q] != ids[p];
+        if (!leader) continue;
+        memcpy(part, grad + p * D, sizeof(float) * (size_t)D);
+        for (int64_t q = p + 1; q < w1; ++q)
+          if (ids[q] == ids[p]) {
+            const float* g = grad + q * D;
+            for (int64_t j = 0; j < D; ++j) part[j] = part[j] + g[j];
+          }
+        float* s = gsum + inv[p] * D;
+        for (int64_t j = 0; j < D; ++j) s[j] = s[j] + part[j];
+      }
+    }
+  }
+  if (inverse) memcpy(inverse, inv, sizeof(int64_t) * (size_t)nocc);
   free(ord);
+  free(inv);
   free(part);
-  return u + 1;
+  free(tot);
+  return U;
 }
 
 /* =========================================================================================================

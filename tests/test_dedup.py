@@ -1,11 +1,16 @@
 """Batch dedup and duplicate-id gradient reduction (srm2/train.py:352 torch.unique, train.py:429
 embedding_dense_backward) and the fused duplicate-id Adam of config C3.
 
-The reference's summation order belongs to ATen and is pinned by no reference test ("parity unpinned"); this
-build defines the order (per id, ascending occurrence index, chunks of 64 summed left to right, chunk sums added
-left to right).  The CPU tests pin the oracle's restatement of that order by properties that a wrong order or a
-dropped term fails; the GPU tests hold the HIP path to the oracle bitwise.
+The sums follow ATen's embedding_dense_backward on this GPU (third-party code the reference calls): up to 3072
+indices, per window of 16 consecutive indices the id's gradients left to right, the window sums added into a zeroed
+row; above, per id its occurrences in runs of 10, each run summed from zero, the run sums added from zero.  The CPU
+tests pin the oracle against ATen's own output (tests/golden/aten_segsum.npz, made on the GPU by
+tests/golden/make_aten_segsum.py) and by properties of the two orders; the GPU tests hold the HIP path to the
+oracle and to the live ATen op bitwise.
 """
+import importlib.util
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -14,61 +19,107 @@ from elara_amd import synth
 from oracle import oracle as O
 
 HP = synth.ADAM
+GOLDEN = Path(__file__).resolve().parent / 'golden'
+ATEN_SMALL = 3072
+
+
+def golden_module():
+    spec = importlib.util.spec_from_file_location('make_aten_segsum', GOLDEN / 'make_aten_segsum.py')
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
 
 
 def bits(a):
     return np.ascontiguousarray(a).view(np.uint32)
 
 
-def lr_sum(rows):
-    """Plain left-to-right float32 sum of rows[0], rows[1], ... starting from rows[0]."""
-    acc = rows[0].astype(np.float32).copy()
+def lr_sum(rows, start=None):
+    """Left-to-right float32 sum of rows, starting from `start` (None: from rows[0])."""
+    acc = rows[0].astype(np.float32).copy() if start is None else np.float32(start) + rows[0]
     for r in rows[1:]:
         acc = (acc + r).astype(np.float32)
     return acc
 
 
+def full_sums(ids, g, U):
+    """Oracle sums as a [U, D] table (rows without an id are zero), as embedding_dense_backward returns them."""
+    u, s, _ = O.segment_sum(ids, g)
+    out = np.zeros((U, g.shape[1]), np.float32)
+    out[u] = s
+    return out
+
+
 # ------------------------------------------------------------------------------------------------------------ CPU
-def test_oracle_segment_sum_short_segments_are_left_to_right():
-    rng = np.random.default_rng(0)
-    ids = rng.integers(0, 300, 5000).astype(np.int64)          # every id occurs well under 64 times
-    g = (rng.standard_normal((5000, 16)) * 10.0 ** rng.integers(-6, 3, (5000, 1))).astype(np.float32)
-    u, s, inv = O.segment_sum(ids, g)
-    assert np.array_equal(u, np.unique(ids)) and np.array_equal(u[inv], ids)
-    for q, i in enumerate(u):
-        assert np.array_equal(bits(s[q]), bits(lr_sum(g[ids == i])))
+def test_oracle_segment_sum_matches_aten_golden():
+    """The oracle reproduces ATen's embedding_dense_backward bit for bit on both of its paths (fixture made by
+    running the ATen op on the GPU)."""
+    mod = golden_module()
+    z = np.load(GOLDEN / 'aten_segsum.npz')
+    assert np.array_equal(z['cases'], mod.CASES)
+    for ci, c in enumerate(mod.CASES):
+        ids, g = mod.case_inputs(*c)
+        assert np.array_equal(mod.checksum(ids, g), z[f'case{ci}_sum']), ci       # same inputs as ATen saw
+        assert np.array_equal(bits(full_sums(ids, g, int(c[1]))), z[f'case{ci}_out']), ci
 
 
-def test_oracle_segment_sum_chunked_order_for_long_segments():
-    """An id with 200 occurrences: chunks [0,64), [64,128), [128,192), [192,200) summed left to right, then the
-    four chunk sums left to right.  Values are chosen so that the plain left-to-right sum differs."""
+def test_oracle_sort_path_sums_runs_of_ten_from_zero():
+    """Above 3072 indices: an id with 205 occurrences (interleaved with 3000 distinct others) sums runs of 10 from
+    zero, then the run sums from zero.  Values are chosen so that the plain left-to-right sum and runs of other
+    lengths give different bits, and a column of -0.0 comes out +0.0."""
     rng = np.random.default_rng(1)
-    n = 200
-    ids = np.full(n, 7, np.int64)
-    g = np.zeros((n, 4), np.float32)
-    g[:, 0] = rng.standard_normal(n).astype(np.float32) * np.float32(1e-3)
-    g[0, 1], g[1:, 1] = np.float32(1.0), np.float32(2.0 ** -24)  # left to right drops every small term; chunked keeps some
-    g[:, 2] = (rng.standard_normal(n) * 1e4).astype(np.float32)
-    g[:, 3] = np.float32(-0.0)
-    _, s, _ = O.segment_sum(ids, g)
-    parts = [lr_sum(g[c:c + 64]) for c in range(0, n, 64)]
-    want = lr_sum(np.stack(parts))
-    assert np.array_equal(bits(s[0]), bits(want))
-    assert s[0, 1] != lr_sum(g)[1]                               # the order is observable
-    assert bits(s[0])[3] == bits(np.float32(-0.0))               # -0 + -0 stays -0: sums start from the first term
+    n_hot, n = 205, 205 + 3000
+    pos = np.sort(rng.choice(n, n_hot, replace=False))
+    ids = np.arange(10, 10 + n, dtype=np.int64)
+    ids[pos] = 7
+    g = (rng.standard_normal((n, 4)) * 1e4).astype(np.float32)
+    hot = np.zeros((n_hot, 4), np.float32)
+    hot[:, 0] = rng.standard_normal(n_hot).astype(np.float32) * np.float32(1e-3)
+    hot[0, 1], hot[1:, 1] = np.float32(1.0), np.float32(2.0 ** -24)
+    hot[:, 2] = (rng.standard_normal(n_hot) * 1e4).astype(np.float32)
+    hot[:, 3] = np.float32(-0.0)
+    g[pos] = hot
+    assert n > ATEN_SMALL
+    u, s, _ = O.segment_sum(ids, g)
+    got = s[np.searchsorted(u, 7)]
+    runs = lambda L: lr_sum(np.stack([lr_sum(hot[c:c + L], 0.0) for c in range(0, n_hot, L)]), 0.0)  # noqa: E731
+    assert np.array_equal(bits(got), bits(runs(10)))
+    for other in (lr_sum(hot), runs(64), runs(9), runs(11)):
+        assert not np.array_equal(bits(got), bits(other))
+    assert bits(got)[3] == 0                                                   # -0 sums to +0
 
 
-def test_oracle_segment_sum_depends_only_on_each_ids_occurrence_order():
-    """Interleaving other ids differently does not change an id's sum (order = its own occurrence order)."""
+def test_oracle_window_path_sums_windows_of_sixteen():
+    """Up to 3072 indices: per window of 16 positions the id's gradients left to right, then the window sums added
+    to a zero row.  Id 5 sits at positions 3, 9, 15 (window 0), 16, 30 (window 1) and 47 (window 2)."""
+    rng = np.random.default_rng(4)
+    n = 60
+    ids = rng.integers(20, 40, n).astype(np.int64)
+    at = [3, 9, 15, 16, 30, 47]
+    ids[at] = 5
+    g = (rng.standard_normal((n, 6)) * np.exp2(rng.integers(-20, 20, (n, 6)))).astype(np.float32)
+    g[at, 0] = np.float32(2.0 ** -24)
+    g[3, 0] = np.float32(1.0)          # windows of 16: (1 + e + e) + (e + e) keeps 2e; one group or 32 keeps none
+    g[at, 5] = np.float32(-0.0)
+    got = full_sums(ids, g, 40)[5]
+    win = lambda groups: lr_sum(np.stack([lr_sum(g[q]) for q in groups]), 0.0)  # noqa: E731
+    want = win([[3, 9, 15], [16, 30], [47]])
+    assert np.array_equal(bits(got), bits(want))
+    assert not np.array_equal(bits(got), bits(win([[3, 9, 15, 16, 30], [47]])))     # windows of 32
+    assert not np.array_equal(bits(got), bits(lr_sum(g[at], 0.0)))                    # one group
+    assert bits(got)[5] == 0
+
+
+def test_oracle_sort_path_depends_only_on_each_ids_occurrence_order():
+    """Above 3072 indices, interleaving other ids differently does not change an id's sum."""
     rng = np.random.default_rng(2)
-    a = (rng.standard_normal((150, 8)) * 1e3).astype(np.float32)
-    b = (rng.standard_normal((90, 8))).astype(np.float32)
-    x_ids = np.concatenate([np.full(150, 3), np.full(90, 9)]).astype(np.int64)
+    a = (rng.standard_normal((2150, 8)) * 1e3).astype(np.float32)
+    b = (rng.standard_normal((1090, 8))).astype(np.float32)
+    x_ids = np.concatenate([np.full(2150, 3), np.full(1090, 9)]).astype(np.int64)
     x_g = np.concatenate([a, b])
-    perm = rng.permutation(240)
-    # keep each id's own relative order: stable sort of the permuted positions per id
-    order = np.concatenate([np.sort(perm[:150]), np.sort(perm[150:])])
-    y_ids = np.empty(240, np.int64)
+    perm = rng.permutation(3240)
+    order = np.concatenate([np.sort(perm[:2150]), np.sort(perm[2150:])])   # each id keeps its own order
+    y_ids = np.empty(3240, np.int64)
     y_g = np.empty_like(x_g)
     y_ids[order] = x_ids
     y_g[order] = x_g
@@ -140,6 +191,46 @@ def test_gpu_embedding_backward_matches_oracle(dev, D):
     want = np.zeros((50000, D), np.float32)
     want[u] = s
     assert np.array_equal(bits(out2.cpu().numpy()), bits(want))
+
+
+ATEN_CASES = [(40, 3, 64), (700, 20, 128), (3072, 9, 256), (3072, 400, 30), (3073, 9, 128), (3073, 7, 512),
+              (20000, 600, 200), (120000, 1000, 128)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('n,U,D', ATEN_CASES)
+def test_gpu_embedding_backward_matches_aten(dev, n, U, D):
+    """Bitwise equal to torch.ops.aten.embedding_dense_backward run on the same GPU (the call of
+    srm2/train.py:429), on ATen's windowed path (n <= 3072) and its sorted path, with a hot id, -0.0 gradients and
+    gradients over 2^-20 .. 2^20; also through the dedup plan (segment_sum_plan over the inverse)."""
+    from elara_amd.dedup import embedding_dense_backward, segment_sum_plan, unique_plan
+    print(f'[gpu-test] aten segment sum n={n} U={U} D={D}', flush=True)
+    ids, g = golden_module().case_inputs(n, U, D, n + U, U - 1, 3)
+    gd, idd = torch.from_numpy(g).to(dev), torch.from_numpy(ids).to(dev)
+    want = torch.ops.aten.embedding_dense_backward(gd, idd, U, -1, False)
+    got = embedding_dense_backward(gd, idd, U)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got.cpu().numpy()), bits(want.cpu().numpy()))
+    assert np.array_equal(bits(got.cpu().numpy()), bits(full_sums(ids, g, U)))
+    u, plan = unique_plan(idd, D, U)
+    out = torch.zeros(U, D, device=dev)
+    segment_sum_plan(gd, plan, out, u)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want.cpu().numpy()))
+
+
+@pytest.mark.gpu
+def test_gpu_aten_golden_cases(dev):
+    """The HIP sum reproduces the committed ATen vectors (both paths, -0.0 ids, hot ids)."""
+    from elara_amd.dedup import embedding_dense_backward
+    mod = golden_module()
+    z = np.load(GOLDEN / 'aten_segsum.npz')
+    for ci, c in enumerate(mod.CASES):
+        print(f'[gpu-test] aten golden case {ci}', flush=True)
+        ids, g = mod.case_inputs(*c)
+        got = embedding_dense_backward(torch.from_numpy(g).to(dev), torch.from_numpy(ids).to(dev), int(c[1]))
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got.cpu().numpy()), z[f'case{ci}_out']), ci
 
 
 @pytest.mark.gpu

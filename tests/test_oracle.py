@@ -183,9 +183,16 @@ def test_segment_sum_order_and_values():
     assert np.array_equal(u[inv], ids)
     tu, tinv = torch.unique(torch.from_numpy(ids), return_inverse=True)
     assert np.array_equal(tu.numpy(), u) and np.array_equal(tinv.numpy(), inv)
+    # 600 indices: ATen's windowed path.  Per id, its occurrences grouped by window (index // 16), each group
+    # summed left to right, the group sums added to zero -- the per-id form the HIP kernels use, against the
+    # oracle's window-by-window form.
     for q, i in enumerate(u):
         occ = np.nonzero(ids == i)[0]
-        acc = g[occ[0]].copy()
-        for o in occ[1:]:
-            acc = (acc + g[o]).astype(np.float32)
-        assert eq(s[q], acc)
+        tot = np.zeros(8, np.float32)
+        for w in np.unique(occ // 16):
+            grp = occ[occ // 16 == w]
+            acc = g[grp[0]].copy()
+            for o in grp[1:]:
+                acc = (acc + g[o]).astype(np.float32)
+            tot = (tot + acc).astype(np.float32)
+        assert eq(s[q], tot)
