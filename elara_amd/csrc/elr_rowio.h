@@ -67,11 +67,45 @@ __device__ __forceinline__ void frag_store(float* __restrict__ p, const RowFrag<
   }
 }
 
+// adam_elem over the lane's fragment, with one range check and one branch for all its elements: the moments and the
+// bias-corrected quotients of every element first, then either the cores (sqrt_core, div_core) for all of them, when
+// every element of every active lane is in their range, or the general sequences.  Same operations, same bits.
 template <int VPL>
 __device__ __forceinline__ void frag_adam(RowFrag<VPL>& w, RowFrag<VPL>& m, RowFrag<VPL>& v, const RowFrag<VPL>& g,
                                           const AdamScalars& s) {
+  float vh[VPL], num[VPL];
+  uint64_t ok = __builtin_amdgcn_read_exec();
 #pragma unroll
-  for (int e = 0; e < VPL; ++e) adam_elem(w.v[e], m.v[e], v.v[e], g.v[e], s);
+  for (int e = 0; e < VPL; ++e) {
+    float mj = s.b1 * m.v[e];
+    float t1 = s.omb1 * g.v[e];
+    mj = mj + t1;
+    float vj = s.b2 * v.v[e];
+    float t2 = s.omb2 * g.v[e];
+    t2 = t2 * g.v[e];
+    vj = vj + t2;
+    m.v[e] = mj;
+    v.v[e] = vj;
+    const float mh = div_by_recip(mj, s.r1);
+    vh[e] = div_by_recip(vj, s.r2);
+    num[e] = s.lr * mh;
+    ok &= sqrt_core_lanes(vh[e]) & quot_num_lanes(num[e]);
+  }
+  if (eps_ok(s.eps) && ok == __builtin_amdgcn_read_exec()) {
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) {
+      float den = sqrt_core(vh[e]);
+      den = den + s.eps;
+      w.v[e] = w.v[e] - div_core(num[e], den);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) {
+      float den = __builtin_sqrtf(vh[e]);
+      den = den + s.eps;
+      w.v[e] = w.v[e] - num[e] / den;
+    }
+  }
 }
 
 // Initial weights of the lane's fragment of row r (D = 64*VPL): elements j = lane*VPL + e.
