@@ -48,7 +48,7 @@ def assemble_rows(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K, D, seed,
     a.table, a.recip, a.table_rows = table.t.data_ptr(), table.r.data_ptr(), table.t.shape[0]
     a.mat, a.mat_rows = _lib.dptr(mat).value, mat.shape[0]
     a.loc, a.R = loc.data_ptr(), loc.numel() - 1
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_assemble(ctypes.byref(a), _lib.stream_of(work))
     _lib.check(rc, 'elr_assemble')
     return work

@@ -6,10 +6,10 @@
 // segment sum, Adam on each unique row).
 //
 // Sort.  Stable LSD radix sort of (id, occurrence index) pairs, 8-bit digits, ceil(key_bits / 8) passes, keys held
-// as uint32 when key_bits <= 32.  Each pass is three launches: per-tile digit histograms (tiles of 4096 keys), one
-// block per digit scanning that digit's per-tile counts, and a scatter in which each key's rank among equal digits
-// of its tile comes from wave ballots (peer mask of the 8 digit bits), per-wave counts in LDS and a running count
-// over the tile's 16 rounds, so equal keys keep their occurrence order.
+// as uint32 when key_bits <= 32.  Each pass is three launches: per-tile digit histograms (tiles of 4096 keys, or
+// 1024 below 2^21 keys), one block per digit scanning that digit's per-tile counts, and a scatter in which each
+// key's rank among equal digits of its tile comes from wave ballots (peer mask of the 8 digit bits), per-wave counts
+// in LDS and a running count over the tile's rounds, so equal keys keep their occurrence order.
 //
 // Segments.  Sorted position i starts a segment when its key differs from position i-1; a scan of those heads
 // gives every position its unique index (the inverse) and every unique id its first position.
@@ -32,14 +32,20 @@
 namespace elr {
 
 constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
-constexpr int64_t kSortTile = (int64_t)kSortThreads * kSortItems;
+// Keys per thread of a sort tile and positions per thread of a segment tile: 16 for large batches (tiles of 4,096),
+// 4 below kBigBatch, so that a batch of a few hundred thousand ids still spreads over several hundred blocks.
+constexpr int kItemsBig = 16;
+constexpr int kItemsSmall = 4;
+constexpr int64_t kBigBatch = int64_t(1) << 21;
+inline int items_for(int64_t n) { return n >= kBigBatch ? kItemsBig : kItemsSmall; }
 constexpr int kRadixBins = 256;
 constexpr int kAtenGroup = 10;                          // NROWS_PER_THREAD of ATen's sort path
 constexpr int kGroupsPerChunk = 6;
 constexpr int kSegChunk = kAtenGroup * kGroupsPerChunk;   // occurrences per parallel chunk (sort path)
 constexpr int64_t kAtenSmall = 3072;                      // ATen's windowed path up to this many indices
 constexpr int kAtenWinShift = 4;                          // its window: 16 indices
+constexpr int64_t kHotLen = 240;                          // sort-path segments longer than this are hot
+constexpr int kSegParts = 8;                              // run sums a final-kernel wave loads together
 constexpr int kSegBlock = 256;
 
 static_assert(kSortThreads == kRadixBins, "one histogram bin per sort thread");
@@ -50,14 +56,14 @@ __device__ __forceinline__ uint32_t digit_of(Key k, int shift) {
 }
 
 // Per-tile digit histogram, digit-major: hist[d * nblk + tile].
-template <typename Src, typename Key>
+template <typename Src, typename Key, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const Src* __restrict__ src, int64_t n, int shift,
                                                              int64_t* __restrict__ hist, int64_t nblk) {
   __shared__ int h[kRadixBins];
   h[threadIdx.x] = 0;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  for (int r = 0; r < kSortItems; ++r) {
+  const int64_t base = (int64_t)blockIdx.x * kSortThreads * ITEMS;
+  for (int r = 0; r < ITEMS; ++r) {
     const int64_t pos = base + (int64_t)r * kSortThreads + threadIdx.x;
     if (pos < n) atomicAdd(&h[digit_of((Key)src[pos], shift)], 1);
   }
@@ -81,7 +87,7 @@ __global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict_
 // positions.  Each item's rank among the tile's items of its digit comes from ballots (wave) and LDS counts (block);
 // the tile is then sorted by digit in LDS and written out run by run, so consecutive threads write consecutive
 // addresses of one digit's bucket instead of 64 scattered ones.
-template <typename Src, typename Key, bool FIRST>
+template <typename Src, typename Key, bool FIRST, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __restrict__ src_keys,
                                                                 const int32_t* __restrict__ src_vals, int64_t n,
                                                                 int shift, const int64_t* __restrict__ offs,
@@ -89,12 +95,13 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
                                                                 Key* __restrict__ dst_keys,
                                                                 int32_t* __restrict__ dst_vals) {
   constexpr int NW = kSortThreads / 64;
+  constexpr int TILE = kSortThreads * ITEMS;
   __shared__ int64_t bo[kRadixBins];   // global position of this tile's first item of digit d
   __shared__ int run[kRadixBins];      // items of digit d in earlier rounds of the tile
   __shared__ int lbase[kRadixBins];    // position of digit d's first item in the tile sorted by digit
   __shared__ int wc[NW][kRadixBins];
-  __shared__ Key lk[kSortTile];
-  __shared__ int32_t lv[kSortTile];
+  __shared__ Key lk[TILE];
+  __shared__ int32_t lv[TILE];
   const int t = threadIdx.x, w = t >> 6;
   {
     // digit bases: exclusive scan of the 256 digit totals (n < 2^31, so they fit in int)
@@ -106,12 +113,12 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
 #pragma unroll
   for (int q = 0; q < NW; ++q) wc[q][t] = 0;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  Key kk[kSortItems];
-  int32_t vv[kSortItems];
-  int rk[kSortItems];
+  const int64_t base = (int64_t)blockIdx.x * TILE;
+  Key kk[ITEMS];
+  int32_t vv[ITEMS];
+  int rk[ITEMS];
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
+  for (int r = 0; r < ITEMS; ++r) {
     const int64_t pos = base + (int64_t)r * kSortThreads + t;
     const bool valid = pos < n;
     const Key k = valid ? (Key)src_keys[pos] : (Key)0;
@@ -153,7 +160,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
+  for (int r = 0; r < ITEMS; ++r) {
     if (rk[r] >= 0) {
       const int lp = lbase[digit_of(kk[r], shift)] + rk[r];
       lk[lp] = kk[r];
@@ -162,7 +169,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   }
   __syncthreads();
   const int64_t rem = n - base;
-  const int nvalid = rem < kSortTile ? (int)rem : (int)kSortTile;
+  const int nvalid = rem < TILE ? (int)rem : TILE;
   for (int j = t; j < nvalid; j += kSortThreads) {
     const Key k = lk[j];
     const uint32_t d = digit_of(k, shift);
@@ -174,11 +181,9 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   }
 }
 
-// Segment kernels take a tile of kSegTile positions per block, in kSegItems rounds of kSegBlock consecutive
+// Segment kernels take a tile of kSegBlock * ITEMS positions per block, in ITEMS rounds of kSegBlock consecutive
 // positions (thread t takes position base + r * kSegBlock + t in round r: every load is coalesced).  Positions are
 // ranked in that order, round by round, with one block scan per round.
-constexpr int kSegItems = 16;
-constexpr int64_t kSegTile = (int64_t)kSegBlock * kSegItems;
 
 template <typename Key>
 __device__ __forceinline__ int is_head(const Key* __restrict__ sk, int64_t i, int64_t n) {
@@ -186,27 +191,27 @@ __device__ __forceinline__ int is_head(const Key* __restrict__ sk, int64_t i, in
 }
 
 // Segment heads: per-block head counts.
-template <typename Key>
+template <typename Key, int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_seg_count(const Key* __restrict__ sk, int64_t n,
                                                          int64_t* __restrict__ bsum) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   int v[1] = {0}, ex[1], tot[1];
-  for (int r = 0; r < kSegItems; ++r) v[0] += is_head(sk, base + (int64_t)r * kSegBlock, n);
+  for (int r = 0; r < ITEMS; ++r) v[0] += is_head(sk, base + (int64_t)r * kSegBlock, n);
   block_excl_scan<kSegBlock, 1>(v, ex, tot);
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
 
 // Segment heads: unique ids, segment starts (seg_start[U] = n), each segment's first occurrence index and the
 // inverse.
-template <typename Key>
+template <typename Key, int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__ sk, const int32_t* __restrict__ sv,
                                                          int64_t n, const int64_t* __restrict__ boff,
                                                          const int64_t* __restrict__ d_U,
                                                          int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
                                                          int32_t* __restrict__ seg_occ0, int64_t* __restrict__ inverse) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   int64_t before = boff[blockIdx.x];   // heads in earlier positions of the tile's earlier rounds
-  for (int r = 0; r < kSegItems; ++r) {
+  for (int r = 0; r < ITEMS; ++r) {
     const int64_t i = base + (int64_t)r * kSegBlock;
     const int f = is_head(sk, i, n);
     int v[1] = {f}, ex[1], tot[1];
@@ -227,32 +232,45 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__
   if (blockIdx.x == 0 && threadIdx.x == 0) seg_start[*d_U] = n;
 }
 
+// Sort path.  A segment of more than kHotLen occurrences is hot: the partial-chunk kernel sums all of its runs (its
+// first chunk included) and one block of the final kernel folds the run sums, its four waves loading together.  Any
+// other segment folds its first chunk in the final kernel's wave, and only its later chunks are partial chunks.
+__device__ __forceinline__ bool seg_hot(int64_t L) { return L > kHotLen; }
+__device__ __forceinline__ int part_chunks(int64_t L) {
+  return (int)(seg_hot(L) ? (L + kSegChunk - 1) / kSegChunk : (L - 1) / kSegChunk);
+}
 __device__ __forceinline__ int extra_chunks(const int64_t* __restrict__ seg_start, int64_t u, int64_t U) {
-  return u < U ? (int)((seg_start[u + 1] - seg_start[u] - 1) / kSegChunk) : 0;
+  return u < U ? part_chunks(seg_start[u + 1] - seg_start[u]) : 0;
 }
 
-// Extra chunks (beyond the first) of each segment: per-block counts.
+// Partial chunks of each segment: per-block counts.  Also clears the hot-segment count.
+template <int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_chunk_count(const int64_t* __restrict__ seg_start,
                                                            const int64_t* __restrict__ d_U,
-                                                           int64_t* __restrict__ bsum) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
+                                                           int64_t* __restrict__ bsum, int64_t* __restrict__ d_hot) {
+  const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   const int64_t U = *d_U;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *d_hot = 0;
   int v[1] = {0}, ex[1], tot[1];
-  for (int r = 0; r < kSegItems; ++r) v[0] += extra_chunks(seg_start, base + (int64_t)r * kSegBlock, U);
+  for (int r = 0; r < ITEMS; ++r) v[0] += extra_chunks(seg_start, base + (int64_t)r * kSegBlock, U);
   block_excl_scan<kSegBlock, 1>(v, ex, tot);
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
 
-// chunk_off[u] = first work item of segment u's extra chunks; chunk_seg[item] = u.
+// chunk_off[u] = first work item of segment u's partial chunks; chunk_seg[item] = u; hot segments are listed in
+// hot_list[0 .. *d_hot) (in no particular order: each is summed on its own).
+template <int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __restrict__ seg_start,
                                                            const int64_t* __restrict__ d_U,
                                                            const int64_t* __restrict__ boff,
                                                            int32_t* __restrict__ chunk_off,
-                                                           int32_t* __restrict__ chunk_seg) {
-  const int64_t base = (int64_t)blockIdx.x * kSegTile + threadIdx.x;
+                                                           int32_t* __restrict__ chunk_seg,
+                                                           int32_t* __restrict__ hot_list,
+                                                           int64_t* __restrict__ d_hot) {
+  const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   const int64_t U = *d_U;
   int64_t before = boff[blockIdx.x];
-  for (int r = 0; r < kSegItems; ++r) {
+  for (int r = 0; r < ITEMS; ++r) {
     const int64_t u = base + (int64_t)r * kSegBlock;
     const int e = extra_chunks(seg_start, u, U);
     int v[1] = {e}, ex[1], tot[1];
@@ -261,6 +279,8 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __rest
       const int64_t off = before + ex[0];
       chunk_off[u] = (int32_t)off;
       for (int c = 0; c < e; ++c) chunk_seg[off + c] = (int32_t)u;
+      if (seg_hot(seg_start[u + 1] - seg_start[u]))
+        hot_list[atomicAdd(reinterpret_cast<unsigned long long*>(d_hot), 1ull)] = (int32_t)u;
     }
     before += tot[0];
     __syncthreads();
@@ -337,7 +357,7 @@ __global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ 
   const int64_t E = *d_E;
   for (int64_t wi = wave_id(); wi < E; wi += wave_count()) {
     const int64_t u = chunk_seg[wi];
-    const int64_t c = wi - chunk_off[u] + 1;
+    const int64_t c = wi - chunk_off[u] + (seg_hot(seg_start[u + 1] - seg_start[u]) ? 0 : 1);
     const int64_t p0 = seg_start[u] + c * kSegChunk;
     int64_t p1 = p0 + kSegChunk;
     const int64_t e = seg_start[u + 1];
@@ -383,10 +403,17 @@ __global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ 
   }
 }
 
-// The group sums of a segment's extra chunks are consecutive parts rows from chunk_off[u] * kGroupsPerChunk (every
-// extra chunk but the last is full): ceil((L - kSegChunk) / kAtenGroup) of them.
+// The group sums of a segment's partial chunks are consecutive parts rows from chunk_off[u] * kGroupsPerChunk (every
+// partial chunk but the last is full): ceil(L / kAtenGroup) of them for a hot segment, else
+// ceil((L - kSegChunk) / kAtenGroup).  inline_len: the occurrences the segment's own wave folds.
 __device__ __forceinline__ int64_t seg_parts(int64_t L, int win_shift) {
-  return win_shift || L <= kSegChunk ? 0 : (L - kSegChunk + kAtenGroup - 1) / kAtenGroup;
+  if (win_shift) return 0;
+  if (seg_hot(L)) return (L + kAtenGroup - 1) / kAtenGroup;
+  return L <= kSegChunk ? 0 : (L - kSegChunk + kAtenGroup - 1) / kAtenGroup;
+}
+__device__ __forceinline__ int64_t inline_len(int64_t L, int win_shift) {
+  if (win_shift) return L;
+  return seg_hot(L) ? 0 : (L < kSegChunk ? L : kSegChunk);
 }
 
 // Final per-segment sum (the inline part -- the first chunk, or the whole segment on the windowed path -- then the
@@ -407,7 +434,7 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
     const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
     const int64_t L = s1 - s0;
     const int64_t row = uniq ? uniq[u] : u;   // NULL: segment u goes to row u
-    const int64_t inl = win_shift ? L : (L < kSegChunk ? L : kSegChunk);
+    const int64_t inl = inline_len(L, win_shift);
     float acc[NQ], tot[NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) acc[q] = tot[q] = 0.0f;
@@ -471,6 +498,88 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
 #endif
 constexpr int kSegPerWave = ELR_SEG_SW;
 
+// The result of one segment: written to out[row] (MODE 0) or applied as an Adam step to state row `row` (MODE 1).
+template <int VPL, int MODE>
+__device__ __forceinline__ void seg_emit(float* __restrict__ out, int64_t row, const RowFrag<VPL>& sum,
+                                         const AdamScalars& s) {
+  constexpr int64_t D = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  if (MODE == 0) {
+    frag_store<VPL>(out + row * D + lane * VPL, sum);
+  } else {
+    float* rec = out + row * 3 * D + lane * VPL;
+    RowFrag<VPL> w = frag_load<VPL, false>(rec), m = frag_load<VPL, false>(rec + D),
+                 v = frag_load<VPL, false>(rec + 2 * D);
+    frag_adam<VPL>(w, m, v, sum, s);
+    frag_store<VPL>(rec, w);
+    frag_store<VPL>(rec + D, m);
+    frag_store<VPL>(rec + 2 * D, v);
+  }
+}
+
+// Hot segments, one block each (grid-stride over hot_list by hot_blocks blocks): the total is
+// ((0 + G1) + G2) + ... over the segment's ceil(L / 10) run sums, consecutive parts rows.  The four waves load
+// 4 * PB run sums together; then wave 0, 1, 2, 3 in turn adds its PB of them to the running total, which passes
+// from wave to wave through LDS, so the additions keep their order.  Every loop bound is block-uniform.
+template <int VPL, int MODE>
+__device__ __forceinline__ void seg_hot_block(const int64_t* __restrict__ seg_start,
+                                              const int64_t* __restrict__ uniq,
+                                              const int32_t* __restrict__ chunk_off,
+                                              const float* __restrict__ parts,
+                                              const int32_t* __restrict__ hot_list, const int64_t* __restrict__ d_hot,
+                                              int64_t hot_blocks, float* __restrict__ out, int64_t nrows,
+                                              const AdamScalars& s, float* __restrict__ relay) {
+  constexpr int64_t D = 64 * VPL;
+  constexpr int PB = VPL <= 2 ? kSegParts : kSegParts / 2;
+  constexpr int NWV = 4;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t nh = *d_hot;
+  for (int64_t h = blockIdx.x; h < nh; h += hot_blocks) {
+    const int64_t u = hot_list[h];
+    const int64_t L = seg_start[u + 1] - seg_start[u];
+    const int64_t nr = (L + kAtenGroup - 1) / kAtenGroup;
+    const float* pr = parts + (int64_t)chunk_off[u] * kGroupsPerChunk * D + lane * VPL;
+    for (int64_t i0 = 0; i0 < nr; i0 += NWV * PB) {
+      const int64_t mine = i0 + wv * PB;
+      RowFrag<VPL> pc[PB];
+#pragma unroll
+      for (int e = 0; e < PB; ++e)
+        if (mine + e < nr) pc[e] = frag_load<VPL, false>(pr + (mine + e) * D);
+      for (int w = 0; w < NWV; ++w) {
+        if (wv == w && mine < nr) {
+          RowFrag<VPL> tot;
+          if (mine == 0) {
+            tot = frag_zero<VPL>();
+          } else {
+#pragma unroll
+            for (int j = 0; j < VPL; ++j) tot.v[j] = relay[lane * VPL + j];
+          }
+#pragma unroll
+          for (int e = 0; e < PB; ++e)
+            if (mine + e < nr) {
+#pragma unroll
+              for (int j = 0; j < VPL; ++j) tot.v[j] = tot.v[j] + pc[e].v[j];
+            }
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) relay[lane * VPL + j] = tot.v[j];
+        }
+        __syncthreads();
+      }
+    }
+    if (wv == 0) {
+      const int64_t row = uniq ? uniq[u] : u;
+      if (row >= 0 && row < nrows) {
+        RowFrag<VPL> tot;
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) tot.v[j] = relay[lane * VPL + j];
+        seg_emit<VPL, MODE>(out, row, tot, s);
+      }
+    }
+    __syncthreads();   // the relay is reused by the block's next hot segment
+  }
+}
+
 template <int VPL, int MODE>
 __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__ grad,
                                                        const int32_t* __restrict__ sv,
@@ -480,13 +589,19 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
                                                        const int32_t* __restrict__ chunk_off,
                                                        const float* __restrict__ parts,
                                                        const int64_t* __restrict__ d_U, int64_t u_base,
-                                                       int win_shift, float* __restrict__ out, int64_t nrows,
-                                                       AdamScalars s) {
+                                                       const int32_t* __restrict__ hot_list,
+                                                       const int64_t* __restrict__ d_hot, int64_t hot_blocks,
+                                                       float* __restrict__ out, int64_t nrows, AdamScalars s) {
   constexpr int64_t D = 64 * VPL;
   constexpr int SW = kSegPerWave;
+  __shared__ float relay[D];
+  if ((int64_t)blockIdx.x < hot_blocks) {
+    seg_hot_block<VPL, MODE>(seg_start, uniq, chunk_off, parts, hot_list, d_hot, hot_blocks, out, nrows, s, relay);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int64_t U = *d_U;
-  const int64_t u0 = u_base + wave_id() * SW;
+  const int64_t u0 = u_base + (((int64_t)blockIdx.x - hot_blocks) * 4 + (threadIdx.x >> 6)) * SW;
   if (u0 >= U) return;
   int64_t s0[SW], len[SW], row[SW], o0[SW];
   bool ok[SW];
@@ -498,7 +613,7 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
     len[q] = ok[q] ? seg_start[u + 1] - s0[q] : 0;
     row[q] = ok[q] ? (uniq ? uniq[u] : u) : -1;   // NULL: segment u goes to row u
     o0[q] = ok[q] ? (int64_t)seg_occ0[u] : 0;
-    ok[q] = ok[q] && row[q] >= 0 && row[q] < nrows;
+    ok[q] = ok[q] && row[q] >= 0 && row[q] < nrows && !seg_hot(len[q]);   // hot segments: a block's
   }
   RowFrag<VPL> w[SW], m[SW], v[SW], acc[SW];
   int32_t my[SW];
@@ -517,47 +632,40 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
     if (!ok[q]) continue;
-    // occurrences [1, inl) fold here: the first chunk (sort path) or the whole segment (windowed path)
-    const int64_t inl = win_shift ? len[q] : (len[q] < kSegChunk ? len[q] : kSegChunk);
+    // the first chunk folds here, run by run (runs of kAtenGroup from the segment's first occurrence, which is
+    // already in acc); then the later chunks' run sums, kSegParts at a time
+    const int inl = (int)(len[q] < kSegChunk ? len[q] : kSegChunk);
     RowFrag<VPL> tot = frag_zero<VPL>();
-    int32_t prev = (int32_t)o0[q];
-    int32_t mb = my[q];
-    constexpr int UN = 8;
-    for (int64_t b0 = 0; b0 < inl; b0 += 64) {
-      if (b0) mb = lane < inl - b0 ? sv[s0[q] + b0 + lane] : 0;
-      const int bl = (int)(inl - b0 < 64 ? inl - b0 : 64);
-      for (int k0 = b0 ? 0 : 1; k0 < bl; k0 += UN) {
-        RowFrag<VPL> g[UN];
+    constexpr int RB = VPL <= 2 ? kAtenGroup : kAtenGroup / 2;   // rows of a run loaded together
+    constexpr int PB = VPL <= 2 ? kSegParts : kSegParts / 2;     // run sums loaded together
+    for (int r0 = 0; r0 < inl; r0 += kAtenGroup) {
+      const int rl = inl - r0 < kAtenGroup ? inl - r0 : kAtenGroup;
+      RowFrag<VPL> run = acc[q];
+      for (int h = 0; h < rl; h += RB) {
+        RowFrag<VPL> g[RB];
 #pragma unroll
-        for (int e = 0; e < UN; ++e)
-          if (k0 + e < bl) {
-            const int64_t o = (int64_t)__builtin_amdgcn_readlane(mb, k0 + e);
+        for (int e = 0; e < RB; ++e)
+          if (h + e < rl && r0 + h + e > 0) {
+            const int64_t o = (int64_t)__builtin_amdgcn_readlane(my[q], r0 + h + e);
             g[e] = frag_load<VPL, true>(grad + o * D + lane * VPL);
           }
 #pragma unroll
-        for (int e = 0; e < UN; ++e)
-          if (k0 + e < bl) {
-            const int32_t o = __builtin_amdgcn_readlane(mb, k0 + e);
-            if (group_head(b0 + k0 + e, o, prev, win_shift)) {
+        for (int e = 0; e < RB; ++e) {
+          if (h + e >= rl) continue;
+          if (h + e == 0) {
+            if (r0 > 0) run = g[e];   // run 0 starts from the preloaded first gradient
+          } else {
 #pragma unroll
-              for (int j = 0; j < VPL; ++j) {
-                tot.v[j] = tot.v[j] + acc[q].v[j];
-                acc[q].v[j] = g[e].v[j];
-              }
-            } else {
-#pragma unroll
-              for (int j = 0; j < VPL; ++j) acc[q].v[j] = acc[q].v[j] + g[e].v[j];
-            }
-            prev = o;
+            for (int j = 0; j < VPL; ++j) run.v[j] = run.v[j] + g[e].v[j];
           }
+        }
       }
-    }
 #pragma unroll
-    for (int j = 0; j < VPL; ++j) tot.v[j] = tot.v[j] + acc[q].v[j];
-    const int64_t np = seg_parts(len[q], win_shift);
+      for (int j = 0; j < VPL; ++j) tot.v[j] = tot.v[j] + run.v[j];
+    }
+    const int64_t np = seg_parts(len[q], 0);
     if (np) {
       const float* pr = parts + (int64_t)chunk_off[u0 + q] * kGroupsPerChunk * D + lane * VPL;
-      constexpr int PB = VPL <= 2 ? 16 : 32 / VPL;   // group sums loaded together, added in order
       for (int64_t c0 = 0; c0 < np; c0 += PB) {
         RowFrag<VPL> pc[PB];
 #pragma unroll
@@ -596,20 +704,22 @@ inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
 struct DedupScratch {
   void* keys[2];
   int32_t* vals[2];
-  int64_t* hist;      // [256 * ntile]
+  int64_t* hist;      // [256 * ntile], ntile = n / (kSortThreads * items_for(n)) rounded up
   int64_t* dtot;      // [256] digit totals
-  int64_t* bsum;      // [n / kSegTile + 1]
-  int64_t* d_tot;     // [2]: U, E
+  int64_t* bsum;      // [n / (kSegBlock * items_for(n)) + 1]
+  int64_t* d_tot;     // [3]: U, E (partial chunks), hot segments
   int64_t* uniq;      // [n]
   int64_t* seg_start; // [n + 1]
   int32_t* seg_occ0;  // [n] first occurrence index of each segment
   int32_t* chunk_off; // [n]
-  int32_t* chunk_seg; // [n / kSegChunk + 1]
-  float* parts;       // [(n / kSegChunk + 1) * kGroupsPerChunk * D] group sums of the extra chunks
+  int32_t* chunk_seg; // [nch]: n / kSegChunk + n / kHotLen + 2 bounds the partial chunks
+  float* parts;       // [nch * kGroupsPerChunk * D] group sums of the partial chunks
+  int32_t* hot_list;  // [n / kHotLen + 1] hot segments
 };
 
 inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void* base) {
-  const int64_t ntile = cdiv(n, kSortTile), nblk = cdiv(n, kSegTile), nch = n / kSegChunk + 1;
+  const int64_t ntile = cdiv(n, kSortThreads * items_for(n)), nblk = cdiv(n, kSegBlock * items_for(n));
+  const int64_t nch = n / kSegChunk + n / kHotLen + 2;
   int64_t o = 0;
   char* b = (char*)base;
   auto take = [&](int64_t bytes) {
@@ -625,21 +735,22 @@ inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void
   s.hist = (int64_t*)take(kRadixBins * ntile * 8);
   s.dtot = (int64_t*)take(kRadixBins * 8);
   s.bsum = (int64_t*)take(nblk * 8);
-  s.d_tot = (int64_t*)take(2 * 8);
+  s.d_tot = (int64_t*)take(3 * 8);
   s.uniq = (int64_t*)take(n * 8);
   s.seg_start = (int64_t*)take((n + 1) * 8);
   s.seg_occ0 = (int32_t*)take(n * 4);
   s.chunk_off = (int32_t*)take(n * 4);
   s.chunk_seg = (int32_t*)take(nch * 4);
   s.parts = (float*)take(nch * kGroupsPerChunk * D * 4);
+  s.hot_list = (int32_t*)take((n / kHotLen + 1) * 4);
   if (out) *out = s;
   return o;
 }
 
 // Sort (ids, positions) by id; returns which buffer holds the result.
-template <typename Key>
+template <typename Key, int ITEMS>
 static int radix_sort(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, hipStream_t st) {
-  const int64_t ntile = cdiv(n, kSortTile);
+  const int64_t ntile = cdiv(n, kSortThreads * ITEMS);
   const int passes = (key_bits + 7) / 8;
   Key* kb[2] = {(Key*)S.keys[0], (Key*)S.keys[1]};
   int cur = 0;
@@ -647,14 +758,14 @@ static int radix_sort(const int64_t* ids, int64_t n, int key_bits, DedupScratch&
     const int shift = 8 * p;
     const int nxt = p == 0 ? 0 : cur ^ 1;
     if (p == 0) {
-      k_radix_hist<int64_t, Key><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
+      k_radix_hist<int64_t, Key, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
       k_radix_hist_scan<<<kRadixBins, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
-      k_radix_scatter<int64_t, Key, true><<<(unsigned)ntile, kSortThreads, 0, st>>>(
+      k_radix_scatter<int64_t, Key, true, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(
           ids, nullptr, n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
     } else {
-      k_radix_hist<Key, Key><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
+      k_radix_hist<Key, Key, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
       k_radix_hist_scan<<<kRadixBins, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
-      k_radix_scatter<Key, Key, false><<<(unsigned)ntile, kSortThreads, 0, st>>>(
+      k_radix_scatter<Key, Key, false, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(
           kb[cur], S.vals[cur], n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
     }
     cur = nxt;
@@ -663,30 +774,44 @@ static int radix_sort(const int64_t* ids, int64_t n, int key_bits, DedupScratch&
 }
 
 // Sort, segment heads (uniq / seg_start / inverse, U in d_tot[0]) and the extra-chunk plan (E in d_tot[1]).
+template <typename Key, int ITEMS>
+static int dedup_core_items(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, int64_t* uniq_out,
+                            int64_t* inverse, hipStream_t st) {
+  const int cur = radix_sort<Key, ITEMS>(ids, n, key_bits, S, st);
+  const Key* sk = (const Key*)S.keys[cur];
+  const int32_t* sv = S.vals[cur];
+  const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
+  int64_t* uniq = uniq_out ? uniq_out : S.uniq;
+  k_seg_count<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
+  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot);
+  k_seg_apply<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start,
+                                                                S.seg_occ0, inverse);
+  return cur;
+}
+
 template <typename Key>
 static int dedup_core(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, int64_t* uniq_out,
                       int64_t* inverse, hipStream_t st) {
-  const int cur = radix_sort<Key>(ids, n, key_bits, S, st);
-  const Key* sk = (const Key*)S.keys[cur];
-  const int32_t* sv = S.vals[cur];
-  const int64_t nblk = cdiv(n, kSegTile);
-  int64_t* uniq = uniq_out ? uniq_out : S.uniq;
-  k_seg_count<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
-  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot);
-  k_seg_apply<Key><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start, S.seg_occ0,
-                                                         inverse);
-  return cur;
+  return items_for(n) == kItemsBig ? dedup_core_items<Key, kItemsBig>(ids, n, key_bits, S, uniq_out, inverse, st)
+                                   : dedup_core_items<Key, kItemsSmall>(ids, n, key_bits, S, uniq_out, inverse, st);
 }
 
 // ATen's windowed order applies up to kAtenSmall indices: returns the window's shift there, 0 on the sort path.
 inline int win_shift_for(int64_t n) { return n <= kAtenSmall ? kAtenWinShift : 0; }
 
+template <int ITEMS>
+static void chunk_plan_items(int64_t n, DedupScratch& S, hipStream_t st) {
+  const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
+  k_chunk_count<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.d_tot + 2);
+  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1);
+  k_chunk_apply<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.chunk_off,
+                                                             S.chunk_seg, S.hot_list, S.d_tot + 2);
+}
+
 static void chunk_plan(int64_t n, DedupScratch& S, hipStream_t st) {
   if (win_shift_for(n)) return;   // the windowed path sums every segment in one wave: no extra chunks
-  const int64_t nblk = cdiv(n, kSegTile);
-  k_chunk_count<<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum);
-  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1);
-  k_chunk_apply<<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.chunk_off, S.chunk_seg);
+  if (items_for(n) == kItemsBig) chunk_plan_items<kItemsBig>(n, S, st);
+  else chunk_plan_items<kItemsSmall>(n, S, st);
 }
 
 // Grid of a grid-stride wave loop: enough blocks to fill the chip several times over, at most one wave per item.
@@ -703,8 +828,8 @@ static void seg_reduce(const float* grad, int64_t D, const int32_t* sv, DedupScr
                        int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
   const int ws = win_shift_for(n);
   if (!ws)
-    k_seg_partials<NQ><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
-                                                                      S.chunk_seg, S.d_tot + 1, S.parts);
+    k_seg_partials<NQ><<<wave_grid(n / kSegChunk + n / kHotLen + 2), 256, 0, st>>>(
+        grad, D, sv, S.seg_start, S.chunk_off, S.chunk_seg, S.d_tot + 1, S.parts);
   k_seg_final<NQ, MODE><<<wave_grid(n), 256, 0, st>>>(grad, D, sv, S.seg_start, uniq, S.chunk_off, S.parts, S.d_tot,
                                                        ws, out, nrows, s);
 }
@@ -712,24 +837,25 @@ static void seg_reduce(const float* grad, int64_t D, const int32_t* sv, DedupScr
 template <int VPL, int MODE>
 static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S, const int64_t* uniq, int64_t n,
                            float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
-  constexpr int64_t D = 64 * VPL;
-  const int ws = win_shift_for(n);
-  if (!ws)
-    k_seg_partials<VPL><<<wave_grid(n / kSegChunk + 1), 256, 0, st>>>(grad, D, sv, S.seg_start, S.chunk_off,
-                                                                       S.chunk_seg, S.d_tot + 1, S.parts);
-  // one launch per range of at most 2^22 blocks (4 waves of kSegPerWave segments each); U <= n
+  constexpr int64_t D = 64 * VPL;   // sort path only (n > kAtenSmall)
+  k_seg_partials<VPL><<<wave_grid(n / kSegChunk + n / kHotLen + 2), 256, 0, st>>>(
+      grad, D, sv, S.seg_start, S.chunk_off, S.chunk_seg, S.d_tot + 1, S.parts);
+  // one launch per range of at most 2^22 blocks (4 waves of kSegPerWave segments each); U <= n.  The first launch
+  // starts with one block per possible hot segment (fewer than n / kHotLen; blocks beyond the count exit at once).
   const int64_t per = kOneShotBlocks * 4 * kSegPerWave;
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
-    k_seg_final_wpr<VPL, MODE><<<(unsigned)cdiv(m, 4 * kSegPerWave), 256, 0, st>>>(
-        grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a, ws, out, nrows, s);
+    const int64_t hb = a == 0 ? n / kHotLen + 1 : 0;
+    k_seg_final_wpr<VPL, MODE><<<(unsigned)(hb + cdiv(m, 4 * kSegPerWave)), 256, 0, st>>>(
+        grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a, S.hot_list, S.d_tot + 2, hb, out,
+        nrows, s);
   }
 }
 
 template <int MODE>
 static int seg_reduce_d(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
                         int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
-  if (aligned16(grad) && aligned16(out)) {
+  if (aligned16(grad) && aligned16(out) && !win_shift_for(n)) {   // ATen's windowed order: the generic kernels
     switch (D) {
       case 64: seg_reduce_wpr<1, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
       case 128: seg_reduce_wpr<2, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;

@@ -72,7 +72,7 @@ def unique(ids, bound=None):
     u = torch.empty(n, dtype=I64, device=dev)
     nu = torch.empty(1, dtype=I64, device=dev)
     scratch, nbytes = _scratch(dev, n, 1)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_unique(_lib.ptr(flat), n, kb, _lib.ptr(u), _lib.ptr(inv), _lib.ptr(nu),
                                    _lib.ptr(scratch), nbytes, _lib.stream_of(flat))
     _lib.check(rc, 'elr_unique')
@@ -112,7 +112,7 @@ def unique_plan_async(ids, D, bound=None):
     plan.buf, plan.nbytes = torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
     u = torch.empty(n, dtype=I64, device=dev)
     nu = torch.empty(1, dtype=I64, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_dedup_plan(_lib.ptr(flat), n, plan.key_bits, _lib.ptr(u), None, _lib.ptr(nu),
                                        _lib.ptr(plan.buf), nbytes, int(D), _lib.stream_of(flat))
     _lib.check(rc, 'elr_dedup_plan')
@@ -138,7 +138,7 @@ def segment_sum_plan(grad, plan, out=None, perm=None):
     if n == 0:
         return out
     g = grad.reshape(n, D).contiguous()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_segment_sum_plan(_lib.ptr(g), n, D, plan.key_bits, _lib.ptr(plan.buf), plan.nbytes,
                                              _lib.ptr(perm), _lib.ptr(out), out.shape[0], _lib.stream_of(g))
     _lib.check(rc, 'elr_segment_sum_plan')
@@ -161,7 +161,7 @@ def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1, 
         return out
     g = grad_output.reshape(n, D).contiguous()
     scratch, nbytes = _scratch(dev, n, D)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_segment_sum(_lib.ptr(g), _lib.ptr(idx), n, D, int(num_weights), _lib.ptr(out),
                                         _lib.ptr(scratch), nbytes, _lib.stream_of(g))
     _lib.check(rc, 'elr_segment_sum')
@@ -183,7 +183,7 @@ def adam_dedup(pool, ids, grad, lr, b1, b2, eps, step):
     dev = pool.device
     scratch, nbytes = _scratch(dev, n, D)
     s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_adam_dedup(_lib.ptr(pool), pool.shape[0], _lib.ptr(idx), _lib.ptr(g), n, D, s,
                                        _lib.ptr(scratch), nbytes, _lib.stream_of(pool))
     _lib.check(rc, 'elr_adam_dedup')

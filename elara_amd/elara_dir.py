@@ -82,7 +82,7 @@ def elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
     out = [e(nL, K, dt=I32), e(nL, K, dt=I32), e(nh), e(nh), e(nev), e(nev, dt=torch.bool), e(nev, K), e(nev), e(nev)]
     scratch, nbytes = _scratch(dev, nev, 0)
     p = _lib.ptr
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_dir_a(ctypes.byref(S), ctypes.byref(P), p(hs), nh, p(L_row), p(L_cnt), nL,
                                   p(ev_slot), nev, int(s), *[p(o) for o in out], p(scratch), nbytes,
                                   _lib.stream_of(st[0]))
@@ -101,7 +101,7 @@ def elara_dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s):
     if na or nc:
         scratch, nbytes = _scratch(dev, 0, nc)
         p = _lib.ptr
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = _lib.lib().elr_dir_b(ctypes.byref(S), ctypes.byref(P), p(a_rows), p(a_k), na, p(c_rows),
                                       p(c_cnt), nc, int(s), p(a_ids), p(c_slots), p(scratch), nbytes,
                                       _lib.stream_of(st[0]))

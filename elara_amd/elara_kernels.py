@@ -53,7 +53,7 @@ def hits(pl, hs, s):
     out_j = torch.empty(n, dtype=I64, device=dev)
     if n:
         p = _lib.ptr
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = _lib.lib().elr_dir_a(ctypes.byref(S), ctypes.byref(P), p(hs), n, None, None, 0, None, 0, int(s),
                                       None, None, p(out_dyn), p(out_j), None, None, None, None, None, None, 0,
                                       _lib.stream_of(anchor))
@@ -71,7 +71,7 @@ def lsteps(pl, rows, cnt):
     ids = torch.empty(n, K, dtype=I32, device=dev)
     if n:
         p = _lib.ptr
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = _lib.lib().elr_dir_a(ctypes.byref(S), ctypes.byref(P), None, 0, p(rows), p(cnt), n, None, 0, 0,
                                       p(steps), p(ids), None, None, None, None, None, None, None, None, 0,
                                       _lib.stream_of(anchor))
@@ -105,7 +105,7 @@ class Directory:
         if n:
             scratch, nbytes = _scratch(dev, n, 0)
             p = _lib.ptr
-            with torch.cuda.device(dev):
+            with _lib.on_device(dev):
                 rc = _lib.lib().elr_dir_evict(ctypes.byref(S), ctypes.byref(P), p(ev_slot), p(ev_row), p(thr), n,
                                               p(rep), p(evl_ids), p(evf), p(ev_dyn), p(scratch), nbytes,
                                               _lib.stream_of(anchor))

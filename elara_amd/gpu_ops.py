@@ -28,7 +28,7 @@ def init_rows(rows, D, seed, bound, out=None):
         if not (out.is_cuda and out.dtype == torch.float32 and out.is_contiguous() and out.numel() >= n * 3 * D):
             raise RuntimeError(f'out must be a contiguous cuda float32 tensor with at least {n}x3x{D} elements')
         rows = rows.to(torch.int64).contiguous()
-        with torch.cuda.device(rows.device):
+        with _lib.on_device(rows.device):
             rc = _lib.lib().elr_init_rows(_lib.ptr(out), _lib.ptr(rows), n, int(D), _seed32(seed), float(bound),
                                          _lib.stream_of(rows))
         _lib.check(rc, 'elr_init_rows')
@@ -79,7 +79,7 @@ def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None
         t = t.contiguous()
         if r is None or r.shape != (t.shape[0], 2) or r.device != t.device:
             r = _recip_host(t.cpu().contiguous()).to(dev)   # a bare [S, 8] table: reciprocals computed here
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = _lib.lib().elr_replay_rows(_lib.ptr(out), _lib.ptr(rows), _lib.ptr(logs), logs.numel() // D,
                                             _lib.ptr(offs), _lib.ptr(steps), _lib.ptr(cnt), n, int(D), int(K),
                                             _seed32(seed), float(bound), _lib.ptr(t), _lib.ptr(r), t.shape[0],

@@ -63,7 +63,7 @@ def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
     grad = grad.contiguous()
     s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
     L = _lib.lib()
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = L.elr_adam_rows(_lib.dptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
                              _lib.ptr(grad), n, D, s, _lib.stream_of(grad))
     _lib.check(rc, 'elr_adam_rows')
@@ -81,6 +81,6 @@ def adam_rows_dense(state, grad, lr, b1, b2, eps, step):
         raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {state.device}')
     grad = grad.contiguous()
     s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
-    with torch.cuda.device(state.device):
+    with _lib.on_device(state.device):
         rc = _lib.lib().elr_adam_rows(_lib.ptr(state), n, None, 1, _lib.ptr(grad), n, D, s, _lib.stream_of(state))
     _lib.check(rc, 'elr_adam_rows')

@@ -66,7 +66,7 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     pout = _lib.PlanOut(*[t.data_ptr() for t in out])
     nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
     scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,
                                           _lib.stream_of(u))
     _lib.check(rc, 'elr_plan_classify')
@@ -104,7 +104,7 @@ def plan_admit(adm_rows, adm_slots, lazy_n, evl, s, n0, C, R, K, code, slot_of, 
         if t.dtype != dt or t.device != dev or not t.is_contiguous():
             raise RuntimeError(f'plan_admit: {name} must be a contiguous {dt} tensor on {dev}')
     p = _lib.ptr
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_plan_admit(p(rows), p(slots), n, int(lazy_n), int(bool(evl)), int(s), int(n0), int(C),
                                        int(R), int(K), p(code), p(slot_of), p(slot_row), p(adm_c0), p(rj), p(rok),
                                        p(pstep), _lib.stream_of(code))

@@ -55,9 +55,9 @@ def copy_rows(dst, dst_idx, src, src_idx=None):
         return dst
     if wd != ws:
         raise RuntimeError(f'row widths differ: {wd} vs {ws}')
-    with torch.cuda.device(dev):
+    with _lib.on_device(dev):
         rc = _lib.lib().elr_copy_rows(_lib.dptr(dst), nd, _lib.ptr(di), _lib.dptr(src), ns, _lib.ptr(si), n, wd,
-                                      ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+                                      ctypes.c_void_p(_lib.raw_stream(dev)))
     _lib.check(rc, 'elr_copy_rows')
     return dst
 
@@ -74,7 +74,7 @@ def mark_rows(rows, n_dev, value, out):
             and n_dev.is_cuda and n_dev.dtype == torch.int64 and out.is_contiguous()):
         raise RuntimeError('mark_rows: rows int64, n_dev int64 and out int32 cuda tensors')
     rows = rows.contiguous()
-    with torch.cuda.device(out.device):
+    with _lib.on_device(out.device):
         rc = _lib.lib().elr_mark_rows(_lib.ptr(rows), _lib.ptr(n_dev), rows.numel(), int(value), _lib.ptr(out),
-                                      out.numel(), ctypes.c_void_p(torch.cuda.current_stream(out.device).cuda_stream))
+                                      out.numel(), ctypes.c_void_p(_lib.raw_stream(out.device)))
     _lib.check(rc, 'elr_mark_rows')
