@@ -83,9 +83,10 @@ class PlanIn(ctypes.Structure):
 
 class PlanOut(ctypes.Structure):
     """elr_plan_out: per-position classes, flags, slots and codes, the class order, the dynamic-slot partition and
-    the host counts."""
+    the host counts; optionally the rows, codes and slots in class-rank order and the L rows in reference order."""
     _fields_ = [('cls', c_vp), ('flags', c_vp), ('sl', c_vp), ('c', c_vp), ('order', c_vp), ('rank', c_vp),
-                ('dyn_out', c_vp), ('counts', c_vp)]
+                ('dyn_out', c_vp), ('counts', c_vp), ('u_ord', c_vp), ('c_ord', c_vp), ('sl_ord', c_vp),
+                ('L_row', c_vp), ('L_cnt', c_vp)]
 
 
 class AssembleArgs(ctypes.Structure):

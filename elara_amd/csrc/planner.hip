@@ -190,9 +190,21 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
     if (k >= 0) {
       int64_t base = 0;
       for (int q = 0; q < k; ++q) base += tot[q];
-      const int64_t pos = base + bu[(int64_t)k * nbu + b] + r;
+      const int64_t within = bu[(int64_t)k * nbu + b] + r;   // position among the rows of its class
+      const int64_t pos = base + within;
       o.order[pos] = i;
       if (o.rank) o.rank[i] = pos;
+      if (o.u_ord) o.u_ord[pos] = p.u[i];
+      if (o.c_ord) o.c_ord[pos] = (int64_t)o.c[i];
+      if (o.sl_ord) o.sl_ord[pos] = (int64_t)o.sl[i];
+      // L rows in the reference's list order: admitted (rank 2), append (rank 5), compact (rank 7)
+      const int64_t loff = k == kRankOf[kLAdm] ? 0
+                           : k == kRankOf[kLApp] ? tot[kRankOf[kLAdm]]
+                           : k == kRankOf[kLCmp] ? tot[kRankOf[kLAdm]] + tot[kRankOf[kLApp]] : -1;
+      if (loff >= 0) {
+        if (o.L_row) o.L_row[loff + within] = p.u[i];
+        if (o.L_cnt) o.L_cnt[loff + within] = (int32_t)o.c[i];
+      }
     }
   } else {
     const int64_t bb = b - nbu;

@@ -18,7 +18,7 @@ F_HIT, F_N, F_L, F_APP, F_ADMIT, F_NEXT = 1, 2, 4, 8, 16, 32
 # counts[16]: 10 class counts, then these
 CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP = 10, 11, 12, 13, 14
 
-PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts')
+PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts u_ord c_ord sl_ord L_row L_cnt')
 
 
 def _dev_i64(t, dev):
@@ -32,7 +32,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     them: slot_of int32 [R], last_seen int32 [R], code int8 [R], kthr int8 [T], toff int64 [T], slot_row int64 [C],
     mat_top / log_top int64 [1].  Returns PlanClass(cls int8 [n], flags uint8 [n], sl int32 [n], c int8 [n],
     order int64 [n] (positions by class rank), rank int64 [n] (its inverse), dyn_out int64 [2 nd], counts int64 [16]
-    on the device)."""
+    on the device, and in class-rank order u_ord, c_ord, sl_ord int64 [n] (u, c, sl at `order`); L_row int64 [n] and
+    L_cnt int32 [n]: the L rows and their codes as admitted, append, compact, valid up to their count)."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -50,7 +51,10 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     out = PlanClass(torch.empty(n, dtype=I8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev),
                     torch.empty(n, dtype=I32, device=dev), torch.empty(n, dtype=I8, device=dev),
                     torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
-                    torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(16, dtype=I64, device=dev))
+                    torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(16, dtype=I64, device=dev),
+                    torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
+                    torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
+                    torch.empty(n, dtype=I32, device=dev))
     p = _lib.ptr
     pin = _lib.PlanIn()
     pin.u, pin.n = u.data_ptr(), n

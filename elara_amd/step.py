@@ -259,6 +259,7 @@ class ElaraStep:
         else:
             ev_slot, keep_dyn = pc.dyn_out[:n_exp], pc.dyn_out[nd + n_exp:]
         rank = pc.rank
+        u_ord, c_ord, sl_ord, L_row, L_cnt = pc.u_ord, pc.c_ord, pc.sl_ord, pc.L_row, pc.L_cnt
         if need > 0:   # overflow: un-admit (non-carry first) and recount
             admit = (pc.flags & F_ADMIT) != 0
             in_next = (pc.flags & F_NEXT) != 0
@@ -271,6 +272,7 @@ class ElaraStep:
             cls = classify_from_flags(pc.flags, admit, self.st_mode == 'T')
             counts = self._host(*torch.bincount(cls.long(), minlength=10))
             order, rank = rank_order(cls)
+            u_ord, c_ord, sl_ord, L_row = u[order], c[order].long(), sl[order].long(), None
         # class-rank bounds: positions b[r] .. b[r+1] of `order` hold the rows of rank r
         b = [0]
         for cl in RANK_CLASSES:
@@ -279,15 +281,16 @@ class ElaraStep:
         p = Plan()
         p.s, p.u, p.n, p.b, p.order, p.rank = s, u, n, b, order, rank
         p.counts = counts
-        u_ord = u[order]
-        c_ord = c[order]
         p.u_ord = u_ord
-        p.hit_slot = sl[order[b[R_HIT]:b[R_HIT + 1]]].long()
+        p.hit_slot = sl_ord[b[R_HIT]:b[R_HIT + 1]]
         rs = lambda r0, r1: slice(b[r0], b[r1 + 1])  # noqa: E731
         # L rows in the reference's order (admitted, append, compact) for the directory's replay inputs
-        Ls = (rs(R_LADM, R_LADM), rs(R_LAPP, R_LAPP), rs(R_LCMP, R_LCMP))
-        p.L_row = torch.cat([u_ord[x] for x in Ls])
-        p.L_cnt = torch.cat([c_ord[x] for x in Ls]).to(I32)
+        if L_row is None:
+            Ls = (rs(R_LADM, R_LADM), rs(R_LAPP, R_LAPP), rs(R_LCMP, R_LCMP))
+            p.L_row = torch.cat([u_ord[x] for x in Ls])
+            p.L_cnt = torch.cat([c_ord[x] for x in Ls]).to(I32)
+        else:
+            p.L_row, p.L_cnt = L_row[:nLa + nLp + nLc], L_cnt[:nLa + nLp + nLc]
         p.nL = (nLa, nLp, nLc)
         st, pv = self.state_list(), self.params()
         (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots,
@@ -309,10 +312,10 @@ class ElaraStep:
                            self.code, self.slot_of, self.slot_row, self.adm_c0, self.rj, self.rok, self.pstep)
         self.dyn_slots = torch.cat([keep_dyn, adm_slots])
         # non-resident lazy rows: append (stay L, entry index = current count) or compact (to M)
-        p.a_ids, p.c_slots = self.be.dir_b(st, pv, u_ord[rs(R_NAPP, R_LAPP)], c_ord[rs(R_NAPP, R_LAPP)].long(),
-                                           u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)].long(), s)
-        p.FN_slot = self.loc[u_ord[rs(R_FN, R_FN)]].to(I64)
-        p.S_slot = self.loc[u_ord[rs(R_S, R_S)]].to(I64)
+        p.a_ids, p.c_slots = self.be.dir_b(st, pv, u_ord[rs(R_NAPP, R_LAPP)], c_ord[rs(R_NAPP, R_LAPP)],
+                                           u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)], s)
+        fs = self.loc[u_ord[rs(R_FN, R_S)]].to(I64)   # MAT slots of the transient F and the S rows (adjacent)
+        p.FN_slot, p.S_slot = fs[:nFn], fs[nFn:]
         st_ = self.stats
         st_['adm'] += n_adm
         st_['ev'] += nev

@@ -248,6 +248,13 @@ typedef struct elr_plan_out {
   int64_t* dyn_out;           /* [2 nd]: slots as [expired | preemptible | protected], then [expired | the rest],
                                  each part in dyn order */
   int64_t* counts;            /* [16] device: 10 class counts, expired, preemptible, protected, mat_top, log_top, 0 */
+  /* Optional outputs in class-rank order (each may be NULL), so that the caller needs no gathers: */
+  int64_t* u_ord;             /* [n] u[order[r]] */
+  int64_t* c_ord;             /* [n] code of u[order[r]] */
+  int64_t* sl_ord;            /* [n] slot_of of u[order[r]] (the hit slots are the first counts[0]) */
+  int64_t* L_row;             /* [n] the L rows as the reference lists them: admitted, append, compact (first
+                                 counts[4] + counts[5] + counts[6] entries) */
+  int32_t* L_cnt;             /* [n] their codes (logged entries), same order */
 } elr_plan_out;
 
 int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd);

@@ -74,7 +74,13 @@ class OracleBackend:
         counts = torch.cat([torch.bincount(cls.long(), minlength=10),
                             torch.stack([exp.sum(), pre.sum(), (dcls == 2).sum()]),
                             mat_top.reshape(1), log_top.reshape(1), torch.zeros(1, dtype=torch.int64)])
-        return PlanClass(cls, flags, sl, c, order, rank, dyn_out, counts)
+        # the rows in class order, and the L rows as the reference lists them: its stable class sort puts classes
+        # 4, 5, 6 (admitted, append, compact) in that order, each in ascending position (srm2/elara.py:260-267)
+        L_sel = [cls == 4, cls == 5, cls == 6]
+        L_row = torch.cat([u[m] for m in L_sel])
+        L_cnt = torch.cat([c[m] for m in L_sel]).to(torch.int32)
+        return PlanClass(cls, flags, sl, c, order, rank, dyn_out, counts, u[order], c[order].long(),
+                         sl[order].long(), L_row, L_cnt)
 
     def segsum(self, g_occ, inv, U, perm=None):
         """Per-unique-row gradient sums (orc_segment_sum's order), row u into perm[u] when perm is given."""
