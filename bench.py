@@ -321,6 +321,7 @@ def mode_c5(args):
                  {'workload': 'C5 full ELARA step, %s: 26 tables (R=%d), batch 16,384 x 26 '
                               'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, tabs.R),
                   'arenas': 'host' if host else 'hbm', 'mat_top': mt, 'log_top': lt,
+                  'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
                   'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, 0.0,
                  extra={'steps_per_s': steps / el, 'stats': s, 'note': 'step_GBps not reported for C5 (mixed '
                         'kernels; per-kernel bytes in profiles/)'})

@@ -41,6 +41,8 @@ SIGNATURES = {
     'elr_selfcheck_quot': (ctypes.c_int, [c_f32, c_vp, c_vp, c_vp, c_vp]),
     'elr_copy_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
     'elr_mark_rows': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_vp]),
+    'elr_glog_put': (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp]),
+    'elr_glog_take': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp]),
     'elr_unique': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_segment_sum': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'elr_adam_dedup': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_f32p, c_vp, c_i64, c_vp]),

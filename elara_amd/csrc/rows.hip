@@ -16,15 +16,40 @@
 
 namespace elr {
 
-template <bool V4>
-__global__ __launch_bounds__(256) void k_copy_rows(float* __restrict__ dst, int64_t dst_rows,
-                                                   const int64_t* __restrict__ dst_idx, const float* __restrict__ src,
-                                                   int64_t src_rows, const int64_t* __restrict__ src_idx, int64_t n,
+// Row index maps: the row of item i, or -1 to skip the item.
+struct IxList {   // idx[i] (NULL: i)
+  const int64_t* idx;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const { return idx ? idx[i] : i; }
+};
+struct IxPair {   // row (dyn[i] - off) * K + j[i] of a [nd, K] grid of rows (j NULL: entry 0)
+  const int64_t* dyn;
+  int64_t off;
+  const int64_t* j;
+  int64_t K, nd;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const {
+    const int64_t d = dyn[i] - off, q = j ? j[i] : 0;
+    return d >= 0 && d < nd && q >= 0 && q < K ? d * K + q : -1;
+  }
+};
+struct IxExpand {   // item i = r * K + k: row clamp(dyn[r], 0, nd - 1) * K + k
+  const int64_t* dyn;
+  int64_t K, nd;
+  __device__ __forceinline__ int64_t operator()(int64_t i) const {
+    const int64_t r = i / K, k = i - r * K;
+    int64_t d = dyn[r];
+    d = d < 0 ? 0 : (d >= nd ? nd - 1 : d);
+    return d * K + k;
+  }
+};
+
+template <bool V4, class DI, class SI>
+__global__ __launch_bounds__(256) void k_copy_rows(float* __restrict__ dst, int64_t dst_rows, DI dix,
+                                                   const float* __restrict__ src, int64_t src_rows, SI six, int64_t n,
                                                    int64_t W) {
   const int lane = threadIdx.x & 63;
   for (int64_t i = wave_id(); i < n; i += wave_count()) {
-    const int64_t d = dst_idx ? dst_idx[i] : i;
-    const int64_t s = src_idx ? src_idx[i] : i;
+    const int64_t d = dix(i);
+    const int64_t s = six(i);
     if (d < 0 || d >= dst_rows || s < 0 || s >= src_rows) continue;
     if (V4) {
       const f32x4* sp = reinterpret_cast<const f32x4*>(src + s * W);
@@ -38,6 +63,19 @@ __global__ __launch_bounds__(256) void k_copy_rows(float* __restrict__ dst, int6
   }
 }
 
+template <class DI, class SI>
+static int copy_rows_launch(float* dst, int64_t dst_rows, DI dix, const float* src, int64_t src_rows, SI six,
+                            int64_t n, int64_t W, void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  int64_t blocks = (n + 3) / 4;
+  if (blocks > 256 * 32) blocks = 256 * 32;
+  if (W % 4 == 0 && aligned16(dst) && aligned16(src))
+    k_copy_rows<true><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dix, src, src_rows, six, n, W);
+  else
+    k_copy_rows<false><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dix, src, src_rows, six, n, W);
+  return launch_status();
+}
+
 }  // namespace elr
 
 extern "C" int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
@@ -46,14 +84,29 @@ extern "C" int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_id
   if (n < 0 || W <= 0 || dst_rows < 0 || src_rows < 0) return ELR_EINVAL;
   if (n == 0) return ELR_OK;
   if (!dst || !src) return ELR_EINVAL;
-  hipStream_t st = (hipStream_t)stream;
-  int64_t blocks = (n + 3) / 4;
-  if (blocks > 256 * 32) blocks = 256 * 32;
-  if (W % 4 == 0 && aligned16(dst) && aligned16(src))
-    k_copy_rows<true><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dst_idx, src, src_rows, src_idx, n, W);
-  else
-    k_copy_rows<false><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dst_idx, src, src_rows, src_idx, n, W);
-  return launch_status();
+  return copy_rows_launch(dst, dst_rows, IxList{dst_idx}, src, src_rows, IxList{src_idx}, n, W, stream);
+}
+
+// Resident-history record glog.index_put_((dyn - dyn_off, j), g) (srm2/elara.py:501, 524): glog [nd, K, W],
+// g [n, W]; j NULL means entry 0 (the admission record); items whose slot or entry is out of range are skipped.
+extern "C" int elr_glog_put(float* glog, int64_t nd, int64_t K, const int64_t* dyn, int64_t dyn_off,
+                            const int64_t* j, const float* g, int64_t n, int64_t W, void* stream) {
+  using namespace elr;
+  if (n < 0 || W <= 0 || nd < 0 || K < 1) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!glog || !dyn || !g) return ELR_EINVAL;
+  return copy_rows_launch(glog, nd * K, IxPair{dyn, dyn_off, j, K, nd}, g, n, IxList{nullptr}, n, W, stream);
+}
+
+// History of rows going back to L (srm2/elara.py:396, 507): logs[ids[r*K + k]] = glog[clamp(dyn[r], 0, nd-1), k]
+// for r < n, k < K; entries whose id is out of range (-1: none) are skipped.
+extern "C" int elr_glog_take(float* logs, int64_t nlogs, const int64_t* ids, const float* glog, int64_t nd,
+                             int64_t K, const int64_t* dyn, int64_t n, int64_t W, void* stream) {
+  using namespace elr;
+  if (n < 0 || W <= 0 || nd < 1 || K < 1 || nlogs < 0) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!logs || !ids || !glog || !dyn) return ELR_EINVAL;
+  return copy_rows_launch(logs, nlogs, IxList{ids}, glog, nd * K, IxExpand{dyn, K, nd}, n * K, W, stream);
 }
 
 // out[rows[i]] = value for i < *n_dev (a device-side count, e.g. the unique rows of a batch whose count the host has

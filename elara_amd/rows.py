@@ -67,6 +67,60 @@ def log_append(logs, ids, g):
     return copy_rows(logs, ids, g, None)
 
 
+def _i64(t, dev, name):
+    if not (t.is_cuda and t.device == dev and t.dtype == torch.int64):
+        raise RuntimeError(f'{name} must be a cuda int64 tensor on {dev}')
+    return t.reshape(-1).contiguous()
+
+
+def glog_put(glog, dyn, j, g, dyn_off=0):
+    """glog.index_put_((dyn - dyn_off, j), g) (srm2/elara.py:501, 524): glog [nd, K, W] cuda float32, dyn / j int64
+    [n] (j None: entry 0), g [n, W].  Items whose slot or entry is out of range are skipped."""
+    if not (glog.is_cuda and glog.dtype == torch.float32 and glog.is_contiguous() and glog.dim() == 3):
+        raise RuntimeError('glog must be a contiguous cuda float32 [nd, K, W] tensor')
+    dev = glog.device
+    nd, K, W = glog.shape
+    dyn = _i64(dyn, dev, 'dyn')
+    n = dyn.numel()
+    if j is not None:
+        j = _i64(j, dev, 'j')
+        if j.numel() != n:
+            raise RuntimeError('j must match dyn')
+    if not (g.is_cuda and g.device == dev and g.dtype == torch.float32 and g.is_contiguous() and g.numel() == n * W):
+        raise RuntimeError(f'g must be a contiguous cuda float32 tensor with {n}x{W} elements')
+    if n == 0:
+        return glog
+    with _lib.on_device(dev):
+        rc = _lib.lib().elr_glog_put(_lib.ptr(glog), nd, K, _lib.ptr(dyn), int(dyn_off), _lib.ptr(j), _lib.ptr(g), n,
+                                     W, ctypes.c_void_p(_lib.raw_stream(dev)))
+    _lib.check(rc, 'elr_glog_put')
+    return glog
+
+
+def glog_take(logs, ids, glog, dyn):
+    """logs[ids[r*K + k]] = glog[clamp(dyn[r], 0, nd-1), k] for every row r and entry k (ids < 0: none): the
+    history entries of evicted rows going back to L, moved into the log arena (srm2/elara.py:396, 507, 569-570).
+    logs [nlogs, W] (GPU or pinned host arena), ids int64 [n*K], glog [nd, K, W], dyn int64 [n]."""
+    if not (glog.is_cuda and glog.dtype == torch.float32 and glog.is_contiguous() and glog.dim() == 3):
+        raise RuntimeError('glog must be a contiguous cuda float32 [nd, K, W] tensor')
+    dev = glog.device
+    nd, K, W = glog.shape
+    nl, wl = _rows2d(logs, 'logs')
+    if wl != W:
+        raise RuntimeError(f'row widths differ: {wl} vs {W}')
+    dyn, ids = _i64(dyn, dev, 'dyn'), _i64(ids, dev, 'ids')
+    n = dyn.numel()
+    if ids.numel() != n * K:
+        raise RuntimeError('ids must hold K entries per row of dyn')
+    if n == 0:
+        return logs
+    with _lib.on_device(dev):
+        rc = _lib.lib().elr_glog_take(_lib.dptr(logs), nl, _lib.ptr(ids), _lib.ptr(glog), nd, K, _lib.ptr(dyn), n, W,
+                                      ctypes.c_void_p(_lib.raw_stream(dev)))
+    _lib.check(rc, 'elr_glog_take')
+    return logs
+
+
 def mark_rows(rows, n_dev, value, out):
     """out[rows[i]] = value for i < n_dev (a device int64 count; rows beyond it are ignored), with no
     synchronisation: rows int64 [n_max] cuda, out int32 [R] cuda."""

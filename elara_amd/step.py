@@ -24,6 +24,8 @@ plan synchronises with the host once (class counts, elara.py:242), plus once mor
 hot-path kernels come from a backend object (HipBackend: this library's HIP kernels), so the same step can be
 driven by another implementation of the kernels (the oracle's) for comparison.
 """
+import gc
+
 import torch
 
 from . import _lib  # noqa: F401  (the library must be present)
@@ -34,7 +36,7 @@ from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
 from .planner import (CNT_EXP, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
                       plan_admit, plan_classify)
-from .rows import copy_rows, mark_rows
+from .rows import copy_rows, glog_put, glog_take, mark_rows
 
 I8, I32, I64 = torch.int8, torch.int32, torch.int64
 # classes (srm2/elara.py:31-32): hit, N admitted / append / compact, L admitted / append / compact, F admitted /
@@ -106,6 +108,12 @@ class HipBackend:
 
     def copy_rows(self, dst, dst_idx, src, src_idx=None):
         copy_rows(dst, dst_idx, src, src_idx)
+
+    def glog_put(self, glog, dyn, j, g, dyn_off=0):
+        glog_put(glog, dyn, j, g, dyn_off)
+
+    def glog_take(self, logs, ids, glog, dyn):
+        glog_take(logs, ids, glog, dyn)
 
 
 class Plan:
@@ -307,7 +315,7 @@ class ElaraStep:
         lazy_n = nNa + nLa
         p.lazy_n = lazy_n
         if lazy_n and self.evl:
-            p.adm_rec_dyn = adm_slots[:lazy_n] - self.n0
+            p.adm_rec_slot = adm_slots[:lazy_n]   # their resident histories start at entry 0 of slot - n0
         self.be.plan_admit(u_ord[rs(R_NADM, R_FADM)], adm_slots, lazy_n, self.evl, s, self.n0, self.C, self.R, K,
                            self.code, self.slot_of, self.slot_row, self.adm_c0, self.rj, self.rok, self.pstep)
         self.dyn_slots = torch.cat([keep_dyn, adm_slots])
@@ -346,23 +354,21 @@ class ElaraStep:
     # ---- update (srm2/elara.py:491-542 and the host worker's writes 544-580, all in HBM) ----
     def update(self, p, G):
         """G [n, D]: the batch's per-row gradients in class-rank order (p.order)."""
-        be, s, D, K, b = self.be, p.s, self.D, self.K, p.b
-        glog2 = self.glog.view(-1, D)
+        be, s, b = self.be, p.s, p.b
         W, w0 = p.work, b[R_NADM]
         rg = lambda r0, r1: G[b[r0]:b[r1 + 1]]  # noqa: E731
         rw = lambda r0, r1: W[b[r0] - w0:b[r1 + 1] - w0]  # noqa: E731
         if b[R_HIT + 1] > b[R_HIT]:
             gh = rg(R_HIT, R_HIT)
             if self.evl:
-                be.copy_rows(glog2, p.hrec_dyn * K + p.hrec_j, gh)
+                be.glog_put(self.glog, p.hrec_dyn, p.hrec_j, gh)
             be.adam(self.pool, p.hit_slot, gh, s)
         if p.ev_slot.numel():
             # evicted slots are read before admissions reuse them: full states of rows going to M into their MAT
             # slots (rows going back to L carry the trash slot), history entries of rows going back to L into
             # their new log ids (-1 for none)
             be.copy_rows(self.mat, p.evf_slots, self.pool, p.ev_slot)
-            src = (p.ev_dyn.clamp(min=0, max=self.Cdyn)[:, None] * K + torch.arange(K, device=self.d)[None, :])
-            be.copy_rows(self.logs, p.evl_ids.reshape(-1), glog2, src.reshape(-1))
+            be.glog_take(self.logs, p.evl_ids, self.glog, p.ev_dyn)
         # Adam on the admitted, compacted and transient work rows (appended rows only log their gradient)
         if b[R_FADM + 1] > b[R_NADM]:
             be.adam_dense(rw(R_NADM, R_FADM), rg(R_NADM, R_FADM), s)
@@ -371,7 +377,7 @@ class ElaraStep:
         if p.adm_slots.numel():
             be.copy_rows(self.pool, p.adm_slots, rw(R_NADM, R_FADM))
         if p.lazy_n and self.evl:   # admission gradient = resident history entry 0 of admitted N / L rows
-            be.copy_rows(glog2, p.adm_rec_dyn * K, rg(R_NADM, R_LADM))
+            be.glog_put(self.glog, p.adm_rec_slot, None, rg(R_NADM, R_LADM), self.n0)
         if p.c_slots.numel():
             be.copy_rows(self.mat, p.c_slots, rw(R_NCMP, R_LCMP))
         if p.a_ids.numel():
@@ -428,11 +434,27 @@ class ElaraStep:
         return out if full else out[:, 0]
 
 
-def run(step, batches, grads, steps=None, on_step=None):
+def run(step, batches, grads, steps=None, on_step=None, freeze_gc=True):
     """Drive `step` over a sequence of batches as srm2/train.py:344-444 does: the batch of logical step j+1 is
     deduplicated and observed L+1 steps ahead (TTL lookahead), plan(s) sees the next depth-1 batches, then the step
     assembles and updates.  batches[j]: int64 occurrence ids; grads(j) or grads[j]: [O_j, D] occurrence gradients.
-    on_step(s, plan) is called after each step."""
+    on_step(s, plan) is called after each step.
+
+    freeze_gc: for the duration of the loop, the objects that exist when it starts are moved out of the Python
+    collector's generations (gc.freeze; gc.unfreeze afterwards).  A step allocates a few thousand short-lived
+    objects, and each full collection they trigger would otherwise walk every long-lived object of the process --
+    on average about 0.17 ms of host time per step at config C5, where the host is the bottleneck."""
+    if not freeze_gc:
+        return _run(step, batches, grads, steps, on_step)
+    gc.collect()
+    gc.freeze()
+    try:
+        return _run(step, batches, grads, steps, on_step)
+    finally:
+        gc.unfreeze()
+
+
+def _run(step, batches, grads, steps, on_step):
     S = len(batches) if steps is None else steps
     U, PLANS = {}, {}
     dev = step.d

@@ -325,6 +325,18 @@ int elr_assemble(const elr_assemble_args* args, void* stream);
 int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
                   const int64_t* src_idx, int64_t n, int64_t W, void* stream);
 
+/* Resident-history record glog.index_put_((dyn - dyn_off, j), g) (srm2/elara.py:501, 524): glog [nd, K, W],
+ * g [n, W], dyn and j int64 [n] (j NULL: entry 0, the admission record of srm2/elara.py:521-524, with dyn the pool
+ * slots and dyn_off the static slot count).  Items whose slot or entry is out of range are skipped. */
+int elr_glog_put(float* glog, int64_t nd, int64_t K, const int64_t* dyn, int64_t dyn_off, const int64_t* j,
+                 const float* g, int64_t n, int64_t W, void* stream);
+
+/* The history entries of evicted rows going back to L, moved into the log arena at their new log ids
+ * (srm2/elara.py:396, 507 gather them from glog; elara.py:569-570 append them): logs[ids[r*K + k]] =
+ * glog[clamp(dyn[r], 0, nd-1), k] for r < n, k < K; ids out of [0, nlogs) (-1: no entry) are skipped. */
+int elr_glog_take(float* logs, int64_t nlogs, const int64_t* ids, const float* glog, int64_t nd, int64_t K,
+                  const int64_t* dyn, int64_t n, int64_t W, void* stream);
+
 /* out[rows[i]] = value for i < min(*n_dev, n_max), with the count read on the device (no counterpart in the
  * reference, which reads the batch's unique count on the host first): the TTL lookahead's record of when rows
  * appear next (srm2/elara.py:160-161) for a batch whose unique count the host reads later.  Rows out of range are

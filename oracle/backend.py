@@ -183,3 +183,18 @@ class OracleBackend:
         s_ = src_idx.numpy().astype(np.int64) if src_idx is not None else np.arange(n)
         ok = (d >= 0) & (d < nd) & (s_ >= 0) & (s_ < ns)
         D2[d[ok]] = S2[s_[ok]]
+
+    def glog_put(self, glog, dyn, j, g, dyn_off=0):
+        """glog.index_put_((dyn - dyn_off, j), g) (srm2/elara.py:501, 524); j None: entry 0."""
+        nd, K, W = glog.shape
+        dd = dyn.long() - dyn_off
+        jj = j.long() if j is not None else torch.zeros_like(dd)
+        ok = (dd >= 0) & (dd < nd) & (jj >= 0) & (jj < K)
+        glog[dd[ok], jj[ok]] = g.reshape(-1, W)[ok]
+
+    def glog_take(self, logs, ids, glog, dyn):
+        """The history entries of rows going back to L into the log arena: glog.view(-1, W) rows
+        dyn * K + k (srm2/elara.py:396, 507) to logs[ids] (ids < 0: none)."""
+        nd, K, W = glog.shape
+        src = (dyn.long().clamp(min=0, max=nd - 1)[:, None] * K + torch.arange(K)[None, :]).reshape(-1)
+        self.copy_rows(logs, ids.reshape(-1), glog.view(-1, W), src)

@@ -122,6 +122,12 @@ def test_planner_executor_dedup_argument_checks():
     assert L.elr_mark_rows(None, fake, 5, 0, fake, 10, None) == -1
     d = ctypes.c_void_p()
     assert L.elr_host_device_ptr(None, ctypes.byref(d)) == -1
+    assert L.elr_glog_put(fake, 10, 3, fake, 0, None, fake, 0, 8, None) == 0                       # n == 0
+    assert L.elr_glog_put(fake, 10, 0, fake, 0, None, fake, 4, 8, None) == -1                      # K < 1
+    assert L.elr_glog_put(fake, 10, 3, None, 0, None, fake, 4, 8, None) == -1                      # no dyn
+    assert L.elr_glog_take(fake, 100, fake, fake, 10, 3, fake, 0, 8, None) == 0                    # n == 0
+    assert L.elr_glog_take(fake, 100, fake, fake, 0, 3, fake, 4, 8, None) == -1                    # nd < 1
+    assert L.elr_glog_take(fake, 100, None, fake, 10, 3, fake, 4, 8, None) == -1                   # no ids
 
 
 def test_ops_raise_without_gpu_tensors():
