@@ -220,6 +220,38 @@ def test_gpu_embedding_backward_matches_aten(dev, n, U, D):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('D', [128, 64, 256, 512, 96])
+def test_gpu_segment_lengths_at_every_boundary(dev, D):
+    """Ids whose occurrence counts sit on each boundary of the kernels' work split -- runs of 10, the first chunk
+    of 60 folded by the id's own wave, partial chunks of 60, hot ids (more than 240 occurrences, folded by a whole
+    block) -- among 4,000 single-occurrence ids: sums bitwise equal to ATen's and the oracle's, and the fused
+    duplicate-id Adam equal to the oracle's sum followed by cpu_adam."""
+    from elara_amd.dedup import adam_dedup, embedding_dense_backward
+    print(f'[gpu-test] segment boundaries D={D}', flush=True)
+    lens = [1, 2, 9, 10, 11, 19, 20, 21, 59, 60, 61, 119, 120, 121, 239, 240, 241, 242, 299, 300, 301, 601, 2999]
+    rng = np.random.default_rng(31)
+    ids = np.concatenate([np.full(L, 10 + 7 * k) for k, L in enumerate(lens)] + [np.arange(1000, 5000)])
+    ids = ids[rng.permutation(ids.size)].astype(np.int64)
+    U = 5000
+    g = (rng.standard_normal((ids.size, D)) * np.exp2(rng.integers(-12, 12, (ids.size, 1)))).astype(np.float32)
+    gd, idd = torch.from_numpy(g).to(dev), torch.from_numpy(ids).to(dev)
+    want = full_sums(ids, g, U)
+    got = embedding_dense_backward(gd, idd, U)
+    aten = torch.ops.aten.embedding_dense_backward(gd, idd, U, -1, False)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got.cpu().numpy()), bits(want))
+    assert np.array_equal(bits(aten.cpu().numpy()), bits(want))
+    state = np.zeros((U, 3, D), np.float32)
+    state[:, 0] = (rng.standard_normal((U, D)) * 0.05).astype(np.float32)
+    gpu = torch.from_numpy(state).to(dev)
+    u, s, _ = O.segment_sum(ids, g)
+    O.cpu_adam(state, u, s, O.adam_scalars(*HP, 3), 8)
+    adam_dedup(gpu, idd, gd, *HP, 3)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(gpu.cpu().numpy()), bits(state))
+
+
+@pytest.mark.gpu
 def test_gpu_aten_golden_cases(dev):
     """The HIP sum reproduces the committed ATen vectors (both paths, -0.0 ids, hot ids)."""
     from elara_amd.dedup import embedding_dense_backward
