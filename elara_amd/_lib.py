@@ -80,7 +80,7 @@ class PlanIn(ctypes.Structure):
     _fields_ = [('u', c_vp), ('n', c_i64), ('next', c_vp * 4), ('n_next', c_i64 * 4), ('nnext', ctypes.c_int),
                 ('slot_of', c_vp), ('last_seen', c_vp), ('code', c_vp), ('kthr', c_vp), ('toff', c_vp), ('T', c_i64),
                 ('dyn', c_vp), ('nd', c_i64), ('slot_row', c_vp), ('mat_top', c_vp), ('log_top', c_vp),
-                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int)]
+                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp)]
 
 
 class PlanOut(ctypes.Structure):
@@ -88,7 +88,7 @@ class PlanOut(ctypes.Structure):
     the host counts; optionally the rows, codes and slots in class-rank order and the L rows in reference order."""
     _fields_ = [('cls', c_vp), ('flags', c_vp), ('sl', c_vp), ('c', c_vp), ('order', c_vp), ('rank', c_vp),
                 ('dyn_out', c_vp), ('counts', c_vp), ('u_ord', c_vp), ('c_ord', c_vp), ('sl_ord', c_vp),
-                ('L_row', c_vp), ('L_cnt', c_vp)]
+                ('L_row', c_vp), ('L_cnt', c_vp), ('loc_ord', c_vp)]
 
 
 class AssembleArgs(ctypes.Structure):

@@ -77,10 +77,11 @@ __global__ __launch_bounds__(kScanBlock) void k_radix_hist_scan(int64_t* __restr
   scan_channels_block(hist + (int64_t)blockIdx.x * ntile, ntile, 1, dtot + blockIdx.x);
 }
 
-// One block: exclusive scan of per-block counts in place, total to *tot.
+// One block: exclusive scan of per-block counts in place, total to *tot (and to *tot2 when given).
 __global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict__ bsum, int64_t n,
-                                                            int64_t* __restrict__ tot) {
+                                                            int64_t* __restrict__ tot, int64_t* __restrict__ tot2) {
   scan_channels_block(bsum, n, 1, tot);
+  if (tot2 && threadIdx.x == 0) *tot2 = *tot;   // the thread that stored *tot
 }
 
 // Stable scatter of one pass.  FIRST: the source keys are the caller's int64 ids and the values are their
@@ -776,14 +777,14 @@ static int radix_sort(const int64_t* ids, int64_t n, int key_bits, DedupScratch&
 // Sort, segment heads (uniq / seg_start / inverse, U in d_tot[0]) and the extra-chunk plan (E in d_tot[1]).
 template <typename Key, int ITEMS>
 static int dedup_core_items(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, int64_t* uniq_out,
-                            int64_t* inverse, hipStream_t st) {
+                            int64_t* inverse, int64_t* n_unique, hipStream_t st) {
   const int cur = radix_sort<Key, ITEMS>(ids, n, key_bits, S, st);
   const Key* sk = (const Key*)S.keys[cur];
   const int32_t* sv = S.vals[cur];
   const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
   int64_t* uniq = uniq_out ? uniq_out : S.uniq;
   k_seg_count<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
-  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot);
+  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot, n_unique);
   k_seg_apply<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start,
                                                                 S.seg_occ0, inverse);
   return cur;
@@ -791,9 +792,10 @@ static int dedup_core_items(const int64_t* ids, int64_t n, int key_bits, DedupSc
 
 template <typename Key>
 static int dedup_core(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, int64_t* uniq_out,
-                      int64_t* inverse, hipStream_t st) {
-  return items_for(n) == kItemsBig ? dedup_core_items<Key, kItemsBig>(ids, n, key_bits, S, uniq_out, inverse, st)
-                                   : dedup_core_items<Key, kItemsSmall>(ids, n, key_bits, S, uniq_out, inverse, st);
+                      int64_t* inverse, int64_t* n_unique, hipStream_t st) {
+  return items_for(n) == kItemsBig
+             ? dedup_core_items<Key, kItemsBig>(ids, n, key_bits, S, uniq_out, inverse, n_unique, st)
+             : dedup_core_items<Key, kItemsSmall>(ids, n, key_bits, S, uniq_out, inverse, n_unique, st);
 }
 
 // ATen's windowed order applies up to kAtenSmall indices: returns the window's shift there, 0 on the sort path.
@@ -803,7 +805,7 @@ template <int ITEMS>
 static void chunk_plan_items(int64_t n, DedupScratch& S, hipStream_t st) {
   const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
   k_chunk_count<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.d_tot + 2);
-  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1);
+  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1, nullptr);
   k_chunk_apply<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.chunk_off,
                                                              S.chunk_seg, S.hot_list, S.d_tot + 2);
 }
@@ -901,10 +903,8 @@ extern "C" int elr_unique(const int64_t* ids, int64_t n, int key_bits, int64_t* 
   DedupScratch S;
   if (scratch_bytes < dedup_scratch_bytes(n, 1, &S, scratch)) return ELR_ECAPACITY;
   hipStream_t st = (hipStream_t)stream;
-  if (key_bits <= 32) dedup_core<uint32_t>(ids, n, key_bits, S, uniq, inverse, st);
-  else dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, st);
-  hipError_t e = hipMemcpyAsync(n_unique, S.d_tot, sizeof(int64_t), hipMemcpyDeviceToDevice, st);
-  if (e != hipSuccess) return (int)e;
+  if (key_bits <= 32) dedup_core<uint32_t>(ids, n, key_bits, S, uniq, inverse, n_unique, st);
+  else dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, n_unique, st);
   return launch_status();
 }
 
@@ -919,8 +919,8 @@ extern "C" int elr_segment_sum(const float* grad, const int64_t* idx, int64_t n,
   if (scratch_bytes < dedup_scratch_bytes(n, D, &S, scratch)) return ELR_ECAPACITY;
   hipStream_t st = (hipStream_t)stream;
   const int kb = bits_for(num_rows);
-  const int cur = kb <= 32 ? dedup_core<uint32_t>(idx, n, kb, S, nullptr, nullptr, st)
-                           : dedup_core<uint64_t>(idx, n, kb, S, nullptr, nullptr, st);
+  const int cur = kb <= 32 ? dedup_core<uint32_t>(idx, n, kb, S, nullptr, nullptr, nullptr, st)
+                           : dedup_core<uint64_t>(idx, n, kb, S, nullptr, nullptr, nullptr, st);
   chunk_plan(n, S, st);
   const AdamScalars none{};
   const int rc = seg_reduce_d<0>(grad, D, S.vals[cur], S, S.uniq, n, out, num_rows, none, st);
@@ -939,8 +939,8 @@ extern "C" int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const
   hipStream_t st = (hipStream_t)stream;
   const AdamScalars s = make_scalars(sc);
   const int kb = bits_for(C);
-  const int cur = kb <= 32 ? dedup_core<uint32_t>(ids, n, kb, S, nullptr, nullptr, st)
-                           : dedup_core<uint64_t>(ids, n, kb, S, nullptr, nullptr, st);
+  const int cur = kb <= 32 ? dedup_core<uint32_t>(ids, n, kb, S, nullptr, nullptr, nullptr, st)
+                           : dedup_core<uint64_t>(ids, n, kb, S, nullptr, nullptr, nullptr, st);
   chunk_plan(n, S, st);
   const int rc = seg_reduce_d<1>(grad, D, S.vals[cur], S, S.uniq, n, state, C, s, st);
   return rc != ELR_OK ? rc : launch_status();
@@ -968,12 +968,10 @@ extern "C" int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64
   DedupScratch S;
   if (plan_bytes < dedup_scratch_bytes(n, D, &S, plan)) return ELR_ECAPACITY;
   hipStream_t st = (hipStream_t)stream;
-  const int cur = key_bits <= 32 ? dedup_core<uint32_t>(ids, n, key_bits, S, uniq, inverse, st)
-                                 : dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, st);
+  const int cur = key_bits <= 32 ? dedup_core<uint32_t>(ids, n, key_bits, S, uniq, inverse, n_unique, st)
+                                 : dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, n_unique, st);
   if (cur != plan_result_buffer(key_bits)) return ELR_EINVAL;
   chunk_plan(n, S, st);
-  hipError_t e = hipMemcpyAsync(n_unique, S.d_tot, sizeof(int64_t), hipMemcpyDeviceToDevice, st);
-  if (e != hipSuccess) return (int)e;
   return launch_status();
 }
 

@@ -160,19 +160,22 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_pl
   }
 }
 
-// Pass 2 (one block): block offsets per class; class totals and the host counts.
+// Pass 2 (one block per channel): block offsets per class; class totals and the host counts.
 __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd,
                                                           int64_t* __restrict__ tot) {
-  scan_channels_block(bu, nbu, kNumCls, tot);
-  scan_channels_block(bd, nbd, kDynCh, tot + kNumCls);
-  __syncthreads();
-  if (threadIdx.x < kNumCls) o.counts[kClsOfRank[threadIdx.x]] = tot[threadIdx.x];
-  if (threadIdx.x < 3) o.counts[kNumCls + threadIdx.x] = tot[kNumCls + threadIdx.x];
-  if (threadIdx.x == 0) {
-    o.counts[13] = p.mat_top ? *p.mat_top : 0;
-    o.counts[14] = p.log_top ? *p.log_top : 0;
-    o.counts[15] = 0;
+  // one block per channel: the kNumCls class channels, then the kDynCh dynamic-slot channels
+  const int c = blockIdx.x;
+  if (c < kNumCls) scan_channels_block(bu + (int64_t)c * nbu, nbu, 1, tot + c);
+  else scan_channels_block(bd + (int64_t)(c - kNumCls) * nbd, nbd, 1, tot + c);
+  if (threadIdx.x == 0) {   // the thread that stored tot[c]
+    if (c < kNumCls) o.counts[kClsOfRank[c]] = tot[c];
+    else if (c < kNumCls + 3) o.counts[c] = tot[c];
+    if (c == 0) {
+      o.counts[13] = p.mat_top ? *p.mat_top : 0;
+      o.counts[14] = p.log_top ? *p.log_top : 0;
+      o.counts[15] = 0;
+    }
   }
 }
 
@@ -197,6 +200,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
       if (o.u_ord) o.u_ord[pos] = p.u[i];
       if (o.c_ord) o.c_ord[pos] = (int64_t)o.c[i];
       if (o.sl_ord) o.sl_ord[pos] = (int64_t)o.sl[i];
+      if (o.loc_ord && p.loc) o.loc_ord[pos] = (int64_t)p.loc[p.u[i]];
       // L rows in the reference's list order: admitted (rank 2), append (rank 5), compact (rank 7)
       const int64_t loff = k == kRankOf[kLAdm] ? 0
                            : k == kRankOf[kLApp] ? tot[kRankOf[kLAdm]]
@@ -279,7 +283,7 @@ extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out,
   int64_t* bd = bu + kNumCls * nbu;
   int64_t* tot = bd + kDynCh * nbd;
   if (nbu + nbd > 0) k_plan_count<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd);
-  k_plan_scan<<<1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
+  k_plan_scan<<<kNumCls + kDynCh, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
   if (nbu + nbd > 0) k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
   return launch_status();
 }

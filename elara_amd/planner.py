@@ -18,14 +18,15 @@ F_HIT, F_N, F_L, F_APP, F_ADMIT, F_NEXT = 1, 2, 4, 8, 16, 32
 # counts[16]: 10 class counts, then these
 CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP = 10, 11, 12, 13, 14
 
-PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts u_ord c_ord sl_ord L_row L_cnt')
+PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts u_ord c_ord sl_ord L_row L_cnt loc_ord')
 
 
 def _dev_i64(t, dev):
     return t.to(device=dev, dtype=I64).contiguous()
 
 
-def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t):
+def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
+                  loc=None):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -33,7 +34,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     mat_top / log_top int64 [1].  Returns PlanClass(cls int8 [n], flags uint8 [n], sl int32 [n], c int8 [n],
     order int64 [n] (positions by class rank), rank int64 [n] (its inverse), dyn_out int64 [2 nd], counts int64 [16]
     on the device, and in class-rank order u_ord, c_ord, sl_ord int64 [n] (u, c, sl at `order`); L_row int64 [n] and
-    L_cnt int32 [n]: the L rows and their codes as admitted, append, compact, valid up to their count)."""
+    L_cnt int32 [n]: the L rows and their codes as admitted, append, compact, valid up to their count; loc_ord int64
+    [n]: loc (int32 [R + 1], when given) of the rows in class-rank order, else None)."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -46,6 +48,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
                         (mat_top, I64, 'mat_top'), (log_top, I64, 'log_top')):
         if t.dtype != dt or t.device != dev or not t.is_contiguous():
             raise RuntimeError(f'plan_classify: {name} must be a contiguous {dt} tensor on {dev}')
+    if loc is not None and (loc.dtype != I32 or loc.device != dev or not loc.is_contiguous()):
+        raise RuntimeError(f'plan_classify: loc must be a contiguous {I32} tensor on {dev}')
     dyn = _dev_i64(dyn, dev)
     n, nd = u.numel(), dyn.numel()
     out = PlanClass(torch.empty(n, dtype=I8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev),
@@ -54,7 +58,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
                     torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(16, dtype=I64, device=dev),
                     torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
                     torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
-                    torch.empty(n, dtype=I32, device=dev))
+                    torch.empty(n, dtype=I32, device=dev),
+                    torch.empty(n, dtype=I64, device=dev) if loc is not None else None)
     p = _lib.ptr
     pin = _lib.PlanIn()
     pin.u, pin.n = u.data_ptr(), n
@@ -67,7 +72,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     pin.dyn, pin.nd, pin.slot_row = dyn.data_ptr(), nd, slot_row.data_ptr()
     pin.mat_top, pin.log_top = mat_top.data_ptr(), log_top.data_ptr()
     pin.s, pin.K, pin.want_t = int(s), int(K), int(bool(want_t))
-    pout = _lib.PlanOut(*[t.data_ptr() for t in out])
+    pin.loc = loc.data_ptr() if loc is not None else None
+    pout = _lib.PlanOut(*[t.data_ptr() if t is not None else None for t in out])
     nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
     scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
     with _lib.on_device(dev):

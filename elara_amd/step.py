@@ -248,7 +248,7 @@ class ElaraStep:
         # classes, class order, expired / preemptible / protected dynamic slots, counts (srm2/elara.py:214-267)
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
-                                   self.st_mode == 'T')
+                                   self.st_mode == 'T', self.loc)
         vals = self._host_list(pc.counts)
         counts = vals[:10]
         n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]
@@ -267,7 +267,7 @@ class ElaraStep:
         else:
             ev_slot, keep_dyn = pc.dyn_out[:n_exp], pc.dyn_out[nd + n_exp:]
         rank = pc.rank
-        u_ord, c_ord, sl_ord, L_row, L_cnt = pc.u_ord, pc.c_ord, pc.sl_ord, pc.L_row, pc.L_cnt
+        u_ord, c_ord, sl_ord, L_row, L_cnt, loc_ord = pc.u_ord, pc.c_ord, pc.sl_ord, pc.L_row, pc.L_cnt, pc.loc_ord
         if need > 0:   # overflow: un-admit (non-carry first) and recount
             admit = (pc.flags & F_ADMIT) != 0
             in_next = (pc.flags & F_NEXT) != 0
@@ -281,6 +281,7 @@ class ElaraStep:
             counts = self._host(*torch.bincount(cls.long(), minlength=10))
             order, rank = rank_order(cls)
             u_ord, c_ord, sl_ord, L_row = u[order], c[order].long(), sl[order].long(), None
+            loc_ord = self.loc[u_ord].long()
         # class-rank bounds: positions b[r] .. b[r+1] of `order` hold the rows of rank r
         b = [0]
         for cl in RANK_CLASSES:
@@ -322,7 +323,8 @@ class ElaraStep:
         # non-resident lazy rows: append (stay L, entry index = current count) or compact (to M)
         p.a_ids, p.c_slots = self.be.dir_b(st, pv, u_ord[rs(R_NAPP, R_LAPP)], c_ord[rs(R_NAPP, R_LAPP)],
                                            u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)], s)
-        fs = self.loc[u_ord[rs(R_FN, R_S)]].to(I64)   # MAT slots of the transient F and the S rows (adjacent)
+        # MAT slots of the transient F and the S rows (adjacent ranks; the directory calls above move no F/S row)
+        fs = loc_ord[rs(R_FN, R_S)]
         p.FN_slot, p.S_slot = fs[:nFn], fs[nFn:]
         st_ = self.stats
         st_['adm'] += n_adm

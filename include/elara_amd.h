@@ -236,6 +236,7 @@ typedef struct elr_plan_in {
   int64_t s;                  /* logical step */
   int K;
   int want_t;                 /* transient updates of non-admitted F rows (st_mode 'T') */
+  const int32_t* loc;         /* [R + 1] MAT slot of each row (only read when out->loc_ord is set) */
 } elr_plan_in;
 
 typedef struct elr_plan_out {
@@ -255,6 +256,8 @@ typedef struct elr_plan_out {
   int64_t* L_row;             /* [n] the L rows as the reference lists them: admitted, append, compact (first
                                  counts[4] + counts[5] + counts[6] entries) */
   int32_t* L_cnt;             /* [n] their codes (logged entries), same order */
+  int64_t* loc_ord;           /* [n] loc of u[order[r]]: the MAT slots of the transient F and S rows, which the
+                                 step's directory calls do not move (they change only resident and N/L rows) */
 } elr_plan_out;
 
 int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd);

@@ -24,7 +24,7 @@ class OracleBackend:
         return u, inv, None
 
     def plan_classify(self, u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s,
-                      K, want_t):
+                      K, want_t, loc=None):
         """Restatement of the planner's classification (srm2/elara.py:214-267) with torch ops on CPU tensors:
         slot lookup and hits (:219-220), next-batch membership (:223-226), admission by TTL (:221), protection of
         the slots the next batches need through a scatter of their slots (:227-229), expiry of unprotected
@@ -80,7 +80,7 @@ class OracleBackend:
         L_row = torch.cat([u[m] for m in L_sel])
         L_cnt = torch.cat([c[m] for m in L_sel]).to(torch.int32)
         return PlanClass(cls, flags, sl, c, order, rank, dyn_out, counts, u[order], c[order].long(),
-                         sl[order].long(), L_row, L_cnt)
+                         sl[order].long(), L_row, L_cnt, loc[u[order]].long() if loc is not None else None)
 
     def segsum(self, g_occ, inv, U, perm=None):
         """Per-unique-row gradient sums (orc_segment_sum's order), row u into perm[u] when perm is given."""
