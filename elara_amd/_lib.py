@@ -80,7 +80,7 @@ class PlanIn(ctypes.Structure):
     _fields_ = [('u', c_vp), ('n', c_i64), ('next', c_vp * 4), ('n_next', c_i64 * 4), ('nnext', ctypes.c_int),
                 ('slot_of', c_vp), ('last_seen', c_vp), ('code', c_vp), ('kthr', c_vp), ('toff', c_vp), ('T', c_i64),
                 ('dyn', c_vp), ('nd', c_i64), ('slot_row', c_vp), ('mat_top', c_vp), ('log_top', c_vp),
-                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp)]
+                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp), ('R', c_i64)]
 
 
 class PlanOut(ctypes.Structure):

@@ -66,8 +66,17 @@ struct RowClass {
   int cls, flags, sl, c;
 };
 
+__device__ __forceinline__ bool row_ok(const elr_plan_in& p, int64_t r) { return p.R <= 0 || (r >= 0 && r < p.R); }
+
 __device__ __forceinline__ RowClass classify_row(const elr_plan_in& p, int64_t r) {
   RowClass o;
+  if (!row_ok(p, r)) {   // out of range: class S with no slot, which the executor's copies and updates skip
+    o.cls = kS;
+    o.flags = 0;
+    o.sl = -1;
+    o.c = p.K + 1;
+    return o;
+  }
   o.sl = p.slot_of[r];
   const bool hit = o.sl >= 0;
   const bool admit = !hit && (int64_t)p.last_seen[r] > p.s;
@@ -90,6 +99,7 @@ __device__ __forceinline__ RowClass classify_row(const elr_plan_in& p, int64_t r
 
 __device__ __forceinline__ int dyn_class(const elr_plan_in& p, int64_t d) {
   const int64_t r = p.slot_row[d];
+  if (r >= 0 && !row_ok(p, r)) return 1;   // a slot holding an out-of-range row: unprotected, not expired
   const bool prot = r >= 0 && in_next(p, r);
   if (prot) return 2;
   const bool expired = r < 0 || (int64_t)p.last_seen[r] <= p.s;
@@ -200,7 +210,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
       if (o.u_ord) o.u_ord[pos] = p.u[i];
       if (o.c_ord) o.c_ord[pos] = (int64_t)o.c[i];
       if (o.sl_ord) o.sl_ord[pos] = (int64_t)o.sl[i];
-      if (o.loc_ord && p.loc) o.loc_ord[pos] = (int64_t)p.loc[p.u[i]];
+      if (o.loc_ord && p.loc) o.loc_ord[pos] = row_ok(p, p.u[i]) ? (int64_t)p.loc[p.u[i]] : -1;
       // L rows in the reference's list order: admitted (rank 2), append (rank 5), compact (rank 7)
       const int64_t loff = k == kRankOf[kLAdm] ? 0
                            : k == kRankOf[kLApp] ? tot[kRankOf[kLAdm]]

@@ -26,7 +26,7 @@ def _dev_i64(t, dev):
 
 
 def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
-                  loc=None):
+                  loc=None, R=0):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -35,7 +35,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     order int64 [n] (positions by class rank), rank int64 [n] (its inverse), dyn_out int64 [2 nd], counts int64 [16]
     on the device, and in class-rank order u_ord, c_ord, sl_ord int64 [n] (u, c, sl at `order`); L_row int64 [n] and
     L_cnt int32 [n]: the L rows and their codes as admitted, append, compact, valid up to their count; loc_ord int64
-    [n]: loc (int32 [R + 1], when given) of the rows in class-rank order, else None)."""
+    [n]: loc (int32 [R + 1], when given) of the rows in class-rank order, else None).  With R > 0 a row of u outside
+    [0, R) is classified S with no slot and no MAT slot (skipped by every later copy and update)."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -73,6 +74,7 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     pin.mat_top, pin.log_top = mat_top.data_ptr(), log_top.data_ptr()
     pin.s, pin.K, pin.want_t = int(s), int(K), int(bool(want_t))
     pin.loc = loc.data_ptr() if loc is not None else None
+    pin.R = int(R)
     pout = _lib.PlanOut(*[t.data_ptr() if t is not None else None for t in out])
     nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
     scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)

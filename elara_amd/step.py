@@ -248,7 +248,7 @@ class ElaraStep:
         # classes, class order, expired / preemptible / protected dynamic slots, counts (srm2/elara.py:214-267)
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
-                                   self.st_mode == 'T', self.loc)
+                                   self.st_mode == 'T', self.loc, self.R)
         vals = self._host_list(pc.counts)
         counts = vals[:10]
         n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]

@@ -237,6 +237,8 @@ typedef struct elr_plan_in {
   int K;
   int want_t;                 /* transient updates of non-admitted F rows (st_mode 'T') */
   const int32_t* loc;         /* [R + 1] MAT slot of each row (only read when out->loc_ord is set) */
+  int64_t R;                  /* rows: a row of u outside [0, R) is classified S with slot -1, code K+1 and MAT
+                                 slot -1, which every later copy and update skips (0: no check) */
 } elr_plan_in;
 
 typedef struct elr_plan_out {

@@ -24,7 +24,7 @@ class OracleBackend:
         return u, inv, None
 
     def plan_classify(self, u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s,
-                      K, want_t, loc=None):
+                      K, want_t, loc=None, R=0):
         """Restatement of the planner's classification (srm2/elara.py:214-267) with torch ops on CPU tensors:
         slot lookup and hits (:219-220), next-batch membership (:223-226), admission by TTL (:221), protection of
         the slots the next batches need through a scatter of their slots (:227-229), expiry of unprotected

@@ -161,6 +161,31 @@ def test_gpu_plan_classify_matches_oracle(dev, name):
 
 
 @pytest.mark.gpu
+def test_gpu_plan_classify_skips_rows_out_of_range(dev):
+    """Rows of u outside [0, R) come out as class S with no pool slot, code K+1 and MAT slot -1 (which every later
+    copy and update skips) and are read nowhere out of bounds; the rows in range are classified as without them."""
+    from elara_amd.planner import plan_classify
+    print('[gpu-test] plan classify, rows out of range', flush=True)
+    cfg = config(T=4, lo=200, hi=2000, B=200, steps=4, C=800, n_static=300)
+    st = make(cfg, dev)
+    R, K = st.R, st.K
+    u = torch.unique(cfg['batches'][0].to(dev))
+    bad = torch.tensor([R, R + 5, 2**40], dtype=torch.int64, device=dev)
+
+    def classify(uu):
+        return plan_classify(uu, [], st.slot_of, st.last_seen, st.code, st.kthr, st.toff, st.dyn_slots, st.slot_row,
+                             st.mat_top, st.log_top, 1, K, True, st.loc, R)
+    a, b = classify(u), classify(torch.cat([u, bad]))
+    torch.cuda.synchronize()
+    n = u.numel()
+    for f in ('cls', 'flags', 'sl', 'c'):
+        assert torch.equal(getattr(b, f)[:n].cpu(), getattr(a, f).cpu()), f
+    assert (b.cls[n:] == 9).all() and (b.sl[n:] == -1).all() and (b.c[n:] == K + 1).all() and (b.flags[n:] == 0).all()
+    assert (b.loc_ord[b.rank[n:]] == -1).all()
+    assert int(b.counts[9]) == int(a.counts[9]) + 3
+
+
+@pytest.mark.gpu
 def test_gpu_assemble_and_admit_match_oracle(dev):
     """elr_assemble (init / replay by entry id / MAT gather segments, including empty ones) and elr_plan_admit
     against the oracle backend's restatements, on synthetic arenas."""
