@@ -10,6 +10,11 @@ roofline: the dominant kernel (replay) -- algorithmic bytes per launch / its mea
 recorded on the launch stream around every 4th timed step's launches; peak 8 TB/s.  cpu_baseline: the CPU oracle's replay + Adam (a C port of the
 reference CPU path, same thread split) on a bounded sample, timed on this host.
 
+Warm-up: the first 20-30 ms of sustained load run at a lower engine clock (measured on the headline step: replay
+288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound, 140 us
+throughout).  The defaults (200 untimed steps, about 55 ms, then 200 timed steps) measure the steady state; an
+explicit --warmup W is honoured exactly.  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode headline|copy] [--no-cpu]
 """
 import argparse
@@ -172,14 +177,25 @@ def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
     return None
 
 
-def _timed_steps(step_fn, steps, warmup):
-    """Run warmup + steps calls of step_fn(i); the timed steps are bracketed by device synchronisation.  Returns
-    (seconds for the timed steps, per-step ms from events on the current stream)."""
+SETTLE_S = 0.08   # --mode c1/c3/c4: untimed load before timing (the engine clock's ramp takes 20-30 ms)
+
+
+def _timed_steps(step_fn, steps, warmup, settle_s=0.0):
+    """Run `warmup` untimed calls of step_fn(i), more (whole batches of `warmup`) until at least `settle_s` seconds
+    of untimed work have passed, then `steps` timed calls bracketed by device synchronisation.  Returns (seconds for
+    the timed steps, per-step ms from events on the current stream, number of untimed calls)."""
     import torch
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        step_fn(i)
-    torch.cuda.synchronize()
+    done = 0
+    t_w = time.perf_counter()
+    while True:
+        for _ in range(warmup):
+            step_fn(done)
+            done += 1
+        torch.cuda.synchronize()
+        if warmup == 0 or time.perf_counter() - t_w >= settle_s:
+            break
+    warmup = done
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
@@ -188,7 +204,7 @@ def _timed_steps(step_fn, steps, warmup):
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    return el, [a.elapsed_time(b) for a, b in ev]
+    return el, [a.elapsed_time(b) for a, b in ev], warmup
 
 
 def _line(metric, value, unit, args, steps, warmup, el, config, gbytes_per_step, dtype='f32', extra=None):
@@ -214,8 +230,10 @@ def mode_c1(args):
     rng = np.random.default_rng(0)
     ids = [torch.from_numpy(synth.unique_rows(rng, R, n)).to(dev) for _ in range(10)]
     gs = [torch.from_numpy(synth.grads(rng, n, D)).to(dev) for _ in range(10)]
-    steps, warmup = 10, 2
-    el, ms = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 10], *synth.ADAM, i + 1), steps, warmup)
+    # t = 1..10 on the timed steps: call i uses batch i % 10 at step (i % 10) + 1, and the warm-up is whole tens
+    steps = 10
+    el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 10], *synth.ADAM, i % 10 + 1),
+                                  steps, 10, SETTLE_S)
     return _line('C1 row-sparse Adam rows/s (d=64)', n * steps / el, 'rows/s', args, steps, warmup, el,
                  {'workload': 'C1 row-sparse Adam: 1,048,576 x 64 fp32 table, 65,536 unique rows per step',
                   'rows_per_step': n, 'dim': D}, adam_bytes(n, D) / 1e9,
@@ -239,8 +257,9 @@ def mode_c3(args):
     ids = [torch.from_numpy(h).to(dev) for h in host]
     gen = torch.Generator(dev).manual_seed(0)
     gs = [torch.randn(B * F, D, device=dev, generator=gen) * 1e-3 for _ in range(4)]
-    steps, warmup = args.steps_c3, 3
-    el, ms = _timed_steps(lambda i: adam_dedup(table, ids[i % 4], gs[i % 4], *synth.ADAM, i + 1), steps, warmup)
+    steps = args.steps_c3
+    el, ms, warmup = _timed_steps(lambda i: adam_dedup(table, ids[i % 4], gs[i % 4], *synth.ADAM, i + 1), steps, 4,
+                                  SETTLE_S)
     O = B * F
     Umean = float(np.mean(U))
     byts = (O * (4 * D + 8) + Umean * (28 * D + 8)) / 1e9
@@ -268,8 +287,9 @@ def mode_c4(args):
     ids = [torch.from_numpy(synth.unique_zipf(rng, z, n)).to(dev) for _ in range(10)]
     gen = torch.Generator(dev).manual_seed(4)
     gs = [torch.randn(n, D, device=dev, generator=gen) * 1e-3 for _ in range(4)]
-    steps, warmup = 50, 3
-    el, ms = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 4], *synth.ADAM, i + 1), steps, warmup)
+    steps = 50
+    el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 4], *synth.ADAM, i + 1), steps, 10,
+                                  SETTLE_S)
     return _line('C4 large-row sparse Adam rows/s (d=256, 153.6 GB table)', n * steps / el, 'rows/s', args, steps,
                  warmup, el, {'workload': 'C4 large-row stress: 50,000,000 x 256 fp32 table (w, m, v: 153.6 GB in '
                                           'HBM), 262,144 unique Zipf(1.1) rows per step', 'rows_per_step': n,
@@ -342,7 +362,7 @@ def copy_calibration(args):
     b = torch.empty_like(a)
     for _ in range(3):
         b.copy_(a)
-    el, ms = _timed_steps(lambda i: b.copy_(a), args.steps, 0)
+    el, ms, _ = _timed_steps(lambda i: b.copy_(a), args.steps, 0)
     mean_ms = float(np.mean(ms))
     return {'mode': 'copy', 'bytes_read_per_launch': nbytes, 'bytes_written_per_launch': nbytes,
             'launches': args.steps + 3, 'mean_launch_ms': mean_ms,
@@ -353,12 +373,12 @@ def copy_calibration(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=50)
-    ap.add_argument('--warmup', type=int, default=5)
+    ap.add_argument('--steps', type=int, default=200)
+    ap.add_argument('--warmup', type=int, default=200)
     ap.add_argument('--mode', default='headline', choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'all'])
     ap.add_argument('--steps-c3', type=int, default=100)
     ap.add_argument('--steps-c5', type=int, default=200)
-    ap.add_argument('--warmup-c5', type=int, default=20)
+    ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     args = ap.parse_args()

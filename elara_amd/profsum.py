@@ -3,6 +3,9 @@
 Counterpart of the reference's torch.profiler summary (srm2/profsum.py:10-25), for rocprofv3 runs:
 
     python -m elara_amd.profsum stats  <run>_results.db            per-kernel calls / total / mean / share
+    python -m elara_amd.profsum stats --last N <run>_results.db    the same over each kernel's last N dispatches
+                                                                   (the timed steps of a run whose untimed
+                                                                   warm-up came first), with min and median
     python -m elara_amd.profsum pmc    <run>_results.db            per-kernel mean of each PMC counter per dispatch
     python -m elara_amd.profsum traffic --kernel SUBSTR \
         --fetch F.db --write W.db --copy-fetch CF.db --copy-write CW.db --copy-bytes N
@@ -33,6 +36,21 @@ def kernel_stats(db):
                                            'from top_kernels order by total_duration desc')]
 
 
+def kernel_stats_last(db, last):
+    """[(name, calls, total_us, mean_us, pct, min_us, median_us)] over each kernel's last `last` dispatches."""
+    per = {}
+    for n, d in _rows(db, 'select name, duration from kernels order by start'):
+        per.setdefault(n, []).append(float(d) / 1e3)
+    out = []
+    for n, ds in per.items():
+        ds = ds[-last:]
+        srt = sorted(ds)
+        out.append((n, len(ds), sum(ds), sum(ds) / len(ds), 0.0, srt[0], srt[len(srt) // 2]))
+    tot = sum(r[2] for r in out) or 1.0
+    out = [r[:4] + (100.0 * r[2] / tot,) + r[5:] for r in out]
+    return sorted(out, key=lambda r: -r[2])
+
+
 def pmc_means(db):
     """{(kernel name, counter): (dispatches, mean value per dispatch)}."""
     out = {}
@@ -54,6 +72,11 @@ def short(name, width=72):
 
 
 def cmd_stats(a):
+    if a.last:
+        print(f'| kernel | calls | total us | mean us | % | min us | median us |\n|---|---:|---:|---:|---:|---:|---:|')
+        for n, c, t, m, p, lo, md in kernel_stats_last(a.db, a.last):
+            print(f'| `{short(n)}` | {c} | {t:.1f} | {m:.2f} | {p:.1f} | {lo:.2f} | {md:.2f} |')
+        return
     print(f'| kernel | calls | total us | mean us | % |\n|---|---:|---:|---:|---:|')
     for n, c, t, m, p in kernel_stats(a.db):
         print(f'| `{short(n)}` | {c} | {t:.1f} | {m:.2f} | {p:.1f} |')
@@ -88,7 +111,8 @@ def cmd_traffic(a):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest='cmd', required=True)
-    s = sub.add_parser('stats'); s.add_argument('db'); s.set_defaults(fn=cmd_stats)
+    s = sub.add_parser('stats'); s.add_argument('db'); s.add_argument('--last', type=int, default=0)
+    s.set_defaults(fn=cmd_stats)
     p = sub.add_parser('pmc'); p.add_argument('db'); p.set_defaults(fn=cmd_pmc)
     t = sub.add_parser('traffic')
     t.add_argument('--kernel', required=True)
