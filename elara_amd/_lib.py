@@ -55,6 +55,7 @@ SIGNATURES = {
     'elr_plan_admit': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_i64, c_i64, c_i64, c_i64, ctypes.c_int,
                                       c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'elr_assemble': (ctypes.c_int, [c_vp, c_vp]),
+    'elr_step_update': (ctypes.c_int, [c_vp, c_vp]),
     'elr_dedup_plan_bytes': (c_i64, [c_i64, c_i64]),
     'elr_dedup_plan': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
     'elr_segment_sum_plan': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
@@ -98,6 +99,18 @@ class AssembleArgs(ctypes.Structure):
                 ('seg_aux', c_i64 * 16), ('seed', c_u32), ('bound', c_f32), ('L_ids', c_vp), ('L_steps', c_vp),
                 ('L_cnt', c_vp), ('nL', c_i64), ('logs', c_vp), ('nlogs', c_i64), ('table', c_vp), ('recip', c_vp),
                 ('table_rows', c_i64), ('mat', c_vp), ('mat_rows', c_i64), ('loc', c_vp), ('R', c_i64)]
+
+
+
+class UpdateArgs(ctypes.Structure):
+    """elr_update_args: the executor's update of one step (srm2/elara.py:491-580)."""
+    _fields_ = [('D', c_i64), ('K', c_i64), ('pool', c_vp), ('pool_rows', c_i64), ('mat', c_vp), ('mat_rows', c_i64),
+                ('logs', c_vp), ('log_rows', c_i64), ('glog', c_vp), ('glog_slots', c_i64), ('grad', c_vp),
+                ('work', c_vp), ('b', c_i64 * 11), ('step', c_i64), ('lr', ctypes.c_double), ('b1', ctypes.c_double),
+                ('b2', ctypes.c_double), ('eps', ctypes.c_double), ('evl', ctypes.c_int32), ('hit_slot', c_vp),
+                ('hrec_dyn', c_vp), ('hrec_j', c_vp), ('nev', c_i64), ('ev_slot', c_vp), ('evf_slots', c_vp),
+                ('evl_ids', c_vp), ('ev_dyn', c_vp), ('adm_slots', c_vp), ('lazy_n', c_i64), ('n0', c_i64),
+                ('c_slots', c_vp), ('a_ids', c_vp), ('fn_slot', c_vp), ('s_slot', c_vp)]
 
 
 def lib():

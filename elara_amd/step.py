@@ -24,6 +24,7 @@ plan synchronises with the host once (class counts, elara.py:242), plus once mor
 hot-path kernels come from a backend object (HipBackend: this library's HIP kernels), so the same step can be
 driven by another implementation of the kernels (the oracle's) for comparison.
 """
+import ctypes
 import gc
 
 import torch
@@ -65,6 +66,7 @@ class HipBackend:
         self.D, self.seed, self.bound, self.hp = D, seed, bound, hp
         self.table = ScalarTable(*hp, max_step, device)
         self.dx = dir_ext()
+        self._arenas = None
 
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
@@ -114,6 +116,38 @@ class HipBackend:
 
     def glog_take(self, logs, ids, glog, dyn):
         glog_take(logs, ids, glog, dyn)
+
+    def step_update(self, es, p, G):
+        """ElaraStep.update in one native call (elr_step_update): the same launches in the same order, issued from
+        C++ with no per-launch Python work."""
+        if self._arenas is None or self._arenas[0] is not es:
+            self._arenas = (es, _lib.dptr(es.pool).value, _lib.dptr(es.mat).value, _lib.dptr(es.logs).value,
+                            _lib.dptr(es.glog).value)
+        _, pool, mat, logs, glog = self._arenas
+        b = p.b
+        nh, nev = b[R_HIT + 1] - b[R_HIT], p.ev_slot.numel()
+        a = _lib.UpdateArgs(
+            self.D, es.K, pool, es.pool.shape[0], mat, es.mat.shape[0], logs, es.logs.shape[0], glog,
+            es.glog.shape[0], _p64(G, b[-1] * self.D, torch.float32), _p64(p.work, (b[R_S] - b[R_NADM]) * 3 * self.D,
+                                                                        torch.float32),
+            (_lib.c_i64 * 11)(*b), p.s, *self.hp, int(bool(es.evl)),
+            _p64(p.hit_slot, nh), _p64(p.hrec_dyn, nh) if es.evl else 0, _p64(p.hrec_j, nh) if es.evl else 0,
+            nev, _p64(p.ev_slot, nev), _p64(p.evf_slots, nev), _p64(p.evl_ids, nev * es.K), _p64(p.ev_dyn, nev),
+            _p64(p.adm_slots, b[R_FADM + 1] - b[R_NADM]), p.lazy_n, es.n0,
+            _p64(p.c_slots, b[R_LCMP + 1] - b[R_NCMP]), _p64(p.a_ids, b[R_LAPP + 1] - b[R_NAPP]),
+            _p64(p.FN_slot, b[R_FN + 1] - b[R_FN]), _p64(p.S_slot, b[R_S + 1] - b[R_S]))
+        _lib.check(_lib.lib().elr_step_update(ctypes.byref(a), ctypes.c_void_p(_lib.raw_stream(G.device))),
+                   'elr_step_update')
+
+
+def _p64(t, n, dtype=torch.int64):
+    """Address of a contiguous tensor of the given dtype on the GPU holding n elements (0 when n == 0)."""
+    if n == 0:
+        return 0
+    if t.dtype != dtype or not t.is_contiguous() or t.numel() != n or not t.is_cuda:
+        raise RuntimeError(f'step_update: expected a contiguous cuda {dtype} tensor of {n} elements, got '
+                           f'{tuple(t.shape)} {t.dtype} {t.device}')
+    return t.data_ptr()
 
 
 class Plan:
@@ -190,6 +224,7 @@ class ElaraStep:
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs')}
         self._deferred = []
+        self._pin = None
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
@@ -229,6 +264,34 @@ class ElaraStep:
         self.stats['syncs'] += 1
         return torch.stack([t.reshape(()).to(I64) for t in ts]).tolist()
 
+    def _host_list_async(self, t):
+        """Start reading t (a device int64 vector) and the deferred counts to the host; returns a function that waits
+        for them and returns t's values.  On the GPU the values go to pinned memory by an asynchronous copy
+        followed by an event, so the host waits only for the work queued before that copy: kernels the caller
+        queues after this call keep the GPU busy while the host waits and then acts on the values."""
+        if not (t.is_cuda and self.d.type == 'cuda'):
+            vals = self._host_list(t)
+            return lambda: vals
+        self.stats['syncs'] += 1
+        n = t.numel()
+        dev = torch.cat([t.reshape(-1).to(I64)] + [x.reshape(-1) for x, _ in self._deferred])
+        m = dev.numel()
+        if self._pin is None or self._pin.numel() < m:
+            self._pin = torch.empty(max(m, 64), dtype=I64, pin_memory=True)
+        host = self._pin[:m]
+        host.copy_(dev, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        deferred, self._deferred = self._deferred, []
+
+        def finish():
+            ev.synchronize()
+            vals = host.tolist()
+            for (_, cb), v in zip(deferred, vals[n:]):
+                cb(v)
+            return vals[:n]
+        return finish
+
     def _host_list(self, t):
         """t.tolist() -- with any deferred device counts read in the same transfer (one synchronisation)."""
         self.stats['syncs'] += 1
@@ -242,14 +305,19 @@ class ElaraStep:
         return vals[:n]
 
     # ---- plan (srm2/elara.py:209-414, cpp directory path) ----
-    def plan(self, s, u, u_nexts):
+    def plan(self, s, u, u_nexts, g_occ=None, dplan=None):
+        """The step's plan.  With g_occ and dplan, the batch's per-row gradients (the segment sum in class-rank
+        order) are queued right after the classification, before the host waits for the class counts, and kept
+        in p.G unless the overflow path reorders the rows."""
         d, K, C = self.d, self.K, self.C
         n = u.numel()
         # classes, class order, expired / preemptible / protected dynamic slots, counts (srm2/elara.py:214-267)
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
                                    self.st_mode == 'T', self.loc, self.R)
-        vals = self._host_list(pc.counts)
+        finish = self._host_list_async(pc.counts)
+        G = self.be.segsum(g_occ, dplan, n, pc.rank) if g_occ is not None else None
+        vals = finish()
         counts = vals[:10]
         n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]
         if mat_top > self.mat_cap - 1 or log_top > self.log_cap:
@@ -281,6 +349,7 @@ class ElaraStep:
             counts = self._host(*torch.bincount(cls.long(), minlength=10))
             order, rank = rank_order(cls)
             u_ord, c_ord, sl_ord, L_row = u[order], c[order].long(), sl[order].long(), None
+            G = None   # the rows' order changed: the segment sum is redone in the new order
             loc_ord = self.loc[u_ord].long()
         # class-rank bounds: positions b[r] .. b[r+1] of `order` hold the rows of rank r
         b = [0]
@@ -289,6 +358,7 @@ class ElaraStep:
         nNa, nNp, nNc, nLa, nLp, nLc, nFa, nFn = counts[1:9]
         p = Plan()
         p.s, p.u, p.n, p.b, p.order, p.rank = s, u, n, b, order, rank
+        p.G = G
         p.counts = counts
         p.u_ord = u_ord
         p.hit_slot = sl_ord[b[R_HIT]:b[R_HIT + 1]]
@@ -355,7 +425,11 @@ class ElaraStep:
 
     # ---- update (srm2/elara.py:491-542 and the host worker's writes 544-580, all in HBM) ----
     def update(self, p, G):
-        """G [n, D]: the batch's per-row gradients in class-rank order (p.order)."""
+        """G [n, D]: the batch's per-row gradients in class-rank order (p.order).  A backend with step_update
+        (the HIP one: elr_step_update) issues the whole update natively, in the order below."""
+        if getattr(self.be, 'step_update', None) is not None:
+            self.be.step_update(self, p, G)
+            return
         be, s, b = self.be, p.s, p.b
         W, w0 = p.work, b[R_NADM]
         rg = lambda r0, r1: G[b[r0]:b[r1 + 1]]  # noqa: E731
@@ -394,9 +468,10 @@ class ElaraStep:
         """Logical step s (1-based): ids int64 [O] (occurrences), g_occ [O, D] their gradients, u the batch's
         unique rows and dplan its dedup plan (from be.unique), u_nexts the unique rows of the next depth-1
         batches."""
-        p = self.plan(s, u, u_nexts)
+        p = self.plan(s, u, u_nexts, g_occ, dplan)
         self.assemble(p)
-        G = self.be.segsum(g_occ, dplan, u.numel(), p.rank)
+        G = p.G if p.G is not None else self.be.segsum(g_occ, dplan, u.numel(), p.rank)
+        p.G = None
         self.update(p, G)
         return p
 

@@ -319,6 +319,68 @@ typedef struct elr_assemble_args {
 
 int elr_assemble(const elr_assemble_args* args, void* stream);
 
+/* ---------------------------------------------------------------------------------------------------------
+ * The executor's update of one step.
+ * Replaces: srm2/elara.py:491-542 (ELARAExecutor.update: Adam on the hits and on the admitted, compacted and
+ * transient rows, the resident-history records, the pool scatter of admissions) and the arena writes of the host
+ * worker, srm2/elara.py:544-580 (evictions to MAT, history entries back to the log arena, compactions and
+ * transient rows to MAT, log appends, the S rows' Adam), all on the device and in one call.
+ *
+ * The batch's unique rows are in class-rank order (elr_plan_classify's `order`): rank r holds positions
+ * b[r] .. b[r+1] of grad [b[ELR_NRANK], D].  The work rows [b[ELR_RANK_S] - b[ELR_RANK_NADM], 3, D] (elr_assemble)
+ * hold the admitted, appended, compacted and transient rows in the same order.  The launches follow the
+ * reference's order of writes: the evicted slots and their glog rows are read before the admissions reuse them.
+ * Index arrays are int64; arenas may be device or mapped pinned host memory (elr_host_device_ptr).  Items whose
+ * index is out of range are skipped.  ELR_EINVAL for inconsistent bounds or a NULL array that a nonzero count
+ * needs.
+ * ------------------------------------------------------------------------------------------------------- */
+#define ELR_RANK_HIT 0
+#define ELR_RANK_NADM 1
+#define ELR_RANK_LADM 2
+#define ELR_RANK_FADM 3
+#define ELR_RANK_NAPP 4
+#define ELR_RANK_LAPP 5
+#define ELR_RANK_NCMP 6
+#define ELR_RANK_LCMP 7
+#define ELR_RANK_FN 8
+#define ELR_RANK_S 9
+#define ELR_NRANK 10
+
+typedef struct elr_update_args {
+  int64_t D, K;
+  float* pool;                /* [pool_rows, 3, D] resident states */
+  int64_t pool_rows;
+  float* mat;                 /* [mat_rows, 3, D] MAT arena */
+  int64_t mat_rows;
+  float* logs;                /* [log_rows, D] log arena */
+  int64_t log_rows;
+  float* glog;                /* [glog_slots, K, D] resident histories of the dynamic slots */
+  int64_t glog_slots;
+  const float* grad;          /* [b[ELR_NRANK], D] per-row gradients in class-rank order */
+  float* work;                /* assembled work rows (updated in place) */
+  int64_t b[ELR_NRANK + 1];   /* class-rank bounds */
+  int64_t step;               /* logical step of the Adam scalars (elr_adam_scalars) */
+  double lr, b1, b2, eps;
+  int32_t evl;                /* resident histories recorded (evl on) */
+  const int64_t* hit_slot;    /* [n_hit] pool slots of the hits */
+  const int64_t* hrec_dyn;    /* [n_hit] history record of the hits: glog slot and entry (elr_dir_a) */
+  const int64_t* hrec_j;
+  int64_t nev;                /* evicted slots */
+  const int64_t* ev_slot;     /* [nev] pool slots */
+  const int64_t* evf_slots;   /* [nev] MAT slots of rows going to M (others: out of range) */
+  const int64_t* evl_ids;     /* [nev, K] new log ids of the history entries of rows going back to L (-1: none) */
+  const int64_t* ev_dyn;      /* [nev] their glog slots */
+  const int64_t* adm_slots;   /* [n_adm] pool slots of the admitted N, L, F rows */
+  int64_t lazy_n;             /* admitted N and L rows: their gradient is entry 0 of glog slot adm_slots[i] - n0 */
+  int64_t n0;                 /* static pool slots */
+  const int64_t* c_slots;     /* [n_cmp] new MAT slots of the compacted rows (elr_dir_b) */
+  const int64_t* a_ids;       /* [n_app] log ids of the appended gradients (elr_dir_b) */
+  const int64_t* fn_slot;     /* [n_fn] MAT slots of the transient F rows */
+  const int64_t* s_slot;      /* [n_s] MAT slots of the S rows */
+} elr_update_args;
+
+int elr_step_update(const elr_update_args* args, void* stream);
+
 
 /* ---------------------------------------------------------------------------------------------------------
  * Row copies: dst[dst_idx[i]] = src[src_idx[i]], i < n, rows of W floats (NULL index = identity).

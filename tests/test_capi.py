@@ -128,6 +128,22 @@ def test_planner_executor_dedup_argument_checks():
     assert L.elr_glog_take(fake, 100, fake, fake, 10, 3, fake, 0, 8, None) == 0                    # n == 0
     assert L.elr_glog_take(fake, 100, fake, fake, 0, 3, fake, 4, 8, None) == -1                    # nd < 1
     assert L.elr_glog_take(fake, 100, None, fake, 10, 3, fake, 4, 8, None) == -1                   # no ids
+    u = _lib.UpdateArgs()
+    u.D, u.K, u.lr, u.b1, u.b2, u.eps, u.step = 128, 3, 1e-3, 0.9, 0.999, 1e-8, 1
+    assert L.elr_step_update(None, None) == -1
+    assert L.elr_step_update(ctypes.byref(u), None) == 0                                            # empty batch
+    for field, bad in (('D', 0), ('K', 0), ('nev', -1), ('lazy_n', 1)):                            # lazy_n > admitted
+        q = _lib.UpdateArgs.from_buffer_copy(u)
+        setattr(q, field, bad)
+        assert L.elr_step_update(ctypes.byref(q), None) == -1, field
+    q = _lib.UpdateArgs.from_buffer_copy(u)
+    q.b[1:] = [5] + [4] * 9                                                                        # bounds decrease
+    assert L.elr_step_update(ctypes.byref(q), None) == -1
+    q.b[1:] = [5] * 10                                                                             # 5 hits, no arrays
+    assert L.elr_step_update(ctypes.byref(q), None) == -1
+    q.grad, q.pool, q.hit_slot = fake.value, fake.value, fake.value
+    q.evl = 1                                                                                      # no history record
+    assert L.elr_step_update(ctypes.byref(q), None) == -1
 
 
 def test_ops_raise_without_gpu_tensors():

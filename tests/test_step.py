@@ -110,6 +110,33 @@ def test_gpu_step_matches_oracle_step(dev, name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('name', ['evl', 'no_evl_S', 'host_arenas'])
+def test_gpu_native_update_matches_python_update(dev, name):
+    """elr_step_update (the whole update in one native call, its five independent row writes in one launch)
+    against the same update issued call by call from Python over the same HIP kernels."""
+    from elara_amd.step import HipBackend, run
+
+    class CallByCall(HipBackend):
+        step_update = None
+
+    print(f'[gpu-test] native update {name}', flush=True)
+    kw = {'evl': {}, 'no_evl_S': {'evl': False, 'st': 'S'}, 'host_arenas': {'host': True}}[name]
+    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=30, **{'C': 2500, 'n_static': 1500, **kw})
+    a = make(cfg, dev)
+    b = make(cfg, dev, CallByCall(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2, dev))
+    gf = grads_fn(cfg, None)
+    run(a, cfg['batches'], gf)
+    run(b, cfg['batches'], gf)
+    torch.cuda.synchronize()
+    assert compare(a, b, cfg) > 0
+    assert a.stats == b.stats
+    s = a.stats
+    need = ('hits', 'adm', 'ev', 'appends', 'S') if name == 'no_evl_S' else ('hits', 'adm', 'ev', 'appends',
+                                                                            'compactions')
+    assert all(s[k] for k in need), s
+
+
+@pytest.mark.gpu
 def test_gpu_step_c5_full_shape(dev):
     """Config C5 shapes: 26 tables (vocab log-uniform in [1e3, 4e7], ~75M rows), batch 16,384 x 26 Zipf(1.1),
     D = 128, pool 337,626 (321,242 static hot rows), K = 3, evl on; 12 steps, HIP vs oracle bitwise."""
