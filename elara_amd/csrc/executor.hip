@@ -1,6 +1,11 @@
 // The executor's update of one step (srm2/elara.py:491-542 ELARAExecutor.update, plus the host worker's arena
 // writes 544-580), issued from native code: one C-ABI call per step instead of a dozen from Python.
 //
+// For D = 64, 128, 256, 512 the row moves ride on the Adam launches (k_adam_exec): the hits record their history
+// and update in place in one pass, and the admitted, compacted and transient rows go from the work array straight
+// to their pool or MAT slots.  The launch list below is the general path (other D), which the fused one follows in
+// its order of writes.
+//
 // The planner has sorted the batch's unique rows by class rank (hits; admitted N, L, F; appended N, L; compacted
 // N, L; transient F; S), so every group is a contiguous range of the per-row gradients G [n, D] and, from the
 // admitted N rows to the transient F rows, of the assembled work rows W [*, 3, D].  The launches, in the order
@@ -88,6 +93,64 @@ static int copy_multi(CopyJobs& jobs, hipStream_t st) {
   return launch_status();
 }
 
+// One Adam launch of the executor with the row moves fused in.  Row i < n reads gradient row g_base + i; with
+// i < n_rec it stores that gradient into entry rec_j[i] (0 when rec_j is NULL) of resident-history slot
+// (rec_dyn ? rec_dyn[i] : its destination row) - rec_off; it reads its state from work row src_base + i (src
+// NULL: in place, from its destination row), applies Adam, and writes the state to destination row dst_a[i]
+// (i < na) or dst_b[i - na].  So the hits record their history and update in place in one pass, and the
+// admitted, compacted and transient rows go from the work array straight to their pool or MAT slots.
+struct ExecAdam {
+  float* dst;
+  int64_t dst_rows;
+  const int64_t* dst_a;
+  int64_t na;
+  const int64_t* dst_b;
+  const float* src;
+  int64_t src_rows, src_base;
+  const float* grad;
+  int64_t g_base, n;
+  float* glog;
+  int64_t nd, K;
+  const int64_t* rec_dyn;
+  const int64_t* rec_j;
+  int64_t rec_off, n_rec;
+};
+
+template <int VPL>
+__global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
+  constexpr int64_t D = 64 * VPL;
+  const int lane = threadIdx.x & 63;
+  for (int64_t i = wave_id(); i < a.n; i += wave_count()) {
+    const int64_t d = i < a.na ? a.dst_a[i] : a.dst_b[i - a.na];
+    const RowFrag<VPL> g = frag_load<VPL, true>(a.grad + (a.g_base + i) * D + lane * VPL);
+    if (i < a.n_rec) {
+      const int64_t slot = (a.rec_dyn ? a.rec_dyn[i] : d) - a.rec_off, e = a.rec_j ? a.rec_j[i] : 0;
+      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K) frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g);
+    }
+    if (d < 0 || d >= a.dst_rows || (a.src && a.src_base + i >= a.src_rows)) continue;
+    const float* sp = (a.src ? a.src + (a.src_base + i) * 3 * D : a.dst + d * 3 * D) + lane * VPL;
+    RowFrag<VPL> w = frag_load<VPL, false>(sp), m = frag_load<VPL, false>(sp + D), v = frag_load<VPL, false>(sp + 2 * D);
+    frag_adam<VPL>(w, m, v, g, s);
+    float* o = a.dst + d * 3 * D + lane * VPL;
+    frag_store<VPL>(o, w);
+    frag_store<VPL>(o + D, m);
+    frag_store<VPL>(o + 2 * D, v);
+  }
+}
+
+static int adam_exec(int vpl, const ExecAdam& a, const AdamScalars& s, hipStream_t st) {
+  if (a.n <= 0) return ELR_OK;
+  int64_t blocks = (a.n + 3) / 4;
+  if (blocks > (int64_t(1) << 20)) blocks = int64_t(1) << 20;
+  switch (vpl) {
+    case 1: k_adam_exec<1><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    case 2: k_adam_exec<2><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    case 4: k_adam_exec<4><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    default: k_adam_exec<8><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+  }
+  return launch_status();
+}
+
 }  // namespace elr
 
 extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
@@ -120,6 +183,44 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   float* Wk = a->work;
   const int64_t w0 = b[ELR_RANK_NADM];
   int rc;
+  const int vpl = wpr_vpl(D);
+  if (vpl && aligned16(a->pool) && aligned16(a->mat) && aligned16(a->glog) && aligned16(Wk) && aligned16(G) &&
+      aligned16(a->logs)) {
+    // fused path: the row moves and the history records ride on the Adam launches
+    const AdamScalars s = make_scalars(sc);
+    const int64_t nd = a->glog_slots;
+    // 1. hits: history record and Adam in place
+    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
+                                      b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
+                                      rec ? n_hit : 0}, s, st)))
+      return rc;
+    // 2. evictions (before admissions reuse the slots)
+    if (a->nev) {
+      if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW,
+                              st)))
+        return rc;
+      if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
+        return rc;
+    }
+    // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
+    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
+                                      n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
+      return rc;
+    // 4. compacted rows into their new MAT slots, transient F rows back into theirs
+    if ((rc = adam_exec(vpl, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
+                                      b[ELR_RANK_NCMP] - w0, G, b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr,
+                                      nullptr, 0, 0}, s, st)))
+      return rc;
+    // 5. appended rows log their gradient
+    if (n_app && (rc = elr_copy_rows(a->logs, a->log_rows, a->a_ids, G + b[ELR_RANK_NAPP] * D, n_app, nullptr,
+                                     n_app, D, st)))
+      return rc;
+    // 6. S rows: Adam in place in the MAT arena
+    if (n_s && (rc = elr_adam_rows(a->mat, a->mat_rows, a->s_slot, 1, G + b[ELR_RANK_S] * D, n_s, D, sc, st)))
+      return rc;
+    return ELR_OK;
+  }
+  // general path (other D, unaligned arrays): the same writes as separate launches
   // 1. hits
   if (n_hit) {
     const float* gh = G + b[ELR_RANK_HIT] * D;
