@@ -40,7 +40,7 @@ SIGNATURES = {
     'elr_selfcheck_sqrt': (ctypes.c_int, [c_vp, c_vp, c_vp]),
     'elr_selfcheck_quot': (ctypes.c_int, [c_f32, c_vp, c_vp, c_vp, c_vp]),
     'elr_copy_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, c_vp]),
-    'elr_mark_rows': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_vp]),
+    'elr_mark_rows': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i32, c_vp, c_i64, c_vp, c_u32, c_vp]),
     'elr_glog_put': (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp]),
     'elr_glog_take': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_i64, c_i64, c_vp]),
     'elr_unique': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
@@ -81,7 +81,8 @@ class PlanIn(ctypes.Structure):
     _fields_ = [('u', c_vp), ('n', c_i64), ('next', c_vp * 4), ('n_next', c_i64 * 4), ('nnext', ctypes.c_int),
                 ('slot_of', c_vp), ('last_seen', c_vp), ('code', c_vp), ('kthr', c_vp), ('toff', c_vp), ('T', c_i64),
                 ('dyn', c_vp), ('nd', c_i64), ('slot_row', c_vp), ('mat_top', c_vp), ('log_top', c_vp),
-                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp), ('R', c_i64)]
+                ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp), ('R', c_i64),
+                ('next_bits', c_vp), ('next_mask', c_u32)]
 
 
 class PlanOut(ctypes.Structure):

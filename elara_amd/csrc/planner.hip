@@ -17,7 +17,8 @@
 //
 // A dynamic slot is protected in the reference when slot_of[un] == d for a row un of the next batches; every
 // occupied dynamic slot satisfies slot_of[slot_row[d]] == d, so the test here is the membership of slot_row[d] in
-// the (ascending, unique) next batches, by binary search.
+// the (ascending, unique) next batches: by binary search, or with one load from the ring of loaded batches
+// (next_bits) when the caller keeps one.
 #include "elr_scan.h"
 
 namespace elr {
@@ -46,6 +47,7 @@ __device__ __forceinline__ bool sorted_has(const int64_t* __restrict__ a, int64_
 }
 
 __device__ __forceinline__ bool in_next(const elr_plan_in& p, int64_t r) {
+  if (p.next_bits) return (p.next_bits[r] & p.next_mask) != 0;
   bool f = false;
   for (int k = 0; k < p.nnext; ++k) f = f || sorted_has(p.next[k], p.n_next[k], r);
   return f;
@@ -219,6 +221,9 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
         if (o.L_row) o.L_row[loff + within] = p.u[i];
         if (o.L_cnt) o.L_cnt[loff + within] = (int32_t)o.c[i];
       }
+      // this batch's bit in the ring: no later plan asks about step s (the rows of u are distinct, so no other
+      // thread writes this word; the dynamic-slot threads read only the bits of next_mask)
+      if (p.next_bits && row_ok(p, p.u[i]) && p.R > 0) p.next_bits[p.u[i]] &= ~(1u << (p.s & 31));
     }
   } else {
     const int64_t bb = b - nbu;
@@ -286,6 +291,7 @@ extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out,
   if (p.n > 0 && (!p.u || !p.slot_of || !p.last_seen || !p.code || !o.cls || !o.flags || !o.sl || !o.c || !o.order))
     return ELR_EINVAL;
   if (p.nd > 0 && (!p.dyn || !p.slot_row || !p.last_seen || !o.dyn_out)) return ELR_EINVAL;
+  if (p.next_bits && (p.R <= 0 || (p.next_mask & (1u << (p.s & 31))))) return ELR_EINVAL;
   if (!scratch || scratch_bytes < elr_plan_scratch_bytes(p.n, p.nd)) return ELR_ECAPACITY;
   hipStream_t st = (hipStream_t)stream;
   const int64_t nbu = plan_blocks(p.n), nbd = plan_blocks(p.nd);

@@ -26,7 +26,7 @@ def _dev_i64(t, dev):
 
 
 def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
-                  loc=None, R=0):
+                  loc=None, R=0, next_bits=None, next_mask=0):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -36,7 +36,11 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     on the device, and in class-rank order u_ord, c_ord, sl_ord int64 [n] (u, c, sl at `order`); L_row int64 [n] and
     L_cnt int32 [n]: the L rows and their codes as admitted, append, compact, valid up to their count; loc_ord int64
     [n]: loc (int32 [R + 1], when given) of the rows in class-rank order, else None).  With R > 0 a row of u outside
-    [0, R) is classified S with no slot and no MAT slot (skipped by every later copy and update)."""
+    [0, R) is classified S with no slot and no MAT slot (skipped by every later copy and update).
+
+    next_bits (int32 [R], with R > 0) and next_mask: the caller's ring of loaded batches (bit t % 32 of
+    next_bits[r] set while the batch of step t holds row r; see rows.mark_rows).  Membership in the next batches is
+    then one load per row instead of searches of u_nexts, and bit s % 32 of u's rows is cleared."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -75,6 +79,11 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     pin.s, pin.K, pin.want_t = int(s), int(K), int(bool(want_t))
     pin.loc = loc.data_ptr() if loc is not None else None
     pin.R = int(R)
+    if next_bits is not None:
+        if not (next_bits.dtype == I32 and next_bits.device == dev and next_bits.is_contiguous()
+                and next_bits.numel() >= R > 0):
+            raise RuntimeError(f'plan_classify: next_bits must be a contiguous {I32} tensor of R rows on {dev}')
+        pin.next_bits, pin.next_mask = next_bits.data_ptr(), int(next_mask) & 0xFFFFFFFF
     pout = _lib.PlanOut(*[t.data_ptr() if t is not None else None for t in out])
     nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
     scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)

@@ -121,14 +121,19 @@ def glog_take(logs, ids, glog, dyn):
     return logs
 
 
-def mark_rows(rows, n_dev, value, out):
+def mark_rows(rows, n_dev, value, out, bits=None, bit=0):
     """out[rows[i]] = value for i < n_dev (a device int64 count; rows beyond it are ignored), with no
-    synchronisation: rows int64 [n_max] cuda, out int32 [R] cuda."""
+    synchronisation: rows int64 [n_max] cuda (distinct), out int32 [R] cuda.  With bits (int32 [R] cuda, the
+    planner's ring of loaded batches), also bits[rows[i]] |= bit."""
     if not (rows.is_cuda and rows.dtype == torch.int64 and out.is_cuda and out.dtype == torch.int32
             and n_dev.is_cuda and n_dev.dtype == torch.int64 and out.is_contiguous()):
         raise RuntimeError('mark_rows: rows int64, n_dev int64 and out int32 cuda tensors')
+    if bits is not None and not (bits.is_cuda and bits.dtype == torch.int32 and bits.is_contiguous()
+                                 and bits.numel() >= out.numel()):
+        raise RuntimeError('mark_rows: bits must be a contiguous cuda int32 tensor covering out')
     rows = rows.contiguous()
     with _lib.on_device(out.device):
         rc = _lib.lib().elr_mark_rows(_lib.ptr(rows), _lib.ptr(n_dev), rows.numel(), int(value), _lib.ptr(out),
-                                      out.numel(), ctypes.c_void_p(_lib.raw_stream(out.device)))
+                                      out.numel(), _lib.ptr(bits), int(bit) & 0xFFFFFFFF,
+                                      ctypes.c_void_p(_lib.raw_stream(out.device)))
     _lib.check(rc, 'elr_mark_rows')

@@ -74,11 +74,13 @@ class HipBackend:
     def unique_async(self, ids, bound=None):
         return unique_plan_async(ids, self.D, bound)
 
-    def mark_rows(self, rows, n_dev, value, out):
-        mark_rows(rows, n_dev, value, out)
+    batch_ring = True   # keeps the planner's ring of loaded batches (ElaraStep.next_bits)
 
-    def plan_classify(self, *args):
-        return plan_classify(*args)
+    def mark_rows(self, rows, n_dev, value, out, bits=None, bit=0):
+        mark_rows(rows, n_dev, value, out, bits, bit)
+
+    def plan_classify(self, *args, **kw):
+        return plan_classify(*args, **kw)
 
     def plan_admit(self, *args):
         plan_admit(*args)
@@ -193,6 +195,11 @@ class ElaraStep:
         self.slot_row = torch.full((C,), -1, dtype=I64, device=d)
         self.pinned = torch.zeros(C, dtype=torch.bool, device=d)
         self.last_seen = torch.full((R,), -1, dtype=I32, device=d)
+        # ring of loaded batches for the planner's "appears in the next batches" test (bit t % 32 of next_bits[r]
+        # set while the batch of logical step t holds row r): one load per row instead of searches of the next
+        # batches' unique rows.  The L + 1 batches loaded ahead and the current one must fit in 32 bits.
+        self.next_bits = (torch.zeros(R, dtype=I32, device=d)
+                          if getattr(self.be, 'batch_ring', False) and d.type == 'cuda' and L + 2 <= 32 else None)
         n0 = 0
         self.static_rows = None
         if static_rows is not None and len(static_rows):
@@ -247,8 +254,13 @@ class ElaraStep:
     def observe(self, step, u, n_dev=None):
         """Record that rows u appear at logical step `step` (the TTL lookahead, srm2/elara.py:160-161); with n_dev
         (a device count) only the first n_dev rows of u, without a synchronisation."""
+        bit = 1 << (step % 32)
         if n_dev is None:
             self.last_seen[u] = step
+            if self.next_bits is not None:
+                self.next_bits[u] = self.next_bits[u] | (bit - (1 << 32) if bit >= 1 << 31 else bit)
+        elif self.next_bits is not None:
+            self.be.mark_rows(u, n_dev, step, self.last_seen, self.next_bits, bit)
         else:
             self.be.mark_rows(u, n_dev, step, self.last_seen)
 
@@ -312,9 +324,13 @@ class ElaraStep:
         d, K, C = self.d, self.K, self.C
         n = u.numel()
         # classes, class order, expired / preemptible / protected dynamic slots, counts (srm2/elara.py:214-267)
+        ring = {}
+        if self.next_bits is not None:
+            ring = dict(next_bits=self.next_bits,
+                        next_mask=sum(1 << ((s + k) % 32) for k in range(1, self.depth)))
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
-                                   self.st_mode == 'T', self.loc, self.R)
+                                   self.st_mode == 'T', self.loc, self.R, **ring)
         finish = self._host_list_async(pc.counts)
         G = self.be.segsum(g_occ, dplan, n, pc.rank) if g_occ is not None else None
         vals = finish()

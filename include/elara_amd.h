@@ -239,6 +239,12 @@ typedef struct elr_plan_in {
   const int32_t* loc;         /* [R + 1] MAT slot of each row (only read when out->loc_ord is set) */
   int64_t R;                  /* rows: a row of u outside [0, R) is classified S with slot -1, code K+1 and MAT
                                  slot -1, which every later copy and update skips (0: no check) */
+  uint32_t* next_bits;        /* [R] optional ring of loaded batches: bit t % 32 of next_bits[r] is set while the
+                                 batch of logical step t holds row r (elr_mark_rows with bits).  When given, "appears in
+                                 one of the next batches" is next_bits[r] & next_mask != 0 (one load in place of the
+                                 searches of next[]), and the scatter pass clears bit s % 32 of the batch's rows: no
+                                 later plan asks about step s */
+  uint32_t next_mask;         /* the bits of the next batches' steps (s+1, s+2, ...), none equal to bit s % 32 */
 } elr_plan_in;
 
 typedef struct elr_plan_out {
@@ -406,10 +412,11 @@ int elr_glog_take(float* logs, int64_t nlogs, const int64_t* ids, const float* g
 
 /* out[rows[i]] = value for i < min(*n_dev, n_max), with the count read on the device (no counterpart in the
  * reference, which reads the batch's unique count on the host first): the TTL lookahead's record of when rows
- * appear next (srm2/elara.py:160-161) for a batch whose unique count the host reads later.  Rows out of range are
- * skipped. */
+ * appear next (srm2/elara.py:160-161) for a batch whose unique count the host reads later.  With bits (may be
+ * NULL), also bits[rows[i]] |= bit: the planner's ring of loaded batches (elr_plan_in.next_bits).  rows must be
+ * distinct.  Rows out of range are skipped. */
 int elr_mark_rows(const int64_t* rows, const int64_t* n_dev, int64_t n_max, int32_t value, int32_t* out,
-                  int64_t out_rows, void* stream);
+                  int64_t out_rows, uint32_t* bits, uint32_t bit, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Exhaustive check of the step-constant division (no counterpart in the reference).  The Adam kernels compute

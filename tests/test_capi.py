@@ -88,6 +88,11 @@ def test_planner_executor_dedup_argument_checks():
     q = _lib.PlanIn.from_buffer_copy(pin)
     q.n = 5                                                        # rows but no row pointers
     assert L.elr_plan_classify(ctypes.byref(q), ctypes.byref(pout), fake, 1 << 20, None) == -1
+    q = _lib.PlanIn.from_buffer_copy(pin)
+    q.next_bits, q.R = fake.value, 0                               # a batch ring needs R
+    assert L.elr_plan_classify(ctypes.byref(q), ctypes.byref(pout), fake, 1 << 20, None) == -1
+    q.R, q.s, q.next_mask = 100, 33, 0b10                          # the mask holds the step's own bit (33 % 32)
+    assert L.elr_plan_classify(ctypes.byref(q), ctypes.byref(pout), fake, 1 << 20, None) == -1
     assert L.elr_plan_scratch_bytes(-1, 0) == -1 and L.elr_plan_scratch_bytes(1000, 10) > 0
     adm = [None] * 8
     assert L.elr_plan_admit(None, None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == 0              # nothing to do
@@ -117,9 +122,9 @@ def test_planner_executor_dedup_argument_checks():
     assert L.elr_segment_sum_plan(fake, 10, 600, 20, fake, 1 << 30, None, fake, 10, None) == -2     # D > 512
     assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1, None, fake, 10, None) == -3             # plan too small
     assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1 << 20, None, fake, -1, None) == -1
-    assert L.elr_mark_rows(None, None, -1, 0, None, 0, None) == -1
-    assert L.elr_mark_rows(None, None, 0, 0, None, 0, None) == 0
-    assert L.elr_mark_rows(None, fake, 5, 0, fake, 10, None) == -1
+    assert L.elr_mark_rows(None, None, -1, 0, None, 0, None, 0, None) == -1
+    assert L.elr_mark_rows(None, None, 0, 0, None, 0, None, 0, None) == 0
+    assert L.elr_mark_rows(None, fake, 5, 0, fake, 10, None, 0, None) == -1
     d = ctypes.c_void_p()
     assert L.elr_host_device_ptr(None, ctypes.byref(d)) == -1
     assert L.elr_glog_put(fake, 10, 3, fake, 0, None, fake, 0, 8, None) == 0                       # n == 0
