@@ -6,6 +6,11 @@ Counterpart of the reference's torch.profiler summary (srm2/profsum.py:10-25), f
     python -m elara_amd.profsum stats --last N <run>_results.db    the same over each kernel's last N dispatches
                                                                    (the timed steps of a run whose untimed
                                                                    warm-up came first), with min and median
+    python -m elara_amd.profsum steps --marker SUBSTR --last N <run>_results.db
+                                                                   per-step kernel time of the last N steps: the
+                                                                   window starts at the N-th last dispatch of the
+                                                                   marker kernel (one launch per step); for each
+                                                                   kernel, launches and microseconds per step
     python -m elara_amd.profsum pmc    <run>_results.db            per-kernel mean of each PMC counter per dispatch
     python -m elara_amd.profsum traffic --kernel SUBSTR \
         --fetch F.db --write W.db --copy-fetch CF.db --copy-write CW.db --copy-bytes N
@@ -51,6 +56,24 @@ def kernel_stats_last(db, last):
     return sorted(out, key=lambda r: -r[2])
 
 
+def step_window(db, marker, last):
+    """(total_us_per_step, launches_per_step, [(name, launches_per_step, us_per_step)]) over the last `last` steps,
+    a step starting at each dispatch of the kernel whose name contains `marker`."""
+    rows = _rows(db, 'select name, start, end from kernels order by start')
+    starts = [st for n, st, _ in rows if marker in n]
+    if len(starts) < last:
+        raise SystemExit(f'{marker!r}: {len(starts)} dispatches, fewer than {last}')
+    t0 = starts[-last]
+    agg = {}
+    for n, st, en in rows:
+        if st >= t0:
+            a = agg.setdefault(n, [0, 0.0])
+            a[0] += 1
+            a[1] += (en - st) / 1e3
+    per = sorted(((n, c / last, t / last) for n, (c, t) in agg.items()), key=lambda r: -r[2])
+    return sum(r[2] for r in per), sum(r[1] for r in per), per
+
+
 def pmc_means(db):
     """{(kernel name, counter): (dispatches, mean value per dispatch)}."""
     out = {}
@@ -80,6 +103,14 @@ def cmd_stats(a):
     print(f'| kernel | calls | total us | mean us | % |\n|---|---:|---:|---:|---:|')
     for n, c, t, m, p in kernel_stats(a.db):
         print(f'| `{short(n)}` | {c} | {t:.1f} | {m:.2f} | {p:.1f} |')
+
+
+def cmd_steps(a):
+    tot, launches, per = step_window(a.db, a.marker, a.last)
+    print(f'{a.last} steps: {tot:.1f} us of kernel time and {launches:.1f} launches per step\n')
+    print('| kernel | launches per step | us per step | % |\n|---|---:|---:|---:|')
+    for n, c, t in per:
+        print(f'| `{short(n)}` | {c:.2f} | {t:.2f} | {100 * t / tot:.1f} |')
 
 
 def cmd_pmc(a):
@@ -113,6 +144,8 @@ def main(argv=None):
     sub = ap.add_subparsers(dest='cmd', required=True)
     s = sub.add_parser('stats'); s.add_argument('db'); s.add_argument('--last', type=int, default=0)
     s.set_defaults(fn=cmd_stats)
+    w = sub.add_parser('steps'); w.add_argument('db'); w.add_argument('--marker', required=True)
+    w.add_argument('--last', type=int, required=True); w.set_defaults(fn=cmd_steps)
     p = sub.add_parser('pmc'); p.add_argument('db'); p.set_defaults(fn=cmd_pmc)
     t = sub.add_parser('traffic')
     t.add_argument('--kernel', required=True)
