@@ -1,97 +1,25 @@
 // The executor's update of one step (srm2/elara.py:491-542 ELARAExecutor.update, plus the host worker's arena
 // writes 544-580), issued from native code: one C-ABI call per step instead of a dozen from Python.
 //
-// For D = 64, 128, 256, 512 the row moves ride on the Adam launches (k_adam_exec): the hits record their history
-// and update in place in one pass, and the admitted, compacted and transient rows go from the work array straight
-// to their pool or MAT slots.  The launch list below is the general path (other D), which the fused one follows in
-// its order of writes.
-//
 // The planner has sorted the batch's unique rows by class rank (hits; admitted N, L, F; appended N, L; compacted
 // N, L; transient F; S), so every group is a contiguous range of the per-row gradients G [n, D] and, from the
 // admitted N rows to the transient F rows, of the assembled work rows W [*, 3, D].  The launches, in the order
 // the reference's update performs its writes:
-//   1. hits: resident-history record glog[hrec_dyn, hrec_j] = g (evl), then Adam on their pool slots;
+//   1. hits: their gradient into their resident history (evl) and Adam in place on their pool slots, one pass;
 //   2. evictions: full states of rows going to M into their MAT slots, and the resident histories of rows going
-//      back to L into their new log ids -- both read the evicted pool slots and glog rows before step 4 reuses
+//      back to L into their new log ids -- both read the evicted pool slots and glog rows before step 3 reuses
 //      them for admissions;
-//   3. Adam on the work rows of the admitted (N, L, F) and of the compacted and transient (N, L, F) groups;
-//   4. (one launch) the admitted rows' states into their pool slots, their admission gradient into entry 0 of
-//      their resident history (evl), the compacted rows' states into their new MAT slots, the appended rows'
-//      gradients into their new log ids, the transient F rows' states back into their MAT slots.  These five
-//      writes touch disjoint rows and read only W and G, so one launch does them in any order;
-//   5. Adam on the S rows' MAT slots.
+//   3. admitted rows: Adam from the work array straight into their pool slots, with the admission record of the N
+//      and L rows (entry 0 of their resident history);
+//   4. compacted rows: Adam from the work array into their new MAT slots; transient F rows back into theirs;
+//   5. appended rows: their gradient into their new log ids;
+//   6. S rows: Adam in place in the MAT arena.
+// Steps 1, 3 and 4 are k_adam_exec launches: the row moves and history records ride on the Adam passes, and the
+// work array is never written back (no later kernel reads it).  D = 64, 128, 256 or 512 (the fused assembly's
+// limits too).
 #include "elr_rowio.h"
 
 namespace elr {
-
-// One job of a multi-copy launch: item i copies src row src_base + i to dst row dst_idx[i] (i when dst_idx is
-// NULL), rows of W floats.  With pair_K > 0 the destination is entry 0 of slot (v - pair_off) of a
-// [pair_nd, pair_K] grid of rows (the admission record of glog); items out of range are skipped.
-struct CopyJob {
-  float* dst;
-  int64_t dst_rows;
-  const int64_t* dst_idx;
-  const float* src;
-  int64_t src_rows;
-  int64_t src_base;
-  int64_t n;
-  int64_t W;
-  int64_t pair_K, pair_off, pair_nd;
-  int v4;   // 16-byte accesses (W % 4 == 0 and both bases 16-byte aligned; set by copy_multi)
-};
-
-constexpr int kMaxJobs = 5;
-
-struct CopyJobs {
-  CopyJob j[kMaxJobs];
-  int64_t end[kMaxJobs];   // cumulative item counts
-  int njobs;
-};
-
-// Grid-stride over the concatenated items of all jobs, one wave per item (wave-uniform job choice).
-__global__ __launch_bounds__(256) void k_copy_multi(CopyJobs jobs) {
-  const int lane = threadIdx.x & 63;
-  const int64_t total = jobs.end[jobs.njobs - 1];
-  for (int64_t t = wave_id(); t < total; t += wave_count()) {
-    int q = 0;
-    while (q + 1 < jobs.njobs && t >= jobs.end[q]) ++q;
-    const CopyJob& J = jobs.j[q];
-    const int64_t i = t - (q ? jobs.end[q - 1] : 0);
-    int64_t d = J.dst_idx ? J.dst_idx[i] : i;
-    if (J.pair_K > 0) {
-      const int64_t slot = d - J.pair_off;
-      d = slot >= 0 && slot < J.pair_nd ? slot * J.pair_K : -1;
-    }
-    const int64_t s = J.src_base + i;
-    if (d < 0 || d >= J.dst_rows || s < 0 || s >= J.src_rows) continue;
-    const float* sp = J.src + s * J.W;
-    float* dp = J.dst + d * J.W;
-    if (J.v4) {
-      for (int64_t c = lane; c < J.W / 4; c += 64)
-        reinterpret_cast<f32x4*>(dp)[c] = reinterpret_cast<const f32x4*>(sp)[c];
-    } else {
-      for (int64_t c = lane; c < J.W; c += 64) dp[c] = sp[c];
-    }
-  }
-}
-
-static int copy_multi(CopyJobs& jobs, hipStream_t st) {
-  int k = 0;
-  int64_t tot = 0;
-  for (int q = 0; q < jobs.njobs; ++q) {
-    if (jobs.j[q].n <= 0) continue;
-    jobs.j[k] = jobs.j[q];
-    jobs.j[k].v4 = (jobs.j[q].W & 3) == 0 && aligned16(jobs.j[q].dst) && aligned16(jobs.j[q].src);
-    tot += jobs.j[q].n;
-    jobs.end[k++] = tot;
-  }
-  jobs.njobs = k;
-  if (!k) return ELR_OK;
-  int64_t blocks = (tot + 3) / 4;
-  if (blocks > 256 * 32) blocks = 256 * 32;
-  k_copy_multi<<<(unsigned)blocks, 256, 0, st>>>(jobs);
-  return launch_status();
-}
 
 // One Adam launch of the executor with the row moves fused in.  Row i < n reads gradient row g_base + i; with
 // i < n_rec it stores that gradient into entry rec_j[i] (0 when rec_j is NULL) of resident-history slot
@@ -184,72 +112,39 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   const int64_t w0 = b[ELR_RANK_NADM];
   int rc;
   const int vpl = wpr_vpl(D);
-  if (vpl && aligned16(a->pool) && aligned16(a->mat) && aligned16(a->glog) && aligned16(Wk) && aligned16(G) &&
-      aligned16(a->logs)) {
-    // fused path: the row moves and the history records ride on the Adam launches
-    const AdamScalars s = make_scalars(sc);
-    const int64_t nd = a->glog_slots;
-    // 1. hits: history record and Adam in place
-    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
-                                      b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
-                                      rec ? n_hit : 0}, s, st)))
-      return rc;
-    // 2. evictions (before admissions reuse the slots)
-    if (a->nev) {
-      if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW,
-                              st)))
-        return rc;
-      if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
-        return rc;
-    }
-    // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
-    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
-                                      n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
-      return rc;
-    // 4. compacted rows into their new MAT slots, transient F rows back into theirs
-    if ((rc = adam_exec(vpl, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
-                                      b[ELR_RANK_NCMP] - w0, G, b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr,
-                                      nullptr, 0, 0}, s, st)))
-      return rc;
-    // 5. appended rows log their gradient
-    if (n_app && (rc = elr_copy_rows(a->logs, a->log_rows, a->a_ids, G + b[ELR_RANK_NAPP] * D, n_app, nullptr,
-                                     n_app, D, st)))
-      return rc;
-    // 6. S rows: Adam in place in the MAT arena
-    if (n_s && (rc = elr_adam_rows(a->mat, a->mat_rows, a->s_slot, 1, G + b[ELR_RANK_S] * D, n_s, D, sc, st)))
-      return rc;
-    return ELR_OK;
-  }
-  // general path (other D, unaligned arrays): the same writes as separate launches
-  // 1. hits
-  if (n_hit) {
-    const float* gh = G + b[ELR_RANK_HIT] * D;
-    if (rec && (rc = elr_glog_put(a->glog, a->glog_slots, K, a->hrec_dyn, 0, a->hrec_j, gh, n_hit, D, st))) return rc;
-    if ((rc = elr_adam_rows(a->pool, a->pool_rows, a->hit_slot, 1, gh, n_hit, D, sc, st))) return rc;
-  }
+  if (!vpl) return ELR_EUNSUPPORTED;
+  if (!aligned16(a->pool) || !aligned16(a->mat) || !aligned16(a->glog) || !aligned16(Wk) || !aligned16(G) ||
+      !aligned16(a->logs))
+    return ELR_EINVAL;
+  const AdamScalars s = make_scalars(sc);
+  const int64_t nd = a->glog_slots;
+  // 1. hits: history record and Adam in place
+  if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
+                                    b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
+                                    rec ? n_hit : 0}, s, st)))
+    return rc;
   // 2. evictions (before admissions reuse the slots)
   if (a->nev) {
-    if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW, st)))
+    if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW,
+                            st)))
       return rc;
-    if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, a->glog_slots, K, a->ev_dyn, a->nev, D, st)))
+    if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
       return rc;
   }
-  // 3. Adam on the admitted rows and on the compacted and transient rows (appended rows only log their gradient)
-  if (n_adm && (rc = elr_adam_rows(Wk, n_adm, nullptr, 1, G + w0 * D, n_adm, D, sc, st))) return rc;
-  if (n_tail && (rc = elr_adam_rows(Wk + (b[ELR_RANK_NCMP] - w0) * RW, n_tail, nullptr, 1,
-                                    G + b[ELR_RANK_NCMP] * D, n_tail, D, sc, st)))
+  // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
+  if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
+                                    n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
     return rc;
-  // 4. the five independent row writes, one launch
-  CopyJobs jobs{};
-  jobs.njobs = kMaxJobs;
-  jobs.j[0] = CopyJob{a->pool, a->pool_rows, a->adm_slots, Wk, n_work, 0, n_adm, RW, 0, 0, 0, 0};
-  jobs.j[1] = CopyJob{a->glog, a->glog_slots * K, a->adm_slots, G, b[ELR_NRANK], w0, rec ? a->lazy_n : 0, D, K, a->n0,
-                      a->glog_slots, 0};
-  jobs.j[2] = CopyJob{a->mat, a->mat_rows, a->c_slots, Wk, n_work, b[ELR_RANK_NCMP] - w0, n_cmp, RW, 0, 0, 0, 0};
-  jobs.j[3] = CopyJob{a->logs, a->log_rows, a->a_ids, G, b[ELR_NRANK], b[ELR_RANK_NAPP], n_app, D, 0, 0, 0, 0};
-  jobs.j[4] = CopyJob{a->mat, a->mat_rows, a->fn_slot, Wk, n_work, b[ELR_RANK_FN] - w0, n_fn, RW, 0, 0, 0, 0};
-  if ((rc = copy_multi(jobs, st))) return rc;
-  // 5. S rows: Adam in place in the MAT arena
+  // 4. compacted rows into their new MAT slots, transient F rows back into theirs
+  if ((rc = adam_exec(vpl, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
+                                    b[ELR_RANK_NCMP] - w0, G, b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr,
+                                    nullptr, 0, 0}, s, st)))
+    return rc;
+  // 5. appended rows log their gradient
+  if (n_app && (rc = elr_copy_rows(a->logs, a->log_rows, a->a_ids, G + b[ELR_RANK_NAPP] * D, n_app, nullptr,
+                                   n_app, D, st)))
+    return rc;
+  // 6. S rows: Adam in place in the MAT arena
   if (n_s && (rc = elr_adam_rows(a->mat, a->mat_rows, a->s_slot, 1, G + b[ELR_RANK_S] * D, n_s, D, sc, st)))
     return rc;
   return ELR_OK;

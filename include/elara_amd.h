@@ -336,9 +336,12 @@ int elr_assemble(const elr_assemble_args* args, void* stream);
  * b[r] .. b[r+1] of grad [b[ELR_NRANK], D].  The work rows [b[ELR_RANK_S] - b[ELR_RANK_NADM], 3, D] (elr_assemble)
  * hold the admitted, appended, compacted and transient rows in the same order.  The launches follow the
  * reference's order of writes: the evicted slots and their glog rows are read before the admissions reuse them.
+ * The row moves and history records ride on the Adam launches: the hits record and update in place, and the
+ * admitted, compacted and transient rows go from the work array straight into their pool / MAT slots (the work
+ * array is not written back).  D = 64, 128, 256 or 512 (else ELR_EUNSUPPORTED), every array 16-byte aligned.
  * Index arrays are int64; arenas may be device or mapped pinned host memory (elr_host_device_ptr).  Items whose
- * index is out of range are skipped.  ELR_EINVAL for inconsistent bounds or a NULL array that a nonzero count
- * needs.
+ * index is out of range are skipped.  ELR_EINVAL for inconsistent bounds, a misaligned array or a NULL array that
+ * a nonzero count needs.
  * ------------------------------------------------------------------------------------------------------- */
 #define ELR_RANK_HIT 0
 #define ELR_RANK_NADM 1

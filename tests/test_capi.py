@@ -137,6 +137,9 @@ def test_planner_executor_dedup_argument_checks():
     u.D, u.K, u.lr, u.b1, u.b2, u.eps, u.step = 128, 3, 1e-3, 0.9, 0.999, 1e-8, 1
     assert L.elr_step_update(None, None) == -1
     assert L.elr_step_update(ctypes.byref(u), None) == 0                                            # empty batch
+    q = _lib.UpdateArgs.from_buffer_copy(u)
+    q.D = 96                                                                                       # D not 64..512
+    assert L.elr_step_update(ctypes.byref(q), None) == -2
     for field, bad in (('D', 0), ('K', 0), ('nev', -1), ('lazy_n', 1)):                            # lazy_n > admitted
         q = _lib.UpdateArgs.from_buffer_copy(u)
         setattr(q, field, bad)
