@@ -88,18 +88,20 @@ def test_step_runs_on_cpu_with_oracle_backend():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow', 'host_arenas',
-                                  'host_arenas_S', 'D64_K2', 'D256_K4', 'K1_kthr0'])
+                                  'host_arenas_S', 'D64_K2', 'D256_K4', 'K1_kthr0', 'L40_no_ring'])
 def test_gpu_step_matches_oracle_step(dev, name):
     """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
-    kernels over the host link."""
+    kernels over the host link.  L40_no_ring: a look-ahead too long for the 32-bit ring of loaded batches, so the
+    planner searches the next batches' sorted rows instead."""
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
     kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
           'host_arenas': {'host': True}, 'host_arenas_S': {'host': True, 'st': 'S'},
           'D64_K2': {'D': 64, 'K': 2, 'kthr': 2}, 'D256_K4': {'D': 256, 'K': 4, 'kthr': 3},
-          'K1_kthr0': {'K': 1, 'kthr': 0}}[name]
+          'K1_kthr0': {'K': 1, 'kthr': 0}, 'L40_no_ring': {'L': 40}}[name]
     cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
     g = make(cfg, dev)
+    assert (g.next_bits is None) == (name == 'L40_no_ring')
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
     gf = grads_fn(cfg, None)
     run(g, cfg['batches'], gf)
@@ -157,7 +159,9 @@ def test_gpu_step_c5_full_shape(dev):
 @pytest.mark.parametrize('name', ['small_evl', 'small_S'])
 def test_gpu_plan_classify_matches_oracle(dev, name):
     """elr_plan_classify against the oracle's torch restatement of the planner classification, on every plan of
-    a run (states as the step produces them, including steps that preempt and overflow): every output bitwise."""
+    a run (states as the step produces them, including steps that preempt and overflow): every output bitwise,
+    with the next batches given as sorted lists and again as a ring of loaded batches (which the plan updates by
+    clearing its own step's bit)."""
     from elara_amd.planner import plan_classify
     from elara_amd.step import run
     print(f'[gpu-test] plan classify {name}', flush=True)
@@ -171,13 +175,33 @@ def test_gpu_plan_classify_matches_oracle(dev, name):
         want = orig(*args)
         g = [a.to(dev) if isinstance(a, torch.Tensor) else a for a in args]
         g[1] = [x.to(dev) for x in args[1]]
-        got = plan_classify(*g)
-        for f in want._fields:
-            x, y = getattr(want, f), getattr(got, f).cpu()
-            if f in ('L_row', 'L_cnt'):   # valid up to the L-row count
-                assert int(want.counts[4] + want.counts[5] + want.counts[6]) == x.numel() <= y.numel(), f
-                y = y[:x.numel()]
-            assert x.dtype == y.dtype and torch.equal(x, y), (len(calls), f)
+        s, R = int(args[11]), int(args[15])
+        # the same plan with a ring of loaded batches in place of the sorted next batches: bit (s + k) % 32 set on
+        # the rows of next batch k, the batch's own bit on its rows, and unrelated bits as noise
+        bits = torch.zeros(R, dtype=torch.int32, device=dev)
+        mask = 0
+        for k, x in enumerate(g[1], start=1):
+            b = (s + k) % 32
+            bits[x] |= (1 << b) - (1 << 32 if b == 31 else 0)
+            mask |= 1 << b
+        noise = (1 << ((s + 7) % 32)) | (1 << ((s + 20) % 32))
+        noise_rows = torch.arange(0, R, 3, device=dev)
+        bits[noise_rows] |= noise - (1 << 32 if noise >= 1 << 31 else 0)
+        own = 1 << (s % 32)
+        bits[g[0]] |= own - (1 << 32 if own >= 1 << 31 else 0)
+        before = bits.clone()
+        for ring in (None, (bits, mask)):
+            got = plan_classify(*g) if ring is None else plan_classify(*g, next_bits=ring[0], next_mask=ring[1])
+            for f in want._fields:
+                x, y = getattr(want, f), getattr(got, f).cpu()
+                if f in ('L_row', 'L_cnt'):   # valid up to the L-row count
+                    assert int(want.counts[4] + want.counts[5] + want.counts[6]) == x.numel() <= y.numel(), f
+                    y = y[:x.numel()]
+                assert x.dtype == y.dtype and torch.equal(x, y), (len(calls), f, ring is not None)
+        # the plan cleared its own step's bit on the batch's rows and nothing else
+        expect = before.clone()
+        expect[g[0]] &= ~own if own < 1 << 31 else ~(own - (1 << 32))
+        assert torch.equal(bits, expect), len(calls)
         calls.append(int(want.counts[10]))
         return want
     be.plan_classify = both
