@@ -111,7 +111,8 @@ class UpdateArgs(ctypes.Structure):
                 ('b2', ctypes.c_double), ('eps', ctypes.c_double), ('evl', ctypes.c_int32), ('hit_slot', c_vp),
                 ('hrec_dyn', c_vp), ('hrec_j', c_vp), ('nev', c_i64), ('ev_slot', c_vp), ('evf_slots', c_vp),
                 ('evl_ids', c_vp), ('ev_dyn', c_vp), ('adm_slots', c_vp), ('lazy_n', c_i64), ('n0', c_i64),
-                ('c_slots', c_vp), ('a_ids', c_vp), ('fn_slot', c_vp), ('s_slot', c_vp)]
+                ('c_slots', c_vp), ('a_ids', c_vp), ('fn_slot', c_vp), ('s_slot', c_vp), ('part', ctypes.c_int32),
+                ('link_blocks', c_i64)]
 
 
 def lib():

@@ -152,6 +152,10 @@ __device__ __forceinline__ int64_t wave_id() {
 }
 __device__ __forceinline__ int64_t wave_count() { return (int64_t)gridDim.x * (blockDim.x >> 6); }
 
+// dst[dst_idx[i]] = src[i] with at most max_blocks blocks (rows.hip; used by the executor's link part).
+int copy_rows_capped(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
+                     int64_t n, int64_t W, int64_t max_blocks, void* stream);
+
 // VPL for D if the wave-per-row kernels handle it (D = 64, 128, 256, 512), else 0.
 inline int wpr_vpl(int64_t D) {
   switch (D) {

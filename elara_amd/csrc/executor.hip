@@ -15,8 +15,9 @@
 //   5. appended rows: their gradient into their new log ids;
 //   6. S rows: Adam in place in the MAT arena.
 // Steps 1, 3 and 4 are k_adam_exec launches: the row moves and history records ride on the Adam passes, and the
-// work array is never written back (no later kernel reads it).  D = 64, 128, 256 or 512 (the fused assembly's
-// limits too).
+// work array is never written back (no later kernel reads it).  Steps 1-3 are the device part and 4-6 the link
+// part (elr_update_args.part): a caller with the arenas in host memory runs the link part on a second stream.
+// D = 64, 128, 256 or 512 (the fused assembly's limits too).
 #include "elr_rowio.h"
 
 namespace elr {
@@ -53,11 +54,13 @@ __global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
     const RowFrag<VPL> g = frag_load<VPL, true>(a.grad + (a.g_base + i) * D + lane * VPL);
     if (i < a.n_rec) {
       const int64_t slot = (a.rec_dyn ? a.rec_dyn[i] : d) - a.rec_off, e = a.rec_j ? a.rec_j[i] : 0;
-      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K) frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g);
+      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K)
+        frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g);
     }
     if (d < 0 || d >= a.dst_rows || (a.src && a.src_base + i >= a.src_rows)) continue;
     const float* sp = (a.src ? a.src + (a.src_base + i) * 3 * D : a.dst + d * 3 * D) + lane * VPL;
-    RowFrag<VPL> w = frag_load<VPL, false>(sp), m = frag_load<VPL, false>(sp + D), v = frag_load<VPL, false>(sp + 2 * D);
+    RowFrag<VPL> w = frag_load<VPL, false>(sp), m = frag_load<VPL, false>(sp + D);
+    RowFrag<VPL> v = frag_load<VPL, false>(sp + 2 * D);
     frag_adam<VPL>(w, m, v, g, s);
     float* o = a.dst + d * 3 * D + lane * VPL;
     frag_store<VPL>(o, w);
@@ -66,10 +69,11 @@ __global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
   }
 }
 
-static int adam_exec(int vpl, const ExecAdam& a, const AdamScalars& s, hipStream_t st) {
+static int adam_exec(int vpl, const ExecAdam& a, const AdamScalars& s, hipStream_t st,
+                     int64_t max_blocks = int64_t(1) << 20) {
   if (a.n <= 0) return ELR_OK;
   int64_t blocks = (a.n + 3) / 4;
-  if (blocks > (int64_t(1) << 20)) blocks = int64_t(1) << 20;
+  if (blocks > max_blocks) blocks = max_blocks;
   switch (vpl) {
     case 1: k_adam_exec<1><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
     case 2: k_adam_exec<2><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
@@ -116,33 +120,39 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   if (!aligned16(a->pool) || !aligned16(a->mat) || !aligned16(a->glog) || !aligned16(Wk) || !aligned16(G) ||
       !aligned16(a->logs))
     return ELR_EINVAL;
+  if (a->part < ELR_UPDATE_ALL || a->part > ELR_UPDATE_LINK || a->link_blocks < 0) return ELR_EINVAL;
+  const int64_t lb = a->link_blocks > 0 ? a->link_blocks : int64_t(1) << 20;
   const AdamScalars s = make_scalars(sc);
   const int64_t nd = a->glog_slots;
-  // 1. hits: history record and Adam in place
-  if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
-                                    b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
-                                    rec ? n_hit : 0}, s, st)))
-    return rc;
-  // 2. evictions (before admissions reuse the slots)
-  if (a->nev) {
-    if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW,
-                            st)))
+  const bool dev_part = a->part != ELR_UPDATE_LINK, link_part = a->part != ELR_UPDATE_DEVICE;
+  if (dev_part) {
+    // 1. hits: history record and Adam in place
+    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
+                                      b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
+                                      rec ? n_hit : 0}, s, st)))
       return rc;
-    if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
+    // 2. evictions (before admissions reuse the slots)
+    if (a->nev) {
+      if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW,
+                              st)))
+        return rc;
+      if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
+        return rc;
+    }
+    // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
+    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
+                                      n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
       return rc;
   }
-  // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
-  if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
-                                    n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
-    return rc;
+  if (!link_part) return ELR_OK;
   // 4. compacted rows into their new MAT slots, transient F rows back into theirs
   if ((rc = adam_exec(vpl, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
                                     b[ELR_RANK_NCMP] - w0, G, b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr,
-                                    nullptr, 0, 0}, s, st)))
+                                    nullptr, 0, 0}, s, st, lb)))
     return rc;
   // 5. appended rows log their gradient
-  if (n_app && (rc = elr_copy_rows(a->logs, a->log_rows, a->a_ids, G + b[ELR_RANK_NAPP] * D, n_app, nullptr,
-                                   n_app, D, st)))
+  if (n_app && (rc = copy_rows_capped(a->logs, a->log_rows, a->a_ids, G + b[ELR_RANK_NAPP] * D, n_app, n_app, D,
+                                      lb, st)))
     return rc;
   // 6. S rows: Adam in place in the MAT arena
   if (n_s && (rc = elr_adam_rows(a->mat, a->mat_rows, a->s_slot, 1, G + b[ELR_RANK_S] * D, n_s, D, sc, st)))

@@ -65,15 +65,25 @@ __global__ __launch_bounds__(256) void k_copy_rows(float* __restrict__ dst, int6
 
 template <class DI, class SI>
 static int copy_rows_launch(float* dst, int64_t dst_rows, DI dix, const float* src, int64_t src_rows, SI six,
-                            int64_t n, int64_t W, void* stream) {
+                            int64_t n, int64_t W, void* stream, int64_t max_blocks = 256 * 32) {
   hipStream_t st = (hipStream_t)stream;
   int64_t blocks = (n + 3) / 4;
-  if (blocks > 256 * 32) blocks = 256 * 32;
+  if (blocks > max_blocks) blocks = max_blocks;
   if (W % 4 == 0 && aligned16(dst) && aligned16(src))
     k_copy_rows<true><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dix, src, src_rows, six, n, W);
   else
     k_copy_rows<false><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dix, src, src_rows, six, n, W);
   return launch_status();
+}
+
+// elr_copy_rows with at most max_blocks blocks (grid-stride): the executor's link part, whose waves mostly wait on
+// the host link, leaves the rest of the GPU to the other stream.
+int copy_rows_capped(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
+                     int64_t n, int64_t W, int64_t max_blocks, void* stream) {
+  if (n < 0 || W <= 0 || dst_rows < 0 || src_rows < 0 || max_blocks < 1) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!dst || !src) return ELR_EINVAL;
+  return copy_rows_launch(dst, dst_rows, IxList{dst_idx}, src, src_rows, IxList{nullptr}, n, W, stream, max_blocks);
 }
 
 }  // namespace elr

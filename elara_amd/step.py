@@ -119,9 +119,9 @@ class HipBackend:
     def glog_take(self, logs, ids, glog, dyn):
         glog_take(logs, ids, glog, dyn)
 
-    def step_update(self, es, p, G):
+    def step_update(self, es, p, G, part=0):
         """ElaraStep.update in one native call (elr_step_update): the same launches in the same order, issued from
-        C++ with no per-launch Python work."""
+        C++ with no per-launch Python work.  part: 0 all, 1 the device part, 2 the link part (ELR_UPDATE_*)."""
         if self._arenas is None or self._arenas[0] is not es:
             self._arenas = (es, _lib.dptr(es.pool).value, _lib.dptr(es.mat).value, _lib.dptr(es.logs).value,
                             _lib.dptr(es.glog).value)
@@ -137,7 +137,8 @@ class HipBackend:
             nev, _p64(p.ev_slot, nev), _p64(p.evf_slots, nev), _p64(p.evl_ids, nev * es.K), _p64(p.ev_dyn, nev),
             _p64(p.adm_slots, b[R_FADM + 1] - b[R_NADM]), p.lazy_n, es.n0,
             _p64(p.c_slots, b[R_LCMP + 1] - b[R_NCMP]), _p64(p.a_ids, b[R_LAPP + 1] - b[R_NAPP]),
-            _p64(p.FN_slot, b[R_FN + 1] - b[R_FN]), _p64(p.S_slot, b[R_S + 1] - b[R_S]))
+            _p64(p.FN_slot, b[R_FN + 1] - b[R_FN]), _p64(p.S_slot, b[R_S + 1] - b[R_S]), int(part),
+            int(es.link_blocks) if part == 2 else 0)
         _lib.check(_lib.lib().elr_step_update(ctypes.byref(a), ctypes.c_void_p(_lib.raw_stream(G.device))),
                    'elr_step_update')
 
@@ -228,6 +229,16 @@ class ElaraStep:
         self.host_arenas = bool(host_arenas and d.type == 'cuda')
         self.mat = torch.empty(self.mat_cap, 3, D, **ad)
         self.logs = torch.empty(self.log_cap + 1, D, **ad)
+        # with host arenas, the update's writes into them (compacted and transient rows into MAT, log appends, S
+        # rows) run on a second stream of default priority while the next step plans and assembles, so the host
+        # link carries both directions at once (update writes, assembly reads).  The next assembly that might read
+        # those rows waits for them: the one two steps later, or the next one if the step overflowed (an
+        # un-admitted row of batch s can reappear in batch s + 1; otherwise a row of batch s + 1 is a hit or admitted
+        # in step s, and the rows the link part writes are neither).
+        self._link = (torch.cuda.Stream(device=d) if self.host_arenas and getattr(self.be, 'step_update', None)
+                      else None)
+        self._link_pending = []
+        self.link_blocks = 32   # blocks per launch of the link part (measured best of 16-128 at C5 with host arenas)
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs')}
         self._deferred = []
@@ -250,6 +261,22 @@ class ElaraStep:
         mt, lt = self._host(self.mat_top, self.log_top)
         if mt > self.mat_cap - 1 or lt > self.log_cap:
             raise RuntimeError(f'arena capacity exceeded (MAT {mt}/{self.mat_cap - 1}, logs {lt}/{self.log_cap})')
+
+    def _wait_link(self, due):
+        """Make the current stream wait for the pending link-stream updates (s, event, overflowed) for which
+        due(s, overflowed) holds."""
+        keep = []
+        cur = torch.cuda.current_stream(self.d) if self._link_pending else None
+        for s_ev, ev, ovf in self._link_pending:
+            if due(s_ev, ovf):
+                cur.wait_event(ev)
+            else:
+                keep.append((s_ev, ev, ovf))
+        self._link_pending = keep
+
+    def join_link(self):
+        """Make the current stream wait for every pending link-stream update (before reading the arenas)."""
+        self._wait_link(lambda s_ev, ovf: True)
 
     def observe(self, step, u, n_dev=None):
         """Record that rows u appear at logical step `step` (the TTL lookahead, srm2/elara.py:160-161); with n_dev
@@ -352,7 +379,8 @@ class ElaraStep:
             ev_slot, keep_dyn = pc.dyn_out[:n_exp], pc.dyn_out[nd + n_exp:]
         rank = pc.rank
         u_ord, c_ord, sl_ord, L_row, L_cnt, loc_ord = pc.u_ord, pc.c_ord, pc.sl_ord, pc.L_row, pc.L_cnt, pc.loc_ord
-        if need > 0:   # overflow: un-admit (non-carry first) and recount
+        overflowed = need > 0
+        if overflowed:   # overflow: un-admit (non-carry first) and recount
             admit = (pc.flags & F_ADMIT) != 0
             in_next = (pc.flags & F_NEXT) != 0
             pri = (~admit).to(I32) * 4 + admit.to(I32) * (2 - 2 * in_next.to(I32))
@@ -375,6 +403,7 @@ class ElaraStep:
         p = Plan()
         p.s, p.u, p.n, p.b, p.order, p.rank = s, u, n, b, order, rank
         p.G = G
+        p.overflowed = overflowed
         p.counts = counts
         p.u_ord = u_ord
         p.hit_slot = sl_ord[b[R_HIT]:b[R_HIT + 1]]
@@ -429,6 +458,7 @@ class ElaraStep:
         """Work array [b[R_S] - b[R_NADM], 3, D] in class-rank order: admitted N / L / F, appended N / L, compacted
         N / L and transient F rows -- N rows by counter-hash init, L rows by replay of their log entries, F rows
         from the MAT arena."""
+        self._wait_link(lambda s_ev, ovf: s_ev <= p.s - 2 or (s_ev == p.s - 1 and ovf))
         b = p.b
         w0 = b[R_NADM]
         nLa, nLp, _ = p.nL
@@ -444,7 +474,19 @@ class ElaraStep:
         """G [n, D]: the batch's per-row gradients in class-rank order (p.order).  A backend with step_update
         (the HIP one: elr_step_update) issues the whole update natively, in the order below."""
         if getattr(self.be, 'step_update', None) is not None:
-            self.be.step_update(self, p, G)
+            if self._link is None:
+                self.be.step_update(self, p, G)
+                return
+            self.be.step_update(self, p, G, part=1)
+            self._link.wait_stream(torch.cuda.current_stream(self.d))
+            with torch.cuda.stream(self._link):
+                self.be.step_update(self, p, G, part=2)
+                ev = torch.cuda.Event()
+                ev.record()
+            for t in (p.work, G, p.c_slots, p.a_ids, p.FN_slot, p.S_slot):   # kept until the link stream is done
+                if t is not None and t.numel():
+                    t.record_stream(self._link)
+            self._link_pending.append((p.s, ev, p.overflowed))
             return
         be, s, b = self.be, p.s, p.b
         W, w0 = p.work, b[R_NADM]
@@ -496,6 +538,7 @@ class ElaraStep:
         """Current (w) -- or (w, m, v) with full=True -- of `rows`: resident rows from the pool, materialised rows
         from the MAT arena, logged and implicit rows by replay from the log arena."""
         K, D = self.K, self.D
+        self.join_link()
         out = torch.empty(rows.numel(), 3, D, device=self.d)
         sl = self.slot_of[rows]
         res = sl >= 0
@@ -578,4 +621,5 @@ def _run(step, batches, grads, steps, on_step):
         p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
         if on_step is not None:
             on_step(s + 1, p)
+    step.join_link()
     step.check_capacity()

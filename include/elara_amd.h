@@ -386,7 +386,20 @@ typedef struct elr_update_args {
   const int64_t* a_ids;       /* [n_app] log ids of the appended gradients (elr_dir_b) */
   const int64_t* fn_slot;     /* [n_fn] MAT slots of the transient F rows */
   const int64_t* s_slot;      /* [n_s] MAT slots of the S rows */
+  int32_t part;               /* ELR_UPDATE_ALL, or one of the two parts below, each in its own call */
+  int64_t link_blocks;        /* > 0: at most this many blocks per launch of the link part (its waves mostly wait on
+                                 the host link; a small grid leaves the GPU to the other stream); 0: no cap */
 } elr_update_args;
+
+/* elr_update_args.part: the whole update, or its two halves for a caller that runs them on two streams (the
+ * capacity tier: the link part writes the arenas in host memory while the device part's stream goes on).
+ * ELR_UPDATE_DEVICE: the hits, the evictions (reading the evicted pool slots and glog rows, which the admissions
+ * then reuse) and the admissions.  ELR_UPDATE_LINK: the compacted and transient rows into MAT, the log appends and
+ * the S rows' Adam; it reads only the work array, the gradients and its index arrays, and writes MAT and log rows
+ * that no row of the device part touches. */
+#define ELR_UPDATE_ALL 0
+#define ELR_UPDATE_DEVICE 1
+#define ELR_UPDATE_LINK 2
 
 int elr_step_update(const elr_update_args* args, void* stream);
 

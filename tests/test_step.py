@@ -88,7 +88,8 @@ def test_step_runs_on_cpu_with_oracle_backend():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow', 'host_arenas',
-                                  'host_arenas_S', 'D64_K2', 'D256_K4', 'K1_kthr0', 'L40_no_ring'])
+                                  'host_arenas_S', 'host_arenas_overflow', 'D64_K2', 'D256_K4', 'K1_kthr0',
+                                  'L40_no_ring'])
 def test_gpu_step_matches_oracle_step(dev, name):
     """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
     kernels over the host link.  L40_no_ring: a look-ahead too long for the 32-bit ring of loaded batches, so the
@@ -97,6 +98,7 @@ def test_gpu_step_matches_oracle_step(dev, name):
     print(f'[gpu-test] elara step {name}', flush=True)
     kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
           'host_arenas': {'host': True}, 'host_arenas_S': {'host': True, 'st': 'S'},
+          'host_arenas_overflow': {'host': True, 'C': 2000},
           'D64_K2': {'D': 64, 'K': 2, 'kthr': 2}, 'D256_K4': {'D': 256, 'K': 4, 'kthr': 3},
           'K1_kthr0': {'K': 1, 'kthr': 0}, 'L40_no_ring': {'L': 40}}[name]
     cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
@@ -109,6 +111,8 @@ def test_gpu_step_matches_oracle_step(dev, name):
     torch.cuda.synchronize()
     assert compare(g, c, cfg) > 0
     assert g.stats == c.stats
+    if name == 'host_arenas_overflow':
+        assert g.stats['overflow'] > 0 and g._link is not None, g.stats
 
 
 @pytest.mark.gpu
