@@ -7,8 +7,9 @@ executor's path for logged rows (srm2/elara.py:485, 514).  Inputs are resident i
 value = rows per second over the K timed steps.
 
 roofline: the dominant kernel (replay) -- algorithmic bytes per launch / its mean duration from HIP events
-recorded on the launch stream around every 4th timed step's launches; peak 8 TB/s.  cpu_baseline: the CPU oracle's replay + Adam (a C port of the
-reference CPU path, same thread split) on a bounded sample, timed on this host.
+recorded on the launch stream around every 4th timed step's launches; peak 8 TB/s.  cpu_baseline: the CPU
+oracle's replay + Adam (a C port of the reference CPU path, same thread split) on a bounded sample, timed on this
+host.
 
 Warm-up: the first 20-30 ms of sustained load run at a lower engine clock (measured on the headline step: replay
 288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound, 140 us

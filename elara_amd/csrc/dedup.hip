@@ -209,7 +209,8 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__
                                                          int64_t n, const int64_t* __restrict__ boff,
                                                          const int64_t* __restrict__ d_U,
                                                          int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
-                                                         int32_t* __restrict__ seg_occ0, int64_t* __restrict__ inverse) {
+                                                         int32_t* __restrict__ seg_occ0,
+                                                         int64_t* __restrict__ inverse) {
   const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   int64_t before = boff[blockIdx.x];   // heads in earlier positions of the tile's earlier rounds
   for (int r = 0; r < ITEMS; ++r) {

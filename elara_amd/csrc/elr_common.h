@@ -87,7 +87,9 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 __device__ __forceinline__ bool quot_num_ok(float n) {  // 2^-60 <= |n| < 2^40
   return __builtin_fabsf(n) >= 0x1.0p-60f && __builtin_fabsf(n) < 0x1.0p40f;
 }
-__device__ __forceinline__ uint64_t quot_num_lanes(float n) { return lanes_in(__builtin_fabsf(n), 0x1.0p-60f, 0x1.0p40f); }
+__device__ __forceinline__ uint64_t quot_num_lanes(float n) {
+  return lanes_in(__builtin_fabsf(n), 0x1.0p-60f, 0x1.0p40f);
+}
 __device__ __forceinline__ bool quot_den_ok(float d) { return d >= 0x1.0p-48f && d < 0x1.0p65f; }
 __device__ __forceinline__ float div_core(float n, float d) {
   float r = __builtin_amdgcn_rcpf(d);

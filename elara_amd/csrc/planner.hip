@@ -253,7 +253,8 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_admit(const int64_t* __rest
                                                            const int64_t* __restrict__ adm_slots, int64_t n_adm,
                                                            int64_t lazy_n, int evl, int64_t s, int64_t n0, int64_t C,
                                                            int64_t R, int K, const int8_t* __restrict__ code,
-                                                           int32_t* __restrict__ slot_of, int64_t* __restrict__ slot_row,
+                                                           int32_t* __restrict__ slot_of,
+                                                           int64_t* __restrict__ slot_row,
                                                            int8_t* __restrict__ adm_c0, int8_t* __restrict__ rj,
                                                            int8_t* __restrict__ rok, int32_t* __restrict__ pstep) {
   const int64_t i = (int64_t)blockIdx.x * kPlanBlock + threadIdx.x;
