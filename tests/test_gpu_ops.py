@@ -45,7 +45,7 @@ def test_adam_dense_equals_identity_slots(dev, D):
 
 
 @pytest.mark.parametrize('D,idx', [(128, torch.int64), (128, torch.int32), (64, torch.int64), (256, torch.int64),
-                                   (512, torch.int32), (30, torch.int64)])
+                                   (512, torch.int32), (30, torch.int64), (100, torch.int64), (192, torch.int32)])
 def test_adam_matches_oracle(dev, D, idx):
     """tests/test_ops.py:12-24: several steps with repeated rows across steps and grads at 3 magnitudes."""
     step_banner(f'adam D={D} idx={idx}')
@@ -175,7 +175,7 @@ def test_replay_matches_golden(dev, golden):
         assert same(out, golden[f'replay{ci}_out']), ci
 
 
-@pytest.mark.parametrize('D,K', [(128, 3), (64, 4), (256, 3), (30, 2), (128, 1)])
+@pytest.mark.parametrize('D,K', [(128, 3), (64, 4), (256, 3), (30, 2), (128, 1), (512, 3), (100, 8), (192, 5)])
 def test_replay_equals_eager(dev, D, K):
     """tests/test_replay.py:19-33 as an assertion: replay == eager GPU Adam == oracle, bitwise; cnt in {0..K}."""
     step_banner(f'replay D={D} K={K}')
