@@ -20,7 +20,7 @@ of it runs as HIP kernels (elara_amd/csrc/dedup.hip) on torch's current stream.
 import torch
 
 from . import _lib
-from .ops import _check_state, adam_scalars
+from .ops import _check_state, _scalars8
 
 I64 = torch.int64
 
@@ -182,7 +182,7 @@ def adam_dedup(pool, ids, grad, lr, b1, b2, eps, step):
     g = grad.reshape(n, D).contiguous()
     dev = pool.device
     scratch, nbytes = _scratch(dev, n, D)
-    s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
+    s = _scalars8(lr, b1, b2, eps, step)
     with _lib.on_device(dev):
         rc = _lib.lib().elr_adam_dedup(_lib.ptr(pool), pool.shape[0], _lib.ptr(idx), _lib.ptr(g), n, D, s,
                                        _lib.ptr(scratch), nbytes, _lib.stream_of(pool))

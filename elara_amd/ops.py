@@ -15,9 +15,24 @@ from .elara_dir import dir_ext  # noqa: F401  (the reference exposes dir_ext fro
 
 def adam_scalars(lr, b1, b2, eps, step):
     """The 8 fp32 Adam scalars of logical step `step` (fp64 arithmetic rounded to fp32), as a list of floats."""
-    out = (_lib.c_f32 * 8)()
-    _lib.lib().elr_adam_scalars(float(lr), float(b1), float(b2), float(eps), int(step), out)
-    return list(out)
+    return list(_scalars8(lr, b1, b2, eps, step))
+
+
+_SC_CACHE = {}
+
+
+def _scalars8(lr, b1, b2, eps, step):
+    """The same as a ctypes float[8] for the C-ABI, cached per (lr, b1, b2, eps, step): the callers pass it read-only,
+    and a training loop asks for the same few steps over and over."""
+    key = (float(lr), float(b1), float(b2), float(eps), int(step))
+    out = _SC_CACHE.get(key)
+    if out is None:
+        out = (_lib.c_f32 * 8)()
+        _lib.lib().elr_adam_scalars(*key, out)
+        if len(_SC_CACHE) > 4096:
+            _SC_CACHE.clear()
+        _SC_CACHE[key] = out
+    return out
 
 
 class _Ext:
@@ -61,7 +76,7 @@ def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
         raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {dev}')
     slots = slots.contiguous()
     grad = grad.contiguous()
-    s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
+    s = _scalars8(lr, b1, b2, eps, step)
     L = _lib.lib()
     with _lib.on_device(dev):
         rc = L.elr_adam_rows(_lib.dptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
@@ -80,7 +95,7 @@ def adam_rows_dense(state, grad, lr, b1, b2, eps, step):
     if not (grad.is_cuda and grad.dtype == torch.float32 and grad.device == state.device and grad.numel() == n * D):
         raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements on {state.device}')
     grad = grad.contiguous()
-    s = _lib.scalars8(adam_scalars(lr, b1, b2, eps, step))
+    s = _scalars8(lr, b1, b2, eps, step)
     with _lib.on_device(state.device):
         rc = _lib.lib().elr_adam_rows(_lib.ptr(state), n, None, 1, _lib.ptr(grad), n, D, s, _lib.stream_of(state))
     _lib.check(rc, 'elr_adam_rows')
