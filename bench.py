@@ -6,8 +6,9 @@ elr_replay_rows) and then take this step's row-sparse Adam update with a fresh g
 executor's path for logged rows (srm2/elara.py:485, 514).  Inputs are resident in HBM before timing starts.
 value = rows per second over the K timed steps.
 
-roofline: the dominant kernel (replay) -- algorithmic bytes per launch / its mean duration from HIP events
-recorded on the launch stream around every 4th timed step's launches; peak 8 TB/s.  cpu_baseline: the CPU
+roofline: the replay kernel -- algorithmic bytes per launch / its mean duration from HIP events (created with
+hipEventDisableSystemFence: timing only, no cache flush) recorded on the launch stream around every 4th timed
+step's launches; peak 8 TB/s.  cpu_baseline: the CPU
 oracle's replay + Adam (a C port of the reference CPU path, same thread split) on a bounded sample, timed on this
 host.
 
@@ -33,6 +34,70 @@ sys.path.insert(0, str(ROOT))
 METRIC = 'sparse-Adam+replay rows/s at d=128; achieved HBM GB/s vs ~8 TB/s peak'
 HBM_PEAK_GBS = 8000.0
 EV_EVERY = 4   # headline: HIP events on every 4th timed step
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000   # hipEventDisableSystemFence, hip_runtime_api.h
+_HIP = None
+
+
+def _hip():
+    """The HIP runtime that torch has loaded (found in this process's mappings, so the events below live in the
+    same runtime as torch's streams and the library's launches)."""
+    global _HIP
+    if _HIP is None:
+        import ctypes
+        with open('/proc/self/maps') as f:
+            path = next((ln.split()[-1] for ln in f if 'libamdhip64' in ln), None)
+        if path is None:
+            raise RuntimeError('the HIP runtime is not loaded')
+        h = ctypes.CDLL(path)
+        vp = ctypes.c_void_p
+        h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(vp), ctypes.c_uint]
+        h.hipEventRecord.argtypes = [vp, vp]
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        h.hipEventDestroy.argtypes = [vp]
+        for fn in (h.hipEventCreateWithFlags, h.hipEventRecord, h.hipEventElapsedTime, h.hipEventDestroy):
+            fn.restype = ctypes.c_int
+        _HIP = h
+    return _HIP
+
+
+class HipEvent:
+    """A HIP timing event created with hipEventDisableSystemFence, with torch.cuda.Event's record / elapsed_time.
+    A default event does a system-scope release when it completes: a write-back and invalidation of the caches,
+    which costs the launch after it a few us and a cold cache.  An event that only times kernels on one GPU needs
+    none of that (hip_runtime_api.h documents the flag for "events that are only being used to measure timing")."""
+
+    def __init__(self):
+        import ctypes
+        self.h = ctypes.c_void_p()
+        rc = _hip().hipEventCreateWithFlags(ctypes.byref(self.h), HIP_EVENT_DISABLE_SYSTEM_FENCE)
+        if rc:
+            raise RuntimeError(f'hipEventCreateWithFlags failed ({rc})')
+
+    def record(self, stream):
+        import ctypes
+        rc = _hip().hipEventRecord(self.h, ctypes.c_void_p(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(f'hipEventRecord failed ({rc})')
+
+    def elapsed_time(self, end):
+        """Milliseconds from this event to `end`; both must have completed."""
+        import ctypes
+        ms = ctypes.c_float()
+        rc = _hip().hipEventElapsedTime(ctypes.byref(ms), self.h, end.h)
+        if rc:
+            raise RuntimeError(f'hipEventElapsedTime failed ({rc})')
+        return ms.value
+
+    def destroy(self):
+        if self.h:
+            _hip().hipEventDestroy(self.h)
+            self.h = None
+
+
+def _destroy(evs):
+    for pair in evs:
+        for e in pair or ():
+            e.destroy()
 
 
 def replay_bytes(n, K, D, nlog):
@@ -129,8 +194,7 @@ def headline(args):
     torch.cuda.synchronize()
     # kernel durations from HIP events on every EV_EVERY-th timed step: each marker costs the step a few us
     # (three per step: 0.268 against 0.258 ms per step), so sampling keeps the instrument out of `value`
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] if i % EV_EVERY == 0 else None
-           for i in range(args.steps)]
+    evs = [[HipEvent() for _ in range(3)] if i % EV_EVERY == 0 else None for i in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -140,6 +204,7 @@ def headline(args):
     evs = [e for e in evs if e is not None]
     rep_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
     adam_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    _destroy(evs)
     rb, ab = replay_bytes(n, K, D, nlog), adam_bytes(n, D)
     rep_gbs = rb / (rep_ms * 1e-3) / 1e9
     res = {
@@ -181,10 +246,12 @@ def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
 SETTLE_S = 0.08   # --mode c1/c3/c4: untimed load before timing (the engine clock's ramp takes 20-30 ms)
 
 
-def _timed_steps(step_fn, steps, warmup, settle_s=0.0):
+def _timed_steps(step_fn, steps, warmup, settle_s=0.0, every=1):
     """Run `warmup` untimed calls of step_fn(i), more (whole batches of `warmup`) until at least `settle_s` seconds
     of untimed work have passed, then `steps` timed calls bracketed by device synchronisation.  Returns (seconds for
-    the timed steps, per-step ms from events on the current stream, number of untimed calls)."""
+    the timed steps, per-step ms from events on the current stream, number of untimed calls).  Only every `every`-th
+    timed step is bracketed by events: each event is a marker packet between launches, which costs a few us of idle
+    GPU, about a tenth of a short step."""
     import torch
     stream = torch.cuda.current_stream()
     done = 0
@@ -197,15 +264,20 @@ def _timed_steps(step_fn, steps, warmup, settle_s=0.0):
         if warmup == 0 or time.perf_counter() - t_w >= settle_s:
             break
     warmup = done
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    ev = [(HipEvent(), HipEvent()) for _ in range(0, steps, every)]
     t0 = time.perf_counter()
     for i in range(steps):
-        ev[i][0].record(stream)
+        if i % every:
+            step_fn(warmup + i)
+            continue
+        ev[i // every][0].record(stream)
         step_fn(warmup + i)
-        ev[i][1].record(stream)
+        ev[i // every][1].record(stream)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    return el, [a.elapsed_time(b) for a, b in ev], warmup
+    ms = [a.elapsed_time(b) for a, b in ev]
+    _destroy(ev)
+    return el, ms, warmup
 
 
 def _line(metric, value, unit, args, steps, warmup, el, config, gbytes_per_step, dtype='f32', extra=None):
@@ -231,10 +303,11 @@ def mode_c1(args):
     rng = np.random.default_rng(0)
     ids = [torch.from_numpy(synth.unique_rows(rng, R, n)).to(dev) for _ in range(10)]
     gs = [torch.from_numpy(synth.grads(rng, n, D)).to(dev) for _ in range(10)]
-    # t = 1..10 on the timed steps: call i uses batch i % 10 at step (i % 10) + 1, and the warm-up is whole tens
-    steps = 10
+    # t = 1..10 on every ten timed calls: call i uses batch i % 10 at step (i % 10) + 1, and the warm-up is whole
+    # tens.  Ten passes are timed, so that the two synchronisations around the timed region are not a tenth of it.
+    steps = 100
     el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 10], *synth.ADAM, i % 10 + 1),
-                                  steps, 10, SETTLE_S)
+                                  steps, 10, SETTLE_S, every=10)
     return _line('C1 row-sparse Adam rows/s (d=64)', n * steps / el, 'rows/s', args, steps, warmup, el,
                  {'workload': 'C1 row-sparse Adam: 1,048,576 x 64 fp32 table, 65,536 unique rows per step',
                   'rows_per_step': n, 'dim': D}, adam_bytes(n, D) / 1e9,
@@ -290,7 +363,7 @@ def mode_c4(args):
     gs = [torch.randn(n, D, device=dev, generator=gen) * 1e-3 for _ in range(4)]
     steps = 50
     el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 4], *synth.ADAM, i + 1), steps, 10,
-                                  SETTLE_S)
+                                  SETTLE_S, every=5)
     return _line('C4 large-row sparse Adam rows/s (d=256, 153.6 GB table)', n * steps / el, 'rows/s', args, steps,
                  warmup, el, {'workload': 'C4 large-row stress: 50,000,000 x 256 fp32 table (w, m, v: 153.6 GB in '
                                           'HBM), 262,144 unique Zipf(1.1) rows per step', 'rows_per_step': n,
