@@ -20,6 +20,10 @@
 // D = 64, 128, 256 or 512 (the fused assembly's limits too).
 #include "elr_rowio.h"
 
+#ifndef ELR_EXEC_U
+#define ELR_EXEC_U 2   // rows per wave in flight
+#endif
+
 namespace elr {
 
 // One Adam launch of the executor with the row moves fused in.  Row i < n reads gradient row g_base + i; with
@@ -45,40 +49,60 @@ struct ExecAdam {
   int64_t rec_off, n_rec;
 };
 
-template <int VPL>
+template <int VPL, int U>
 __global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
   constexpr int64_t D = 64 * VPL;
   const int lane = threadIdx.x & 63;
-  for (int64_t i = wave_id(); i < a.n; i += wave_count()) {
-    const int64_t d = i < a.na ? a.dst_a[i] : a.dst_b[i - a.na];
-    const RowFrag<VPL> g = frag_load<VPL, true>(a.grad + (a.g_base + i) * D + lane * VPL);
-    if (i < a.n_rec) {
-      const int64_t slot = (a.rec_dyn ? a.rec_dyn[i] : d) - a.rec_off, e = a.rec_j ? a.rec_j[i] : 0;
-      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K)
-        frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g);
+  for (int64_t i0 = wave_id() * U; i0 < a.n; i0 += wave_count() * U) {
+    int64_t d[U];
+    bool ok[U];
+    RowFrag<VPL> g[U], w[U], m[U], v[U];
+    // every row's loads first, so that U rows are in flight per wave
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u;
+      ok[u] = i < a.n;
+      if (!ok[u]) continue;
+      d[u] = i < a.na ? a.dst_a[i] : a.dst_b[i - a.na];
+      g[u] = frag_load<VPL, true>(a.grad + (a.g_base + i) * D + lane * VPL);
+      ok[u] = d[u] >= 0 && d[u] < a.dst_rows && !(a.src && a.src_base + i >= a.src_rows);
+      if (!ok[u]) continue;
+      const float* sp = (a.src ? a.src + (a.src_base + i) * 3 * D : a.dst + d[u] * 3 * D) + lane * VPL;
+      w[u] = frag_load<VPL, false>(sp);
+      m[u] = frag_load<VPL, false>(sp + D);
+      v[u] = frag_load<VPL, false>(sp + 2 * D);
     }
-    if (d < 0 || d >= a.dst_rows || (a.src && a.src_base + i >= a.src_rows)) continue;
-    const float* sp = (a.src ? a.src + (a.src_base + i) * 3 * D : a.dst + d * 3 * D) + lane * VPL;
-    RowFrag<VPL> w = frag_load<VPL, false>(sp), m = frag_load<VPL, false>(sp + D);
-    RowFrag<VPL> v = frag_load<VPL, false>(sp + 2 * D);
-    frag_adam<VPL>(w, m, v, g, s);
-    float* o = a.dst + d * 3 * D + lane * VPL;
-    frag_store<VPL>(o, w);
-    frag_store<VPL>(o + D, m);
-    frag_store<VPL>(o + 2 * D, v);
+    // history records (also for a row whose destination is out of range)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u;
+      if (i >= a.n || i >= a.n_rec) continue;
+      const int64_t slot = (a.rec_dyn ? a.rec_dyn[i] : d[u]) - a.rec_off, e = a.rec_j ? a.rec_j[i] : 0;
+      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K) frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (!ok[u]) continue;
+      frag_adam<VPL>(w[u], m[u], v[u], g[u], s);
+      float* o = a.dst + d[u] * 3 * D + lane * VPL;
+      frag_store<VPL>(o, w[u]);
+      frag_store<VPL>(o + D, m[u]);
+      frag_store<VPL>(o + 2 * D, v[u]);
+    }
   }
 }
 
 static int adam_exec(int vpl, const ExecAdam& a, const AdamScalars& s, hipStream_t st,
                      int64_t max_blocks = int64_t(1) << 20) {
+  constexpr int U = ELR_EXEC_U;
   if (a.n <= 0) return ELR_OK;
-  int64_t blocks = (a.n + 3) / 4;
+  int64_t blocks = (a.n + 4 * U - 1) / (4 * U);
   if (blocks > max_blocks) blocks = max_blocks;
   switch (vpl) {
-    case 1: k_adam_exec<1><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
-    case 2: k_adam_exec<2><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
-    case 4: k_adam_exec<4><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
-    default: k_adam_exec<8><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    case 1: k_adam_exec<1, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    case 2: k_adam_exec<2, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    case 4: k_adam_exec<4, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    default: k_adam_exec<8, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
   }
   return launch_status();
 }
