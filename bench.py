@@ -281,11 +281,11 @@ def _timed_steps(step_fn, steps, warmup, settle_s=0.0, every=1):
 
 
 def _line(metric, value, unit, args, steps, warmup, el, config, gbytes_per_step, dtype='f32', extra=None):
-    gbs = gbytes_per_step * steps / el
+    gbs = gbytes_per_step * steps / el if gbytes_per_step is not None else None
     res = {'metric': metric, 'value': value, 'unit': unit, 'n_gpus': 1, 'steps': steps, 'warmup': warmup,
            'ms_per_step': el / steps * 1e3, 'higher_is_better': True, 'scaling': 'weak', 'vs_baseline': None,
            'dtype': dtype, 'data': 'synthetic', 'config': config,
-           'step_GBps': gbs, 'step_frac_of_hbm_peak': gbs / HBM_PEAK_GBS}
+           'step_GBps': gbs, 'step_frac_of_hbm_peak': gbs / HBM_PEAK_GBS if gbs is not None else None}
     if extra:
         res.update(extra)
     return res
@@ -421,7 +421,7 @@ def mode_c5(args):
                               'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, tabs.R),
                   'arenas': 'host' if host else 'hbm', 'mat_top': mt, 'log_top': lt,
                   'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
-                  'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, 0.0,
+                  'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, None,
                  extra={'steps_per_s': steps / el, 'stats': s, 'note': 'step_GBps not reported for C5 (mixed '
                         'kernels; per-kernel bytes in profiles/)'})
 
