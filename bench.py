@@ -1,6 +1,6 @@
 """Benchmark of the ELARA sparse-update hot path on one MI355X.
 
-Step (the headline, BASELINE metric "sparse-Adam+replay rows/s at d=128"): config C2's 262,144 logged rows at
+Step (the headline metric, "sparse-Adam+replay rows/s at d=128"): config C2's 262,144 logged rows at
 D=128 (c ~ U{1,2,3} gradients each, steps with gaps U{1..50}) are materialised by exact replay (init + c Adam steps,
 elr_replay_rows) and then take this step's row-sparse Adam update with a fresh gradient (elr_adam_rows) -- the
 executor's path for logged rows (srm2/elara.py:485, 514).  Inputs are resident in HBM before timing starts.

@@ -78,7 +78,8 @@ __global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
       const int64_t i = i0 + u;
       if (i >= a.n || i >= a.n_rec) continue;
       const int64_t slot = (a.rec_dyn ? a.rec_dyn[i] : d[u]) - a.rec_off, e = a.rec_j ? a.rec_j[i] : 0;
-      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K) frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g[u]);
+      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K)
+        frag_store<VPL>(a.glog + (slot * a.K + e) * D + lane * VPL, g[u]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {

@@ -47,7 +47,8 @@ def main():
     cases = [(128, 0, float(np.float32(1 / np.sqrt(128)))), (64, 1234, 0.01), (256, 42, 0.125), (24, 7, 0.5),
              (128, 2**31 + 5, 0.01)]
     for ci, (D, seed, bound) in enumerate(cases):
-        rows = np.concatenate([np.arange(4), rng.integers(0, 30_000_000, 6), [2**32 // D - 1, 2**32 // D, 2**32 // D + 1],
+        rows = np.concatenate([np.arange(4), rng.integers(0, 30_000_000, 6),
+                               [2**32 // D - 1, 2**32 // D, 2**32 // D + 1],
                                [2**32 - 1, 2**32, 2**32 + 1, 2**33 + 12345, 2**40 + 7, 2**62 + 3]]).astype(np.int64)
         out = run_init(torch.from_numpy(rows), D, seed, bound)
         vec[f'init{ci}_rows'] = rows
@@ -68,7 +69,8 @@ def main():
                                   torch.from_numpy(steps), torch.from_numpy(cnt), seed, bound, torch.from_numpy(table),
                                   D, K, BLOCK=next_pow2(D))
         for k_, v_ in dict(rows=rows, cnt=cnt, steps=steps, logs=logs, offs=offs, table=table,
-                           meta=np.array([D, K, seed], dtype=np.int64), bound=np.array([bound]), out=out.numpy()).items():
+                           meta=np.array([D, K, seed], dtype=np.int64), bound=np.array([bound]),
+                           out=out.numpy()).items():
             vec[f'replay{ci}_{k_}'] = v_
     # ---- adam: [C,3,D] state with nonzero m, v; grads at three magnitudes; steps 1, 2, 7, 1000
     for ci, (D, step, gs) in enumerate([(128, 1, 1e-2), (64, 2, 1.0), (128, 7, 1e-1), (32, 1000, 1e-3)]):

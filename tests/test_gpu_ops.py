@@ -1,7 +1,7 @@
 """GPU parity of Adam, init and replay (through the C-ABI) against the CPU oracle and the reference's vectors.
 
 Bar: bitwise fp32 equality.  Mirrors the reference's tests/test_ops.py:10-24 and tests/test_replay.py:16-33 with
-assertions, plus the BASELINE configs C1 (full size) and C2 (full size).
+assertions, plus the benchmark configs C1 (full size) and C2 (full size).
 """
 import numpy as np
 import pytest
