@@ -30,11 +30,8 @@ def _case(n, W, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('W', WIDTHS)
-@pytest.mark.parametrize('n', SIZES)
+@pytest.mark.parametrize('n,W', [(n, W) for n in SIZES for W in WIDTHS if n * W <= 150_000_000])   # under 0.6 GB
 def test_gpu_copy_rows_matches_indexing(dev, n, W):
-    if n * W > 150_000_000:
-        pytest.skip('keeps the case under 0.6 GB')
     print(f'[gpu-test] copy_rows n={n} W={W}', flush=True)
     dst, src, di, si = _case(n, W, seed=n + W)
     want = dst.copy()
