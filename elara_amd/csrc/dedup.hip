@@ -8,8 +8,8 @@
 // Sort.  Stable LSD radix sort of (id, occurrence index) pairs, 8-bit digits, ceil(key_bits / 8) passes, keys held
 // as uint32 when key_bits <= 32.  Each pass is three launches: per-tile digit histograms (tiles of 4096 keys, or
 // 1024 below 2^21 keys), one block per digit scanning that digit's per-tile counts, and a scatter in which each
-// key's rank among equal digits of its tile comes from wave ballots (peer mask of the 8 digit bits), per-wave counts
-// in LDS and a running count over the tile's rounds, so equal keys keep their occurrence order.
+// key's rank among equal digits of its tile comes from wave ballots (peer mask of the 8 digit bits), a per-wave
+// running count in LDS and a scan over the tile's waves, so equal keys keep their occurrence order.
 //
 // Segments.  Sorted position i starts a segment when its key differs from position i-1; a scan of those heads
 // gives every position its unique index (the inverse) and every unique id its first position.
@@ -85,9 +85,13 @@ __global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict_
 }
 
 // Stable scatter of one pass.  FIRST: the source keys are the caller's int64 ids and the values are their
-// positions.  Each item's rank among the tile's items of its digit comes from ballots (wave) and LDS counts (block);
-// the tile is then sorted by digit in LDS and written out run by run, so consecutive threads write consecutive
-// addresses of one digit's bucket instead of 64 scattered ones.
+// positions.  Wave w of the block takes the tile's w-th quarter, 64 consecutive positions per round, so an item's
+// rank among the tile's items of its digit is: items of that digit in earlier waves' quarters, plus those of its
+// own wave's earlier rounds (a per-wave running count in LDS, which only that wave touches, in program order), plus
+// its peers in the same round below its lane (ballots).  The waves run their rounds without block barriers; one
+// scan over the waves' counts per digit at the end gives the first term.  The tile is then sorted by digit in LDS
+// and written out run by run, so consecutive threads write consecutive addresses of one digit's bucket instead of
+// 64 scattered ones.
 template <typename Src, typename Key, bool FIRST, int ITEMS>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __restrict__ src_keys,
                                                                 const int32_t* __restrict__ src_vals, int64_t n,
@@ -98,29 +102,28 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   constexpr int NW = kSortThreads / 64;
   constexpr int TILE = kSortThreads * ITEMS;
   __shared__ int64_t bo[kRadixBins];   // global position of this tile's first item of digit d
-  __shared__ int run[kRadixBins];      // items of digit d in earlier rounds of the tile
+  __shared__ int run[kRadixBins];      // items of digit d in the tile
   __shared__ int lbase[kRadixBins];    // position of digit d's first item in the tile sorted by digit
-  __shared__ int wc[NW][kRadixBins];
+  __shared__ int wc[NW][kRadixBins];   // per wave: running count of digit d, then the count in earlier waves
   __shared__ Key lk[TILE];
   __shared__ int32_t lv[TILE];
-  const int t = threadIdx.x, w = t >> 6;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   {
     // digit bases: exclusive scan of the 256 digit totals (n < 2^31, so they fit in int)
     int v[1] = {(int)dtot[t]}, ex[1], tot[1];
     block_excl_scan<kSortThreads, 1>(v, ex, tot);
     bo[t] = (int64_t)ex[0] + offs[(int64_t)t * nblk + blockIdx.x];
   }
-  run[t] = 0;
 #pragma unroll
   for (int q = 0; q < NW; ++q) wc[q][t] = 0;
   __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * TILE;
+  const int64_t tile0 = (int64_t)blockIdx.x * TILE, base = tile0 + (int64_t)w * (ITEMS * 64);
   Key kk[ITEMS];
   int32_t vv[ITEMS];
   int rk[ITEMS];
 #pragma unroll
   for (int r = 0; r < ITEMS; ++r) {
-    const int64_t pos = base + (int64_t)r * kSortThreads + t;
+    const int64_t pos = base + (int64_t)r * 64 + lane;
     const bool valid = pos < n;
     const Key k = valid ? (Key)src_keys[pos] : (Key)0;
     kk[r] = k;
@@ -134,25 +137,28 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
       m &= bit ? bal : ~bal;
     }
     const int lr = __popcll(m & lanemask_lt());
-    if (valid && lr == 0) wc[w][d] = __popcll(m);
-    __syncthreads();
-    rk[r] = -1;
-    if (valid) {
-      int rank = run[d] + lr;
-#pragma unroll
-      for (int q = 0; q < NW; ++q) rank += q < w ? wc[q][d] : 0;
-      rk[r] = rank;
-    }
-    __syncthreads();
-    int add = 0;
+    // every lane reads its digit's running count before the group's lowest lane adds the group's size: one wave's
+    // LDS accesses take effect in program order
+    const int before = valid ? wc[w][d] : 0;
+    rk[r] = valid ? before + lr : -1;
+    if (valid && lr == 0) wc[w][d] = before + __popcll(m);
+  }
+  __syncthreads();
+  {
+    // per digit: exclusive scan over the waves, and the tile's total
+    int acc = 0;
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-      add += wc[q][t];
-      wc[q][t] = 0;
+      const int c = wc[q][t];
+      wc[q][t] = acc;
+      acc += c;
     }
-    run[t] += add;
-    __syncthreads();
+    run[t] = acc;
   }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < ITEMS; ++r)
+    if (rk[r] >= 0) rk[r] += wc[w][digit_of(kk[r], shift)];
   {
     // the tile sorted by digit: digit d's items start at the exclusive scan of the tile's digit counts
     int v[1] = {run[t]}, ex[1], tot[1];
@@ -169,7 +175,7 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
     }
   }
   __syncthreads();
-  const int64_t rem = n - base;
+  const int64_t rem = n - tile0;
   const int nvalid = rem < TILE ? (int)rem : TILE;
   for (int j = t; j < nvalid; j += kSortThreads) {
     const Key k = lk[j];
