@@ -117,13 +117,55 @@ static void launch_adam_wpr(float* state, int64_t C, const Idx* slots, const flo
   }
 }
 
+// D = 64: two rows per wave, half a wave (32 lanes of 8 bytes) per row, so that each load and store instruction
+// moves 512 bytes instead of the 256 of a wave-per-row pass.  Same per-element operations as every other Adam kernel
+// here; frag_adam's range check then covers the lanes of both rows.
+#ifndef ELR_D64_PAIR
+#define ELR_D64_PAIR 1
+#endif
+
+template <typename Idx>
+__global__ __launch_bounds__(256) void k_adam_rows_d64_pair(float* __restrict__ state, int64_t C,
+                                                            const Idx* __restrict__ slots, int64_t base,
+                                                            const float* __restrict__ grad, int64_t n,
+                                                            AdamScalars s) {
+  constexpr int64_t D = 64;
+  const int lane = threadIdx.x & 63;
+  const int64_t i = wave_id() * 2 + (lane >> 5);
+  const int off = (lane & 31) * 2;
+  int64_t sl = i < n ? (slots ? (int64_t)slots[i] : base + i) : -1;
+  if (sl >= C) sl = -1;
+  if (sl < 0) return;
+  float* rec = state + sl * 3 * D + off;
+  RowFrag<2> w = frag_load<2, false>(rec), m = frag_load<2, false>(rec + D), v = frag_load<2, false>(rec + 2 * D);
+  const RowFrag<2> g = frag_load<2, true>(grad + i * D + off);
+  frag_adam<2>(w, m, v, g, s);
+  frag_store<2>(rec, w);
+  frag_store<2>(rec + D, m);
+  frag_store<2>(rec + 2 * D, v);
+}
+
+template <typename Idx>
+static void launch_adam_d64_pair(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n,
+                                 const AdamScalars& s, hipStream_t st) {
+  constexpr int64_t per = wpr_rows_per_launch(2);
+  for (int64_t a = 0; a < n; a += per) {
+    const int64_t m = n - a < per ? n - a : per;
+    k_adam_rows_d64_pair<Idx><<<grid_for((m + 1) / 2, 4, kOneShotBlocks), 256, 0, st>>>(
+        state, C, slots ? slots + a : nullptr, a, grad + a * 64, m, s);
+  }
+}
+
 template <typename Idx>
 static int launch_adam(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n, int64_t D,
                        const AdamScalars& s, hipStream_t st) {
   const int vpl = wpr_vpl(D);
   if (vpl && aligned16(state) && aligned16(grad)) {
     switch (vpl) {
-      case 1: launch_adam_wpr<1, Idx>(state, C, slots, grad, n, s, st); break;
+      case 1:
+        if (ELR_D64_PAIR) launch_adam_d64_pair<Idx>(state, C, slots, grad, n, s, st);
+        else launch_adam_wpr<1, Idx>(state, C, slots, grad, n, s, st);
+        break;
       case 2: launch_adam_wpr<2, Idx>(state, C, slots, grad, n, s, st); break;
       case 4: launch_adam_wpr<4, Idx>(state, C, slots, grad, n, s, st); break;
       default: launch_adam_wpr<8, Idx>(state, C, slots, grad, n, s, st); break;

@@ -44,8 +44,9 @@ def test_adam_dense_equals_identity_slots(dev, D):
     assert same(a, b)
 
 
-@pytest.mark.parametrize('D,idx', [(128, torch.int64), (128, torch.int32), (64, torch.int64), (256, torch.int64),
-                                   (512, torch.int32), (30, torch.int64), (100, torch.int64), (192, torch.int32)])
+@pytest.mark.parametrize('D,idx', [(128, torch.int64), (128, torch.int32), (64, torch.int64), (64, torch.int32),
+                                   (256, torch.int64), (512, torch.int32), (30, torch.int64), (100, torch.int64),
+                                   (192, torch.int32)])
 def test_adam_matches_oracle(dev, D, idx):
     """tests/test_ops.py:12-24: several steps with repeated rows across steps and grads at 3 magnitudes."""
     step_banner(f'adam D={D} idx={idx}')
