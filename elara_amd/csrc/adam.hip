@@ -120,10 +120,6 @@ static void launch_adam_wpr(float* state, int64_t C, const Idx* slots, const flo
 // D = 64: two rows per wave, half a wave (32 lanes of 8 bytes) per row, so that each load and store instruction
 // moves 512 bytes instead of the 256 of a wave-per-row pass.  Same per-element operations as every other Adam kernel
 // here; frag_adam's range check then covers the lanes of both rows.
-#ifndef ELR_D64_PAIR
-#define ELR_D64_PAIR 1
-#endif
-
 template <typename Idx>
 __global__ __launch_bounds__(256) void k_adam_rows_d64_pair(float* __restrict__ state, int64_t C,
                                                             const Idx* __restrict__ slots, int64_t base,
@@ -162,10 +158,7 @@ static int launch_adam(float* state, int64_t C, const Idx* slots, const float* g
   const int vpl = wpr_vpl(D);
   if (vpl && aligned16(state) && aligned16(grad)) {
     switch (vpl) {
-      case 1:
-        if (ELR_D64_PAIR) launch_adam_d64_pair<Idx>(state, C, slots, grad, n, s, st);
-        else launch_adam_wpr<1, Idx>(state, C, slots, grad, n, s, st);
-        break;
+      case 1: launch_adam_d64_pair<Idx>(state, C, slots, grad, n, s, st); break;   // C1: 22.8 us, 25.5 a wave per row
       case 2: launch_adam_wpr<2, Idx>(state, C, slots, grad, n, s, st); break;
       case 4: launch_adam_wpr<4, Idx>(state, C, slots, grad, n, s, st); break;
       default: launch_adam_wpr<8, Idx>(state, C, slots, grad, n, s, st); break;
