@@ -8,14 +8,15 @@ value = rows per second over the K timed steps.
 
 roofline: the replay kernel -- algorithmic bytes per launch / its mean duration from HIP events (created with
 hipEventDisableSystemFence: timing only, no cache flush) recorded on the launch stream around every 4th timed
-step's launches; peak 8 TB/s.  cpu_baseline: the CPU
-oracle's replay + Adam (a C port of the reference CPU path, same thread split) on a bounded sample, timed on this
-host.
+step's launches; peak 8 TB/s.  cpu_baseline: the same step on this host's cores at nthreads = nproc, with every Adam
+step done by the reference's own compiled cpu_adam (oracle/_ref), on a bounded sample of the rows; the oracle's C
+port of the whole step is reported beside it.
 
-Warm-up: the first 20-30 ms of sustained load run at a lower engine clock (measured on the headline step: replay
-288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound, 140 us
-throughout).  The defaults (200 untimed steps, about 55 ms, then 200 timed steps) measure the steady state; an
-explicit --warmup W is honoured exactly.  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
+Clock settle and warm-up: the first 20-30 ms of sustained load run at a lower engine clock (measured on the headline
+step: replay 288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound,
+140 us throughout).  Before the W warm-up steps, the headline runs --settle-ms (default 100) of untimed Adam launches
+on the step's own buffers, so the W warm-up and K timed steps all run at the steady clock, whatever W is; the line
+reports the settle under `clock_settle`.  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode headline|copy] [--no-cpu]
 """
@@ -111,44 +112,22 @@ def adam_bytes(n, D, idx_bytes=8):
     return n * (28 * D + idx_bytes)
 
 
-def cpu_sample_baseline(w, D, K, seed, bound, table_np, threads, pass_s=2.5):
-    """Time the oracle's replay + Adam (kind 'port': the C restatement of the reference CPU path with its
-    contiguous-chunk thread split) on a bounded sample of the workload.  The sample starts at 16,384 rows and
-    grows up to the whole step; each of 1 warm-up + 3 timed passes repeats the sample step for >= pass_s seconds
-    (about 10 s of CPU work in all); the median pass rate is reported."""
-    from elara_amd import synth
-    from oracle import oracle as O
-    n = min(w.n, 16_384)
-    rng = np.random.default_rng(5)
-    while True:
-        rows, cnt, steps, offs = w.rows[:n], w.cnt[:n], w.steps[:n], w.offs[:n]
-        nlog = int(cnt.sum())
-        logs = w.logs[:nlog]
-        g = synth.grads(rng, n, D)
-        idx = np.arange(n, dtype=np.int64)
-        sc = O.adam_scalars(*synth.ADAM, w.max_step + 1)
-
-        def once():
-            out = O.replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table_np, nthreads=threads)
-            O.cpu_adam(out, idx, g, sc, threads)
-
-        t0 = time.perf_counter(); once(); dt = time.perf_counter() - t0
-        if dt >= 0.5 or n >= w.n:
-            break
-        n = min(w.n, n * 4)
-    reps = max(1, int(np.ceil(pass_s / max(dt, 1e-6))))
-    rates = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            once()
-        rates.append(n * reps / (time.perf_counter() - t0))
-    rate = float(np.median(rates))
-    per_row = (replay_bytes(n, K, D, int(w.cnt[:n].sum())) + adam_bytes(n, D)) / n
-    return {'value': rate, 'unit': 'rows/s', 'cores': threads, 'kind': 'port',
-            'sample': f'oracle replay (K=3) + cpu_adam of the first {n} of the {w.n} C2 rows at D={D}, repeated '
-                      f'{reps}x per pass, {threads} threads, median of 3 passes after 1 warm-up',
-            'gbs': rate * per_row / 1e9, 'host_cpu': _cpu_model()}
+def host_cpus():
+    """The host's CPU facts for the baseline: nproc (GNU coreutils' count of usable processing units: the affinity
+    mask, or OMP_NUM_THREADS where it is set, as it is on the GPU box), the online CPU count and the model."""
+    import shutil
+    import subprocess
+    nproc = None
+    exe = shutil.which('nproc')
+    if exe:
+        try:
+            nproc = int(subprocess.run([exe], capture_output=True, text=True, check=True).stdout.strip())
+        except (OSError, ValueError, subprocess.CalledProcessError):
+            nproc = None
+    if not nproc:
+        nproc = len(os.sched_getaffinity(0))
+    return {'nproc': nproc, 'online_cpus': os.cpu_count(), 'affinity_cpus': len(os.sched_getaffinity(0)),
+            'model': _cpu_model()}
 
 
 def _cpu_model():
@@ -159,6 +138,114 @@ def _cpu_model():
     except OSError:
         pass
     return 'unknown'
+
+
+def _timed_passes(once, n_rows, pass_s, passes=3):
+    """Rows per second of `once` (which processes n_rows rows): one warm-up call, then `passes` passes that each
+    repeat it for at least pass_s seconds; the median pass rate and the repetitions per pass."""
+    t0 = time.perf_counter()
+    once()
+    dt = time.perf_counter() - t0
+    reps = max(1, int(np.ceil(pass_s / max(dt, 1e-6))))
+    rates = []
+    for _ in range(passes):
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            once()
+        rates.append(n_rows * reps / (time.perf_counter() - t0))
+    return float(np.median(rates)), reps
+
+
+def cpu_sample_baseline(w, D, K, seed, bound, table_np, grad_np, step_t, pass_s=2.5):
+    """The CPU path of the headline step on this host, at nthreads = nproc, on a bounded sample of its rows.
+
+    Main figure (kind 'reference'): every Adam step is the reference's own compiled cpu_adam (srm2/csrc/srm2_cpu.cpp
+    :37-56, built from the reference's source by oracle/Makefile into oracle/_ref), applied as the reference's
+    exactness test applies it (tests/test_replay.py:19-27): the rows' initial states, then for each log slot k and
+    each logical step t one cpu_adam call on the rows whose k-th entry is at t, then the step's Adam on every row.
+    The initial states come from the oracle's init (the reference's init exists only as a GPU kernel,
+    srm2/gpu_ops.py:26-48).  Extra figure (kind 'port'): the oracle's per-row replay (one pass over each row's
+    entries) + the oracle's cpu_adam, the same arithmetic restated in C with the reference's thread split.
+    The sample: the first n rows of the step (16,384 rows, grown up to the whole step until one call takes 0.5 s);
+    1 warm-up + 3 passes of >= pass_s seconds each; the median pass rate."""
+    from elara_amd import synth
+    from oracle import oracle as O
+    from oracle import ref as REF
+    cpu = host_cpus()
+    th = cpu['nproc']
+    E = REF.cpu()
+    lr, b1, b2, eps = synth.ADAM
+
+    def sample(n):
+        rows, cnt, steps, offs = w.rows[:n], w.cnt[:n], w.steps[:n], w.offs[:n]
+        nlog = int(cnt.sum())
+        return rows, cnt, steps, offs, w.logs[:nlog], np.ascontiguousarray(grad_np[:n])
+
+    res = {}
+    if E is not None:
+        import torch
+        n = min(w.n, 16_384)
+        while True:
+            rows, cnt, steps, offs, logs, g = sample(n)
+            init = torch.from_numpy(O.init_rows(rows, D, seed, bound))
+            groups = []   # (row indices, their gradients, step) in the reference test's order
+            for k in range(K):
+                sel = np.nonzero(cnt > k)[0]
+                sk = steps[sel, k]
+                for t in np.unique(sk).tolist():
+                    idx = sel[sk == t]
+                    groups.append((torch.from_numpy(idx.astype(np.int64)),
+                                   torch.from_numpy(np.ascontiguousarray(logs[offs[idx] + k])), int(t)))
+            all_rows = torch.arange(n, dtype=torch.int64)
+            gt = torch.from_numpy(g)
+
+            def once():
+                st = init.clone()
+                for idx, gk, t in groups:
+                    E.cpu_adam(st, idx, gk, lr, b1, b2, eps, t, th)
+                E.cpu_adam(st, all_rows, gt, lr, b1, b2, eps, step_t, th)
+
+            t0 = time.perf_counter(); once(); dt = time.perf_counter() - t0
+            if dt >= 0.5 or n >= w.n:
+                break
+            n = min(w.n, n * 4)
+        rate, reps = _timed_passes(once, n, pass_s)
+        per_row = (replay_bytes(n, K, D, int(cnt.sum())) + adam_bytes(n, D)) / n
+        res = {'value': rate, 'unit': 'rows/s', 'cores': th, 'kind': 'reference',
+               'sample': f'the first {n} of the {w.n} C2 rows at D={D}: the oracle-initialised states copied in, then '
+                         f'the reference cpu_adam '
+                         f'(oracle/_ref, built from srm2/csrc/srm2_cpu.cpp) per log slot and logical step '
+                         f'({len(groups)} calls) and once more for the step\'s update; {th} threads (nproc); '
+                         f'repeated {reps}x per pass, median of 3 passes after 1 warm-up',
+               'gbs': rate * per_row / 1e9}
+    # the port: one pass per row over its entries (oracle replay) + the oracle's cpu_adam
+    n = min(w.n, 16_384)
+    while True:
+        rows, cnt, steps, offs, logs, g = sample(n)
+        idx = np.arange(n, dtype=np.int64)
+        sc = O.adam_scalars(*synth.ADAM, step_t)
+
+        def once_port():
+            out = O.replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table_np, nthreads=th)
+            O.cpu_adam(out, idx, g, sc, th)
+
+        t0 = time.perf_counter(); once_port(); dt = time.perf_counter() - t0
+        if dt >= 0.5 or n >= w.n:
+            break
+        n = min(w.n, n * 4)
+    rate_p, reps_p = _timed_passes(once_port, n, pass_s)
+    per_row = (replay_bytes(n, K, D, int(cnt.sum())) + adam_bytes(n, D)) / n
+    port = {'value': rate_p, 'unit': 'rows/s', 'cores': th, 'kind': 'port',
+            'sample': f'oracle per-row replay (K=3) + oracle cpu_adam of the first {n} of the {w.n} C2 rows at '
+                      f'D={D}, {th} threads (nproc), repeated {reps_p}x per pass, median of 3 passes after 1 warm-up',
+            'gbs': rate_p * per_row / 1e9}
+    if not res:   # no reference build on this host: the port is the baseline
+        res = port
+    else:
+        res['port'] = port
+    res.update({'nproc': cpu['nproc'], 'host_cpu': cpu['model'], 'online_cpus': cpu['online_cpus'],
+                'affinity_cpus': cpu['affinity_cpus']})
+    return res
 
 
 def headline(args):
@@ -189,6 +276,14 @@ def headline(args):
         gpu_adam(out, slots, grad, *synth.ADAM, step_t)
         if ev: ev[2].record(stream)
 
+    # clock settle: the engine clock leaves its idle level only after 20-30 ms of sustained load, and replay, whose
+    # arithmetic is close to its memory time, follows it (288, 138, 125 us per launch over the first three 25-step
+    # windows, then steady).  Untimed launches of the step's Adam kernel on the step's own buffers load the GPU for
+    # settle_ms before the warm-up, so the warm-up and timed steps run at the steady clock.  Replay itself is not
+    # launched here: its every launch is a warm-up or a timed one, so a trace's average over all of them is the
+    # steady-state figure.
+    out.zero_()
+    settle = _settle(lambda: gpu_adam(out, slots, grad, *synth.ADAM, step_t), args.settle_ms * 1e-3)
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
@@ -221,11 +316,27 @@ def headline(args):
                     'adam': {'ms': adam_ms, 'GBps': ab / (adam_ms * 1e-3) / 1e9, 'bytes': ab,
                              'frac': ab / (adam_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}},
         'step_GBps': (rb + ab) / (elapsed / args.steps) / 1e9,
+        'clock_settle': settle,
     }
     if not args.no_cpu:
-        res['cpu_baseline'] = cpu_sample_baseline(w, D, K, seed, bound, table.t.cpu().numpy(),
-                                                  threads=min(16, os.cpu_count() or 1))
+        res['cpu_baseline'] = cpu_sample_baseline(w, D, K, seed, bound, table.t.cpu().numpy(), grad.cpu().numpy(),
+                                                  step_t)
     return res
+
+
+def _settle(launch, settle_s):
+    """Untimed load before a benchmark: `launch()` in batches of 8, synchronised after each batch, until settle_s
+    seconds have passed.  Returns what was run (launch count and milliseconds)."""
+    import torch
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(8):
+            launch()
+        n += 8
+        torch.cuda.synchronize()
+    return {'kernel': 'row-sparse Adam on the step buffers', 'launches': n,
+            'ms': (time.perf_counter() - t0) * 1e3}
 
 
 def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
@@ -455,6 +566,8 @@ def main():
     ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
+    ap.add_argument('--settle-ms', type=float, default=100.0,
+                    help='headline: untimed load (Adam launches) before the warm-up, so the engine clock is steady')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path (rows would shard by owner, with '
