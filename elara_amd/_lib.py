@@ -46,6 +46,7 @@ SIGNATURES = {
     'elr_unique': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_segment_sum': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'elr_adam_dedup': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_f32p, c_vp, c_i64, c_vp]),
+    'elr_adam_dedup_noalloc': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_f32p, c_vp]),
     'elr_dir_a': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64] + [c_vp] * 9
                   + [c_vp, c_i64, c_vp]),
     'elr_dir_evict': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),

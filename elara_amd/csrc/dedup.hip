@@ -997,3 +997,58 @@ extern "C" int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int
   const int rc = seg_reduce_d<0>(grad, D, S.vals[plan_result_buffer(key_bits)], S, perm, n, out, out_rows, none, st);
   return rc != ELR_OK ? rc : launch_status();
 }
+
+// ---- duplicate-id Adam that allocates nothing ------------------------------------------------------------------
+// elr_adam_dedup with its scratch in a file-scope device array instead of a caller buffer, for callers that cannot
+// allocate device memory (code under graph capture, tight serving loops).  The array (ELR_NOALLOC_SCRATCH_BYTES)
+// exists once per GPU the library runs on, for the life of the process.  In host code `scratch` names only a
+// host-side stand-in; the device address is obtained once per device with hipGetSymbolAddress, with that device
+// current, and only that address is handed to kernels.  Every kernel writes the parts of the scratch it later
+// reads (the hot-segment counter is zeroed by the segment kernel itself), so nothing needs clearing between calls.
+// All calls on one GPU share its array: calls that overlap in time on one GPU (two streams, two host threads) race.
+#include <atomic>
+#include <mutex>
+
+namespace elr {
+constexpr int kNoAllocMaxDevices = 64;
+std::atomic<void*> g_noalloc_ptr[kNoAllocMaxDevices];
+std::mutex g_noalloc_mu;
+}  // namespace elr
+
+static __device__ __align__(256) unsigned char scratch[ELR_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` on the current device (resolved on the first call per device).
+static int noalloc_scratch(void** out) {
+  using namespace elr;
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kNoAllocMaxDevices) return ELR_EUNSUPPORTED;
+  void* p = g_noalloc_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> g(g_noalloc_mu);
+    p = g_noalloc_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!p) return ELR_EINVAL;
+      g_noalloc_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return ELR_OK;
+}
+
+extern "C" int elr_adam_dedup_noalloc(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n,
+                                      int64_t D, const float sc[8], void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || D < 1 || C < 0 || !sc) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!state || !ids || !grad) return ELR_EINVAL;
+  if (D > 512) return ELR_EUNSUPPORTED;
+  if (dedup_scratch_bytes(n, D, nullptr, nullptr) > (int64_t)ELR_NOALLOC_SCRATCH_BYTES) return ELR_ECAPACITY;
+  void* base = nullptr;
+  const int rc = noalloc_scratch(&base);
+  if (rc != ELR_OK) return rc;
+  return elr_adam_dedup(state, C, ids, grad, n, D, sc, base, (int64_t)ELR_NOALLOC_SCRATCH_BYTES, stream);
+}

@@ -8,7 +8,8 @@
  *     needs no HIP include) and is asynchronous on that stream; nothing uses the legacy default stream.
  *   - Return value: ELR_OK (0) on success, a negative ELR_E* code for an invalid argument detected on the
  *     host, or a positive hipError_t from the launch.  elr_error_string() describes a code.
- *   - The library keeps no mutable global state (re-entrant; callable from several host threads).
+ *   - The library keeps no mutable global state (re-entrant; callable from several host threads), except the
+ *     per-device scratch array of elr_adam_dedup_noalloc and the cache of its device addresses.
  *   - Device-side index checks: a row whose index (slot, log offset, step) is out of range is skipped and left
  *     unwritten instead of faulting.  The reference leaves such inputs undefined; callers must not rely on it.
  *
@@ -184,6 +185,18 @@ int elr_segment_sum(const float* grad, const int64_t* idx, int64_t n, int64_t D,
  * Each unique id gets one Adam step (scalars sc) with the sum of its gradients.  D <= 512. */
 int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
                    const float sc[8], void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Duplicate-id row-sparse Adam that allocates nothing (no counterpart in the reference; for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments and results as elr_adam_dedup, without the scratch arguments: the scratch is a device array of
+ * ELR_NOALLOC_SCRATCH_BYTES inside the library, one per GPU it runs on, held until the process ends.  Calls with
+ * elr_dedup_scratch_bytes(n, D) > ELR_NOALLOC_SCRATCH_BYTES return ELR_ECAPACITY before any launch (at D = 128:
+ * n up to about 589,000 occurrences).  No hipMalloc / hipFree or allocating library call is made.  Every call on
+ * one GPU uses that GPU's array: calls that overlap in time on one GPU (two streams or threads) race.  The device
+ * is the current one (hipGetDevice); `stream` must belong to it. */
+#define ELR_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int elr_adam_dedup_noalloc(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
+                           const float sc[8], void* stream);
 
 /* Dedup plan (no counterpart in the reference; the reference sorts each batch twice, in torch.unique and in the
  * embedding backward): elr_dedup_plan is elr_unique that keeps its sort -- sorted positions, segment starts, first
