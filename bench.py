@@ -7,16 +7,17 @@ executor's path for logged rows (srm2/elara.py:485, 514).  Inputs are resident i
 value = rows per second over the K timed steps.
 
 roofline: the replay kernel -- algorithmic bytes per launch / its mean duration from HIP events (created with
-hipEventDisableSystemFence: timing only, no cache flush) recorded on the launch stream around every 4th timed
-step's launches; peak 8 TB/s.  cpu_baseline: the same step on this host's cores at nthreads = nproc, with every Adam
-step done by the reference's own compiled cpu_adam (oracle/_ref), on a bounded sample of the rows; the oracle's C
-port of the whole step is reported beside it.
+hipEventDisableSystemFence: timing only, no cache flush) recorded on the launch stream around the launches of every
+2nd timed step from step 1 on; peak 8 TB/s.  cpu_baseline: the same step on this host's cores at nthreads = nproc,
+with every Adam step done by the reference's own compiled cpu_adam (oracle/_ref), on a bounded sample of the rows;
+the oracle's C port of the whole step is reported beside it.
 
 Clock settle and warm-up: the first 20-30 ms of sustained load run at a lower engine clock (measured on the headline
 step: replay 288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound,
-140 us throughout).  Before the W warm-up steps, the headline runs --settle-ms (default 100) of untimed Adam launches
-on the step's own buffers, so the W warm-up and K timed steps all run at the steady clock, whatever W is; the line
-reports the settle under `clock_settle`.  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
+140 us throughout).  Before the W warm-up steps, the headline runs --settle-ms (default 100) of untimed steps, so the
+W warm-up and K timed steps all run at the steady clock, whatever W is; the line reports it under `clock_settle`.
+The timed region starts 2 ms after the synchronisation that precedes it (a launch right after a synchronisation
+overlaps write-backs that synchronisation started).  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode headline|copy] [--no-cpu]
 """
@@ -34,7 +35,8 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = 'sparse-Adam+replay rows/s at d=128; achieved HBM GB/s vs ~8 TB/s peak'
 HBM_PEAK_GBS = 8000.0
-EV_EVERY = 4   # headline: HIP events on every 4th timed step
+EV_EVERY = 2   # headline: HIP events on every 2nd timed step (steps 1, 3, 5, ...)
+POST_SYNC_IDLE_S = 0.002   # headline: host idle between the synchronisation and the timed region
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000   # hipEventDisableSystemFence, hip_runtime_api.h
 _HIP = None
 
@@ -278,18 +280,22 @@ def headline(args):
 
     # clock settle: the engine clock leaves its idle level only after 20-30 ms of sustained load, and replay, whose
     # arithmetic is close to its memory time, follows it (288, 138, 125 us per launch over the first three 25-step
-    # windows, then steady).  Untimed launches of the step's Adam kernel on the step's own buffers load the GPU for
-    # settle_ms before the warm-up, so the warm-up and timed steps run at the steady clock.  Replay itself is not
-    # launched here: its every launch is a warm-up or a timed one, so a trace's average over all of them is the
-    # steady-state figure.
+    # windows, then steady).  settle_ms of untimed headline steps run before the W warm-up steps, so the warm-up and
+    # timed steps run at the steady clock whatever W is.  (A memory-bound load does not do it: after 100 ms of Adam
+    # launches alone, replay still ran 125 us per launch against 119-121 after the same time of whole steps.)
     out.zero_()
-    settle = _settle(lambda: gpu_adam(out, slots, grad, *synth.ADAM, step_t), args.settle_ms * 1e-3)
+    settle = _settle(one_step, args.settle_ms * 1e-3, 'the headline step (replay + Adam) on its own buffers')
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
-    # kernel durations from HIP events on every EV_EVERY-th timed step: each marker costs the step a few us
-    # (three per step: 0.268 against 0.258 ms per step), so sampling keeps the instrument out of `value`
-    evs = [[HipEvent() for _ in range(3)] if i % EV_EVERY == 0 else None for i in range(args.steps)]
+    # the host synchronisation above starts write-backs the first launch after it would overlap: launched at once,
+    # that replay took 140-190 us, launched 0.1-10 ms later 129-132 us (steady state: 118-124).  The timed region
+    # starts after POST_SYNC_IDLE_S.
+    time.sleep(POST_SYNC_IDLE_S)
+    # kernel durations from HIP events on every EV_EVERY-th timed step, from step 1 on (the first timed launch is
+    # the one after the synchronisation): each marker costs the step a few us (three per step: 0.268 against 0.258
+    # ms per step), so sampling keeps the instrument out of `value`
+    evs = [[HipEvent() for _ in range(3)] if i % EV_EVERY == 1 else None for i in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -324,9 +330,9 @@ def headline(args):
     return res
 
 
-def _settle(launch, settle_s):
+def _settle(launch, settle_s, what):
     """Untimed load before a benchmark: `launch()` in batches of 8, synchronised after each batch, until settle_s
-    seconds have passed.  Returns what was run (launch count and milliseconds)."""
+    seconds have passed.  Returns what was run (`what`, call count and milliseconds)."""
     import torch
     n = 0
     t0 = time.perf_counter()
@@ -335,8 +341,7 @@ def _settle(launch, settle_s):
             launch()
         n += 8
         torch.cuda.synchronize()
-    return {'kernel': 'row-sparse Adam on the step buffers', 'launches': n,
-            'ms': (time.perf_counter() - t0) * 1e3}
+    return {'work': what, 'calls': n, 'ms': (time.perf_counter() - t0) * 1e3}
 
 
 def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
@@ -567,7 +572,7 @@ def main():
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--settle-ms', type=float, default=100.0,
-                    help='headline: untimed load (Adam launches) before the warm-up, so the engine clock is steady')
+                    help='headline: untimed steps before the warm-up, so the engine clock is steady')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU only: this build has no multi-GPU path (rows would shard by owner, with '

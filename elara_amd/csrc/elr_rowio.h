@@ -108,6 +108,65 @@ __device__ __forceinline__ void frag_adam(RowFrag<VPL>& w, RowFrag<VPL>& m, RowF
   }
 }
 
+// Range check of the Adam cores, deferred: per lane, the smallest and largest vh and |num| of every element and
+// step the fast path computed.  The cores' operand ranges hold for all of them exactly when vmin >= 2^-96,
+// vmax < inf, nmin >= 2^-60 and nmax < 2^40 (min / max ignore a NaN operand; a NaN vh or num gives NaN through the
+// cores as through the general sequences, so a NaN needs no recompute).  Two min3 / max3 instructions per two
+// elements instead of four compares per element.
+struct RangeAcc {
+  float vmin, vmax, nmin, nmax;
+};
+__device__ __forceinline__ RangeAcc range_acc_init() {
+  return RangeAcc{__builtin_inff(), 0.0f, __builtin_inff(), 0.0f};
+}
+__device__ __forceinline__ bool range_acc_ok(const RangeAcc& a) {
+  return a.vmin >= 0x1.0p-96f && a.vmax < __builtin_inff() && a.nmin >= 0x1.0p-60f && a.nmax < 0x1.0p40f;
+}
+
+// One Adam step of the lane's fragment on the fast path only (the cores sqrt_core and div_core), with the operand
+// ranges folded into acc; the caller recomputes the row on the general path when range_acc_ok(acc) fails on some
+// lane.
+template <int VPL>
+__device__ __forceinline__ void frag_adam_fast(RowFrag<VPL>& w, RowFrag<VPL>& m, RowFrag<VPL>& v,
+                                               const RowFrag<VPL>& g, const AdamScalars& s, RangeAcc& acc) {
+  float vh[VPL], num[VPL];
+#pragma unroll
+  for (int e = 0; e < VPL; ++e) {
+    float mj = s.b1 * m.v[e];
+    const float t1 = s.omb1 * g.v[e];
+    mj = mj + t1;
+    float vj = s.b2 * v.v[e];
+    float t2 = s.omb2 * g.v[e];
+    t2 = t2 * g.v[e];
+    vj = vj + t2;
+    m.v[e] = mj;
+    v.v[e] = vj;
+    const float mh = div_by_recip(mj, s.r1);
+    vh[e] = div_by_recip(vj, s.r2);
+    num[e] = s.lr * mh;
+  }
+#pragma unroll
+  for (int e = 0; e < VPL; e += 2) {
+    if (e + 1 < VPL) {
+      acc.vmin = __builtin_fminf(acc.vmin, __builtin_fminf(vh[e], vh[e + 1]));
+      acc.vmax = __builtin_fmaxf(acc.vmax, __builtin_fmaxf(vh[e], vh[e + 1]));
+      acc.nmin = __builtin_fminf(acc.nmin, __builtin_fminf(__builtin_fabsf(num[e]), __builtin_fabsf(num[e + 1])));
+      acc.nmax = __builtin_fmaxf(acc.nmax, __builtin_fmaxf(__builtin_fabsf(num[e]), __builtin_fabsf(num[e + 1])));
+    } else {
+      acc.vmin = __builtin_fminf(acc.vmin, vh[e]);
+      acc.vmax = __builtin_fmaxf(acc.vmax, vh[e]);
+      acc.nmin = __builtin_fminf(acc.nmin, __builtin_fabsf(num[e]));
+      acc.nmax = __builtin_fmaxf(acc.nmax, __builtin_fabsf(num[e]));
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < VPL; ++e) {
+    float den = sqrt_core(vh[e]);
+    den = den + s.eps;
+    w.v[e] = w.v[e] - div_core(num[e], den);
+  }
+}
+
 // Initial weights of the lane's fragment of row r (D = 64*VPL): elements j = lane*VPL + e.
 template <int VPL>
 __device__ __forceinline__ RowFrag<VPL> frag_init(int64_t r, int lane, uint32_t seed, float bound) {

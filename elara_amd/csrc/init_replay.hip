@@ -226,9 +226,25 @@ __global__ __launch_bounds__(256) void k_replay_wpr(float* __restrict__ out, con
   for (int u = 0; u < U; ++u) {
     if (c[u] < 0) continue;
     RowFrag<VPL> w = frag_init<VPL>(r[u], lane, seed, bound), m = frag_zero<VPL>(), v = frag_zero<VPL>();
+    // the cores for every step, their operand ranges checked once per row (deferred: a min / max per lane, one
+    // vote per row); a row that fails the check is recomputed on the general path, which gives the same bits
+    RangeAcc acc = range_acc_init();
+    bool eps_all = true;
 #pragma unroll
     for (int k = 0; k < K; ++k)
-      if (k < c[u]) frag_adam<VPL>(w, m, v, g[u][k], table_scalars(table, recip, st[u][k]));
+      if (k < c[u]) {
+        const AdamScalars sc = table_scalars(table, recip, st[u][k]);
+        eps_all = eps_all && eps_ok(sc.eps);
+        frag_adam_fast<VPL>(w, m, v, g[u][k], sc, acc);
+      }
+    if (!(eps_all && wave_all(range_acc_ok(acc)))) {
+      w = frag_init<VPL>(r[u], lane, seed, bound);
+      m = frag_zero<VPL>();
+      v = frag_zero<VPL>();
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        if (k < c[u]) frag_adam<VPL>(w, m, v, g[u][k], table_scalars(table, recip, st[u][k]));
+    }
     float* dst = out + (i0 + u) * 3 * D + lane * VPL;
     frag_store<VPL>(dst, w);
     frag_store<VPL>(dst + D, m);
