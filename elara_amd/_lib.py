@@ -83,7 +83,7 @@ class PlanIn(ctypes.Structure):
                 ('slot_of', c_vp), ('last_seen', c_vp), ('code', c_vp), ('kthr', c_vp), ('toff', c_vp), ('T', c_i64),
                 ('dyn', c_vp), ('nd', c_i64), ('slot_row', c_vp), ('mat_top', c_vp), ('log_top', c_vp),
                 ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp), ('R', c_i64),
-                ('next_bits', c_vp), ('next_mask', c_u32)]
+                ('next_bits', c_vp), ('next_mask', c_u32), ('carry', ctypes.c_int), ('live', c_vp)]
 
 
 class PlanOut(ctypes.Structure):

@@ -1,13 +1,15 @@
 // Planner classification of one ELARA step (srm2/elara.py:214-267, the part before the class counts go to the host):
 // three launches in place of the reference planner's chain of elementwise torch ops, bincount and stable argsorts.
 //
-//   unique rows u[i] of the batch: slot sl = slot_of[u], hit = sl >= 0, admit = !hit && last_seen[u] > s,
-//     in_next = u appears in one of the next batches, c = code[u], app = c < kthr[table_of(u)], and the class
+//   unique rows u[i] of the batch: slot sl = slot_of[u], hit = sl >= 0, in_next = u appears in one of the next
+//     batches, admit = !hit && (ttl: last_seen[u] > s; carry: in_next), c = code[u], app = c < kthr[table_of(u)],
+//     and the class
 //       hit -> HIT;  c == 0 (N) -> admit ? NADM : app ? NAPP : NCMP;  1 <= c <= K (L) -> LADM / LAPP / LCMP;
 //       otherwise (M) -> admit ? FADM : want_T ? FNADM : S                              (elara.py:244-258)
 //   dynamic pool slots d = dyn[j] (row r = slot_row[d]): protected when r appears in one of the next batches
-//     (the slot holds a row the pipeline needs, elara.py:227-229), expired when last_seen[r] <= s (the row's TTL is
-//     over, elara.py:231-233); class 0 = expired and unprotected, 1 = unprotected (preemptible), 2 = protected.
+//     (the slot holds a row the pipeline needs, elara.py:227-229), expired when last_seen[r] <= s (ttl: the row's
+//     TTL is over) or always (carry) (elara.py:231-233); class 0 = expired and unprotected, 1 = unprotected
+//     (preemptible), 2 = protected.
 //
 // Outputs: the positions of u sorted stably by class rank (`order`, and its inverse `rank`), the dynamic slots
 // partitioned stably by class ([class 0 | class 1 | class 2] and [class 0 | classes 1, 2 in dyn order], so that the
@@ -81,8 +83,8 @@ __device__ __forceinline__ RowClass classify_row(const elr_plan_in& p, int64_t r
   }
   o.sl = p.slot_of[r];
   const bool hit = o.sl >= 0;
-  const bool admit = !hit && (int64_t)p.last_seen[r] > p.s;
   const bool nxt = in_next(p, r);
+  const bool admit = !hit && (p.carry ? nxt : (int64_t)p.last_seen[r] > p.s);
   o.c = p.code[r];
   const int64_t t = table_of(p.toff, p.T, r);
   const int thr = (t >= 0 && t < p.T) ? (int)p.kthr[t] : 0;
@@ -104,7 +106,7 @@ __device__ __forceinline__ int dyn_class(const elr_plan_in& p, int64_t d) {
   if (r >= 0 && !row_ok(p, r)) return 1;   // a slot holding an out-of-range row: unprotected, not expired
   const bool prot = r >= 0 && in_next(p, r);
   if (prot) return 2;
-  const bool expired = r < 0 || (int64_t)p.last_seen[r] <= p.s;
+  const bool expired = p.carry || r < 0 || (int64_t)p.last_seen[r] <= p.s;
   return expired ? 0 : 1;
 }
 
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_pla
     if (c == 0) {
       o.counts[13] = p.mat_top ? *p.mat_top : 0;
       o.counts[14] = p.log_top ? *p.log_top : 0;
-      o.counts[15] = 0;
+      o.counts[15] = p.live ? *p.live : 0;
     }
   }
 }

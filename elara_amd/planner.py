@@ -16,7 +16,7 @@ I8, I32, I64 = torch.int8, torch.int32, torch.int64
 C_HIT, C_NADM, C_NAPP, C_NCMP, C_LADM, C_LAPP, C_LCMP, C_FADM, C_FNADM, C_S = range(10)
 F_HIT, F_N, F_L, F_APP, F_ADMIT, F_NEXT = 1, 2, 4, 8, 16, 32
 # counts[16]: 10 class counts, then these
-CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP = 10, 11, 12, 13, 14
+CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP, CNT_LIVE = 10, 11, 12, 13, 14, 15
 
 PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts u_ord c_ord sl_ord L_row L_cnt loc_ord')
 
@@ -26,7 +26,7 @@ def _dev_i64(t, dev):
 
 
 def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
-                  loc=None, R=0, next_bits=None, next_mask=0):
+                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -40,7 +40,11 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
 
     next_bits (int32 [R], with R > 0) and next_mask: the caller's ring of loaded batches (bit t % 32 of
     next_bits[r] set while the batch of step t holds row r; see rows.mark_rows).  Membership in the next batches is
-    then one load per row instead of searches of u_nexts, and bit s % 32 of u's rows is cleared."""
+    then one load per row instead of searches of u_nexts, and bit s % 32 of u's rows is cleared.
+
+    carry: the 'carry' residency (srm2/elara.py:221, 231-233): a missing row is admitted when it appears in the next
+    batches, and every unprotected dynamic slot is expired; otherwise 'ttl'.  live (int64 [1], optional): the live
+    log-entry counter, copied into counts[15] for the host."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -50,7 +54,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
         raise RuntimeError('plan_classify: at most 4 next batches')
     for t, dt, name in ((slot_of, I32, 'slot_of'), (last_seen, I32, 'last_seen'), (code, I8, 'code'),
                         (kthr, I8, 'kthr'), (toff, I64, 'toff'), (slot_row, I64, 'slot_row'),
-                        (mat_top, I64, 'mat_top'), (log_top, I64, 'log_top')):
+                        (mat_top, I64, 'mat_top'), (log_top, I64, 'log_top')) + (
+                            ((live, I64, 'live'),) if live is not None else ()):
         if t.dtype != dt or t.device != dev or not t.is_contiguous():
             raise RuntimeError(f'plan_classify: {name} must be a contiguous {dt} tensor on {dev}')
     if loc is not None and (loc.dtype != I32 or loc.device != dev or not loc.is_contiguous()):
@@ -79,6 +84,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     pin.s, pin.K, pin.want_t = int(s), int(K), int(bool(want_t))
     pin.loc = loc.data_ptr() if loc is not None else None
     pin.R = int(R)
+    pin.carry = int(bool(carry))
+    pin.live = live.data_ptr() if live is not None else None
     if next_bits is not None:
         if not (next_bits.dtype == I32 and next_bits.device == dev and next_bits.is_contiguous()
                 and next_bits.numel() >= R > 0):

@@ -35,7 +35,7 @@ from .dedup import segment_sum_plan, unique_plan, unique_plan_async
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
-from .planner import (CNT_EXP, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
+from .planner import (CNT_EXP, CNT_LIVE, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
                       plan_admit, plan_classify)
 from .rows import copy_rows, glog_put, glog_take, mark_rows
 
@@ -132,8 +132,8 @@ class HipBackend:
             self.D, es.K, pool, es.pool.shape[0], mat, es.mat.shape[0], logs, es.logs.shape[0], glog,
             es.glog.shape[0], _p64(G, b[-1] * self.D, torch.float32), _p64(p.work, (b[R_S] - b[R_NADM]) * 3 * self.D,
                                                                         torch.float32),
-            (_lib.c_i64 * 11)(*b), p.s, *self.hp, int(bool(es.evl)),
-            _p64(p.hit_slot, nh), _p64(p.hrec_dyn, nh) if es.evl else 0, _p64(p.hrec_j, nh) if es.evl else 0,
+            (_lib.c_i64 * 11)(*b), p.s, *self.hp, int(bool(p.evl)),
+            _p64(p.hit_slot, nh), _p64(p.hrec_dyn, nh) if p.evl else 0, _p64(p.hrec_j, nh) if p.evl else 0,
             nev, _p64(p.ev_slot, nev), _p64(p.evf_slots, nev), _p64(p.evl_ids, nev * es.K), _p64(p.ev_dyn, nev),
             _p64(p.adm_slots, b[R_FADM + 1] - b[R_NADM]), p.lazy_n, es.n0,
             _p64(p.c_slots, b[R_LCMP + 1] - b[R_NCMP]), _p64(p.a_ids, b[R_LAPP + 1] - b[R_NAPP]),
@@ -157,25 +157,52 @@ class Plan:
     pass
 
 
+class HostBudgetExceeded(RuntimeError):
+    """The capacity-tier arenas would exceed the enforced host budget (srm2/store.py:26-27): raised by the plan of
+    the step whose allocations cross it, after that plan's directory calls and before its update."""
+
+
+CHUNK = 64 << 20   # fault granularity of the capacity-tier accounting, in bytes (srm2/store.py:23)
+
+
 class ElaraStep:
     """Planner + executor of ELARA over HBM-resident arenas.
 
     toff: first row of each table (int64 [T]); R total rows; D width; C pool slots; static_rows: pinned hot rows
     (the `static` base, srm2/train.py:262-270) or None; K = Kmax; kthr: materialisation threshold per table (or one
-    int); evl: residency-aware representation (evicted rows may return to L); L: TTL lookahead; depth: number of
-    batches u_nexts covers plus one (srm2/train.py:366); st_mode 'T' (transient full-state updates on the GPU) or
-    'S' (materialised cold rows updated in the MAT arena); log_cap / mat_cap: arena capacities in rows;
-    host_arenas: keep the MAT and log arenas in pinned host memory (the capacity tier, srm2/elara.py:40-103).
+    int); evl: the residency-aware representation (evicted rows may return to L; srm2/elara.py:110-116): 0 or False
+    off, 1 or True on, 2 gated by memory pressure (switched on, once, by the first plan that finds the arenas'
+    used bytes (3 mat_top + live) * D * 4 at or above evl_gate_frac of host_budget; never on without a budget);
+    dyn: dynamic residency 'ttl' (admitted when the row recurs within the lookahead, kept while it does) or
+    'carry' (admitted when it appears in the next depth-1 batches, evicted as soon as it does not;
+    srm2/elara.py:221, 231-233); L: TTL lookahead; depth: number of batches u_nexts covers plus one
+    (srm2/train.py:366); st_mode 'T' (transient full-state updates on the GPU) or 'S' (materialised cold rows
+    updated in the MAT arena); log_cap / mat_cap: arena capacities in rows (row log_cap of the log arena and row
+    mat_cap - 1 of the MAT arena are trash rows); host_arenas: keep the MAT and log arenas in pinned host memory
+    (the capacity tier, srm2/elara.py:40-103); host_budget: bytes the arenas may hold, accounted as the
+    reference's ArenaStore does (faulted in chunks of budget_chunk bytes up to each arena's top; 0: no budget),
+    HostBudgetExceeded when a step would pass it (srm2/elara.py:63-81).
     """
 
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
-                 backend=None, host_arenas=False):
+                 backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK):
         d = torch.device(device)
         self.d, self.R, self.D, self.C, self.K, self.L, self.depth = d, R, D, C, K, L, depth
         self.MAT = K + 1
         self.st_mode = st_mode
-        self.evl = bool(evl)
+        if dyn not in ('ttl', 'carry') or st_mode not in ('S', 'T'):
+            raise ValueError(f'dyn must be ttl or carry and st_mode S or T (got {dyn!r}, {st_mode!r})')
+        self.dyn = dyn
+        self.evl_mode = int(evl)
+        if self.evl_mode not in (0, 1, 2):
+            raise ValueError(f'evl must be 0, 1 or 2 (got {evl!r})')
+        self.evl = self.evl_mode == 1
+        self.evl_gate_frac = float(evl_gate_frac)
+        self.host_budget = int(host_budget)
+        self.budget_chunk = int(budget_chunk)
+        self.faulted = {'mat': 0, 'log': 0}   # arena rows the budget accounting holds (ArenaStore.faulted)
+        self._observed = 0   # highest logical step whose batch has been observed (the lookahead)
         self.hp = hp
         self.be = backend or HipBackend(D, seed, bound, hp, max_step, d)
         self.toff = torch.as_tensor(toff, dtype=I64).to(d)
@@ -240,7 +267,7 @@ class ElaraStep:
         self._link_pending = []
         self.link_blocks = 32   # blocks per launch of the link part (measured best of 16-128 at C5 with host arenas)
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
-                                     'compactions', 'appends', 'syncs')}
+                                     'compactions', 'appends', 'syncs', 'barriers')}
         self._deferred = []
         self._pin = None
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
@@ -263,24 +290,25 @@ class ElaraStep:
             raise RuntimeError(f'arena capacity exceeded (MAT {mt}/{self.mat_cap - 1}, logs {lt}/{self.log_cap})')
 
     def _wait_link(self, due):
-        """Make the current stream wait for the pending link-stream updates (s, event, overflowed) for which
-        due(s, overflowed) holds."""
+        """Make the current stream wait for the pending link-stream updates (s, event, link_next) for which
+        due(s, link_next) holds (link_next: the plan's flag that the next step's rows may be among them)."""
         keep = []
         cur = torch.cuda.current_stream(self.d) if self._link_pending else None
-        for s_ev, ev, ovf in self._link_pending:
-            if due(s_ev, ovf):
+        for s_ev, ev, nxt in self._link_pending:
+            if due(s_ev, nxt):
                 cur.wait_event(ev)
             else:
-                keep.append((s_ev, ev, ovf))
+                keep.append((s_ev, ev, nxt))
         self._link_pending = keep
 
     def join_link(self):
         """Make the current stream wait for every pending link-stream update (before reading the arenas)."""
-        self._wait_link(lambda s_ev, ovf: True)
+        self._wait_link(lambda s_ev, nxt: True)
 
     def observe(self, step, u, n_dev=None):
         """Record that rows u appear at logical step `step` (the TTL lookahead, srm2/elara.py:160-161); with n_dev
         (a device count) only the first n_dev rows of u, without a synchronisation."""
+        self._observed = max(self._observed, int(step))
         bit = 1 << (step % 32)
         if n_dev is None:
             self.last_seen[u] = step
@@ -357,14 +385,20 @@ class ElaraStep:
                         next_mask=sum(1 << ((s + k) % 32) for k in range(1, self.depth)))
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
-                                   self.st_mode == 'T', self.loc, self.R, **ring)
+                                   self.st_mode == 'T', self.loc, self.R, carry=self.dyn == 'carry', live=self.live,
+                                   **ring)
         finish = self._host_list_async(pc.counts)
         G = self.be.segsum(g_occ, dplan, n, pc.rank) if g_occ is not None else None
         vals = finish()
         counts = vals[:10]
         n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]
-        if mat_top > self.mat_cap - 1 or log_top > self.log_cap:
-            raise RuntimeError(f'arena capacity exceeded (MAT {mat_top}/{self.mat_cap}, logs {log_top}/{self.log_cap})')
+        live = vals[CNT_LIVE]
+        # memory-pressure gate of the residency-aware representation (srm2/elara.py:212-213, 423-425): the arenas'
+        # used bytes as the previous step left them against the budget; sticky once on
+        if (self.evl_mode == 2 and not self.evl and self.host_budget > 0
+                and (mat_top * 3 + live) * self.D * 4 >= self.evl_gate_frac * self.host_budget):
+            self.evl = True
+            self.stats['evl_on_step'] = s
         sl, c, order = pc.sl, pc.c, pc.order
         n_adm = counts[C_NADM] + counts[C_LADM] + counts[C_FADM]
         nd = self.dyn_slots.numel()
@@ -380,6 +414,7 @@ class ElaraStep:
         rank = pc.rank
         u_ord, c_ord, sl_ord, L_row, L_cnt, loc_ord = pc.u_ord, pc.c_ord, pc.sl_ord, pc.L_row, pc.L_cnt, pc.loc_ord
         overflowed = need > 0
+        barrier = False
         if overflowed:   # overflow: un-admit (non-carry first) and recount
             admit = (pc.flags & F_ADMIT) != 0
             in_next = (pc.flags & F_NEXT) != 0
@@ -390,7 +425,10 @@ class ElaraStep:
             self.stats['overflow'] += need
             n_adm -= need
             cls = classify_from_flags(pc.flags, admit, self.st_mode == 'T')
-            counts = self._host(*torch.bincount(cls.long(), minlength=10))
+            # with the class counts: how many of the dropped rows recur in the next batches (carry rows) -- the
+            # reference's exactness barrier (srm2/elara.py:252-257)
+            *counts, n_carry_drop = self._host(*torch.bincount(cls.long(), minlength=10), in_next[drop].sum())
+            barrier = n_carry_drop > 0
             order, rank = rank_order(cls)
             u_ord, c_ord, sl_ord, L_row = u[order], c[order].long(), sl[order].long(), None
             G = None   # the rows' order changed: the segment sum is redone in the new order
@@ -404,6 +442,12 @@ class ElaraStep:
         p.s, p.u, p.n, p.b, p.order, p.rank = s, u, n, b, order, rank
         p.G = G
         p.overflowed = overflowed
+        p.barrier = barrier
+        # the next step's assembly waits for this step's writes into host arenas when a row of the next batch may be
+        # among them: after an overflow (an un-admitted row), or when the next batch was not observed before this
+        # plan (its rows were then not admitted for it)
+        p.link_next = overflowed or self._observed <= s
+        p.evl = self.evl
         p.counts = counts
         p.u_ord = u_ord
         p.hit_slot = sl_ord[b[R_HIT]:b[R_HIT + 1]]
@@ -416,11 +460,20 @@ class ElaraStep:
         else:
             p.L_row, p.L_cnt = L_row[:nLa + nLp + nLc], L_cnt[:nLa + nLp + nLc]
         p.nL = (nLa, nLp, nLc)
+        nev = ev_slot.numel()
+        # the step's allocations at most: a MAT slot per eviction and compaction, a log entry per append and K per
+        # eviction, the latter from the free stack first (n_lfree = log_top - live).  Raised here, before any
+        # directory call, when that could pass an arena's capacity; with a host budget, the exact tops are read
+        # after the directory calls whenever the bound could fault a new chunk (budget_account).
+        mt_hi = mat_top + nev + nNc + nLc
+        lt_hi = log_top + max(0, nev * K + nNp + nLp - (log_top - live))
+        if mt_hi > self.mat_cap - 1 or lt_hi > self.log_cap:
+            raise RuntimeError(f'arena capacity: step {s} may allocate up to MAT row {mt_hi} (capacity '
+                               f'{self.mat_cap - 1}) and log entry {lt_hi} (capacity {self.log_cap})')
         st, pv = self.state_list(), self.params()
         (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots,
          p.ev_dyn) = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s)
         p.ev_slot = ev_slot
-        nev = ev_slot.numel()
         # admissions (srm2/elara.py:345-367): admitted N, L, F rows take slots from the free stack's top
         pool_free = torch.cat([self.free, ev_slot])
         nf = self.n_free + nev
@@ -451,14 +504,48 @@ class ElaraStep:
         st_['S'] += counts[C_S]
         st_['compactions'] += nNc + nLc
         st_['appends'] += nNp + nLp
+        st_['barriers'] += int(barrier)
+        if self.host_budget and (mt_hi > self.faulted['mat'] or lt_hi > self.faulted['log']):
+            self.budget_account(*self._host(self.mat_top, self.log_top))
         return p
+
+    def budget_account(self, mat_top, log_top):
+        """Fault the arenas' accounting up to the tops a step left (ArenaStore.fault, srm2/elara.py:63-81, as the
+        update worker calls it, srm2/elara.py:555-557): each arena is held in steps of budget_chunk bytes (a fault
+        takes at least one step, at most the arena's capacity), MAT records 12 * D bytes, log entries 4 * D.
+        HostBudgetExceeded if the held bytes would pass host_budget."""
+        for which, top in (('mat', mat_top), ('log', log_top)):
+            rec = (3 if which == 'mat' else 1) * self.D * 4
+            step = max(1, self.budget_chunk // rec)
+            cap = self.mat_cap - 1 if which == 'mat' else self.log_cap
+            cur = self.faulted[which]
+            if top <= cur:
+                continue
+            new = min(cap, max(top, cur + step))
+            if self.host_budget and self.resident_bytes() + (new - cur) * rec > self.host_budget:
+                raise HostBudgetExceeded(f'arena store would exceed host budget {self.host_budget / 2**30:.3f} GiB '
+                                         f'(mat rows {mat_top}, log entries {log_top})')
+            self.faulted[which] = new
+
+    def resident_bytes(self):
+        """Bytes the budget accounting holds (ArenaStore.resident_bytes, srm2/elara.py:60-61)."""
+        return self.faulted['mat'] * 12 * self.D + self.faulted['log'] * 4 * self.D
+
+    def footprint(self):
+        """The arenas' footprint as the reference reports it (ArenaStore.footprint, srm2/elara.py:95-103); one
+        host synchronisation."""
+        mt, lt, live = self._host(self.mat_top, self.log_top, self.live)
+        D = self.D
+        return {'store': 'elara_arena', 'mat_rows': mt, 'live_log_entries': live, 'log_arena_entries': lt,
+                'store_bytes': mt * 3 * D * 4 + live * D * 4, 'mat_bytes': mt * 3 * D * 4, 'log_bytes': live * D * 4,
+                'index_bytes': 0, 'resident_bytes': self.resident_bytes()}
 
     # ---- assemble (srm2/elara.py:471-489): full states of the non-resident rows, one fused launch ----
     def assemble(self, p):
         """Work array [b[R_S] - b[R_NADM], 3, D] in class-rank order: admitted N / L / F, appended N / L, compacted
         N / L and transient F rows -- N rows by counter-hash init, L rows by replay of their log entries, F rows
         from the MAT arena."""
-        self._wait_link(lambda s_ev, ovf: s_ev <= p.s - 2 or (s_ev == p.s - 1 and ovf))
+        self._wait_link(lambda s_ev, nxt: s_ev <= p.s - 2 or (s_ev == p.s - 1 and nxt))
         b = p.b
         w0 = b[R_NADM]
         nLa, nLp, _ = p.nL
@@ -486,7 +573,7 @@ class ElaraStep:
             for t in (p.work, G, p.c_slots, p.a_ids, p.FN_slot, p.S_slot):   # kept until the link stream is done
                 if t is not None and t.numel():
                     t.record_stream(self._link)
-            self._link_pending.append((p.s, ev, p.overflowed))
+            self._link_pending.append((p.s, ev, p.link_next))
             return
         be, s, b = self.be, p.s, p.b
         W, w0 = p.work, b[R_NADM]
@@ -494,7 +581,7 @@ class ElaraStep:
         rw = lambda r0, r1: W[b[r0] - w0:b[r1 + 1] - w0]  # noqa: E731
         if b[R_HIT + 1] > b[R_HIT]:
             gh = rg(R_HIT, R_HIT)
-            if self.evl:
+            if p.evl:
                 be.glog_put(self.glog, p.hrec_dyn, p.hrec_j, gh)
             be.adam(self.pool, p.hit_slot, gh, s)
         if p.ev_slot.numel():
@@ -510,7 +597,7 @@ class ElaraStep:
             be.adam_dense(rw(R_NCMP, R_FN), rg(R_NCMP, R_FN), s)
         if p.adm_slots.numel():
             be.copy_rows(self.pool, p.adm_slots, rw(R_NADM, R_FADM))
-        if p.lazy_n and self.evl:   # admission gradient = resident history entry 0 of admitted N / L rows
+        if p.lazy_n and p.evl:   # admission gradient = resident history entry 0 of admitted N / L rows
             be.glog_put(self.glog, p.adm_rec_slot, None, rg(R_NADM, R_LADM), self.n0)
         if p.c_slots.numel():
             be.copy_rows(self.mat, p.c_slots, rw(R_NCMP, R_LCMP))
@@ -525,7 +612,9 @@ class ElaraStep:
     def step(self, s, ids, g_occ, u, dplan, u_nexts):
         """Logical step s (1-based): ids int64 [O] (occurrences), g_occ [O, D] their gradients, u the batch's
         unique rows and dplan its dedup plan (from be.unique), u_nexts the unique rows of the next depth-1
-        batches."""
+        batches.  The lookahead is the caller's: batches s+1 .. s+L are observed (observe) before this call, as
+        run() does (srm2/train.py:359-366); if batch s+1 was not, the next step waits for this step's writes into
+        host arenas before it assembles."""
         p = self.plan(s, u, u_nexts, g_occ, dplan)
         self.assemble(p)
         G = p.G if p.G is not None else self.be.segsum(g_occ, dplan, u.numel(), p.rank)

@@ -258,6 +258,10 @@ typedef struct elr_plan_in {
                                  searches of next[]), and the scatter pass clears bit s % 32 of the batch's rows: no
                                  later plan asks about step s */
   uint32_t next_mask;         /* the bits of the next batches' steps (s+1, s+2, ...), none equal to bit s % 32 */
+  int carry;                  /* residency 'carry' (srm2/elara.py:221, 231-233): a missing row is admitted when it
+                                 appears in one of the next batches, and every unprotected dynamic slot is expired;
+                                 0: 'ttl' (admitted when last_seen > s; expired when last_seen of its row <= s) */
+  const int64_t* live;        /* device counter copied into counts[15] (may be NULL) */
 } elr_plan_in;
 
 typedef struct elr_plan_out {
@@ -269,7 +273,8 @@ typedef struct elr_plan_out {
   int64_t* rank;              /* [n] inverse of order (may be NULL) */
   int64_t* dyn_out;           /* [2 nd]: slots as [expired | preemptible | protected], then [expired | the rest],
                                  each part in dyn order */
-  int64_t* counts;            /* [16] device: 10 class counts, expired, preemptible, protected, mat_top, log_top, 0 */
+  int64_t* counts;            /* [16] device: 10 class counts, expired, preemptible, protected, mat_top, log_top,
+                                 live */
   /* Optional outputs in class-rank order (each may be NULL), so that the caller needs no gathers: */
   int64_t* u_ord;             /* [n] u[order[r]] */
   int64_t* c_ord;             /* [n] code of u[order[r]] */

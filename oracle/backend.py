@@ -24,12 +24,13 @@ class OracleBackend:
         return u, inv, None
 
     def plan_classify(self, u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s,
-                      K, want_t, loc=None, R=0):
+                      K, want_t, loc=None, R=0, carry=False, live=None):
         """Restatement of the planner's classification (srm2/elara.py:214-267) with torch ops on CPU tensors:
-        slot lookup and hits (:219-220), next-batch membership (:223-226), admission by TTL (:221), protection of
-        the slots the next batches need through a scatter of their slots (:227-229), expiry of unprotected
-        dynamic slots (:231-233), class per row (:244-258) and the stable class orders (:242, 260-267).  Returns
-        what elara_amd.planner.plan_classify returns."""
+        slot lookup and hits (:219-220), next-batch membership (:223-226), admission by TTL or, with carry, by
+        next-batch membership (:221), protection of the slots the next batches need through a scatter of their
+        slots (:227-229), expiry of unprotected dynamic slots (:231-233; with carry every unprotected slot), class
+        per row (:244-258) and the stable class orders (:242, 260-267).  Returns what
+        elara_amd.planner.plan_classify returns."""
         from elara_amd.planner import PlanClass
         n = u.numel()
         sl = slot_of[u]
@@ -39,7 +40,7 @@ class OracleBackend:
             if un.numel():
                 j = torch.searchsorted(un, u).clamp(max=un.numel() - 1)
                 in_next |= un[j] == u
-        admit = ~hit & (last_seen[u].long() > s)
+        admit = ~hit & (in_next if carry else last_seen[u].long() > s)
         C = slot_row.numel()
         prot = torch.zeros(C + 1, dtype=torch.bool)
         for un in u_nexts:
@@ -47,7 +48,7 @@ class OracleBackend:
             prot[torch.where(sn >= 0, sn, torch.full_like(sn, C))] = True
         dyn = dyn.long()
         unprot = ~prot[dyn]
-        exp = unprot & (last_seen[slot_row[dyn]].long() <= s)
+        exp = unprot if carry else unprot & (last_seen[slot_row[dyn]].long() <= s)
         pre = unprot & ~exp
         c = code[u]
         thr = kthr[torch.searchsorted(toff, u, right=True) - 1]
@@ -73,7 +74,8 @@ class OracleBackend:
                                                                                       stable=True)]])
         counts = torch.cat([torch.bincount(cls.long(), minlength=10),
                             torch.stack([exp.sum(), pre.sum(), (dcls == 2).sum()]),
-                            mat_top.reshape(1), log_top.reshape(1), torch.zeros(1, dtype=torch.int64)])
+                            mat_top.reshape(1), log_top.reshape(1),
+                            live.reshape(1) if live is not None else torch.zeros(1, dtype=torch.int64)])
         # the rows in class order, and the L rows as the reference lists them: its stable class sort puts classes
         # 4, 5, 6 (admitted, append, compact) in that order, each in ascending position (srm2/elara.py:260-267)
         L_sel = [cls == 4, cls == 5, cls == 6]
