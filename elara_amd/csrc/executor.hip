@@ -17,7 +17,8 @@
 // Steps 1, 3 and 4 are k_adam_exec launches: the row moves and history records ride on the Adam passes, and the
 // work array is never written back (no later kernel reads it).  Steps 1-3 are the device part and 4-6 the link
 // part (elr_update_args.part): a caller with the arenas in host memory runs the link part on a second stream.
-// D = 64, 128, 256 or 512 (the fused assembly's limits too).
+// D = 64, 128, 256 or 512 with 16-byte aligned arrays: wave-per-row kernels (elr_rowio.h); any other D or alignment:
+// the same launches with the generic kernel, a wave per row whose lanes step through the row one float at a time.
 #include "elr_rowio.h"
 
 #ifndef ELR_EXEC_U
@@ -93,13 +94,41 @@ __global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
   }
 }
 
-static int adam_exec(int vpl, const ExecAdam& a, const AdamScalars& s, hipStream_t st,
+// k_adam_exec for any D: a wave per row, lane l handling elements l, l + 64, ... (same rows, same writes).
+__global__ __launch_bounds__(256) void k_adam_exec_gen(ExecAdam a, AdamScalars s, int64_t D) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t i = wave_id(); i < a.n; i += wave_count()) {
+    const int64_t d = i < a.na ? a.dst_a[i] : a.dst_b[i - a.na];
+    const float* g = a.grad + (a.g_base + i) * D;
+    if (i < a.n_rec) {   // history record (also for a row whose destination is out of range)
+      const int64_t slot = (a.rec_dyn ? a.rec_dyn[i] : d) - a.rec_off, e = a.rec_j ? a.rec_j[i] : 0;
+      if (slot >= 0 && slot < a.nd && e >= 0 && e < a.K) {
+        float* h = a.glog + (slot * a.K + e) * D;
+        for (int64_t j = lane; j < D; j += 64) h[j] = g[j];
+      }
+    }
+    if (d < 0 || d >= a.dst_rows || (a.src && a.src_base + i >= a.src_rows)) continue;
+    const float* sp = a.src ? a.src + (a.src_base + i) * 3 * D : a.dst + d * 3 * D;
+    float* o = a.dst + d * 3 * D;
+    for (int64_t j = lane; j < D; j += 64) {
+      float w = sp[j], m = sp[D + j], v = sp[2 * D + j];
+      adam_elem(w, m, v, g[j], s);
+      o[j] = w;
+      o[D + j] = m;
+      o[2 * D + j] = v;
+    }
+  }
+}
+
+// vpl = 0: the generic kernel for D.
+static int adam_exec(int vpl, int64_t D, const ExecAdam& a, const AdamScalars& s, hipStream_t st,
                      int64_t max_blocks = int64_t(1) << 20) {
   constexpr int U = ELR_EXEC_U;
   if (a.n <= 0) return ELR_OK;
   int64_t blocks = (a.n + 4 * U - 1) / (4 * U);
   if (blocks > max_blocks) blocks = max_blocks;
   switch (vpl) {
+    case 0: k_adam_exec_gen<<<(unsigned)blocks, 256, 0, st>>>(a, s, D); break;
     case 1: k_adam_exec<1, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
     case 2: k_adam_exec<2, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
     case 4: k_adam_exec<4, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
@@ -140,11 +169,9 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   float* Wk = a->work;
   const int64_t w0 = b[ELR_RANK_NADM];
   int rc;
-  const int vpl = wpr_vpl(D);
-  if (!vpl) return ELR_EUNSUPPORTED;
-  if (!aligned16(a->pool) || !aligned16(a->mat) || !aligned16(a->glog) || !aligned16(Wk) || !aligned16(G) ||
-      !aligned16(a->logs))
-    return ELR_EINVAL;
+  const bool al = aligned16(a->pool) && aligned16(a->mat) && aligned16(a->glog) && aligned16(Wk) && aligned16(G) &&
+                  aligned16(a->logs);
+  const int vpl = al ? wpr_vpl(D) : 0;
   if (a->part < ELR_UPDATE_ALL || a->part > ELR_UPDATE_LINK || a->link_blocks < 0) return ELR_EINVAL;
   const int64_t lb = a->link_blocks > 0 ? a->link_blocks : int64_t(1) << 20;
   const AdamScalars s = make_scalars(sc);
@@ -152,7 +179,7 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   const bool dev_part = a->part != ELR_UPDATE_LINK, link_part = a->part != ELR_UPDATE_DEVICE;
   if (dev_part) {
     // 1. hits: history record and Adam in place
-    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
+    if ((rc = adam_exec(vpl, D, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
                                       b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
                                       rec ? n_hit : 0}, s, st)))
       return rc;
@@ -165,13 +192,13 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
         return rc;
     }
     // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
-    if ((rc = adam_exec(vpl, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
+    if ((rc = adam_exec(vpl, D, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
                                       n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
       return rc;
   }
   if (!link_part) return ELR_OK;
   // 4. compacted rows into their new MAT slots, transient F rows back into theirs
-  if ((rc = adam_exec(vpl, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
+  if ((rc = adam_exec(vpl, D, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
                                     b[ELR_RANK_NCMP] - w0, G, b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr,
                                     nullptr, 0, 0}, s, st, lb)))
     return rc;

@@ -357,25 +357,23 @@ def test_gpu_dedup_edge_cases(dev):
 
 
 @pytest.mark.gpu
-def test_gpu_c3_full_size_two_steps(dev):
-    """Config C3 at full size: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step; touched rows bitwise
-    equal to the oracle (segment sum + cpu_adam on a compact copy of the touched rows)."""
+def test_gpu_c3_full_size_twelve_steps(dev):
+    """Config C3 at full size: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step, 12 steps (the hot
+    rows' m and v accumulate over all of them); touched rows bitwise equal to the oracle (segment sum + cpu_adam on
+    a compact copy of the touched rows)."""
     from elara_amd.dedup import adam_dedup
     from elara_amd.gpu_ops import init_rows
-    print('[gpu-test] C3 full size', flush=True)
-    R, D, B, F = 10_000_000, 128, 131_072, 26
+    print('[gpu-test] C3 full size, 12 steps', flush=True)
+    R, D, B, F, steps = 10_000_000, 128, 131_072, 26, 12
     z = synth.ZipfFields([R] * F, 1.05, seed=0, offsets=[0] * F)
     rng = np.random.default_rng(0)
     table = init_rows(torch.arange(R, device=dev), D, 0, synth.bound_for(D))
-    batches = []
-    for t in (1, 2):
-        ids = z.draw(rng, B)
-        g = torch.randn(ids.size, D, device=dev, generator=torch.Generator(dev).manual_seed(t)) * 1e-3
-        batches.append((ids, g))
-    touched = np.unique(np.concatenate([b[0] for b in batches]))
+    ids_all = [z.draw(rng, B) for _ in range(steps)]
+    touched = np.unique(np.concatenate(ids_all))
     tt = torch.from_numpy(touched).to(dev)
     compact = table[tt].cpu().numpy()
-    for t, (ids, g) in enumerate(batches, start=1):
+    for t, ids in enumerate(ids_all, start=1):
+        g = torch.randn(ids.size, D, device=dev, generator=torch.Generator(dev).manual_seed(t)) * 1e-3
         adam_dedup(table, torch.from_numpy(ids).to(dev), g, *HP, t)
         u, s, _ = O.segment_sum(ids, g.cpu().numpy())
         O.cpu_adam(compact, np.searchsorted(touched, u).astype(np.int64), s, O.adam_scalars(*HP, t), 16)
@@ -384,13 +382,13 @@ def test_gpu_c3_full_size_two_steps(dev):
 
 
 @pytest.mark.gpu
-def test_gpu_c4_large_row_stress_three_steps(dev):
+def test_gpu_c4_large_row_stress_ten_steps(dev):
     """Config C4: 50,000,000 x 256 table (weight + m + v = 153.6 GB in HBM), 262,144 unique Zipf(1.1) ids per
-    step; touched rows bitwise equal to the oracle's cpu_adam on a compact copy (the table exceeds host memory
-    budgets for a full CPU copy)."""
+    step, 10 steps; touched rows bitwise equal to the oracle's cpu_adam on a compact copy (the table exceeds host
+    memory budgets for a full CPU copy)."""
     from elara_amd.gpu_ops import init_rows
     from elara_amd.ops import gpu_adam
-    print('[gpu-test] C4 large rows', flush=True)
+    print('[gpu-test] C4 large rows, 10 steps', flush=True)
     R, D, n = 50_000_000, 256, 262_144
     z = synth.ZipfFields([R], 1.1, seed=4, offsets=[0])
     rng = np.random.default_rng(4)
@@ -398,7 +396,7 @@ def test_gpu_c4_large_row_stress_three_steps(dev):
     for a in range(0, R, 1 << 23):   # init in slices: rows a .. a+8M
         rows = torch.arange(a, min(R, a + (1 << 23)), device=dev)
         init_rows(rows, D, 0, synth.bound_for(D), out=table[a:a + rows.numel()])
-    steps = [synth.unique_zipf(rng, z, n) for _ in range(3)]
+    steps = [synth.unique_zipf(rng, z, n) for _ in range(10)]
     touched = np.unique(np.concatenate(steps))
     tt = torch.from_numpy(touched).to(dev)
     compact = table[tt].cpu().numpy()
