@@ -6,11 +6,12 @@ elr_replay_rows) and then take this step's row-sparse Adam update with a fresh g
 executor's path for logged rows (srm2/elara.py:485, 514).  Inputs are resident in HBM before timing starts.
 value = rows per second over the K timed steps.
 
-roofline: the replay kernel -- algorithmic bytes per launch / its mean duration from HIP events (created with
-hipEventDisableSystemFence: timing only, no cache flush) recorded on the launch stream around the launches of every
-2nd timed step from step 1 on; peak 8 TB/s.  cpu_baseline: the same step on this host's cores at nthreads = nproc,
-with every Adam step done by the reference's own compiled cpu_adam (oracle/_ref), on a bounded sample of the rows;
-the oracle's C port of the whole step is reported beside it.
+roofline: the replay kernel -- algorithmic bytes per launch / its mean duration over the K timed launches, from HIP
+events that each launch records itself at its kernel's start and end (hipExtLaunchKernelGGL through
+elr_replay_rows_timed / elr_adam_rows_timed: the kernel's own duration, as rocprofv3 reports it, and no marker
+packets in the queue); peak 8 TB/s.  cpu_baseline: the same step on this host's cores at nthreads = nproc, with every
+Adam step done by the reference's own compiled cpu_adam (oracle/_ref), on a bounded sample of the rows; the oracle's
+C port of the whole step is reported beside it.
 
 Clock settle and warm-up: the first 20-30 ms of sustained load run at a lower engine clock (measured on the headline
 step: replay 288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound,
@@ -35,7 +36,6 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = 'sparse-Adam+replay rows/s at d=128; achieved HBM GB/s vs ~8 TB/s peak'
 HBM_PEAK_GBS = 8000.0
-EV_EVERY = 2   # headline: HIP events on every 2nd timed step (steps 1, 3, 5, ...)
 POST_SYNC_IDLE_S = 0.002   # headline: host idle between the synchronisation and the timed region
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000   # hipEventDisableSystemFence, hip_runtime_api.h
 _HIP = None
@@ -272,11 +272,11 @@ def headline(args):
     stream = torch.cuda.current_stream(dev)
 
     def one_step(ev=None):
-        if ev: ev[0].record(stream)
-        replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=out)
-        if ev: ev[1].record(stream)
-        gpu_adam(out, slots, grad, *synth.ADAM, step_t)
-        if ev: ev[2].record(stream)
+        # ev: four HIP events the two launches record themselves at their kernels' start and end
+        # (hipExtLaunchKernelGGL): a kernel's duration as a profiler reports it, with no marker packet between launches
+        replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=out,
+                    events=(ev[0].h.value, ev[1].h.value) if ev else None)
+        gpu_adam(out, slots, grad, *synth.ADAM, step_t, events=(ev[2].h.value, ev[3].h.value) if ev else None)
 
     # clock settle: the engine clock leaves its idle level only after 20-30 ms of sustained load, and replay, whose
     # arithmetic is close to its memory time, follows it (288, 138, 125 us per launch over the first three 25-step
@@ -292,19 +292,18 @@ def headline(args):
     # that replay took 140-190 us, launched 0.1-10 ms later 129-132 us (steady state: 118-124).  The timed region
     # starts after POST_SYNC_IDLE_S.
     time.sleep(POST_SYNC_IDLE_S)
-    # kernel durations from HIP events on every EV_EVERY-th timed step, from step 1 on (the first timed launch is
-    # the one after the synchronisation): each marker costs the step a few us (three per step: 0.268 against 0.258
-    # ms per step), so sampling keeps the instrument out of `value`
-    evs = [[HipEvent() for _ in range(3)] if i % EV_EVERY == 1 else None for i in range(args.steps)]
+    # every timed launch is timed by its own dispatch (no extra packets in the queue, so the instrument stays out of
+    # `value`); the roofline takes the mean over all K launches
+    evs = [[HipEvent() for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         one_step(evs[i])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    evs = [e for e in evs if e is not None]
-    rep_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in evs]))
-    adam_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in evs]))
+    rep_all = [e[0].elapsed_time(e[1]) for e in evs]
+    adam_all = [e[2].elapsed_time(e[3]) for e in evs]
+    rep_ms, adam_ms = float(np.mean(rep_all)), float(np.mean(adam_all))
     _destroy(evs)
     rb, ab = replay_bytes(n, K, D, nlog), adam_bytes(n, D)
     rep_gbs = rb / (rep_ms * 1e-3) / 1e9
@@ -317,8 +316,9 @@ def headline(args):
                    'kmax': K, 'log_entries': nlog, 'parallelism': 'single GPU'},
         'roofline': {'bound': 'hbm', 'kernel': 'elr::k_replay_wpr<2, 3, 2>', 'achieved': rep_gbs, 'peak': HBM_PEAK_GBS,
                      'unit': 'GB/s', 'frac': rep_gbs / HBM_PEAK_GBS, 'traffic': _traffic('elr::k_replay_wpr<2, 3, 2>'),
-                     'algorithmic_bytes_per_launch': rb, 'mean_launch_ms': rep_ms},
-        'kernels': {'replay': {'ms': rep_ms, 'GBps': rep_gbs, 'bytes': rb},
+                     'algorithmic_bytes_per_launch': rb, 'mean_launch_ms': rep_ms,
+                     'median_launch_ms': float(np.median(rep_all)), 'launches_timed': len(rep_all)},
+        'kernels': {'replay': {'ms': rep_ms, 'GBps': rep_gbs, 'bytes': rb, 'ms_first': rep_all[0]},
                     'adam': {'ms': adam_ms, 'GBps': ab / (adam_ms * 1e-3) / 1e9, 'bytes': ab,
                              'frac': ab / (adam_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}},
         'step_GBps': (rb + ab) / (elapsed / args.steps) / 1e9,
@@ -460,6 +460,32 @@ def mode_c3(args):
                  extra={'unique_rows_per_s': Umean * steps / el, 'mean_step_ms_events': float(np.mean(ms))})
 
 
+def mode_rows(args):
+    """Row order on the C3 table (10,000,000 x 128, 15.36 GB): row-sparse Adam on 1,200,000 rows (about C3's
+    unique rows per step), --rows-order consecutive (one contiguous run) or random (uniform without replacement,
+    sorted ascending, as C3's unique ids are).  Same kernel, same bytes: the difference is the DRAM access pattern."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.gpu_ops import init_rows
+    from elara_amd.ops import gpu_adam
+    dev = torch.device('cuda:0')
+    R, D, n = 10_000_000, 128, 1_200_000
+    table = init_rows(torch.arange(R, device=dev), D, 0, synth.bound_for(D))
+    rng = np.random.default_rng(0)
+    if args.rows_order == 'consecutive':
+        rows = torch.arange(3_000_000, 3_000_000 + n, device=dev)
+    else:
+        rows = torch.from_numpy(np.sort(rng.choice(R, n, replace=False))).to(dev)
+    g = torch.from_numpy(synth.grads(rng, n, D)).to(dev)
+    steps = 50
+    el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, rows, g, *synth.ADAM, i + 1), steps, 5, SETTLE_S)
+    return _line(f'row-sparse Adam rows/s on the C3 table, {args.rows_order} rows (d=128)', n * steps / el,
+                 'rows/s', args, steps, warmup, el,
+                 {'workload': f'Adam on 1,200,000 {args.rows_order} rows of a 10,000,000 x 128 fp32 table',
+                  'rows_per_step': n, 'dim': D, 'order': args.rows_order}, adam_bytes(n, D) / 1e9,
+                 extra={'mean_launch_ms': float(np.mean(ms))})
+
+
 def mode_c4(args):
     """Config C4: 50,000,000 x 256 table (153.6 GB resident), 262,144 unique Zipf(1.1) ids per step, 50 steps."""
     import torch
@@ -565,7 +591,9 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=200)
-    ap.add_argument('--mode', default='headline', choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'all'])
+    ap.add_argument('--mode', default='headline', choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'rows', 'all'])
+    ap.add_argument('--rows-order', default='random', choices=['random', 'consecutive'],
+                    help='--mode rows: the order of the updated rows')
     ap.add_argument('--steps-c3', type=int, default=100)
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=100)
@@ -579,7 +607,7 @@ def main():
               'an all-to-all of occurrence gradients; not implemented); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     fns = {'headline': headline, 'copy': copy_calibration, 'c1': mode_c1, 'c3': mode_c3, 'c4': mode_c4,
-           'c5': mode_c5}
+           'c5': mode_c5, 'rows': mode_rows}
     for m in (['headline', 'c1', 'c3', 'c4', 'c5'] if args.mode == 'all' else [args.mode]):
         res = fns[m](args)
         print(json.dumps(res, default=float), flush=True)

@@ -30,10 +30,14 @@ SIGNATURES = {
     'elr_adam_scalars': (None, [c_f64, c_f64, c_f64, c_f64, c_i64, c_f32p]),
     'elr_scalar_table': (ctypes.c_int, [c_f64, c_f64, c_f64, c_f64, c_i64, c_vp]),
     'elr_adam_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_f32p, c_vp]),
+    'elr_adam_rows_timed': (ctypes.c_int, [c_vp, c_i64, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_f32p, c_vp, c_vp,
+                                           c_vp]),
     'elr_init_rows': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, c_u32, c_f32, c_vp]),
     'elr_scalar_recip': (ctypes.c_int, [c_vp, c_i64, c_vp]),
     'elr_replay_rows': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_u32,
                                        c_f32, c_vp, c_vp, c_i64, c_vp]),
+    'elr_replay_rows_timed': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i64, ctypes.c_int,
+                                             c_u32, c_f32, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp]),
     'elr_dir_scratch_bytes': (c_i64, [c_i64, c_i64]),
     'elr_dedup_scratch_bytes': (c_i64, [c_i64, c_i64]),
     'elr_selfcheck_div': (ctypes.c_int, [c_f32, c_vp, c_vp, c_vp]),

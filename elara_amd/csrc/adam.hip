@@ -106,14 +106,15 @@ __global__ __launch_bounds__(256) void k_adam_rows_wpr(float* __restrict__ state
 
 template <int VPL, typename Idx>
 static void launch_adam_wpr(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n,
-                            const AdamScalars& s, hipStream_t st) {
+                            const AdamScalars& s, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   constexpr int U = ELR_ADAM_U;
   constexpr int64_t D = 64 * VPL;
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
-    k_adam_rows_wpr<VPL, Idx, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(
-        state, C, slots ? slots + a : nullptr, a, grad + a * D, m, s);
+    launch_timed(k_adam_rows_wpr<VPL, Idx, U>, grid_for((m + U - 1) / U, 4, kOneShotBlocks), st,
+                 a == 0 ? e0 : nullptr, a + m >= n ? e1 : nullptr, state, C, slots ? slots + a : nullptr, a,
+                 grad + a * D, m, s);
   }
 }
 
@@ -143,25 +144,25 @@ __global__ __launch_bounds__(256) void k_adam_rows_d64_pair(float* __restrict__ 
 
 template <typename Idx>
 static void launch_adam_d64_pair(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n,
-                                 const AdamScalars& s, hipStream_t st) {
+                                 const AdamScalars& s, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   constexpr int64_t per = wpr_rows_per_launch(2);
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
-    k_adam_rows_d64_pair<Idx><<<grid_for((m + 1) / 2, 4, kOneShotBlocks), 256, 0, st>>>(
-        state, C, slots ? slots + a : nullptr, a, grad + a * 64, m, s);
+    launch_timed(k_adam_rows_d64_pair<Idx>, grid_for((m + 1) / 2, 4, kOneShotBlocks), st, a == 0 ? e0 : nullptr,
+                 a + m >= n ? e1 : nullptr, state, C, slots ? slots + a : nullptr, a, grad + a * 64, m, s);
   }
 }
 
 template <typename Idx>
 static int launch_adam(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n, int64_t D,
-                       const AdamScalars& s, hipStream_t st) {
+                       const AdamScalars& s, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
   const int vpl = wpr_vpl(D);
   if (vpl && aligned16(state) && aligned16(grad)) {
     switch (vpl) {
-      case 1: launch_adam_d64_pair<Idx>(state, C, slots, grad, n, s, st); break;   // C1: 22.8 us, 25.5 a wave per row
-      case 2: launch_adam_wpr<2, Idx>(state, C, slots, grad, n, s, st); break;
-      case 4: launch_adam_wpr<4, Idx>(state, C, slots, grad, n, s, st); break;
-      default: launch_adam_wpr<8, Idx>(state, C, slots, grad, n, s, st); break;
+      case 1: launch_adam_d64_pair<Idx>(state, C, slots, grad, n, s, st, e0, e1); break;   // C1: 22.8 us, 25.5 a
+      case 2: launch_adam_wpr<2, Idx>(state, C, slots, grad, n, s, st, e0, e1); break;     // wave per row
+      case 4: launch_adam_wpr<4, Idx>(state, C, slots, grad, n, s, st, e0, e1); break;
+      default: launch_adam_wpr<8, Idx>(state, C, slots, grad, n, s, st, e0, e1); break;
     }
     return launch_status();
   }
@@ -170,9 +171,9 @@ static int launch_adam(float* state, int64_t C, const Idx* slots, const float* g
     const int lg = lanes_per_row_log2(nchunk);
     const int64_t rpw = 64 >> lg;
     const int64_t waves = (n + rpw - 1) / rpw;
-    k_adam_rows_v4<Idx><<<grid_for(waves, 4), 256, 0, st>>>(state, C, slots, grad, n, (int)nchunk, lg, s);
+    launch_timed(k_adam_rows_v4<Idx>, grid_for(waves, 4), st, e0, e1, state, C, slots, grad, n, (int)nchunk, lg, s);
   } else {
-    k_adam_rows_scalar<Idx><<<grid_for(n, 4), 256, 0, st>>>(state, C, slots, grad, n, D, s);
+    launch_timed(k_adam_rows_scalar<Idx>, grid_for(n, 4), st, e0, e1, state, C, slots, grad, n, D, s);
   }
   return launch_status();
 }
@@ -209,11 +210,17 @@ extern "C" int elr_scalar_recip(const float* table_host, int64_t table_rows, dou
 
 extern "C" int elr_adam_rows(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n,
                              int64_t D, const float sc[8], void* stream) {
+  return elr_adam_rows_timed(state, C, slots, idx64, grad, n, D, sc, nullptr, nullptr, stream);
+}
+
+extern "C" int elr_adam_rows_timed(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n,
+                                   int64_t D, const float sc[8], void* start_event, void* stop_event, void* stream) {
   if (n < 0 || D <= 0 || C < 0 || !sc) return ELR_EINVAL;
   if (n == 0) return ELR_OK;
   if (!state || !grad) return ELR_EINVAL;   // slots == NULL: row i of grad updates state row i
   const elr::AdamScalars s = elr::make_scalars(sc);
   hipStream_t st = (hipStream_t)stream;
-  if (idx64) return elr::launch_adam(state, C, (const int64_t*)slots, grad, n, D, s, st);
-  return elr::launch_adam(state, C, (const int32_t*)slots, grad, n, D, s, st);
+  hipEvent_t e0 = (hipEvent_t)start_event, e1 = (hipEvent_t)stop_event;
+  if (idx64) return elr::launch_adam(state, C, (const int64_t*)slots, grad, n, D, s, st, e0, e1);
+  return elr::launch_adam(state, C, (const int32_t*)slots, grad, n, D, s, st, e0, e1);
 }

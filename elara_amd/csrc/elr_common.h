@@ -9,6 +9,7 @@
 // what the reference's CPU Adam computes (srm2/csrc/srm2_cpu.cpp:22-34, built with -ffp-contract=off).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

@@ -44,16 +44,18 @@ __device__ __forceinline__ RowFrag<VPL> frag_load(const float* __restrict__ p) {
 // Stores are marked non-temporal: every row written here (updated Adam state, replayed rows, fresh rows) is read
 // again only by a later kernel, after far more than the caches hold has streamed through.  Measured on the C2 Adam
 // step (d=128): 158 us with ordinary stores, 140 us with non-temporal ones.
-template <int VPL>
+template <int VPL, bool NT = true>
 __device__ __forceinline__ void frag_store(float* __restrict__ p, const RowFrag<VPL>& r) {
   if constexpr (VPL == 1) {
-    __builtin_nontemporal_store(r.v[0], p);
+    if constexpr (NT) __builtin_nontemporal_store(r.v[0], p);
+    else *p = r.v[0];
   } else if constexpr (VPL == 2) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     f2 t;
     t.x = r.v[0];
     t.y = r.v[1];
-    __builtin_nontemporal_store(t, reinterpret_cast<f2*>(p));
+    if constexpr (NT) __builtin_nontemporal_store(t, reinterpret_cast<f2*>(p));
+    else *reinterpret_cast<f2*>(p) = t;
   } else {
 #pragma unroll
     for (int q = 0; q < VPL / 4; ++q) {
@@ -62,7 +64,8 @@ __device__ __forceinline__ void frag_store(float* __restrict__ p, const RowFrag<
       t.y = r.v[4 * q + 1];
       t.z = r.v[4 * q + 2];
       t.w = r.v[4 * q + 3];
-      __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p) + q);
+      if constexpr (NT) __builtin_nontemporal_store(t, reinterpret_cast<f32x4*>(p) + q);
+      else reinterpret_cast<f32x4*>(p)[q] = t;
     }
   }
 }
@@ -210,6 +213,14 @@ __device__ __forceinline__ int64_t wave_id() {
   return (int64_t)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)));
 }
 __device__ __forceinline__ int64_t wave_count() { return (int64_t)gridDim.x * (blockDim.x >> 6); }
+
+// Launch `kern` on grid g; with timing events (either may be NULL), hipExtLaunchKernelGGL has the dispatch itself
+// record them at the kernel's start and end, as a profiler times a kernel (no marker packets between launches).
+template <typename Kern, typename... Args>
+inline void launch_timed(Kern kern, unsigned g, hipStream_t st, hipEvent_t e0, hipEvent_t e1, Args... args) {
+  if (e0 || e1) hipExtLaunchKernelGGL(kern, dim3(g), dim3(256), 0, st, e0, e1, 0, args...);
+  else kern<<<g, 256, 0, st>>>(args...);
+}
 
 // dst[dst_idx[i]] = src[i] with at most max_blocks blocks (rows.hip; used by the executor's link part).
 int copy_rows_capped(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,

@@ -255,15 +255,16 @@ __global__ __launch_bounds__(256) void k_replay_wpr(float* __restrict__ out, con
 template <int VPL, int K>
 static void launch_replay_wpr(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                               const int32_t* steps, const int32_t* cnt, int64_t n, uint32_t seed, float bound,
-                              const float* table, const double* recip, int64_t table_rows, hipStream_t st) {
+                              const float* table, const double* recip, int64_t table_rows, hipStream_t st,
+                              hipEvent_t e0, hipEvent_t e1) {
   constexpr int U = ELR_REPLAY_U;
   constexpr int64_t D = 64 * VPL;
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
-    k_replay_wpr<VPL, K, U><<<grid_for((m + U - 1) / U, 4, kOneShotBlocks), 256, 0, st>>>(
-        out + a * 3 * D, rows + a, logs, nlogs, offs + a, steps + a * K, cnt + a, m, seed, bound, table, recip,
-        table_rows);
+    launch_timed(k_replay_wpr<VPL, K, U>, grid_for((m + U - 1) / U, 4, kOneShotBlocks), st, a == 0 ? e0 : nullptr,
+                 a + m >= n ? e1 : nullptr, out + a * 3 * D, rows + a, logs, nlogs, offs + a, steps + a * K, cnt + a,
+                 m, seed, bound, table, recip, table_rows);
   }
 }
 
@@ -282,11 +283,13 @@ static void launch_init_wpr(float* out, const int64_t* rows, int64_t n, uint32_t
 template <int K>
 static int launch_replay(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                          const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, uint32_t seed, float bound,
-                         const float* table, const double* recip, int64_t table_rows, hipStream_t st) {
+                         const float* table, const double* recip, int64_t table_rows, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1) {
   const int vpl = wpr_vpl(D);
   if (K <= 4 && vpl && recip && aligned16(out) && aligned16(logs)) {
 #define ELR_WPR_REPLAY(V) \
-  launch_replay_wpr<V, K>(out, rows, logs, nlogs, offs, steps, cnt, n, seed, bound, table, recip, table_rows, st)
+  launch_replay_wpr<V, K>(out, rows, logs, nlogs, offs, steps, cnt, n, seed, bound, table, recip, table_rows, st, \
+                          e0, e1)
     switch (vpl) {
       case 1: ELR_WPR_REPLAY(1); break;
       case 2: ELR_WPR_REPLAY(2); break;
@@ -300,12 +303,11 @@ static int launch_replay(float* out, const int64_t* rows, const float* logs, int
     const int64_t nchunk = D / 4;
     const int lg = lanes_per_row_log2(nchunk);
     const int64_t rpw = 64 >> lg;
-    k_replay_v4<K><<<grid_for((n + rpw - 1) / rpw, 4), 256, 0, st>>>(out, rows, logs, nlogs, offs, steps, cnt, n,
-                                                                     (int)nchunk, lg, seed, bound, table, recip,
-                                                                     table_rows);
+    launch_timed(k_replay_v4<K>, grid_for((n + rpw - 1) / rpw, 4), st, e0, e1, out, rows, logs, nlogs, offs, steps,
+                 cnt, n, (int)nchunk, lg, seed, bound, table, recip, table_rows);
   } else {
-    k_replay_scalar<K><<<grid_for(n, 4), 256, 0, st>>>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound,
-                                                       table, recip, table_rows);
+    launch_timed(k_replay_scalar<K>, grid_for(n, 4), st, e0, e1, out, rows, logs, nlogs, offs, steps, cnt, n, D, seed,
+                 bound, table, recip, table_rows);
   }
   return launch_status();
 }
@@ -342,6 +344,15 @@ extern "C" int elr_replay_rows(float* out, const int64_t* rows, const float* log
                                const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed,
                                float bound, const float* table, const double* recip, int64_t table_rows,
                                void* stream) {
+  return elr_replay_rows_timed(out, rows, logs, nlogs, offs, steps, cnt, n, D, K, seed, bound, table, recip,
+                               table_rows, nullptr, nullptr, stream);
+}
+
+extern "C" int elr_replay_rows_timed(float* out, const int64_t* rows, const float* logs, int64_t nlogs,
+                                     const int64_t* offs, const int32_t* steps, const int32_t* cnt, int64_t n,
+                                     int64_t D, int K, uint32_t seed, float bound, const float* table,
+                                     const double* recip, int64_t table_rows, void* start_event, void* stop_event,
+                                     void* stream) {
   if (n < 0 || D <= 0 || nlogs < 0 || table_rows < 0) return ELR_EINVAL;
   if (K < 1 || K > 8) return ELR_EUNSUPPORTED;
   if (n == 0) return ELR_OK;
@@ -351,7 +362,7 @@ extern "C" int elr_replay_rows(float* out, const int64_t* rows, const float* log
 #define ELR_REPLAY_CASE(KK) \
   case KK:                  \
     return elr::launch_replay<KK>(out, rows, logs, nlogs, offs, steps, cnt, n, D, seed, bound, table, recip, \
-                                  table_rows, st);
+                                  table_rows, st, (hipEvent_t)start_event, (hipEvent_t)stop_event);
     ELR_REPLAY_CASE(1)
     ELR_REPLAY_CASE(2)
     ELR_REPLAY_CASE(3)

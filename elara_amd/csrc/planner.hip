@@ -189,6 +189,26 @@ __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_pla
       o.counts[13] = p.mat_top ? *p.mat_top : 0;
       o.counts[14] = p.log_top ? *p.log_top : 0;
       o.counts[15] = p.live ? *p.live : 0;
+      // rows of u outside [0, R) (u ascending: they are the ones below the first row >= 0 and from the first row
+      // >= R on); the caller raises on them instead of letting the step skip them
+      int64_t bad = 0;
+      if (p.R > 0 && p.n > 0) {
+        int64_t lo = 0, hi = p.n;   // first index with u >= 0
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (p.u[mid] < 0) lo = mid + 1;
+          else hi = mid;
+        }
+        bad = lo;
+        lo = 0, hi = p.n;           // first index with u >= R
+        while (lo < hi) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (p.u[mid] < p.R) lo = mid + 1;
+          else hi = mid;
+        }
+        bad += p.n - lo;
+      }
+      o.counts[16] = bad;
     }
   }
 }

@@ -53,9 +53,11 @@ class ScalarTable:
         self.r = _recip_host(host).to(device)
 
 
-def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None):
+def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None, events=None):
     """rows int64 [n]; logs [sum(cnt), D] with row i's entries at offs[i]; steps int32 [n,K]; cnt int32 [n];
-    table: ScalarTable (or its [S,8] tensor) -> out [n,3,D].  Allocates `out` when None."""
+    table: ScalarTable (or its [S,8] tensor) -> out [n,3,D].  Allocates `out` when None.  events: optional
+    (start, stop) hipEvent_t handles (integers) that the launch itself records at the kernel's start and end
+    (elr_replay_rows_timed); not recorded when n == 0."""
     n = rows.numel()
     if out is None:
         out = torch.empty(n, 3, D, device=rows.device)
@@ -79,10 +81,11 @@ def replay_rows(rows, logs, offs, steps, cnt, D, K, seed, bound, table, out=None
         t = t.contiguous()
         if r is None or r.shape != (t.shape[0], 2) or r.device != t.device:
             r = _recip_host(t.cpu().contiguous()).to(dev)   # a bare [S, 8] table: reciprocals computed here
+        e0, e1 = events if events is not None else (None, None)
         with _lib.on_device(dev):
-            rc = _lib.lib().elr_replay_rows(_lib.ptr(out), _lib.ptr(rows), _lib.ptr(logs), logs.numel() // D,
-                                            _lib.ptr(offs), _lib.ptr(steps), _lib.ptr(cnt), n, int(D), int(K),
-                                            _seed32(seed), float(bound), _lib.ptr(t), _lib.ptr(r), t.shape[0],
-                                            _lib.stream_of(rows))
+            rc = _lib.lib().elr_replay_rows_timed(_lib.ptr(out), _lib.ptr(rows), _lib.ptr(logs), logs.numel() // D,
+                                                  _lib.ptr(offs), _lib.ptr(steps), _lib.ptr(cnt), n, int(D), int(K),
+                                                  _seed32(seed), float(bound), _lib.ptr(t), _lib.ptr(r), t.shape[0],
+                                                  e0, e1, _lib.stream_of(rows))
         _lib.check(rc, 'elr_replay_rows')
     return out

@@ -57,10 +57,11 @@ def _check_state(pool, name='pool'):
                            f'{tuple(pool.shape)} {pool.dtype} {pool.device}')
 
 
-def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
+def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step, events=None):
     """pool [C,3,D] cuda float32 (updated in place); slots int32/int64 [n] (unique rows of pool); grad [n,D]
     (row i -> slots[i]).  srm2/ops.py:59-67.  pool may also be a pinned host arena (the capacity tier): the kernel
-    then updates it over the host link."""
+    then updates it over the host link.  events: optional (start, stop) hipEvent_t handles (integers) that the launch
+    itself records at the kernel's start and end (elr_adam_rows_timed); not recorded when n == 0."""
     n = slots.numel()
     if n == 0:
         return
@@ -78,9 +79,10 @@ def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step):
     grad = grad.contiguous()
     s = _scalars8(lr, b1, b2, eps, step)
     L = _lib.lib()
+    e0, e1 = events if events is not None else (None, None)
     with _lib.on_device(dev):
-        rc = L.elr_adam_rows(_lib.dptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
-                             _lib.ptr(grad), n, D, s, _lib.stream_of(grad))
+        rc = L.elr_adam_rows_timed(_lib.dptr(pool), pool.shape[0], _lib.ptr(slots), int(slots.dtype == torch.int64),
+                                   _lib.ptr(grad), n, D, s, e0, e1, _lib.stream_of(grad))
     _lib.check(rc, 'elr_adam_rows')
 
 

@@ -16,7 +16,7 @@ I8, I32, I64 = torch.int8, torch.int32, torch.int64
 C_HIT, C_NADM, C_NAPP, C_NCMP, C_LADM, C_LAPP, C_LCMP, C_FADM, C_FNADM, C_S = range(10)
 F_HIT, F_N, F_L, F_APP, F_ADMIT, F_NEXT = 1, 2, 4, 8, 16, 32
 # counts[16]: 10 class counts, then these
-CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP, CNT_LIVE = 10, 11, 12, 13, 14, 15
+CNT_EXP, CNT_PRE, CNT_PROT, CNT_MAT_TOP, CNT_LOG_TOP, CNT_LIVE, CNT_BAD, NCOUNTS = 10, 11, 12, 13, 14, 15, 16, 17
 
 PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts u_ord c_ord sl_ord L_row L_cnt loc_ord')
 
@@ -32,11 +32,12 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
     them: slot_of int32 [R], last_seen int32 [R], code int8 [R], kthr int8 [T], toff int64 [T], slot_row int64 [C],
     mat_top / log_top int64 [1].  Returns PlanClass(cls int8 [n], flags uint8 [n], sl int32 [n], c int8 [n],
-    order int64 [n] (positions by class rank), rank int64 [n] (its inverse), dyn_out int64 [2 nd], counts int64 [16]
+    order int64 [n] (positions by class rank), rank int64 [n] (its inverse), dyn_out int64 [2 nd], counts int64 [17]
     on the device, and in class-rank order u_ord, c_ord, sl_ord int64 [n] (u, c, sl at `order`); L_row int64 [n] and
     L_cnt int32 [n]: the L rows and their codes as admitted, append, compact, valid up to their count; loc_ord int64
     [n]: loc (int32 [R + 1], when given) of the rows in class-rank order, else None).  With R > 0 a row of u outside
-    [0, R) is classified S with no slot and no MAT slot (skipped by every later copy and update).
+    [0, R) is classified S with no slot and no MAT slot (skipped by every later copy and update), and counted in
+    counts[16].
 
     next_bits (int32 [R], with R > 0) and next_mask: the caller's ring of loaded batches (bit t % 32 of
     next_bits[r] set while the batch of step t holds row r; see rows.mark_rows).  Membership in the next batches is
@@ -65,7 +66,7 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     out = PlanClass(torch.empty(n, dtype=I8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev),
                     torch.empty(n, dtype=I32, device=dev), torch.empty(n, dtype=I8, device=dev),
                     torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
-                    torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(16, dtype=I64, device=dev),
+                    torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(NCOUNTS, dtype=I64, device=dev),
                     torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
                     torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
                     torch.empty(n, dtype=I32, device=dev),

@@ -35,8 +35,8 @@ from .dedup import segment_sum_plan, unique_plan, unique_plan_async
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
-from .planner import (CNT_EXP, CNT_LIVE, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, classify_from_flags,
-                      plan_admit, plan_classify)
+from .planner import (CNT_BAD, CNT_EXP, CNT_LIVE, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT,
+                      classify_from_flags, plan_admit, plan_classify)
 from .rows import copy_rows, glog_put, glog_take, mark_rows
 
 I8, I32, I64 = torch.int8, torch.int32, torch.int64
@@ -311,6 +311,8 @@ class ElaraStep:
         self._observed = max(self._observed, int(step))
         bit = 1 << (step % 32)
         if n_dev is None:
+            if u.device.type == 'cpu' and u.numel() and (int(u.min()) < 0 or int(u.max()) >= self.R):
+                raise ValueError(f'step {step}: rows of the batch lie outside [0, {self.R})')
             self.last_seen[u] = step
             if self.next_bits is not None:
                 self.next_bits[u] = self.next_bits[u] | (bit - (1 << 32) if bit >= 1 << 31 else bit)
@@ -393,6 +395,8 @@ class ElaraStep:
         counts = vals[:10]
         n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]
         live = vals[CNT_LIVE]
+        if vals[CNT_BAD]:
+            raise ValueError(f'step {s}: {vals[CNT_BAD]} rows of the batch lie outside [0, {self.R})')
         # memory-pressure gate of the residency-aware representation (srm2/elara.py:212-213, 423-425): the arenas'
         # used bytes as the previous step left them against the budget; sticky once on
         if (self.evl_mode == 2 and not self.evl and self.host_budget > 0

@@ -73,6 +73,13 @@ int elr_scalar_recip(const float* table_host, int64_t table_rows, double* recip_
 int elr_adam_rows(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n, int64_t D,
                   const float sc[8], void* stream);
 
+/* elr_adam_rows with kernel timing (no counterpart in the reference): start_event / stop_event (hipEvent_t, either
+ * may be NULL) are recorded by the launches themselves at the start of the first and the end of the last kernel
+ * (hipExtLaunchKernelGGL), with no marker packet between launches -- a kernel's duration as a profiler reports it.
+ * With n == 0 nothing is launched and the events are not recorded. */
+int elr_adam_rows_timed(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n,
+                        int64_t D, const float sc[8], void* start_event, void* stop_event, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Counter-hash initial state.
  * Replaces: srm2/gpu_ops.py:41-48 init_rows / _init_rows (hash gpu_ops.py:15-23).  out[i] = (w0(rows[i]), 0, 0)
@@ -93,6 +100,12 @@ int elr_init_rows(float* out, const int64_t* rows, int64_t n, int64_t D, uint32_
 int elr_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
                     const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed, float bound,
                     const float* table, const double* recip, int64_t table_rows, void* stream);
+
+/* elr_replay_rows with kernel timing (no counterpart in the reference), as elr_adam_rows_timed. */
+int elr_replay_rows_timed(float* out, const int64_t* rows, const float* logs, int64_t nlogs, const int64_t* offs,
+                          const int32_t* steps, const int32_t* cnt, int64_t n, int64_t D, int K, uint32_t seed,
+                          float bound, const float* table, const double* recip, int64_t table_rows,
+                          void* start_event, void* stop_event, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * State directory.
@@ -273,8 +286,8 @@ typedef struct elr_plan_out {
   int64_t* rank;              /* [n] inverse of order (may be NULL) */
   int64_t* dyn_out;           /* [2 nd]: slots as [expired | preemptible | protected], then [expired | the rest],
                                  each part in dyn order */
-  int64_t* counts;            /* [16] device: 10 class counts, expired, preemptible, protected, mat_top, log_top,
-                                 live */
+  int64_t* counts;            /* [17] device: 10 class counts, expired, preemptible, protected, mat_top, log_top,
+                                 live, rows of u outside [0, R) (0 when R is 0) */
   /* Optional outputs in class-rank order (each may be NULL), so that the caller needs no gathers: */
   int64_t* u_ord;             /* [n] u[order[r]] */
   int64_t* c_ord;             /* [n] code of u[order[r]] */

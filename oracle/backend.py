@@ -75,7 +75,8 @@ class OracleBackend:
         counts = torch.cat([torch.bincount(cls.long(), minlength=10),
                             torch.stack([exp.sum(), pre.sum(), (dcls == 2).sum()]),
                             mat_top.reshape(1), log_top.reshape(1),
-                            live.reshape(1) if live is not None else torch.zeros(1, dtype=torch.int64)])
+                            live.reshape(1) if live is not None else torch.zeros(1, dtype=torch.int64),
+                            (((u < 0) | (u >= R)).sum() if R > 0 else torch.zeros((), dtype=torch.int64)).reshape(1)])
         # the rows in class order, and the L rows as the reference lists them: its stable class sort puts classes
         # 4, 5, 6 (admitted, append, compact) in that order, each in ascending position (srm2/elara.py:260-267)
         L_sel = [cls == 4, cls == 5, cls == 6]

@@ -277,3 +277,29 @@ def test_replay_extreme_gradients(dev, D):
     out = replay_rows(t(rows), t(logs), t(offs), t(steps), t(cnt), D, K, 5, 0.03, table)
     torch.cuda.synchronize()
     assert same(out, O.replay_rows(rows, logs, offs, steps, cnt, D, K, 5, 0.03, table.t.cpu().numpy()))
+
+
+@pytest.mark.gpu
+def test_timed_launches_record_kernel_events(dev):
+    """elr_replay_rows_timed / elr_adam_rows_timed (gpu_ops.replay_rows / ops.gpu_adam with events): the same bits as
+    the untimed calls, and the two events the launch records bracket the kernel (positive, plausible duration)."""
+    import bench
+    print('[gpu-test] timed launches', flush=True)
+    w = synth.ReplayLog(n=4096, D=128, K=3, seed=9)
+    table = ScalarTable(*HP, w.max_step + 2, dev)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    args = (t(w.rows), t(w.logs), t(w.offs), t(w.steps), t(w.cnt), 128, 3, 5, 0.03, table)
+    a = replay_rows(*args)
+    ev = [bench.HipEvent() for _ in range(4)]
+    b = replay_rows(*args, events=(ev[0].h.value, ev[1].h.value))
+    g = t(synth.grads(np.random.default_rng(2), w.n, 128))
+    idx = torch.arange(w.n, device=dev)
+    gpu_adam(a, idx, g, *HP, w.max_step + 1)
+    gpu_adam(b, idx, g, *HP, w.max_step + 1, events=(ev[2].h.value, ev[3].h.value))
+    torch.cuda.synchronize()
+    assert same(a, b.cpu().numpy())
+    for x, y in ((ev[0], ev[1]), (ev[2], ev[3])):
+        ms = x.elapsed_time(y)
+        assert 0.0 < ms < 50.0, ms
+    for e in ev:
+        e.destroy()

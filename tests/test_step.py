@@ -87,6 +87,20 @@ def test_step_runs_on_cpu_with_oracle_backend():
     assert int(st.code.min()) >= 0 and int(st.code.max()) <= st.MAT
 
 
+@pytest.mark.parametrize('where', ['cpu', pytest.param('gpu', marks=pytest.mark.gpu)])
+def test_step_raises_on_rows_out_of_range(where, request):
+    """A batch row outside [0, R) is an error of the caller (undefined in the reference): the plan raises before it
+    changes the directory, instead of the kernels skipping the row."""
+    from elara_amd.step import run
+    cfg = config(T=4, lo=200, hi=2000, B=200, steps=4, C=800, n_static=300)
+    dev = request.getfixturevalue('dev') if where == 'gpu' else 'cpu'
+    st = make(cfg, dev, OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2) if where == 'cpu' else None)
+    batches = [b.clone() for b in cfg['batches']]
+    batches[2][5] = cfg['R'] + 7
+    with pytest.raises(ValueError, match='outside'):
+        run(st, batches, grads_fn(cfg, None))
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow', 'host_arenas',
                                   'host_arenas_S', 'host_arenas_overflow', 'D64_K2', 'D256_K4', 'K1_kthr0',
@@ -263,6 +277,7 @@ def test_gpu_plan_classify_skips_rows_out_of_range(dev):
     assert (b.cls[n:] == 9).all() and (b.sl[n:] == -1).all() and (b.c[n:] == K + 1).all() and (b.flags[n:] == 0).all()
     assert (b.loc_ord[b.rank[n:]] == -1).all()
     assert int(b.counts[9]) == int(a.counts[9]) + 3
+    assert int(b.counts[16]) == 3 and int(a.counts[16]) == 0   # counted for the step, which raises on them
 
 
 @pytest.mark.gpu
