@@ -38,7 +38,9 @@ constexpr int kItemsBig = 16;
 constexpr int kItemsSmall = 4;
 constexpr int64_t kBigBatch = int64_t(1) << 21;
 inline int items_for(int64_t n) { return n >= kBigBatch ? kItemsBig : kItemsSmall; }
-constexpr int kRadixBins = 256;
+constexpr int kRadixBins = 256;      // bins of an 8-bit digit; passes take 8, 9 or 10 bits (sort_plan)
+constexpr int kRadixMaxBits = 10;
+constexpr int kRadixMaxBins = 1 << kRadixMaxBits;
 constexpr int kAtenGroup = 10;                          // NROWS_PER_THREAD of ATen's sort path
 constexpr int kGroupsPerChunk = 6;
 constexpr int kSegChunk = kAtenGroup * kGroupsPerChunk;   // occurrences per parallel chunk (sort path)
@@ -48,27 +50,61 @@ constexpr int64_t kHotLen = 240;                          // sort-path segments 
 constexpr int kSegParts = 8;                              // run sums a final-kernel wave loads together
 constexpr int kSegBlock = 256;
 
-static_assert(kSortThreads == kRadixBins, "one histogram bin per sort thread");
+static_assert(kSortThreads == kRadixBins, "at least one histogram bin per sort thread");
 
-template <typename Key>
+template <int RB, typename Key>
 __device__ __forceinline__ uint32_t digit_of(Key k, int shift) {
-  return (uint32_t)((k >> shift) & (Key)(kRadixBins - 1));
+  return (uint32_t)((k >> shift) & (Key)((1u << RB) - 1));
 }
 
-// Per-tile digit histogram, digit-major: hist[d * nblk + tile].
-template <typename Src, typename Key, int ITEMS>
+// Passes and digit width of a sort of key_bits-bit keys: one pass fewer than 8-bit digits need when digits of at
+// most max_bits bits then suffice (27-bit keys: 3 passes of 9 bits instead of 4 of 8), else 8-bit digits.
+inline void sort_plan(int key_bits, int max_bits, int& passes, int& rb) {
+  const int p8 = (key_bits + 7) / 8;
+  if (p8 > 1) {
+    const int w = (key_bits + p8 - 2) / (p8 - 1);
+    if (w <= max_bits) {
+      passes = p8 - 1;
+      rb = w < 8 ? 8 : w;
+      return;
+    }
+  }
+  passes = p8;
+  rb = 8;
+}
+
+// Per-tile histogram of RB-bit digits, digit-major: hist[d * nblk + tile].
+template <typename Src, typename Key, int ITEMS, int RB>
 __global__ __launch_bounds__(kSortThreads) void k_radix_hist(const Src* __restrict__ src, int64_t n, int shift,
                                                              int64_t* __restrict__ hist, int64_t nblk) {
-  __shared__ int h[kRadixBins];
-  h[threadIdx.x] = 0;
+  constexpr int BINS = 1 << RB;
+  __shared__ int h[BINS];
+  for (int b = threadIdx.x; b < BINS; b += kSortThreads) h[b] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortThreads * ITEMS;
   for (int r = 0; r < ITEMS; ++r) {
     const int64_t pos = base + (int64_t)r * kSortThreads + threadIdx.x;
-    if (pos < n) atomicAdd(&h[digit_of((Key)src[pos], shift)], 1);
+    if (pos < n) atomicAdd(&h[digit_of<RB>((Key)src[pos], shift)], 1);
   }
   __syncthreads();
-  hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = h[threadIdx.x];
+  for (int b = threadIdx.x; b < BINS; b += kSortThreads) hist[(int64_t)b * nblk + blockIdx.x] = h[b];
+}
+
+// Exclusive prefix over BINS values held BPT per thread (thread t holds bins t*BPT .. t*BPT + BPT - 1, in x[]):
+// the prefixes to ex[], the total of all bins to *total.
+template <int BPT>
+__device__ __forceinline__ void bins_excl_scan(const int (&x)[BPT], int (&ex)[BPT], int& total) {
+  int loc = 0;
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
+    ex[j] = loc;
+    loc += x[j];
+  }
+  int v[1] = {loc}, e[1], tot[1];
+  block_excl_scan<kSortThreads, 1>(v, e, tot);
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) ex[j] += e[0];
+  total = tot[0];
 }
 
 // One block per digit: exclusive scan of that digit's per-tile counts (in place) and the digit's total.
@@ -92,7 +128,7 @@ __global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict_
 // scan over the waves' counts per digit at the end gives the first term.  The tile is then sorted by digit in LDS
 // and written out run by run, so consecutive threads write consecutive addresses of one digit's bucket instead of
 // 64 scattered ones.
-template <typename Src, typename Key, bool FIRST, int ITEMS>
+template <typename Src, typename Key, bool FIRST, int ITEMS, int RB>
 __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __restrict__ src_keys,
                                                                 const int32_t* __restrict__ src_vals, int64_t n,
                                                                 int shift, const int64_t* __restrict__ offs,
@@ -101,21 +137,28 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
                                                                 int32_t* __restrict__ dst_vals) {
   constexpr int NW = kSortThreads / 64;
   constexpr int TILE = kSortThreads * ITEMS;
-  __shared__ int64_t bo[kRadixBins];   // global position of this tile's first item of digit d
-  __shared__ int run[kRadixBins];      // items of digit d in the tile
-  __shared__ int lbase[kRadixBins];    // position of digit d's first item in the tile sorted by digit
-  __shared__ int wc[NW][kRadixBins];   // per wave: running count of digit d, then the count in earlier waves
+  constexpr int BINS = 1 << RB, BPT = BINS / kSortThreads;   // digits per thread in the per-digit steps
+  static_assert(BPT * kSortThreads == BINS, "RB >= 8");
+  __shared__ int bo[BINS];       // global position of this tile's first item of digit d (n < 2^31)
+  __shared__ int run[BINS];      // items of digit d in the tile
+  __shared__ int lbase[BINS];    // position of digit d's first item in the tile sorted by digit
+  __shared__ int wc[NW][BINS];   // per wave: running count of digit d, then the count in earlier waves
   __shared__ Key lk[TILE];
   __shared__ int32_t lv[TILE];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
   {
-    // digit bases: exclusive scan of the 256 digit totals (n < 2^31, so they fit in int)
-    int v[1] = {(int)dtot[t]}, ex[1], tot[1];
-    block_excl_scan<kSortThreads, 1>(v, ex, tot);
-    bo[t] = (int64_t)ex[0] + offs[(int64_t)t * nblk + blockIdx.x];
+    // digit bases: exclusive scan of the digit totals (n < 2^31, so they fit in int)
+    int x[BPT], ex[BPT], total;
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) x[j] = (int)dtot[t * BPT + j];
+    bins_excl_scan<BPT>(x, ex, total);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) bo[t * BPT + j] = ex[j] + (int)offs[(int64_t)(t * BPT + j) * nblk + blockIdx.x];
   }
 #pragma unroll
-  for (int q = 0; q < NW; ++q) wc[q][t] = 0;
+  for (int q = 0; q < NW; ++q)
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) wc[q][t * BPT + j] = 0;
   __syncthreads();
   const int64_t tile0 = (int64_t)blockIdx.x * TILE, base = tile0 + (int64_t)w * (ITEMS * 64);
   Key kk[ITEMS];
@@ -128,10 +171,10 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
     const Key k = valid ? (Key)src_keys[pos] : (Key)0;
     kk[r] = k;
     vv[r] = valid ? (FIRST ? (int32_t)pos : src_vals[pos]) : 0;
-    const uint32_t d = digit_of(k, shift);
+    const uint32_t d = digit_of<RB>(k, shift);
     uint64_t m = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < RB; ++b) {
       const bool bit = (d >> b) & 1u;
       const uint64_t bal = __ballot(bit);
       m &= bit ? bal : ~bal;
@@ -144,32 +187,37 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
     if (valid && lr == 0) wc[w][d] = before + __popcll(m);
   }
   __syncthreads();
-  {
+  int runs[BPT];
+#pragma unroll
+  for (int j = 0; j < BPT; ++j) {
     // per digit: exclusive scan over the waves, and the tile's total
+    const int dd = t * BPT + j;
     int acc = 0;
 #pragma unroll
     for (int q = 0; q < NW; ++q) {
-      const int c = wc[q][t];
-      wc[q][t] = acc;
+      const int c = wc[q][dd];
+      wc[q][dd] = acc;
       acc += c;
     }
-    run[t] = acc;
+    runs[j] = acc;
+    run[dd] = acc;
   }
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < ITEMS; ++r)
-    if (rk[r] >= 0) rk[r] += wc[w][digit_of(kk[r], shift)];
+    if (rk[r] >= 0) rk[r] += wc[w][digit_of<RB>(kk[r], shift)];
   {
     // the tile sorted by digit: digit d's items start at the exclusive scan of the tile's digit counts
-    int v[1] = {run[t]}, ex[1], tot[1];
-    block_excl_scan<kSortThreads, 1>(v, ex, tot);
-    lbase[t] = ex[0];
+    int ex[BPT], total;
+    bins_excl_scan<BPT>(runs, ex, total);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) lbase[t * BPT + j] = ex[j];
   }
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < ITEMS; ++r) {
     if (rk[r] >= 0) {
-      const int lp = lbase[digit_of(kk[r], shift)] + rk[r];
+      const int lp = lbase[digit_of<RB>(kk[r], shift)] + rk[r];
       lk[lp] = kk[r];
       lv[lp] = vv[r];
     }
@@ -179,8 +227,8 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   const int nvalid = rem < TILE ? (int)rem : TILE;
   for (int j = t; j < nvalid; j += kSortThreads) {
     const Key k = lk[j];
-    const uint32_t d = digit_of(k, shift);
-    const int64_t dst = bo[d] + (j - lbase[d]);
+    const uint32_t d = digit_of<RB>(k, shift);
+    const int64_t dst = (int64_t)bo[d] + (j - lbase[d]);
     if (dst >= 0 && dst < n) {
       dst_keys[dst] = k;
       dst_vals[dst] = lv[j];
@@ -740,8 +788,8 @@ inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void
   s.keys[1] = take(n * 8);
   s.vals[0] = (int32_t*)take(n * 4);
   s.vals[1] = (int32_t*)take(n * 4);
-  s.hist = (int64_t*)take(kRadixBins * ntile * 8);
-  s.dtot = (int64_t*)take(kRadixBins * 8);
+  s.hist = (int64_t*)take(kRadixMaxBins * ntile * 8);
+  s.dtot = (int64_t*)take(kRadixMaxBins * 8);
   s.bsum = (int64_t*)take(nblk * 8);
   s.d_tot = (int64_t*)take(3 * 8);
   s.uniq = (int64_t*)take(n * 8);
@@ -755,27 +803,55 @@ inline int64_t dedup_scratch_bytes(int64_t n, int64_t D, DedupScratch* out, void
   return o;
 }
 
+// Widest digit of a sort with Key keys: 64-bit keys stop at 9 bits to keep the scatter's LDS tile within 64 KiB.
+template <typename Key>
+constexpr int max_digit_bits() { return sizeof(Key) == 8 ? 9 : kRadixMaxBits; }
+
+// Passes of a sort of key_bits-bit Key keys (sort_plan); the result sits in buffer (passes - 1) % 2.
+template <typename Key>
+inline int sort_passes(int key_bits) {
+  int passes, rb;
+  sort_plan(key_bits, max_digit_bits<Key>(), passes, rb);
+  return passes;
+}
+
+// One pass over RB-bit digit p of the keys: histogram, scan, stable scatter from buffer cur (the caller's ids on
+// the first pass) to buffer nxt.
+template <typename Key, int ITEMS, int RB>
+static void radix_pass(const int64_t* ids, int64_t n, int p, int cur, int nxt, DedupScratch& S, hipStream_t st) {
+  const int64_t ntile = cdiv(n, kSortThreads * ITEMS);
+  const int shift = RB * p;
+  Key* kb[2] = {(Key*)S.keys[0], (Key*)S.keys[1]};
+  if (p == 0) {
+    k_radix_hist<int64_t, Key, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
+    k_radix_hist_scan<<<1u << RB, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
+    k_radix_scatter<int64_t, Key, true, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(
+        ids, nullptr, n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
+  } else {
+    k_radix_hist<Key, Key, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
+    k_radix_hist_scan<<<1u << RB, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
+    k_radix_scatter<Key, Key, false, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(
+        kb[cur], S.vals[cur], n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
+  }
+}
+
 // Sort (ids, positions) by id; returns which buffer holds the result.
 template <typename Key, int ITEMS>
 static int radix_sort(const int64_t* ids, int64_t n, int key_bits, DedupScratch& S, hipStream_t st) {
-  const int64_t ntile = cdiv(n, kSortThreads * ITEMS);
-  const int passes = (key_bits + 7) / 8;
-  Key* kb[2] = {(Key*)S.keys[0], (Key*)S.keys[1]};
+  int passes, rb;
+  sort_plan(key_bits, max_digit_bits<Key>(), passes, rb);
   int cur = 0;
   for (int p = 0; p < passes; ++p) {
-    const int shift = 8 * p;
     const int nxt = p == 0 ? 0 : cur ^ 1;
-    if (p == 0) {
-      k_radix_hist<int64_t, Key, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
-      k_radix_hist_scan<<<kRadixBins, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
-      k_radix_scatter<int64_t, Key, true, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(
-          ids, nullptr, n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
-    } else {
-      k_radix_hist<Key, Key, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
-      k_radix_hist_scan<<<kRadixBins, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
-      k_radix_scatter<Key, Key, false, ITEMS><<<(unsigned)ntile, kSortThreads, 0, st>>>(
-          kb[cur], S.vals[cur], n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
+    if constexpr (max_digit_bits<Key>() >= 10) {
+      if (rb == 10) {
+        radix_pass<Key, ITEMS, 10>(ids, n, p, cur, nxt, S, st);
+        cur = nxt;
+        continue;
+      }
     }
+    if (rb == 9) radix_pass<Key, ITEMS, 9>(ids, n, p, cur, nxt, S, st);
+    else radix_pass<Key, ITEMS, 8>(ids, n, p, cur, nxt, S, st);
     cur = nxt;
   }
   return cur;
@@ -958,7 +1034,9 @@ extern "C" int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const
 // chunks; the scratch then holds the plan (sorted positions, segment starts, first occurrences, chunk plan, U).
 // elr_segment_sum_plan sums a gradient batch over that plan without sorting again.  The sorted result lives in the
 // scratch buffer that the last radix pass wrote: with p passes, buffer (p - 1) % 2.
-static int plan_result_buffer(int key_bits) { return ((key_bits + 7) / 8 - 1) % 2; }
+static int plan_result_buffer(int key_bits) {
+  return ((key_bits <= 32 ? elr::sort_passes<uint32_t>(key_bits) : elr::sort_passes<uint64_t>(key_bits)) - 1) % 2;
+}
 
 extern "C" int64_t elr_dedup_plan_bytes(int64_t n, int64_t D) {
   using namespace elr;

@@ -176,6 +176,25 @@ def test_gpu_unique_matches_torch(dev, case):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('key_bits', [1, 8, 9, 12, 17, 20, 24, 27, 30, 32, 33, 40, 63])
+@pytest.mark.parametrize('n', [70001, (1 << 21) + 3])
+def test_gpu_unique_every_digit_width(dev, key_bits, n):
+    """The sort takes 8-, 9- or 10-bit digits (fewer passes: 27-bit keys in 3 passes of 9 bits, 30-bit keys in 3 of
+    10); for each key width from the caller's bound, both tile sizes (below and above 2^21 ids) give torch.unique's
+    rows and inverse.  Ids are spread over the whole width, with duplicates and the extreme keys 0 and 2^b - 1."""
+    from elara_amd.dedup import unique
+    rng = np.random.default_rng(key_bits * 7 + n % 5)
+    hi = (1 << key_bits) - 1
+    ids = rng.integers(0, hi, n, dtype=np.int64, endpoint=True)
+    ids[rng.integers(0, n, n // 3)] = ids[rng.integers(0, n, n // 3)]     # duplicates
+    ids[:2], ids[-1] = [0, hi], hi
+    print(f'[gpu-test] unique key_bits={key_bits} n={n}', flush=True)
+    u, inv = unique(torch.from_numpy(ids).to(dev), bound=hi + 1)
+    tu, tinv = torch.unique(torch.from_numpy(ids), return_inverse=True)
+    assert torch.equal(u.cpu(), tu) and torch.equal(inv.cpu(), tinv)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize('D', [128, 64, 30, 200])
 def test_gpu_embedding_backward_matches_oracle(dev, D):
     from elara_amd.dedup import embedding_dense_backward
@@ -266,7 +285,8 @@ def test_gpu_aten_golden_cases(dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('D,case', [(128, 'zipf'), (64, 'long'), (30, 'zipf'), (128, 'big_ids')])
+@pytest.mark.parametrize('D,case', [(128, 'zipf'), (64, 'long'), (30, 'zipf'), (128, 'big_ids'), (128, 'bits27'),
+                                    (64, 'bits17')])
 def test_gpu_dedup_plan_matches_unique_and_backward(dev, D, case):
     """unique_plan + segment_sum_plan (one sort reused by the sum) give torch.unique's rows and the oracle's sums,
     into rows u or perm[u] (a permutation, and a scatter into a larger output)."""
@@ -280,6 +300,11 @@ def test_gpu_dedup_plan_matches_unique_and_backward(dev, D, case):
         ids = np.concatenate([np.full(5000, 77), rng.integers(0, 3000, 30000)])[rng.permutation(35000)].astype(np.int64)
         g = rng.standard_normal((ids.size, D)).astype(np.float32)
         bound = 3000
+    elif case in ('bits27', 'bits17'):       # sorts of 3 passes of 9 bits, 2 passes of 9 bits
+        bound = 1 << int(case[4:])
+        ids = rng.integers(0, bound, 60000).astype(np.int64)
+        ids[rng.integers(0, ids.size, 20000)] = ids[rng.integers(0, ids.size, 20000)]
+        g = rng.standard_normal((ids.size, D)).astype(np.float32)
     else:
         ids = (rng.integers(0, 2**40, 40000) // 5 * 5).astype(np.int64)
         g = rng.standard_normal((ids.size, D)).astype(np.float32)
