@@ -546,10 +546,12 @@ def mode_c5(args):
         if s == W:
             torch.cuda.synchronize()
             mark['stats'] = dict(st.stats)
+            mark['wait'] = st.wait_s
             mark['t0'] = time.perf_counter()
     torch.cuda.synchronize()
     if W == 0:
         mark['stats'] = dict(st.stats)
+        mark['wait'] = st.wait_s
         mark['t0'] = time.perf_counter()
     run(st, batches, lambda j: gs[j % 8], on_step=on_step)
     torch.cuda.synchronize()
@@ -564,8 +566,11 @@ def mode_c5(args):
                   'arenas': 'host' if host else 'hbm', 'mat_top': mt, 'log_top': lt,
                   'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
                   'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, None,
-                 extra={'steps_per_s': steps / el, 'stats': s, 'note': 'step_GBps not reported for C5 (mixed '
-                        'kernels; per-kernel bytes in profiles/)'})
+                 extra={'steps_per_s': steps / el, 'stats': s,
+                        'host_wait_us_per_step': (st.wait_s - mark['wait']) / steps * 1e6,
+                        'note': 'step_GBps not reported for C5 (mixed kernels; per-kernel bytes in profiles/); '
+                                'host_wait_us_per_step: time the host spends waiting for the GPU at the plan\'s '
+                                'synchronisation (near 0: the host is the bottleneck)'})
 
 
 def copy_calibration(args):

@@ -26,6 +26,7 @@ driven by another implementation of the kernels (the oracle's) for comparison.
 """
 import ctypes
 import gc
+import time
 
 import torch
 
@@ -268,6 +269,7 @@ class ElaraStep:
         self.link_blocks = 32   # blocks per launch of the link part (measured best of 16-128 at C5 with host arenas)
         self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs', 'barriers')}
+        self.wait_s = 0.0   # host time spent waiting for the GPU at the plans' synchronisations
         self._deferred = []
         self._pin = None
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
@@ -354,7 +356,9 @@ class ElaraStep:
         deferred, self._deferred = self._deferred, []
 
         def finish():
+            t0 = time.perf_counter()
             ev.synchronize()
+            self.wait_s += time.perf_counter() - t0
             vals = host.tolist()
             for (_, cb), v in zip(deferred, vals[n:]):
                 cb(v)

@@ -204,7 +204,7 @@ int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* gra
  * Same arguments and results as elr_adam_dedup, without the scratch arguments: the scratch is a device array of
  * ELR_NOALLOC_SCRATCH_BYTES inside the library, one per GPU it runs on, held until the process ends.  Calls with
  * elr_dedup_scratch_bytes(n, D) > ELR_NOALLOC_SCRATCH_BYTES return ELR_ECAPACITY before any launch (at D = 128:
- * n up to about 589,000 occurrences).  No hipMalloc / hipFree or allocating library call is made.  Every call on
+ * n up to about 558,000 occurrences).  No hipMalloc / hipFree or allocating library call is made.  Every call on
  * one GPU uses that GPU's array: calls that overlap in time on one GPU (two streams or threads) race.  The device
  * is the current one (hipGetDevice); `stream` must belong to it. */
 #define ELR_NOALLOC_SCRATCH_BYTES (64ll << 20)
@@ -320,7 +320,8 @@ int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots, int64_t n_
  *                   j = seg_aux[g] + (k - seg_start) read from logs[L_ids[j*K + q]] at step L_steps[j*K + q] for
  *                   q < L_cnt[j] (elr_dir_a's replay inputs);
  *   ELR_ASM_GATHER  the state held in the MAT arena at mat[loc[row]].
- * D in {64, 128, 256, 512}, K <= 4.  Rows with out-of-range inputs are skipped.
+ * Any D >= 1 (wave-per-row kernels for D = 64, 128, 256, 512 with 16-byte aligned arrays, generic ones otherwise);
+ * 1 <= K <= 8 (ELR_EUNSUPPORTED above).  Rows with out-of-range inputs are skipped.
  * ------------------------------------------------------------------------------------------------------- */
 #define ELR_ASM_INIT 0
 #define ELR_ASM_REPLAY 1
@@ -369,10 +370,10 @@ int elr_assemble(const elr_assemble_args* args, void* stream);
  * reference's order of writes: the evicted slots and their glog rows are read before the admissions reuse them.
  * The row moves and history records ride on the Adam launches: the hits record and update in place, and the
  * admitted, compacted and transient rows go from the work array straight into their pool / MAT slots (the work
- * array is not written back).  D = 64, 128, 256 or 512 (else ELR_EUNSUPPORTED), every array 16-byte aligned.
- * Index arrays are int64; arenas may be device or mapped pinned host memory (elr_host_device_ptr).  Items whose
- * index is out of range are skipped.  ELR_EINVAL for inconsistent bounds, a misaligned array or a NULL array that
- * a nonzero count needs.
+ * array is not written back).  Any D >= 1: wave-per-row kernels for D = 64, 128, 256 or 512 with every array
+ * 16-byte aligned, generic kernels otherwise.  Index arrays are int64; arenas may be device or mapped pinned host
+ * memory (elr_host_device_ptr).  Items whose index is out of range are skipped.  ELR_EINVAL for inconsistent
+ * bounds or a NULL array that a nonzero count needs.
  * ------------------------------------------------------------------------------------------------------- */
 #define ELR_RANK_HIT 0
 #define ELR_RANK_NADM 1
