@@ -59,6 +59,8 @@ SIGNATURES = {
     'elr_plan_scratch_bytes': (c_i64, [c_i64, c_i64]),
     'elr_plan_admit': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_i64, c_i64, c_i64, c_i64, ctypes.c_int,
                                       c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
+    'elr_plan_admit_slots': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_i64, c_i64, c_i64, c_i64,
+                                            ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'elr_assemble': (ctypes.c_int, [c_vp, c_vp]),
     'elr_step_update': (ctypes.c_int, [c_vp, c_vp]),
     'elr_dedup_plan_bytes': (c_i64, [c_i64, c_i64]),
@@ -106,6 +108,12 @@ class AssembleArgs(ctypes.Structure):
                 ('L_cnt', c_vp), ('nL', c_i64), ('logs', c_vp), ('nlogs', c_i64), ('table', c_vp), ('recip', c_vp),
                 ('table_rows', c_i64), ('mat', c_vp), ('mat_rows', c_i64), ('loc', c_vp), ('R', c_i64)]
 
+
+
+class SlotsArgs(ctypes.Structure):
+    """elr_slots_args: the pool-slot bookkeeping of a step's admissions (srm2/elara.py:345-347, 368)."""
+    _fields_ = [('free_stack', c_vp), ('n_free', c_i64), ('ev_slot', c_vp), ('nev', c_i64), ('keep', c_vp),
+                ('nkeep', c_i64), ('adm_slots', c_vp), ('dyn_out', c_vp)]
 
 
 class UpdateArgs(ctypes.Structure):
@@ -202,3 +210,9 @@ def dptr(t):
 
 def scalars8(vals):
     return (ctypes.c_float * 8)(*vals)
+
+
+def split_empty(dev, dtype, sizes):
+    """Uninitialised 1-D tensors of the given sizes, views of one allocation: one allocator call and one split for a
+    launch's outputs of one dtype (fewer Python-level tensor constructions than an allocation each)."""
+    return torch.empty(sum(sizes), dtype=dtype, device=dev).split(list(sizes))

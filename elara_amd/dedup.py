@@ -94,9 +94,10 @@ def unique_plan(ids, D, bound=None):
     return u, plan
 
 
-def unique_plan_async(ids, D, bound=None):
+def unique_plan_async(ids, D, bound=None, nu_out=None):
     """unique_plan without reading the unique count: returns (u_full, plan, nu) with u_full [n] whose first nu
-    entries are the unique ids, nu the count on the device (None when n == 0).  Set plan.U once nu is known."""
+    entries are the unique ids, nu the count on the device (None when n == 0).  Set plan.U once nu is known.
+    nu_out (int64 [1] on the device, optional): where the count goes, else a new tensor."""
     flat = _ids(ids)
     n = flat.numel()
     dev = flat.device
@@ -111,7 +112,9 @@ def unique_plan_async(ids, D, bound=None):
         _lib.check(nbytes, 'elr_dedup_plan_bytes')
     plan.buf, plan.nbytes = torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
     u = torch.empty(n, dtype=I64, device=dev)
-    nu = torch.empty(1, dtype=I64, device=dev)
+    if nu_out is not None and not (nu_out.dtype == I64 and nu_out.device == dev and nu_out.numel() == 1):
+        raise RuntimeError(f'nu_out must be an int64 tensor of one element on {dev}')
+    nu = nu_out if nu_out is not None else torch.empty(1, dtype=I64, device=dev)
     with _lib.on_device(dev):
         rc = _lib.lib().elr_dedup_plan(_lib.ptr(flat), n, plan.key_bits, _lib.ptr(u), None, _lib.ptr(nu),
                                        _lib.ptr(plan.buf), nbytes, int(D), _lib.stream_of(flat))

@@ -11,6 +11,7 @@ reference's dtypes and shapes.  Both calls run as HIP kernels (elara_amd/csrc/di
 stream, with no host synchronisation: the allocator counters stay in device memory.
 """
 import ctypes
+import weakref
 
 import torch
 
@@ -25,18 +26,20 @@ _STATE_CACHE = {}
 
 def _state(st, pv):
     """The validated DirState / DirParams of (st, pv).  A directory is called once or twice per step with the same
-    17 tensors, so the structures are kept per (tensor addresses and sizes, pv) and validated once."""
+    17 tensor objects, so the structures are kept per (tensor identities, pv) and validated once.  The entry holds
+    weak references to the tensors and is used only while each one is still the very object it was made from
+    (a tensor's storage cannot change address without a new tensor object, except by in-place resizing, which the
+    directory's fixed-size arrays never see)."""
     if len(st) != 17 or len(pv) != 8:
         raise RuntimeError('st must hold the 17 directory tensors and pv the 8 parameters')
-    key = (tuple((t.data_ptr(), t.numel(), t.dtype, t.device, t.is_contiguous()) for t in st),
-           tuple(int(x) for x in pv))
+    key = (tuple(map(id, st)), tuple(int(x) for x in pv))
     hit = _STATE_CACHE.get(key)
-    if hit is not None:
-        return hit
+    if hit is not None and all(r() is t for r, t in zip(hit[0], st)):
+        return hit[1]
     res = _state_checked(st, pv)
     if len(_STATE_CACHE) >= 16:
         _STATE_CACHE.clear()
-    _STATE_CACHE[key] = res
+    _STATE_CACHE[key] = (tuple(weakref.ref(t) for t in st), res)
     return res
 
 
@@ -58,6 +61,8 @@ def _state_checked(st, pv):
 
 
 def _idx(t, dev, dtype=I64):
+    if isinstance(t, torch.Tensor) and t.dtype == dtype and t.device == dev and t.dim() == 1 and t.is_contiguous():
+        return t
     t = torch.as_tensor(t, device=dev)
     if t.device != dev:
         raise RuntimeError(f'index tensors must be on {dev}')
@@ -78,9 +83,14 @@ def elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
     nh, nL, nev = hs.numel(), L_row.numel(), ev_slot.numel()
     if L_cnt.numel() != nL:
         raise RuntimeError('L_cnt must have one count per L row')
-    e = lambda *shape, dt=I64: torch.empty(*shape, dtype=dt, device=dev)  # noqa: E731
-    out = [e(nL, K, dt=I32), e(nL, K, dt=I32), e(nh), e(nh), e(nev), e(nev, dt=torch.bool), e(nev, K), e(nev), e(nev)]
-    scratch, nbytes = _scratch(dev, nev, 0)
+    nbytes = int(_lib.lib().elr_dir_scratch_bytes(nev, 0))
+    if nbytes < 0:
+        _lib.check(nbytes, 'elr_dir_scratch_bytes')
+    i32 = _lib.split_empty(dev, I32, (nL * K, nL * K))
+    h, hj, er, evl, evf, evd = _lib.split_empty(dev, I64, (nh, nh, nev, nev * K, nev, nev))
+    out = [i32[0].view(nL, K), i32[1].view(nL, K), h, hj, er, torch.empty(nev, dtype=torch.bool, device=dev),
+           evl.view(nev, K), evf, evd]
+    scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     p = _lib.ptr
     with _lib.on_device(dev):
         rc = _lib.lib().elr_dir_a(ctypes.byref(S), ctypes.byref(P), p(hs), nh, p(L_row), p(L_cnt), nL,
@@ -96,10 +106,12 @@ def elara_dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s):
     na, nc = a_rows.numel(), c_rows.numel()
     if a_k.numel() != na or c_cnt.numel() != nc:
         raise RuntimeError('a_k must match a_rows and c_cnt must match c_rows')
-    a_ids = torch.empty(na, dtype=I64, device=dev)
-    c_slots = torch.empty(nc, dtype=I64, device=dev)
+    nbytes = int(_lib.lib().elr_dir_scratch_bytes(0, nc)) if na or nc else 0
+    if nbytes < 0:
+        _lib.check(nbytes, 'elr_dir_scratch_bytes')
+    a_ids, c_slots = _lib.split_empty(dev, I64, (na, nc))
     if na or nc:
-        scratch, nbytes = _scratch(dev, 0, nc)
+        scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         p = _lib.ptr
         with _lib.on_device(dev):
             rc = _lib.lib().elr_dir_b(ctypes.byref(S), ctypes.byref(P), p(a_rows), p(a_k), na, p(c_rows),

@@ -5,6 +5,7 @@ sorted stably by class, the dynamic pool slots partitioned into expired / preemp
 block of counts for the host (one small read, the plan's only synchronisation in the common case).
 """
 import ctypes
+import weakref
 from collections import namedtuple
 
 import torch
@@ -22,11 +23,32 @@ PlanClass = namedtuple('PlanClass', 'cls flags sl c order rank dyn_out counts u_
 
 
 def _dev_i64(t, dev):
+    if t.dtype == I64 and t.device == dev and t.is_contiguous():
+        return t
     return t.to(device=dev, dtype=I64).contiguous()
 
 
+_CHECKED = {}
+
+
+def _check_state(dev, named):
+    """dtype / device / contiguity of the planner's state tensors, checked once per set of tensor objects (a step
+    passes the same directory tensors to every plan); weak references make sure the entry is used only while each
+    tensor is still the very object that was checked."""
+    key = tuple(id(t) for t, _, _ in named)
+    hit = _CHECKED.get(key)
+    if hit is not None and all(r() is t for r, (t, _, _) in zip(hit, named)):
+        return
+    for t, dt, name in named:
+        if t.dtype != dt or t.device != dev or not t.is_contiguous():
+            raise RuntimeError(f'plan_classify: {name} must be a contiguous {dt} tensor on {dev}')
+    if len(_CHECKED) >= 16:
+        _CHECKED.clear()
+    _CHECKED[key] = tuple(weakref.ref(t) for t, _, _ in named)
+
+
 def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
-                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None):
+                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None, counts_out=None):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -45,7 +67,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
 
     carry: the 'carry' residency (srm2/elara.py:221, 231-233): a missing row is admitted when it appears in the next
     batches, and every unprotected dynamic slot is expired; otherwise 'ttl'.  live (int64 [1], optional): the live
-    log-entry counter, copied into counts[15] for the host."""
+    log-entry counter, copied into counts[15] for the host.  counts_out (int64 [17] on the device, optional): where
+    the counts go (e.g. a buffer the caller reads together with other values), else a new tensor."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -53,24 +76,28 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     nexts = [_dev_i64(x, dev) for x in u_nexts if x.numel()]
     if len(nexts) > 4:
         raise RuntimeError('plan_classify: at most 4 next batches')
-    for t, dt, name in ((slot_of, I32, 'slot_of'), (last_seen, I32, 'last_seen'), (code, I8, 'code'),
-                        (kthr, I8, 'kthr'), (toff, I64, 'toff'), (slot_row, I64, 'slot_row'),
-                        (mat_top, I64, 'mat_top'), (log_top, I64, 'log_top')) + (
-                            ((live, I64, 'live'),) if live is not None else ()):
-        if t.dtype != dt or t.device != dev or not t.is_contiguous():
-            raise RuntimeError(f'plan_classify: {name} must be a contiguous {dt} tensor on {dev}')
-    if loc is not None and (loc.dtype != I32 or loc.device != dev or not loc.is_contiguous()):
-        raise RuntimeError(f'plan_classify: loc must be a contiguous {I32} tensor on {dev}')
+    _check_state(dev, ((slot_of, I32, 'slot_of'), (last_seen, I32, 'last_seen'), (code, I8, 'code'),
+                       (kthr, I8, 'kthr'), (toff, I64, 'toff'), (slot_row, I64, 'slot_row'),
+                       (mat_top, I64, 'mat_top'), (log_top, I64, 'log_top'))
+                 + (((live, I64, 'live'),) if live is not None else ()) + (((loc, I32, 'loc'),) if loc is not None
+                                                                           else ()))
+    if counts_out is not None and not (counts_out.dtype == I64 and counts_out.device == dev
+                                       and counts_out.is_contiguous() and counts_out.numel() == NCOUNTS):
+        raise RuntimeError(f'plan_classify: counts_out must be a contiguous {I64} tensor of {NCOUNTS} on {dev}')
     dyn = _dev_i64(dyn, dev)
     n, nd = u.numel(), dyn.numel()
-    out = PlanClass(torch.empty(n, dtype=I8, device=dev), torch.empty(n, dtype=torch.uint8, device=dev),
-                    torch.empty(n, dtype=I32, device=dev), torch.empty(n, dtype=I8, device=dev),
-                    torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
-                    torch.empty(2 * nd, dtype=I64, device=dev), torch.empty(NCOUNTS, dtype=I64, device=dev),
-                    torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
-                    torch.empty(n, dtype=I64, device=dev), torch.empty(n, dtype=I64, device=dev),
-                    torch.empty(n, dtype=I32, device=dev),
-                    torch.empty(n, dtype=I64, device=dev) if loc is not None else None)
+    nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
+    if nbytes < 0:
+        _lib.check(nbytes, 'elr_plan_scratch_bytes')
+    o64 = _lib.split_empty(dev, I64, (n, n, 2 * nd, 0 if counts_out is not None else NCOUNTS, n, n, n, n,
+                                      n if loc is not None else 0))
+    o32 = _lib.split_empty(dev, I32, (n, n))
+    o8 = _lib.split_empty(dev, I8, (n, n))
+    flags = torch.empty(n, dtype=torch.uint8, device=dev)
+    scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
+    parts = [o8[0], flags, o32[0], o8[1], o64[0], o64[1], o64[2], counts_out if counts_out is not None else o64[3],
+             o64[4], o64[5], o64[6], o64[7], o32[1], o64[8] if loc is not None else None]
+    out = PlanClass(*parts)
     p = _lib.ptr
     pin = _lib.PlanIn()
     pin.u, pin.n = u.data_ptr(), n
@@ -93,8 +120,6 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
             raise RuntimeError(f'plan_classify: next_bits must be a contiguous {I32} tensor of R rows on {dev}')
         pin.next_bits, pin.next_mask = next_bits.data_ptr(), int(next_mask) & 0xFFFFFFFF
     pout = _lib.PlanOut(*[t.data_ptr() if t is not None else None for t in out])
-    nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
-    scratch = torch.empty(max(nbytes, 8), dtype=torch.uint8, device=dev)
     with _lib.on_device(dev):
         rc = _lib.lib().elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,
                                           _lib.stream_of(u))
@@ -138,3 +163,31 @@ def plan_admit(adm_rows, adm_slots, lazy_n, evl, s, n0, C, R, K, code, slot_of, 
                                        int(R), int(K), p(code), p(slot_of), p(slot_row), p(adm_c0), p(rj), p(rok),
                                        p(pstep), _lib.stream_of(code))
     _lib.check(rc, 'elr_plan_admit')
+
+
+def plan_admit_slots(free_stack, n_free, ev_slot, keep, adm_rows, lazy_n, evl, s, n0, C, R, K, code, slot_of, slot_row,
+                     adm_c0, rj, rok, pstep, dyn_out):
+    """plan_admit with the pool-slot bookkeeping before it, in one launch (elr_plan_admit_slots, srm2/elara.py:345-347,
+    352-368): the evicted slots ev_slot are pushed on the free stack free_stack[:n_free] (updated in place; new depth
+    n_free + nev - n_adm), its top n_adm entries go to the rows adm_rows, and dyn_out[:nkeep + n_adm] receives keep
+    followed by those slots.  Returns the admitted slots (int64 [n_adm])."""
+    dev = code.device
+    n_adm, nev, nkeep = adm_rows.numel(), ev_slot.numel(), keep.numel()
+    for t, name in ((free_stack, 'free_stack'), (dyn_out, 'dyn_out'), (ev_slot, 'ev_slot'), (keep, 'keep'),
+                    (adm_rows, 'adm_rows')):
+        if t.dtype != I64 or t.device != dev or not t.is_contiguous():
+            raise RuntimeError(f'plan_admit_slots: {name} must be a contiguous {I64} tensor on {dev}')
+    if free_stack.numel() < n_free + nev or dyn_out.numel() < nkeep + n_adm or n_adm > n_free + nev:
+        raise RuntimeError('plan_admit_slots: stack or output too small, or more admissions than free slots')
+    _check_state(dev, ((code, I8, 'code'), (slot_of, I32, 'slot_of'), (slot_row, I64, 'slot_row'),
+                       (adm_c0, I8, 'adm_c0'), (rj, I8, 'rj'), (rok, I8, 'rok'), (pstep, I32, 'pstep')))
+    adm_slots = torch.empty(n_adm, dtype=I64, device=dev)
+    a = _lib.SlotsArgs(free_stack.data_ptr(), int(n_free), ev_slot.data_ptr(), nev, keep.data_ptr(), nkeep,
+                       adm_slots.data_ptr(), dyn_out.data_ptr())
+    p = _lib.ptr
+    with _lib.on_device(dev):
+        rc = _lib.lib().elr_plan_admit_slots(ctypes.byref(a), p(adm_rows), n_adm, int(lazy_n), int(bool(evl)), int(s),
+                                             int(n0), int(C), int(R), int(K), p(code), p(slot_of), p(slot_row),
+                                             p(adm_c0), p(rj), p(rok), p(pstep), _lib.stream_of(code))
+    _lib.check(rc, 'elr_plan_admit_slots')
+    return adm_slots

@@ -36,8 +36,8 @@ from .dedup import segment_sum_plan, unique_plan, unique_plan_async
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
-from .planner import (CNT_BAD, CNT_EXP, CNT_LIVE, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT,
-                      classify_from_flags, plan_admit, plan_classify)
+from .planner import (CNT_BAD, CNT_EXP, CNT_LIVE, CNT_LOG_TOP, CNT_MAT_TOP, CNT_PRE, F_ADMIT, F_NEXT, NCOUNTS,
+                      classify_from_flags, plan_admit, plan_admit_slots, plan_classify)
 from .rows import copy_rows, glog_put, glog_take, mark_rows
 
 I8, I32, I64 = torch.int8, torch.int32, torch.int64
@@ -72,8 +72,10 @@ class HipBackend:
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
 
-    def unique_async(self, ids, bound=None):
-        return unique_plan_async(ids, self.D, bound)
+    def unique_async(self, ids, bound=None, nu_out=None):
+        return unique_plan_async(ids, self.D, bound, nu_out)
+
+    sync_counts = True   # takes counts_out / nu_out: the plan's counts and the deferred counts in one device buffer
 
     batch_ring = True   # keeps the planner's ring of loaded batches (ElaraStep.next_bits)
 
@@ -85,6 +87,9 @@ class HipBackend:
 
     def plan_admit(self, *args):
         plan_admit(*args)
+
+    def plan_admit_slots(self, *args):
+        return plan_admit_slots(*args)
 
     def segsum(self, g_occ, dplan, U, perm=None):
         return segment_sum_plan(g_occ, dplan, torch.empty(U, self.D, device=g_occ.device), perm)
@@ -243,6 +248,15 @@ class ElaraStep:
         self.free = torch.arange(C - 1, n0 - 1, -1, dtype=I64, device=d)
         self.n_free = C - n0
         self.dyn_slots = torch.empty(0, dtype=I64, device=d)
+        # with a backend that keeps the free stack and the dynamic slot list in place (plan_admit_slots), their
+        # storage: the stack holds at most C entries, the slot list at most C - n0
+        self._slots_in_place = getattr(self.be, 'plan_admit_slots', None) is not None
+        if self._slots_in_place:
+            self._free_buf = torch.empty(C, dtype=I64, device=d)
+            self._free_buf[:C - n0] = self.free
+            self.free = self._free_buf[:C - n0]
+            self._dyn_buf = torch.empty(max(C - n0, 1), dtype=I64, device=d)
+            self.dyn_slots = self._dyn_buf[:0]
         self.adm_c0 = torch.full((C,), -1, dtype=I8, device=d)
         self.rj = torch.zeros(C, dtype=I8, device=d)
         self.rok = torch.zeros(C, dtype=I8, device=d)
@@ -272,6 +286,14 @@ class ElaraStep:
         self.wait_s = 0.0   # host time spent waiting for the GPU at the plans' synchronisations
         self._deferred = []
         self._pin = None
+        # one device buffer for everything a plan's synchronisation reads: the class counts in [0, NCOUNTS), the
+        # unique counts of batches loaded ahead in a ring after them (each read at the next synchronisation), so
+        # the read is a single copy with no gathering kernel
+        sync = d.type == 'cuda' and getattr(self.be, 'sync_counts', False)
+        self._sync = torch.zeros(64, dtype=I64, device=d) if sync else None
+        self._sync_next = NCOUNTS
+        self.dedup_ahead = True   # run() sorts the batches loaded ahead on a second stream (dedup_stream)
+        self._side = None
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
@@ -327,6 +349,25 @@ class ElaraStep:
         """Read the device int64 scalar t at the next host synchronisation and pass it to cb."""
         self._deferred.append((t, cb))
 
+    def dedup_stream(self):
+        """The stream run() queues the dedup of the batches loaded ahead on (a stream of default priority, made on
+        first use), or None to keep it on the current stream: with the HIP backend unless dedup_ahead is False."""
+        if not (self.dedup_ahead and self.d.type == 'cuda' and getattr(self.be, 'sync_counts', False)):
+            return None
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=self.d)
+        return self._side
+
+    def count_slot(self):
+        """A device int64 [1] for a count the next synchronisation reads (defer_count), inside the plan's sync buffer;
+        None without one.  The ring holds 64 - NCOUNTS slots, far more than the counts deferred between two
+        synchronisations."""
+        if self._sync is None:
+            return None
+        i = self._sync_next
+        self._sync_next = i + 1 if i + 1 < self._sync.numel() else NCOUNTS
+        return self._sync[i:i + 1]
+
     def flush_deferred(self):
         """One host synchronisation that resolves every deferred count (counted in stats like any other)."""
         self._host_list(torch.zeros(0, dtype=I64, device=self.d))
@@ -345,7 +386,15 @@ class ElaraStep:
             return lambda: vals
         self.stats['syncs'] += 1
         n = t.numel()
-        dev = torch.cat([t.reshape(-1).to(I64)] + [x.reshape(-1) for x, _ in self._deferred])
+        sb = self._sync
+        if sb is not None and t.data_ptr() == sb.data_ptr() and all(
+                x.data_ptr() - sb.data_ptr() in range(0, sb.numel() * 8, 8) for x, _ in self._deferred):
+            # everything to read lies in the sync buffer: copy it whole, pick the deferred values by offset
+            dev = sb
+            picks = list(range(n)) + [(x.data_ptr() - sb.data_ptr()) // 8 for x, _ in self._deferred]
+        else:
+            dev = torch.cat([t.reshape(-1).to(I64)] + [x.reshape(-1) for x, _ in self._deferred])
+            picks = None
         m = dev.numel()
         if self._pin is None or self._pin.numel() < m:
             self._pin = torch.empty(max(m, 64), dtype=I64, pin_memory=True)
@@ -360,6 +409,8 @@ class ElaraStep:
             ev.synchronize()
             self.wait_s += time.perf_counter() - t0
             vals = host.tolist()
+            if picks is not None:
+                vals = [vals[i] for i in picks]
             for (_, cb), v in zip(deferred, vals[n:]):
                 cb(v)
             return vals[:n]
@@ -389,6 +440,8 @@ class ElaraStep:
         if self.next_bits is not None:
             ring = dict(next_bits=self.next_bits,
                         next_mask=sum(1 << ((s + k) % 32) for k in range(1, self.depth)))
+        if self._sync is not None:
+            ring['counts_out'] = self._sync[:NCOUNTS]
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
                                    self.st_mode == 'T', self.loc, self.R, carry=self.dyn == 'carry', live=self.live,
@@ -483,19 +536,27 @@ class ElaraStep:
          p.ev_dyn) = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s)
         p.ev_slot = ev_slot
         # admissions (srm2/elara.py:345-367): admitted N, L, F rows take slots from the free stack's top
-        pool_free = torch.cat([self.free, ev_slot])
-        nf = self.n_free + nev
-        adm_slots = pool_free[nf - n_adm:]
-        self.free = pool_free[:nf - n_adm]
-        self.n_free = nf - n_adm
-        p.adm_slots = adm_slots
         lazy_n = nNa + nLa
         p.lazy_n = lazy_n
+        nf = self.n_free + nev
+        if self._slots_in_place:   # the stack push, the admissions and the new slot list in one launch
+            adm_slots = self.be.plan_admit_slots(self._free_buf, self.n_free, ev_slot, keep_dyn,
+                                                 u_ord[rs(R_NADM, R_FADM)], lazy_n, self.evl, s, self.n0, self.C,
+                                                 self.R, K, self.code, self.slot_of, self.slot_row, self.adm_c0,
+                                                 self.rj, self.rok, self.pstep, self._dyn_buf)
+            self.free = self._free_buf[:nf - n_adm]
+            self.dyn_slots = self._dyn_buf[:keep_dyn.numel() + n_adm]
+        else:
+            pool_free = torch.cat([self.free, ev_slot])
+            adm_slots = pool_free[nf - n_adm:]
+            self.free = pool_free[:nf - n_adm]
+            self.be.plan_admit(u_ord[rs(R_NADM, R_FADM)], adm_slots, lazy_n, self.evl, s, self.n0, self.C, self.R,
+                               K, self.code, self.slot_of, self.slot_row, self.adm_c0, self.rj, self.rok, self.pstep)
+            self.dyn_slots = torch.cat([keep_dyn, adm_slots])
+        self.n_free = nf - n_adm
+        p.adm_slots = adm_slots
         if lazy_n and self.evl:
             p.adm_rec_slot = adm_slots[:lazy_n]   # their resident histories start at entry 0 of slot - n0
-        self.be.plan_admit(u_ord[rs(R_NADM, R_FADM)], adm_slots, lazy_n, self.evl, s, self.n0, self.C, self.R, K,
-                           self.code, self.slot_of, self.slot_row, self.adm_c0, self.rj, self.rok, self.pstep)
-        self.dyn_slots = torch.cat([keep_dyn, adm_slots])
         # non-resident lazy rows: append (stay L, entry index = current count) or compact (to M)
         p.a_ids, p.c_slots = self.be.dir_b(st, pv, u_ord[rs(R_NAPP, R_LAPP)], c_ord[rs(R_NAPP, R_LAPP)],
                                            u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)], s)
@@ -689,12 +750,40 @@ def run(step, batches, grads, steps=None, on_step=None, freeze_gc=True):
 
 def _run(step, batches, grads, steps, on_step):
     S = len(batches) if steps is None else steps
-    U, PLANS = {}, {}
+    U, PLANS, AHEAD = {}, {}, {}
     dev = step.d
+    side = step.dedup_stream()
 
-    def load(j):
-        # the batch's unique count is read at the next host synchronisation (the plan's), not here
-        u, dplan, nu = step.be.unique_async(batches[j].to(dev), step.R)
+    def dedup(j):
+        """Batch j's dedup plan.  With a side stream it is queued there one step before the batch is observed, so
+        that its sort runs beside the next step's kernels; the tensors it makes are used on the main stream later
+        (record_stream keeps the allocator from reusing them before that work is done)."""
+        src = batches[j]
+        ids = src.to(dev)
+        slot = step.count_slot()
+        kw = {} if slot is None else {'nu_out': slot}
+        if side is None:
+            AHEAD[j] = (*step.be.unique_async(ids, step.R, **kw), None)
+            return
+        main = torch.cuda.current_stream(dev)
+        if src.device != ids.device or src.data_ptr() != ids.data_ptr():
+            side.wait_stream(main)   # the copy that made ids
+        with torch.cuda.stream(side):
+            u, dplan, nu = step.be.unique_async(ids, step.R, **kw)
+            ev = torch.cuda.Event()
+            ev.record()
+        ids.record_stream(side)
+        for t in (u, dplan.buf, nu if slot is None else None):
+            if t is not None:
+                t.record_stream(main)
+        AHEAD[j] = (u, dplan, nu, ev)
+
+    def observe(j):
+        """Mark batch j's rows (the lookahead) on the main stream, its unique count read at the next host
+        synchronisation (the plan's)."""
+        u, dplan, nu, ev = AHEAD.pop(j)
+        if ev is not None:
+            torch.cuda.current_stream(dev).wait_event(ev)
         PLANS[j] = dplan
         if nu is None:
             U[j] = u
@@ -708,11 +797,16 @@ def _run(step, batches, grads, steps, on_step):
         step.defer_count(nu, resolve)
 
     for j in range(min(S, step.L + 1)):
-        load(j)
+        dedup(j)
+        observe(j)
+    if step.L + 1 < S:
+        dedup(step.L + 1)
     step.flush_deferred()
     for s in range(S):
         if s + step.L + 1 < S:
-            load(s + step.L + 1)
+            observe(s + step.L + 1)
+        if s + step.L + 2 < S:
+            dedup(s + step.L + 2)
         u_nexts = [U[s + k] for k in range(1, step.depth) if s + k < S]
         g = grads(s) if callable(grads) else grads[s]
         p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)

@@ -311,6 +311,27 @@ int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots, int64_t n_
                    int64_t s, int64_t n0, int64_t C, int64_t R, int K, const int8_t* code, int32_t* slot_of,
                    int64_t* slot_row, int8_t* adm_c0, int8_t* rj, int8_t* rok, int32_t* pstep, void* stream);
 
+/* The admissions with the pool-slot bookkeeping that precedes them (srm2/elara.py:345-347, 368), in one launch:
+ * the evicted slots ev_slot [nev] are pushed on the free stack free_stack[0, n_free), the top n_adm entries of the
+ * result become adm_slots (bottom first) and are admitted as elr_plan_admit does, the entries below them stay on
+ * the stack (free_stack is updated in place; its new depth is n_free + nev - n_adm), and dyn_out receives keep
+ * [nkeep] followed by adm_slots: the occupied dynamic slots after the step.  dyn_out must not overlap keep or
+ * free_stack.  n_adm <= n_free + nev <= C. */
+typedef struct elr_slots_args {
+  int64_t* free_stack;        /* [>= n_free + nev] free pool slots, bottom first */
+  int64_t n_free;
+  const int64_t* ev_slot;     /* [nev] evicted slots, pushed in this order */
+  int64_t nev;
+  const int64_t* keep;        /* [nkeep] occupied dynamic slots the step keeps */
+  int64_t nkeep;
+  int64_t* adm_slots;         /* [n_adm] out */
+  int64_t* dyn_out;           /* [nkeep + n_adm] out */
+} elr_slots_args;
+
+int elr_plan_admit_slots(const elr_slots_args* slots, const int64_t* adm_rows, int64_t n_adm, int64_t lazy_n, int evl,
+                         int64_t s, int64_t n0, int64_t C, int64_t R, int K, const int8_t* code, int32_t* slot_of,
+                         int64_t* slot_row, int8_t* adm_c0, int8_t* rj, int8_t* rok, int32_t* pstep, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Fused weight assembly: srm2/elara.py:471-489 (ELARAExecutor.assemble) -- the full states [n, 3, D] of the
  * step's non-resident rows in one launch.  Work row k (row rows[k]) lies in segment g (positions

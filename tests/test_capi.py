@@ -98,6 +98,14 @@ def test_planner_executor_dedup_argument_checks():
     assert L.elr_plan_admit(None, None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == 0              # nothing to do
     assert L.elr_plan_admit(None, None, 3, 4, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1             # lazy_n > n
     assert L.elr_plan_admit(None, None, 3, 1, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1             # null pointers
+    sl = _lib.SlotsArgs()
+    assert L.elr_plan_admit_slots(None, None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1            # no args
+    assert L.elr_plan_admit_slots(ctypes.byref(sl), None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == 0  # empty
+    sl.n_free, sl.nev = 2, 1
+    assert L.elr_plan_admit_slots(ctypes.byref(sl), fake, 4, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1  # 4 > 3
+    assert L.elr_plan_admit_slots(ctypes.byref(sl), fake, 2, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1  # nulls
+    sl.n_free, sl.nev = 8, 4
+    assert L.elr_plan_admit_slots(ctypes.byref(sl), None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1  # 12 > C
     a = _lib.AssembleArgs()
     a.n, a.D, a.K, a.nseg = 0, 128, 3, 1
     assert L.elr_assemble(None, None) == -1
