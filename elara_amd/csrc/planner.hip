@@ -141,15 +141,21 @@ __device__ __forceinline__ int block_class_rank(int k, int (&tot)[NCH]) {
 }
 
 // Pass 1: classify and count per block.  Blocks [0, nbu) take the unique rows, blocks [nbu, nbu + nbd) the dynamic
-// slots.  Block counts go channel-major: bu[c * nbu + b], bd[c * nbd + b].
+// slots.  Block counts go channel-major: bu[c * nbu + b], bd[c * nbd + b]; bbad[b]: the block's rows outside [0, R).
 __global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
-                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd) {
+                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd,
+                                                           int64_t* __restrict__ bbad) {
   const int64_t b = blockIdx.x;
   if (b < nbu) {
+    __shared__ int nbad;
+    if (threadIdx.x == 0) nbad = 0;
     const int64_t i = b * kPlanBlock + threadIdx.x;
     int k = -1;
+    bool bad = false;
     if (i < p.n) {
-      const RowClass rc = classify_row(p, p.u[i]);
+      const int64_t r = p.u[i];
+      const RowClass rc = classify_row(p, r);
+      bad = !row_ok(p, r);
       k = kRankOf[rc.cls];
       o.cls[i] = (int8_t)rc.cls;
       o.flags[i] = (uint8_t)rc.flags;
@@ -157,8 +163,12 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_pl
       o.c[i] = (int8_t)rc.c;
     }
     int tot[kNumCls];
-    block_class_rank<kNumCls>(k, tot);
+    block_class_rank<kNumCls>(k, tot);   // synchronises the block: nbad is zeroed before the adds below
+    const uint64_t mb = __builtin_amdgcn_ballot_w64(bad);
+    if ((threadIdx.x & 63) == 0 && mb) atomicAdd(&nbad, (int)__builtin_popcountll(mb));
     if (threadIdx.x < kNumCls) bu[threadIdx.x * nbu + b] = tot[threadIdx.x];
+    __syncthreads();
+    if (threadIdx.x == 0) bbad[b] = nbad;
   } else {
     const int64_t bb = b - nbu;
     const int64_t j = bb * kPlanBlock + threadIdx.x;
@@ -177,38 +187,21 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_pl
 // Pass 2 (one block per channel): block offsets per class; class totals and the host counts.
 __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd,
-                                                          int64_t* __restrict__ tot) {
-  // one block per channel: the kNumCls class channels, then the kDynCh dynamic-slot channels
+                                                          int64_t* __restrict__ bbad, int64_t* __restrict__ tot) {
+  // one block per channel: the kNumCls class channels, the kDynCh dynamic-slot channels, then the rows outside
+  // [0, R), which the caller raises on instead of letting the step skip them
   const int c = blockIdx.x;
   if (c < kNumCls) scan_channels_block(bu + (int64_t)c * nbu, nbu, 1, tot + c);
-  else scan_channels_block(bd + (int64_t)(c - kNumCls) * nbd, nbd, 1, tot + c);
+  else if (c < kNumCls + kDynCh) scan_channels_block(bd + (int64_t)(c - kNumCls) * nbd, nbd, 1, tot + c);
+  else scan_channels_block(bbad, nbu, 1, tot + c);
   if (threadIdx.x == 0) {   // the thread that stored tot[c]
     if (c < kNumCls) o.counts[kClsOfRank[c]] = tot[c];
     else if (c < kNumCls + 3) o.counts[c] = tot[c];
+    else if (c == kNumCls + kDynCh) o.counts[16] = tot[c];
     if (c == 0) {
       o.counts[13] = p.mat_top ? *p.mat_top : 0;
       o.counts[14] = p.log_top ? *p.log_top : 0;
       o.counts[15] = p.live ? *p.live : 0;
-      // rows of u outside [0, R) (u ascending: they are the ones below the first row >= 0 and from the first row
-      // >= R on); the caller raises on them instead of letting the step skip them
-      int64_t bad = 0;
-      if (p.R > 0 && p.n > 0) {
-        int64_t lo = 0, hi = p.n;   // first index with u >= 0
-        while (lo < hi) {
-          const int64_t mid = (lo + hi) >> 1;
-          if (p.u[mid] < 0) lo = mid + 1;
-          else hi = mid;
-        }
-        bad = lo;
-        lo = 0, hi = p.n;           // first index with u >= R
-        while (lo < hi) {
-          const int64_t mid = (lo + hi) >> 1;
-          if (p.u[mid] < p.R) lo = mid + 1;
-          else hi = mid;
-        }
-        bad += p.n - lo;
-      }
-      o.counts[16] = bad;
     }
   }
 }
@@ -331,7 +324,7 @@ extern "C" int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd) {
   using namespace elr;
   if (n < 0 || nd < 0) return -1;
   const int64_t nbu = plan_blocks(n), nbd = plan_blocks(nd);
-  return ((kNumCls * nbu + kDynCh * nbd + kNumCls + kDynCh) * 8 + 255) & ~int64_t(255);
+  return ((kNumCls * nbu + kDynCh * nbd + nbu + kNumCls + kDynCh + 1) * 8 + 255) & ~int64_t(255);
 }
 
 extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
@@ -353,9 +346,10 @@ extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out,
   const int64_t nbu = plan_blocks(p.n), nbd = plan_blocks(p.nd);
   int64_t* bu = (int64_t*)scratch;
   int64_t* bd = bu + kNumCls * nbu;
-  int64_t* tot = bd + kDynCh * nbd;
-  if (nbu + nbd > 0) k_plan_count<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd);
-  k_plan_scan<<<kNumCls + kDynCh, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
+  int64_t* bbad = bd + kDynCh * nbd;
+  int64_t* tot = bbad + nbu;
+  if (nbu + nbd > 0) k_plan_count<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad);
+  k_plan_scan<<<kNumCls + kDynCh + 1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot);
   if (nbu + nbd > 0) k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
   return launch_status();
 }
