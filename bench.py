@@ -17,8 +17,9 @@ Clock settle and warm-up: the first 20-30 ms of sustained load run at a lower en
 step: replay 288, 138, 125 us per launch over the first 25-step windows, then a steady 121 us; Adam, memory-bound,
 140 us throughout).  Before the W warm-up steps, the headline runs --settle-ms (default 100) of untimed steps, so the
 W warm-up and K timed steps all run at the steady clock, whatever W is; the line reports it under `clock_settle`.
-The timed region starts 2 ms after the synchronisation that precedes it (a launch right after a synchronisation
-overlaps write-backs that synchronisation started).  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
+The timed region follows the synchronisation before it at once: an idle gap lets the engine clock drop, and the
+timed launches then run while it climbs back (replay 116 us per launch with no gap or 0.5 ms, 118-121 us after a 2 ms
+gap, 134-140 us after 20 ms).  The --mode c1/c3/c4 lines warm up for at least 80 ms of load.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode headline|copy] [--no-cpu]
 """
@@ -36,7 +37,6 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = 'sparse-Adam+replay rows/s at d=128; achieved HBM GB/s vs ~8 TB/s peak'
 HBM_PEAK_GBS = 8000.0
-POST_SYNC_IDLE_S = 0.002   # headline: host idle between the synchronisation and the timed region
 HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000   # hipEventDisableSystemFence, hip_runtime_api.h
 _HIP = None
 
@@ -284,17 +284,13 @@ def headline(args):
     # timed steps run at the steady clock whatever W is.  (A memory-bound load does not do it: after 100 ms of Adam
     # launches alone, replay still ran 125 us per launch against 119-121 after the same time of whole steps.)
     out.zero_()
+    # every timed launch is timed by its own dispatch (no extra packets in the queue, so the instrument stays out of
+    # `value`); the roofline takes the mean over all K launches.  The events are made before the load starts, so that
+    # no host work leaves the GPU idle between the warm-up and the timed steps.
+    evs = [[HipEvent() for _ in range(4)] for _ in range(args.steps)]
     settle = _settle(one_step, args.settle_ms * 1e-3, 'the headline step (replay + Adam) on its own buffers')
     for _ in range(args.warmup):
         one_step()
-    torch.cuda.synchronize()
-    # the host synchronisation above starts write-backs the first launch after it would overlap: launched at once,
-    # that replay took 140-190 us, launched 0.1-10 ms later 129-132 us (steady state: 118-124).  The timed region
-    # starts after POST_SYNC_IDLE_S.
-    time.sleep(POST_SYNC_IDLE_S)
-    # every timed launch is timed by its own dispatch (no extra packets in the queue, so the instrument stays out of
-    # `value`); the roofline takes the mean over all K launches
-    evs = [[HipEvent() for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -331,16 +327,23 @@ def headline(args):
 
 
 def _settle(launch, settle_s, what):
-    """Untimed load before a benchmark: `launch()` in batches of 8, synchronised after each batch, until settle_s
-    seconds have passed.  Returns what was run (`what`, call count and milliseconds)."""
+    """Untimed load before a benchmark: `launch()` in batches of 8 until settle_s seconds have passed, with two
+    batches queued ahead of the one running (the host waits on the event of the batch before last), so the GPU never
+    idles in between.  Returns what was run (`what`, call count and milliseconds)."""
     import torch
     n = 0
+    pending = []
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < settle_s:
         for _ in range(8):
             launch()
         n += 8
-        torch.cuda.synchronize()
+        ev = torch.cuda.Event()
+        ev.record()
+        pending.append(ev)
+        if len(pending) > 2:
+            pending.pop(0).synchronize()
+    torch.cuda.synchronize()
     return {'work': what, 'calls': n, 'ms': (time.perf_counter() - t0) * 1e3}
 
 
