@@ -337,3 +337,46 @@ def test_gpu_assemble_and_admit_match_oracle(dev):
         torch.cuda.synchronize()
         for x, y in zip(o, g):
             assert torch.equal(x, y.cpu())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('n_free,nev,n_adm,nkeep', [(50, 20, 30, 40), (50, 20, 60, 10), (10, 30, 40, 0),
+                                                    (40, 0, 15, 25), (5, 8, 0, 30), (0, 12, 12, 3)])
+def test_gpu_plan_admit_slots_matches_stack_arithmetic(dev, n_free, nev, n_adm, nkeep):
+    """elr_plan_admit_slots against the free-stack arithmetic it replaces (srm2/elara.py:345-347, 368, as the step
+    writes it with torch ops): pool_free = cat(free, ev_slot), the top n_adm entries admitted, the rest the new
+    stack, the new slot list cat(keep, admitted); and the admissions' directory fields against plan_admit."""
+    from elara_amd.step import HipBackend
+    print(f'[gpu-test] admit_slots n_free={n_free} nev={nev} n_adm={n_adm} nkeep={nkeep}', flush=True)
+    rng = np.random.default_rng(n_free * 7 + nev * 3 + n_adm)
+    D, K, R, C, n0 = 64, 3, 3000, 400, 100
+    hb = HipBackend(D, 42, synth.bound_for(D), HP, 20, dev)
+    ob = OracleBackend(D, 42, synth.bound_for(D), HP, 20)
+    slots = rng.permutation(np.arange(n0, C)).astype(np.int64)
+    free, ev_slot, keep = slots[:n_free], slots[n_free:n_free + nev], slots[n_free + nev:n_free + nev + nkeep]
+    pool_free = np.concatenate([free, ev_slot])
+    adm = pool_free[pool_free.size - n_adm:]
+    a_rows = torch.from_numpy(rng.choice(R, n_adm, replace=False).astype(np.int64))
+    lazy = n_adm // 2
+    code = torch.from_numpy(rng.integers(0, K + 2, R).astype(np.int8))
+    st = lambda: [torch.full((R,), -1, dtype=torch.int32), torch.full((C,), -1, dtype=torch.int64),  # noqa: E731
+                  torch.full((C,), -1, dtype=torch.int8), torch.zeros(C, dtype=torch.int8),
+                  torch.zeros(C, dtype=torch.int8), torch.zeros((C - n0 + 1, K), dtype=torch.int32)]
+    o = st()
+    ob.plan_admit(a_rows, torch.from_numpy(adm.copy()), lazy, True, 9, n0, C, R, K, code, *o)
+    fbuf = torch.full((C,), -7, dtype=torch.int64)
+    fbuf[:n_free] = torch.from_numpy(free)
+    fbuf = fbuf.to(dev)
+    dyn = torch.full((C,), -7, dtype=torch.int64, device=dev)
+    g = [t.to(dev) for t in st()]
+    got = hb.plan_admit_slots(fbuf, n_free, torch.from_numpy(ev_slot).to(dev), torch.from_numpy(keep).to(dev),
+                              a_rows.to(dev), lazy, True, 9, n0, C, R, K, code.to(dev), *g, dyn)
+    torch.cuda.synchronize()
+    rest = pool_free.size - n_adm
+    assert np.array_equal(got.cpu().numpy(), adm)
+    assert np.array_equal(fbuf.cpu().numpy()[:rest], pool_free[:rest])
+    assert np.array_equal(fbuf.cpu().numpy()[rest:], np.full(C - rest, -7)) or rest < n_free
+    assert np.array_equal(dyn.cpu().numpy()[:nkeep + n_adm], np.concatenate([keep, adm]))
+    assert (dyn.cpu().numpy()[nkeep + n_adm:] == -7).all()
+    for x, y in zip(o, g):
+        assert torch.equal(x, y.cpu())
