@@ -62,6 +62,9 @@ SIGNATURES = {
     'elr_plan_admit_slots': (ctypes.c_int, [c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_i64, c_i64, c_i64, c_i64,
                                             ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp]),
     'elr_assemble': (ctypes.c_int, [c_vp, c_vp]),
+    'elr_step_exec_bytes': (c_i64, [c_vp]),
+    'elr_step_exec': (ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp]),
+    'elr_abi_sizes': (ctypes.c_int, [c_vp, ctypes.c_int]),
     'elr_step_update': (ctypes.c_int, [c_vp, c_vp]),
     'elr_dedup_plan_bytes': (c_i64, [c_i64, c_i64]),
     'elr_dedup_plan': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
@@ -126,6 +129,26 @@ class UpdateArgs(ctypes.Structure):
                 ('evl_ids', c_vp), ('ev_dyn', c_vp), ('adm_slots', c_vp), ('lazy_n', c_i64), ('n0', c_i64),
                 ('c_slots', c_vp), ('a_ids', c_vp), ('fn_slot', c_vp), ('s_slot', c_vp), ('part', ctypes.c_int32),
                 ('link_blocks', c_i64)]
+
+
+class ExecArgs(ctypes.Structure):
+    """elr_exec_args: the rest of a planned step in one call (elr_step_exec)."""
+    _fields_ = [('dir', DirState), ('pv', DirParams), ('s', c_i64), ('b', c_i64 * 11), ('u_ord', c_vp), ('c_ord', c_vp),
+                ('sl_ord', c_vp), ('loc_ord', c_vp), ('L_row', c_vp), ('L_cnt', c_vp), ('slots', SlotsArgs),
+                ('seed', c_u32), ('bound', c_f32), ('table', c_vp), ('recip', c_vp), ('table_rows', c_i64),
+                ('upd', UpdateArgs)]
+
+
+EXEC_OUT_FIELDS = ('L_steps', 'L_ids', 'hrec_dyn', 'hrec_j', 'ev_row', 'rep', 'evl_ids', 'evf_slots', 'ev_dyn',
+                   'adm_slots', 'a_ids', 'c_slots', 'work')
+
+
+class ExecOut(ctypes.Structure):
+    """elr_exec_out: byte offsets in the workspace of the arrays elr_step_exec writes."""
+    _fields_ = [(n, c_i64) for n in EXEC_OUT_FIELDS]
+
+
+ABI_STRUCTS = (DirState, DirParams, PlanIn, PlanOut, AssembleArgs, SlotsArgs, UpdateArgs, ExecArgs, ExecOut)
 
 
 def lib():
@@ -216,3 +239,6 @@ def split_empty(dev, dtype, sizes):
     """Uninitialised 1-D tensors of the given sizes, views of one allocation: one allocator call and one split for a
     launch's outputs of one dtype (fewer Python-level tensor constructions than an allocation each)."""
     return torch.empty(sum(sizes), dtype=dtype, device=dev).split(list(sizes))
+
+
+ESIZE = {torch.int8: 1, torch.bool: 1, torch.uint8: 1, torch.int32: 4, torch.int64: 8, torch.float32: 4}

@@ -1,0 +1,189 @@
+// The rest of a planned ELARA step in one call (elr_step_exec): directory call A, the admissions with their
+// pool-slot bookkeeping, directory call B, the fused assembly and the update, in the order the planner and
+// executor issue them (srm2/elara.py:271-414, 471-580), with every intermediate array carved from one workspace.
+// Host code only: it calls the library's own entry points, so each piece keeps its checks and kernels.
+#include "elr_common.h"
+
+namespace {
+
+struct ExecLayout {
+  elr_exec_out o;
+  int64_t dir_a_scratch, dir_a_scratch_bytes, dir_b_scratch, dir_b_scratch_bytes, total;
+};
+
+int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
+
+// Byte layout of the workspace for args; false when the bounds are inconsistent.
+bool exec_layout(const elr_exec_args& a, ExecLayout& L) {
+  const int64_t* b = a.b;
+  for (int r = 0; r < ELR_NRANK; ++r)
+    if (b[r] < 0 || b[r + 1] < b[r]) return false;
+  const int64_t K = a.pv.K, D = a.upd.D;
+  if (K < 1 || D < 1 || a.slots.nev < 0) return false;
+  const int64_t nh = b[ELR_RANK_HIT + 1] - b[ELR_RANK_HIT];
+  const int64_t nL = (b[ELR_RANK_LADM + 1] - b[ELR_RANK_LADM]) + (b[ELR_RANK_LAPP + 1] - b[ELR_RANK_LAPP]) +
+                     (b[ELR_RANK_LCMP + 1] - b[ELR_RANK_LCMP]);
+  const int64_t nev = a.slots.nev, n_adm = b[ELR_RANK_FADM + 1] - b[ELR_RANK_NADM];
+  const int64_t na = b[ELR_RANK_LAPP + 1] - b[ELR_RANK_NAPP], nc = b[ELR_RANK_LCMP + 1] - b[ELR_RANK_NCMP];
+  const int64_t nw = b[ELR_RANK_S] - b[ELR_RANK_NADM];
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o += al256(bytes);
+    return at;
+  };
+  L.o.L_steps = take(nL * K * 4);
+  L.o.L_ids = take(nL * K * 4);
+  L.o.hrec_dyn = take(nh * 8);
+  L.o.hrec_j = take(nh * 8);
+  L.o.ev_row = take(nev * 8);
+  L.o.rep = take(nev);
+  L.o.evl_ids = take(nev * K * 8);
+  L.o.evf_slots = take(nev * 8);
+  L.o.ev_dyn = take(nev * 8);
+  L.o.adm_slots = take(n_adm * 8);
+  L.o.a_ids = take(na * 8);
+  L.o.c_slots = take(nc * 8);
+  L.o.work = take(nw * 3 * D * 4);
+  L.dir_a_scratch_bytes = elr_dir_scratch_bytes(nev, 0);
+  L.dir_b_scratch_bytes = elr_dir_scratch_bytes(0, nc);
+  if (L.dir_a_scratch_bytes < 0 || L.dir_b_scratch_bytes < 0) return false;
+  L.dir_a_scratch = take(L.dir_a_scratch_bytes > 0 ? L.dir_a_scratch_bytes : 1);
+  L.dir_b_scratch = take(L.dir_b_scratch_bytes > 0 ? L.dir_b_scratch_bytes : 1);
+  L.total = o;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int64_t elr_step_exec_bytes(const elr_exec_args* args) {
+  if (!args) return ELR_EINVAL;
+  ExecLayout L;
+  if (!exec_layout(*args, L)) return ELR_EINVAL;
+  return L.total;
+}
+
+extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_bytes, elr_exec_out* out, void* stream) {
+  if (!args || !out) return ELR_EINVAL;
+  const elr_exec_args& a = *args;
+  ExecLayout L;
+  if (!exec_layout(a, L)) return ELR_EINVAL;
+  if (!ws || ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255)) return ELR_ECAPACITY;
+  *out = L.o;
+  char* w = static_cast<char*>(ws);
+  auto at = [&](int64_t off) { return static_cast<void*>(w + off); };
+  const int64_t* b = a.b;
+  const int64_t K = a.pv.K, D = a.upd.D, s = a.s;
+  const int64_t nh = b[ELR_RANK_HIT + 1] - b[ELR_RANK_HIT];
+  const int64_t nLa = b[ELR_RANK_LADM + 1] - b[ELR_RANK_LADM], nLp = b[ELR_RANK_LAPP + 1] - b[ELR_RANK_LAPP],
+                nLc = b[ELR_RANK_LCMP + 1] - b[ELR_RANK_LCMP], nL = nLa + nLp + nLc;
+  const int64_t nNa = b[ELR_RANK_NADM + 1] - b[ELR_RANK_NADM];
+  const int64_t nev = a.slots.nev, n_adm = b[ELR_RANK_FADM + 1] - b[ELR_RANK_NADM];
+  const int64_t na = b[ELR_RANK_LAPP + 1] - b[ELR_RANK_NAPP], nc = b[ELR_RANK_LCMP + 1] - b[ELR_RANK_NCMP];
+  const int64_t w0 = b[ELR_RANK_NADM], nw = b[ELR_RANK_S] - w0;
+  const int64_t lazy_n = nNa + nLa;
+  const bool evl = a.pv.evl != 0;
+  int32_t* L_steps = static_cast<int32_t*>(at(L.o.L_steps));
+  int32_t* L_ids = static_cast<int32_t*>(at(L.o.L_ids));
+  int64_t* hrec_dyn = static_cast<int64_t*>(at(L.o.hrec_dyn));
+  int64_t* hrec_j = static_cast<int64_t*>(at(L.o.hrec_j));
+  int64_t* evl_ids = static_cast<int64_t*>(at(L.o.evl_ids));
+  int64_t* evf_slots = static_cast<int64_t*>(at(L.o.evf_slots));
+  int64_t* ev_dyn = static_cast<int64_t*>(at(L.o.ev_dyn));
+  int64_t* adm_slots = static_cast<int64_t*>(at(L.o.adm_slots));
+  int64_t* a_ids = static_cast<int64_t*>(at(L.o.a_ids));
+  int64_t* c_slots = static_cast<int64_t*>(at(L.o.c_slots));
+  float* work = static_cast<float*>(at(L.o.work));
+  int rc;
+  // directory call A: replay inputs of the L rows, history records of the hits, the evictions
+  if ((rc = elr_dir_a(&a.dir, &a.pv, a.sl_ord + b[ELR_RANK_HIT], nh, a.L_row, a.L_cnt, nL, a.slots.ev_slot, nev, s,
+                      L_steps, L_ids, hrec_dyn, hrec_j, static_cast<int64_t*>(at(L.o.ev_row)),
+                      static_cast<uint8_t*>(at(L.o.rep)), evl_ids, evf_slots, ev_dyn, at(L.dir_a_scratch),
+                      L.dir_a_scratch_bytes, stream)))
+    return rc;
+  // admissions: the evicted slots pushed on the free stack, the admitted rows' slots popped from its top
+  elr_slots_args sl = a.slots;
+  sl.adm_slots = adm_slots;
+  if ((rc = elr_plan_admit_slots(&sl, a.u_ord + w0, n_adm, lazy_n, evl ? 1 : 0, s, a.pv.n0, a.pv.n0 + a.pv.Cdyn,
+                                 a.pv.R, (int)K, a.dir.code, a.dir.slot_of, a.dir.slot_row, a.dir.adm_c0, a.dir.rj,
+                                 a.dir.rok, a.dir.pstep, stream)))
+    return rc;
+  // directory call B: appends (entry index = the row's current count) and compactions of the non-resident lazy rows
+  if ((rc = elr_dir_b(&a.dir, &a.pv, a.u_ord + b[ELR_RANK_NAPP], a.c_ord + b[ELR_RANK_NAPP], na,
+                      a.u_ord + b[ELR_RANK_NCMP], a.c_ord + b[ELR_RANK_NCMP], nc, s, a_ids, c_slots,
+                      at(L.dir_b_scratch), L.dir_b_scratch_bytes, stream)))
+    return rc;
+  // the work rows in class-rank order: admitted N / L / F, appended N / L, compacted N / L, transient F
+  if (nw > 0) {
+    elr_assemble_args g{};
+    g.work = work;
+    g.rows = a.u_ord + w0;
+    g.n = nw;
+    g.D = D;
+    g.K = (int)K;
+    const int rank_of[8] = {ELR_RANK_NADM, ELR_RANK_LADM, ELR_RANK_FADM, ELR_RANK_NAPP,
+                            ELR_RANK_LAPP, ELR_RANK_NCMP, ELR_RANK_LCMP, ELR_RANK_FN};
+    const int kind_of[8] = {ELR_ASM_INIT, ELR_ASM_REPLAY, ELR_ASM_GATHER, ELR_ASM_INIT,
+                            ELR_ASM_REPLAY, ELR_ASM_INIT, ELR_ASM_REPLAY, ELR_ASM_GATHER};
+    const int64_t aux_of[8] = {0, 0, 0, 0, nLa, 0, nLa + nLp, 0};
+    g.nseg = 8;
+    for (int q = 0; q < 8; ++q) {
+      g.seg_end[q] = b[rank_of[q] + 1] - w0;
+      g.seg_kind[q] = kind_of[q];
+      g.seg_aux[q] = aux_of[q];
+    }
+    g.seed = a.seed;
+    g.bound = a.bound;
+    g.L_ids = L_ids;
+    g.L_steps = L_steps;
+    g.L_cnt = a.L_cnt;
+    g.nL = nL;
+    g.logs = a.upd.logs;
+    g.nlogs = a.upd.log_rows;
+    g.table = a.table;
+    g.recip = a.recip;
+    g.table_rows = a.table_rows;
+    g.mat = a.upd.mat;
+    g.mat_rows = a.upd.mat_rows;
+    g.loc = a.dir.loc;
+    g.R = a.pv.R;
+    if ((rc = elr_assemble(&g, stream))) return rc;
+  }
+  // the update: hits, evictions, admissions, compactions, transient and S rows, log appends
+  elr_update_args u = a.upd;
+  for (int r = 0; r <= ELR_NRANK; ++r) u.b[r] = b[r];
+  u.K = K;
+  u.work = work;
+  u.step = s;
+  u.evl = evl ? 1 : 0;
+  u.hit_slot = a.sl_ord + b[ELR_RANK_HIT];
+  u.hrec_dyn = evl ? hrec_dyn : nullptr;
+  u.hrec_j = evl ? hrec_j : nullptr;
+  u.nev = nev;
+  u.ev_slot = a.slots.ev_slot;
+  u.evf_slots = evf_slots;
+  u.evl_ids = evl_ids;
+  u.ev_dyn = ev_dyn;
+  u.adm_slots = adm_slots;
+  u.lazy_n = lazy_n;
+  u.n0 = a.pv.n0;
+  u.c_slots = c_slots;
+  u.a_ids = a_ids;
+  u.fn_slot = a.loc_ord + b[ELR_RANK_FN];
+  u.s_slot = a.loc_ord + b[ELR_RANK_S];
+  u.part = ELR_UPDATE_ALL;
+  u.link_blocks = 0;
+  return elr_step_update(&u, stream);
+}
+
+extern "C" int elr_abi_sizes(int64_t* out, int n) {
+  if (!out || n < 0) return ELR_EINVAL;
+  const int64_t sz[] = {(int64_t)sizeof(elr_dir_state), (int64_t)sizeof(elr_dir_params), (int64_t)sizeof(elr_plan_in),
+                        (int64_t)sizeof(elr_plan_out), (int64_t)sizeof(elr_assemble_args),
+                        (int64_t)sizeof(elr_slots_args), (int64_t)sizeof(elr_update_args),
+                        (int64_t)sizeof(elr_exec_args), (int64_t)sizeof(elr_exec_out)};
+  const int m = (int)(sizeof(sz) / sizeof(sz[0]));
+  const int k = n < m ? n : m;
+  for (int i = 0; i < k; ++i) out[i] = sz[i];
+  return k;
+}

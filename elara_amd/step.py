@@ -68,6 +68,7 @@ class HipBackend:
         self.table = ScalarTable(*hp, max_step, device)
         self.dx = dir_ext()
         self._arenas = None
+        self._exec = None
 
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
@@ -125,13 +126,56 @@ class HipBackend:
     def glog_take(self, logs, ids, glog, dyn):
         glog_take(logs, ids, glog, dyn)
 
-    def step_update(self, es, p, G, part=0):
-        """ElaraStep.update in one native call (elr_step_update): the same launches in the same order, issued from
-        C++ with no per-launch Python work.  part: 0 all, 1 the device part, 2 the link part (ELR_UPDATE_*)."""
+    def _arena_ptrs(self, es):
         if self._arenas is None or self._arenas[0] is not es:
             self._arenas = (es, _lib.dptr(es.pool).value, _lib.dptr(es.mat).value, _lib.dptr(es.logs).value,
                             _lib.dptr(es.glog).value)
-        _, pool, mat, logs, glog = self._arenas
+        return self._arenas[1:]
+
+    def step_exec(self, es, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord):
+        """ElaraStep's calls after the class-count synchronisation -- directory call A, the admissions with the slot
+        bookkeeping, call B, the assembly and the update -- in one native call (elr_step_exec), in that order on the
+        current stream.  Returns the workspace and the offsets of the arrays written there."""
+        from .elara_dir import _state
+        S, P, dev, _ = _state(es.state_list(), es.params())
+        pool, mat, logs, glog = self._arena_ptrs(es)
+        a = _lib.ExecArgs()
+        a.dir, a.pv, a.s = S, P, p.s
+        a.b[:] = p.b
+        n = p.b[-1]
+        for name, t, dt in (('u_ord', u_ord, I64), ('c_ord', c_ord, I64), ('sl_ord', sl_ord, I64),
+                            ('loc_ord', loc_ord, I64), ('L_row', p.L_row, I64), ('L_cnt', p.L_cnt, I32)):
+            if t.dtype != dt or not t.is_contiguous() or t.device != dev:
+                raise RuntimeError(f'step_exec: {name} must be a contiguous {dt} tensor on {dev}')
+            setattr(a, name, t.data_ptr())
+        if G.dtype != torch.float32 or not G.is_contiguous() or G.numel() != n * self.D:
+            raise RuntimeError(f'step_exec: the gradients must be a contiguous float32 [{n}, {self.D}] tensor')
+        sl = a.slots
+        sl.free_stack, sl.n_free = es._free_buf.data_ptr(), es.n_free
+        sl.ev_slot, sl.nev = ev_slot.data_ptr(), ev_slot.numel()
+        sl.keep, sl.nkeep = keep_dyn.data_ptr(), keep_dyn.numel()
+        sl.dyn_out = es._dyn_buf.data_ptr()
+        a.seed, a.bound = int(self.seed) & 0xFFFFFFFF, float(self.bound)
+        a.table, a.recip, a.table_rows = self.table.t.data_ptr(), self.table.r.data_ptr(), self.table.t.shape[0]
+        u = a.upd
+        u.D, u.K = self.D, es.K
+        u.pool, u.pool_rows, u.mat, u.mat_rows = pool, es.pool.shape[0], mat, es.mat.shape[0]
+        u.logs, u.log_rows, u.glog, u.glog_slots = logs, es.logs.shape[0], glog, es.glog.shape[0]
+        u.grad = G.data_ptr()
+        u.lr, u.b1, u.b2, u.eps = self.hp
+        L = _lib.lib()
+        nb = int(L.elr_step_exec_bytes(ctypes.byref(a)))
+        _lib.check(min(nb, 0), 'elr_step_exec_bytes')
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        off = _lib.ExecOut()
+        _lib.check(L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), nb, ctypes.byref(off),
+                                   ctypes.c_void_p(_lib.raw_stream(dev))), 'elr_step_exec')
+        return ws, off
+
+    def step_update(self, es, p, G, part=0):
+        """ElaraStep.update in one native call (elr_step_update): the same launches in the same order, issued from
+        C++ with no per-launch Python work.  part: 0 all, 1 the device part, 2 the link part (ELR_UPDATE_*)."""
+        pool, mat, logs, glog = self._arena_ptrs(es)
         b = p.b
         nh, nev = b[R_HIT + 1] - b[R_HIT], p.ev_slot.numel()
         a = _lib.UpdateArgs(
@@ -160,7 +204,39 @@ def _p64(t, n, dtype=torch.int64):
 
 
 class Plan:
-    pass
+    """One step's plan.  With the native executor (HipBackend.step_exec) the arrays it writes -- the directory calls'
+    outputs, the admitted slots, the work rows -- live in its workspace and become tensors on first access."""
+
+    # name: (field of elr_exec_out, dtype, shape keys)
+    _VIEWS = {'L_steps': ('L_steps', I32, ('nL', 'K')), 'L_ids': ('L_ids', I32, ('nL', 'K')),
+              'hrec_dyn': ('hrec_dyn', I64, ('nh',)), 'hrec_j': ('hrec_j', I64, ('nh',)),
+              'ev_row': ('ev_row', I64, ('nev',)), 'ev_rep': ('rep', torch.bool, ('nev',)),
+              'evl_ids': ('evl_ids', I64, ('nev', 'K')), 'evf_slots': ('evf_slots', I64, ('nev',)),
+              'ev_dyn': ('ev_dyn', I64, ('nev',)), 'adm_slots': ('adm_slots', I64, ('n_adm',)),
+              'a_ids': ('a_ids', I64, ('na',)), 'c_slots': ('c_slots', I64, ('nc',)),
+              'work': ('work', torch.float32, ('nw', 3, 'D'))}
+
+    def __getattr__(self, name):
+        d = self.__dict__
+        if '_ws' not in d or name not in Plan._VIEWS and name not in ('FN_slot', 'S_slot', 'adm_rec_slot'):
+            raise AttributeError(name)
+        if name in ('FN_slot', 'S_slot'):
+            b, r = self.b, R_FN if name == 'FN_slot' else R_S
+            v = d['_loc_ord'][b[r]:b[r + 1]]
+        elif name == 'adm_rec_slot':
+            if not (self.lazy_n and self.evl):
+                raise AttributeError(name)
+            v = self.adm_slots[:self.lazy_n]
+        else:
+            field, dt, shape = Plan._VIEWS[name]
+            dims = [x if isinstance(x, int) else d['_dims'][x] for x in shape]
+            n = 1
+            for x in dims:
+                n *= x
+            o = getattr(d['_off'], field)
+            v = d['_ws'][o:o + n * _lib.ESIZE[dt]].view(dt).view(*dims)
+        setattr(self, name, v)
+        return v
 
 
 class HostBudgetExceeded(RuntimeError):
@@ -531,14 +607,34 @@ class ElaraStep:
         if mt_hi > self.mat_cap - 1 or lt_hi > self.log_cap:
             raise RuntimeError(f'arena capacity: step {s} may allocate up to MAT row {mt_hi} (capacity '
                                f'{self.mat_cap - 1}) and log entry {lt_hi} (capacity {self.log_cap})')
-        st, pv = self.state_list(), self.params()
-        (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots,
-         p.ev_dyn) = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s)
         p.ev_slot = ev_slot
-        # admissions (srm2/elara.py:345-367): admitted N, L, F rows take slots from the free stack's top
         lazy_n = nNa + nLa
         p.lazy_n = lazy_n
         nf = self.n_free + nev
+        # the native executor takes the rest of the step in one call, unless the host must look at the arenas'
+        # tops between the directory calls and the update (a host budget this step could reach) or the update's
+        # host-arena writes go to the link stream
+        native = (getattr(self.be, 'step_exec', None) is not None and self._link is None and self._slots_in_place
+                  and g_occ is not None and not (self.host_budget and (mt_hi > self.faulted['mat']
+                                                                       or lt_hi > self.faulted['log'])))
+        if native:
+            if G is None:
+                G = self.be.segsum(g_occ, dplan, n, rank)
+            p._ws, p._off = self.be.step_exec(self, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord)
+            p._dims = dict(nL=nLa + nLp + nLc, K=K, nh=counts[C_HIT], nev=nev, n_adm=n_adm, na=nNp + nLp,
+                           nc=nNc + nLc, nw=b[R_S] - b[R_NADM], D=self.D)
+            p._loc_ord = loc_ord
+            p.G = None
+            p.done = True
+            self.free = self._free_buf[:nf - n_adm]
+            self.dyn_slots = self._dyn_buf[:keep_dyn.numel() + n_adm]
+            self.n_free = nf - n_adm
+            self._plan_stats(p, n_adm, nev, barrier)
+            return p
+        st, pv = self.state_list(), self.params()
+        (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots,
+         p.ev_dyn) = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s)
+        # admissions (srm2/elara.py:345-367): admitted N, L, F rows take slots from the free stack's top
         if self._slots_in_place:   # the stack push, the admissions and the new slot list in one launch
             adm_slots = self.be.plan_admit_slots(self._free_buf, self.n_free, ev_slot, keep_dyn,
                                                  u_ord[rs(R_NADM, R_FADM)], lazy_n, self.evl, s, self.n0, self.C,
@@ -563,6 +659,14 @@ class ElaraStep:
         # MAT slots of the transient F and the S rows (adjacent ranks; the directory calls above move no F/S row)
         fs = loc_ord[rs(R_FN, R_S)]
         p.FN_slot, p.S_slot = fs[:nFn], fs[nFn:]
+        self._plan_stats(p, n_adm, nev, barrier)
+        if self.host_budget and (mt_hi > self.faulted['mat'] or lt_hi > self.faulted['log']):
+            self.budget_account(*self._host(self.mat_top, self.log_top))
+        return p
+
+    def _plan_stats(self, p, n_adm, nev, barrier):
+        counts = p.counts
+        nNa, nNp, nNc, nLa, nLp, nLc, nFa, nFn = counts[1:9]
         st_ = self.stats
         st_['adm'] += n_adm
         st_['ev'] += nev
@@ -574,9 +678,6 @@ class ElaraStep:
         st_['compactions'] += nNc + nLc
         st_['appends'] += nNp + nLp
         st_['barriers'] += int(barrier)
-        if self.host_budget and (mt_hi > self.faulted['mat'] or lt_hi > self.faulted['log']):
-            self.budget_account(*self._host(self.mat_top, self.log_top))
-        return p
 
     def budget_account(self, mat_top, log_top):
         """Fault the arenas' accounting up to the tops a step left (ArenaStore.fault, srm2/elara.py:63-81, as the
@@ -685,6 +786,8 @@ class ElaraStep:
         run() does (srm2/train.py:359-366); if batch s+1 was not, the next step waits for this step's writes into
         host arenas before it assembles."""
         p = self.plan(s, u, u_nexts, g_occ, dplan)
+        if getattr(p, 'done', False):   # the native executor has issued the assembly and the update
+            return p
         self.assemble(p)
         G = p.G if p.G is not None else self.be.segsum(g_occ, dplan, u.numel(), p.rank)
         p.G = None

@@ -458,6 +458,52 @@ int elr_step_update(const elr_update_args* args, void* stream);
 
 
 /* ---------------------------------------------------------------------------------------------------------
+ * The rest of a planned step in one call: srm2/elara.py:271-414 after the class-count synchronisation (call A of
+ * the directory, the admissions with the pool-slot bookkeeping, call B), the fused assembly (elara.py:471-489) and
+ * the executor's update with the host worker's arena writes (elara.py:491-580), issued from C++ in that order on
+ * one stream: elr_dir_a, elr_plan_admit_slots, elr_dir_b, elr_assemble, elr_step_update.  No counterpart in the
+ * reference, whose planner issues these as separate torch and extension calls; it is the same work with the
+ * per-call host cost of one call.  The caller has classified the batch (elr_plan_classify) and read its counts;
+ * `ws` (device, >= elr_step_exec_bytes(args) bytes, 256-byte aligned) receives every intermediate array, at the
+ * offsets elr_step_exec reports in `out` (bytes from ws).
+ * ------------------------------------------------------------------------------------------------------- */
+typedef struct elr_exec_args {
+  elr_dir_state dir;          /* the directory (as elr_dir_a) */
+  elr_dir_params pv;          /* R, K, Lcap, n0, Cdyn, MAT, trash, evl */
+  int64_t s;                  /* logical step */
+  int64_t b[ELR_NRANK + 1];   /* class-rank bounds of the batch */
+  const int64_t* u_ord;       /* [b[ELR_NRANK]] rows, codes, pool slots, MAT slots in class-rank order */
+  const int64_t* c_ord;
+  const int64_t* sl_ord;
+  const int64_t* loc_ord;
+  const int64_t* L_row;       /* [nL] the L rows as admitted, append, compact (nL = the three L ranks' rows) */
+  const int32_t* L_cnt;
+  elr_slots_args slots;       /* free stack, evicted and kept slots, dyn_out (adm_slots: filled from ws) */
+  uint32_t seed;              /* counter-hash init */
+  float bound;
+  const float* table;         /* [table_rows, 8] Adam scalars, [table_rows, 2] reciprocals */
+  const double* recip;
+  int64_t table_rows;
+  elr_update_args upd;        /* D, K, the arenas and their rows, grad, lr, b1, b2, eps, n0 (the other fields are set
+                                 by the call) */
+} elr_exec_args;
+
+/* Offsets (bytes from ws) of the arrays elr_step_exec writes: elr_dir_a's nine outputs (L_steps, L_ids, hrec_dyn,
+ * hrec_j, ev_row, rep, evl_ids, evf_slots, ev_dyn), the admitted slots, elr_dir_b's a_ids and c_slots, and the work
+ * rows [b[ELR_RANK_S] - b[ELR_RANK_NADM], 3, D]. */
+typedef struct elr_exec_out {
+  int64_t L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep, evl_ids, evf_slots, ev_dyn, adm_slots, a_ids, c_slots, work;
+} elr_exec_out;
+
+int64_t elr_step_exec_bytes(const elr_exec_args* args);
+int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_bytes, elr_exec_out* out, void* stream);
+
+/* sizeof of this header's structs, for a binding to check its layouts (no counterpart in the reference): out[0..8] =
+ * elr_dir_state, elr_dir_params, elr_plan_in, elr_plan_out, elr_assemble_args, elr_slots_args, elr_update_args,
+ * elr_exec_args, elr_exec_out (at most n of them); returns the number written. */
+int elr_abi_sizes(int64_t* out, int n);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Row copies: dst[dst_idx[i]] = src[src_idx[i]], i < n, rows of W floats (NULL index = identity).
  * Replaces: the gradient-log append logs[A_ids] = g (srm2/elara.py:569-570 with srm2/csrc/srm2_cpu.cpp:167-180
  * cs_append semantics; here the log arena is in HBM), the resident-history record glog.index_put_((dyn, j), g)

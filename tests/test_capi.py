@@ -30,6 +30,35 @@ def test_library_exports_every_declared_symbol():
     assert set(names) <= set(_lib.SIGNATURES), 'binding lacks a signature for a declared entry point'
 
 
+def test_struct_layouts_match_the_library():
+    """Every ctypes mirror of a header struct has the size the library was compiled with (elr_abi_sizes)."""
+    out = (ctypes.c_int64 * len(_lib.ABI_STRUCTS))()
+    assert _lib.lib().elr_abi_sizes(out, len(out)) == len(out)
+    assert list(out) == [ctypes.sizeof(t) for t in _lib.ABI_STRUCTS]
+
+
+def test_step_exec_checks_and_workspace_size():
+    """elr_step_exec_bytes lays out the workspace from the bounds alone; bad bounds and a short workspace are
+    rejected on the host."""
+    L = _lib.lib()
+    a = _lib.ExecArgs()
+    a.pv.K, a.upd.D = 3, 64
+    assert L.elr_step_exec_bytes(ctypes.byref(a)) > 0                                   # empty step: scratch only
+    a.b[1:] = [5, 7, 9, 9, 12, 12, 15, 15, 16, 20]                                      # hits 5, N adm 2, L adm 2, ...
+    a.slots.nev = 4
+    nb = L.elr_step_exec_bytes(ctypes.byref(a))
+    assert nb >= (16 - 5) * 3 * 64 * 4                                                 # the work rows at least
+    a.slots.nev = 40
+    assert L.elr_step_exec_bytes(ctypes.byref(a)) > nb                                  # more evictions, more bytes
+    a.b[3] = 4                                                                           # bounds decrease
+    assert L.elr_step_exec_bytes(ctypes.byref(a)) == -1
+    o = _lib.ExecOut()
+    assert L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(256), 1 << 30, ctypes.byref(o), None) == -1
+    a.b[3] = 9
+    assert L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(256), 10, ctypes.byref(o), None) == -3    # too small
+    assert L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(272), 1 << 30, ctypes.byref(o), None) == -3  # unaligned
+
+
 def test_version_and_errors():
     L = _lib.lib()
     assert L.elr_version() >= 100

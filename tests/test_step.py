@@ -144,12 +144,14 @@ def test_gpu_step_matches_oracle_step(dev, name):
 @pytest.mark.gpu
 @pytest.mark.parametrize('name', ['evl', 'no_evl_S', 'host_arenas'])
 def test_gpu_native_update_matches_python_update(dev, name):
-    """elr_step_update (the whole update in one native call, its five independent row writes in one launch)
-    against the same update issued call by call from Python over the same HIP kernels."""
+    """elr_step_exec (directory calls, admissions, assembly and update in one native call; host arenas: the
+    update's two parts by elr_step_update) against the same step issued call by call from Python over the same HIP
+    kernels."""
     from elara_amd.step import HipBackend, run
 
     class CallByCall(HipBackend):
         step_update = None
+        step_exec = None
 
     print(f'[gpu-test] native update {name}', flush=True)
     kw = {'evl': {}, 'no_evl_S': {'evl': False, 'st': 'S'}, 'host_arenas': {'host': True}}[name]
