@@ -20,7 +20,7 @@ of it runs as HIP kernels (elara_amd/csrc/dedup.hip) on torch's current stream.
 import torch
 
 from . import _lib
-from .ops import _check_state, _scalars8
+from .ops import _check_state, _scalars8, check_rows
 
 I64 = torch.int64
 
@@ -171,13 +171,16 @@ def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1, 
     return out
 
 
-def adam_dedup(pool, ids, grad, lr, b1, b2, eps, step):
+def adam_dedup(pool, ids, grad, lr, b1, b2, eps, step, check=False):
     """pool [C,3,D] cuda float32 (updated in place); ids int32/int64 [n] rows of pool, repeats allowed; grad [n,D]
-    (row i belongs to ids[i]).  Each unique id gets one Adam step with the sum of its gradients."""
+    (row i belongs to ids[i]).  Each unique id gets one Adam step with the sum of its gradients.  An id outside
+    [0, C) is skipped; check=True raises IndexError for it first (one host synchronisation)."""
     idx = _ids(ids)
     n = idx.numel()
     if n == 0:
         return
+    if check:
+        check_rows(idx, pool.shape[0], 'ids')
     _check_state(pool)
     D = pool.shape[2]
     if not (grad.is_cuda and grad.dtype == torch.float32 and grad.numel() == n * D):

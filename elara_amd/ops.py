@@ -57,14 +57,26 @@ def _check_state(pool, name='pool'):
                            f'{tuple(pool.shape)} {pool.dtype} {pool.device}')
 
 
-def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step, events=None):
+def check_rows(idx, rows, what='slots'):
+    """IndexError unless every entry of idx lies in [0, rows) (one min/max reduction and one host read)."""
+    if idx.numel():
+        lo, hi = (int(x) for x in torch.aminmax(idx))
+        if lo < 0 or hi >= rows:
+            raise IndexError(f'{what} out of range: [{lo}, {hi}] not within [0, {rows})')
+
+
+def gpu_adam(pool, slots, grad, lr, b1, b2, eps, step, events=None, check=False):
     """pool [C,3,D] cuda float32 (updated in place); slots int32/int64 [n] (unique rows of pool); grad [n,D]
     (row i -> slots[i]).  srm2/ops.py:59-67.  pool may also be a pinned host arena (the capacity tier): the kernel
     then updates it over the host link.  events: optional (start, stop) hipEvent_t handles (integers) that the launch
-    itself records at the kernel's start and end (elr_adam_rows_timed); not recorded when n == 0."""
+    itself records at the kernel's start and end (elr_adam_rows_timed); not recorded when n == 0.  A slot outside
+    [0, C) is skipped by the kernel (the reference leaves it undefined); check=True raises IndexError for it first,
+    at the cost of a host synchronisation."""
     n = slots.numel()
     if n == 0:
         return
+    if check:
+        check_rows(slots, pool.shape[0])
     if pool.is_cuda:
         _check_state(pool)
     elif not (_lib.is_arena(pool) and pool.dim() == 3 and pool.shape[1] == 3):

@@ -303,3 +303,25 @@ def test_timed_launches_record_kernel_events(dev):
         assert 0.0 < ms < 50.0, ms
     for e in ev:
         e.destroy()
+
+
+@pytest.mark.gpu
+def test_gpu_adam_check_raises_on_rows_out_of_range(dev):
+    """gpu_adam / adam_dedup skip a row outside [0, C) (undefined in the reference); with check=True they raise
+    IndexError before any launch, and run as usual on valid rows."""
+    from elara_amd.dedup import adam_dedup
+    from elara_amd.ops import gpu_adam
+    print('[gpu-test] adam check', flush=True)
+    pool = torch.zeros(10, 3, 64, device=dev)
+    g = torch.ones(3, 64, device=dev)
+    for bad in ([0, 4, 10], [-1, 2, 3]):
+        with pytest.raises(IndexError):
+            gpu_adam(pool, torch.tensor(bad, device=dev), g, *synth.ADAM, 1, check=True)
+        with pytest.raises(IndexError):
+            adam_dedup(pool, torch.tensor(bad, device=dev), g, *synth.ADAM, 1, check=True)
+    torch.cuda.synchronize()
+    assert not pool.any()                                      # nothing was launched
+    gpu_adam(pool, torch.tensor([0, 4, 9], device=dev), g, *synth.ADAM, 1, check=True)
+    adam_dedup(pool, torch.tensor([1, 1, 2], device=dev), g, *synth.ADAM, 1, check=True)
+    torch.cuda.synchronize()
+    assert pool[[0, 4, 9, 1, 2], 0].ne(0).all() and not pool[[3, 5, 6, 7, 8]].any()
