@@ -168,8 +168,10 @@ class HipBackend:
         _lib.check(min(nb, 0), 'elr_step_exec_bytes')
         ws = torch.empty(nb, dtype=torch.uint8, device=dev)
         off = _lib.ExecOut()
-        _lib.check(L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), nb, ctypes.byref(off),
-                                   ctypes.c_void_p(_lib.raw_stream(dev))), 'elr_step_exec')
+        with _lib.on_device(dev):
+            rc = L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), nb, ctypes.byref(off),
+                                 ctypes.c_void_p(_lib.raw_stream(dev)))
+        _lib.check(rc, 'elr_step_exec')
         return ws, off
 
     def step_update(self, es, p, G, part=0):
@@ -189,8 +191,9 @@ class HipBackend:
             _p64(p.c_slots, b[R_LCMP + 1] - b[R_NCMP]), _p64(p.a_ids, b[R_LAPP + 1] - b[R_NAPP]),
             _p64(p.FN_slot, b[R_FN + 1] - b[R_FN]), _p64(p.S_slot, b[R_S + 1] - b[R_S]), int(part),
             int(es.link_blocks) if part == 2 else 0)
-        _lib.check(_lib.lib().elr_step_update(ctypes.byref(a), ctypes.c_void_p(_lib.raw_stream(G.device))),
-                   'elr_step_update')
+        with _lib.on_device(G.device):
+            rc = _lib.lib().elr_step_update(ctypes.byref(a), ctypes.c_void_p(_lib.raw_stream(G.device)))
+        _lib.check(rc, 'elr_step_update')
 
 
 def _p64(t, n, dtype=torch.int64):
