@@ -10,9 +10,10 @@
 // push onto the free stack at n_lfree + rank (elara_dir.cpp:23-34).
 //
 // The device counters n_lfree, log_top, mat_top, live stay in HBM; nothing is read back to the host.  Grid-wide
-// ranks come from a three-step scan: per-block counts, one single-block scan that also advances the counters
-// (keeping their old values in scratch), then an apply pass.  Stack pops and pushes are separate launches,
-// because a push may reuse a stack position that another block still has to pop.
+// ranks come from per-block counts (the count kernel also keeps the counters' old values in scratch) and an apply
+// pass whose blocks add up the counts of the blocks before them and whose block 0 advances the counters; grids of
+// more than kFusedScanBlocks blocks scan the counts in a single-block launch between the two instead.  Stack pops
+// and pushes are separate launches, because a push may reuse a stack position that another block still has to pop.
 //
 // Trash conventions are the reference's (srm2/elara.py:119-123): loc/ent row R, pstep row Cdyn, MAT slot `trash`.
 // The reference scatters values of invalid entries into lstep[Lcap] and lfree[Lcap] (which value lands there is
@@ -27,7 +28,8 @@ namespace elr {
 
 constexpr int kDirBlock = 256;
 
-// Old counter values kept by the scan step for the apply steps.
+// Old counter values kept for the apply steps: block 0 of the count kernel stores nf0, top0 and mt0 (every block of
+// it reads the same counters, which nothing writes during that launch); nf1 comes with the counter update.
 struct DirHdr {
   int64_t nf0;   // n_lfree before this call's log allocation
   int64_t top0;  // log_top before it
@@ -35,9 +37,63 @@ struct DirHdr {
   int64_t nf1;   // n_lfree after the log allocation (push base of the releases)
 };
 
+// Grids of at most this many blocks skip the single-block scan launch: each block of the apply kernel sums the
+// per-block counts of the blocks before it itself (one count per thread), and its block 0 advances the counters.
+// Larger grids scan the counts in a launch of their own (k_dir_scan), whose reads then grow with the grid only once.
+constexpr int64_t kFusedScanBlocks = kDirBlock;
+
 template <int NCH>
 __device__ __forceinline__ void dir_block_scan(const int (&v)[NCH], int (&ex)[NCH], int (&tot)[NCH]) {
   block_excl_scan<kDirBlock, NCH>(v, ex, tot);
+}
+
+__device__ __forceinline__ void dir_snapshot(const elr_dir_state& st, DirHdr* hdr) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    hdr->nf0 = *st.n_lfree;
+    hdr->top0 = *st.log_top;
+    hdr->mt0 = *st.mat_top;
+  }
+}
+
+// n_lfree after `nalloc` log allocations (elara_dir.cpp:18: the free stack is popped first).
+__device__ __forceinline__ int64_t nf_after_alloc(int64_t nf0, int64_t nalloc) {
+  return nf0 - (nalloc < nf0 ? nalloc : nf0);
+}
+
+// Counter update of one call from the old values in h (elara_dir.cpp:18-19 alloc, 31 release, 42 MAT, in the
+// reference's order: log allocation, MAT allocation, release); returns n_lfree after the allocation.
+__device__ __forceinline__ int64_t dir_advance(const elr_dir_state& st, int64_t nf0, int64_t top0, int64_t mt0,
+                                               int64_t nalloc, int64_t nmat, int64_t nrel) {
+  const int64_t nf1 = nf_after_alloc(nf0, nalloc);
+  *st.log_top = top0 + nalloc - (nf0 - nf1);
+  *st.mat_top = mt0 + nmat;
+  *st.n_lfree = nf1 + nrel;
+  *st.live = *st.live + nalloc - nrel;
+  return nf1;
+}
+
+// Block offsets of a grid of nblk <= kFusedScanBlocks blocks from its raw per-block counts (channel c at
+// bsum[c*nblk .. c*nblk+nblk)): off[c] = sum over the blocks before this one, tot[c] = sum over all.  Every thread
+// of the block must call it; it synchronises before and after, so it may sit beside other block scans.
+template <int NCH>
+__device__ __forceinline__ void fused_offsets(const int64_t* __restrict__ bsum, int64_t nblk, int64_t (&off)[NCH],
+                                              int64_t (&tot)[NCH]) {
+  __shared__ int sh[NCH];
+  int v[NCH], ex[NCH], t[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) v[c] = (int64_t)threadIdx.x < nblk ? (int)bsum[c * nblk + threadIdx.x] : 0;
+  __syncthreads();
+  block_excl_scan<kDirBlock, NCH>(v, ex, t);
+  if (threadIdx.x == blockIdx.x)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) sh[c] = ex[c];
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    off[c] = sh[c];
+    tot[c] = t[c];
+  }
+  __syncthreads();
 }
 
 __device__ __forceinline__ bool in_range(int64_t x, int64_t hi) { return x >= 0 && x < hi; }
@@ -138,7 +194,9 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st,
                                                                const int8_t* __restrict__ thr_in,
                                                                int64_t* __restrict__ ev_row, uint8_t* __restrict__ rep,
                                                                int64_t* __restrict__ ev_dyn,
-                                                               int64_t* __restrict__ bsum, int64_t nblk) {
+                                                               int64_t* __restrict__ bsum, int64_t nblk,
+                                                               DirHdr* __restrict__ hdr) {
+  dir_snapshot(st, hdr);
   const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
   int v[3] = {0, 0, 0};
   if (i < nev) {
@@ -173,11 +231,10 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st,
     for (int c = 0; c < 3; ++c) bsum[c * nblk + blockIdx.x] = tot[c];
 }
 
-// Single-block exclusive scan of the per-block counts of `nch` channels (in place) and the counter update.
+// Grids of more than kFusedScanBlocks blocks: single-block exclusive scan of the per-block counts of `nch`
+// channels (in place) and the counter update, from the old counters that the count kernel kept in hdr.
 // Channel roles: mode 0 (call A): 0 = log allocations, 1 = MAT allocations, 2 = releases.
 //                mode 1 (call B): 0 = MAT allocations, 1 = releases; `nappend` log allocations (rank = item).
-// Counter arithmetic of elara_dir.cpp:18-19 (alloc), 31 (release), 42 (MAT), in the reference's order: log
-// allocation, MAT allocation, release.
 __global__ __launch_bounds__(kScanBlock) void k_dir_scan(elr_dir_state st, int mode, int64_t nappend,
                                                          int64_t* __restrict__ bsum, int64_t nblk, int nch,
                                                          DirHdr* __restrict__ hdr) {
@@ -190,22 +247,14 @@ __global__ __launch_bounds__(kScanBlock) void k_dir_scan(elr_dir_state st, int m
     const int64_t nalloc = mode == 0 ? chan_tot[0] : nappend;
     const int64_t nmat = mode == 0 ? chan_tot[1] : (nch > 0 ? chan_tot[0] : 0);
     const int64_t nrel = mode == 0 ? chan_tot[2] : (nch > 1 ? chan_tot[1] : 0);
-    DirHdr h;
-    h.nf0 = *st.n_lfree;
-    h.top0 = *st.log_top;
-    h.mt0 = *st.mat_top;
-    const int64_t used = nalloc < h.nf0 ? nalloc : h.nf0;
-    h.nf1 = h.nf0 - used;
-    *st.log_top = h.top0 + nalloc - used;
-    *st.mat_top = h.mt0 + nmat;
-    *st.n_lfree = h.nf1 + nrel;
-    *st.live = *st.live + nalloc - nrel;
-    *hdr = h;
+    hdr->nf1 = dir_advance(st, hdr->nf0, hdr->top0, hdr->mt0, nalloc, nmat, nrel);
   }
 }
 
 // A4: apply the eviction representation (elara_dir.cpp:79-93 except the stack pushes): log ids of rows going back
-// to L (ent, lstep), MAT slots (loc, evf_slots), codes; records each item's release rank for A5.
+// to L (ent, lstep), MAT slots (loc, evf_slots), codes; records each item's release rank for A5.  fused: bsum holds
+// the raw per-block counts (grid of at most kFusedScanBlocks blocks) and block 0 advances the counters; otherwise
+// k_dir_scan has turned bsum into block offsets and advanced them.
 __global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st, elr_dir_params p,
                                                                const int64_t* __restrict__ ev_slot, int64_t nev,
                                                                const int64_t* __restrict__ ev_row,
@@ -214,10 +263,19 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st,
                                                                int64_t* __restrict__ evl_ids,
                                                                int64_t* __restrict__ evf_slots,
                                                                const int64_t* __restrict__ boff, int64_t nblk,
-                                                               const DirHdr* __restrict__ hdr,
-                                                               int64_t* __restrict__ rel_rank) {
+                                                               DirHdr* hdr, int64_t* __restrict__ rel_rank,
+                                                               bool fused) {
   const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
   const int64_t K = p.K;
+  const int64_t nf0 = hdr->nf0, top0 = hdr->top0, mt0 = hdr->mt0;
+  int64_t off[3], gtot[3];
+  if (fused) {
+    fused_offsets<3>(boff, nblk, off, gtot);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, top0, mt0, gtot[0], gtot[1], gtot[2]);
+  } else {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) off[c] = boff[c * nblk + blockIdx.x];
+  }
   int64_t row = -1, c0 = -1, j = 0;
   bool rp = false;
   EvCounts c{0, 0, 0};
@@ -234,16 +292,15 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st,
   int v[3] = {c.nalloc, c.nmat, c.nrel}, ex[3], tot[3];
   dir_block_scan<3>(v, ex, tot);
   if (i >= nev) return;
-  const DirHdr h = *hdr;
   // log ids for the resident history: ent[row, max(c0,0) + k] = id, lstep[id] = pstep[dyn, k]  (k < j)
-  const int64_t rA = boff[0 * nblk + blockIdx.x] + ex[0];
+  const int64_t rA = off[0] + ex[0];
   int64_t dyn = ev_dyn[i];
   if (!in_range(dyn, p.Cdyn)) dyn = p.Cdyn;
   const int64_t kb = c0 > 0 ? c0 : 0;
   for (int64_t k = 0; k < K; ++k) {
     int64_t id = -1;
     if (k < c.nalloc) {
-      id = log_id_of_rank(st.lfree, p.Lcap, h.nf0, h.top0, rA + k);
+      id = log_id_of_rank(st.lfree, p.Lcap, nf0, top0, rA + k);
       if (kb + k < K) st.ent[row * K + kb + k] = (int32_t)id;
       if (in_range(id, p.Lcap)) st.lstep[id] = st.pstep[dyn * K + k];
     }
@@ -253,13 +310,13 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st,
   int64_t slot = -1;
   if (in_range(row, p.R)) {
     const int64_t cur = st.loc[row];
-    slot = c.nmat ? h.mt0 + boff[1 * nblk + blockIdx.x] + ex[1] : cur;
+    slot = c.nmat ? mt0 + off[1] + ex[1] : cur;
     if (c.nmat) st.loc[row] = (int32_t)slot;
     const int64_t tj = c0 + j;
     st.code[row] = rp ? (int8_t)(tj < 127 ? tj : 127) : (int8_t)p.MAT;
   }
   evf_slots[i] = rp ? p.trash : slot;
-  rel_rank[i] = boff[2 * nblk + blockIdx.x] + ex[2];
+  rel_rank[i] = off[2] + ex[2];
 }
 
 // Push the released entries of rows[i] (k < cnt, ent >= 0; `rank` = item's first push rank) and clear them
@@ -301,7 +358,8 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_b_count(elr_dir_state st, elr
                                                            const int64_t* __restrict__ c_rows,
                                                            const int64_t* __restrict__ c_cnt, int64_t nc, int32_t s,
                                                            int64_t* __restrict__ a_ids, int64_t* __restrict__ bsum,
-                                                           int64_t nblk_c, int64_t nblk_a) {
+                                                           int64_t nblk_c, int64_t nblk_a, DirHdr* __restrict__ hdr) {
+  dir_snapshot(st, hdr);
   const int64_t K = p.K;
   if ((int64_t)blockIdx.x < nblk_a) {
     const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
@@ -335,15 +393,29 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_b_count(elr_dir_state st, elr
   }
 }
 
-// B3: compactions (elara_dir.cpp:107-108): MAT slot, release of all logs, code = MAT.
+// B3: compactions (elara_dir.cpp:107-108): MAT slot, release of all logs, code = MAT.  fused: bsum holds the raw
+// per-block counts (grid of at most kFusedScanBlocks blocks, at least one) and block 0 advances the counters for
+// the `na` appends and the compactions; otherwise k_dir_scan has turned bsum into block offsets and advanced them.
 __global__ __launch_bounds__(kDirBlock) void k_dir_b_compact(elr_dir_state st, elr_dir_params p,
                                                              const int64_t* __restrict__ c_rows,
                                                              const int64_t* __restrict__ c_cnt, int64_t nc,
                                                              int64_t* __restrict__ c_slots,
                                                              const int64_t* __restrict__ boff, int64_t nblk,
-                                                             const DirHdr* __restrict__ hdr) {
+                                                             DirHdr* hdr, bool fused, int64_t na) {
   const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
   const int64_t K = p.K;
+  const int64_t mt0 = hdr->mt0;
+  int64_t off[2], gtot[2], nf1;
+  if (fused) {
+    fused_offsets<2>(boff, nblk, off, gtot);
+    const int64_t nf0 = hdr->nf0;
+    nf1 = nf_after_alloc(nf0, na);
+    if (blockIdx.x == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, hdr->top0, mt0, na, gtot[0], gtot[1]);
+  } else {
+    off[0] = boff[blockIdx.x];
+    off[1] = boff[nblk + blockIdx.x];
+    nf1 = hdr->nf1;
+  }
   int64_t row = -1, cnt = 0, cur = -1;
   int v[2] = {0, 0};
   if (i < nc) {
@@ -362,11 +434,10 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_b_compact(elr_dir_state st, e
     c_slots[i] = -1;
     return;
   }
-  const DirHdr h = *hdr;
-  const int64_t slot = v[0] ? h.mt0 + boff[0 * nblk + blockIdx.x] + ex[0] : cur;
+  const int64_t slot = v[0] ? mt0 + off[0] + ex[0] : cur;
   if (v[0]) st.loc[row] = (int32_t)slot;
   c_slots[i] = slot;
-  release_row(st, p, row, cnt, h.nf1 + boff[1 * nblk + blockIdx.x] + ex[1]);
+  release_row(st, p, row, cnt, nf1 + off[1] + ex[1]);
   st.code[row] = (int8_t)p.MAT;
 }
 
@@ -399,11 +470,12 @@ static void launch_evict(const elr_dir_state& S, const elr_dir_params& P, const 
   int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
   int64_t* rel_rank = (int64_t*)(base + align8(sizeof(DirHdr)) + align8(3 * nblk * 8));
   const int64_t* rows = ev_row_in ? ev_row_in : ev_row_out;
+  const bool fused = nblk <= kFusedScanBlocks;
   k_dir_evict_count<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep,
-                                                            ev_dyn, bsum, nblk);
-  k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 0, 0, bsum, nblk, 3, hdr);
+                                                            ev_dyn, bsum, nblk, hdr);
+  if (!fused) k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 0, 0, bsum, nblk, 3, hdr);
   k_dir_evict_apply<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, rows, rep, ev_dyn, evl_ids,
-                                                            evf_slots, bsum, nblk, hdr, rel_rank);
+                                                            evf_slots, bsum, nblk, hdr, rel_rank, fused);
   k_dir_evict_release<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, rows, rep, rel_rank, hdr);
 }
 
@@ -468,11 +540,16 @@ extern "C" int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const
   DirHdr* hdr = (DirHdr*)base;
   const int64_t nblk_c = nblocks(nc), nblk_a = nblocks(na);
   int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
+  const bool fused = nblk_c <= kFusedScanBlocks;
   k_dir_b_count<<<(unsigned)(nblk_a + nblk_c), kDirBlock, 0, strm>>>(S, P, a_rows, a_k, na, c_rows, c_cnt, nc,
-                                                                     (int32_t)s, a_ids, bsum, nblk_c, nblk_a);
-  k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 1, na, bsum, nblk_c, 2, hdr);
-  if (nc) {
-    k_dir_b_compact<<<(unsigned)nblk_c, kDirBlock, 0, strm>>>(S, P, c_rows, c_cnt, nc, c_slots, bsum, nblk_c, hdr);
+                                                                     (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr);
+  if (fused) {   // at least one block: it advances the counters also when there are only appends
+    k_dir_b_compact<<<(unsigned)(nblk_c ? nblk_c : 1), kDirBlock, 0, strm>>>(S, P, c_rows, c_cnt, nc, c_slots, bsum,
+                                                                             nblk_c, hdr, true, na);
+  } else {
+    k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 1, na, bsum, nblk_c, 2, hdr);
+    k_dir_b_compact<<<(unsigned)nblk_c, kDirBlock, 0, strm>>>(S, P, c_rows, c_cnt, nc, c_slots, bsum, nblk_c, hdr,
+                                                              false, na);
   }
   return launch_status();
 }

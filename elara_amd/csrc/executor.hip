@@ -14,11 +14,16 @@
 //   4. compacted rows: Adam from the work array into their new MAT slots; transient F rows back into theirs;
 //   5. appended rows: their gradient into their new log ids;
 //   6. S rows: Adam in place in the MAT arena.
-// Steps 1, 3 and 4 are k_adam_exec launches: the row moves and history records ride on the Adam passes, and the
-// work array is never written back (no later kernel reads it).  Steps 1-3 are the device part and 4-6 the link
-// part (elr_update_args.part): a caller with the arenas in host memory runs the link part on a second stream.
+// Steps 1, 3 and 4 are Adam passes of k_adam_exec: the row moves and history records ride on them, and the work
+// array is never written back (no later kernel reads it).  Step 2 is one launch (both copies), and steps 3-5 share
+// one k_adam_exec launch, block ranges per part (their rows, slots and log ids are disjoint); step 1 stays a launch
+// of its own, since a hit's slot can be evicted in the same step (elara.py:226-227: the eviction copies the state
+// after this step's update).  Steps 1-3 are the device part and 4-6 the link part (elr_update_args.part): a caller
+// with the arenas in host memory runs the link part on a second stream, with each of its steps a launch of its own.
 // D = 64, 128, 256 or 512 with 16-byte aligned arrays: wave-per-row kernels (elr_rowio.h); any other D or alignment:
 // the same launches with the generic kernel, a wave per row whose lanes step through the row one float at a time.
+#include <initializer_list>
+
 #include "elr_rowio.h"
 
 #ifndef ELR_EXEC_U
@@ -27,12 +32,14 @@
 
 namespace elr {
 
-// One Adam launch of the executor with the row moves fused in.  Row i < n reads gradient row g_base + i; with
-// i < n_rec it stores that gradient into entry rec_j[i] (0 when rec_j is NULL) of resident-history slot
-// (rec_dyn ? rec_dyn[i] : its destination row) - rec_off; it reads its state from work row src_base + i (src
+// One part of an Adam launch of the executor with the row moves fused in.  Row i < n reads gradient row
+// g_base + i; with i < n_rec it stores that gradient into entry rec_j[i] (0 when rec_j is NULL) of resident-history
+// slot (rec_dyn ? rec_dyn[i] : its destination row) - rec_off; it reads its state from work row src_base + i (src
 // NULL: in place, from its destination row), applies Adam, and writes the state to destination row dst_a[i]
 // (i < na) or dst_b[i - na].  So the hits record their history and update in place in one pass, and the
-// admitted, compacted and transient rows go from the work array straight to their pool or MAT slots.
+// admitted, compacted and transient rows go from the work array straight to their pool or MAT slots.  With
+// copy set, the part only stores gradient row g_base + i into row dst_a[i] of dst, rows of D floats (the appended
+// rows' log entries).
 struct ExecAdam {
   float* dst;
   int64_t dst_rows;
@@ -48,13 +55,44 @@ struct ExecAdam {
   const int64_t* rec_dyn;
   const int64_t* rec_j;
   int64_t rec_off, n_rec;
+  int copy;
 };
 
+// Up to kExecParts parts in one launch: part q takes the blocks [bbeg[q], bbeg[q+1]) (a grid-stride loop over
+// its rows inside them).
+constexpr int kExecParts = 3;
+struct ExecMulti {
+  ExecAdam part[kExecParts];
+  int64_t bbeg[kExecParts + 1];
+};
+
+// The part of this block (block-uniform) and the block's wave index and wave count within it.
+__device__ __forceinline__ int exec_part(const ExecMulti& x, int64_t& wid, int64_t& wcount) {
+  const int64_t b = blockIdx.x;
+  int q = 0;
+#pragma unroll
+  for (int r = 1; r < kExecParts; ++r) q += b >= x.bbeg[r] ? 1 : 0;
+  const int64_t b0 = x.bbeg[q], nb = x.bbeg[q + 1] - b0;
+  wid = (b - b0) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  wcount = nb * (blockDim.x >> 6);
+  return q;
+}
+
 template <int VPL, int U>
-__global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
+__global__ __launch_bounds__(256) void k_adam_exec(ExecMulti x, AdamScalars s) {
   constexpr int64_t D = 64 * VPL;
   const int lane = threadIdx.x & 63;
-  for (int64_t i0 = wave_id() * U; i0 < a.n; i0 += wave_count() * U) {
+  int64_t wid, wcount;
+  const ExecAdam& a = x.part[exec_part(x, wid, wcount)];
+  if (a.copy) {
+    for (int64_t i = wid; i < a.n; i += wcount) {
+      const int64_t d = a.dst_a[i];
+      if (d < 0 || d >= a.dst_rows) continue;
+      frag_store<VPL>(a.dst + d * D + lane * VPL, frag_load<VPL, true>(a.grad + (a.g_base + i) * D + lane * VPL));
+    }
+    return;
+  }
+  for (int64_t i0 = wid * U; i0 < a.n; i0 += wcount * U) {
     int64_t d[U];
     bool ok[U];
     RowFrag<VPL> g[U], w[U], m[U], v[U];
@@ -95,9 +133,21 @@ __global__ __launch_bounds__(256) void k_adam_exec(ExecAdam a, AdamScalars s) {
 }
 
 // k_adam_exec for any D: a wave per row, lane l handling elements l, l + 64, ... (same rows, same writes).
-__global__ __launch_bounds__(256) void k_adam_exec_gen(ExecAdam a, AdamScalars s, int64_t D) {
+__global__ __launch_bounds__(256) void k_adam_exec_gen(ExecMulti x, AdamScalars s, int64_t D) {
   const int lane = threadIdx.x & 63;
-  for (int64_t i = wave_id(); i < a.n; i += wave_count()) {
+  int64_t wid, wcount;
+  const ExecAdam& a = x.part[exec_part(x, wid, wcount)];
+  if (a.copy) {
+    for (int64_t i = wid; i < a.n; i += wcount) {
+      const int64_t d = a.dst_a[i];
+      if (d < 0 || d >= a.dst_rows) continue;
+      const float* g = a.grad + (a.g_base + i) * D;
+      float* o = a.dst + d * D;
+      for (int64_t j = lane; j < D; j += 64) o[j] = g[j];
+    }
+    return;
+  }
+  for (int64_t i = wid; i < a.n; i += wcount) {
     const int64_t d = i < a.na ? a.dst_a[i] : a.dst_b[i - a.na];
     const float* g = a.grad + (a.g_base + i) * D;
     if (i < a.n_rec) {   // history record (also for a row whose destination is out of range)
@@ -120,19 +170,31 @@ __global__ __launch_bounds__(256) void k_adam_exec_gen(ExecAdam a, AdamScalars s
   }
 }
 
-// vpl = 0: the generic kernel for D.
-static int adam_exec(int vpl, int64_t D, const ExecAdam& a, const AdamScalars& s, hipStream_t st,
-                     int64_t max_blocks = int64_t(1) << 20) {
+// One launch over the parts with rows (vpl = 0: the generic kernel for D), each part on at most max_blocks
+// blocks; without any rows, no launch.
+static int adam_exec(int vpl, int64_t D, std::initializer_list<ExecAdam> parts, const AdamScalars& s,
+                     hipStream_t st, int64_t max_blocks = int64_t(1) << 20) {
   constexpr int U = ELR_EXEC_U;
-  if (a.n <= 0) return ELR_OK;
-  int64_t blocks = (a.n + 4 * U - 1) / (4 * U);
-  if (blocks > max_blocks) blocks = max_blocks;
+  ExecMulti x{};
+  int q = 0;
+  int64_t blocks = 0;
+  for (const ExecAdam& a : parts) {
+    if (a.n <= 0) continue;
+    if (q == kExecParts) return ELR_EINVAL;
+    int64_t nb = (a.n + (a.copy ? 4 : 4 * U) - 1) / (a.copy ? 4 : 4 * U);
+    if (nb > max_blocks) nb = max_blocks;
+    x.part[q] = a;
+    x.bbeg[q++] = blocks;
+    blocks += nb;
+  }
+  if (!q) return ELR_OK;
+  for (int r = q; r <= kExecParts; ++r) x.bbeg[r] = blocks;
   switch (vpl) {
-    case 0: k_adam_exec_gen<<<(unsigned)blocks, 256, 0, st>>>(a, s, D); break;
-    case 1: k_adam_exec<1, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
-    case 2: k_adam_exec<2, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
-    case 4: k_adam_exec<4, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
-    default: k_adam_exec<8, U><<<(unsigned)blocks, 256, 0, st>>>(a, s); break;
+    case 0: k_adam_exec_gen<<<(unsigned)blocks, 256, 0, st>>>(x, s, D); break;
+    case 1: k_adam_exec<1, U><<<(unsigned)blocks, 256, 0, st>>>(x, s); break;
+    case 2: k_adam_exec<2, U><<<(unsigned)blocks, 256, 0, st>>>(x, s); break;
+    case 4: k_adam_exec<4, U><<<(unsigned)blocks, 256, 0, st>>>(x, s); break;
+    default: k_adam_exec<8, U><<<(unsigned)blocks, 256, 0, st>>>(x, s); break;
   }
   return launch_status();
 }
@@ -142,7 +204,7 @@ static int adam_exec(int vpl, int64_t D, const ExecAdam& a, const AdamScalars& s
 extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   using namespace elr;
   if (!a) return ELR_EINVAL;
-  const int64_t D = a->D, K = a->K, RW = 3 * D;
+  const int64_t D = a->D, K = a->K;
   const int64_t* b = a->b;
   if (D <= 0 || K < 1 || a->pool_rows < 0 || a->mat_rows < 0 || a->log_rows < 0 || a->glog_slots < 0)
     return ELR_EINVAL;
@@ -177,35 +239,32 @@ extern "C" int elr_step_update(const elr_update_args* a, void* stream) {
   const AdamScalars s = make_scalars(sc);
   const int64_t nd = a->glog_slots;
   const bool dev_part = a->part != ELR_UPDATE_LINK, link_part = a->part != ELR_UPDATE_DEVICE;
+  // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
+  const ExecAdam adm{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
+                     n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0};
+  // 4. compacted rows into their new MAT slots, transient F rows back into theirs
+  const ExecAdam tail{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work, b[ELR_RANK_NCMP] - w0, G,
+                      b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr, nullptr, 0, 0};
+  // 5. appended rows log their gradient
+  const ExecAdam app{a->logs, a->log_rows, a->a_ids, n_app, nullptr, nullptr, 0, 0, G, b[ELR_RANK_NAPP], n_app,
+                     nullptr, 0, K, nullptr, nullptr, 0, 0, 1};
   if (dev_part) {
     // 1. hits: history record and Adam in place
-    if ((rc = adam_exec(vpl, D, ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
-                                      b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
-                                      rec ? n_hit : 0}, s, st)))
+    if ((rc = adam_exec(vpl, D, {ExecAdam{a->pool, a->pool_rows, a->hit_slot, n_hit, nullptr, nullptr, 0, 0, G,
+                                          b[ELR_RANK_HIT], n_hit, a->glog, nd, K, a->hrec_dyn, a->hrec_j, 0,
+                                          rec ? n_hit : 0}}, s, st)))
       return rc;
     // 2. evictions (before admissions reuse the slots)
-    if (a->nev) {
-      if ((rc = elr_copy_rows(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->nev, RW,
-                              st)))
-        return rc;
-      if ((rc = elr_glog_take(a->logs, a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
-        return rc;
-    }
-    // 3. admitted rows: Adam from the work array into their pool slots, admission record of the N and L rows
-    if ((rc = adam_exec(vpl, D, ExecAdam{a->pool, a->pool_rows, a->adm_slots, n_adm, nullptr, Wk, n_work, 0, G, w0,
-                                      n_adm, a->glog, nd, K, nullptr, nullptr, a->n0, rec ? a->lazy_n : 0}, s, st)))
+    if (a->nev && (rc = evict_move(a->mat, a->mat_rows, a->evf_slots, a->pool, a->pool_rows, a->ev_slot, a->logs,
+                                   a->log_rows, a->evl_ids, a->glog, nd, K, a->ev_dyn, a->nev, D, st)))
       return rc;
+    // 3, with 4 and 5 when the whole update runs here
+    if ((rc = link_part ? adam_exec(vpl, D, {adm, tail, app}, s, st) : adam_exec(vpl, D, {adm}, s, st))) return rc;
+  } else {
+    if ((rc = adam_exec(vpl, D, {tail}, s, st, lb))) return rc;
+    if ((rc = adam_exec(vpl, D, {app}, s, st, lb))) return rc;
   }
   if (!link_part) return ELR_OK;
-  // 4. compacted rows into their new MAT slots, transient F rows back into theirs
-  if ((rc = adam_exec(vpl, D, ExecAdam{a->mat, a->mat_rows, a->c_slots, n_cmp, a->fn_slot, Wk, n_work,
-                                    b[ELR_RANK_NCMP] - w0, G, b[ELR_RANK_NCMP], n_tail, a->glog, nd, K, nullptr,
-                                    nullptr, 0, 0}, s, st, lb)))
-    return rc;
-  // 5. appended rows log their gradient
-  if (n_app && (rc = copy_rows_capped(a->logs, a->log_rows, a->a_ids, G + b[ELR_RANK_NAPP] * D, n_app, n_app, D,
-                                      lb, st)))
-    return rc;
   // 6. S rows: Adam in place in the MAT arena
   if (n_s && (rc = elr_adam_rows(a->mat, a->mat_rows, a->s_slot, 1, G + b[ELR_RANK_S] * D, n_s, D, sc, st)))
     return rc;

@@ -42,37 +42,72 @@ struct IxExpand {   // item i = r * K + k: row clamp(dyn[r], 0, nd - 1) * K + k
   }
 };
 
+// One row copy: n rows of W floats, dst row dix(i) = src row six(i).
+template <class DI, class SI>
+struct CopyPart {
+  float* dst;
+  int64_t dst_rows;
+  DI dix;
+  const float* src;
+  int64_t src_rows;
+  SI six;
+  int64_t n, W;
+};
+
+// Rows wid, wid + wcount, ... of copy c by one wave.
 template <bool V4, class DI, class SI>
-__global__ __launch_bounds__(256) void k_copy_rows(float* __restrict__ dst, int64_t dst_rows, DI dix,
-                                                   const float* __restrict__ src, int64_t src_rows, SI six, int64_t n,
-                                                   int64_t W) {
+__device__ __forceinline__ void copy_part(const CopyPart<DI, SI>& c, int64_t wid, int64_t wcount) {
   const int lane = threadIdx.x & 63;
-  for (int64_t i = wave_id(); i < n; i += wave_count()) {
-    const int64_t d = dix(i);
-    const int64_t s = six(i);
-    if (d < 0 || d >= dst_rows || s < 0 || s >= src_rows) continue;
+  const int64_t W = c.W;
+  for (int64_t i = wid; i < c.n; i += wcount) {
+    const int64_t d = c.dix(i);
+    const int64_t s = c.six(i);
+    if (d < 0 || d >= c.dst_rows || s < 0 || s >= c.src_rows) continue;
     if (V4) {
-      const f32x4* sp = reinterpret_cast<const f32x4*>(src + s * W);
-      f32x4* dp = reinterpret_cast<f32x4*>(dst + d * W);
-      for (int64_t c = lane; c < W / 4; c += 64) dp[c] = sp[c];
+      const f32x4* sp = reinterpret_cast<const f32x4*>(c.src + s * W);
+      f32x4* dp = reinterpret_cast<f32x4*>(c.dst + d * W);
+      for (int64_t k = lane; k < W / 4; k += 64) dp[k] = sp[k];
     } else {
-      const float* sp = src + s * W;
-      float* dp = dst + d * W;
-      for (int64_t c = lane; c < W; c += 64) dp[c] = sp[c];
+      const float* sp = c.src + s * W;
+      float* dp = c.dst + d * W;
+      for (int64_t k = lane; k < W; k += 64) dp[k] = sp[k];
     }
   }
 }
 
+template <bool V4, class DI, class SI>
+__global__ __launch_bounds__(256) void k_copy_rows(CopyPart<DI, SI> c) {
+  copy_part<V4>(c, wave_id(), wave_count());
+}
+
+// Two independent copies in one launch: blocks [0, nb1) take the first, the others the second.
+template <bool V4, class DI1, class SI1, class DI2, class SI2>
+__global__ __launch_bounds__(256) void k_copy_rows2(CopyPart<DI1, SI1> c1, CopyPart<DI2, SI2> c2, int64_t nb1) {
+  const int64_t b = blockIdx.x, wpb = blockDim.x >> 6, w = threadIdx.x >> 6;
+  if (b < nb1) copy_part<V4>(c1, b * wpb + w, nb1 * wpb);
+  else copy_part<V4>(c2, (b - nb1) * wpb + w, ((int64_t)gridDim.x - nb1) * wpb);
+}
+
+template <class DI, class SI>
+inline bool copy_v4(const CopyPart<DI, SI>& c) {
+  return c.W % 4 == 0 && aligned16(c.dst) && aligned16(c.src);
+}
+
+inline int64_t copy_blocks(int64_t n, int64_t max_blocks) {
+  const int64_t b = (n + 3) / 4;
+  return b > max_blocks ? max_blocks : b;
+}
+
+constexpr int64_t kCopyMaxBlocks = 256 * 32;
+
 template <class DI, class SI>
 static int copy_rows_launch(float* dst, int64_t dst_rows, DI dix, const float* src, int64_t src_rows, SI six,
-                            int64_t n, int64_t W, void* stream, int64_t max_blocks = 256 * 32) {
+                            int64_t n, int64_t W, void* stream, int64_t max_blocks = kCopyMaxBlocks) {
   hipStream_t st = (hipStream_t)stream;
-  int64_t blocks = (n + 3) / 4;
-  if (blocks > max_blocks) blocks = max_blocks;
-  if (W % 4 == 0 && aligned16(dst) && aligned16(src))
-    k_copy_rows<true><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dix, src, src_rows, six, n, W);
-  else
-    k_copy_rows<false><<<(unsigned)blocks, 256, 0, st>>>(dst, dst_rows, dix, src, src_rows, six, n, W);
+  const CopyPart<DI, SI> c{dst, dst_rows, dix, src, src_rows, six, n, W};
+  const unsigned blocks = (unsigned)copy_blocks(n, max_blocks);
+  if (copy_v4(c)) k_copy_rows<true><<<blocks, 256, 0, st>>>(c);
+  else k_copy_rows<false><<<blocks, 256, 0, st>>>(c);
   return launch_status();
 }
 
@@ -84,6 +119,24 @@ int copy_rows_capped(float* dst, int64_t dst_rows, const int64_t* dst_idx, const
   if (n == 0) return ELR_OK;
   if (!dst || !src) return ELR_EINVAL;
   return copy_rows_launch(dst, dst_rows, IxList{dst_idx}, src, src_rows, IxList{nullptr}, n, W, stream, max_blocks);
+}
+
+// The executor's eviction moves in one launch: mat[evf_slots[i]] = pool[ev_slot[i]] (rows of 3D floats, i < nev)
+// and the resident histories logs[evl_ids[r*K + k]] = glog[clamp(ev_dyn[r], 0, nd-1), k] (elr_glog_take).
+int evict_move(float* mat, int64_t mat_rows, const int64_t* evf_slots, const float* pool, int64_t pool_rows,
+               const int64_t* ev_slot, float* logs, int64_t log_rows, const int64_t* evl_ids, const float* glog,
+               int64_t nd, int64_t K, const int64_t* ev_dyn, int64_t nev, int64_t D, void* stream) {
+  if (nev < 0 || D <= 0 || nd < 1 || K < 1 || mat_rows < 0 || pool_rows < 0 || log_rows < 0) return ELR_EINVAL;
+  if (nev == 0) return ELR_OK;
+  if (!mat || !evf_slots || !pool || !ev_slot || !logs || !evl_ids || !glog || !ev_dyn) return ELR_EINVAL;
+  const CopyPart<IxList, IxList> c1{mat, mat_rows, IxList{evf_slots}, pool, pool_rows, IxList{ev_slot}, nev, 3 * D};
+  const CopyPart<IxList, IxExpand> c2{logs, log_rows, IxList{evl_ids}, glog, nd * K, IxExpand{ev_dyn, K, nd},
+                                      nev * K, D};
+  const int64_t nb1 = copy_blocks(c1.n, kCopyMaxBlocks), nb2 = copy_blocks(c2.n, kCopyMaxBlocks);
+  hipStream_t st = (hipStream_t)stream;
+  if (copy_v4(c1) && copy_v4(c2)) k_copy_rows2<true><<<(unsigned)(nb1 + nb2), 256, 0, st>>>(c1, c2, nb1);
+  else k_copy_rows2<false><<<(unsigned)(nb1 + nb2), 256, 0, st>>>(c1, c2, nb1);
+  return launch_status();
 }
 
 }  // namespace elr

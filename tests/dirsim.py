@@ -71,6 +71,7 @@ class Sim:
         o = np.argsort(~exp, kind='stable')
         n_exp = int(exp.sum())
         ev_slot, keep_dyn = dl[o[:n_exp]], dl[o[n_exp:]]
+        self.nev_max = max(getattr(self, 'nev_max', 0), int(ev_slot.size))
         c = code[u].astype(I64)
         thr = self.kthr[np.searchsorted(self.toff, u, side='right') - 1].astype(I64)
         isN, isL = c == 0, (c >= 1) & (c <= K)

@@ -108,6 +108,17 @@ def test_gpu_directory_large_multiblock(dev):
 
 
 @pytest.mark.gpu
+def test_gpu_directory_evictions_beyond_fused_scan(dev):
+    """More than 65,536 evictions in a call (more than 256 blocks): the eviction counts are scanned in a launch of
+    their own instead of inside the apply kernel (the smaller calls of every other test take the fused path)."""
+    print('[gpu-test] directory evictions beyond the fused scan', flush=True)
+    sim = Sim(seed=14, R=600_000, C=400_000, n0=2_000, K=3, T=4, batch=500_000, vocab_skew=0.3)
+    st0 = sim.initial_state()
+    run(sim, [OracleImpl(sim, st0), gpu_impl(sim, st0, dev)], 5)
+    assert sim.nev_max > 256 * 256
+
+
+@pytest.mark.gpu
 def test_gpu_dir_b_scan_beyond_one_scan_block(dev):
     """300,000 compactions in one call (more than 1024 blocks: the single-block scan loops over chunks with a
     carry), then 200,000 appends that pop the whole free stack and continue with the bump pointer."""
