@@ -22,102 +22,9 @@
 // Index safety: every gathered or scattered index is checked against its array's extent; an item whose slot, row
 // or entry id is out of range is treated as carrying nothing (no writes).  The reference leaves such inputs
 // undefined.
-#include "elr_scan.h"
+#include "elr_dir_dev.h"
 
 namespace elr {
-
-constexpr int kDirBlock = 256;
-
-// Old counter values kept for the apply steps: block 0 of the count kernel stores nf0, top0 and mt0 (every block of
-// it reads the same counters, which nothing writes during that launch); nf1 comes with the counter update.
-struct DirHdr {
-  int64_t nf0;   // n_lfree before this call's log allocation
-  int64_t top0;  // log_top before it
-  int64_t mt0;   // mat_top before this call's MAT allocation
-  int64_t nf1;   // n_lfree after the log allocation (push base of the releases)
-};
-
-// Grids of at most this many blocks skip the single-block scan launch: each block of the apply kernel sums the
-// per-block counts of the blocks before it itself (one count per thread), and its block 0 advances the counters.
-// Larger grids scan the counts in a launch of their own (k_dir_scan), whose reads then grow with the grid only once.
-constexpr int64_t kFusedScanBlocks = kDirBlock;
-
-template <int NCH>
-__device__ __forceinline__ void dir_block_scan(const int (&v)[NCH], int (&ex)[NCH], int (&tot)[NCH]) {
-  block_excl_scan<kDirBlock, NCH>(v, ex, tot);
-}
-
-__device__ __forceinline__ void dir_snapshot(const elr_dir_state& st, DirHdr* hdr) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) {
-    hdr->nf0 = *st.n_lfree;
-    hdr->top0 = *st.log_top;
-    hdr->mt0 = *st.mat_top;
-  }
-}
-
-// n_lfree after `nalloc` log allocations (elara_dir.cpp:18: the free stack is popped first).
-__device__ __forceinline__ int64_t nf_after_alloc(int64_t nf0, int64_t nalloc) {
-  return nf0 - (nalloc < nf0 ? nalloc : nf0);
-}
-
-// Counter update of one call from the old values in h (elara_dir.cpp:18-19 alloc, 31 release, 42 MAT, in the
-// reference's order: log allocation, MAT allocation, release); returns n_lfree after the allocation.
-__device__ __forceinline__ int64_t dir_advance(const elr_dir_state& st, int64_t nf0, int64_t top0, int64_t mt0,
-                                               int64_t nalloc, int64_t nmat, int64_t nrel) {
-  const int64_t nf1 = nf_after_alloc(nf0, nalloc);
-  *st.log_top = top0 + nalloc - (nf0 - nf1);
-  *st.mat_top = mt0 + nmat;
-  *st.n_lfree = nf1 + nrel;
-  *st.live = *st.live + nalloc - nrel;
-  return nf1;
-}
-
-// Block offsets of a grid of nblk <= kFusedScanBlocks blocks from its raw per-block counts (channel c at
-// bsum[c*nblk .. c*nblk+nblk)): off[c] = sum over the blocks before this one, tot[c] = sum over all.  Every thread
-// of the block must call it; it synchronises before and after, so it may sit beside other block scans.
-template <int NCH>
-__device__ __forceinline__ void fused_offsets(const int64_t* __restrict__ bsum, int64_t nblk, int64_t (&off)[NCH],
-                                              int64_t (&tot)[NCH]) {
-  __shared__ int sh[NCH];
-  int v[NCH], ex[NCH], t[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) v[c] = (int64_t)threadIdx.x < nblk ? (int)bsum[c * nblk + threadIdx.x] : 0;
-  __syncthreads();
-  block_excl_scan<kDirBlock, NCH>(v, ex, t);
-  if (threadIdx.x == blockIdx.x)
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) sh[c] = ex[c];
-  __syncthreads();
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    off[c] = sh[c];
-    tot[c] = t[c];
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ bool in_range(int64_t x, int64_t hi) { return x >= 0 && x < hi; }
-
-// searchsorted(toff, row, right=True) - 1, with ATen's wrap of index -1 to T-1 (elara_dir.cpp:46-48, 75).
-__device__ __forceinline__ int64_t table_of(const int64_t* __restrict__ toff, int64_t T, int64_t row) {
-  int64_t lo = 0, hi = T;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (toff[mid] <= row) lo = mid + 1; else hi = mid;
-  }
-  const int64_t t = lo - 1;
-  return t < 0 ? t + T : t;
-}
-
-// Log id of allocation rank `rank` (elara_dir.cpp:15-17): free stack top-down first, then the bump pointer.
-__device__ __forceinline__ int64_t log_id_of_rank(const int32_t* __restrict__ lfree, int64_t Lcap, int64_t nf0,
-                                                  int64_t top0, int64_t rank) {
-  if (rank < nf0) {
-    const int64_t fi = nf0 - 1 - rank;
-    return in_range(fi, Lcap + 1) ? (int64_t)lfree[fi] : -1;
-  }
-  return top0 + rank - nf0;
-}
 
 // ---------------------------------------------------------------------------------------------------------------
 // A1: replay inputs of L rows (elara_dir.cpp:56-59) and resident-history recording of hits (elara_dir.cpp:60-71).
@@ -163,74 +70,6 @@ __global__ __launch_bounds__(kDirBlock) void k_dir_lsteps_hits(elr_dir_state st,
   st.rok[sl] = (int8_t)(ok && !(dyn && !rec));
 }
 
-// Per-item quantities of an eviction (elara_dir.cpp:73-77, 80, 89, 92).
-struct EvCounts {
-  int nalloc;  // log ids for the resident history (rows going back to L): k < j
-  int nmat;    // 1 if the row goes to M and has no MAT slot yet
-  int nrel;    // host-log entries released (rows going to M): k < max(c0, 0) with ent >= 0
-};
-
-__device__ __forceinline__ EvCounts ev_counts(const elr_dir_state& st, const elr_dir_params& p, int64_t row, bool rep,
-                                              int64_t c0, int64_t j) {
-  EvCounts c{0, 0, 0};
-  if (!in_range(row, p.R)) return c;
-  const int64_t K = p.K;
-  if (rep) {
-    c.nalloc = (int)(j < 0 ? 0 : (j > K ? K : j));
-  } else {
-    c.nmat = st.loc[row] < 0 ? 1 : 0;
-    const int64_t cnt = c0 > 0 ? c0 : 0;
-    for (int64_t k = 0; k < K && k < cnt; ++k) c.nrel += st.ent[row * K + k] >= 0 ? 1 : 0;
-  }
-  return c;
-}
-
-// A2: eviction representation and per-block allocation counts (elara_dir.cpp:73-78).  With ev_row_in (the
-// Directory.evict form, srm2/elara_kernels.py:152-171) the caller supplies the evicted rows and their thresholds
-// and has already cleared slot_of / slot_row; otherwise the rows come from slot_row and are unmapped here.
-__global__ __launch_bounds__(kDirBlock) void k_dir_evict_count(elr_dir_state st, elr_dir_params p,
-                                                               const int64_t* __restrict__ ev_slot, int64_t nev,
-                                                               const int64_t* __restrict__ ev_row_in,
-                                                               const int8_t* __restrict__ thr_in,
-                                                               int64_t* __restrict__ ev_row, uint8_t* __restrict__ rep,
-                                                               int64_t* __restrict__ ev_dyn,
-                                                               int64_t* __restrict__ bsum, int64_t nblk,
-                                                               DirHdr* __restrict__ hdr) {
-  dir_snapshot(st, hdr);
-  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
-  int v[3] = {0, 0, 0};
-  if (i < nev) {
-    const int64_t sl = ev_slot[i];
-    const int64_t C = p.n0 + p.Cdyn;
-    int64_t row = -1, c0 = -1, j = 0;
-    bool rp = false;
-    if (in_range(sl, C)) {
-      row = ev_row_in ? ev_row_in[i] : st.slot_row[sl];
-      c0 = st.adm_c0[sl];
-      j = st.rj[sl];
-      if (p.evl && in_range(row, p.R)) {
-        const int64_t th = thr_in ? (int64_t)thr_in[i] : (int64_t)st.kthr[table_of(st.toff, st.T, row)];
-        rp = st.rok[sl] != 0 && (c0 + j) <= th;
-      }
-      if (!ev_row_in) {
-        if (in_range(row, p.R)) st.slot_of[row] = -1;
-        st.slot_row[sl] = -1;
-      }
-    }
-    if (!ev_row_in) ev_row[i] = row;
-    rep[i] = rp ? 1 : 0;
-    ev_dyn[i] = sl - p.n0;
-    const EvCounts c = ev_counts(st, p, row, rp, c0, j);
-    v[0] = c.nalloc;
-    v[1] = c.nmat;
-    v[2] = c.nrel;
-  }
-  int ex[3], tot[3];
-  dir_block_scan<3>(v, ex, tot);
-  if (threadIdx.x == 0)
-    for (int c = 0; c < 3; ++c) bsum[c * nblk + blockIdx.x] = tot[c];
-}
-
 // Grids of more than kFusedScanBlocks blocks: single-block exclusive scan of the per-block counts of `nch`
 // channels (in place) and the counter update, from the old counters that the count kernel kept in hdr.
 // Channel roles: mode 0 (call A): 0 = log allocations, 1 = MAT allocations, 2 = releases.
@@ -251,203 +90,6 @@ __global__ __launch_bounds__(kScanBlock) void k_dir_scan(elr_dir_state st, int m
   }
 }
 
-// A4: apply the eviction representation (elara_dir.cpp:79-93 except the stack pushes): log ids of rows going back
-// to L (ent, lstep), MAT slots (loc, evf_slots), codes; records each item's release rank for A5.  fused: bsum holds
-// the raw per-block counts (grid of at most kFusedScanBlocks blocks) and block 0 advances the counters; otherwise
-// k_dir_scan has turned bsum into block offsets and advanced them.
-__global__ __launch_bounds__(kDirBlock) void k_dir_evict_apply(elr_dir_state st, elr_dir_params p,
-                                                               const int64_t* __restrict__ ev_slot, int64_t nev,
-                                                               const int64_t* __restrict__ ev_row,
-                                                               const uint8_t* __restrict__ rep,
-                                                               const int64_t* __restrict__ ev_dyn,
-                                                               int64_t* __restrict__ evl_ids,
-                                                               int64_t* __restrict__ evf_slots,
-                                                               const int64_t* __restrict__ boff, int64_t nblk,
-                                                               DirHdr* hdr, int64_t* __restrict__ rel_rank,
-                                                               bool fused) {
-  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
-  const int64_t K = p.K;
-  const int64_t nf0 = hdr->nf0, top0 = hdr->top0, mt0 = hdr->mt0;
-  int64_t off[3], gtot[3];
-  if (fused) {
-    fused_offsets<3>(boff, nblk, off, gtot);
-    if (blockIdx.x == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, top0, mt0, gtot[0], gtot[1], gtot[2]);
-  } else {
-#pragma unroll
-    for (int c = 0; c < 3; ++c) off[c] = boff[c * nblk + blockIdx.x];
-  }
-  int64_t row = -1, c0 = -1, j = 0;
-  bool rp = false;
-  EvCounts c{0, 0, 0};
-  if (i < nev) {
-    const int64_t sl = ev_slot[i];
-    row = ev_row[i];
-    rp = rep[i] != 0;
-    if (in_range(sl, p.n0 + p.Cdyn)) {
-      c0 = st.adm_c0[sl];
-      j = st.rj[sl];
-    }
-    c = ev_counts(st, p, row, rp, c0, j);
-  }
-  int v[3] = {c.nalloc, c.nmat, c.nrel}, ex[3], tot[3];
-  dir_block_scan<3>(v, ex, tot);
-  if (i >= nev) return;
-  // log ids for the resident history: ent[row, max(c0,0) + k] = id, lstep[id] = pstep[dyn, k]  (k < j)
-  const int64_t rA = off[0] + ex[0];
-  int64_t dyn = ev_dyn[i];
-  if (!in_range(dyn, p.Cdyn)) dyn = p.Cdyn;
-  const int64_t kb = c0 > 0 ? c0 : 0;
-  for (int64_t k = 0; k < K; ++k) {
-    int64_t id = -1;
-    if (k < c.nalloc) {
-      id = log_id_of_rank(st.lfree, p.Lcap, nf0, top0, rA + k);
-      if (kb + k < K) st.ent[row * K + kb + k] = (int32_t)id;
-      if (in_range(id, p.Lcap)) st.lstep[id] = st.pstep[dyn * K + k];
-    }
-    evl_ids[i * K + k] = id;
-  }
-  // MAT slot for rows going to M (elara_dir.cpp:36-44, 89-90); rows going back to L get the trash slot
-  int64_t slot = -1;
-  if (in_range(row, p.R)) {
-    const int64_t cur = st.loc[row];
-    slot = c.nmat ? mt0 + off[1] + ex[1] : cur;
-    if (c.nmat) st.loc[row] = (int32_t)slot;
-    const int64_t tj = c0 + j;
-    st.code[row] = rp ? (int8_t)(tj < 127 ? tj : 127) : (int8_t)p.MAT;
-  }
-  evf_slots[i] = rp ? p.trash : slot;
-  rel_rank[i] = off[2] + ex[2];
-}
-
-// Push the released entries of rows[i] (k < cnt, ent >= 0; `rank` = item's first push rank) and clear them
-// (elara_dir.cpp:25-33).
-__device__ __forceinline__ void release_row(const elr_dir_state& st, const elr_dir_params& p, int64_t row,
-                                            int64_t cnt, int64_t push_at) {
-  const int64_t K = p.K;
-  int64_t q = 0;
-  for (int64_t k = 0; k < K && k < cnt; ++k) {
-    const int32_t e = st.ent[row * K + k];
-    if (e >= 0) {
-      const int64_t dst = push_at + q++;
-      if (in_range(dst, p.Lcap)) st.lfree[dst] = e;
-      st.ent[row * K + k] = -1;
-    }
-  }
-}
-
-// A5: releases of rows going to M (after every pop of this call).
-__global__ __launch_bounds__(kDirBlock) void k_dir_evict_release(elr_dir_state st, elr_dir_params p,
-                                                                 const int64_t* __restrict__ ev_slot, int64_t nev,
-                                                                 const int64_t* __restrict__ ev_row,
-                                                                 const uint8_t* __restrict__ rep,
-                                                                 const int64_t* __restrict__ rel_rank,
-                                                                 const DirHdr* __restrict__ hdr) {
-  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
-  if (i >= nev || rep[i]) return;
-  const int64_t row = ev_row[i], sl = ev_slot[i];
-  if (!in_range(row, p.R) || !in_range(sl, p.n0 + p.Cdyn)) return;
-  const int64_t c0 = st.adm_c0[sl];
-  release_row(st, p, row, c0 > 0 ? c0 : 0, hdr->nf1 + rel_rank[i]);
-}
-
-// B1: appends (elara_dir.cpp:102-106; log id of append i has rank i) and per-block counts of the compactions
-// (MAT slots needed, entries released).  Appended and compacted rows are disjoint.
-__global__ __launch_bounds__(kDirBlock) void k_dir_b_count(elr_dir_state st, elr_dir_params p,
-                                                           const int64_t* __restrict__ a_rows,
-                                                           const int64_t* __restrict__ a_k, int64_t na,
-                                                           const int64_t* __restrict__ c_rows,
-                                                           const int64_t* __restrict__ c_cnt, int64_t nc, int32_t s,
-                                                           int64_t* __restrict__ a_ids, int64_t* __restrict__ bsum,
-                                                           int64_t nblk_c, int64_t nblk_a, DirHdr* __restrict__ hdr) {
-  dir_snapshot(st, hdr);
-  const int64_t K = p.K;
-  if ((int64_t)blockIdx.x < nblk_a) {
-    const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
-    if (i >= na) return;
-    const int64_t id = log_id_of_rank(st.lfree, p.Lcap, *st.n_lfree, *st.log_top, i);
-    a_ids[i] = id;
-    const int64_t row = a_rows[i], k = a_k[i];
-    if (in_range(row, p.R) && in_range(k, K)) {
-      st.ent[row * K + k] = (int32_t)id;
-      st.code[row] = (int8_t)(k + 1);
-    }
-    if (in_range(id, p.Lcap)) st.lstep[id] = s;
-    return;
-  }
-  const int64_t b = (int64_t)blockIdx.x - nblk_a;
-  const int64_t i = b * kDirBlock + threadIdx.x;
-  int v[2] = {0, 0};
-  if (i < nc) {
-    const int64_t row = c_rows[i];
-    if (in_range(row, p.R)) {
-      v[0] = st.loc[row] < 0 ? 1 : 0;
-      const int64_t cnt = c_cnt[i];
-      for (int64_t k = 0; k < K && k < cnt; ++k) v[1] += st.ent[row * K + k] >= 0 ? 1 : 0;
-    }
-  }
-  int ex[2], tot[2];
-  dir_block_scan<2>(v, ex, tot);
-  if (threadIdx.x == 0) {
-    bsum[0 * nblk_c + b] = tot[0];
-    bsum[1 * nblk_c + b] = tot[1];
-  }
-}
-
-// B3: compactions (elara_dir.cpp:107-108): MAT slot, release of all logs, code = MAT.  fused: bsum holds the raw
-// per-block counts (grid of at most kFusedScanBlocks blocks, at least one) and block 0 advances the counters for
-// the `na` appends and the compactions; otherwise k_dir_scan has turned bsum into block offsets and advanced them.
-__global__ __launch_bounds__(kDirBlock) void k_dir_b_compact(elr_dir_state st, elr_dir_params p,
-                                                             const int64_t* __restrict__ c_rows,
-                                                             const int64_t* __restrict__ c_cnt, int64_t nc,
-                                                             int64_t* __restrict__ c_slots,
-                                                             const int64_t* __restrict__ boff, int64_t nblk,
-                                                             DirHdr* hdr, bool fused, int64_t na) {
-  const int64_t i = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
-  const int64_t K = p.K;
-  const int64_t mt0 = hdr->mt0;
-  int64_t off[2], gtot[2], nf1;
-  if (fused) {
-    fused_offsets<2>(boff, nblk, off, gtot);
-    const int64_t nf0 = hdr->nf0;
-    nf1 = nf_after_alloc(nf0, na);
-    if (blockIdx.x == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, hdr->top0, mt0, na, gtot[0], gtot[1]);
-  } else {
-    off[0] = boff[blockIdx.x];
-    off[1] = boff[nblk + blockIdx.x];
-    nf1 = hdr->nf1;
-  }
-  int64_t row = -1, cnt = 0, cur = -1;
-  int v[2] = {0, 0};
-  if (i < nc) {
-    row = c_rows[i];
-    cnt = c_cnt[i];
-    if (in_range(row, p.R)) {
-      cur = st.loc[row];
-      v[0] = cur < 0 ? 1 : 0;
-      for (int64_t k = 0; k < K && k < cnt; ++k) v[1] += st.ent[row * K + k] >= 0 ? 1 : 0;
-    }
-  }
-  int ex[2], tot[2];
-  dir_block_scan<2>(v, ex, tot);
-  if (i >= nc) return;
-  if (!in_range(row, p.R)) {
-    c_slots[i] = -1;
-    return;
-  }
-  const int64_t slot = v[0] ? mt0 + off[0] + ex[0] : cur;
-  if (v[0]) st.loc[row] = (int32_t)slot;
-  c_slots[i] = slot;
-  release_row(st, p, row, cnt, nf1 + off[1] + ex[1]);
-  st.code[row] = (int8_t)p.MAT;
-}
-
-inline int64_t nblocks(int64_t n) { return (n + kDirBlock - 1) / kDirBlock; }
-inline int64_t align8(int64_t b) { return (b + 255) & ~int64_t(255); }
-
-// Scratch layout: [DirHdr][bsum: nch * nblk int64][per-item release ranks: nev int64]
-inline int64_t dir_a_scratch(int64_t nev) { return align8(sizeof(DirHdr)) + align8(3 * nblocks(nev) * 8) + nev * 8; }
-inline int64_t dir_b_scratch(int64_t nc) { return align8(sizeof(DirHdr)) + align8(2 * nblocks(nc) * 8); }
-
 inline bool params_ok(const elr_dir_state* st, const elr_dir_params* p) {
   return st && p && p->K >= 1 && p->K <= 126 && p->R >= 0 && p->Lcap >= 0 && p->n0 >= 0 && p->Cdyn >= 0 &&
          st->code && st->loc && st->ent && st->lstep && st->lfree && st->n_lfree && st->log_top && st->mat_top &&
@@ -455,28 +97,95 @@ inline bool params_ok(const elr_dir_state* st, const elr_dir_params* p) {
          st->rok && st->T >= 1;
 }
 
-}  // namespace elr
+DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
+                            const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
+                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, void* scratch) {
+  char* base = (char*)scratch;
+  DirHdr* hdr = (DirHdr*)base;
+  const int64_t nblk = dir_nblocks(nev);
+  int64_t* bsum = (int64_t*)(base + dir_align(sizeof(DirHdr)));
+  int64_t* rel_rank = (int64_t*)(base + dir_align(sizeof(DirHdr)) + dir_align(3 * nblk * 8));
+  const int64_t* rows = ev_row_in ? ev_row_in : ev_row_out;
+  DirEvictPlan e;
+  e.nblk = nblk;
+  e.fused = nblk <= kFusedScanBlocks;
+  e.count = DirEvictCount{S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep, ev_dyn, bsum, nblk, hdr};
+  e.apply = DirEvictApply{S, P, ev_slot, nev, rows, rep, ev_dyn, evl_ids, evf_slots, bsum, nblk, hdr, rel_rank,
+                          e.fused};
+  e.release = DirEvictRelease{S, P, ev_slot, nev, rows, rep, rel_rank, hdr};
+  return e;
+}
 
-namespace elr {
+void dir_evict_scan(const DirEvictPlan& e, hipStream_t strm) {
+  if (!e.fused) k_dir_scan<<<1, kScanBlock, 0, strm>>>(e.count.st, 0, 0, e.count.bsum, e.nblk, 3, e.count.hdr);
+}
+
+DirBPlan dir_b_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* a_rows, const int64_t* a_k,
+                    int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids,
+                    int64_t* c_slots, void* scratch) {
+  char* base = (char*)scratch;
+  DirHdr* hdr = (DirHdr*)base;
+  const int64_t nblk_c = dir_nblocks(nc), nblk_a = dir_nblocks(na);
+  int64_t* bsum = (int64_t*)(base + dir_align(sizeof(DirHdr)));
+  DirBPlan e;
+  e.na = na;
+  e.nblk_c = nblk_c;
+  e.fused = nblk_c <= kFusedScanBlocks;
+  e.count = DirBCount{S, P, a_rows, a_k, na, c_rows, c_cnt, nc, (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr};
+  e.count_blocks = nblk_a + nblk_c;
+  e.compact = DirBCompact{S, P, c_rows, c_cnt, nc, c_slots, bsum, nblk_c, hdr, e.fused, na};
+  // fused: at least one block, which advances the counters also when there are only appends
+  e.compact_blocks = e.fused ? (nblk_c ? nblk_c : 1) : nblk_c;
+  return e;
+}
+
+void dir_b_scan(const DirBPlan& e, hipStream_t strm) {
+  if (!e.fused) k_dir_scan<<<1, kScanBlock, 0, strm>>>(e.count.st, 1, e.na, e.count.bsum, e.nblk_c, 2, e.count.hdr);
+}
+
+int dir_a_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t* hs, int64_t nh, const int64_t* L_row,
+                const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot, int64_t nev, int32_t* L_steps,
+                int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, int64_t* ev_row, uint8_t* rep, int64_t* evl_ids,
+                int64_t* evf_slots, int64_t* ev_dyn, void* scratch, int64_t scratch_bytes) {
+  if (!params_ok(st, p) || nh < 0 || nL < 0 || nev < 0) return ELR_EINVAL;
+  if ((nh && (!hs || !hrec_dyn || !hrec_j)) || (nL && (!L_row || !L_cnt || !L_steps || !L_ids)) ||
+      (nev && (!ev_slot || !ev_row || !rep || !evl_ids || !evf_slots || !ev_dyn)))
+    return ELR_EINVAL;
+  if (nev && (!scratch || scratch_bytes < dir_a_scratch(nev))) return ELR_ECAPACITY;
+  return ELR_OK;
+}
+
+void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
+                            const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s, int32_t* L_steps,
+                            int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm) {
+  const int64_t n1 = nL * P.K + nh;
+  if (n1) {
+    k_dir_lsteps_hits<<<(unsigned)dir_nblocks(n1), kDirBlock, 0, strm>>>(S, P, hs, nh, L_row, L_cnt, nL, (int32_t)s,
+                                                                         L_steps, L_ids, hrec_dyn, hrec_j);
+  }
+}
+
+int dir_b_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,
+                int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t* a_ids, int64_t* c_slots,
+                void* scratch, int64_t scratch_bytes) {
+  if (!params_ok(st, p) || na < 0 || nc < 0) return ELR_EINVAL;
+  if ((na && (!a_rows || !a_k || !a_ids)) || (nc && (!c_rows || !c_cnt || !c_slots))) return ELR_EINVAL;
+  if (na == 0 && nc == 0) return ELR_OK;
+  if (!scratch || scratch_bytes < dir_b_scratch(nc)) return ELR_ECAPACITY;
+  return ELR_OK;
+}
 
 // The eviction part of call A (A2..A5) over nev slots; rows come from ev_row_in when given (then ev_row_out is
 // not written and may be NULL).
 static void launch_evict(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
                          const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
                          int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, void* scratch, hipStream_t strm) {
-  char* base = (char*)scratch;
-  DirHdr* hdr = (DirHdr*)base;
-  const int64_t nblk = nblocks(nev);
-  int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
-  int64_t* rel_rank = (int64_t*)(base + align8(sizeof(DirHdr)) + align8(3 * nblk * 8));
-  const int64_t* rows = ev_row_in ? ev_row_in : ev_row_out;
-  const bool fused = nblk <= kFusedScanBlocks;
-  k_dir_evict_count<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep,
-                                                            ev_dyn, bsum, nblk, hdr);
-  if (!fused) k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 0, 0, bsum, nblk, 3, hdr);
-  k_dir_evict_apply<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, rows, rep, ev_dyn, evl_ids,
-                                                            evf_slots, bsum, nblk, hdr, rel_rank, fused);
-  k_dir_evict_release<<<(unsigned)nblk, kDirBlock, 0, strm>>>(S, P, ev_slot, nev, rows, rep, rel_rank, hdr);
+  const DirEvictPlan e = dir_evict_plan(S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep, evl_ids, evf_slots,
+                                        ev_dyn, scratch);
+  launch1(e.count, e.nblk, strm);
+  dir_evict_scan(e, strm);
+  launch1(e.apply, e.nblk, strm);
+  launch1(e.release, e.nblk, strm);
 }
 
 }  // namespace elr
@@ -493,20 +202,13 @@ extern "C" int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const
                          int64_t* ev_row, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn,
                          void* scratch, int64_t scratch_bytes, void* stream) {
   using namespace elr;
-  if (!params_ok(st, p) || nh < 0 || nL < 0 || nev < 0) return ELR_EINVAL;
-  if ((nh && (!hs || !hrec_dyn || !hrec_j)) || (nL && (!L_row || !L_cnt || !L_steps || !L_ids)) ||
-      (nev && (!ev_slot || !ev_row || !rep || !evl_ids || !evf_slots || !ev_dyn)))
-    return ELR_EINVAL;
-  if (nev && (!scratch || scratch_bytes < dir_a_scratch(nev))) return ELR_ECAPACITY;
+  int rc = dir_a_check(st, p, hs, nh, L_row, L_cnt, nL, ev_slot, nev, L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep,
+                       evl_ids, evf_slots, ev_dyn, scratch, scratch_bytes);
+  if (rc) return rc;
   hipStream_t strm = (hipStream_t)stream;
   const elr_dir_state S = *st;
   const elr_dir_params P = *p;
-  const int32_t s32 = (int32_t)s;
-  const int64_t n1 = nL * P.K + nh;
-  if (n1) {
-    k_dir_lsteps_hits<<<(unsigned)nblocks(n1), kDirBlock, 0, strm>>>(S, P, hs, nh, L_row, L_cnt, nL, s32, L_steps,
-                                                                     L_ids, hrec_dyn, hrec_j);
-  }
+  dir_lsteps_hits_launch(S, P, hs, nh, L_row, L_cnt, nL, s, L_steps, L_ids, hrec_dyn, hrec_j, strm);
   if (nev) launch_evict(S, P, ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids, evf_slots, ev_dyn, scratch, strm);
   return launch_status();
 }
@@ -529,27 +231,12 @@ extern "C" int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const
                          int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s,
                          int64_t* a_ids, int64_t* c_slots, void* scratch, int64_t scratch_bytes, void* stream) {
   using namespace elr;
-  if (!params_ok(st, p) || na < 0 || nc < 0) return ELR_EINVAL;
-  if ((na && (!a_rows || !a_k || !a_ids)) || (nc && (!c_rows || !c_cnt || !c_slots))) return ELR_EINVAL;
-  if (na == 0 && nc == 0) return ELR_OK;
-  if (!scratch || scratch_bytes < dir_b_scratch(nc)) return ELR_ECAPACITY;
+  const int rc = dir_b_check(st, p, a_rows, a_k, na, c_rows, c_cnt, nc, a_ids, c_slots, scratch, scratch_bytes);
+  if (rc || (na == 0 && nc == 0)) return rc;
   hipStream_t strm = (hipStream_t)stream;
-  const elr_dir_state S = *st;
-  const elr_dir_params P = *p;
-  char* base = (char*)scratch;
-  DirHdr* hdr = (DirHdr*)base;
-  const int64_t nblk_c = nblocks(nc), nblk_a = nblocks(na);
-  int64_t* bsum = (int64_t*)(base + align8(sizeof(DirHdr)));
-  const bool fused = nblk_c <= kFusedScanBlocks;
-  k_dir_b_count<<<(unsigned)(nblk_a + nblk_c), kDirBlock, 0, strm>>>(S, P, a_rows, a_k, na, c_rows, c_cnt, nc,
-                                                                     (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr);
-  if (fused) {   // at least one block: it advances the counters also when there are only appends
-    k_dir_b_compact<<<(unsigned)(nblk_c ? nblk_c : 1), kDirBlock, 0, strm>>>(S, P, c_rows, c_cnt, nc, c_slots, bsum,
-                                                                             nblk_c, hdr, true, na);
-  } else {
-    k_dir_scan<<<1, kScanBlock, 0, strm>>>(S, 1, na, bsum, nblk_c, 2, hdr);
-    k_dir_b_compact<<<(unsigned)nblk_c, kDirBlock, 0, strm>>>(S, P, c_rows, c_cnt, nc, c_slots, bsum, nblk_c, hdr,
-                                                              false, na);
-  }
+  const DirBPlan e = dir_b_plan(*st, *p, a_rows, a_k, na, c_rows, c_cnt, nc, s, a_ids, c_slots, scratch);
+  launch1(e.count, e.count_blocks, strm);
+  dir_b_scan(e, strm);
+  launch1(e.compact, e.compact_blocks, strm);
   return launch_status();
 }

@@ -21,6 +21,7 @@
 // occupied dynamic slot satisfies slot_of[slot_row[d]] == d, so the test here is the membership of slot_row[d] in
 // the (ascending, unique) next batches: by binary search, or with one load from the ring of loaded batches
 // (next_bits) when the caller keeps one.
+#include "elr_admit_dev.h"
 #include "elr_scan.h"
 
 namespace elr {
@@ -261,24 +262,6 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
 
 inline int64_t plan_blocks(int64_t m) { return (m + kPlanBlock - 1) / kPlanBlock; }
 
-// Admissions of one step (srm2/elara.py:352-367): row adm_rows[i] takes pool slot adm_slots[i]; the first lazy_n
-// rows are N/L rows (they keep their code as c0 and, with evl, start a resident history whose step 0 is s), the rest
-// are F rows (c0 = -1).
-__device__ __forceinline__ void admit_one(int64_t i, int64_t r, int64_t a, int64_t lazy_n, int evl, int64_t s,
-                                          int64_t n0, int64_t C, int64_t R, int K, const int8_t* __restrict__ code,
-                                          int32_t* __restrict__ slot_of, int64_t* __restrict__ slot_row,
-                                          int8_t* __restrict__ adm_c0, int8_t* __restrict__ rj,
-                                          int8_t* __restrict__ rok, int32_t* __restrict__ pstep) {
-  if (r < 0 || r >= R || a < n0 || a >= C) return;
-  const bool il = i < lazy_n, lazy = il && evl;
-  slot_of[r] = (int32_t)a;
-  slot_row[a] = r;
-  adm_c0[a] = il ? code[r] : (int8_t)-1;
-  rj[a] = lazy ? 1 : 0;
-  rok[a] = lazy ? 1 : 0;
-  if (lazy) pstep[(a - n0) * K] = (int32_t)s;
-}
-
 __global__ __launch_bounds__(kPlanBlock) void k_plan_admit(const int64_t* __restrict__ adm_rows,
                                                            const int64_t* __restrict__ adm_slots, int64_t n_adm,
                                                            int64_t lazy_n, int evl, int64_t s, int64_t n0, int64_t C,
@@ -291,31 +274,6 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_admit(const int64_t* __rest
   if (i >= n_adm) return;
   admit_one(i, adm_rows[i], adm_slots[i], lazy_n, evl, s, n0, C, R, K, code, slot_of, slot_row, adm_c0, rj, rok,
             pstep);
-}
-
-// The pool-slot bookkeeping of the admissions (srm2/elara.py:345-347, 368) together with the admissions: the stack
-// is free_stack[0, n_free) followed by ev_slot[0, nev); its top n_adm entries are the admitted rows' slots (bottom
-// first), the evicted slots below them are written above n_free in place (the stack's reads at positions < n_free
-// and its writes at positions >= n_free never meet), and dyn_out = keep, then the admitted slots.
-__global__ __launch_bounds__(kPlanBlock) void k_plan_admit_slots(elr_slots_args sl, const int64_t* __restrict__ adm_rows,
-                                                                 int64_t n_adm, int64_t lazy_n, int evl, int64_t s,
-                                                                 int64_t n0, int64_t C, int64_t R, int K,
-                                                                 const int8_t* __restrict__ code,
-                                                                 int32_t* __restrict__ slot_of,
-                                                                 int64_t* __restrict__ slot_row,
-                                                                 int8_t* __restrict__ adm_c0, int8_t* __restrict__ rj,
-                                                                 int8_t* __restrict__ rok, int32_t* __restrict__ pstep) {
-  const int64_t i = (int64_t)blockIdx.x * kPlanBlock + threadIdx.x;
-  const int64_t nf = sl.n_free + sl.nev, rest = nf - n_adm;
-  if (i < n_adm) {
-    const int64_t pos = rest + i;
-    const int64_t a = pos < sl.n_free ? sl.free_stack[pos] : sl.ev_slot[pos - sl.n_free];
-    sl.adm_slots[i] = a;
-    sl.dyn_out[sl.nkeep + i] = a;
-    admit_one(i, adm_rows[i], a, lazy_n, evl, s, n0, C, R, K, code, slot_of, slot_row, adm_c0, rj, rok, pstep);
-  }
-  if (i < sl.nkeep) sl.dyn_out[i] = sl.keep[i];
-  if (i < sl.nev && sl.n_free + i < rest) sl.free_stack[sl.n_free + i] = sl.ev_slot[i];
 }
 
 }  // namespace elr
@@ -369,6 +327,24 @@ extern "C" int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots,
   return launch_status();
 }
 
+namespace elr {
+
+int admit_slots_check(const elr_slots_args& sl, const int64_t* adm_rows, int64_t n_adm, int64_t lazy_n, int64_t n0,
+                      int64_t C, int64_t R, int K, const int8_t* code, int32_t* slot_of, int64_t* slot_row,
+                      int8_t* adm_c0, int8_t* rj, int8_t* rok, int32_t* pstep) {
+  if (n_adm < 0 || lazy_n < 0 || lazy_n > n_adm || n0 < 0 || n0 > C || K < 1 || R < 0) return ELR_EINVAL;
+  if (sl.n_free < 0 || sl.nev < 0 || sl.nkeep < 0 || n_adm > sl.n_free + sl.nev || sl.n_free + sl.nev > C)
+    return ELR_EINVAL;
+  if (admit_slots_blocks(sl, n_adm) == 0) return ELR_OK;
+  if ((sl.n_free + sl.nev > 0 && !sl.free_stack) || (sl.nev > 0 && !sl.ev_slot) || (sl.nkeep > 0 && !sl.keep) ||
+      (n_adm + sl.nkeep > 0 && !sl.dyn_out) || (n_adm > 0 && (!sl.adm_slots || !adm_rows || !code || !slot_of ||
+                                                              !slot_row || !adm_c0 || !rj || !rok || !pstep)))
+    return ELR_EINVAL;
+  return ELR_OK;
+}
+
+}  // namespace elr
+
 extern "C" int elr_plan_admit_slots(const elr_slots_args* slots, const int64_t* adm_rows, int64_t n_adm,
                                     int64_t lazy_n, int evl, int64_t s, int64_t n0, int64_t C, int64_t R, int K,
                                     const int8_t* code, int32_t* slot_of, int64_t* slot_row, int8_t* adm_c0, int8_t* rj,
@@ -376,17 +352,12 @@ extern "C" int elr_plan_admit_slots(const elr_slots_args* slots, const int64_t* 
   using namespace elr;
   if (!slots) return ELR_EINVAL;
   const elr_slots_args& sl = *slots;
-  if (n_adm < 0 || lazy_n < 0 || lazy_n > n_adm || n0 < 0 || n0 > C || K < 1 || R < 0) return ELR_EINVAL;
-  if (sl.n_free < 0 || sl.nev < 0 || sl.nkeep < 0 || n_adm > sl.n_free + sl.nev || sl.n_free + sl.nev > C)
-    return ELR_EINVAL;
-  const int64_t m = n_adm > sl.nkeep ? (n_adm > sl.nev ? n_adm : sl.nev) : (sl.nkeep > sl.nev ? sl.nkeep : sl.nev);
-  if (m == 0) return ELR_OK;
-  if ((sl.n_free + sl.nev > 0 && !sl.free_stack) || (sl.nev > 0 && !sl.ev_slot) || (sl.nkeep > 0 && !sl.keep) ||
-      (n_adm + sl.nkeep > 0 && !sl.dyn_out) || (n_adm > 0 && (!sl.adm_slots || !adm_rows || !code || !slot_of ||
-                                                              !slot_row || !adm_c0 || !rj || !rok || !pstep)))
-    return ELR_EINVAL;
-  hipStream_t st = (hipStream_t)stream;
-  k_plan_admit_slots<<<(unsigned)plan_blocks(m), kPlanBlock, 0, st>>>(sl, adm_rows, n_adm, lazy_n, evl, s, n0, C, R, K,
-                                                                       code, slot_of, slot_row, adm_c0, rj, rok, pstep);
+  const int rc = admit_slots_check(sl, adm_rows, n_adm, lazy_n, n0, C, R, K, code, slot_of, slot_row, adm_c0, rj, rok,
+                                   pstep);
+  const int64_t blocks = admit_slots_blocks(sl, n_adm);
+  if (rc || blocks == 0) return rc;
+  launch1(PlanAdmitSlots{sl, adm_rows, n_adm, lazy_n, evl, s, n0, C, R, K, code, slot_of, slot_row, adm_c0, rj, rok,
+                         pstep},
+          blocks, (hipStream_t)stream);
   return launch_status();
 }

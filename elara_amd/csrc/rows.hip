@@ -12,93 +12,14 @@
 // One wave per row, 16-byte accesses when the width and both bases allow it; a row whose source or destination
 // index is out of range is skipped.  Duplicate destinations race (the reference's index_put_ leaves their
 // value unspecified too).
-#include "elr_rowio.h"
+#include "elr_copy_dev.h"
 
 namespace elr {
-
-// Row index maps: the row of item i, or -1 to skip the item.
-struct IxList {   // idx[i] (NULL: i)
-  const int64_t* idx;
-  __device__ __forceinline__ int64_t operator()(int64_t i) const { return idx ? idx[i] : i; }
-};
-struct IxPair {   // row (dyn[i] - off) * K + j[i] of a [nd, K] grid of rows (j NULL: entry 0)
-  const int64_t* dyn;
-  int64_t off;
-  const int64_t* j;
-  int64_t K, nd;
-  __device__ __forceinline__ int64_t operator()(int64_t i) const {
-    const int64_t d = dyn[i] - off, q = j ? j[i] : 0;
-    return d >= 0 && d < nd && q >= 0 && q < K ? d * K + q : -1;
-  }
-};
-struct IxExpand {   // item i = r * K + k: row clamp(dyn[r], 0, nd - 1) * K + k
-  const int64_t* dyn;
-  int64_t K, nd;
-  __device__ __forceinline__ int64_t operator()(int64_t i) const {
-    const int64_t r = i / K, k = i - r * K;
-    int64_t d = dyn[r];
-    d = d < 0 ? 0 : (d >= nd ? nd - 1 : d);
-    return d * K + k;
-  }
-};
-
-// One row copy: n rows of W floats, dst row dix(i) = src row six(i).
-template <class DI, class SI>
-struct CopyPart {
-  float* dst;
-  int64_t dst_rows;
-  DI dix;
-  const float* src;
-  int64_t src_rows;
-  SI six;
-  int64_t n, W;
-};
-
-// Rows wid, wid + wcount, ... of copy c by one wave.
-template <bool V4, class DI, class SI>
-__device__ __forceinline__ void copy_part(const CopyPart<DI, SI>& c, int64_t wid, int64_t wcount) {
-  const int lane = threadIdx.x & 63;
-  const int64_t W = c.W;
-  for (int64_t i = wid; i < c.n; i += wcount) {
-    const int64_t d = c.dix(i);
-    const int64_t s = c.six(i);
-    if (d < 0 || d >= c.dst_rows || s < 0 || s >= c.src_rows) continue;
-    if (V4) {
-      const f32x4* sp = reinterpret_cast<const f32x4*>(c.src + s * W);
-      f32x4* dp = reinterpret_cast<f32x4*>(c.dst + d * W);
-      for (int64_t k = lane; k < W / 4; k += 64) dp[k] = sp[k];
-    } else {
-      const float* sp = c.src + s * W;
-      float* dp = c.dst + d * W;
-      for (int64_t k = lane; k < W; k += 64) dp[k] = sp[k];
-    }
-  }
-}
 
 template <bool V4, class DI, class SI>
 __global__ __launch_bounds__(256) void k_copy_rows(CopyPart<DI, SI> c) {
   copy_part<V4>(c, wave_id(), wave_count());
 }
-
-// Two independent copies in one launch: blocks [0, nb1) take the first, the others the second.
-template <bool V4, class DI1, class SI1, class DI2, class SI2>
-__global__ __launch_bounds__(256) void k_copy_rows2(CopyPart<DI1, SI1> c1, CopyPart<DI2, SI2> c2, int64_t nb1) {
-  const int64_t b = blockIdx.x, wpb = blockDim.x >> 6, w = threadIdx.x >> 6;
-  if (b < nb1) copy_part<V4>(c1, b * wpb + w, nb1 * wpb);
-  else copy_part<V4>(c2, (b - nb1) * wpb + w, ((int64_t)gridDim.x - nb1) * wpb);
-}
-
-template <class DI, class SI>
-inline bool copy_v4(const CopyPart<DI, SI>& c) {
-  return c.W % 4 == 0 && aligned16(c.dst) && aligned16(c.src);
-}
-
-inline int64_t copy_blocks(int64_t n, int64_t max_blocks) {
-  const int64_t b = (n + 3) / 4;
-  return b > max_blocks ? max_blocks : b;
-}
-
-constexpr int64_t kCopyMaxBlocks = 256 * 32;
 
 template <class DI, class SI>
 static int copy_rows_launch(float* dst, int64_t dst_rows, DI dix, const float* src, int64_t src_rows, SI six,
@@ -129,13 +50,10 @@ int evict_move(float* mat, int64_t mat_rows, const int64_t* evf_slots, const flo
   if (nev < 0 || D <= 0 || nd < 1 || K < 1 || mat_rows < 0 || pool_rows < 0 || log_rows < 0) return ELR_EINVAL;
   if (nev == 0) return ELR_OK;
   if (!mat || !evf_slots || !pool || !ev_slot || !logs || !evl_ids || !glog || !ev_dyn) return ELR_EINVAL;
-  const CopyPart<IxList, IxList> c1{mat, mat_rows, IxList{evf_slots}, pool, pool_rows, IxList{ev_slot}, nev, 3 * D};
-  const CopyPart<IxList, IxExpand> c2{logs, log_rows, IxList{evl_ids}, glog, nd * K, IxExpand{ev_dyn, K, nd},
-                                      nev * K, D};
-  const int64_t nb1 = copy_blocks(c1.n, kCopyMaxBlocks), nb2 = copy_blocks(c2.n, kCopyMaxBlocks);
   hipStream_t st = (hipStream_t)stream;
-  if (copy_v4(c1) && copy_v4(c2)) k_copy_rows2<true><<<(unsigned)(nb1 + nb2), 256, 0, st>>>(c1, c2, nb1);
-  else k_copy_rows2<false><<<(unsigned)(nb1 + nb2), 256, 0, st>>>(c1, c2, nb1);
+  evict_move_visit(evict_move_prep(mat, mat_rows, evf_slots, pool, pool_rows, ev_slot, logs, log_rows, evl_ids, glog,
+                                   nd, K, ev_dyn, nev, D),
+                   [&](const auto& f, int64_t blocks) { launch1(f, blocks, st); });
   return launch_status();
 }
 

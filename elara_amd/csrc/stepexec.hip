@@ -1,8 +1,29 @@
 // The rest of a planned ELARA step in one call (elr_step_exec): directory call A, the admissions with their
-// pool-slot bookkeeping, directory call B, the fused assembly and the update, in the order the planner and
-// executor issue them (srm2/elara.py:271-414, 471-580), with every intermediate array carved from one workspace.
-// Host code only: it calls the library's own entry points, so each piece keeps its checks and kernels.
-#include "elr_common.h"
+// pool-slot bookkeeping, directory call B, the fused assembly and the update (srm2/elara.py:271-414, 471-580), with
+// every intermediate array carved from one workspace.  Each piece keeps its entry point's checks and kernels.
+//
+// The directory's eviction, admission and call-B kernels are small launches (a few dozen blocks each) that wait on
+// one another.  Each of the first four shares its launch with a large row kernel that does not depend on it
+// (elr_launch.h), in this order:
+//   1. call A's replay inputs and hit records
+//   2. eviction counts   + the hits' Adam pass
+//   3. eviction apply    + the assembly of the work rows
+//   4. eviction release  + the eviction moves (states to MAT, histories to the log arena)
+//   5. admissions        + call B's appends and counts
+//   6. call B's compactions
+//   7. the admitted, compacted, transient and appended rows; 8. the S rows
+// (and the directory's scan launches for grids above kFusedScanBlocks).  The pairs touch disjoint data: the
+// eviction kernels read and write only the directory, and their outputs feed later launches; the assembly reads the
+// replay inputs of launch 1, the log and MAT rows of L and F rows and the F rows' MAT slots; the hits write their
+// pool slots and history records, which the eviction moves read two launches later (a hit's slot may be evicted in
+// the same step); the moves read evf_slots and evl_ids of launch 3; the admissions write the slots the eviction
+// kernels of launches 2-4 read, and call B pops the log ids that launch 4 pushed.  (Pairing the apply kernel, the
+// largest of the eviction kernels in registers, with the assembly rather than the Adam pass keeps both pairs at the
+// occupancy of their row kernel.)
+#include "elr_admit_dev.h"
+#include "elr_asm_dev.h"
+#include "elr_dir_dev.h"
+#include "elr_exec_dev.h"
 
 namespace {
 
@@ -64,6 +85,7 @@ extern "C" int64_t elr_step_exec_bytes(const elr_exec_args* args) {
 }
 
 extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_bytes, elr_exec_out* out, void* stream) {
+  using namespace elr;
   if (!args || !out) return ELR_EINVAL;
   const elr_exec_args& a = *args;
   ExecLayout L;
@@ -95,60 +117,66 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   int64_t* c_slots = static_cast<int64_t*>(at(L.o.c_slots));
   float* work = static_cast<float*>(at(L.o.work));
   int rc;
-  // directory call A: replay inputs of the L rows, history records of the hits, the evictions
-  if ((rc = elr_dir_a(&a.dir, &a.pv, a.sl_ord + b[ELR_RANK_HIT], nh, a.L_row, a.L_cnt, nL, a.slots.ev_slot, nev, s,
-                      L_steps, L_ids, hrec_dyn, hrec_j, static_cast<int64_t*>(at(L.o.ev_row)),
-                      static_cast<uint8_t*>(at(L.o.rep)), evl_ids, evf_slots, ev_dyn, at(L.dir_a_scratch),
-                      L.dir_a_scratch_bytes, stream)))
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int64_t* ev_row = static_cast<int64_t*>(at(L.o.ev_row));
+  uint8_t* rep = static_cast<uint8_t*>(at(L.o.rep));
+  // call A: replay inputs of the L rows, history records of the hits, the evictions
+  if ((rc = dir_a_check(&a.dir, &a.pv, a.sl_ord + b[ELR_RANK_HIT], nh, a.L_row, a.L_cnt, nL, a.slots.ev_slot, nev,
+                        L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep, evl_ids, evf_slots, ev_dyn,
+                        at(L.dir_a_scratch), L.dir_a_scratch_bytes)))
     return rc;
   // admissions: the evicted slots pushed on the free stack, the admitted rows' slots popped from its top
   elr_slots_args sl = a.slots;
   sl.adm_slots = adm_slots;
-  if ((rc = elr_plan_admit_slots(&sl, a.u_ord + w0, n_adm, lazy_n, evl ? 1 : 0, s, a.pv.n0, a.pv.n0 + a.pv.Cdyn,
-                                 a.pv.R, (int)K, a.dir.code, a.dir.slot_of, a.dir.slot_row, a.dir.adm_c0, a.dir.rj,
-                                 a.dir.rok, a.dir.pstep, stream)))
+  const int64_t C = a.pv.n0 + a.pv.Cdyn;
+  if ((rc = admit_slots_check(sl, a.u_ord + w0, n_adm, lazy_n, a.pv.n0, C, a.pv.R, (int)K, a.dir.code, a.dir.slot_of,
+                              a.dir.slot_row, a.dir.adm_c0, a.dir.rj, a.dir.rok, a.dir.pstep)))
     return rc;
-  // directory call B: appends (entry index = the row's current count) and compactions of the non-resident lazy rows
-  if ((rc = elr_dir_b(&a.dir, &a.pv, a.u_ord + b[ELR_RANK_NAPP], a.c_ord + b[ELR_RANK_NAPP], na,
-                      a.u_ord + b[ELR_RANK_NCMP], a.c_ord + b[ELR_RANK_NCMP], nc, s, a_ids, c_slots,
-                      at(L.dir_b_scratch), L.dir_b_scratch_bytes, stream)))
+  const PlanAdmitSlots admit{sl, a.u_ord + w0, n_adm, lazy_n, evl ? 1 : 0, s, a.pv.n0, C, a.pv.R, (int)K,
+                             a.dir.code, a.dir.slot_of, a.dir.slot_row, a.dir.adm_c0, a.dir.rj, a.dir.rok,
+                             a.dir.pstep};
+  // call B: appends (entry index = the row's current count) and compactions of the non-resident lazy rows
+  const int64_t* a_rows = a.u_ord + b[ELR_RANK_NAPP];
+  const int64_t* a_k = a.c_ord + b[ELR_RANK_NAPP];
+  const int64_t* c_rows = a.u_ord + b[ELR_RANK_NCMP];
+  const int64_t* c_cnt = a.c_ord + b[ELR_RANK_NCMP];
+  if ((rc = dir_b_check(&a.dir, &a.pv, a_rows, a_k, na, c_rows, c_cnt, nc, a_ids, c_slots, at(L.dir_b_scratch),
+                        L.dir_b_scratch_bytes)))
     return rc;
   // the work rows in class-rank order: admitted N / L / F, appended N / L, compacted N / L, transient F
-  if (nw > 0) {
-    elr_assemble_args g{};
-    g.work = work;
-    g.rows = a.u_ord + w0;
-    g.n = nw;
-    g.D = D;
-    g.K = (int)K;
-    const int rank_of[8] = {ELR_RANK_NADM, ELR_RANK_LADM, ELR_RANK_FADM, ELR_RANK_NAPP,
-                            ELR_RANK_LAPP, ELR_RANK_NCMP, ELR_RANK_LCMP, ELR_RANK_FN};
-    const int kind_of[8] = {ELR_ASM_INIT, ELR_ASM_REPLAY, ELR_ASM_GATHER, ELR_ASM_INIT,
-                            ELR_ASM_REPLAY, ELR_ASM_INIT, ELR_ASM_REPLAY, ELR_ASM_GATHER};
-    const int64_t aux_of[8] = {0, 0, 0, 0, nLa, 0, nLa + nLp, 0};
-    g.nseg = 8;
-    for (int q = 0; q < 8; ++q) {
-      g.seg_end[q] = b[rank_of[q] + 1] - w0;
-      g.seg_kind[q] = kind_of[q];
-      g.seg_aux[q] = aux_of[q];
-    }
-    g.seed = a.seed;
-    g.bound = a.bound;
-    g.L_ids = L_ids;
-    g.L_steps = L_steps;
-    g.L_cnt = a.L_cnt;
-    g.nL = nL;
-    g.logs = a.upd.logs;
-    g.nlogs = a.upd.log_rows;
-    g.table = a.table;
-    g.recip = a.recip;
-    g.table_rows = a.table_rows;
-    g.mat = a.upd.mat;
-    g.mat_rows = a.upd.mat_rows;
-    g.loc = a.dir.loc;
-    g.R = a.pv.R;
-    if ((rc = elr_assemble(&g, stream))) return rc;
+  elr_assemble_args g{};
+  g.work = work;
+  g.rows = a.u_ord + w0;
+  g.n = nw;
+  g.D = D;
+  g.K = (int)K;
+  const int rank_of[8] = {ELR_RANK_NADM, ELR_RANK_LADM, ELR_RANK_FADM, ELR_RANK_NAPP,
+                          ELR_RANK_LAPP, ELR_RANK_NCMP, ELR_RANK_LCMP, ELR_RANK_FN};
+  const int kind_of[8] = {ELR_ASM_INIT, ELR_ASM_REPLAY, ELR_ASM_GATHER, ELR_ASM_INIT,
+                          ELR_ASM_REPLAY, ELR_ASM_INIT, ELR_ASM_REPLAY, ELR_ASM_GATHER};
+  const int64_t aux_of[8] = {0, 0, 0, 0, nLa, 0, nLa + nLp, 0};
+  g.nseg = 8;
+  for (int q = 0; q < 8; ++q) {
+    g.seg_end[q] = b[rank_of[q] + 1] - w0;
+    g.seg_kind[q] = kind_of[q];
+    g.seg_aux[q] = aux_of[q];
   }
+  g.seed = a.seed;
+  g.bound = a.bound;
+  g.L_ids = L_ids;
+  g.L_steps = L_steps;
+  g.L_cnt = a.L_cnt;
+  g.nL = nL;
+  g.logs = a.upd.logs;
+  g.nlogs = a.upd.log_rows;
+  g.table = a.table;
+  g.recip = a.recip;
+  g.table_rows = a.table_rows;
+  g.mat = a.upd.mat;
+  g.mat_rows = a.upd.mat_rows;
+  g.loc = a.dir.loc;
+  g.R = a.pv.R;
+  if (nw > 0 && (rc = assemble_check(g))) return rc;
   // the update: hits, evictions, admissions, compactions, transient and S rows, log appends
   elr_update_args u = a.upd;
   for (int r = 0; r <= ELR_NRANK; ++r) u.b[r] = b[r];
@@ -173,7 +201,42 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   u.s_slot = a.loc_ord + b[ELR_RANK_S];
   u.part = ELR_UPDATE_ALL;
   u.link_blocks = 0;
-  return elr_step_update(&u, stream);
+  UpdatePrep up;
+  if ((rc = update_prep(&u, up))) return rc;
+  ExecMulti hx;
+  int64_t hblocks;
+  exec_multi({up.hits}, int64_t(1) << 20, hx, hblocks);
+
+  // 1.
+  const elr_dir_state S = a.dir;
+  const elr_dir_params P = a.pv;
+  dir_lsteps_hits_launch(S, P, a.sl_ord + b[ELR_RANK_HIT], nh, a.L_row, a.L_cnt, nL, s, L_steps, L_ids, hrec_dyn,
+                         hrec_j, st);
+  // 2-4. (without evictions: the assembly, the hits and no moves)
+  const int64_t ev_blocks = nev ? dir_nblocks(nev) : 0;
+  DirEvictPlan ep{};
+  if (nev)
+    ep = dir_evict_plan(S, P, a.slots.ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids, evf_slots, ev_dyn,
+                        at(L.dir_a_scratch));
+  exec_visit(up.vpl, D, hx, hblocks, up.s, [&](const auto& f, int64_t nb) { launch2(ep.count, ev_blocks, f, nb, st); });
+  if (nev) dir_evict_scan(ep, st);
+  if (nw > 0) assemble_visit(g, [&](const auto& f, int64_t nb) { launch2(ep.apply, ev_blocks, f, nb, st); });
+  else launch1(ep.apply, ev_blocks, st);
+  if (nev) evict_move_visit(up.move, [&](const auto& f, int64_t nb) { launch2(ep.release, ev_blocks, f, nb, st); });
+  // 5-6.
+  const int64_t adm_blocks = admit_slots_blocks(sl, n_adm);
+  if (na || nc) {
+    const DirBPlan bp = dir_b_plan(S, P, a_rows, a_k, na, c_rows, c_cnt, nc, s, a_ids, c_slots, at(L.dir_b_scratch));
+    launch2(admit, adm_blocks, bp.count, bp.count_blocks, st);
+    dir_b_scan(bp, st);
+    launch1(bp.compact, bp.compact_blocks, st);
+  } else {
+    launch1(admit, adm_blocks, st);
+  }
+  // 7-8.
+  if ((rc = launch_status())) return rc;
+  if ((rc = adam_exec(up, {up.adm, up.tail, up.app}, st))) return rc;
+  return update_s_rows(up, st);
 }
 
 extern "C" int elr_abi_sizes(int64_t* out, int n) {

@@ -460,10 +460,12 @@ int elr_step_update(const elr_update_args* args, void* stream);
 /* ---------------------------------------------------------------------------------------------------------
  * The rest of a planned step in one call: srm2/elara.py:271-414 after the class-count synchronisation (call A of
  * the directory, the admissions with the pool-slot bookkeeping, call B), the fused assembly (elara.py:471-489) and
- * the executor's update with the host worker's arena writes (elara.py:491-580), issued from C++ in that order on
- * one stream: elr_dir_a, elr_plan_admit_slots, elr_dir_b, elr_assemble, elr_step_update.  No counterpart in the
- * reference, whose planner issues these as separate torch and extension calls; it is the same work with the
- * per-call host cost of one call.  The caller has classified the batch (elr_plan_classify) and read its counts;
+ * the executor's update with the host worker's arena writes (elara.py:491-580), issued from C++ on the caller's
+ * stream: the kernels of elr_dir_a, elr_plan_admit_slots, elr_dir_b, elr_assemble and elr_step_update, with the
+ * directory's small eviction and admission launches each sharing a launch with an independent row kernel (seven
+ * launches in all when no directory scan needs a launch of its own).  No counterpart in the reference, whose
+ * planner issues these as separate torch and extension calls; it is the same work with the per-call host cost of
+ * one call.  The caller has classified the batch (elr_plan_classify) and read its counts;
  * `ws` (device, >= elr_step_exec_bytes(args) bytes, 256-byte aligned) receives every intermediate array, at the
  * offsets elr_step_exec reports in `out` (bytes from ws).
  * ------------------------------------------------------------------------------------------------------- */
