@@ -36,8 +36,11 @@ inline void launch2(const F1& f1, int64_t n1, const F2& f2, int64_t n2, hipStrea
   else k_run2<F1, F2><<<(unsigned)(n1 + n2), kFunctorBlock, 0, st>>>(f1, n1, f2);
 }
 
-// Global wave index and wave count of a body's block.
-__device__ __forceinline__ int64_t body_wave(int64_t block) { return block * (kFunctorBlock / 64) + (threadIdx.x >> 6); }
+// Global wave index and wave count of a body's block, wave-uniform (SGPR) values: indices derived from them address
+// kernel arguments and row bases with scalar instructions.
+__device__ __forceinline__ int64_t body_wave(int64_t block) {
+  return (int64_t)__builtin_amdgcn_readfirstlane((int)(block * (kFunctorBlock / 64) + (threadIdx.x >> 6)));
+}
 __device__ __forceinline__ int64_t body_waves(int64_t nblocks) { return nblocks * (kFunctorBlock / 64); }
 
 }  // namespace elr
