@@ -603,12 +603,60 @@ def copy_calibration(args):
             'copy_frac_of_hbm_peak': 2 * nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def host_sync_costs(args):
+    """Host time per call of cross-stream ordering against plain launches, with the GPU busy (about 1 ms of work
+    queued first, so that no call waits for the GPU): the measurement behind keeping the C5 step's launches on one
+    stream.  Each figure is the mean over 2,000 calls (1,000 for the composite ones) of one small elementwise
+    launch, an event record, a record plus another stream's wait on it, and a fork / launch / join / launch
+    sequence against two launches on one stream."""
+    import torch
+    dev = torch.device('cuda:0')
+    s0 = torch.cuda.current_stream(dev)
+    s1 = torch.cuda.Stream(device=dev)
+    x = torch.zeros(1 << 20, device=dev)
+    y = torch.zeros(1 << 26, device=dev)
+    ev = [torch.cuda.Event(), torch.cuda.Event()]
+
+    def timed(fn, n):
+        for _ in range(20):
+            y.mul_(1.0001)
+        t0 = time.perf_counter()
+        for i in range(n):
+            fn(i)
+        dt = (time.perf_counter() - t0) / n * 1e6
+        torch.cuda.synchronize()
+        return dt
+
+    def fork_join(i):
+        ev[0].record(s0)
+        s1.wait_event(ev[0])
+        with torch.cuda.stream(s1):
+            x.add_(1)
+        ev[1].record(s1)
+        s0.wait_event(ev[1])
+        x.add_(1)
+
+    def two_launches(i):
+        x.add_(1)
+        x.add_(1)
+    out = {}
+    for rep in range(2):   # the second pass is reported (the first loads code and warms the runtime)
+        out = {'launch_us': timed(lambda i: x.add_(1), 2000),
+               'event_record_us': timed(lambda i: ev[0].record(s0), 2000),
+               'record_and_wait_us': timed(lambda i: (ev[0].record(s0), s1.wait_event(ev[0])), 2000),
+               'fork_launch_join_launch_us': timed(fork_join, 1000),
+               'two_launches_us': timed(two_launches, 1000)}
+    torch.cuda.synchronize()
+    return {'mode': 'hostsync', **out, 'note': 'host microseconds per call, Python and torch overhead included'}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=200)
-    ap.add_argument('--mode', default='headline', choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'rows', 'all'])
+    ap.add_argument('--mode', default='headline',
+                    choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'rows', 'hostsync', 'all'])
     ap.add_argument('--rows-order', default='random', choices=['random', 'consecutive'],
                     help='--mode rows: the order of the updated rows')
     ap.add_argument('--steps-c3', type=int, default=100)
@@ -624,7 +672,7 @@ def main():
               'an all-to-all of occurrence gradients; not implemented); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     fns = {'headline': headline, 'copy': copy_calibration, 'c1': mode_c1, 'c3': mode_c3, 'c4': mode_c4,
-           'c5': mode_c5, 'rows': mode_rows}
+           'c5': mode_c5, 'rows': mode_rows, 'hostsync': host_sync_costs}
     for m in (['headline', 'c1', 'c3', 'c4', 'c5'] if args.mode == 'all' else [args.mode]):
         res = fns[m](args)
         print(json.dumps(res, default=float), flush=True)

@@ -69,7 +69,11 @@ SIGNATURES = {
     'elr_dedup_plan_bytes': (c_i64, [c_i64, c_i64]),
     'elr_dedup_plan': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
     'elr_segment_sum_plan': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
+    'elr_segment_sum_plan_final': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64,
+                                                  c_vp]),
     'elr_plan_classify': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
+    'elr_plan_classify_seg': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64,
+                                             c_vp]),
 }
 
 DIR_FIELDS = ('code', 'loc', 'ent', 'lstep', 'lfree', 'n_lfree', 'log_top', 'mat_top', 'live', 'adm_c0', 'rj',

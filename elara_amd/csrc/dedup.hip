@@ -26,8 +26,8 @@
 // only when both terms are), so starting a group from its first gradient gives the same bits.  Long (Zipf-hot)
 // segments are cut into chunks of 6 groups summed in parallel by different waves (partial sums per group, added in
 // order by the segment's own wave).
-#include "elr_rowio.h"
 #include "elr_scan.h"
+#include "elr_seg_dev.h"
 
 namespace elr {
 
@@ -41,12 +41,8 @@ inline int items_for(int64_t n) { return n >= kBigBatch ? kItemsBig : kItemsSmal
 constexpr int kRadixBins = 256;      // bins of an 8-bit digit; passes take 8, 9 or 10 bits (sort_plan)
 constexpr int kRadixMaxBits = 10;
 constexpr int kRadixMaxBins = 1 << kRadixMaxBits;
-constexpr int kAtenGroup = 10;                          // NROWS_PER_THREAD of ATen's sort path
-constexpr int kGroupsPerChunk = 6;
-constexpr int kSegChunk = kAtenGroup * kGroupsPerChunk;   // occurrences per parallel chunk (sort path)
 constexpr int64_t kAtenSmall = 3072;                      // ATen's windowed path up to this many indices
 constexpr int kAtenWinShift = 4;                          // its window: 16 indices
-constexpr int64_t kHotLen = 240;                          // sort-path segments longer than this are hot
 constexpr int kSegParts = 8;                              // run sums a final-kernel wave loads together
 constexpr int kSegBlock = 256;
 
@@ -291,7 +287,6 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__
 // Sort path.  A segment of more than kHotLen occurrences is hot: the partial-chunk kernel sums all of its runs (its
 // first chunk included) and one block of the final kernel folds the run sums, its four waves loading together.  Any
 // other segment folds its first chunk in the final kernel's wave, and only its later chunks are partial chunks.
-__device__ __forceinline__ bool seg_hot(int64_t L) { return L > kHotLen; }
 __device__ __forceinline__ int part_chunks(int64_t L) {
   return (int)(seg_hot(L) ? (L + kSegChunk - 1) / kSegChunk : (L - 1) / kSegChunk);
 }
@@ -391,69 +386,6 @@ __device__ __forceinline__ void fold_range(const float* __restrict__ grad, int64
           for (int q = 0; q < NQ; ++q) acc[q] = acc[q] + g[u][q];
         }
         prev = o;
-      }
-    }
-  }
-}
-
-// Group sums of the extra chunks (sort path), one wave per chunk (grid-stride over the E work items): chunk wi's
-// group gi goes to parts row wi * kGroupsPerChunk + gi.  The rows of GB groups load together; the sums are stored
-// after the last load (a store in flight would hold up the wait for the next loads).
-template <int NQ>
-__global__ __launch_bounds__(256) void k_seg_partials(const float* __restrict__ grad, int64_t D,
-                                                      const int32_t* __restrict__ sv,
-                                                      const int64_t* __restrict__ seg_start,
-                                                      const int32_t* __restrict__ chunk_off,
-                                                      const int32_t* __restrict__ chunk_seg,
-                                                      const int64_t* __restrict__ d_E, float* __restrict__ parts) {
-  constexpr int GB = NQ == 1 ? 6 : (NQ == 2 ? 3 : 1);
-  constexpr int RB = GB * kAtenGroup;
-  static_assert(kGroupsPerChunk % GB == 0, "whole batches of groups per chunk");
-  const int lane = threadIdx.x & 63;
-  const int64_t E = *d_E;
-  for (int64_t wi = wave_id(); wi < E; wi += wave_count()) {
-    const int64_t u = chunk_seg[wi];
-    const int64_t c = wi - chunk_off[u] + (seg_hot(seg_start[u + 1] - seg_start[u]) ? 0 : 1);
-    const int64_t p0 = seg_start[u] + c * kSegChunk;
-    int64_t p1 = p0 + kSegChunk;
-    const int64_t e = seg_start[u + 1];
-    if (p1 > e) p1 = e;
-    const int len = (int)(p1 - p0);
-    const int32_t my = lane < len ? sv[p0 + lane] : 0;
-    float acc[kGroupsPerChunk][NQ];
-#pragma unroll
-    for (int b = 0; b < kGroupsPerChunk / GB; ++b) {
-      const int k0 = b * RB;
-      if (k0 >= len) break;
-      float g[RB][NQ];
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        if (k0 + r < len) {
-          const int64_t o = (int64_t)__builtin_amdgcn_readlane(my, k0 + r);
-          const float* row = grad + o * D;
-#pragma unroll
-          for (int q = 0; q < NQ; ++q) {
-            const int64_t j = lane + 64 * q;
-            g[r][q] = j < D ? __builtin_nontemporal_load(row + j) : 0.0f;
-          }
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        if (k0 + r < len) {
-          const int gi = b * GB + r / kAtenGroup;
-#pragma unroll
-          for (int q = 0; q < NQ; ++q) acc[gi][q] = r % kAtenGroup == 0 ? g[r][q] : acc[gi][q] + g[r][q];
-        }
-      }
-    }
-#pragma unroll
-    for (int gi = 0; gi < kGroupsPerChunk; ++gi) {
-      if (gi * kAtenGroup >= len) break;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int64_t j = lane + 64 * q;
-        if (j < D) parts[(wi * kGroupsPerChunk + gi) * D + j] = acc[gi][q];
       }
     }
   }
@@ -753,7 +685,6 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
 }
 
 // ---- host side -------------------------------------------------------------------------------------------------
-inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
 
 // Scratch carve-up for n occurrences of width D.
@@ -899,32 +830,26 @@ static void chunk_plan(int64_t n, DedupScratch& S, hipStream_t st) {
   else chunk_plan_items<kItemsSmall>(n, S, st);
 }
 
-// Grid of a grid-stride wave loop: enough blocks to fill the chip several times over, at most one wave per item.
-inline unsigned wave_grid(int64_t items) {
-  int64_t b = cdiv(items, 4);
-  const int64_t cap = 256 * 16;
-  if (b > cap) b = cap;
-  if (b < 1) b = 1;
-  return (unsigned)b;
+
+template <int NQ>
+inline SegPartials<NQ> seg_partials_of(const float* grad, int64_t D, const int32_t* sv, const DedupScratch& S) {
+  return SegPartials<NQ>{grad, D, sv, S.seg_start, S.chunk_off, S.chunk_seg, S.d_tot + 1, S.parts};
 }
 
 template <int NQ, int MODE>
 static void seg_reduce(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
-                       int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+                       int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st, bool partials) {
   const int ws = win_shift_for(n);
-  if (!ws)
-    k_seg_partials<NQ><<<wave_grid(n / kSegChunk + n / kHotLen + 2), 256, 0, st>>>(
-        grad, D, sv, S.seg_start, S.chunk_off, S.chunk_seg, S.d_tot + 1, S.parts);
+  if (!ws && partials) launch1(seg_partials_of<NQ>(grad, D, sv, S), seg_partials_blocks(n), st);
   k_seg_final<NQ, MODE><<<wave_grid(n), 256, 0, st>>>(grad, D, sv, S.seg_start, uniq, S.chunk_off, S.parts, S.d_tot,
                                                        ws, out, nrows, s);
 }
 
 template <int VPL, int MODE>
 static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S, const int64_t* uniq, int64_t n,
-                           float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+                           float* out, int64_t nrows, const AdamScalars& s, hipStream_t st, bool partials) {
   constexpr int64_t D = 64 * VPL;   // sort path only (n > kAtenSmall)
-  k_seg_partials<VPL><<<wave_grid(n / kSegChunk + n / kHotLen + 2), 256, 0, st>>>(
-      grad, D, sv, S.seg_start, S.chunk_off, S.chunk_seg, S.d_tot + 1, S.parts);
+  if (partials) launch1(seg_partials_of<VPL>(grad, D, sv, S), seg_partials_blocks(n), st);
   // one launch per range of at most 2^22 blocks (4 waves of kSegPerWave segments each); U <= n.  The first launch
   // starts with one block per possible hot segment (fewer than n / kHotLen; blocks beyond the count exit at once).
   const int64_t per = kOneShotBlocks * 4 * kSegPerWave;
@@ -939,24 +864,25 @@ static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S
 
 template <int MODE>
 static int seg_reduce_d(const float* grad, int64_t D, const int32_t* sv, DedupScratch& S, const int64_t* uniq,
-                        int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st) {
+                        int64_t n, float* out, int64_t nrows, const AdamScalars& s, hipStream_t st,
+                        bool partials = true) {
   if (aligned16(grad) && aligned16(out) && !win_shift_for(n)) {   // ATen's windowed order: the generic kernels
     switch (D) {
-      case 64: seg_reduce_wpr<1, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
-      case 128: seg_reduce_wpr<2, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
-      case 256: seg_reduce_wpr<4, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
-      case 512: seg_reduce_wpr<8, MODE>(grad, sv, S, uniq, n, out, nrows, s, st); return ELR_OK;
+      case 64: seg_reduce_wpr<1, MODE>(grad, sv, S, uniq, n, out, nrows, s, st, partials); return ELR_OK;
+      case 128: seg_reduce_wpr<2, MODE>(grad, sv, S, uniq, n, out, nrows, s, st, partials); return ELR_OK;
+      case 256: seg_reduce_wpr<4, MODE>(grad, sv, S, uniq, n, out, nrows, s, st, partials); return ELR_OK;
+      case 512: seg_reduce_wpr<8, MODE>(grad, sv, S, uniq, n, out, nrows, s, st, partials); return ELR_OK;
       default: break;
     }
   }
   const int64_t nq = cdiv(D, 64);
   switch (nq) {
-    case 1: seg_reduce<1, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
-    case 2: seg_reduce<2, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    case 1: seg_reduce<1, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st, partials); break;
+    case 2: seg_reduce<2, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st, partials); break;
     case 3:
-    case 4: seg_reduce<4, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    case 4: seg_reduce<4, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st, partials); break;
     case 5: case 6: case 7:
-    case 8: seg_reduce<8, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st); break;
+    case 8: seg_reduce<8, MODE>(grad, D, sv, S, uniq, n, out, nrows, s, st, partials); break;
     default: return ELR_EUNSUPPORTED;
   }
   return ELR_OK;
@@ -1060,10 +986,27 @@ extern "C" int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64
   return launch_status();
 }
 
-extern "C" int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
-                                    int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows,
-                                    void* stream) {
-  using namespace elr;
+namespace elr {
+
+int seg_partials_prep(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan, int64_t plan_bytes,
+                      SegPartialsLaunch& out) {
+  out.blocks = 0;
+  if (!dedup_sizes_ok(n) || D < 1 || key_bits < 1 || key_bits > 64) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!grad || !plan) return ELR_EINVAL;
+  if (D > 512) return ELR_EUNSUPPORTED;
+  DedupScratch S;
+  if (plan_bytes < dedup_scratch_bytes(n, D, &S, const_cast<void*>(plan))) return ELR_ECAPACITY;
+  if (win_shift_for(n)) return ELR_OK;
+  out.a = seg_partials_of<1>(grad, D, S.vals[plan_result_buffer(key_bits)], S);
+  out.blocks = seg_partials_blocks(n);
+  return ELR_OK;
+}
+
+// elr_segment_sum_plan, with or without the partial chunks (computed earlier by elr_plan_classify_seg).
+static int segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                            int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows, void* stream,
+                            bool partials) {
   if (!dedup_sizes_ok(n) || D < 1 || key_bits < 1 || key_bits > 64 || out_rows < 0) return ELR_EINVAL;
   if (n == 0) return ELR_OK;
   if (!grad || !plan || !out) return ELR_EINVAL;
@@ -1072,8 +1015,23 @@ extern "C" int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int
   if (plan_bytes < dedup_scratch_bytes(n, D, &S, const_cast<void*>(plan))) return ELR_ECAPACITY;
   hipStream_t st = (hipStream_t)stream;
   const AdamScalars none{};
-  const int rc = seg_reduce_d<0>(grad, D, S.vals[plan_result_buffer(key_bits)], S, perm, n, out, out_rows, none, st);
+  const int rc = seg_reduce_d<0>(grad, D, S.vals[plan_result_buffer(key_bits)], S, perm, n, out, out_rows, none, st,
+                                 partials);
   return rc != ELR_OK ? rc : launch_status();
+}
+
+}  // namespace elr
+
+extern "C" int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                                    int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows,
+                                    void* stream) {
+  return elr::segment_sum_plan(grad, n, D, key_bits, plan, plan_bytes, perm, out, out_rows, stream, true);
+}
+
+extern "C" int elr_segment_sum_plan_final(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                                          int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows,
+                                          void* stream) {
+  return elr::segment_sum_plan(grad, n, D, key_bits, plan, plan_bytes, perm, out, out_rows, stream, false);
 }
 
 // ---- duplicate-id Adam that allocates nothing ------------------------------------------------------------------

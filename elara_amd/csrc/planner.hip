@@ -22,6 +22,7 @@
 // the (ascending, unique) next batches: by binary search, or with one load from the ring of loaded batches
 // (next_bits) when the caller keeps one.
 #include "elr_admit_dev.h"
+#include "elr_seg_dev.h"
 #include "elr_scan.h"
 
 namespace elr {
@@ -143,10 +144,17 @@ __device__ __forceinline__ int block_class_rank(int k, int (&tot)[NCH]) {
 
 // Pass 1: classify and count per block.  Blocks [0, nbu) take the unique rows, blocks [nbu, nbu + nbd) the dynamic
 // slots.  Block counts go channel-major: bu[c * nbu + b], bd[c * nbd + b]; bbad[b]: the block's rows outside [0, R).
-__global__ __launch_bounds__(kPlanBlock) void k_plan_count(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
-                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd,
-                                                           int64_t* __restrict__ bbad) {
-  const int64_t b = blockIdx.x;
+struct PlanCount {
+  elr_plan_in p;
+  elr_plan_out o;
+  int64_t nbu, nbd;
+  int64_t* bu;
+  int64_t* bd;
+  int64_t* bbad;
+  __device__ void operator()(int64_t b, int64_t) const;
+};
+
+__device__ void PlanCount::operator()(int64_t b, int64_t) const {
   if (b < nbu) {
     __shared__ int nbad;
     if (threadIdx.x == 0) nbad = 0;
@@ -285,9 +293,10 @@ extern "C" int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd) {
   return ((kNumCls * nbu + kDynCh * nbd + nbu + kNumCls + kDynCh + 1) * 8 + 255) & ~int64_t(255);
 }
 
-extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
-                                 void* stream) {
-  using namespace elr;
+namespace elr {
+
+// elr_plan_classify's checks; 0 when the call may launch.
+static int plan_classify_check(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes) {
   if (!in || !out) return ELR_EINVAL;
   const elr_plan_in& p = *in;
   const elr_plan_out& o = *out;
@@ -300,16 +309,47 @@ extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out,
   if (p.nd > 0 && (!p.dyn || !p.slot_row || !p.last_seen || !o.dyn_out)) return ELR_EINVAL;
   if (p.next_bits && (p.R <= 0 || (p.next_mask & (1u << (p.s & 31))))) return ELR_EINVAL;
   if (!scratch || scratch_bytes < elr_plan_scratch_bytes(p.n, p.nd)) return ELR_ECAPACITY;
-  hipStream_t st = (hipStream_t)stream;
+  return ELR_OK;
+}
+
+// The three launches of the classification; the count pass beside the segment sum's partial chunks when given
+// (blocks of the count pass first).
+static int plan_classify_launch(const elr_plan_in& p, const elr_plan_out& o, void* scratch, hipStream_t st,
+                                const SegPartialsLaunch* seg) {
   const int64_t nbu = plan_blocks(p.n), nbd = plan_blocks(p.nd);
   int64_t* bu = (int64_t*)scratch;
   int64_t* bd = bu + kNumCls * nbu;
   int64_t* bbad = bd + kDynCh * nbd;
   int64_t* tot = bbad + nbu;
-  if (nbu + nbd > 0) k_plan_count<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad);
+  const PlanCount count{p, o, nbu, nbd, bu, bd, bbad};
+  if (seg && seg->blocks > 0)
+    seg_partials_visit(*seg, [&](const auto& f, int64_t nb) { launch2(count, nbu + nbd, f, nb, st); });
+  else
+    launch1(count, nbu + nbd, st);
   k_plan_scan<<<kNumCls + kDynCh + 1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot);
   if (nbu + nbd > 0) k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
   return launch_status();
+}
+
+}  // namespace elr
+
+extern "C" int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
+                                 void* stream) {
+  using namespace elr;
+  const int rc = plan_classify_check(in, out, scratch, scratch_bytes);
+  if (rc) return rc;
+  return plan_classify_launch(*in, *out, scratch, (hipStream_t)stream, nullptr);
+}
+
+extern "C" int elr_plan_classify_seg(const elr_plan_in* in, const elr_plan_out* out, void* scratch,
+                                     int64_t scratch_bytes, const float* grad, int64_t n_occ, int64_t D, int key_bits,
+                                     const void* dplan, int64_t dplan_bytes, void* stream) {
+  using namespace elr;
+  int rc = plan_classify_check(in, out, scratch, scratch_bytes);
+  if (rc) return rc;
+  SegPartialsLaunch seg;
+  if ((rc = seg_partials_prep(grad, n_occ, D, key_bits, dplan, dplan_bytes, seg))) return rc;
+  return plan_classify_launch(*in, *out, scratch, (hipStream_t)stream, &seg);
 }
 
 extern "C" int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots, int64_t n_adm, int64_t lazy_n, int evl,

@@ -122,9 +122,11 @@ def unique_plan_async(ids, D, bound=None, nu_out=None):
     return u, plan, nu
 
 
-def segment_sum_plan(grad, plan, out=None, perm=None):
+def segment_sum_plan(grad, plan, out=None, perm=None, partials_done=False):
     """Per-segment sums of grad [n, D] over a unique_plan: segment u into row perm[u] (or u) of out [rows, D]
-    (allocated [U, D] when None), in embedding_dense_backward's summation order for n = plan.n indices."""
+    (allocated [U, D] when None), in embedding_dense_backward's summation order for n = plan.n indices.
+    partials_done: the partial chunks of these gradients over this plan were computed already (planner.plan_classify
+    with seg=(grad, plan)); only the rest of the sum is queued (elr_segment_sum_plan_final)."""
     n, D = plan.n, plan.D
     if not (grad.is_cuda and grad.dtype == torch.float32 and grad.numel() == n * D):
         raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements')
@@ -142,9 +144,10 @@ def segment_sum_plan(grad, plan, out=None, perm=None):
         return out
     g = grad.reshape(n, D).contiguous()
     with _lib.on_device(dev):
-        rc = _lib.lib().elr_segment_sum_plan(_lib.ptr(g), n, D, plan.key_bits, _lib.ptr(plan.buf), plan.nbytes,
-                                             _lib.ptr(perm), _lib.ptr(out), out.shape[0], _lib.stream_of(g))
-    _lib.check(rc, 'elr_segment_sum_plan')
+        fn = _lib.lib().elr_segment_sum_plan_final if partials_done else _lib.lib().elr_segment_sum_plan
+        rc = fn(_lib.ptr(g), n, D, plan.key_bits, _lib.ptr(plan.buf), plan.nbytes, _lib.ptr(perm), _lib.ptr(out),
+                out.shape[0], _lib.stream_of(g))
+    _lib.check(rc, 'elr_segment_sum_plan_final' if partials_done else 'elr_segment_sum_plan')
     return out
 
 

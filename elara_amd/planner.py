@@ -48,7 +48,7 @@ def _check_state(dev, named):
 
 
 def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
-                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None, counts_out=None):
+                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None, counts_out=None, seg=None):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -68,7 +68,11 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
     carry: the 'carry' residency (srm2/elara.py:221, 231-233): a missing row is admitted when it appears in the next
     batches, and every unprotected dynamic slot is expired; otherwise 'ttl'.  live (int64 [1], optional): the live
     log-entry counter, copied into counts[15] for the host.  counts_out (int64 [17] on the device, optional): where
-    the counts go (e.g. a buffer the caller reads together with other values), else a new tensor."""
+    the counts go (e.g. a buffer the caller reads together with other values), else a new tensor.
+
+    seg=(grad, dplan): also the partial chunks of the segment sum of grad [n_occ, D] over the batch's dedup plan
+    (dedup.unique_plan), in the classification's first launch (elr_plan_classify_seg); complete the sum with
+    dedup.segment_sum_plan(grad, dplan, ..., partials_done=True)."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -121,9 +125,20 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
         pin.next_bits, pin.next_mask = next_bits.data_ptr(), int(next_mask) & 0xFFFFFFFF
     pout = _lib.PlanOut(*[t.data_ptr() if t is not None else None for t in out])
     with _lib.on_device(dev):
-        rc = _lib.lib().elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,
-                                          _lib.stream_of(u))
-    _lib.check(rc, 'elr_plan_classify')
+        if seg is None:
+            rc = _lib.lib().elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,
+                                              _lib.stream_of(u))
+        else:
+            grad, dplan = seg
+            n_occ, D = dplan.n, dplan.D
+            if not (grad.is_cuda and grad.device == dev and grad.dtype == torch.float32 and grad.is_contiguous()
+                    and grad.numel() == n_occ * D):
+                raise RuntimeError(f'plan_classify: seg grad must be a contiguous float32 tensor of {n_occ}x{D} on '
+                                   f'{dev}')
+            rc = _lib.lib().elr_plan_classify_seg(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,
+                                                  grad.data_ptr(), n_occ, D, dplan.key_bits, p(dplan.buf),
+                                                  dplan.nbytes, _lib.stream_of(u))
+    _lib.check(rc, 'elr_plan_classify' if seg is None else 'elr_plan_classify_seg')
     return out
 
 

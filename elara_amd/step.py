@@ -92,8 +92,12 @@ class HipBackend:
     def plan_admit_slots(self, *args):
         return plan_admit_slots(*args)
 
-    def segsum(self, g_occ, dplan, U, perm=None):
-        return segment_sum_plan(g_occ, dplan, torch.empty(U, self.D, device=g_occ.device), perm)
+    # the planner's first launch also sums the segment sum's partial chunks (plan_classify(seg=...)); segsum then
+    # queues the rest (partials_done)
+    seg_in_plan = True
+
+    def segsum(self, g_occ, dplan, U, perm=None, partials_done=False):
+        return segment_sum_plan(g_occ, dplan, torch.empty(U, self.D, device=g_occ.device), perm, partials_done)
 
     def assemble(self, rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K):
         return assemble_rows(rows, segs, L_ids, L_steps, L_cnt, logs, mat, loc, K, self.D, self.seed, self.bound,
@@ -521,12 +525,17 @@ class ElaraStep:
                         next_mask=sum(1 << ((s + k) % 32) for k in range(1, self.depth)))
         if self._sync is not None:
             ring['counts_out'] = self._sync[:NCOUNTS]
+        seg_in_plan = g_occ is not None and getattr(self.be, 'seg_in_plan', False)
+        if seg_in_plan:
+            g_occ = g_occ.contiguous()
+            ring['seg'] = (g_occ, dplan)
+        sk = {'partials_done': True} if seg_in_plan else {}
         pc = self.be.plan_classify(u, u_nexts, self.slot_of, self.last_seen, self.code, self.kthr, self.toff,
                                    self.dyn_slots, self.slot_row, self.mat_top, self.log_top, s, K,
                                    self.st_mode == 'T', self.loc, self.R, carry=self.dyn == 'carry', live=self.live,
                                    **ring)
         finish = self._host_list_async(pc.counts)
-        G = self.be.segsum(g_occ, dplan, n, pc.rank) if g_occ is not None else None
+        G = self.be.segsum(g_occ, dplan, n, pc.rank, **sk) if g_occ is not None else None
         vals = finish()
         counts = vals[:10]
         n_exp, n_pre, mat_top, log_top = vals[CNT_EXP], vals[CNT_PRE], vals[CNT_MAT_TOP], vals[CNT_LOG_TOP]
@@ -622,7 +631,7 @@ class ElaraStep:
                                                                        or lt_hi > self.faulted['log'])))
         if native:
             if G is None:
-                G = self.be.segsum(g_occ, dplan, n, rank)
+                G = self.be.segsum(g_occ, dplan, n, rank, **sk)
             p._ws, p._off = self.be.step_exec(self, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord)
             p._dims = dict(nL=nLa + nLp + nLc, K=K, nh=counts[C_HIT], nev=nev, n_adm=n_adm, na=nNp + nLp,
                            nc=nNc + nLc, nw=b[R_S] - b[R_NADM], D=self.D)

@@ -222,6 +222,12 @@ int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, i
                    void* plan, int64_t plan_bytes, int64_t D, void* stream);
 int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan, int64_t plan_bytes,
                          const int64_t* perm, float* out, int64_t out_rows, void* stream);
+/* elr_segment_sum_plan in two parts, for a caller that queues the first beside other work: the partial chunks of
+ * the long segments (written into `plan`; elr_plan_classify_seg computes them with the planner's count pass), then
+ * this call, the rest of the sum.  Same arguments and results as elr_segment_sum_plan once the partial chunks of
+ * the same plan and gradients are in place. */
+int elr_segment_sum_plan_final(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                               int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Planner classification of one step: srm2/elara.py:214-267 (ELARAPlanner.plan up to the class counts) -- the
@@ -302,6 +308,14 @@ typedef struct elr_plan_out {
 int64_t elr_plan_scratch_bytes(int64_t n, int64_t nd);
 int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
                       void* stream);
+/* elr_plan_classify whose first launch also computes the partial chunks of the segment sum of grad [n_occ, D] over
+ * the dedup plan `dplan` (elr_dedup_plan of the same batch; no counterpart in the reference): the two are
+ * independent, and the count pass's small latency-bound blocks then cost no launch of their own.  The segment sum
+ * is completed by elr_segment_sum_plan_final with the same grad and plan.  Errors of either part's arguments are
+ * reported before any launch. */
+int elr_plan_classify_seg(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
+                          const float* grad, int64_t n_occ, int64_t D, int key_bits, const void* dplan,
+                          int64_t dplan_bytes, void* stream);
 
 /* Admissions of one step (srm2/elara.py:352-367): row adm_rows[i] takes dynamic pool slot adm_slots[i]
  * (slot_of, slot_row); the first lazy_n rows are N/L rows (adm_c0 = their code; with evl their resident history

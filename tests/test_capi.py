@@ -123,6 +123,16 @@ def test_planner_executor_dedup_argument_checks():
     q.R, q.s, q.next_mask = 100, 33, 0b10                          # the mask holds the step's own bit (33 % 32)
     assert L.elr_plan_classify(ctypes.byref(q), ctypes.byref(pout), fake, 1 << 20, None) == -1
     assert L.elr_plan_scratch_bytes(-1, 0) == -1 and L.elr_plan_scratch_bytes(1000, 10) > 0
+    # the classification with the segment sum's partial chunks: either part's bad arguments, before any launch
+    assert L.elr_plan_classify_seg(None, None, None, 0, fake, 10, 8, 20, fake, 1 << 20, None) == -1
+    assert L.elr_plan_classify_seg(ctypes.byref(pin), ctypes.byref(pout), fake, 1 << 20, fake, 10, 8, 0, fake,
+                                   1 << 20, None) == -1                                             # key bits
+    assert L.elr_plan_classify_seg(ctypes.byref(pin), ctypes.byref(pout), fake, 1 << 20, fake, 10, 600, 20, fake,
+                                   1 << 30, None) == -2                                             # D > 512
+    assert L.elr_plan_classify_seg(ctypes.byref(pin), ctypes.byref(pout), fake, 1 << 20, fake, 10, 8, 20, fake, 1,
+                                   None) == -3                                                      # plan too small
+    assert L.elr_plan_classify_seg(ctypes.byref(pin), ctypes.byref(pout), fake, 1 << 20, None, 10, 8, 20, fake,
+                                   1 << 20, None) == -1                                             # no gradients
     adm = [None] * 8
     assert L.elr_plan_admit(None, None, 0, 0, 1, 1, 0, 10, 10, 3, *adm[:7], None) == 0              # nothing to do
     assert L.elr_plan_admit(None, None, 3, 4, 1, 1, 0, 10, 10, 3, *adm[:7], None) == -1             # lazy_n > n
@@ -159,6 +169,9 @@ def test_planner_executor_dedup_argument_checks():
     assert L.elr_segment_sum_plan(fake, 10, 600, 20, fake, 1 << 30, None, fake, 10, None) == -2     # D > 512
     assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1, None, fake, 10, None) == -3             # plan too small
     assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1 << 20, None, fake, -1, None) == -1
+    assert L.elr_segment_sum_plan_final(fake, 10, 600, 20, fake, 1 << 30, None, fake, 10, None) == -2
+    assert L.elr_segment_sum_plan_final(fake, 10, 8, 20, fake, 1, None, fake, 10, None) == -3
+    assert L.elr_segment_sum_plan_final(None, 10, 8, 20, fake, 1 << 20, None, fake, 10, None) == -1
     assert L.elr_mark_rows(None, None, -1, 0, None, 0, None, 0, None) == -1
     assert L.elr_mark_rows(None, None, 0, 0, None, 0, None, 0, None) == 0
     assert L.elr_mark_rows(None, fake, 5, 0, fake, 10, None, 0, None) == -1

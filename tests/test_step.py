@@ -257,6 +257,58 @@ def test_gpu_plan_classify_matches_oracle(dev, name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('n_occ,D', [(2_000, 128), (60_000, 128), (400_000, 128), (150_000, 96), (100_000, 64)])
+def test_gpu_plan_classify_seg_matches_separate_calls(dev, n_occ, D):
+    """elr_plan_classify_seg (the classification with the segment sum's partial chunks in its first launch) and
+    elr_segment_sum_plan_final give bitwise what elr_plan_classify and elr_segment_sum_plan give, on Zipf batches
+    with hot ids (partial chunks), a batch on ATen's windowed path (no partial chunks) and widths of the generic
+    kernels.  The split call runs first, on its own freshly sorted plan, so that it cannot read partial chunks the
+    other call left behind."""
+    from elara_amd.dedup import segment_sum_plan, unique_plan
+    from elara_amd.planner import plan_classify
+    print(f'[gpu-test] plan classify seg n={n_occ} D={D}', flush=True)
+    g = torch.Generator(device='cpu').manual_seed(n_occ + D)
+    R, C, T, K = 200_000, 6_000, 4, 3
+    vocab = torch.randperm(R, generator=g)[:50_000]
+    w = 1.0 / torch.arange(1, vocab.numel() + 1, dtype=torch.float64) ** 1.1
+    ids = vocab[torch.multinomial(w, n_occ, replacement=True, generator=g)].to(dev)
+    grad = (torch.randn(n_occ, D, generator=g) * 1e-2).to(dev)
+    slot_of = torch.full((R,), -1, dtype=torch.int32)
+    held = torch.randperm(R, generator=g)[:C - 100]
+    slot_of[held] = torch.arange(C - 100, dtype=torch.int32)
+    slot_row = torch.full((C,), -1, dtype=torch.int64)
+    slot_row[:C - 100] = held
+    state = dict(slot_of=slot_of, last_seen=torch.randint(0, 12, (R,), generator=g, dtype=torch.int32),
+                 code=torch.randint(0, K + 2, (R,), generator=g, dtype=torch.int8),
+                 kthr=torch.randint(0, K + 1, (T,), generator=g, dtype=torch.int8),
+                 toff=torch.tensor([0, R // 4, R // 2, 3 * R // 4], dtype=torch.int64),
+                 dyn=torch.arange(500, C - 100, dtype=torch.int64), slot_row=slot_row,
+                 mat_top=torch.tensor([7], dtype=torch.int64), log_top=torch.tensor([11], dtype=torch.int64))
+    st = {k: v.to(dev) for k, v in state.items()}
+    nxt = [torch.unique(vocab[torch.randint(0, 20_000, (3_000,), generator=g)]).to(dev)]
+    loc = torch.randint(-1, 1000, (R + 1,), generator=g, dtype=torch.int32).to(dev)
+    args = lambda u: (u, nxt, st['slot_of'], st['last_seen'], st['code'], st['kthr'], st['toff'],  # noqa: E731
+                      st['dyn'], st['slot_row'], st['mat_top'], st['log_top'], 6, K, True)
+    u_b, plan_b = unique_plan(ids, D, R)
+    pc_b = plan_classify(*args(u_b), loc=loc, R=R, seg=(grad, plan_b))
+    G_b = segment_sum_plan(grad, plan_b, torch.empty(u_b.numel(), D, device=dev), pc_b.rank, partials_done=True)
+    u_a, plan_a = unique_plan(ids, D, R)
+    pc_a = plan_classify(*args(u_a), loc=loc, R=R)
+    G_a = segment_sum_plan(grad, plan_a, torch.empty(u_a.numel(), D, device=dev), pc_a.rank)
+    torch.cuda.synchronize()
+    assert torch.equal(u_a, u_b)
+    nL = int(pc_a.counts[4] + pc_a.counts[5] + pc_a.counts[6])
+    for f in pc_a._fields:
+        x, y = getattr(pc_a, f), getattr(pc_b, f)
+        if f in ('L_row', 'L_cnt'):   # valid up to the L-row count
+            x, y = x[:nL], y[:nL]
+        assert (x is None) == (y is None) and (x is None or torch.equal(x, y)), f
+    assert torch.equal(G_a, G_b)
+    hot = int(torch.bincount(ids).max())
+    assert (n_occ <= 3072) or hot > 240, hot   # partial chunks exist beyond the windowed path
+
+
+@pytest.mark.gpu
 def test_gpu_plan_classify_skips_rows_out_of_range(dev):
     """Rows of u outside [0, R) come out as class S with no pool slot, code K+1 and MAT slot -1 (which every later
     copy and update skips) and are read nowhere out of bounds; the rows in range are classified as without them."""
