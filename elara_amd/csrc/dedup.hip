@@ -605,8 +605,13 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
   }
   RowFrag<VPL> w[SW], m[SW], v[SW], acc[SW];
   int32_t my[SW];
+  // short: every segment of the wave fits one run of at most FB occurrences (wave-uniform: the lengths are scalar
+  // loads).  Their remaining rows then load together, all segments' at once, before any addition.
+  constexpr int FB = VPL <= 2 ? kAtenGroup : 4;
+  bool short_segs = true;
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
+    short_segs = short_segs && (!ok[q] || len[q] <= FB);
     if (!ok[q]) continue;
     acc[q] = frag_load<VPL, true>(grad + o0[q] * D + lane * VPL);
     if (MODE == 1) {
@@ -617,9 +622,34 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
     }
     my[q] = (lane >= 1 && lane < len[q]) ? sv[s0[q] + lane] : 0;
   }
+  if (short_segs) {
+    // the same additions as the general loop below for one run: ((first + g1) + g2) + ..., then +0 + run
+    RowFrag<VPL> g[SW][FB - 1];
+#pragma unroll
+    for (int q = 0; q < SW; ++q)
+#pragma unroll
+      for (int e = 1; e < FB; ++e)
+        if (ok[q] && e < len[q]) {
+          const int64_t o = (int64_t)__builtin_amdgcn_readlane(my[q], e);
+          g[q][e - 1] = frag_load<VPL, true>(grad + o * D + lane * VPL);
+        }
+#pragma unroll
+    for (int q = 0; q < SW; ++q) {
+      if (!ok[q]) continue;
+      RowFrag<VPL> run = acc[q];
+#pragma unroll
+      for (int e = 1; e < FB; ++e)
+        if (e < len[q]) {
+#pragma unroll
+          for (int j = 0; j < VPL; ++j) run.v[j] = run.v[j] + g[q][e - 1].v[j];
+        }
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) acc[q].v[j] = 0.0f + run.v[j];
+    }
+  }
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
-    if (!ok[q]) continue;
+    if (!ok[q] || short_segs) continue;
     // the first chunk folds here, run by run (runs of kAtenGroup from the segment's first occurrence, which is
     // already in acc); then the later chunks' run sums, kSegParts at a time
     const int inl = (int)(len[q] < kSegChunk ? len[q] : kSegChunk);
