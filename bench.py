@@ -444,10 +444,13 @@ def mode_c1(args):
 
 def mode_c3(args):
     """Config C3: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step with duplicates: dedup, ATen-order
-    segment sum and Adam on the unique rows (elr_adam_dedup).  Four resident batches are cycled."""
+    segment sum and Adam on the unique rows.  Four resident batches are cycled.  Each step's ids are sorted into a
+    dedup plan one step ahead on a second stream (elr_dedup_plan), beside the previous step's sum and Adam on the
+    main stream (elr_adam_dedup_plan), as the ELARA step sorts its batches ahead; --c3-serial: sort, sum and Adam of
+    a step in one call (elr_adam_dedup).  The same work per step either way, with the same results."""
     import torch
     from elara_amd import synth
-    from elara_amd.dedup import adam_dedup
+    from elara_amd.dedup import adam_dedup, adam_dedup_plan, unique_plan_async
     from elara_amd.gpu_ops import init_rows
     dev = torch.device('cuda:0')
     R, D, B, F = 10_000_000, 128, 131_072, 26
@@ -460,14 +463,40 @@ def mode_c3(args):
     gen = torch.Generator(dev).manual_seed(0)
     gs = [torch.randn(B * F, D, device=dev, generator=gen) * 1e-3 for _ in range(4)]
     steps = args.steps_c3
-    el, ms, warmup = _timed_steps(lambda i: adam_dedup(table, ids[i % 4], gs[i % 4], *synth.ADAM, i + 1), steps, 4,
-                                  SETTLE_S)
+    if args.c3_serial:
+        def step(i):
+            adam_dedup(table, ids[i % 4], gs[i % 4], *synth.ADAM, i + 1)
+    else:
+        main = torch.cuda.current_stream(dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(main)   # the resident batches and the table
+        ahead = {}
+
+        def plan(j):
+            with torch.cuda.stream(side):
+                u, p, _ = unique_plan_async(ids[j % 4], D, R)
+                ev = torch.cuda.Event()
+                ev.record()
+            u.record_stream(main)
+            p.buf.record_stream(main)
+            ahead[j] = (u, p, ev)
+
+        def step(i):
+            if i not in ahead:
+                plan(i)
+            u, p, ev = ahead.pop(i)
+            main.wait_event(ev)
+            adam_dedup_plan(table, u, gs[i % 4], p, *synth.ADAM, i + 1)
+            plan(i + 1)
+    el, ms, warmup = _timed_steps(step, steps, 4, SETTLE_S)
     O = B * F
     Umean = float(np.mean(U))
     byts = (O * (4 * D + 8) + Umean * (28 * D + 8)) / 1e9
     return _line('C3 duplicate-id sparse Adam occurrences/s (d=128)', O * steps / el, 'occurrences/s', args, steps,
                  warmup, el, {'workload': 'C3 duplicate-id Adam: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) '
                                           'ids per step, dedup + segment sum in ATen order + Adam',
+                              'dedup': 'one call per step' if args.c3_serial else 'sorted one step ahead on a '
+                                                                                  'second stream',
                               'occurrences_per_step': O, 'unique_rows_per_step': Umean, 'dim': D}, byts,
                  extra={'unique_rows_per_s': Umean * steps / el, 'mean_step_ms_events': float(np.mean(ms))})
 
@@ -660,6 +689,8 @@ def main():
     ap.add_argument('--rows-order', default='random', choices=['random', 'consecutive'],
                     help='--mode rows: the order of the updated rows')
     ap.add_argument('--steps-c3', type=int, default=100)
+    ap.add_argument('--c3-serial', action='store_true',
+                    help='C3: sort, sum and Adam of each step in one call (no dedup ahead on a second stream)')
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')

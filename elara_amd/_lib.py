@@ -71,6 +71,8 @@ SIGNATURES = {
     'elr_segment_sum_plan': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'elr_segment_sum_plan_final': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64,
                                                   c_vp]),
+    'elr_adam_dedup_plan': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp,
+                                           c_vp]),
     'elr_plan_classify': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_plan_classify_seg': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64,
                                              c_vp]),

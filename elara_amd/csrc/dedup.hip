@@ -1064,6 +1064,22 @@ extern "C" int elr_segment_sum_plan_final(const float* grad, int64_t n, int64_t 
   return elr::segment_sum_plan(grad, n, D, key_bits, plan, plan_bytes, perm, out, out_rows, stream, false);
 }
 
+extern "C" int elr_adam_dedup_plan(float* state, int64_t C, const int64_t* uniq, const float* grad, int64_t n,
+                                   int64_t D, int key_bits, const void* plan, int64_t plan_bytes, const float sc[8],
+                                   void* stream) {
+  using namespace elr;
+  if (!dedup_sizes_ok(n) || D < 1 || C < 0 || key_bits < 1 || key_bits > 64 || !sc) return ELR_EINVAL;
+  if (n == 0) return ELR_OK;
+  if (!state || !uniq || !grad || !plan) return ELR_EINVAL;
+  if (D > 512) return ELR_EUNSUPPORTED;
+  DedupScratch S;
+  if (plan_bytes < dedup_scratch_bytes(n, D, &S, const_cast<void*>(plan))) return ELR_ECAPACITY;
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = seg_reduce_d<1>(grad, D, S.vals[plan_result_buffer(key_bits)], S, uniq, n, state, C,
+                                 make_scalars(sc), st);
+  return rc != ELR_OK ? rc : launch_status();
+}
+
 // ---- duplicate-id Adam that allocates nothing ------------------------------------------------------------------
 // elr_adam_dedup with its scratch in a file-scope device array instead of a caller buffer, for callers that cannot
 // allocate device memory (code under graph capture, tight serving loops).  The array (ELR_NOALLOC_SCRATCH_BYTES)

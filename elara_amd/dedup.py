@@ -174,6 +174,29 @@ def embedding_dense_backward(grad_output, indices, num_weights, padding_idx=-1, 
     return out
 
 
+def adam_dedup_plan(pool, u, grad, plan, lr, b1, b2, eps, step):
+    """adam_dedup over a dedup plan made earlier for the same ids (unique_plan / unique_plan_async, for instance
+    queued on another stream a step ahead): u is that call's unique ids (u_full of unique_plan_async: its first
+    U entries, U read on the device), grad [n, D] the occurrence gradients in the ids' order."""
+    n, D = plan.n, plan.D
+    if n == 0:
+        return
+    _check_state(pool)
+    if pool.shape[2] != D:
+        raise RuntimeError(f'adam_dedup_plan: pool rows of width {pool.shape[2]}, plan of width {D}')
+    if not (grad.is_cuda and grad.dtype == torch.float32 and grad.numel() == n * D):
+        raise RuntimeError(f'grad must be a cuda float32 tensor with {n}x{D} elements')
+    if not (u.is_cuda and u.dtype == I64 and u.is_contiguous() and u.numel() >= plan.U):
+        raise RuntimeError('adam_dedup_plan: u must be the plan\'s contiguous int64 unique ids')
+    g = grad.reshape(n, D).contiguous()
+    dev = pool.device
+    s = _scalars8(lr, b1, b2, eps, step)
+    with _lib.on_device(dev):
+        rc = _lib.lib().elr_adam_dedup_plan(_lib.ptr(pool), pool.shape[0], _lib.ptr(u), _lib.ptr(g), n, D,
+                                            plan.key_bits, _lib.ptr(plan.buf), plan.nbytes, s, _lib.stream_of(pool))
+    _lib.check(rc, 'elr_adam_dedup_plan')
+
+
 def adam_dedup(pool, ids, grad, lr, b1, b2, eps, step, check=False):
     """pool [C,3,D] cuda float32 (updated in place); ids int32/int64 [n] rows of pool, repeats allowed; grad [n,D]
     (row i belongs to ids[i]).  Each unique id gets one Adam step with the sum of its gradients.  An id outside

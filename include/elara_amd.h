@@ -228,6 +228,12 @@ int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, 
  * the same plan and gradients are in place. */
 int elr_segment_sum_plan_final(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
                                int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows, void* stream);
+/* elr_adam_dedup over a dedup plan made earlier (elr_dedup_plan of the same ids, possibly on another stream and
+ * ahead of time; no counterpart in the reference, where each step sorts its batch where it updates): uniq is that
+ * call's unique-id output (its first U entries, U on the device in the plan, are the rows updated).  Bitwise what
+ * elr_adam_dedup gives for those ids and gradients; rows outside [0, C) are skipped. */
+int elr_adam_dedup_plan(float* state, int64_t C, const int64_t* uniq, const float* grad, int64_t n, int64_t D,
+                        int key_bits, const void* plan, int64_t plan_bytes, const float sc[8], void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Planner classification of one step: srm2/elara.py:214-267 (ELARAPlanner.plan up to the class counts) -- the

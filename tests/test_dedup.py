@@ -361,6 +361,34 @@ def test_gpu_adam_dedup_matches_oracle(dev, D, idx):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('D,n_field', [(128, 4000), (96, 4000), (64, 4000), (128, 100)])
+def test_gpu_adam_dedup_plan_matches_adam_dedup(dev, D, n_field):
+    """elr_adam_dedup_plan over a plan sorted ahead on a second stream equals elr_adam_dedup bitwise (n_field 100:
+    2,600 ids, ATen's windowed path)."""
+    from elara_amd.dedup import adam_dedup, adam_dedup_plan, unique_plan_async
+    print(f'[gpu-test] adam_dedup_plan D={D} n={n_field * 26}', flush=True)
+    R = 200000
+    rng = np.random.default_rng(17)
+    state = torch.from_numpy((rng.standard_normal((R, 3, D)) * 0.05).astype(np.float32)).to(dev)
+    a, b = state.clone(), state.clone()
+    side = torch.cuda.Stream(device=dev)
+    main = torch.cuda.current_stream(dev)
+    for t in range(1, 4):
+        ids_np, g_np = zipf_case(200 + t, n_field, 26, R, 1.05, D)
+        ids, g = torch.from_numpy(ids_np).to(dev), torch.from_numpy(g_np).to(dev)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            u, plan, _ = unique_plan_async(ids, D, R)
+            ev = torch.cuda.Event()
+            ev.record()
+        main.wait_event(ev)
+        adam_dedup_plan(b, u, g, plan, *HP, t)
+        adam_dedup(a, ids, g, *HP, t)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+
+
+@pytest.mark.gpu
 def test_gpu_dedup_edge_cases(dev):
     from elara_amd.dedup import adam_dedup, embedding_dense_backward, unique
     z = torch.empty(0, dtype=torch.int64, device=dev)
@@ -385,8 +413,9 @@ def test_gpu_dedup_edge_cases(dev):
 def test_gpu_c3_full_size_twelve_steps(dev):
     """Config C3 at full size: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step, 12 steps (the hot
     rows' m and v accumulate over all of them); touched rows bitwise equal to the oracle (segment sum + cpu_adam on
-    a compact copy of the touched rows)."""
-    from elara_amd.dedup import adam_dedup
+    a compact copy of the touched rows).  Even steps take the plan form (elr_dedup_plan, then
+    elr_adam_dedup_plan)."""
+    from elara_amd.dedup import adam_dedup, adam_dedup_plan, unique_plan_async
     from elara_amd.gpu_ops import init_rows
     print('[gpu-test] C3 full size, 12 steps', flush=True)
     R, D, B, F, steps = 10_000_000, 128, 131_072, 26, 12
@@ -399,7 +428,11 @@ def test_gpu_c3_full_size_twelve_steps(dev):
     compact = table[tt].cpu().numpy()
     for t, ids in enumerate(ids_all, start=1):
         g = torch.randn(ids.size, D, device=dev, generator=torch.Generator(dev).manual_seed(t)) * 1e-3
-        adam_dedup(table, torch.from_numpy(ids).to(dev), g, *HP, t)
+        if t % 2:
+            adam_dedup(table, torch.from_numpy(ids).to(dev), g, *HP, t)
+        else:   # the pipelined form bench.py times: a dedup plan made beforehand, then the sum and Adam over it
+            u, plan, _ = unique_plan_async(torch.from_numpy(ids).to(dev), D, R)
+            adam_dedup_plan(table, u, g, plan, *HP, t)
         u, s, _ = O.segment_sum(ids, g.cpu().numpy())
         O.cpu_adam(compact, np.searchsorted(touched, u).astype(np.int64), s, O.adam_scalars(*HP, t), 16)
     torch.cuda.synchronize()
