@@ -222,15 +222,6 @@ inline void launch_timed(Kern kern, unsigned g, hipStream_t st, hipEvent_t e0, h
   else kern<<<g, 256, 0, st>>>(args...);
 }
 
-// dst[dst_idx[i]] = src[i] with at most max_blocks blocks (rows.hip; used by the executor's link part).
-int copy_rows_capped(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
-                     int64_t n, int64_t W, int64_t max_blocks, void* stream);
-
-// The executor's eviction moves (state rows to MAT, resident histories to the log arena) in one launch (rows.hip).
-int evict_move(float* mat, int64_t mat_rows, const int64_t* evf_slots, const float* pool, int64_t pool_rows,
-               const int64_t* ev_slot, float* logs, int64_t log_rows, const int64_t* evl_ids, const float* glog,
-               int64_t nd, int64_t K, const int64_t* ev_dyn, int64_t nev, int64_t D, void* stream);
-
 // VPL for D if the wave-per-row kernels handle it (D = 64, 128, 256, 512), else 0.
 inline int wpr_vpl(int64_t D) {
   switch (D) {

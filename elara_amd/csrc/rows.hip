@@ -32,31 +32,6 @@ static int copy_rows_launch(float* dst, int64_t dst_rows, DI dix, const float* s
   return launch_status();
 }
 
-// elr_copy_rows with at most max_blocks blocks (grid-stride): the executor's link part, whose waves mostly wait on
-// the host link, leaves the rest of the GPU to the other stream.
-int copy_rows_capped(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
-                     int64_t n, int64_t W, int64_t max_blocks, void* stream) {
-  if (n < 0 || W <= 0 || dst_rows < 0 || src_rows < 0 || max_blocks < 1) return ELR_EINVAL;
-  if (n == 0) return ELR_OK;
-  if (!dst || !src) return ELR_EINVAL;
-  return copy_rows_launch(dst, dst_rows, IxList{dst_idx}, src, src_rows, IxList{nullptr}, n, W, stream, max_blocks);
-}
-
-// The executor's eviction moves in one launch: mat[evf_slots[i]] = pool[ev_slot[i]] (rows of 3D floats, i < nev)
-// and the resident histories logs[evl_ids[r*K + k]] = glog[clamp(ev_dyn[r], 0, nd-1), k] (elr_glog_take).
-int evict_move(float* mat, int64_t mat_rows, const int64_t* evf_slots, const float* pool, int64_t pool_rows,
-               const int64_t* ev_slot, float* logs, int64_t log_rows, const int64_t* evl_ids, const float* glog,
-               int64_t nd, int64_t K, const int64_t* ev_dyn, int64_t nev, int64_t D, void* stream) {
-  if (nev < 0 || D <= 0 || nd < 1 || K < 1 || mat_rows < 0 || pool_rows < 0 || log_rows < 0) return ELR_EINVAL;
-  if (nev == 0) return ELR_OK;
-  if (!mat || !evf_slots || !pool || !ev_slot || !logs || !evl_ids || !glog || !ev_dyn) return ELR_EINVAL;
-  hipStream_t st = (hipStream_t)stream;
-  evict_move_visit(evict_move_prep(mat, mat_rows, evf_slots, pool, pool_rows, ev_slot, logs, log_rows, evl_ids, glog,
-                                   nd, K, ev_dyn, nev, D),
-                   [&](const auto& f, int64_t blocks) { launch1(f, blocks, st); });
-  return launch_status();
-}
-
 }  // namespace elr
 
 extern "C" int elr_copy_rows(float* dst, int64_t dst_rows, const int64_t* dst_idx, const float* src, int64_t src_rows,
