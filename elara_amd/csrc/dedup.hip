@@ -607,7 +607,11 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
   int32_t my[SW];
   // short: every segment of the wave fits one run of at most FB occurrences (wave-uniform: the lengths are scalar
   // loads).  Their remaining rows then load together, all segments' at once, before any addition.
+#ifdef ELR_SEG_FB
+  constexpr int FB = ELR_SEG_FB;
+#else
   constexpr int FB = VPL <= 2 ? kAtenGroup : 4;
+#endif
   bool short_segs = true;
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
