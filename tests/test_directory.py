@@ -119,6 +119,65 @@ def test_gpu_directory_evictions_beyond_fused_scan(dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('nev', [256 * 256, 256 * 256 + 1])
+def test_gpu_directory_evictions_at_the_fused_scan_limit(dev, nev):
+    """Exactly 256 blocks of evictions (the apply kernel sums the block counts itself) and one item more (the
+    counts are scanned in a launch of their own): call A's outputs and the whole directory equal the oracle's.  The
+    evicted slots hold N, L and F rows with host-log entries, MAT slots and resident histories of every length, so
+    that every allocator (log ids from the free stack and the bump pointer, MAT slots, releases) takes part."""
+    import torch
+    from elara_amd.elara_dir import dir_ext
+    print(f'[gpu-test] directory evictions nev={nev}', flush=True)
+    R, K, n0, Cdyn = 400_000, 3, 10, 70_000
+    st = O.DirState(R, n0 + Cdyn, K, n0, np.array([0, R // 2], np.int64), np.array([2, 3], np.int8))
+    pv = st.params(True)
+    rng = np.random.default_rng(21 + nev)
+    rows = rng.permutation(R)[:Cdyn].astype(np.int64)
+    kind = rng.random(Cdyn)
+    c0 = np.where(kind < 0.4, rng.integers(1, K + 1, Cdyn), np.where(kind < 0.7, 0, -1)).astype(np.int64)
+    for k in range(K):                                  # the L rows' host-log entries (appends, oracle only)
+        sel = rows[c0 > k]
+        O.dir_b(st, pv, sel, np.full(sel.size, k, np.int64), [], [], 1 + k)
+    f_rows = rows[c0 < 0]                               # F rows: materialised, half of them with a MAT slot
+    st.code[f_rows] = st.MAT
+    held = f_rows[::2]
+    st.loc[held] = np.arange(held.size, dtype=np.int32)
+    st.mat_top[0] = held.size
+    some = rows[(c0 == 0) & (kind < 0.5)]               # and some N rows holding a MAT slot from earlier
+    st.loc[some] = np.arange(held.size, held.size + some.size, dtype=np.int32)
+    st.mat_top[0] += some.size
+    free = rng.permutation(int(st.log_top[0]))[:5_000].astype(np.int32)   # a free stack to pop from
+    st.ent[np.isin(st.ent, free)] = -1
+    st.lfree[:free.size] = free
+    st.n_lfree[0] = free.size
+    st.live[0] = int((st.ent >= 0).sum())
+    slots = np.arange(n0, n0 + Cdyn, dtype=np.int64)    # admissions, as the planner makes them
+    st.slot_of[rows] = slots.astype(np.int32)
+    st.slot_row[slots] = rows
+    st.adm_c0[slots] = c0.astype(np.int8)
+    j = rng.integers(0, K + 1, Cdyn)
+    st.rj[slots] = j.astype(np.int8)
+    st.rok[slots] = (rng.random(Cdyn) < 0.8).astype(np.int8)
+    st.pstep[:Cdyn * K] = rng.integers(1, 50, Cdyn * K).astype(np.int32)
+    ev_slot = rng.permutation(slots)[:nev]
+    gst = [torch.from_numpy(getattr(st, f).copy()).to(dev) for f in O.DIR_FIELDS]
+    e = np.empty(0, np.int64)
+    want = O.dir_a(st, pv, e, e, np.empty(0, np.int32), ev_slot, 60)
+    T = lambda a, dt=torch.int64: torch.from_numpy(np.ascontiguousarray(a)).to(dev, dt)  # noqa: E731
+    got = dir_ext().elara_dir_a(gst, list(pv), T(e), T(e), T(e, torch.int32), T(ev_slot), 60)
+    torch.cuda.synchronize()
+    for k, (w, g) in enumerate(zip(want, got)):
+        assert np.array_equal(np.asarray(w).reshape(-1), g.cpu().numpy().reshape(-1)), k
+    for i, f in enumerate(O.DIR_FIELDS):
+        a, b = getattr(st, f).reshape(-1), gst[i].cpu().numpy().reshape(-1)
+        if f in ('lstep', 'lfree'):
+            a, b = a[:-1], b[:-1]
+        assert np.array_equal(a, b), f
+    rep = np.asarray(want[5]).astype(bool)
+    assert 0 < rep.sum() < nev and int(st.n_lfree[0]) > 0
+
+
+@pytest.mark.gpu
 def test_gpu_dir_b_scan_beyond_one_scan_block(dev):
     """300,000 compactions in one call (more than 1024 blocks: the single-block scan loops over chunks with a
     carry), then 200,000 appends that pop the whole free stack and continue with the bump pointer."""
