@@ -218,6 +218,46 @@ def test_gpu_dir_b_scan_beyond_one_scan_block(dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('nc', [256 * 256, 256 * 256 + 1])
+def test_gpu_dir_b_at_the_fused_scan_limit(dev, nc):
+    """Call B with exactly 256 blocks of compactions (the compaction kernel sums the block counts itself) and one
+    item more (a scan launch of its own), together with appends that pop the free stack: outputs and directory
+    equal the oracle's."""
+    import torch
+    from elara_amd.elara_dir import dir_ext
+    print(f'[gpu-test] dir_b nc={nc}', flush=True)
+    rng = np.random.default_rng(30 + nc)
+    R, K, C = 400_000, 3, 8
+    st = O.DirState(R, C, K, 0, np.array([0], np.int64), np.array([3], np.int8))
+    pv = st.params(True)
+    perm = rng.permutation(R).astype(np.int64)
+    logged, fresh = perm[:150_000], perm[150_000:160_000]
+    cnt = rng.integers(1, 4, logged.size)
+    for k in range(3):
+        sel = logged[cnt > k]
+        O.dir_b(st, pv, sel, np.full(sel.size, k, np.int64), [], [], 1 + k)
+    crow = logged[:nc]
+    ccnt = cnt[:nc].astype(np.int64)
+    pre = crow[::3]                                     # a third already hold a MAT slot
+    st.loc[pre] = np.arange(pre.size, dtype=np.int32)
+    st.mat_top[0] = pre.size
+    done = logged[nc:nc + 2_000]                        # their entries released earlier: a free stack to pop
+    O.dir_b(st, pv, [], [], done, cnt[nc:nc + 2_000].astype(np.int64), 5)
+    gst = [torch.from_numpy(getattr(st, f).copy()).to(dev) for f in O.DIR_FIELDS]
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int64)).to(dev)  # noqa: E731
+    want = O.dir_b(st, pv, fresh, np.zeros(fresh.size, np.int64), crow, ccnt, 9)
+    got = dir_ext().elara_dir_b(gst, list(pv), T(fresh), T(np.zeros(fresh.size)), T(crow), T(ccnt), 9)
+    torch.cuda.synchronize()
+    for w, g in zip(want, got):
+        assert np.array_equal(w, g.cpu().numpy())
+    for i, f in enumerate(O.DIR_FIELDS):
+        a, b = getattr(st, f).reshape(-1), gst[i].cpu().numpy().reshape(-1)
+        if f in ('lstep', 'lfree'):
+            a, b = a[:-1], b[:-1]
+        assert np.array_equal(a, b), f
+
+
+@pytest.mark.gpu
 def test_gpu_directory_empty_calls(dev):
     import torch
     from elara_amd.elara_dir import dir_ext
