@@ -171,6 +171,29 @@ def test_gpu_native_update_matches_python_update(dev, name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('name', ['one_batch_repeated', 'two_batches_alternating'])
+def test_gpu_step_degenerate_batches(dev, name):
+    """Batches that repeat: one batch over and over (from its second step most rows are hits, and steps come with
+    few or no admissions, appends or compactions, so the native executor issues paired launches with an empty
+    side), and two batches alternating (rows leave and come back every other step).  Equal to the oracle-driven
+    step."""
+    from elara_amd.step import run
+    print(f'[gpu-test] elara step {name}', flush=True)
+    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=12, C=9000, n_static=1500)
+    b = cfg['batches']
+    cfg['batches'] = [b[0]] * 12 if name == 'one_batch_repeated' else [b[0], b[1]] * 6
+    g = make(cfg, dev)
+    c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
+    gf = grads_fn(cfg, None)
+    run(g, cfg['batches'], gf)
+    run(c, cfg['batches'], gf)
+    torch.cuda.synchronize()
+    assert compare(g, c, cfg) > 0
+    assert g.stats == c.stats
+    assert g.stats['hits'] > g.stats['adm'] > 0, g.stats
+
+
+@pytest.mark.gpu
 def test_gpu_step_c5_full_shape(dev):
     """Config C5 shapes: 26 tables (vocab log-uniform in [1e3, 4e7], ~75M rows), batch 16,384 x 26 Zipf(1.1),
     D = 128, pool 337,626 (321,242 static hot rows), K = 3, evl on; 200 steps (the pool's steady-state churn and
