@@ -20,7 +20,7 @@ struct DirHdr {
 
 // Grids of at most this many blocks skip the single-block scan launch: each block of the apply kernel sums the
 // per-block counts of the blocks before it itself (one count per thread), and its block 0 advances the counters.
-// Larger grids scan the counts in a launch of their own (k_dir_scan), whose reads then grow with the grid only once.
+// Larger grids scan the counts in a launch of their own (k_dir_scan) rather than have every block read them all.
 constexpr int64_t kFusedScanBlocks = kDirBlock;
 
 template <int NCH>
@@ -41,8 +41,8 @@ __device__ __forceinline__ int64_t nf_after_alloc(int64_t nf0, int64_t nalloc) {
   return nf0 - (nalloc < nf0 ? nalloc : nf0);
 }
 
-// Counter update of one call from the old values in h (elara_dir.cpp:18-19 alloc, 31 release, 42 MAT, in the
-// reference's order: log allocation, MAT allocation, release); returns n_lfree after the allocation.
+// Counter update of one call from the counters' old values nf0, top0, mt0 (elara_dir.cpp:18-19 alloc, 31 release,
+// 42 MAT, in the reference's order: log allocation, MAT allocation, release); returns n_lfree after the allocation.
 __device__ __forceinline__ int64_t dir_advance(const elr_dir_state& st, int64_t nf0, int64_t top0, int64_t mt0,
                                                int64_t nalloc, int64_t nmat, int64_t nrel) {
   const int64_t nf1 = nf_after_alloc(nf0, nalloc);
