@@ -54,6 +54,12 @@ SIGNATURES = {
     'elr_dir_a': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64] + [c_vp] * 9
                   + [c_vp, c_i64, c_vp]),
     'elr_dir_evict': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp]),
+    'elr_dir_evict_deferred': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp,
+                                              c_i64, c_vp]),
+    'elr_dir_a_deferred': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64] + [c_vp] * 10
+                           + [c_vp, c_i64, c_vp]),
+    'elr_dir_b_release': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, ctypes.c_int, c_vp, c_vp,
+                                         c_i64, c_i64, c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_dir_b': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_vp, c_vp, c_vp, c_i64,
                                  c_vp]),
     'elr_plan_scratch_bytes': (c_i64, [c_i64, c_i64]),
@@ -142,7 +148,7 @@ class ExecArgs(ctypes.Structure):
     _fields_ = [('dir', DirState), ('pv', DirParams), ('s', c_i64), ('b', c_i64 * 11), ('u_ord', c_vp), ('c_ord', c_vp),
                 ('sl_ord', c_vp), ('loc_ord', c_vp), ('L_row', c_vp), ('L_cnt', c_vp), ('slots', SlotsArgs),
                 ('seed', c_u32), ('bound', c_f32), ('table', c_vp), ('recip', c_vp), ('table_rows', c_i64),
-                ('upd', UpdateArgs)]
+                ('upd', UpdateArgs), ('dir_order', c_i64)]
 
 
 EXEC_OUT_FIELDS = ('L_steps', 'L_ids', 'hrec_dyn', 'hrec_j', 'ev_row', 'rep', 'evl_ids', 'evf_slots', 'ev_dyn',

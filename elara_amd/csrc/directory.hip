@@ -99,7 +99,7 @@ inline bool params_ok(const elr_dir_state* st, const elr_dir_params* p) {
 
 DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
                             const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
-                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, void* scratch) {
+                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch) {
   char* base = (char*)scratch;
   DirHdr* hdr = (DirHdr*)base;
   const int64_t nblk = dir_nblocks(nev);
@@ -108,10 +108,12 @@ DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, con
   const int64_t* rows = ev_row_in ? ev_row_in : ev_row_out;
   DirEvictPlan e;
   e.nblk = nblk;
+  e.rel_nblk = rel_cnt ? 0 : nblk;
   e.fused = nblk <= kFusedScanBlocks;
-  e.count = DirEvictCount{S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep, ev_dyn, bsum, nblk, hdr};
+  e.count = DirEvictCount{S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep, ev_dyn, bsum, nblk, hdr,
+                          rel_cnt != nullptr};
   e.apply = DirEvictApply{S, P, ev_slot, nev, rows, rep, ev_dyn, evl_ids, evf_slots, bsum, nblk, hdr, rel_rank,
-                          e.fused};
+                          e.fused, rel_cnt};
   e.release = DirEvictRelease{S, P, ev_slot, nev, rows, rep, rel_rank, hdr};
   return e;
 }
@@ -121,19 +123,18 @@ void dir_evict_scan(const DirEvictPlan& e, hipStream_t strm) {
 }
 
 DirBPlan dir_b_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* a_rows, const int64_t* a_k,
-                    int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids,
-                    int64_t* c_slots, void* scratch) {
+                    int64_t na, const DirBItems& it, int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch) {
   char* base = (char*)scratch;
   DirHdr* hdr = (DirHdr*)base;
-  const int64_t nblk_c = dir_nblocks(nc), nblk_a = dir_nblocks(na);
+  const int64_t nblk_c = dir_nblocks(it.nr + it.nc), nblk_a = dir_nblocks(na);
   int64_t* bsum = (int64_t*)(base + dir_align(sizeof(DirHdr)));
   DirBPlan e;
   e.na = na;
   e.nblk_c = nblk_c;
   e.fused = nblk_c <= kFusedScanBlocks;
-  e.count = DirBCount{S, P, a_rows, a_k, na, c_rows, c_cnt, nc, (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr};
+  e.count = DirBCount{S, P, a_rows, a_k, na, it, (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr};
   e.count_blocks = nblk_a + nblk_c;
-  e.compact = DirBCompact{S, P, c_rows, c_cnt, nc, c_slots, bsum, nblk_c, hdr, e.fused, na};
+  e.compact = DirBCompact{S, P, it, c_slots, bsum, nblk_c, hdr, e.fused, na};
   // fused: at least one block, which advances the counters also when there are only appends
   e.compact_blocks = e.fused ? (nblk_c ? nblk_c : 1) : nblk_c;
   return e;
@@ -166,12 +167,14 @@ void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, con
 }
 
 int dir_b_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,
-                int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t* a_ids, int64_t* c_slots,
-                void* scratch, int64_t scratch_bytes) {
-  if (!params_ok(st, p) || na < 0 || nc < 0) return ELR_EINVAL;
-  if ((na && (!a_rows || !a_k || !a_ids)) || (nc && (!c_rows || !c_cnt || !c_slots))) return ELR_EINVAL;
-  if (na == 0 && nc == 0) return ELR_OK;
-  if (!scratch || scratch_bytes < dir_b_scratch(nc)) return ELR_ECAPACITY;
+                int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, const int64_t* r_rows,
+                const int64_t* r_cnt, int64_t nr, int64_t* a_ids, int64_t* c_slots, void* scratch,
+                int64_t scratch_bytes) {
+  if (!params_ok(st, p) || na < 0 || nc < 0 || nr < 0) return ELR_EINVAL;
+  if ((na && (!a_rows || !a_k || !a_ids)) || (nc && (!c_rows || !c_cnt || !c_slots)) || (nr && (!r_rows || !r_cnt)))
+    return ELR_EINVAL;
+  if (na == 0 && nc == 0 && nr == 0) return ELR_OK;
+  if (!scratch || scratch_bytes < dir_b_scratch(nr + nc)) return ELR_ECAPACITY;
   return ELR_OK;
 }
 
@@ -179,13 +182,45 @@ int dir_b_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t*
 // not written and may be NULL).
 static void launch_evict(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
                          const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
-                         int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, void* scratch, hipStream_t strm) {
+                         int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch,
+                         hipStream_t strm) {
   const DirEvictPlan e = dir_evict_plan(S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep, evl_ids, evf_slots,
-                                        ev_dyn, scratch);
+                                        ev_dyn, rel_cnt, scratch);
   launch1(e.count, e.nblk, strm);
   dir_evict_scan(e, strm);
   launch1(e.apply, e.nblk, strm);
-  launch1(e.release, e.nblk, strm);
+  launch1(e.release, e.rel_nblk, strm);
+}
+
+static int dir_a_impl(const elr_dir_state* st, const elr_dir_params* p, const int64_t* hs, int64_t nh,
+                      const int64_t* L_row, const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot, int64_t nev,
+                      int64_t s, int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j,
+                      int64_t* ev_row, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn,
+                      int64_t* rel_cnt, void* scratch, int64_t scratch_bytes, void* stream) {
+  int rc = dir_a_check(st, p, hs, nh, L_row, L_cnt, nL, ev_slot, nev, L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep,
+                       evl_ids, evf_slots, ev_dyn, scratch, scratch_bytes);
+  if (rc) return rc;
+  hipStream_t strm = (hipStream_t)stream;
+  const elr_dir_state S = *st;
+  const elr_dir_params P = *p;
+  dir_lsteps_hits_launch(S, P, hs, nh, L_row, L_cnt, nL, s, L_steps, L_ids, hrec_dyn, hrec_j, strm);
+  if (nev)
+    launch_evict(S, P, ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids, evf_slots, ev_dyn, rel_cnt, scratch,
+                 strm);
+  return launch_status();
+}
+
+static int dir_evict_impl(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot,
+                          const int64_t* ev_row, const int8_t* thr, int64_t nev, uint8_t* rep, int64_t* evl_ids,
+                          int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch,
+                          int64_t scratch_bytes, void* stream) {
+  if (!params_ok(st, p) || nev < 0) return ELR_EINVAL;
+  if (nev == 0) return ELR_OK;
+  if (!ev_slot || !ev_row || !thr || !rep || !evl_ids || !evf_slots || !ev_dyn) return ELR_EINVAL;
+  if (!scratch || scratch_bytes < dir_a_scratch(nev)) return ELR_ECAPACITY;
+  launch_evict(*st, *p, ev_slot, nev, ev_row, thr, nullptr, rep, evl_ids, evf_slots, ev_dyn, rel_cnt, scratch,
+               (hipStream_t)stream);
+  return launch_status();
 }
 
 }  // namespace elr
@@ -201,42 +236,59 @@ extern "C" int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const
                          int64_t s, int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j,
                          int64_t* ev_row, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn,
                          void* scratch, int64_t scratch_bytes, void* stream) {
-  using namespace elr;
-  int rc = dir_a_check(st, p, hs, nh, L_row, L_cnt, nL, ev_slot, nev, L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep,
-                       evl_ids, evf_slots, ev_dyn, scratch, scratch_bytes);
-  if (rc) return rc;
-  hipStream_t strm = (hipStream_t)stream;
-  const elr_dir_state S = *st;
-  const elr_dir_params P = *p;
-  dir_lsteps_hits_launch(S, P, hs, nh, L_row, L_cnt, nL, s, L_steps, L_ids, hrec_dyn, hrec_j, strm);
-  if (nev) launch_evict(S, P, ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids, evf_slots, ev_dyn, scratch, strm);
-  return launch_status();
+  return elr::dir_a_impl(st, p, hs, nh, L_row, L_cnt, nL, ev_slot, nev, s, L_steps, L_ids, hrec_dyn, hrec_j, ev_row,
+                         rep, evl_ids, evf_slots, ev_dyn, nullptr, scratch, scratch_bytes, stream);
+}
+
+extern "C" int elr_dir_a_deferred(const elr_dir_state* st, const elr_dir_params* p, const int64_t* hs, int64_t nh,
+                                  const int64_t* L_row, const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot,
+                                  int64_t nev, int64_t s, int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn,
+                                  int64_t* hrec_j, int64_t* ev_row, uint8_t* rep, int64_t* evl_ids,
+                                  int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch,
+                                  int64_t scratch_bytes, void* stream) {
+  if (nev && !rel_cnt) return ELR_EINVAL;
+  return elr::dir_a_impl(st, p, hs, nh, L_row, L_cnt, nL, ev_slot, nev, s, L_steps, L_ids, hrec_dyn, hrec_j, ev_row,
+                         rep, evl_ids, evf_slots, ev_dyn, rel_cnt, scratch, scratch_bytes, stream);
 }
 
 extern "C" int elr_dir_evict(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot,
                              const int64_t* ev_row, const int8_t* thr, int64_t nev, uint8_t* rep, int64_t* evl_ids,
                              int64_t* evf_slots, int64_t* ev_dyn, void* scratch, int64_t scratch_bytes,
                              void* stream) {
+  return elr::dir_evict_impl(st, p, ev_slot, ev_row, thr, nev, rep, evl_ids, evf_slots, ev_dyn, nullptr, scratch,
+                             scratch_bytes, stream);
+}
+
+extern "C" int elr_dir_evict_deferred(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot,
+                                      const int64_t* ev_row, const int8_t* thr, int64_t nev, uint8_t* rep,
+                                      int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt,
+                                      void* scratch, int64_t scratch_bytes, void* stream) {
+  if (nev > 0 && !rel_cnt) return ELR_EINVAL;
+  return elr::dir_evict_impl(st, p, ev_slot, ev_row, thr, nev, rep, evl_ids, evf_slots, ev_dyn, rel_cnt, scratch,
+                             scratch_bytes, stream);
+}
+
+extern "C" int elr_dir_b_release(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows,
+                                 const int64_t* a_k, int64_t na, const int64_t* c_rows, const int64_t* c_cnt,
+                                 int64_t nc, int c_release, const int64_t* r_rows, const int64_t* r_cnt, int64_t nr,
+                                 int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch, int64_t scratch_bytes,
+                                 void* stream) {
   using namespace elr;
-  if (!params_ok(st, p) || nev < 0) return ELR_EINVAL;
-  if (nev == 0) return ELR_OK;
-  if (!ev_slot || !ev_row || !thr || !rep || !evl_ids || !evf_slots || !ev_dyn) return ELR_EINVAL;
-  if (!scratch || scratch_bytes < dir_a_scratch(nev)) return ELR_ECAPACITY;
-  launch_evict(*st, *p, ev_slot, nev, ev_row, thr, nullptr, rep, evl_ids, evf_slots, ev_dyn, scratch,
-               (hipStream_t)stream);
+  const int rc = dir_b_check(st, p, a_rows, a_k, na, c_rows, c_cnt, nc, r_rows, r_cnt, nr, a_ids, c_slots, scratch,
+                             scratch_bytes);
+  if (rc || (na == 0 && nc == 0 && nr == 0)) return rc;
+  hipStream_t strm = (hipStream_t)stream;
+  const DirBItems it{c_rows, c_cnt, nc, r_rows, r_cnt, nr, c_release != 0};
+  const DirBPlan e = dir_b_plan(*st, *p, a_rows, a_k, na, it, s, a_ids, c_slots, scratch);
+  launch1(e.count, e.count_blocks, strm);
+  dir_b_scan(e, strm);
+  launch1(e.compact, e.compact_blocks, strm);
   return launch_status();
 }
 
 extern "C" int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,
                          int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s,
                          int64_t* a_ids, int64_t* c_slots, void* scratch, int64_t scratch_bytes, void* stream) {
-  using namespace elr;
-  const int rc = dir_b_check(st, p, a_rows, a_k, na, c_rows, c_cnt, nc, a_ids, c_slots, scratch, scratch_bytes);
-  if (rc || (na == 0 && nc == 0)) return rc;
-  hipStream_t strm = (hipStream_t)stream;
-  const DirBPlan e = dir_b_plan(*st, *p, a_rows, a_k, na, c_rows, c_cnt, nc, s, a_ids, c_slots, scratch);
-  launch1(e.count, e.count_blocks, strm);
-  dir_b_scan(e, strm);
-  launch1(e.compact, e.compact_blocks, strm);
-  return launch_status();
+  return elr_dir_b_release(st, p, a_rows, a_k, na, c_rows, c_cnt, nc, 1, nullptr, nullptr, 0, s, a_ids, c_slots,
+                           scratch, scratch_bytes, stream);
 }

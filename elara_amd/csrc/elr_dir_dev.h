@@ -124,7 +124,8 @@ __device__ __forceinline__ EvCounts ev_counts(const elr_dir_state& st, const elr
 
 // A2: eviction representation and per-block allocation counts (elara_dir.cpp:73-78).  With ev_row_in (the
 // Directory.evict form, srm2/elara_kernels.py:152-171) the caller supplies the evicted rows and their thresholds
-// and has already cleared slot_of / slot_row; otherwise the rows come from slot_row and are unmapped here.
+// and has already cleared slot_of / slot_row; otherwise the rows come from slot_row and are unmapped here.  defer:
+// the releases of rows going to M are left to call B (the Triton path's order), so this call counts none.
 struct DirEvictCount {
   elr_dir_state st;
   elr_dir_params p;
@@ -138,6 +139,7 @@ struct DirEvictCount {
   int64_t* bsum;
   int64_t nblk;
   DirHdr* hdr;
+  bool defer;
   __device__ void operator()(int64_t blk, int64_t) const {
     dir_snapshot(blk, st, hdr);
     const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
@@ -166,7 +168,7 @@ struct DirEvictCount {
       const EvCounts c = ev_counts(st, p, row, rp, c0, j);
       v[0] = c.nalloc;
       v[1] = c.nmat;
-      v[2] = c.nrel;
+      v[2] = defer ? 0 : c.nrel;
     }
     int ex[3], tot[3];
     dir_block_scan<3>(v, ex, tot);
@@ -178,7 +180,9 @@ struct DirEvictCount {
 // A4: apply the eviction representation (elara_dir.cpp:79-93 except the stack pushes): log ids of rows going back
 // to L (ent, lstep), MAT slots (loc, evf_slots), codes; records each item's release rank for A5.  fused: bsum holds
 // the raw per-block counts (grid of at most kFusedScanBlocks blocks) and block 0 advances the counters; otherwise
-// k_dir_scan has turned bsum into block offsets and advanced them.
+// k_dir_scan has turned bsum into block offsets and advanced them.  With rel_cnt (deferred releases, no A5) each
+// item's release count goes there instead: max(c0, 0) for a row going to M, 0 for one going back to L
+// (srm2/elara_kernels.py:71-72, the release part of Directory.evict).
 struct DirEvictApply {
   elr_dir_state st;
   elr_dir_params p;
@@ -194,6 +198,7 @@ struct DirEvictApply {
   DirHdr* hdr;
   int64_t* rel_rank;
   bool fused;
+  int64_t* rel_cnt;
   __device__ void operator()(int64_t blk, int64_t) const {
     const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
     const int64_t K = p.K;
@@ -218,6 +223,7 @@ struct DirEvictApply {
         j = st.rj[sl];
       }
       c = ev_counts(st, p, row, rp, c0, j);
+      if (rel_cnt) c.nrel = 0;
     }
     int v[3] = {c.nalloc, c.nmat, c.nrel}, ex[3], tot[3];
     dir_block_scan<3>(v, ex, tot);
@@ -246,7 +252,8 @@ struct DirEvictApply {
       st.code[row] = rp ? (int8_t)(tj < 127 ? tj : 127) : (int8_t)p.MAT;
     }
     evf_slots[i] = rp ? p.trash : slot;
-    rel_rank[i] = off[2] + ex[2];
+    if (rel_cnt) rel_cnt[i] = rp ? 0 : (c0 > 0 ? c0 : 0);
+    else rel_rank[i] = off[2] + ex[2];
   }
 };
 
@@ -286,17 +293,56 @@ struct DirEvictRelease {
   }
 };
 
-// B1: appends (elara_dir.cpp:102-106; log id of append i has rank i) and per-block counts of the compactions
-// (MAT slots needed, entries released).  Appended and compacted rows are disjoint.
+// Logged entries of `row` among its first cnt (elara_dir.cpp:27: the ones a release pushes).
+__device__ __forceinline__ int live_entries(const elr_dir_state& st, const elr_dir_params& p, int64_t row,
+                                            int64_t cnt) {
+  int n = 0;
+  for (int64_t k = 0; k < p.K && k < cnt; ++k) n += st.ent[row * p.K + k] >= 0 ? 1 : 0;
+  return n;
+}
+
+// The items of call B after its appends: nr release items (the first r_cnt[i] entries of r_rows[i]) and then nc
+// compactions (c_rows[i] with c_cnt[i] entries, released too when c_release).  Item q's counts: MAT slot needed and
+// entries released, pushed in item order.  The reference's default order (elara_dir.cpp:107-108) is nr = 0,
+// c_release; the Triton path's (srm2/elara_kernels.py:188-209) pushes the evictions' deferred part first.
+struct DirBItems {
+  const int64_t* c_rows;
+  const int64_t* c_cnt;
+  int64_t nc;
+  const int64_t* r_rows;
+  const int64_t* r_cnt;
+  int64_t nr;
+  bool c_release;
+  __device__ __forceinline__ int64_t n() const { return nr + nc; }
+  __device__ __forceinline__ bool is_rel(int64_t q) const { return q < nr; }
+  __device__ __forceinline__ int64_t row(int64_t q) const { return q < nr ? r_rows[q] : c_rows[q - nr]; }
+  __device__ __forceinline__ int64_t cnt(int64_t q) const { return q < nr ? r_cnt[q] : c_cnt[q - nr]; }
+  __device__ __forceinline__ bool releases(int64_t q) const { return q < nr || c_release; }
+};
+
+// Counts of item q (MAT slot needed, entries released); cur = the row's MAT slot (-1: none or a release item).
+__device__ __forceinline__ void b_item_counts(const elr_dir_state& st, const elr_dir_params& p, const DirBItems& it,
+                                              int64_t q, int64_t& row, int64_t& cnt, int64_t& cur, int (&v)[2]) {
+  row = it.row(q);
+  cnt = it.cnt(q);
+  cur = -1;
+  if (!in_range(row, p.R)) return;
+  if (!it.is_rel(q)) {
+    cur = st.loc[row];
+    v[0] = cur < 0 ? 1 : 0;
+  }
+  if (it.releases(q)) v[1] = live_entries(st, p, row, cnt);
+}
+
+// B1: appends (elara_dir.cpp:102-106; log id of append i has rank i) and per-block counts of the other items.
+// Appended rows are disjoint from the compacted and the released ones.
 struct DirBCount {
   elr_dir_state st;
   elr_dir_params p;
   const int64_t* a_rows;
   const int64_t* a_k;
   int64_t na;
-  const int64_t* c_rows;
-  const int64_t* c_cnt;
-  int64_t nc;
+  DirBItems it;
   int32_t s;
   int64_t* a_ids;
   int64_t* bsum;
@@ -320,15 +366,11 @@ struct DirBCount {
       return;
     }
     const int64_t b = (int64_t)blk - nblk_a;
-    const int64_t i = b * kDirBlock + threadIdx.x;
+    const int64_t q = b * kDirBlock + threadIdx.x;
     int v[2] = {0, 0};
-    if (i < nc) {
-      const int64_t row = c_rows[i];
-      if (in_range(row, p.R)) {
-        v[0] = st.loc[row] < 0 ? 1 : 0;
-        const int64_t cnt = c_cnt[i];
-        for (int64_t k = 0; k < K && k < cnt; ++k) v[1] += st.ent[row * K + k] >= 0 ? 1 : 0;
-      }
+    if (q < it.n()) {
+      int64_t row, cnt, cur;
+      b_item_counts(st, p, it, q, row, cnt, cur, v);
     }
     int ex[2], tot[2];
     dir_block_scan<2>(v, ex, tot);
@@ -339,15 +381,14 @@ struct DirBCount {
   }
 };
 
-// B3: compactions (elara_dir.cpp:107-108): MAT slot, release of all logs, code = MAT.  fused: bsum holds the raw
-// per-block counts (grid of at most kFusedScanBlocks blocks, at least one) and block 0 advances the counters for
-// the `na` appends and the compactions; otherwise k_dir_scan has turned bsum into block offsets and advanced them.
+// B3: compactions (elara_dir.cpp:107-108): MAT slot, release of their logs (c_release), code = MAT; release items:
+// the push alone.  fused: bsum holds the raw per-block counts (grid of at most kFusedScanBlocks blocks, at least
+// one) and block 0 advances the counters for the `na` appends and the items; otherwise k_dir_scan has turned bsum
+// into block offsets and advanced them.
 struct DirBCompact {
   elr_dir_state st;
   elr_dir_params p;
-  const int64_t* c_rows;
-  const int64_t* c_cnt;
-  int64_t nc;
+  DirBItems it;
   int64_t* c_slots;
   const int64_t* boff;
   int64_t nblk;
@@ -355,8 +396,7 @@ struct DirBCompact {
   bool fused;
   int64_t na;
   __device__ void operator()(int64_t blk, int64_t) const {
-    const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
-    const int64_t K = p.K;
+    const int64_t q = (int64_t)blk * kDirBlock + threadIdx.x;
     const int64_t mt0 = hdr->mt0;
     int64_t off[2], gtot[2], nf1;
     if (fused) {
@@ -371,26 +411,20 @@ struct DirBCompact {
     }
     int64_t row = -1, cnt = 0, cur = -1;
     int v[2] = {0, 0};
-    if (i < nc) {
-      row = c_rows[i];
-      cnt = c_cnt[i];
-      if (in_range(row, p.R)) {
-        cur = st.loc[row];
-        v[0] = cur < 0 ? 1 : 0;
-        for (int64_t k = 0; k < K && k < cnt; ++k) v[1] += st.ent[row * K + k] >= 0 ? 1 : 0;
-      }
-    }
+    if (q < it.n()) b_item_counts(st, p, it, q, row, cnt, cur, v);
     int ex[2], tot[2];
     dir_block_scan<2>(v, ex, tot);
-    if (i >= nc) return;
+    if (q >= it.n()) return;
+    const bool rel = it.is_rel(q);
     if (!in_range(row, p.R)) {
-      c_slots[i] = -1;
+      if (!rel) c_slots[q - it.nr] = -1;
       return;
     }
+    if (it.releases(q)) release_row(st, p, row, cnt, nf1 + off[1] + ex[1]);
+    if (rel) return;
     const int64_t slot = v[0] ? mt0 + off[0] + ex[0] : cur;
     if (v[0]) st.loc[row] = (int32_t)slot;
-    c_slots[i] = slot;
-    release_row(st, p, row, cnt, nf1 + off[1] + ex[1]);
+    c_slots[q - it.nr] = slot;
     st.code[row] = (int8_t)p.MAT;
   }
 };
@@ -401,7 +435,9 @@ inline int64_t dir_align(int64_t b) { return (b + 255) & ~int64_t(255); }
 inline int64_t dir_a_scratch(int64_t nev) {
   return dir_align(sizeof(DirHdr)) + dir_align(3 * dir_nblocks(nev) * 8) + nev * 8;
 }
-inline int64_t dir_b_scratch(int64_t nc) { return dir_align(sizeof(DirHdr)) + dir_align(2 * dir_nblocks(nc) * 8); }
+inline int64_t dir_b_scratch(int64_t nitems) {
+  return dir_align(sizeof(DirHdr)) + dir_align(2 * dir_nblocks(nitems) * 8);
+}
 
 // Host side (directory.hip).  The checks of elr_dir_a / elr_dir_b's arguments; the replay inputs and hit records
 // (call A's first launch); the eviction part of call A and call B as functors with their grids, in launch order:
@@ -411,8 +447,9 @@ int dir_a_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t*
                 int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, int64_t* ev_row, uint8_t* rep, int64_t* evl_ids,
                 int64_t* evf_slots, int64_t* ev_dyn, void* scratch, int64_t scratch_bytes);
 int dir_b_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,
-                int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t* a_ids, int64_t* c_slots,
-                void* scratch, int64_t scratch_bytes);
+                int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, const int64_t* r_rows,
+                const int64_t* r_cnt, int64_t nr, int64_t* a_ids, int64_t* c_slots, void* scratch,
+                int64_t scratch_bytes);
 void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
                             const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s, int32_t* L_steps,
                             int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm);
@@ -421,12 +458,15 @@ struct DirEvictPlan {
   DirEvictCount count;
   DirEvictApply apply;
   DirEvictRelease release;
-  int64_t nblk;   // grid of each of the three
-  bool fused;     // no scan launch
+  int64_t nblk;       // grid of each of the three
+  int64_t rel_nblk;   // grid of the release launch (0 when the releases are deferred)
+  bool fused;         // no scan launch
 };
+// rel_cnt: NULL for the reference's default order (the release launch pushes the host logs of rows going to M);
+// otherwise those releases are deferred to call B and their counts written there (the release launch is empty).
 DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
                             const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
-                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, void* scratch);
+                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch);
 void dir_evict_scan(const DirEvictPlan& e, hipStream_t strm);
 
 struct DirBPlan {
@@ -435,9 +475,9 @@ struct DirBPlan {
   int64_t count_blocks, compact_blocks, nblk_c, na;
   bool fused;
 };
+// Call B over its items (DirBItems: release items, then compactions).
 DirBPlan dir_b_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* a_rows, const int64_t* a_k,
-                    int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids,
-                    int64_t* c_slots, void* scratch);
+                    int64_t na, const DirBItems& it, int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch);
 void dir_b_scan(const DirBPlan& e, hipStream_t strm);
 
 }  // namespace elr

@@ -12,7 +12,9 @@
 //   5. admissions        + call B's appends and counts
 //   6. call B's compactions
 //   7. the admitted, compacted, transient and appended rows; 8. the S rows
-// (and the directory's scan launches for grids above kFusedScanBlocks).  The pairs touch disjoint data: the
+// (and the directory's scan launches for grids above kFusedScanBlocks).  In the Triton path's order (dir_order 1)
+// launch 4 holds no release: the host logs of rows going to M are pushed by call B's compaction launch, ahead of
+// the compacted rows' logs and after the appends' pops.  The pairs touch disjoint data: the
 // eviction kernels read and write only the directory, and their outputs feed later launches; the assembly reads the
 // replay inputs of launch 1, the log and MAT rows of L and F rows and the F rows' MAT slots; the hits write their
 // pool slots and history records, which the eviction moves read two launches later (a hit's slot may be evicted in
@@ -29,6 +31,7 @@ namespace {
 
 struct ExecLayout {
   elr_exec_out o;
+  int64_t rel_cnt;  // the evictions' deferred release counts (Triton order only)
   int64_t dir_a_scratch, dir_a_scratch_bytes, dir_b_scratch, dir_b_scratch_bytes, total;
 };
 
@@ -40,7 +43,7 @@ bool exec_layout(const elr_exec_args& a, ExecLayout& L) {
   for (int r = 0; r < ELR_NRANK; ++r)
     if (b[r] < 0 || b[r + 1] < b[r]) return false;
   const int64_t K = a.pv.K, D = a.upd.D;
-  if (K < 1 || D < 1 || a.slots.nev < 0) return false;
+  if (K < 1 || D < 1 || a.slots.nev < 0 || (a.dir_order != 0 && a.dir_order != 1)) return false;
   const int64_t nh = b[ELR_RANK_HIT + 1] - b[ELR_RANK_HIT];
   const int64_t nL = (b[ELR_RANK_LADM + 1] - b[ELR_RANK_LADM]) + (b[ELR_RANK_LAPP + 1] - b[ELR_RANK_LAPP]) +
                      (b[ELR_RANK_LCMP + 1] - b[ELR_RANK_LCMP]);
@@ -66,8 +69,10 @@ bool exec_layout(const elr_exec_args& a, ExecLayout& L) {
   L.o.a_ids = take(na * 8);
   L.o.c_slots = take(nc * 8);
   L.o.work = take(nw * 3 * D * 4);
+  const int64_t nr = a.dir_order ? nev : 0;
+  L.rel_cnt = take(nr * 8);
   L.dir_a_scratch_bytes = elr_dir_scratch_bytes(nev, 0);
-  L.dir_b_scratch_bytes = elr_dir_scratch_bytes(0, nc);
+  L.dir_b_scratch_bytes = elr_dir_scratch_bytes(0, nc + nr);
   if (L.dir_a_scratch_bytes < 0 || L.dir_b_scratch_bytes < 0) return false;
   L.dir_a_scratch = take(L.dir_a_scratch_bytes > 0 ? L.dir_a_scratch_bytes : 1);
   L.dir_b_scratch = take(L.dir_b_scratch_bytes > 0 ? L.dir_b_scratch_bytes : 1);
@@ -105,6 +110,9 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   const int64_t w0 = b[ELR_RANK_NADM], nw = b[ELR_RANK_S] - w0;
   const int64_t lazy_n = nNa + nLa;
   const bool evl = a.pv.evl != 0;
+  // Triton order: the host logs of rows going to M are released by call B, after its appends
+  const int64_t nr = a.dir_order ? nev : 0;
+  int64_t* rel_cnt = a.dir_order ? static_cast<int64_t*>(at(L.rel_cnt)) : nullptr;
   int32_t* L_steps = static_cast<int32_t*>(at(L.o.L_steps));
   int32_t* L_ids = static_cast<int32_t*>(at(L.o.L_ids));
   int64_t* hrec_dyn = static_cast<int64_t*>(at(L.o.hrec_dyn));
@@ -140,8 +148,8 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   const int64_t* a_k = a.c_ord + b[ELR_RANK_NAPP];
   const int64_t* c_rows = a.u_ord + b[ELR_RANK_NCMP];
   const int64_t* c_cnt = a.c_ord + b[ELR_RANK_NCMP];
-  if ((rc = dir_b_check(&a.dir, &a.pv, a_rows, a_k, na, c_rows, c_cnt, nc, a_ids, c_slots, at(L.dir_b_scratch),
-                        L.dir_b_scratch_bytes)))
+  if ((rc = dir_b_check(&a.dir, &a.pv, a_rows, a_k, na, c_rows, c_cnt, nc, ev_row, rel_cnt, nr, a_ids, c_slots,
+                        at(L.dir_b_scratch), L.dir_b_scratch_bytes)))
     return rc;
   // the work rows in class-rank order: admitted N / L / F, appended N / L, compacted N / L, transient F
   elr_assemble_args g{};
@@ -217,16 +225,18 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   DirEvictPlan ep{};
   if (nev)
     ep = dir_evict_plan(S, P, a.slots.ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids, evf_slots, ev_dyn,
-                        at(L.dir_a_scratch));
+                        rel_cnt, at(L.dir_a_scratch));
   exec_visit(up.vpl, D, hx, hblocks, up.s, [&](const auto& f, int64_t nb) { launch2(ep.count, ev_blocks, f, nb, st); });
   if (nev) dir_evict_scan(ep, st);
   if (nw > 0) assemble_visit(g, [&](const auto& f, int64_t nb) { launch2(ep.apply, ev_blocks, f, nb, st); });
   else launch1(ep.apply, ev_blocks, st);
-  if (nev) evict_move_visit(up.move, [&](const auto& f, int64_t nb) { launch2(ep.release, ev_blocks, f, nb, st); });
+  if (nev)
+    evict_move_visit(up.move, [&](const auto& f, int64_t nb) { launch2(ep.release, ep.rel_nblk, f, nb, st); });
   // 5-6.
   const int64_t adm_blocks = admit_slots_blocks(sl, n_adm);
-  if (na || nc) {
-    const DirBPlan bp = dir_b_plan(S, P, a_rows, a_k, na, c_rows, c_cnt, nc, s, a_ids, c_slots, at(L.dir_b_scratch));
+  if (na || nc || nr) {
+    const DirBItems it{c_rows, c_cnt, nc, ev_row, rel_cnt, nr, true};
+    const DirBPlan bp = dir_b_plan(S, P, a_rows, a_k, na, it, s, a_ids, c_slots, at(L.dir_b_scratch));
     launch2(admit, adm_blocks, bp.count, bp.count_blocks, st);
     dir_b_scan(bp, st);
     launch1(bp.compact, bp.compact_blocks, st);

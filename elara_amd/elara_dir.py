@@ -9,6 +9,11 @@ st is the list of the 17 directory tensors in the reference's order (elara_dir.c
 srm2/elara.py:275-277), updated in place; pv = (R, K, Lcap, n0, Cdyn, MAT, trash, evl).  Outputs have the
 reference's dtypes and shapes.  Both calls run as HIP kernels (elara_amd/csrc/directory.hip) on torch's current
 stream, with no host synchronisation: the allocator counters stay in device memory.
+
+The planner's Triton directory path allocates its log ids in another order (srm2/elara_kernels.py: every allocation
+of a step before any release).  elara_dir_a(..., deferred=True) and elara_dir_b(..., rel=(ev_row, rel_cnt)) give that
+order: call A leaves the host logs of rows going to M in place and returns their release counts as a 10th
+output, which call B releases after its appends and ahead of the compacted rows' logs.
 """
 import ctypes
 import weakref
@@ -76,7 +81,7 @@ def _scratch(dev, nev, nc):
     return torch.empty(max(n, 1), dtype=torch.uint8, device=dev), n
 
 
-def elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
+def elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s, deferred=False):
     S, P, dev, K = _state(st, pv)
     hs, L_row, ev_slot = _idx(hs, dev), _idx(L_row, dev), _idx(ev_slot, dev)
     L_cnt = _idx(L_cnt, dev, I32)
@@ -92,6 +97,14 @@ def elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
            evl.view(nev, K), evf, evd]
     scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
     p = _lib.ptr
+    if deferred:
+        rel_cnt = torch.empty(nev, dtype=I64, device=dev)
+        with _lib.on_device(dev):
+            rc = _lib.lib().elr_dir_a_deferred(ctypes.byref(S), ctypes.byref(P), p(hs), nh, p(L_row), p(L_cnt), nL,
+                                               p(ev_slot), nev, int(s), *[p(o) for o in out], p(rel_cnt),
+                                               p(scratch), nbytes, _lib.stream_of(st[0]))
+        _lib.check(rc, 'elr_dir_a_deferred')
+        return out + [rel_cnt]
     with _lib.on_device(dev):
         rc = _lib.lib().elr_dir_a(ctypes.byref(S), ctypes.byref(P), p(hs), nh, p(L_row), p(L_cnt), nL,
                                   p(ev_slot), nev, int(s), *[p(o) for o in out], p(scratch), nbytes,
@@ -100,23 +113,32 @@ def elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
     return out
 
 
-def elara_dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s):
+def elara_dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=None, c_release=True):
+    """Call B; rel = (rows, counts): releases pushed after the appends and ahead of the compacted rows' (which are
+    released only when c_release), as elr_dir_b_release."""
     S, P, dev, K = _state(st, pv)
     a_rows, a_k, c_rows, c_cnt = (_idx(x, dev) for x in (a_rows, a_k, c_rows, c_cnt))
-    na, nc = a_rows.numel(), c_rows.numel()
-    if a_k.numel() != na or c_cnt.numel() != nc:
-        raise RuntimeError('a_k must match a_rows and c_cnt must match c_rows')
-    nbytes = int(_lib.lib().elr_dir_scratch_bytes(0, nc)) if na or nc else 0
+    r_rows, r_cnt = (None, None) if rel is None else (_idx(rel[0], dev), _idx(rel[1], dev))
+    na, nc, nr = a_rows.numel(), c_rows.numel(), 0 if rel is None else r_rows.numel()
+    if a_k.numel() != na or c_cnt.numel() != nc or (rel is not None and r_cnt.numel() != nr):
+        raise RuntimeError('a_k must match a_rows, c_cnt c_rows and the release counts their rows')
+    nbytes = int(_lib.lib().elr_dir_scratch_bytes(0, nc + nr)) if na or nc or nr else 0
     if nbytes < 0:
         _lib.check(nbytes, 'elr_dir_scratch_bytes')
     a_ids, c_slots = _lib.split_empty(dev, I64, (na, nc))
-    if na or nc:
+    if na or nc or nr:
         scratch = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
         p = _lib.ptr
         with _lib.on_device(dev):
-            rc = _lib.lib().elr_dir_b(ctypes.byref(S), ctypes.byref(P), p(a_rows), p(a_k), na, p(c_rows),
-                                      p(c_cnt), nc, int(s), p(a_ids), p(c_slots), p(scratch), nbytes,
-                                      _lib.stream_of(st[0]))
+            if rel is None and c_release:
+                rc = _lib.lib().elr_dir_b(ctypes.byref(S), ctypes.byref(P), p(a_rows), p(a_k), na, p(c_rows),
+                                          p(c_cnt), nc, int(s), p(a_ids), p(c_slots), p(scratch), nbytes,
+                                          _lib.stream_of(st[0]))
+            else:
+                rc = _lib.lib().elr_dir_b_release(ctypes.byref(S), ctypes.byref(P), p(a_rows), p(a_k), na,
+                                                  p(c_rows), p(c_cnt), nc, int(bool(c_release)),
+                                                  p(r_rows) if nr else None, p(r_cnt) if nr else None, nr, int(s),
+                                                  p(a_ids), p(c_slots), p(scratch), nbytes, _lib.stream_of(st[0]))
         _lib.check(rc, 'elr_dir_b')
     return [a_ids, c_slots]
 

@@ -12,12 +12,12 @@ lstep, lfree, n_lfree, log_top, mat_top, live, adm_c0, rj, pstep, kthr, toff, sl
 (or K), log_cap, n0, Cdyn, MAT, mat_trash, evict_logs (or evl) -- srm2/elara.py ELARAPlanner, or elara_amd.step
 .ElaraStep.  The calls run the HIP directory kernels of elr_dir_a / elr_dir_evict / elr_dir_b.
 
-Allocation order.  The reference's Triton path allocates every log id of a step before any release; its default
-(`cpp`) path releases the host logs of rows evicted to M right after the eviction allocations and the logs of
-compacted rows after the appends (srm2/elara_dir.cpp:80-94, 102-108).  This front end uses the `cpp` order: evict()
-and compact() release at once, the release part evict() returns carries zero counts, and release() only checks
-that the parts it is given were released already.  Log ids therefore follow the `cpp` path; they are storage
-addresses only, and every state and weight is the same under both orders (srm2/elara_kernels.py:5-7).
+Allocation order: the Triton path's own (srm2/elara_kernels.py:5-7).  Every log id of a step is allocated before any
+of its releases: evict() releases nothing and returns the host logs of rows going to M as its release part,
+appends() pops after the evictions' allocations, compact() assigns MAT slots only, and release(parts) pushes the
+parts' entries in the order given (elr_dir_evict_deferred, elr_dir_b_release).  The reference's default (`cpp`)
+directory releases at once instead (srm2/elara_dir.cpp:80-94, 102-108), so its log ids differ; every other state
+and every weight is the same under both orders.
 """
 import ctypes
 
@@ -84,13 +84,11 @@ class Directory:
 
     def __init__(self, pl):
         self.pl = pl
-        self._released = []
 
     def evict(self, ev_slot, ev_row, thr):
         """Eviction representation of slots already unmapped by the caller: back to L if the full history fits
         thr, else to M.  Returns (rep int64 [n], evl_ids int64 [n,K], evf_slots int64 [n] (trash for rows going
-        back to L), release part (ev_row, counts) -- counts are zero: the host logs of rows going to M are released
-        here already)."""
+        back to L), release part (ev_row, counts): the host-log entries of rows going to M, for release())."""
         pl = self.pl
         S, P, dev, K, anchor = _state(pl)
         ev_slot, ev_row = _idx(ev_slot, dev), _idx(ev_row, dev)
@@ -102,37 +100,36 @@ class Directory:
         evl_ids = torch.empty(n, K, dtype=I64, device=dev)
         evf = torch.empty(n, dtype=I64, device=dev)
         ev_dyn = torch.empty(n, dtype=I64, device=dev)
+        rel_cnt = torch.empty(n, dtype=I64, device=dev)
         if n:
             scratch, nbytes = _scratch(dev, n, 0)
             p = _lib.ptr
             with _lib.on_device(dev):
-                rc = _lib.lib().elr_dir_evict(ctypes.byref(S), ctypes.byref(P), p(ev_slot), p(ev_row), p(thr), n,
-                                              p(rep), p(evl_ids), p(evf), p(ev_dyn), p(scratch), nbytes,
-                                              _lib.stream_of(anchor))
-            _lib.check(rc, 'elr_dir_evict')
-        part = (ev_row, torch.zeros(n, dtype=I64, device=dev))
-        self._released.append(part[0])
-        return rep.to(I64), evl_ids, evf, part
+                rc = _lib.lib().elr_dir_evict_deferred(ctypes.byref(S), ctypes.byref(P), p(ev_slot), p(ev_row),
+                                                       p(thr), n, p(rep), p(evl_ids), p(evf), p(ev_dyn),
+                                                       p(rel_cnt), p(scratch), nbytes, _lib.stream_of(anchor))
+            _lib.check(rc, 'elr_dir_evict_deferred')
+        return rep.to(I64), evl_ids, evf, (ev_row, rel_cnt)
 
     def appends(self, rows, ks, s):
         """One new log entry per row at entry index ks (the row stays L): returns the log ids int64 [n]."""
         return self._dir_b(rows, ks, None, None, s)[0]
 
     def compact(self, rows, cnt):
-        """MAT slots for rows going to M (code = MAT); their cnt logged entries are released here already."""
-        slots = self._dir_b(None, None, rows, cnt, 0)[1]
-        self._released.append(rows)
-        return slots
+        """MAT slots for rows going to M (code = MAT); their cnt logged entries are released by release()."""
+        return self._dir_b(None, None, rows, cnt, 0, c_release=False)[1]
 
     def release(self, parts):
-        """Releases of the step: already done by evict() and compact() (this build's allocation order)."""
-        for rows, _ in parts:
-            if rows.numel() and not any(rows is r for r in self._released):
-                raise RuntimeError('release(): only the parts returned by evict() or passed to compact() can be '
-                                   'released (they are released there already)')
-        self._released = []
+        """parts: list of (rows, counts): push the first counts[i] logged entries of each row onto the free stack,
+        in the order of the parts and rows, after this step's allocations."""
+        parts = [(r, c) for r, c in parts if r.numel()]
+        if not parts:
+            return
+        rows = torch.cat([r.to(I64) for r, _ in parts])
+        cnt = torch.cat([c.to(I64) for _, c in parts])
+        self._dir_b(None, None, None, None, 0, rel=(rows, cnt))
 
-    def _dir_b(self, a_rows, a_k, c_rows, c_cnt, s):
+    def _dir_b(self, a_rows, a_k, c_rows, c_cnt, s, rel=None, c_release=True):
         pl = self.pl
         dev = pl.code.device
         z = torch.empty(0, dtype=I64, device=dev)
@@ -145,4 +142,5 @@ class Directory:
         if evl is None:
             evl = pl.evl
         pv = [pl.R, _K(pl), pl.log_cap, pl.n0, pl.Cdyn, pl.MAT, pl.mat_trash, int(bool(evl))]
-        return elara_dir_b([getattr(pl, n) for n in ST_NAMES], pv, a_rows, a_k, c_rows, c_cnt, s)
+        return elara_dir_b([getattr(pl, n) for n in ST_NAMES], pv, a_rows, a_k, c_rows, c_cnt, s, rel=rel,
+                           c_release=c_release)

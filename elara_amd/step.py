@@ -106,11 +106,11 @@ class HipBackend:
     def adam_dense(self, state, grad, s):
         adam_rows_dense(state, grad, *self.hp, s)
 
-    def dir_a(self, st, pv, hs, L_row, L_cnt, ev_slot, s):
-        return self.dx.elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s)
+    def dir_a(self, st, pv, hs, L_row, L_cnt, ev_slot, s, deferred=False):
+        return self.dx.elara_dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s, deferred=deferred)
 
-    def dir_b(self, st, pv, a_rows, a_k, c_rows, c_cnt, s):
-        return self.dx.elara_dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s)
+    def dir_b(self, st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=None):
+        return self.dx.elara_dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=rel)
 
     def init_rows(self, rows):
         return init_rows(rows, self.D, self.seed, self.bound)
@@ -167,6 +167,7 @@ class HipBackend:
         u.logs, u.log_rows, u.glog, u.glog_slots = logs, es.logs.shape[0], glog, es.glog.shape[0]
         u.grad = G.data_ptr()
         u.lr, u.b1, u.b2, u.eps = self.hp
+        a.dir_order = 1 if es.dir_impl == 'triton' else 0
         L = _lib.lib()
         nb = int(L.elr_step_exec_bytes(ctypes.byref(a)))
         _lib.check(min(nb, 0), 'elr_step_exec_bytes')
@@ -270,13 +271,20 @@ class ElaraStep:
     mat_cap - 1 of the MAT arena are trash rows); host_arenas: keep the MAT and log arenas in pinned host memory
     (the capacity tier, srm2/elara.py:40-103); host_budget: bytes the arenas may hold, accounted as the
     reference's ArenaStore does (faulted in chunks of budget_chunk bytes up to each arena's top; 0: no budget),
-    HostBudgetExceeded when a step would pass it (srm2/elara.py:63-81).
+    HostBudgetExceeded when a step would pass it (srm2/elara.py:63-81); dir_impl: the log-id allocation order of
+    the reference directory it stands in for (srm2/elara.py:150-155, srm2/train.py:133): 'cpp' (the default) or
+    'ref', equal, or 'triton', which allocates every log id of a step before any release (srm2/elara_kernels.py);
+    the other states are the same under all three.
     """
 
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
-                 backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK):
+                 backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK,
+                 dir_impl='cpp'):
         d = torch.device(device)
+        if dir_impl not in ('cpp', 'ref', 'triton'):
+            raise ValueError(f"dir_impl must be 'cpp', 'ref' or 'triton' (got {dir_impl!r})")
+        self.dir_impl = dir_impl
         self.d, self.R, self.D, self.C, self.K, self.L, self.depth = d, R, D, C, K, L, depth
         self.MAT = K + 1
         self.st_mode = st_mode
@@ -644,8 +652,9 @@ class ElaraStep:
             self._plan_stats(p, n_adm, nev, barrier)
             return p
         st, pv = self.state_list(), self.params()
-        (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots,
-         p.ev_dyn) = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s)
+        triton = self.dir_impl == 'triton'
+        outs = self.be.dir_a(st, pv, p.hit_slot, p.L_row, p.L_cnt, ev_slot, s, deferred=triton)
+        (p.L_steps, p.L_ids, p.hrec_dyn, p.hrec_j, p.ev_row, p.ev_rep, p.evl_ids, p.evf_slots, p.ev_dyn) = outs[:9]
         # admissions (srm2/elara.py:345-367): admitted N, L, F rows take slots from the free stack's top
         if self._slots_in_place:   # the stack push, the admissions and the new slot list in one launch
             adm_slots = self.be.plan_admit_slots(self._free_buf, self.n_free, ev_slot, keep_dyn,
@@ -666,8 +675,10 @@ class ElaraStep:
         if lazy_n and self.evl:
             p.adm_rec_slot = adm_slots[:lazy_n]   # their resident histories start at entry 0 of slot - n0
         # non-resident lazy rows: append (stay L, entry index = current count) or compact (to M)
+        # (the Triton path's order: the evictions' deferred releases go first, after the appends' pops)
         p.a_ids, p.c_slots = self.be.dir_b(st, pv, u_ord[rs(R_NAPP, R_LAPP)], c_ord[rs(R_NAPP, R_LAPP)],
-                                           u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)], s)
+                                           u_ord[rs(R_NCMP, R_LCMP)], c_ord[rs(R_NCMP, R_LCMP)], s,
+                                           rel=(p.ev_row, outs[9]) if triton else None)
         # MAT slots of the transient F and the S rows (adjacent ranks; the directory calls above move no F/S row)
         fs = loc_ord[rs(R_FN, R_S)]
         p.FN_slot, p.S_slot = fs[:nFn], fs[nFn:]

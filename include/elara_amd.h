@@ -157,7 +157,8 @@ int elr_dir_a(const elr_dir_state* st, const elr_dir_params* p, const int64_t* h
 /* The eviction part of call A in the form of srm2/elara_kernels.py:152-171 Directory.evict: the caller has unmapped
  * the evicted slots (slot_of / slot_row) itself and passes their rows ev_row int64 [nev] and thresholds thr int8
  * [nev] (kthr of each row's table).  Outputs as elr_dir_a's rep, evl_ids, evf_slots, ev_dyn.  Allocation order:
- * this build's (the one of elr_dir_a: the released host logs of rows going to M are pushed at once). */
+ * elr_dir_a's (the released host logs of rows going to M are pushed at once); elr_dir_evict_deferred below keeps
+ * the Triton path's. */
 int elr_dir_evict(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot, const int64_t* ev_row,
                   const int8_t* thr, int64_t nev, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots,
                   int64_t* ev_dyn, void* scratch, int64_t scratch_bytes, void* stream);
@@ -168,6 +169,39 @@ int elr_dir_evict(const elr_dir_state* st, const elr_dir_params* p, const int64_
 int elr_dir_b(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k, int64_t na,
               const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids, int64_t* c_slots,
               void* scratch, int64_t scratch_bytes, void* stream);
+
+/* The reference's Triton directory path (srm2/elara.py:279-318, 374-378 with srm2/elara_kernels.py), whose log ids
+ * follow another allocation order: every log id of a step is allocated before any of its releases.  States other
+ * than the log ids (and the free stack holding them) are the same under both orders.
+ *
+ * Replaces: lsteps + hits + Directory.evict (elara_kernels.py:16-60, 152-171) in the planner's call sequence.  As
+ * elr_dir_a, except that the host logs of rows going to M are not released: rel_cnt int64 [nev] receives each
+ * evicted row's release count (max(c0, 0) for a row going to M, 0 for one going back to L; the release part of
+ * elara_kernels.py:171), for elr_dir_b_release. */
+int elr_dir_a_deferred(const elr_dir_state* st, const elr_dir_params* p, const int64_t* hs, int64_t nh,
+                       const int64_t* L_row, const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot, int64_t nev,
+                       int64_t s, int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j,
+                       int64_t* ev_row, uint8_t* rep, int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn,
+                       int64_t* rel_cnt, void* scratch, int64_t scratch_bytes, void* stream);
+
+/* Replaces: Directory.evict (elara_kernels.py:152-171): elr_dir_evict with the releases deferred as in
+ * elr_dir_a_deferred (rel_cnt int64 [nev]). */
+int elr_dir_evict_deferred(const elr_dir_state* st, const elr_dir_params* p, const int64_t* ev_slot,
+                           const int64_t* ev_row, const int8_t* thr, int64_t nev, uint8_t* rep, int64_t* evl_ids,
+                           int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch,
+                           int64_t scratch_bytes, void* stream);
+
+/* Replaces: Directory.appends, .compact and .release (elara_kernels.py:173-209).  Appends of a_rows [na] at entry a_k
+ * -> a_ids (log ids popped as elr_dir_b pops them); MAT slots and code = MAT of the compacted rows c_rows [nc] ->
+ * c_slots; then the releases, pushed onto the free stack in this order: the first r_cnt[i] logged entries of each
+ * r_rows[i] (i < nr), then -- when c_release -- the first c_cnt[i] of each compacted row.  elr_dir_b is this call
+ * with c_release = 1 and nr = 0.  The planner's Triton path: the evictions' (ev_row, rel_cnt) as r and c_release =
+ * 1, after elr_dir_a_deferred.  All inputs int64.  `scratch` (device, >= elr_dir_scratch_bytes(0, nc + nr) bytes)
+ * is needed when na + nc + nr > 0. */
+int elr_dir_b_release(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,
+                      int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int c_release,
+                      const int64_t* r_rows, const int64_t* r_cnt, int64_t nr, int64_t s, int64_t* a_ids,
+                      int64_t* c_slots, void* scratch, int64_t scratch_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------------------
  * Batch dedup and duplicate-id gradient reduction.
@@ -508,6 +542,9 @@ typedef struct elr_exec_args {
   int64_t table_rows;
   elr_update_args upd;        /* D, K, the arenas and their rows, grad, lr, b1, b2, eps, n0 (the other fields are set
                                  by the call) */
+  int64_t dir_order;          /* log-id allocation order: 0 = elara_dir.cpp's (the reference's default directory,
+                                 equal to its torch path), 1 = its Triton path's (as elr_dir_a_deferred followed by
+                                 elr_dir_b_release) */
 } elr_exec_args;
 
 /* Offsets (bytes from ws) of the arrays elr_step_exec writes: elr_dir_a's nine outputs (L_steps, L_ids, hrec_dyn,

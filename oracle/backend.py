@@ -153,12 +153,15 @@ class OracleBackend:
         v.K = int(pv[1])
         return v
 
-    def dir_a(self, st, pv, hs, L_row, L_cnt, ev_slot, s):
-        out = O.dir_a(self._view(st, pv), pv, hs.numpy(), L_row.numpy(), L_cnt.numpy(), ev_slot.numpy(), s)
+    def dir_a(self, st, pv, hs, L_row, L_cnt, ev_slot, s, deferred=False):
+        out = O.dir_a(self._view(st, pv), pv, hs.numpy(), L_row.numpy(), L_cnt.numpy(), ev_slot.numpy(), s,
+                      deferred=deferred)
         return [torch.from_numpy(np.ascontiguousarray(o)) for o in out]
 
-    def dir_b(self, st, pv, a_rows, a_k, c_rows, c_cnt, s):
-        out = O.dir_b(self._view(st, pv), pv, a_rows.numpy(), a_k.numpy(), c_rows.numpy(), c_cnt.numpy(), s)
+    def dir_b(self, st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=None):
+        rel = None if rel is None else (rel[0].numpy(), rel[1].numpy())
+        out = O.dir_b(self._view(st, pv), pv, a_rows.numpy(), a_k.numpy(), c_rows.numpy(), c_cnt.numpy(), s,
+                      rel=rel)
         return [torch.from_numpy(o) for o in out]
 
     def init_rows(self, rows):

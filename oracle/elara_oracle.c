@@ -343,11 +343,15 @@ static int64_t orc_table_of(const orc_dir* d, int64_t row) {
 }
 
 /* elara_dir.cpp:50-96 (call A).  Outputs: L_steps i32[nL,K], L_ids i32[nL,K], hrec_dyn i64[nh], hrec_j i64[nh],
- * ev_row i64[nev], rep u8[nev], evl_ids i64[nev,K], evf_slots i64[nev], ev_dyn i64[nev]. */
+ * ev_row i64[nev], rep u8[nev], evl_ids i64[nev,K], evf_slots i64[nev], ev_dyn i64[nev].
+ * rel_cnt != NULL: the order of the reference's Triton path (srm2/elara_kernels.py:63-75, 152-171: Directory.evict
+ * allocates and assigns MAT slots but releases nothing; its release part (ev_row, counts[1]) with counts[1] =
+ * rep ? 0 : max(c0, 0) is pushed by Directory.release after the step's appends): the host logs of rows going to M
+ * stay, and rel_cnt i64[nev] receives those counts for orc_dir_b. */
 int orc_dir_a(orc_dir* d, const orc_dir_params* p, const int64_t* hs, int64_t nh, const int64_t* L_row,
               const int32_t* L_cnt, int64_t nL, const int64_t* ev_slot, int64_t nev, int64_t s,
               int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, int64_t* ev_row, uint8_t* rep,
-              int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn) {
+              int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt) {
   const int64_t K = p->K;
   /* replay inputs (elara_dir.cpp:56-59) */
   for (int64_t i = 0; i < nL; ++i)
@@ -408,10 +412,12 @@ int orc_dir_a(orc_dir* d, const orc_dir_params* p, const int64_t* hs, int64_t nh
   for (int64_t i = 0; i < nev; ++i)
     if (rep[i]) evf_slots[i] = p->trash;
   if (nev) {
-    int64_t* cnt = (int64_t*)malloc(sizeof(int64_t) * (size_t)nev);
+    int64_t* cnt = rel_cnt ? rel_cnt : (int64_t*)malloc(sizeof(int64_t) * (size_t)nev);
     for (int64_t i = 0; i < nev; ++i) cnt[i] = rep[i] ? 0 : (c0[i] > 0 ? c0[i] : 0);
-    orc_free_logs(d, p, ev_row, cnt, nev);
-    free(cnt);
+    if (!rel_cnt) {
+      orc_free_logs(d, p, ev_row, cnt, nev);
+      free(cnt);
+    }
     for (int64_t i = 0; i < nev; ++i) {
       int64_t t = c0[i] + jj[i];
       d->code[ev_row[i]] = rep[i] ? (int8_t)(t < 127 ? t : 127) : (int8_t)p->MAT;
@@ -422,9 +428,15 @@ int orc_dir_a(orc_dir* d, const orc_dir_params* p, const int64_t* hs, int64_t nh
 }
 
 /* elara_dir.cpp:98-110 (call B): appends (stay L), then compactions (to M).  Outputs a_ids i64[na], c_slots
- * i64[nc]. */
+ * i64[nc].  Releases: those of r_rows[0..nr) (the first r_cnt[i] entries each), then, when c_release, those of the
+ * compacted rows, as one push sequence.  The reference's default order is nr = 0, c_release = 1; its Triton path
+ * (srm2/elara_kernels.py:173-209: appends, compact without release, then release([ev part, (c_rows, c_cnt)])) is
+ * the evictions' deferred part as r with c_release = 1.  Directory.release places entry k of item i at n_lfree +
+ * (counts before i) + k; every counted entry exists there by construction (elara_kernels.py:208), so that equals
+ * the packed push of orc_free_logs. */
 int orc_dir_b(orc_dir* d, const orc_dir_params* p, const int64_t* a_rows, const int64_t* a_k, int64_t na,
-              const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids, int64_t* c_slots) {
+              const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, int64_t s, int64_t* a_ids, int64_t* c_slots,
+              int c_release, const int64_t* r_rows, const int64_t* r_cnt, int64_t nr) {
   const int64_t K = p->K;
   uint8_t* ones = (uint8_t*)malloc((size_t)(na > 0 ? na : 1));
   memset(ones, 1, (size_t)(na > 0 ? na : 1));
@@ -434,9 +446,16 @@ int orc_dir_b(orc_dir* d, const orc_dir_params* p, const int64_t* a_rows, const 
   for (int64_t i = 0; i < na; ++i) d->lstep[a_ids[i]] = (int32_t)s;
   for (int64_t i = 0; i < na; ++i) d->code[a_rows[i]] = (int8_t)(a_k[i] + 1);
   orc_alloc_mat(d, c_rows, NULL, nc, c_slots);
-  if (nc) {
-    orc_free_logs(d, p, c_rows, c_cnt, nc);
-    for (int64_t i = 0; i < nc; ++i) d->code[c_rows[i]] = (int8_t)p->MAT;
+  const int64_t nrel = nr + (c_release ? nc : 0);
+  if (nrel) {
+    int64_t* rows = (int64_t*)malloc(sizeof(int64_t) * (size_t)nrel);
+    int64_t* cnt = (int64_t*)malloc(sizeof(int64_t) * (size_t)nrel);
+    for (int64_t i = 0; i < nr; ++i) { rows[i] = r_rows[i]; cnt[i] = r_cnt[i]; }
+    for (int64_t i = nr; i < nrel; ++i) { rows[i] = c_rows[i - nr]; cnt[i] = c_cnt[i - nr]; }
+    orc_free_logs(d, p, rows, cnt, nrel);
+    free(rows);
+    free(cnt);
   }
+  for (int64_t i = 0; i < nc; ++i) d->code[c_rows[i]] = (int8_t)p->MAT;
   return 0;
 }

@@ -164,8 +164,10 @@ class DirState:
         return _Dir(*[_p(getattr(self, f)) for f in DIR_FIELDS], self.kthr.size)
 
 
-def dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
-    """Oracle of elara_dir_a (srm2/csrc/elara_dir.cpp:50-96); mutates st.  Returns the 9 outputs as numpy."""
+def dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s, deferred=False):
+    """Oracle of elara_dir_a (srm2/csrc/elara_dir.cpp:50-96); mutates st.  Returns the 9 outputs as numpy.
+    deferred: the Triton path's order (srm2/elara_kernels.py:152-171): the host logs of rows going to M are not
+    released, and a 10th output holds their release counts (for dir_b's `rel`)."""
     K = st.K
     hs = np.ascontiguousarray(hs, np.int64); L_row = np.ascontiguousarray(L_row, np.int64)
     L_cnt = np.ascontiguousarray(L_cnt, np.int32); ev_slot = np.ascontiguousarray(ev_slot, np.int64)
@@ -174,19 +176,29 @@ def dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s):
     hrec_dyn = np.empty(nh, np.int64); hrec_j = np.empty(nh, np.int64)
     ev_row = np.empty(nev, np.int64); rep = np.empty(nev, np.uint8); evl_ids = np.empty((nev, K), np.int64)
     evf = np.empty(nev, np.int64); ev_dyn = np.empty(nev, np.int64)
+    rel_cnt = np.zeros(nev, np.int64) if deferred else None
     d = st._c(); p = _Params(*pv)
     lib().orc_dir_a(ctypes.byref(d), ctypes.byref(p), _p(hs), ctypes.c_int64(nh), _p(L_row), _p(L_cnt),
                     ctypes.c_int64(nL), _p(ev_slot), ctypes.c_int64(nev), ctypes.c_int64(s), _p(L_steps), _p(L_ids),
-                    _p(hrec_dyn), _p(hrec_j), _p(ev_row), _p(rep), _p(evl_ids), _p(evf), _p(ev_dyn))
-    return [L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep.astype(bool), evl_ids, evf, ev_dyn]
+                    _p(hrec_dyn), _p(hrec_j), _p(ev_row), _p(rep), _p(evl_ids), _p(evf), _p(ev_dyn),
+                    _p(rel_cnt) if deferred else None)
+    out = [L_steps, L_ids, hrec_dyn, hrec_j, ev_row, rep.astype(bool), evl_ids, evf, ev_dyn]
+    return out + [rel_cnt] if deferred else out
 
 
-def dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s):
-    """Oracle of elara_dir_b (srm2/csrc/elara_dir.cpp:98-110); mutates st.  Returns (a_ids, c_slots)."""
+def dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=None, c_release=True):
+    """Oracle of elara_dir_b (srm2/csrc/elara_dir.cpp:98-110); mutates st.  Returns (a_ids, c_slots).
+    rel = (rows, counts): releases pushed after the appends, ahead of the compacted rows' (which are released only
+    when c_release) -- the Triton path's Directory.compact / .release (srm2/elara_kernels.py:188-209)."""
     a_rows = np.ascontiguousarray(a_rows, np.int64); a_k = np.ascontiguousarray(a_k, np.int64)
     c_rows = np.ascontiguousarray(c_rows, np.int64); c_cnt = np.ascontiguousarray(c_cnt, np.int64)
     a_ids = np.empty(a_rows.size, np.int64); c_slots = np.empty(c_rows.size, np.int64)
+    r_rows, r_cnt = (np.zeros(0, np.int64),) * 2 if rel is None else \
+        (np.ascontiguousarray(rel[0], np.int64), np.ascontiguousarray(rel[1], np.int64))
+    if r_rows.size != r_cnt.size:
+        raise ValueError('rel rows and counts must have the same length')
     d = st._c(); p = _Params(*pv)
     lib().orc_dir_b(ctypes.byref(d), ctypes.byref(p), _p(a_rows), _p(a_k), ctypes.c_int64(a_rows.size), _p(c_rows),
-                    _p(c_cnt), ctypes.c_int64(c_rows.size), ctypes.c_int64(s), _p(a_ids), _p(c_slots))
+                    _p(c_cnt), ctypes.c_int64(c_rows.size), ctypes.c_int64(s), _p(a_ids), _p(c_slots),
+                    ctypes.c_int(int(bool(c_release))), _p(r_rows), _p(r_cnt), ctypes.c_int64(r_rows.size))
     return [a_ids, c_slots]

@@ -129,16 +129,23 @@ class Sim:
 # ------------------------------------------------------------------------------------------------------------
 # implementations
 class OracleImpl:
-    """The C oracle (oracle/elara_oracle.c) on numpy arrays."""
+    """The C oracle (oracle/elara_oracle.c) on numpy arrays.  triton: the allocation order of the reference's Triton
+    directory (srm2/elara_kernels.py): call A keeps the releases of rows going to M for call B, which pushes them
+    after its appends and ahead of the compacted rows' logs."""
 
-    def __init__(self, sim, st):
-        self.sim, self.st = sim, st.copy()
+    def __init__(self, sim, st, triton=False):
+        self.sim, self.st, self.triton = sim, st.copy(), triton
+        self.rel = None
 
     def view(self):
         return {f: getattr(self.st, f) for f in O.DIR_FIELDS}
 
     def dir_a(self, hs, L_row, L_cnt, ev_slot, s):
-        return O.dir_a(self.st, self.sim.pv, hs, L_row, L_cnt, ev_slot, s)
+        out = O.dir_a(self.st, self.sim.pv, hs, L_row, L_cnt, ev_slot, s, deferred=self.triton)
+        if self.triton:
+            self.rel = (out[4], out[9])
+            out = out[:9]
+        return out
 
     def admit(self, rows, slots, adm_c0, lazy, pst, s):
         st = self.st
@@ -150,16 +157,17 @@ class OracleImpl:
         st.pstep[pst * self.sim.K] = s
 
     def dir_b(self, a_rows, a_k, c_rows, c_cnt, s):
-        return O.dir_b(self.st, self.sim.pv, a_rows, a_k, c_rows, c_cnt, s)
+        return O.dir_b(self.st, self.sim.pv, a_rows, a_k, c_rows, c_cnt, s, rel=self.rel)
 
 
 class TorchImpl:
     """The 17 directory tensors on a torch device, driven through a dir_ext()-like module (the reference's
     elara_dir.cpp build on CPU tensors, or elara_amd's HIP directory on the GPU)."""
 
-    def __init__(self, sim, st, ext, device='cpu'):
+    def __init__(self, sim, st, ext, device='cpu', triton=False):
         import torch
         self.torch, self.sim, self.ext, self.dev = torch, sim, ext, device
+        self.triton, self.rel = triton, None   # triton: elara_amd's deferred-release calls, as OracleImpl
         self.st = [torch.from_numpy(np.ascontiguousarray(getattr(st, f))).to(device) for f in O.DIR_FIELDS]
         self.st[11] = self.st[11].reshape(sim.Cdyn + 1, sim.K)
 
@@ -172,8 +180,12 @@ class TorchImpl:
 
     def dir_a(self, hs, L_row, L_cnt, ev_slot, s):
         torch = self.torch
+        kw = {'deferred': True} if self.triton else {}
         out = self.ext.elara_dir_a(self.st, list(self.sim.pv), self.t(hs, torch.int64), self.t(L_row, torch.int64),
-                                   self.t(L_cnt, torch.int32), self.t(ev_slot, torch.int64), int(s))
+                                   self.t(L_cnt, torch.int32), self.t(ev_slot, torch.int64), int(s), **kw)
+        if self.triton:
+            self.rel = (out[4], out[9])
+            out = out[:9]
         return [o.cpu().numpy() for o in out]
 
     def admit(self, rows, slots, adm_c0, lazy, pst, s):
@@ -190,8 +202,9 @@ class TorchImpl:
 
     def dir_b(self, a_rows, a_k, c_rows, c_cnt, s):
         torch = self.torch
+        kw = {'rel': self.rel} if self.triton else {}
         out = self.ext.elara_dir_b(self.st, list(self.sim.pv), self.t(a_rows, torch.int64), self.t(a_k, torch.int64),
-                                   self.t(c_rows, torch.int64), self.t(c_cnt, torch.int64), int(s))
+                                   self.t(c_rows, torch.int64), self.t(c_cnt, torch.int64), int(s), **kw)
         return [o.cpu().numpy() for o in out]
 
 
@@ -247,7 +260,8 @@ def check_invariants(view, sim):
 
 class FacadeImpl(TorchImpl):
     """The directory driven through the elara_kernels-style front end (hits / lsteps / Directory), in the call
-    sequence of the reference planner's fused path (srm2/elara.py:281-283, 292-293, 312-318, 376-378)."""
+    sequence of the reference planner's fused path (srm2/elara.py:281-283, 292-293, 312-318, 376-378), and with
+    that path's allocation order (compare with OracleImpl(triton=True))."""
 
     class _Planner:
         pass

@@ -21,6 +21,10 @@ pressure gate of evict_logs=2 is the executor's (srm2/elara.py:423-425), reading
 step.  The pinned static rows get code MAT before the first plan, as the executor's load_static does at set-up
 (srm2/elara.py:433-439).
 
+The configurations named triton_* rerun a configuration above with dir_impl='triton', the reference's Triton
+directory (srm2/elara_kernels.py), whose log ids follow its own allocation order (every allocation of a step before
+any release).  Its kernels run in Triton's interpreter (TRITON_INTERPRET=1) on the same CPU tensors.
+
 Batches come from elara_amd.synth (numpy, seeded): configuration inputs are stored in the fixture as well, so the
 tests do not depend on the generator staying the same.
 """
@@ -28,8 +32,10 @@ import os
 import sys
 from pathlib import Path
 
-import numpy as np
-import torch
+os.environ.setdefault('TRITON_INTERPRET', '1')   # before srm2.elara_kernels imports triton
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
 
 ROOT = Path(__file__).resolve().parents[2]
 REF = Path(os.environ.get('ELARA_REFERENCE', '/root/reference'))
@@ -51,6 +57,8 @@ CONFIGS = {
     'evl_gate': (5, 100, 3000, 300, 40, 700, 400, 3, 3, 8, 3, 'T', 'ttl', 2, 1_250_000, 7),
     'budget_raise': (5, 100, 3000, 300, 40, 700, 400, 3, 3, 8, 3, 'T', 'ttl', 1, 800_000, 8),
 }
+# the Triton directory's runs: name -> the configuration above it repeats
+TRITON = {f'triton_{b}': b for b in ('ttl_evl', 'ttl_S_overflow', 'ttl_K4_kthr', 'carry_overflow', 'evl_gate')}
 D = 32   # width used by the store accounting and the gate (the planner itself is width-free)
 
 
@@ -60,7 +68,7 @@ def batches_of(T, lo, hi, B, steps, seed):
     return tabs, rng, [np.unique(tabs.batch(rng, B)) for _ in range(steps)]
 
 
-def run(name, cfg):
+def run(name, cfg, dir_impl='ref'):
     import srm2.elara as E
     from oracle import ref as REFBUILD
     (T, lo, hi, B, steps, C, n_static, K, kthr, L, depth, st, dyn, evl, budget, seed) = cfg
@@ -68,7 +76,8 @@ def run(name, cfg):
     static = tabs.static_rows(rng, B, n_static, n_batches=10)
     kt = torch.tensor(kthr if isinstance(kthr, tuple) else [kthr] * T, dtype=torch.int8)
     pl = E.ELARAPlanner(tabs.R, C, K, 'static', dyn, st, torch.from_numpy(static), L, torch.device('cpu'),
-                        torch.from_numpy(tabs.toff), kt, evict_logs=evl, fused_dir=False, dir_impl='ref')
+                        torch.from_numpy(tabs.toff), kt, evict_logs=evl, fused_dir=dir_impl == 'triton',
+                        dir_impl=dir_impl)
     pl.code[pl.static_rows] = pl.MAT   # the executor's load_static (srm2/elara.py:433-439), run before training
     store = None
     if budget:
@@ -140,7 +149,8 @@ def run(name, cfg):
     out[f'{name}/kthr'] = kt.numpy()
     out[f'{name}/meta'] = np.array([tabs.R, C, K, L, depth, int(st == 'S'), int(dyn == 'carry'), evl, budget,
                                     CHUNK_TEST if budget else 0, D, done, raised_at, pl.log_cap,
-                                    int(pl.stats.get('preempt', 0)), int(pl.stats['overflow'])], np.int64)
+                                    int(pl.stats.get('preempt', 0)), int(pl.stats['overflow']),
+                                    int(dir_impl == 'triton')], np.int64)
     store_res = [0, 0] if store is None else [store.faulted['mat'], store.faulted['log']]
     out[f'{name}/store_faulted'] = np.array(store_res, np.int64)
     print(f'{name}: {done} steps, raised_at {raised_at}, stats {pl.stats}, evl_on {pl.evict_logs}, '
@@ -149,9 +159,11 @@ def run(name, cfg):
 
 
 def main():
-    vec = {'configs': np.array(list(CONFIGS))}
+    vec = {'configs': np.array(list(CONFIGS) + list(TRITON))}
     for name, cfg in CONFIGS.items():
         vec.update(run(name, cfg))
+    for name, base in TRITON.items():
+        vec.update(run(name, CONFIGS[base], dir_impl='triton'))
     np.savez_compressed(OUT, **vec)
     print(f'wrote {OUT} ({OUT.stat().st_size} bytes)')
 

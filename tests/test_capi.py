@@ -59,6 +59,43 @@ def test_step_exec_checks_and_workspace_size():
     assert L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(272), 1 << 30, ctypes.byref(o), None) == -3  # unaligned
 
 
+def test_triton_order_argument_checks():
+    """The Triton-order directory calls reject missing release arrays, a short scratch and an unknown step order on
+    the host (no call here reaches the GPU: each returns before any launch or has nothing to launch)."""
+    L = _lib.lib()
+    fake = ctypes.c_void_p(256)          # never dereferenced
+    S = _lib.DirState(*([256] * 17), 1)
+    P = _lib.DirParams(100, 3, 200, 0, 10, 4, 100, 1)
+    sp, pp = ctypes.byref(S), ctypes.byref(P)
+    outs = [fake] * 9
+    # elr_dir_a_deferred: evictions need rel_cnt
+    assert L.elr_dir_a_deferred(sp, pp, None, 0, None, None, 0, fake, 4, 1, *outs, None, fake, 1 << 20, None) == -1
+    assert L.elr_dir_evict_deferred(sp, pp, fake, fake, fake, 4, fake, fake, fake, fake, None, fake, 1 << 20,
+                                    None) == -1
+    assert L.elr_dir_evict_deferred(sp, pp, None, None, None, 0, None, None, None, None, None, None, 0, None) == 0
+    # elr_dir_b_release: release items need rows and counts; the scratch covers them
+    assert L.elr_dir_b_release(sp, pp, None, None, 0, None, None, 0, 1, None, fake, 5, 1, None, None, fake, 1 << 20,
+                               None) == -1
+    need = L.elr_dir_scratch_bytes(0, 70_000)
+    assert need > L.elr_dir_scratch_bytes(0, 60_000) > 0
+    assert L.elr_dir_b_release(sp, pp, None, None, 0, fake, fake, 60_000, 1, fake, fake, 10_000, 1, None, fake,
+                               fake, need - 1, None) == -3
+    assert L.elr_dir_b_release(sp, pp, None, None, 0, None, None, 0, 1, None, None, 0, 1, None, None, None, 0,
+                               None) == 0
+    assert L.elr_dir_b_release(sp, pp, None, None, -1, None, None, 0, 1, None, None, 0, 1, None, None, None, 0,
+                               None) == -1
+    # the step's order flag
+    a = _lib.ExecArgs()
+    a.pv.K, a.upd.D = 3, 64
+    a.b[1:] = [5, 7, 9, 9, 12, 12, 15, 15, 16, 20]
+    a.slots.nev = 40
+    nb0 = L.elr_step_exec_bytes(ctypes.byref(a))
+    a.dir_order = 1
+    assert L.elr_step_exec_bytes(ctypes.byref(a)) > nb0          # the deferred release counts
+    a.dir_order = 2
+    assert L.elr_step_exec_bytes(ctypes.byref(a)) == -1
+
+
 def test_version_and_errors():
     L = _lib.lib()
     assert L.elr_version() >= 100

@@ -1,5 +1,9 @@
 """State directory (srm2/csrc/elara_dir.cpp elara_dir_a / elara_dir_b): the C oracle against the reference's own
-build (oracle/_ref, CPU tensors) and the HIP path (elr_dir_a / elr_dir_b through the C-ABI) against both.
+build (oracle/_ref, CPU tensors) and the HIP path (elr_dir_a / elr_dir_b through the C-ABI) against both.  The
+Triton path's allocation order (srm2/elara_kernels.py; the oracle's deferred releases, elr_dir_a_deferred,
+elr_dir_evict_deferred, elr_dir_b_release) is pinned by the reference planner's golden vectors
+(tests/test_planner_golden.py), by a hand-worked step and by its equality with the default order in everything
+but the log ids; the GPU calls and the Triton front end are checked against it here.
 
 Every step compares all 9 + 2 outputs and the whole directory (17 arrays) bitwise, except the two trash elements
 lstep[Lcap] and lfree[Lcap], whose contents the reference leaves unspecified.  Each run also checks the invariants
@@ -67,10 +71,66 @@ def test_oracle_allocators_by_hand():
     assert c_slots.tolist() == [1] and st.mat_top[0] == 2
 
 
+def test_oracle_triton_order_by_hand():
+    """One step in both orders.  Row 1 (two host-log entries, ids 0 and 1) is evicted to M; then rows 3 and 4 are
+    appended and row 2 (one entry, id 2) compacted.  Default order (elara_dir.cpp:80-94, 102-108): the eviction
+    pushes ids 0 and 1 at once, the appends pop them (1, then 0), the compaction pushes 2.  Triton order
+    (srm2/elara_kernels.py:152-209): the appends bump ids 3 and 4, then the releases push 0, 1 (the eviction's part)
+    and 2 (the compaction's)."""
+    R, C, K = 10, 4, 3
+    res = {}
+    for triton in (False, True):
+        st = O.DirState(R, C, K, 0, np.array([0], np.int64), np.array([1], np.int8), log_cap=20)
+        pv = st.params(True)
+        a_ids, _ = O.dir_b(st, pv, [1, 1, 2], [0, 1, 0], [], [], 1)
+        assert a_ids.tolist() == [0, 1, 2] and st.code[[1, 2]].tolist() == [2, 1]
+        st.slot_of[1], st.slot_row[0], st.adm_c0[0], st.rj[0], st.rok[0] = 0, 1, 2, 0, 1   # row 1 admitted (L)
+        e = np.empty(0, np.int64)
+        out = O.dir_a(st, pv, e, e, np.empty(0, np.int32), [0], 2, deferred=triton)
+        assert out[4].tolist() == [1] and not out[5][0] and out[7].tolist() == [0]      # to M, MAT slot 0
+        if triton:
+            assert out[9].tolist() == [2] and st.n_lfree[0] == 0 and st.ent[1 * K:1 * K + 2].tolist() == [0, 1]
+        else:
+            assert st.lfree[:2].tolist() == [0, 1] and st.n_lfree[0] == 2 and st.ent[1 * K] == -1
+        a_ids, c_slots = O.dir_b(st, pv, [3, 4], [0, 0], [2], [1], 3, rel=(out[4], out[9]) if triton else None)
+        assert c_slots.tolist() == [1] and st.code[[1, 2, 3, 4]].tolist() == [4, 4, 1, 1]
+        res[triton] = (a_ids.tolist(), st.lfree[:int(st.n_lfree[0])].tolist(), int(st.log_top[0]), int(st.live[0]))
+    assert res[False] == ([1, 0], [2], 3, 2)
+    assert res[True] == ([3, 4], [0, 1, 2], 5, 2)
+
+
+@pytest.mark.parametrize('name', sorted(CONFIGS))
+def test_oracle_triton_order_changes_only_log_ids(name):
+    """Over 60 planned steps the two orders agree on every state and output except the log ids: the same codes,
+    MAT slots, residency and resident histories, the same rows holding log entries and the same logical step in
+    each (lstep[ent[r, k]]), and only the ids themselves (and the free stack holding them) may differ; both keep
+    the allocator invariants."""
+    sim = Sim(**CONFIGS[name])
+    st0 = sim.initial_state()
+    a, b = OracleImpl(sim, st0), OracleImpl(sim, st0, triton=True)
+    K, differs = sim.K, 0
+    for s in range(1, 61):
+        (A0, A1), (B0, B1) = sim.step(s, [a, b])   # calls A and B of each order
+        va, vb = a.view(), b.view()
+        for f in ('code', 'loc', 'mat_top', 'live', 'adm_c0', 'rj', 'rok', 'pstep', 'slot_of', 'slot_row'):
+            assert np.array_equal(va[f], vb[f]), (s, f)
+        ea, eb = va['ent'][:sim.R * K], vb['ent'][:sim.R * K]
+        assert np.array_equal(ea >= 0, eb >= 0), s
+        assert np.array_equal(va['lstep'][ea[ea >= 0]], vb['lstep'][eb[eb >= 0]]), s
+        for k in (0, 2, 3, 4, 5, 7, 8):                   # call A's outputs except L_ids and evl_ids
+            assert np.array_equal(np.asarray(A0[k]), np.asarray(B0[k])), (s, k)
+        for k in (1, 6):
+            assert np.array_equal(np.asarray(A0[k]) >= 0, np.asarray(B0[k]) >= 0), (s, k)
+        assert np.array_equal(A1[1], B1[1]) and A1[0].size == B1[0].size, s     # c_slots; as many append ids
+        differs += int(not np.array_equal(ea, eb))
+        check_invariants(vb, sim)
+    assert differs > 0 or not sim.evl   # the orders do differ once rows go to M with host logs
+
+
 # ------------------------------------------------------------------------------------------------------------- GPU
-def gpu_impl(sim, st0, dev):
+def gpu_impl(sim, st0, dev, triton=False):
     from elara_amd.elara_dir import dir_ext
-    return TorchImpl(sim, st0, dir_ext(), device=dev)
+    return TorchImpl(sim, st0, dir_ext(), device=dev, triton=triton)
 
 
 @pytest.mark.gpu
@@ -87,15 +147,15 @@ def test_gpu_directory_matches_oracle_and_reference(dev, name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('name', ['default', 'k4_no_static', 'evl_off'])
+@pytest.mark.parametrize('name', sorted(CONFIGS))
 def test_gpu_directory_facade_matches_oracle(dev, name):
     """The elara_kernels-style front end (hits / lsteps / Directory.evict / appends / compact / release), driven in
-    the reference planner's fused-path call sequence, gives the same outputs and states as the oracle (this build
-    uses the cpp allocation order behind both front ends)."""
+    the reference planner's fused-path call sequence, gives the same outputs and states as the oracle in the Triton
+    path's allocation order, and so do elr_dir_a_deferred / elr_dir_b_release called as the step calls them."""
     print(f'[gpu-test] directory facade {name}', flush=True)
     sim = Sim(**CONFIGS[name])
     st0 = sim.initial_state()
-    run(sim, [OracleImpl(sim, st0), FacadeImpl(sim, st0, dev)], 60)
+    run(sim, [OracleImpl(sim, st0, triton=True), FacadeImpl(sim, st0, dev), gpu_impl(sim, st0, dev, True)], 60)
 
 
 @pytest.mark.gpu
@@ -115,6 +175,17 @@ def test_gpu_directory_evictions_beyond_fused_scan(dev):
     sim = Sim(seed=14, R=600_000, C=400_000, n0=2_000, K=3, T=4, batch=500_000, vocab_skew=0.3)
     st0 = sim.initial_state()
     run(sim, [OracleImpl(sim, st0), gpu_impl(sim, st0, dev)], 5)
+    assert sim.nev_max > 256 * 256
+
+
+@pytest.mark.gpu
+def test_gpu_directory_triton_order_beyond_fused_scan(dev):
+    """The Triton path's order with more than 65,536 evictions per call: call B's release items (one per eviction,
+    ahead of the compactions) take it past 256 blocks, so its counts are scanned in a launch of their own."""
+    print('[gpu-test] directory triton order beyond the fused scan', flush=True)
+    sim = Sim(seed=15, R=600_000, C=400_000, n0=2_000, K=3, T=4, batch=500_000, vocab_skew=0.3)
+    st0 = sim.initial_state()
+    run(sim, [OracleImpl(sim, st0, triton=True), gpu_impl(sim, st0, dev, True)], 5)
     assert sim.nev_max > 256 * 256
 
 
@@ -219,13 +290,15 @@ def test_gpu_dir_b_scan_beyond_one_scan_block(dev):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('nc', [256 * 256, 256 * 256 + 1])
-def test_gpu_dir_b_at_the_fused_scan_limit(dev, nc):
-    """Call B with exactly 256 blocks of compactions (the compaction kernel sums the block counts itself) and one
-    item more (a scan launch of its own), together with appends that pop the free stack: outputs and directory
-    equal the oracle's."""
+@pytest.mark.parametrize('order', ['cpp', 'triton'])
+def test_gpu_dir_b_at_the_fused_scan_limit(dev, nc, order):
+    """Call B with exactly 256 blocks of items (the compaction kernel sums the block counts itself) and one item
+    more (a scan launch of its own), together with appends that pop the free stack: outputs and directory equal the
+    oracle's.  Items: nc compactions (cpp), or a third of them release items ahead of the compactions (triton,
+    elr_dir_b_release)."""
     import torch
     from elara_amd.elara_dir import dir_ext
-    print(f'[gpu-test] dir_b nc={nc}', flush=True)
+    print(f'[gpu-test] dir_b nc={nc} {order}', flush=True)
     rng = np.random.default_rng(30 + nc)
     R, K, C = 400_000, 3, 8
     st = O.DirState(R, C, K, 0, np.array([0], np.int64), np.array([3], np.int8))
@@ -245,8 +318,14 @@ def test_gpu_dir_b_at_the_fused_scan_limit(dev, nc):
     O.dir_b(st, pv, [], [], done, cnt[nc:nc + 2_000].astype(np.int64), 5)
     gst = [torch.from_numpy(getattr(st, f).copy()).to(dev) for f in O.DIR_FIELDS]
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int64)).to(dev)  # noqa: E731
-    want = O.dir_b(st, pv, fresh, np.zeros(fresh.size, np.int64), crow, ccnt, 9)
-    got = dir_ext().elara_dir_b(gst, list(pv), T(fresh), T(np.zeros(fresh.size)), T(crow), T(ccnt), 9)
+    rel = None
+    if order == 'triton':
+        nr = nc // 3
+        rel = (crow[:nr], ccnt[:nr])
+        crow, ccnt = crow[nr:], ccnt[nr:]
+    want = O.dir_b(st, pv, fresh, np.zeros(fresh.size, np.int64), crow, ccnt, 9, rel=rel)
+    got = dir_ext().elara_dir_b(gst, list(pv), T(fresh), T(np.zeros(fresh.size)), T(crow), T(ccnt), 9,
+                                rel=None if rel is None else (T(rel[0]), T(rel[1])))
     torch.cuda.synchronize()
     for w, g in zip(want, got):
         assert np.array_equal(w, g.cpu().numpy())

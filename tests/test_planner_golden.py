@@ -2,7 +2,9 @@
 tests/golden/make_planner_vectors.py, which runs srm2/elara.py's ELARAPlanner (dir_impl='ref') on CPU tensors over
 the configurations there (TTL and carry residency, evl off / on / gated by memory pressure, preemption, overflow
 with carry barriers, per-table thresholds, a host budget that is exceeded) and drives the reference's ArenaStore
-accounting.  ElaraStep plans the same batches -- on the oracle backend (CPU) and on this library's kernels (GPU) --
+accounting; the triton_* configurations repeat five of them with the reference's Triton directory
+(dir_impl='triton', srm2/elara_kernels.py, in Triton's interpreter), whose log ids follow its own allocation order,
+and ElaraStep plans them with dir_impl='triton'.  ElaraStep plans the same batches -- on the oracle backend (CPU) and on this library's kernels (GPU) --
 and must produce, step by step, the same classes, evictions, admissions, replay inputs, resident-history records,
 log ids and MAT slots, the same barriers and representation switch, the same HostBudgetExceeded step, and at the
 end the same directory and residency state."""
@@ -37,14 +39,16 @@ def per_step(z, name, key):
 def run_config(name, device, backend):
     from elara_amd.step import ElaraStep, HostBudgetExceeded, run
     z = _fix()
-    (R, C, K, L, depth, st_S, carry, evl, budget, chunk, D, done, raised_at, log_cap, _, _) = z[f'{name}/meta'].tolist()
+    meta = z[f'{name}/meta'].tolist()
+    (R, C, K, L, depth, st_S, carry, evl, budget, chunk, D, done, raised_at, log_cap, _, _) = meta[:16]
+    triton = len(meta) > 16 and meta[16] == 1
     U = per_step(z, name, 'U')
     steps = len(U)
     st = ElaraStep(z[f'{name}/toff'], R, D, C, static_rows=z[f'{name}/static'], K=K,
                    kthr=torch.from_numpy(z[f'{name}/kthr']), evl=evl, L=L, depth=depth, st_mode='S' if st_S else 'T',
                    dyn='carry' if carry else 'ttl', seed=42, bound=synth.bound_for(D), hp=HP, max_step=steps + 2,
                    log_cap=log_cap, mat_cap=R + 1, device=device, backend=backend, host_budget=budget,
-                   budget_chunk=chunk or (64 << 20))
+                   budget_chunk=chunk or (64 << 20), dir_impl='triton' if triton else 'cpp')
     got = {k: [] for k in FIELDS}
 
     def on_step(s, p):
