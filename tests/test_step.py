@@ -24,7 +24,7 @@ def make(cfg, device, backend=None):
                      st_mode=cfg.get('st', 'T'), seed=42, bound=cfg['bound'], hp=HP, max_step=cfg['steps'] + 2,
                      log_cap=cfg['log_cap'], mat_cap=cfg['mat_cap'], device=device, backend=backend,
                      host_arenas=cfg.get('host', False), dyn=cfg.get('dyn', 'ttl'), host_budget=cfg.get('budget', 0),
-                     budget_chunk=cfg.get('chunk', 64 << 20))
+                     budget_chunk=cfg.get('chunk', 64 << 20), dir_impl=cfg.get('dir_impl', 'cpp'))
 
 
 def config(T, lo, hi, B, steps, C, n_static, D=128, seed=0, **kw):
@@ -87,6 +87,27 @@ def test_step_runs_on_cpu_with_oracle_backend():
     assert int(st.code.min()) >= 0 and int(st.code.max()) <= st.MAT
 
 
+def test_step_weights_do_not_depend_on_the_allocation_order():
+    """Log ids are storage addresses only (srm2/elara_kernels.py:5-7): the same batches planned in the default and in
+    the Triton directory's allocation order give bitwise the same weights and moments for every touched row, the
+    same codes, MAT slots and residency, while the log ids themselves differ."""
+    from elara_amd.step import run
+    cfg = config(T=5, lo=100, hi=3000, B=300, steps=30, C=700, n_static=400, kthr=2)
+    steps = {}
+    for impl in ('cpp', 'triton'):
+        st = make({**cfg, 'dir_impl': impl}, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
+        run(st, cfg['batches'], grads_fn(cfg, 'cpu'))
+        steps[impl] = st
+    a, b = steps['cpp'], steps['triton']
+    rows = torch.unique(torch.cat(cfg['batches']))
+    wa, wb = a.eval_weights(rows, full=True), b.eval_weights(rows, full=True)
+    assert torch.equal(wa.view(torch.int32), wb.view(torch.int32))
+    for name in ('code', 'loc', 'mat_top', 'live', 'slot_of', 'slot_row', 'adm_c0', 'rj', 'rok', 'pstep'):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    assert torch.equal(a.ent >= 0, b.ent >= 0) and not torch.equal(a.ent, b.ent)
+    assert a.stats == b.stats and a.stats['compactions'] and a.stats['ev']
+
+
 @pytest.mark.parametrize('where', ['cpu', pytest.param('gpu', marks=pytest.mark.gpu)])
 def test_step_raises_on_rows_out_of_range(where, request):
     """A batch row outside [0, R) is an error of the caller (undefined in the reference): the plan raises before it
@@ -105,14 +126,16 @@ def test_step_raises_on_rows_out_of_range(where, request):
 @pytest.mark.parametrize('name', ['small_evl', 'small_no_evl', 'small_S', 'small_overflow', 'host_arenas',
                                   'host_arenas_S', 'host_arenas_overflow', 'D64_K2', 'D256_K4', 'K1_kthr0',
                                   'L40_no_ring', 'D32_K8', 'D96', 'D200_K5_S', 'carry', 'carry_overflow_host',
-                                  'evl_gate'])
+                                  'evl_gate', 'triton', 'triton_host_S'])
 def test_gpu_step_matches_oracle_step(dev, name):
     """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
     kernels over the host link.  L40_no_ring: a look-ahead too long for the 32-bit ring of loaded batches, so the
     planner searches the next batches' sorted rows instead.  D32_K8, D96, D200_K5_S: widths the wave-per-row
     kernels do not take (the generic assembly and update kernels, srm2/gpu_ops.py:97 takes any D) and up to K = 8
     log entries per row.  carry*: carry residency (srm2/train.py:43 elara_carry); evl_gate: the representation
-    switched on by memory pressure part way through (the reference's default, srm2/train.py:128-130)."""
+    switched on by memory pressure part way through (the reference's default, srm2/train.py:128-130).  triton*: the
+    Triton directory's allocation order (srm2/elara_kernels.py), through the native step executor and, with host
+    arenas, through the call-by-call directory entry points."""
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
     kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
@@ -122,7 +145,8 @@ def test_gpu_step_matches_oracle_step(dev, name):
           'K1_kthr0': {'K': 1, 'kthr': 0}, 'L40_no_ring': {'L': 40}, 'D32_K8': {'D': 32, 'K': 8, 'kthr': 6},
           'D96': {'D': 96}, 'D200_K5_S': {'D': 200, 'K': 5, 'kthr': 4, 'st': 'S'}, 'carry': {'dyn': 'carry'},
           'carry_overflow_host': {'dyn': 'carry', 'C': 1800, 'host': True},
-          'evl_gate': {'evl': 2, 'budget': 14_000_000, 'chunk': 64 << 10}}[name]
+          'evl_gate': {'evl': 2, 'budget': 14_000_000, 'chunk': 64 << 10}, 'triton': {'dir_impl': 'triton'},
+          'triton_host_S': {'dir_impl': 'triton', 'host': True, 'st': 'S', 'kthr': 2}}[name]
     cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
     g = make(cfg, dev)
     assert (g.next_bits is None) == (name == 'L40_no_ring')
