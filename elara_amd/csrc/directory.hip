@@ -5,6 +5,9 @@
 //   call A:  replay inputs of L rows; resident-history recording of hits; eviction representation
 //            (back to L: log ids for the resident history, MAT trash slot; to M: MAT slot, release host logs)
 //   call B:  appends (stay L, one log id each), then compactions (to M: MAT slot, release all logs)
+// and, as elr_dir_a_deferred / elr_dir_evict_deferred / elr_dir_b_release, in the order of the reference's Triton
+// directory (srm2/elara_kernels.py), where every allocation of a step comes before any release: call A releases
+// nothing, and call B pushes the evictions' releases after its appends' pops, ahead of the compacted rows' logs.
 // Allocation ranks are exclusive prefix counts in row-major (item, k) order: the log allocator pops the free stack
 // top-down and then bumps log_top (elara_dir.cpp:13-21), MAT slots bump mat_top (elara_dir.cpp:36-44), releases
 // push onto the free stack at n_lfree + rank (elara_dir.cpp:23-34).
