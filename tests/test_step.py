@@ -218,16 +218,18 @@ def test_gpu_step_degenerate_batches(dev, name):
 
 
 @pytest.mark.gpu
-def test_gpu_step_c5_full_shape(dev):
+@pytest.mark.parametrize('dir_impl,steps', [('cpp', 200), ('triton', 100)])
+def test_gpu_step_c5_full_shape(dev, dir_impl, steps):
     """Config C5 shapes: 26 tables (vocab log-uniform in [1e3, 4e7], ~75M rows), batch 16,384 x 26 Zipf(1.1),
     D = 128, pool 337,626 (321,242 static hot rows), K = 3, evl on; 200 steps (the pool's steady-state churn and
     m / v of hot rows over many steps), HIP vs oracle bitwise: directory, pool, histories, arenas and the
     eval-style weights of every touched row.  Arena capacities as measured at this shape (about 47k log entries
-    and 7k MAT rows per step in steady state) with headroom; the plan's capacity check raises if they run out."""
+    and 7k MAT rows per step in steady state) with headroom; the plan's capacity check raises if they run out.
+    Also 100 steps in the Triton directory's allocation order."""
     from elara_amd.step import run
-    print('[gpu-test] elara step C5 full shape, 200 steps', flush=True)
-    steps = 200
-    cfg = config(T=26, lo=1e3, hi=4e7, B=16384, steps=steps, C=337_626, n_static=337_626 - 16_384)
+    print(f'[gpu-test] elara step C5 full shape, {steps} steps, {dir_impl} order', flush=True)
+    cfg = config(T=26, lo=1e3, hi=4e7, B=16384, steps=steps, C=337_626, n_static=337_626 - 16_384,
+                 dir_impl=dir_impl)
     cfg['log_cap'] = 2_000_000 + steps * 60_000
     cfg['mat_cap'] = 1_000_000 + steps * 12_000
     g = make(cfg, dev)
