@@ -578,7 +578,7 @@ def mode_c5(args):
     mat_cap = total * 20_000 + 1_000_000 if host else total * O // 2
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
                    seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=log_cap,
-                   mat_cap=mat_cap, device=dev, host_arenas=host)
+                   mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl)
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
     mark = {}
@@ -604,7 +604,7 @@ def mode_c5(args):
     return _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
                  {'workload': 'C5 full ELARA step, %s: 26 tables (R=%d), batch 16,384 x 26 '
                               'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, tabs.R),
-                  'arenas': 'host' if host else 'hbm', 'mat_top': mt, 'log_top': lt,
+                  'arenas': 'host' if host else 'hbm', 'dir_impl': args.dir_impl, 'mat_top': mt, 'log_top': lt,
                   'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
                   'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, None,
                  extra={'steps_per_s': steps / el, 'stats': s,
@@ -694,6 +694,8 @@ def main():
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
+    ap.add_argument('--dir-impl', default='cpp', choices=['cpp', 'ref', 'triton'],
+                    help="C5's directory allocation order (the reference's --elara-dir-impl; cpp and ref are equal)")
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
     ap.add_argument('--settle-ms', type=float, default=100.0,
                     help='headline: untimed steps before the warm-up, so the engine clock is steady')
