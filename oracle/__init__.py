@@ -31,4 +31,9 @@ How each function is pinned (checked against something other than itself; tests 
                      state and every output compared, over 60-step planner simulations in 5 configurations
                      (tests/dirsim.py); a hand-worked allocation sequence; invariants of srm2/train.py:474-477
                      (live == #valid entries, live + n_lfree == log_top)  [tests/test_directory.py]
+                     In the Triton path's order (rel_cnt / rel arguments, srm2/elara_kernels.py): == the
+                     reference's ELARAPlanner with dir_impl='triton' (its kernels in Triton's CPU interpreter),
+                     per step and final state, 5 configurations (tests/golden/planner_vectors.npz); a hand-worked
+                     step in both orders; equal to the default order in every state but the log ids
+                     [tests/test_planner_golden.py, tests/test_directory.py]
 """
