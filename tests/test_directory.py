@@ -354,3 +354,38 @@ def test_gpu_directory_empty_calls(dev):
     assert not diff_states(before, comparable_state(g.view(), sim))
     with pytest.raises(RuntimeError):
         dir_ext().elara_dir_a(g.st[:16], list(sim.pv), z, z, z.to(torch.int32), z, 3)
+
+
+@pytest.mark.gpu
+def test_gpu_facade_release_pushes_parts_in_the_order_given(dev):
+    """Directory.release(parts) pushes the parts' entries in the order of the list (srm2/elara_kernels.py:199-209),
+    whatever that order: with the compactions' part before the evictions' (the reverse of the planner's call), the
+    free stack, the counters and the later allocations equal the oracle's pushes in that order."""
+    import torch
+    print('[gpu-test] facade release order', flush=True)
+    sim = Sim(**CONFIGS['default'])
+    st0 = sim.initial_state()
+    o, f = OracleImpl(sim, st0, triton=True), FacadeImpl(sim, st0, dev)
+
+    def o_b(a_rows, a_k, c_rows, c_cnt, s):
+        a_ids, c_slots = O.dir_b(o.st, sim.pv, a_rows, a_k, c_rows, c_cnt, s, c_release=False)
+        O.dir_b(o.st, sim.pv, [], [], [], [], s, rel=(np.concatenate([c_rows, o.rel[0]]),
+                                                      np.concatenate([c_cnt, o.rel[1]])))
+        return [a_ids, c_slots]
+
+    def f_b(a_rows, a_k, c_rows, c_cnt, s):
+        c_rows_t, c_cnt_t = f.t(c_rows, torch.int64), f.t(c_cnt, torch.int64)
+        a_ids = f.dirk.appends(f.t(a_rows, torch.int64), f.t(a_k, torch.int64), int(s))
+        c_slots = f.dirk.compact(c_rows_t, c_cnt_t)
+        f.dirk.release([(c_rows_t, c_cnt_t), f.rel_ev])
+        return [a_ids.cpu().numpy(), c_slots.cpu().numpy()]
+
+    o.dir_b, f.dir_b = o_b, f_b
+    released = 0
+    for s in range(1, 41):
+        sim.step(s, [o, f])
+        d = diff_states(comparable_state(o.view(), sim), comparable_state(f.view(), sim))
+        assert not d, (s, d)
+        released += int(o.rel[1].sum())
+        check_invariants(o.view(), sim)
+    assert released > 0
