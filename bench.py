@@ -250,6 +250,132 @@ def cpu_sample_baseline(w, D, K, seed, bound, table_np, grad_np, step_t, pass_s=
     return res
 
 
+def _cpu_facts(res):
+    cpu = host_cpus()
+    res.update({'nproc': cpu['nproc'], 'host_cpu': cpu['model'], 'online_cpus': cpu['online_cpus'],
+                'affinity_cpus': cpu['affinity_cpus']})
+    return res
+
+
+def cpu_adam_baseline(D, table_rows, batches, grads, what, pass_s=2.5):
+    """Row-sparse Adam on this host (configs C1 and C4): the reference's own compiled cpu_adam (oracle/_ref, from
+    srm2/csrc/srm2_cpu.cpp:37-56) at nthreads = nproc, timed as the reference's test times it (one warm-up call,
+    then repeated passes; tests/test_ops.py:26-46), over a host table of table_rows rows and the given batches
+    (row ids into it, and their gradients) applied at steps 1, 2, ...  Rows per second and the same algorithmic
+    bytes per row as the GPU line; kind 'port' with the oracle's cpu_adam when the reference build is absent."""
+    import torch
+    from elara_amd import synth
+    from oracle import oracle as O
+    from oracle import ref as REF
+    th = host_cpus()['nproc']
+    E = REF.cpu()
+    lr, b1, b2, eps = synth.ADAM
+    table = torch.from_numpy(O.init_rows(np.arange(table_rows, dtype=np.int64), D, 0, synth.bound_for(D)))
+    table[:, 1:] = 0
+    rows = [torch.from_numpy(np.ascontiguousarray(b, np.int64)) for b in batches]
+    gs = [torch.from_numpy(np.ascontiguousarray(g, np.float32)) for g in grads]
+    n_rows = sum(r.numel() for r in rows)
+    if E is not None:
+        def once():
+            for t, (r, g) in enumerate(zip(rows, gs), start=1):
+                E.cpu_adam(table, r, g, lr, b1, b2, eps, t, th)
+    else:
+        tn = table.numpy()
+        scs = [O.adam_scalars(*synth.ADAM, t) for t in range(1, len(rows) + 1)]
+
+        def once():
+            for r, g, sc in zip(rows, gs, scs):
+                O.cpu_adam(tn, r.numpy(), g.numpy(), sc, th)
+    rate, reps = _timed_passes(once, n_rows, pass_s)
+    return _cpu_facts({'value': rate, 'unit': 'rows/s', 'cores': th, 'kind': 'reference' if E is not None else 'port',
+                       'sample': f'{what}: {len(rows)} steps of {rows[0].numel()} rows each on a host table of '
+                                 f'{table_rows} x {D} (w, m, v), the '
+                                 + ('reference cpu_adam (oracle/_ref, built from srm2/csrc/srm2_cpu.cpp)'
+                                    if E is not None else 'oracle cpu_adam') +
+                                 f', {th} threads (nproc); repeated {reps}x per pass, median of 3 passes after 1 '
+                                 f'warm-up',
+                       'gbs': rate * adam_bytes(1, D) / 1e9})
+
+
+def cpu_c3_baseline(ids, g, D, pass_s=2.5):
+    """Config C3 on this host, one step of the workload (3,407,872 occurrences): the oracle's sort and segment sum
+    in ATen's order (orc_segment_sum), run on nproc threads over a split of the ids by id mod nproc (an id's sum
+    depends only on its own occurrences in position order, so the split gives the same sums; done before timing),
+    then the reference's compiled cpu_adam (oracle/_ref) at nthreads = nproc on a host table holding the step's
+    unique rows.  Occurrences per second, as the GPU line."""
+    import torch
+    from concurrent.futures import ThreadPoolExecutor
+    from elara_amd import synth
+    from oracle import oracle as O
+    from oracle import ref as REF
+    th = host_cpus()['nproc']
+    E = REF.cpu()
+    lr, b1, b2, eps = synth.ADAM
+    part = ids % th
+    parts = [(np.ascontiguousarray(ids[part == q]), np.ascontiguousarray(g[part == q])) for q in range(th)]
+    u_all = np.unique(ids)
+    table = torch.from_numpy(O.init_rows(u_all, D, 0, synth.bound_for(D)))
+    table[:, 1:] = 0
+    pool = ThreadPoolExecutor(th)
+
+    def once():
+        res = list(pool.map(lambda pg: O.segment_sum(*pg)[:2], parts))
+        u = np.concatenate([r[0] for r in res])
+        s = np.concatenate([r[1] for r in res])
+        rows = torch.from_numpy(np.searchsorted(u_all, u).astype(np.int64))
+        if E is not None:
+            E.cpu_adam(table, rows, torch.from_numpy(s), lr, b1, b2, eps, 1, th)
+        else:
+            O.cpu_adam(table.numpy(), rows.numpy(), s, O.adam_scalars(*synth.ADAM, 1), th)
+    try:
+        rate, reps = _timed_passes(once, ids.size, pass_s)
+    finally:
+        pool.shutdown()
+    U = u_all.size
+    per_occ = (ids.size * (4 * D + 8) + U * (28 * D + 8)) / ids.size
+    return _cpu_facts({'value': rate, 'unit': 'occurrences/s', 'cores': th,
+                       'kind': 'reference' if E is not None else 'port',
+                       'sample': f'one C3 step ({ids.size} occurrences, {U} unique rows): the oracle\'s sort and '
+                                 f'ATen-order segment sum on {th} threads (ids split by id mod {th} before timing), '
+                                 f'then the ' + ('reference cpu_adam (oracle/_ref)' if E is not None else
+                                                 'oracle cpu_adam') +
+                                 f' at {th} threads on a host table of the step\'s unique rows; repeated {reps}x per '
+                                 f'pass, median of 3 passes after 1 warm-up',
+                       'unique_rows_per_s': rate * U / ids.size, 'gbs': rate * per_occ / 1e9})
+
+
+def cpu_c5_baseline(tabs, static, batches_host, grads_host, C, D, steps=20, warmup=10):
+    """Config C5 on this host: the same ElaraStep driven by the oracle's kernels (oracle/backend.py: the CPU
+    restatement of every kernel, on CPU tensors, nthreads = nproc) -- the reference has no CPU implementation of
+    its GPU step, so this is a port.  `warmup` untimed steps (the pool fills), then `steps` timed ones; arenas
+    sized for that many steps.  Unique rows per second, as the GPU line."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.step import ElaraStep, run
+    from oracle.backend import OracleBackend
+    th = host_cpus()['nproc']
+    total = warmup + steps
+    be = OracleBackend(D, 42, synth.bound_for(D), synth.ADAM, total + 2, nthreads=th)
+    st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
+                   seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2,
+                   log_cap=2_000_000 + total * 60_000, mat_cap=1_000_000 + total * 12_000, device='cpu', backend=be)
+    mark = {}
+
+    def on_step(s, p):
+        if s == warmup:
+            mark['t0'] = time.perf_counter()
+            mark['stats'] = dict(st.stats)
+    run(st, batches_host[:total], lambda j: grads_host[j % len(grads_host)], on_step=on_step)
+    el = time.perf_counter() - mark['t0']
+    d = {k: v - mark['stats'][k] for k, v in st.stats.items()}
+    uniq = d['hits'] + d['N'] + d['L'] + d['F'] + d['S']
+    return _cpu_facts({'value': uniq / el, 'unit': 'rows/s', 'cores': th, 'kind': 'port',
+                       'sample': f'the first {total} C5 batches through ElaraStep on CPU tensors with the oracle\'s '
+                                 f'kernels (oracle/backend.py, {th} threads): {warmup} untimed steps, then {steps} '
+                                 f'timed; the same tables, static rows and batches as the GPU run',
+                       'ms_per_step': el / steps * 1e3})
+
+
 def headline(args):
     import torch
     from elara_amd import synth
@@ -316,7 +442,11 @@ def headline(args):
                      'median_launch_ms': float(np.median(rep_all)), 'launches_timed': len(rep_all)},
         'kernels': {'replay': {'ms': rep_ms, 'GBps': rep_gbs, 'bytes': rb, 'ms_first': rep_all[0]},
                     'adam': {'ms': adam_ms, 'GBps': ab / (adam_ms * 1e-3) / 1e9, 'bytes': ab,
-                             'frac': ab / (adam_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}},
+                             'frac': ab / (adam_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                             'note': 'partly cache-served: its 262,144 rows (403 MB) were written by the replay '
+                                     'launch just before, and the 256 MB Infinity Cache can return part of them; '
+                                     'on rows not written just before the same kernel reaches 0.61 (random rows '
+                                     'of a 15 GB table) to 0.76 (C4)'}},
         'step_GBps': (rb + ab) / (elapsed / args.steps) / 1e9,
         'clock_settle': settle,
     }
@@ -349,16 +479,21 @@ def _settle(launch, settle_s, what):
 
 def _traffic(kernel, profile='replay_adam_c2_d128_traffic.md'):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE, each
-    scaled by the same counter's reading for a copy kernel of known size), or None if absent."""
+    scaled by the same counter's reading for a copy kernel of known size), or None if absent or stale: the summary
+    records the source hash of the library it measured (elara_amd.build.source_hash), and a figure taken on other
+    kernel code than this build's is not reported."""
+    from elara_amd.build import source_hash
     p = ROOT / 'profiles' / profile
     if not p.exists():
         return None
-    cur = None
+    cur, stamp, want = None, None, source_hash()
     for line in p.read_text().splitlines():
         if line.startswith('kernel: '):
-            cur = line[len('kernel: '):].strip()
+            cur, stamp = line[len('kernel: '):].strip(), None
+        elif line.startswith('source_hash = '):
+            stamp = line.split('=', 1)[1].strip()
         elif line.startswith('bytes_per_launch = ') and cur and cur in kernel:
-            return int(float(line.split('=', 1)[1]))
+            return int(float(line.split('=', 1)[1])) if stamp == want else None
     return None
 
 
@@ -436,10 +571,14 @@ def mode_c1(args):
     steps = 100
     el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 10], *synth.ADAM, i % 10 + 1),
                                   steps, 10, SETTLE_S, every=10)
-    return _line('C1 row-sparse Adam rows/s (d=64)', n * steps / el, 'rows/s', args, steps, warmup, el,
-                 {'workload': 'C1 row-sparse Adam: 1,048,576 x 64 fp32 table, 65,536 unique rows per step',
-                  'rows_per_step': n, 'dim': D}, adam_bytes(n, D) / 1e9,
-                 extra={'mean_launch_ms': float(np.mean(ms))})
+    res = _line('C1 row-sparse Adam rows/s (d=64)', n * steps / el, 'rows/s', args, steps, warmup, el,
+                {'workload': 'C1 row-sparse Adam: 1,048,576 x 64 fp32 table, 65,536 unique rows per step',
+                 'rows_per_step': n, 'dim': D}, adam_bytes(n, D) / 1e9,
+                extra={'mean_launch_ms': float(np.mean(ms))})
+    if not args.no_cpu:
+        res['cpu_baseline'] = cpu_adam_baseline(D, R, [x.cpu().numpy() for x in ids], [g.cpu().numpy() for g in gs],
+                                                'the C1 workload itself (t = 1..10)')
+    return res
 
 
 def mode_c3(args):
@@ -492,13 +631,26 @@ def mode_c3(args):
     O = B * F
     Umean = float(np.mean(U))
     byts = (O * (4 * D + 8) + Umean * (28 * D + 8)) / 1e9
-    return _line('C3 duplicate-id sparse Adam occurrences/s (d=128)', O * steps / el, 'occurrences/s', args, steps,
-                 warmup, el, {'workload': 'C3 duplicate-id Adam: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) '
-                                          'ids per step, dedup + segment sum in ATen order + Adam',
-                              'dedup': 'one call per step' if args.c3_serial else 'sorted one step ahead on a '
-                                                                                  'second stream',
-                              'occurrences_per_step': O, 'unique_rows_per_step': Umean, 'dim': D}, byts,
-                 extra={'unique_rows_per_s': Umean * steps / el, 'mean_step_ms_events': float(np.mean(ms))})
+    res = _line('C3 duplicate-id sparse Adam occurrences/s (d=128)', O * steps / el, 'occurrences/s', args, steps,
+                warmup, el, {'workload': 'C3 duplicate-id Adam: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) '
+                                         'ids per step, dedup + segment sum in ATen order + Adam',
+                             'dedup': 'one call per step' if args.c3_serial else 'sorted one step ahead on a '
+                                                                                 'second stream',
+                             'occurrences_per_step': O, 'unique_rows_per_step': Umean, 'dim': D}, byts,
+                extra={'unique_rows_per_s': Umean * steps / el, 'mean_step_ms_events': float(np.mean(ms))})
+    if not args.c3_serial:
+        # the one-call form (sort, sum and Adam of a step in one call, as the reference sorts per step) on the same
+        # table and batches, right after: its figures beside the main ones
+        el1, ms1, w1 = _timed_steps(lambda i: adam_dedup(table, ids[i % 4], gs[i % 4], *synth.ADAM, steps + i + 1),
+                                    steps, 4, SETTLE_S)
+        res['serial'] = {'dedup': 'one call per step (elr_adam_dedup)', 'ms_per_step': el1 / steps * 1e3,
+                         'value': O * steps / el1, 'step_GBps': byts * steps / el1,
+                         'step_frac_of_hbm_peak': byts * steps / el1 / HBM_PEAK_GBS}
+    if not args.no_cpu:
+        del table
+        torch.cuda.empty_cache()
+        res['cpu_baseline'] = cpu_c3_baseline(host[0], gs[0].cpu().numpy(), D)
+    return res
 
 
 def mode_rows(args):
@@ -547,11 +699,22 @@ def mode_c4(args):
     steps = 50
     el, ms, warmup = _timed_steps(lambda i: gpu_adam(table, ids[i % 10], gs[i % 4], *synth.ADAM, i + 1), steps, 10,
                                   SETTLE_S, every=5)
-    return _line('C4 large-row sparse Adam rows/s (d=256, 153.6 GB table)', n * steps / el, 'rows/s', args, steps,
-                 warmup, el, {'workload': 'C4 large-row stress: 50,000,000 x 256 fp32 table (w, m, v: 153.6 GB in '
-                                          'HBM), 262,144 unique Zipf(1.1) rows per step', 'rows_per_step': n,
-                              'dim': D}, adam_bytes(n, D) / 1e9,
-                 extra={'mean_launch_ms': float(np.mean(ms))})
+    res = _line('C4 large-row sparse Adam rows/s (d=256, 153.6 GB table)', n * steps / el, 'rows/s', args, steps,
+                warmup, el, {'workload': 'C4 large-row stress: 50,000,000 x 256 fp32 table (w, m, v: 153.6 GB in '
+                                         'HBM), 262,144 unique Zipf(1.1) rows per step', 'rows_per_step': n,
+                             'dim': D}, adam_bytes(n, D) / 1e9,
+                extra={'mean_launch_ms': float(np.mean(ms))})
+    if not args.no_cpu:
+        # the touched-row compact copy (the 153.6 GB table does not fit host memory): the first batch's rows as a
+        # host table of n rows, each batch's ids mapped into it, four steps (the GPU line's four gradient buffers)
+        del table
+        torch.cuda.empty_cache()
+        b0 = ids[0].cpu().numpy()
+        order = np.argsort(b0)
+        res['cpu_baseline'] = cpu_adam_baseline(
+            D, n, [np.argsort(order).astype(np.int64)] * 4, [g.cpu().numpy() for g in gs],
+            'the touched-row compact copy of one C4 batch (262,144 rows in Zipf first-appearance order)')
+    return res
 
 
 def mode_c5(args):
@@ -601,7 +764,7 @@ def mode_c5(args):
     uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
     mt, lt = (int(x) for x in (st.mat_top, st.log_top))
     where = 'pinned host arenas (capacity tier)' if host else 'HBM-resident arenas'
-    return _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
+    res = _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
                  {'workload': 'C5 full ELARA step, %s: 26 tables (R=%d), batch 16,384 x 26 '
                               'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, tabs.R),
                   'arenas': 'host' if host else 'hbm', 'dir_impl': args.dir_impl, 'mat_top': mt, 'log_top': lt,
@@ -612,6 +775,12 @@ def mode_c5(args):
                         'note': 'step_GBps not reported for C5 (mixed kernels; per-kernel bytes in profiles/); '
                                 'host_wait_us_per_step: time the host spends waiting for the GPU at the plan\'s '
                                 'synchronisation (near 0: the host is the bottleneck)'})
+    res['dir_check'] = st.dir_check()
+    if not args.no_cpu:
+        ncpu = min(total, 30)
+        res['cpu_baseline'] = cpu_c5_baseline(tabs, static, [b.cpu() for b in batches[:ncpu]], [g.cpu() for g in gs],
+                                              C, D, steps=ncpu - 10, warmup=10)
+    return res
 
 
 def copy_calibration(args):

@@ -28,6 +28,7 @@ SIGNATURES = {
     'elr_version': (ctypes.c_int, []),
     'elr_host_device_ptr': (ctypes.c_int, [c_vp, ctypes.POINTER(c_vp)]),
     'elr_adam_scalars': (None, [c_f64, c_f64, c_f64, c_f64, c_i64, c_f32p]),
+    'elr_cpu_adam': (ctypes.c_int, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i64, c_f32p, ctypes.c_int]),
     'elr_scalar_table': (ctypes.c_int, [c_f64, c_f64, c_f64, c_f64, c_i64, c_vp]),
     'elr_adam_rows': (ctypes.c_int, [c_vp, c_i64, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_f32p, c_vp]),
     'elr_adam_rows_timed': (ctypes.c_int, [c_vp, c_i64, c_vp, ctypes.c_int, c_vp, c_i64, c_i64, c_f32p, c_vp, c_vp,

@@ -27,6 +27,18 @@ def sources():
     return sorted(CSRC.glob('*.hip'))
 
 
+def source_hash():
+    """16 hex digits identifying the library's kernel code: SHA-256 over the compile flags, the C header and every
+    kernel source and device header (by name and contents).  Profile summaries record it, so that a figure measured
+    on other kernels can be recognised as stale."""
+    import hashlib
+    h = hashlib.sha256(' '.join(CFLAGS[:-1]).encode())
+    for f in [HERE.parent / 'include' / 'elara_amd.h', *sorted(CSRC.glob('*.hip')), *sorted(CSRC.glob('*.h'))]:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def _compile(src, obj):
     cmd = [HIPCC, *CFLAGS, '-c', str(src), '-o', str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)

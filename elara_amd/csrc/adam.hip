@@ -67,9 +67,7 @@ __global__ __launch_bounds__(256) void k_adam_rows_scalar(float* __restrict__ st
 // Wave-per-row variant for D = 64*VPL: the slot of each row is a wave-uniform (scalar) load; the U rows of a wave
 // issue all their w, m, v, g loads before the first update.  No loop (see init_replay.hip): one row group per
 // wave, large calls split into several launches on the host.
-#ifndef ELR_ADAM_U
-#define ELR_ADAM_U 1
-#endif
+constexpr int kAdamRowsPerWave = 1;
 
 template <int VPL, typename Idx, int U>
 __global__ __launch_bounds__(256) void k_adam_rows_wpr(float* __restrict__ state, int64_t C,
@@ -107,7 +105,7 @@ __global__ __launch_bounds__(256) void k_adam_rows_wpr(float* __restrict__ state
 template <int VPL, typename Idx>
 static void launch_adam_wpr(float* state, int64_t C, const Idx* slots, const float* grad, int64_t n,
                             const AdamScalars& s, hipStream_t st, hipEvent_t e0, hipEvent_t e1) {
-  constexpr int U = ELR_ADAM_U;
+  constexpr int U = kAdamRowsPerWave;
   constexpr int64_t D = 64 * VPL;
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {

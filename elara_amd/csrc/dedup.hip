@@ -481,10 +481,7 @@ __global__ __launch_bounds__(256) void k_seg_final(const float* __restrict__ gra
 // All per-segment metadata (bounds, row id, first occurrence) are scalar loads issued together, then the first
 // gradient row, the row's w, m, v (MODE 1) and the next 63 occurrence indices load in parallel: a one-occurrence
 // segment -- the common case -- costs two dependent memory round trips.
-#ifndef ELR_SEG_SW
-#define ELR_SEG_SW 2
-#endif
-constexpr int kSegPerWave = ELR_SEG_SW;
+constexpr int kSegPerWave = 2;
 
 // The result of one segment: written to out[row] (MODE 0) or applied as an Adam step to state row `row` (MODE 1).
 template <int VPL, int MODE>
@@ -607,11 +604,7 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
   int32_t my[SW];
   // short: every segment of the wave fits one run of at most FB occurrences (wave-uniform: the lengths are scalar
   // loads).  Their remaining rows then load together, all segments' at once, before any addition.
-#ifdef ELR_SEG_FB
-  constexpr int FB = ELR_SEG_FB;
-#else
   constexpr int FB = VPL <= 2 ? kAtenGroup : 4;
-#endif
   bool short_segs = true;
 #pragma unroll
   for (int q = 0; q < SW; ++q) {
@@ -1103,13 +1096,20 @@ std::mutex g_noalloc_mu;
 
 static __device__ __align__(256) unsigned char scratch[ELR_NOALLOC_SCRATCH_BYTES];
 
-// Device address of `scratch` on the current device (resolved on the first call per device).
-static int noalloc_scratch(void** out) {
+// Device address of `scratch` on the current device (resolved on the first call per device).  A stream of another
+// device is refused (ELR_EINVAL): its kernels would be handed this device's address.
+static int noalloc_scratch(void** out, hipStream_t stream) {
   using namespace elr;
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kNoAllocMaxDevices) return ELR_EUNSUPPORTED;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return (int)e;
+    if ((int)sdev != dev) return ELR_EINVAL;
+  }
   void* p = g_noalloc_ptr[dev].load(std::memory_order_acquire);
   if (!p) {
     std::lock_guard<std::mutex> g(g_noalloc_mu);
@@ -1134,7 +1134,7 @@ extern "C" int elr_adam_dedup_noalloc(float* state, int64_t C, const int64_t* id
   if (D > 512) return ELR_EUNSUPPORTED;
   if (dedup_scratch_bytes(n, D, nullptr, nullptr) > (int64_t)ELR_NOALLOC_SCRATCH_BYTES) return ELR_ECAPACITY;
   void* base = nullptr;
-  const int rc = noalloc_scratch(&base);
+  const int rc = noalloc_scratch(&base, static_cast<hipStream_t>(stream));
   if (rc != ELR_OK) return rc;
   return elr_adam_dedup(state, C, ids, grad, n, D, sc, base, (int64_t)ELR_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -8,11 +8,10 @@
 #include "elr_launch.h"
 #include "elr_rowio.h"
 
-#ifndef ELR_EXEC_U
-#define ELR_EXEC_U 2   // rows per wave in flight
-#endif
 
 namespace elr {
+
+constexpr int kExecRowsPerWave = 2;   // rows per wave in flight
 
 // One part of an Adam launch of the executor with the row moves fused in.  Row i < n reads gradient row
 // g_base + i; with i < n_rec it stores that gradient into entry rec_j[i] (0 when rec_j is NULL) of resident-history
@@ -168,7 +167,7 @@ __device__ inline void AdamExecGen::operator()(int64_t blk, int64_t) const {
 // The parts with rows of one launch, each part on at most max_blocks blocks; false when there are more than
 // kExecParts of them.
 inline bool exec_multi(std::initializer_list<ExecAdam> parts, int64_t max_blocks, ExecMulti& x, int64_t& blocks) {
-  constexpr int U = ELR_EXEC_U;
+  constexpr int U = kExecRowsPerWave;
   x = ExecMulti{};
   int q = 0;
   blocks = 0;
@@ -188,7 +187,7 @@ inline bool exec_multi(std::initializer_list<ExecAdam> parts, int64_t max_blocks
 // The Adam functor for vpl (0: the generic one for D), passed to visit(functor, blocks).
 template <class Visit>
 inline void exec_visit(int vpl, int64_t D, const ExecMulti& x, int64_t blocks, const AdamScalars& s, Visit&& visit) {
-  constexpr int U = ELR_EXEC_U;
+  constexpr int U = kExecRowsPerWave;
   switch (vpl) {
     case 0: visit(AdamExecGen{x, s, D}, blocks); break;
     case 1: visit(AdamExec<1, U>{x, s}, blocks); break;

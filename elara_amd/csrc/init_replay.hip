@@ -155,12 +155,8 @@ __global__ __launch_bounds__(256) void k_replay_scalar(float* __restrict__ out, 
 }
 
 // ---- wave-per-row kernels (D = 64*VPL) ------------------------------------------------------------------------------
-#ifndef ELR_REPLAY_U
-#define ELR_REPLAY_U 2
-#endif
-#ifndef ELR_INIT_U
-#define ELR_INIT_U 2
-#endif
+constexpr int kReplayRowsPerWave = 2;
+constexpr int kInitRowsPerWave = 2;
 
 template <int VPL, int U>
 __global__ __launch_bounds__(256) void k_init_rows_wpr(float* __restrict__ out, const int64_t* __restrict__ rows,
@@ -257,7 +253,7 @@ static void launch_replay_wpr(float* out, const int64_t* rows, const float* logs
                               const int32_t* steps, const int32_t* cnt, int64_t n, uint32_t seed, float bound,
                               const float* table, const double* recip, int64_t table_rows, hipStream_t st,
                               hipEvent_t e0, hipEvent_t e1) {
-  constexpr int U = ELR_REPLAY_U;
+  constexpr int U = kReplayRowsPerWave;
   constexpr int64_t D = 64 * VPL;
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {
@@ -270,7 +266,7 @@ static void launch_replay_wpr(float* out, const int64_t* rows, const float* logs
 
 template <int VPL>
 static void launch_init_wpr(float* out, const int64_t* rows, int64_t n, uint32_t seed, float bound, hipStream_t st) {
-  constexpr int U = ELR_INIT_U;
+  constexpr int U = kInitRowsPerWave;
   constexpr int64_t D = 64 * VPL;
   constexpr int64_t per = wpr_rows_per_launch(U);
   for (int64_t a = 0; a < n; a += per) {

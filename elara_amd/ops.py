@@ -2,6 +2,8 @@
 
     gpu_adam(pool, slots, grad, lr, b1, b2, eps, step)       srm2/ops.py:59-67
     ext().adam_scalars(lr, b1, b2, eps, step) -> [8 floats]  srm2/csrc/srm2_cpu.cpp:255-257
+    ext().cpu_adam(state, rows, grad, lr, b1, b2, eps, step, nthreads)
+                                                             srm2/csrc/srm2_cpu.cpp:37-56 (host tensors)
     dir_ext().elara_dir_a / elara_dir_b                      srm2/ops.py:32-39 (defined in elara_amd.elara_dir)
 
 The update runs in the HIP kernel behind elr_adam_rows (elara_amd/csrc/adam.hip) on torch's current stream;
@@ -35,17 +37,36 @@ def _scalars8(lr, b1, b2, eps, step):
     return out
 
 
+def cpu_adam(state, rows, grad, lr, b1, b2, eps, step, nthreads=1):
+    """Row-sparse Adam on host tensors (srm2/csrc/srm2_cpu.cpp:37-56, ext().cpu_adam): state [R,3,D] float32 CPU
+    (updated in place), rows int64 [n], grad float32 [n,D], on nthreads host threads (elr_cpu_adam).  Non-contiguous
+    or non-CPU inputs raise RuntimeError, as the reference's TORCH_CHECK does."""
+    if not (state.device.type == 'cpu' and rows.device.type == 'cpu' and grad.device.type == 'cpu'):
+        raise RuntimeError('cpu_adam: state, rows and grad must be CPU tensors')
+    if not (state.is_contiguous() and grad.is_contiguous() and rows.is_contiguous()):
+        raise RuntimeError('cpu_adam: state, rows and grad must be contiguous')
+    if state.dtype != torch.float32 or grad.dtype != torch.float32 or rows.dtype != torch.int64 or state.dim() != 3:
+        raise RuntimeError('cpu_adam: expected float32 state [R,3,D], int64 rows and float32 grad')
+    n, D = rows.numel(), state.shape[2]
+    if grad.numel() != n * D:
+        raise RuntimeError(f'cpu_adam: grad must hold {n}x{D} elements')
+    rc = _lib.lib().elr_cpu_adam(_lib.ptr(state), state.shape[0], _lib.ptr(rows), _lib.ptr(grad), n, D,
+                                 _scalars8(lr, b1, b2, eps, step), int(nthreads))
+    _lib.check(rc, 'elr_cpu_adam')
+
+
 class _Ext:
     """Mirror of the reference's `ext()` module for the functions on this path."""
 
     adam_scalars = staticmethod(adam_scalars)
+    cpu_adam = staticmethod(cpu_adam)
 
 
 _ext = _Ext()
 
 
 def ext():
-    """Counterpart of srm2/ops.py:19-26 ext(): the native helpers (here: adam_scalars)."""
+    """Counterpart of srm2/ops.py:19-26 ext(): the native helpers (here: adam_scalars and cpu_adam)."""
     _lib.lib()
     return _ext
 

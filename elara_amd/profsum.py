@@ -129,6 +129,8 @@ def cmd_traffic(a):
     rd = f_kib * 1024.0 * f_scale
     wr = w_kib * 1024.0 * w_scale
     print(f'kernel: {a.kernel}')
+    from elara_amd.build import source_hash
+    print(f'source_hash = {source_hash()}')
     print(f'FETCH_SIZE_KiB_per_dispatch = {f_kib:.2f}')
     print(f'WRITE_SIZE_KiB_per_dispatch = {w_kib:.2f}')
     print(f'copy_bytes = {a.copy_bytes}')

@@ -724,6 +724,17 @@ class ElaraStep:
         """Bytes the budget accounting holds (ArenaStore.resident_bytes, srm2/elara.py:60-61)."""
         return self.faulted['mat'] * 12 * self.D + self.faulted['log'] * 4 * self.D
 
+    def dir_check(self):
+        """The directory's consistency check that the reference records at the end of every ELARA run
+        (srm2/train.py:474-477): the live log entries equal the valid entry ids, and live entries plus the free
+        stack's depth equal the log arena's top.  One host synchronisation (not counted in stats['syncs'])."""
+        self.join_link()
+        valid = (self.ent[:self.R * self.K] >= 0).sum()
+        live, nf, top, mt, ev = torch.stack([t.reshape(()).to(I64) for t in (
+            self.live, self.n_lfree, self.log_top, self.mat_top, valid)]).tolist()
+        return {'live': live, 'ent_valid': ev, 'n_free': nf, 'log_top': top, 'mat_top': mt,
+                'ok': live == ev and live + nf == top}
+
     def footprint(self):
         """The arenas' footprint as the reference reports it (ArenaStore.footprint, srm2/elara.py:95-103); one
         host synchronisation."""

@@ -80,6 +80,15 @@ int elr_adam_rows(float* state, int64_t C, const void* slots, int idx64, const f
 int elr_adam_rows_timed(float* state, int64_t C, const void* slots, int idx64, const float* grad, int64_t n,
                         int64_t D, const float sc[8], void* start_event, void* stop_event, void* stream);
 
+/* Row-sparse Adam on the host (no GPU involved), for rows held in host memory.
+ * Replaces: srm2/csrc/srm2_cpu.cpp:37-56 cpu_adam (bound as ext().cpu_adam, srm2_cpu.cpp:249; called by the host
+ * update worker, srm2/elara.py:567, and srm2/store.py:67, 181).  Same arithmetic and order as elr_adam_rows, on
+ * nthreads host threads over contiguous ranges of `rows` (one thread below 256 rows).  All pointers host memory:
+ *   state fp32 [R,3,D]; rows int64 [n] (unique within a call; rows outside [0, R) are skipped); grad fp32 [n,D];
+ *   sc from elr_adam_scalars.  Blocks until done. */
+int elr_cpu_adam(float* state, int64_t R, const int64_t* rows, const float* grad, int64_t n, int64_t D,
+                 const float sc[8], int nthreads);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Counter-hash initial state.
  * Replaces: srm2/gpu_ops.py:41-48 init_rows / _init_rows (hash gpu_ops.py:15-23).  out[i] = (w0(rows[i]), 0, 0)
@@ -240,7 +249,7 @@ int elr_adam_dedup(float* state, int64_t C, const int64_t* ids, const float* gra
  * elr_dedup_scratch_bytes(n, D) > ELR_NOALLOC_SCRATCH_BYTES return ELR_ECAPACITY before any launch (at D = 128:
  * n up to about 558,000 occurrences).  No hipMalloc / hipFree or allocating library call is made.  Every call on
  * one GPU uses that GPU's array: calls that overlap in time on one GPU (two streams or threads) race.  The device
- * is the current one (hipGetDevice); `stream` must belong to it. */
+ * is the current one (hipGetDevice); a `stream` of another device returns ELR_EINVAL before any launch. */
 #define ELR_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int elr_adam_dedup_noalloc(float* state, int64_t C, const int64_t* ids, const float* grad, int64_t n, int64_t D,
                            const float sc[8], void* stream);

@@ -200,23 +200,32 @@ int orc_replay_rows(float* out, const int64_t* rows, const float* logs, int64_t 
 #define ORC_ATEN_WINDOW 16
 #define ORC_ATEN_NROWS 10
 
-static const int64_t* g_sort_ids;
+/* Occurrences sorted by (id, position): a stable sort by id.  The pairs carry their own key, so the comparator
+ * reads no global and concurrent calls are safe. */
+typedef struct orc_occ {
+  int64_t id, pos;
+} orc_occ;
 static int cmp_occ(const void* a, const void* b) {
-  int64_t i = *(const int64_t*)a, j = *(const int64_t*)b;
-  int64_t x = g_sort_ids[i], y = g_sort_ids[j];
-  if (x != y) return x < y ? -1 : 1;
-  return i < j ? -1 : (i > j);
+  const orc_occ* p = (const orc_occ*)a;
+  const orc_occ* q = (const orc_occ*)b;
+  if (p->id != q->id) return p->id < q->id ? -1 : 1;
+  return p->pos < q->pos ? -1 : (p->pos > q->pos);
 }
 
 int64_t orc_segment_sum(const int64_t* ids, const float* grad, int64_t nocc, int64_t D, int64_t* uniq,
                         float* gsum, int64_t* inverse) {
+  orc_occ* occ = (orc_occ*)malloc(sizeof(orc_occ) * (size_t)(nocc > 0 ? nocc : 1));
   int64_t* ord = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nocc > 0 ? nocc : 1));
   int64_t* inv = (int64_t*)malloc(sizeof(int64_t) * (size_t)(nocc > 0 ? nocc : 1));
   float* part = (float*)malloc(sizeof(float) * (size_t)(D > 0 ? D : 1));
   float* tot = (float*)malloc(sizeof(float) * (size_t)(D > 0 ? D : 1));
-  for (int64_t i = 0; i < nocc; ++i) ord[i] = i;
-  g_sort_ids = ids;
-  qsort(ord, (size_t)nocc, sizeof(int64_t), cmp_occ);   /* ties by position: a stable sort */
+  for (int64_t i = 0; i < nocc; ++i) {
+    occ[i].id = ids[i];
+    occ[i].pos = i;
+  }
+  qsort(occ, (size_t)nocc, sizeof(orc_occ), cmp_occ);   /* ties by position: a stable sort */
+  for (int64_t i = 0; i < nocc; ++i) ord[i] = occ[i].pos;
+  free(occ);
   int64_t U = 0;
   for (int64_t q0 = 0; q0 < nocc;) {
     int64_t q1 = q0 + 1;

@@ -186,6 +186,28 @@ def dir_a(st, pv, hs, L_row, L_cnt, ev_slot, s, deferred=False):
     return out + [rel_cnt] if deferred else out
 
 
+def _check_counted_entries(st, pv, rows, cnt):
+    """The Triton path's release (srm2/elara_kernels.py:104-116, 199-209) reserves stack positions from the
+    requested counts and adds their total to n_lfree, skipping entries that are -1; this build (the HIP kernels and
+    orc_dir_b) pushes the live entries packed and counts those.  The two agree exactly when every counted entry
+    exists (the reference's comment at elara_kernels.py:208 states it holds by construction): asserted here for
+    every release of the Triton order, so that a break shows as a failure instead of silently different ids."""
+    R, K = int(pv[0]), int(pv[1])
+    rows = np.asarray(rows, np.int64)
+    cnt = np.minimum(np.maximum(np.asarray(cnt, np.int64), 0), K)
+    ok = (rows >= 0) & (rows < R)
+    rows, cnt = rows[ok], cnt[ok]
+    if not rows.size:
+        return
+    kk = np.arange(K, dtype=np.int64)
+    e = st.ent[rows[:, None] * K + kk[None, :]]
+    missing = (kk[None, :] < cnt[:, None]) & (e < 0)
+    if missing.any():
+        i = int(np.flatnonzero(missing.any(axis=1))[0])
+        raise AssertionError(f'Triton-order release of row {int(rows[i])}: {int(cnt[i])} entries counted, '
+                             f'{int((e[i] >= 0).sum())} live')
+
+
 def dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=None, c_release=True):
     """Oracle of elara_dir_b (srm2/csrc/elara_dir.cpp:98-110); mutates st.  Returns (a_ids, c_slots).
     rel = (rows, counts): releases pushed after the appends, ahead of the compacted rows' (which are released only
@@ -197,6 +219,8 @@ def dir_b(st, pv, a_rows, a_k, c_rows, c_cnt, s, rel=None, c_release=True):
         (np.ascontiguousarray(rel[0], np.int64), np.ascontiguousarray(rel[1], np.int64))
     if r_rows.size != r_cnt.size:
         raise ValueError('rel rows and counts must have the same length')
+    if rel is not None:
+        _check_counted_entries(st, pv, np.concatenate([r_rows, c_rows]), np.concatenate([r_cnt, c_cnt]))
     d = st._c(); p = _Params(*pv)
     lib().orc_dir_b(ctypes.byref(d), ctypes.byref(p), _p(a_rows), _p(a_k), ctypes.c_int64(a_rows.size), _p(c_rows),
                     _p(c_cnt), ctypes.c_int64(c_rows.size), ctypes.c_int64(s), _p(a_ids), _p(c_slots),

@@ -115,6 +115,44 @@ def test_scalars_and_table_match_oracle():
         assert np.array_equal(tab.view(np.uint32), O.scalar_table(*hp, 200).view(np.uint32))
 
 
+@pytest.mark.parametrize('D,nthreads', [(64, 1), (128, 16), (100, 4), (3, 8)])
+def test_cpu_adam_host_entry_point_matches_reference(D, nthreads):
+    """elr_cpu_adam (ext().cpu_adam, host memory, no GPU) against the reference's own compiled cpu_adam
+    (srm2/csrc/srm2_cpu.cpp:37-56, oracle/_ref) and the oracle, bitwise, over 6 steps with gradients including
+    subnormal, huge and signed-zero values; rows outside [0, R) are skipped, and non-contiguous inputs raise as the
+    reference's TORCH_CHECK does."""
+    import torch
+    from elara_amd.ops import ext
+    from oracle import ref as REF
+    rng = np.random.default_rng(D + nthreads)
+    R, n = 3000, 700
+    base = rng.standard_normal((R, 3, D)).astype(np.float32) * 0.05
+    base[:, 1:] = 0
+    ours, orc = torch.from_numpy(base.copy()), base.copy()
+    refm = REF.cpu()
+    theirs = torch.from_numpy(base.copy())
+    HP = (1e-3, 0.9, 0.999, 1e-8)
+    for t in range(1, 7):
+        rows = rng.choice(R, n, replace=False).astype(np.int64)
+        g = (rng.standard_normal((n, D)) * 1e-3).astype(np.float32)
+        g[0, :] = 1e-42
+        g[1, :] = -0.0
+        g[2, :] = 3e30
+        rt, gt = torch.from_numpy(rows), torch.from_numpy(g)
+        ext().cpu_adam(ours, rt, gt, *HP, t, nthreads)
+        O.cpu_adam(orc, rows, g, O.adam_scalars(*HP, t), nthreads)
+        if refm is not None:
+            refm.cpu_adam(theirs, rt, gt, *HP, t, nthreads)
+    assert np.array_equal(ours.numpy().view(np.uint32), orc.view(np.uint32))
+    if refm is not None:
+        assert torch.equal(ours.view(torch.int32), theirs.view(torch.int32))
+    before = ours.clone()
+    ext().cpu_adam(ours, torch.tensor([-1, R, R + 5]), torch.ones(3, D), *HP, 7, nthreads)
+    assert torch.equal(before, ours)
+    with pytest.raises(RuntimeError):
+        ext().cpu_adam(ours, torch.arange(4)[::2], torch.ones(2, D), *HP, 7, nthreads)
+
+
 def test_scalar_recip_is_the_correctly_rounded_double_reciprocal():
     tab = O.scalar_table(1e-3, 0.9, 0.999, 1e-8, 3000)
     r = np.empty((tab.shape[0], 2), np.float64)

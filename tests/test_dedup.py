@@ -409,63 +409,131 @@ def test_gpu_dedup_edge_cases(dev):
         unique(torch.tensor([-1, 2], device=dev))
 
 
+class _OraclePipe:
+    """The CPU side of a long full-size run: each step's oracle work split into a part that is independent per step
+    (`prep`, run by a pool of threads, several steps at once; the oracle's C calls release the GIL) and the part
+    that carries state from step to step (`apply`, run here, in step order).  drain() applies every submitted
+    step; at most `depth` steps are in flight (each holds its gradients in host memory)."""
+
+    def __init__(self, prep, apply, workers=6, depth=6):
+        from concurrent.futures import ThreadPoolExecutor
+        self.prep, self.apply, self.depth = prep, apply, depth
+        self.pool = ThreadPoolExecutor(workers)
+        self.q = []
+
+    def submit(self, t, *args):
+        self.q.append((t, self.pool.submit(self.prep, t, *args)))
+        while len(self.q) > self.depth:
+            self._pop()
+
+    def _pop(self):
+        t, f = self.q.pop(0)
+        self.apply(t, f.result())
+
+    def drain(self):
+        while self.q:
+            self._pop()
+
+    def close(self):
+        self.drain()
+        self.pool.shutdown()
+
+
+def _draw_all(fn, steps, workers=8):
+    """fn(t) for t = 1 .. steps, computed by a pool of threads (each step draws from its own generator)."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(workers) as ex:
+        return list(ex.map(fn, range(1, steps + 1)))
+
+
 @pytest.mark.gpu
-def test_gpu_c3_full_size_twelve_steps(dev):
-    """Config C3 at full size: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step, 12 steps (the hot
-    rows' m and v accumulate over all of them); touched rows bitwise equal to the oracle (segment sum + cpu_adam on
-    a compact copy of the touched rows).  Even steps take the plan form (elr_dedup_plan, then
-    elr_adam_dedup_plan)."""
+def test_gpu_c3_full_size_all_steps(dev):
+    """Config C3 at full size and length: 10,000,000 x 128 table, 131,072 x 26 Zipf(1.05) ids per step, all 100
+    steps, so the hot rows' m and v accumulate over the whole run.  The touched rows are compared bitwise with the
+    oracle (segment sum in ATen's order, then cpu_adam on a compact copy of the touched rows) after steps 10 and 50
+    and at the end.  Odd steps take the one-call form (elr_adam_dedup), even steps the plan form bench.py times
+    (elr_dedup_plan made beforehand, then elr_adam_dedup_plan)."""
     from elara_amd.dedup import adam_dedup, adam_dedup_plan, unique_plan_async
     from elara_amd.gpu_ops import init_rows
-    print('[gpu-test] C3 full size, 12 steps', flush=True)
-    R, D, B, F, steps = 10_000_000, 128, 131_072, 26, 12
+    R, D, B, F, steps = 10_000_000, 128, 131_072, 26, 100
+    print(f'[gpu-test] C3 full size, {steps} steps', flush=True)
     z = synth.ZipfFields([R] * F, 1.05, seed=0, offsets=[0] * F)
-    rng = np.random.default_rng(0)
+    ids_all = _draw_all(lambda t: z.draw(np.random.default_rng([0, t]), B), steps)
+    seen = np.zeros(R, bool)
+    for ids in ids_all:
+        seen[ids] = True
+    touched = np.flatnonzero(seen).astype(np.int64)
+    del seen
     table = init_rows(torch.arange(R, device=dev), D, 0, synth.bound_for(D))
-    ids_all = [z.draw(rng, B) for _ in range(steps)]
-    touched = np.unique(np.concatenate(ids_all))
     tt = torch.from_numpy(touched).to(dev)
     compact = table[tt].cpu().numpy()
-    for t, ids in enumerate(ids_all, start=1):
-        g = torch.randn(ids.size, D, device=dev, generator=torch.Generator(dev).manual_seed(t)) * 1e-3
-        if t % 2:
-            adam_dedup(table, torch.from_numpy(ids).to(dev), g, *HP, t)
-        else:   # the pipelined form bench.py times: a dedup plan made beforehand, then the sum and Adam over it
-            u, plan, _ = unique_plan_async(torch.from_numpy(ids).to(dev), D, R)
-            adam_dedup_plan(table, u, g, plan, *HP, t)
-        u, s, _ = O.segment_sum(ids, g.cpu().numpy())
-        O.cpu_adam(compact, np.searchsorted(touched, u).astype(np.int64), s, O.adam_scalars(*HP, t), 16)
-    torch.cuda.synchronize()
-    assert np.array_equal(bits(table[tt].cpu().numpy()), bits(compact))
+
+    def prep(t, ids, g):
+        u, s, _ = O.segment_sum(ids, g)
+        return np.searchsorted(touched, u).astype(np.int64), s
+
+    def apply(t, us):
+        O.cpu_adam(compact, us[0], us[1], O.adam_scalars(*HP, t), 16)
+
+    pipe = _OraclePipe(prep, apply)
+    try:
+        for t, ids in enumerate(ids_all, start=1):
+            g = torch.randn(ids.size, D, device=dev, generator=torch.Generator(dev).manual_seed(t)) * 1e-3
+            if t % 2:
+                adam_dedup(table, torch.from_numpy(ids).to(dev), g, *HP, t)
+            else:
+                u, plan, _ = unique_plan_async(torch.from_numpy(ids).to(dev), D, R)
+                adam_dedup_plan(table, u, g, plan, *HP, t)
+            pipe.submit(t, ids, g.cpu().numpy())
+            if t in (10, 50, steps):
+                pipe.drain()
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(table[tt].cpu().numpy()), bits(compact)), f'C3 differs after step {t}'
+                print(f'[gpu-test] C3 step {t}: {touched.size} touched rows equal', flush=True)
+    finally:
+        pipe.close()
 
 
 @pytest.mark.gpu
-def test_gpu_c4_large_row_stress_ten_steps(dev):
-    """Config C4: 50,000,000 x 256 table (weight + m + v = 153.6 GB in HBM), 262,144 unique Zipf(1.1) ids per
-    step, 10 steps; touched rows bitwise equal to the oracle's cpu_adam on a compact copy (the table exceeds host
-    memory budgets for a full CPU copy)."""
+def test_gpu_c4_large_row_stress_all_steps(dev):
+    """Config C4 at full size and length: 50,000,000 x 256 table (weight + m + v = 153.6 GB in HBM), 262,144 unique
+    Zipf(1.1) ids per step, all 50 steps; the touched rows compared bitwise with the oracle's cpu_adam on a
+    compact copy (the table exceeds host memory budgets for a full CPU copy) after steps 10 and 25 and at the
+    end."""
     from elara_amd.gpu_ops import init_rows
     from elara_amd.ops import gpu_adam
-    print('[gpu-test] C4 large rows, 10 steps', flush=True)
-    R, D, n = 50_000_000, 256, 262_144
+    R, D, n, steps = 50_000_000, 256, 262_144, 50
+    print(f'[gpu-test] C4 large rows, {steps} steps', flush=True)
     z = synth.ZipfFields([R], 1.1, seed=4, offsets=[0])
-    rng = np.random.default_rng(4)
     table = torch.empty(R, 3, D, device=dev)
     for a in range(0, R, 1 << 23):   # init in slices: rows a .. a+8M
         rows = torch.arange(a, min(R, a + (1 << 23)), device=dev)
         init_rows(rows, D, 0, synth.bound_for(D), out=table[a:a + rows.numel()])
-    steps = [synth.unique_zipf(rng, z, n) for _ in range(10)]
-    touched = np.unique(np.concatenate(steps))
+    ids_all = _draw_all(lambda t: synth.unique_zipf(np.random.default_rng([4, t]), z, n), steps)
+    touched = np.unique(np.concatenate(ids_all))
     tt = torch.from_numpy(touched).to(dev)
     compact = table[tt].cpu().numpy()
-    for t, ids in enumerate(steps, start=1):
-        g = (rng.standard_normal((n, D)) * 1e-3).astype(np.float32)
-        gpu_adam(table, torch.from_numpy(ids).to(dev), torch.from_numpy(g).to(dev), *HP, t)
-        O.cpu_adam(compact, np.searchsorted(touched, ids).astype(np.int64), g, O.adam_scalars(*HP, t), 16)
-    torch.cuda.synchronize()
-    assert np.array_equal(bits(table[tt].cpu().numpy()), bits(compact))
+
+    def prep(t, ids):
+        g = (np.random.default_rng([40, t]).standard_normal((n, D)) * 1e-3).astype(np.float32)
+        return np.searchsorted(touched, ids).astype(np.int64), g
+
+    def apply(t, rg):
+        O.cpu_adam(compact, rg[0], rg[1], O.adam_scalars(*HP, t), 16)
+        gpu_adam(table, torch.from_numpy(ids_all[t - 1]).to(dev), torch.from_numpy(rg[1]).to(dev), *HP, t)
+
+    pipe = _OraclePipe(prep, apply)
+    try:
+        for t, ids in enumerate(ids_all, start=1):
+            pipe.submit(t, ids)
+            if t in (10, 25, steps):
+                pipe.drain()
+                torch.cuda.synchronize()
+                assert np.array_equal(bits(table[tt].cpu().numpy()), bits(compact)), f'C4 differs after step {t}'
+                print(f'[gpu-test] C4 step {t}: {touched.size} touched rows equal', flush=True)
+    finally:
+        pipe.close()
     # the untouched neighbours of a touched row are still their initial state
     probe = np.setdiff1d(np.clip(touched[:1000] + 1, 0, R - 1), touched)[:200]
-    from oracle import oracle as OO
     assert np.array_equal(bits(table[torch.from_numpy(probe).to(dev)].cpu().numpy()),
-                          bits(OO.init_rows(probe, D, 0, synth.bound_for(D))))
+                          bits(O.init_rows(probe, D, 0, synth.bound_for(D))))

@@ -99,6 +99,21 @@ def test_oracle_triton_order_by_hand():
     assert res[True] == ([3, 4], [0, 1, 2], 5, 2)
 
 
+def test_oracle_triton_release_counts_every_entry():
+    """The Triton path's release reserves stack positions by the requested counts and skips missing entries
+    (srm2/elara_kernels.py:104-116, 199-209); this build packs the live ones.  They agree only while every counted
+    entry exists, which the oracle asserts on every Triton-order release: a release item counting an entry the row
+    does not hold fails loudly instead of giving other log ids."""
+    R, C, K = 10, 4, 3
+    st = O.DirState(R, C, K, 0, np.array([0], np.int64), np.array([3], np.int8), log_cap=20)
+    pv = st.params(True)
+    O.dir_b(st, pv, [2], [0], [], [], 1)                                  # row 2 holds one entry
+    O.dir_b(st, pv, [], [], [], [], 2, rel=(np.array([2]), np.array([1])))   # counted 1, holds 1: fine
+    O.dir_b(st, pv, [5], [0], [], [], 3)                                  # row 5 holds one entry
+    with pytest.raises(AssertionError, match='2 entries counted, 1 live'):
+        O.dir_b(st, pv, [], [], [5], [2], 4, rel=(np.zeros(0, np.int64),) * 2)
+
+
 @pytest.mark.parametrize('name', sorted(CONFIGS))
 def test_oracle_triton_order_changes_only_log_ids(name):
     """Over 60 planned steps the two orders agree on every state and output except the log ids: the same codes,
