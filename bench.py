@@ -771,10 +771,12 @@ def mode_c5(args):
                   'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
                   'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, None,
                  extra={'steps_per_s': steps / el, 'stats': s,
+                        'device_driven': st.sync_free,
+                        'syncs_per_step': s['syncs'] / steps,
                         'host_wait_us_per_step': (st.wait_s - mark['wait']) / steps * 1e6,
-                        'note': 'step_GBps not reported for C5 (mixed kernels; per-kernel bytes in profiles/); '
-                                'host_wait_us_per_step: time the host spends waiting for the GPU at the plan\'s '
-                                'synchronisation (near 0: the host is the bottleneck)'})
+                        'note': 'device_driven: the step\'s counts stay on the GPU (elr_plan_step, '
+                                'elr_step_exec_dev) and the host issues every step without waiting; otherwise '
+                                'host_wait_us_per_step is the time the host waits at the plan\'s synchronisation'})
     res['dir_check'] = st.dir_check()
     if not args.no_cpu:
         ncpu = min(total, 30)

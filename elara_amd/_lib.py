@@ -83,6 +83,11 @@ SIGNATURES = {
     'elr_plan_classify': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp]),
     'elr_plan_classify_seg': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64,
                                              c_vp]),
+    'elr_plan_step_scratch_bytes': (c_i64, [c_i64, c_i64]),
+    'elr_plan_step': (ctypes.c_int, [c_vp, c_vp, c_vp, c_vp, c_i64, c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64,
+                                     c_vp]),
+    'elr_step_exec_dev_bytes': (c_i64, [c_vp]),
+    'elr_step_exec_dev': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
 }
 
 DIR_FIELDS = ('code', 'loc', 'ent', 'lstep', 'lfree', 'n_lfree', 'log_top', 'mat_top', 'live', 'adm_c0', 'rj',
@@ -105,7 +110,23 @@ class PlanIn(ctypes.Structure):
                 ('slot_of', c_vp), ('last_seen', c_vp), ('code', c_vp), ('kthr', c_vp), ('toff', c_vp), ('T', c_i64),
                 ('dyn', c_vp), ('nd', c_i64), ('slot_row', c_vp), ('mat_top', c_vp), ('log_top', c_vp),
                 ('s', c_i64), ('K', ctypes.c_int), ('want_t', ctypes.c_int), ('loc', c_vp), ('R', c_i64),
-                ('next_bits', c_vp), ('next_mask', c_u32), ('carry', ctypes.c_int), ('live', c_vp)]
+                ('next_bits', c_vp), ('next_mask', c_u32), ('carry', ctypes.c_int), ('live', c_vp), ('n_dev', c_vp),
+                ('nd_dev', c_vp)]
+
+
+# the device-driven step (elr_plan_step / elr_step_exec_dev): descriptor and control-state words
+DESC_WORDS, CTL_WORDS = 40, 32
+D_B, D_NEV, D_KEEP_OFF, D_NKEEP, D_NFREE, D_NADM, D_LAZY, D_NL = 0, 11, 12, 13, 14, 15, 16, 17
+D_SKIP, D_OVERFLOW, D_TAKE, D_BARRIER, D_NROWS, D_ND, D_MAT_HI, D_LOG_HI = 28, 29, 30, 31, 32, 33, 34, 35
+S_NFREE, S_ND, S_ERR, S_ERR_STEP, S_ERR_A, S_ERR_B, S_ERR_C, S_STATS = 0, 1, 2, 3, 4, 5, 6, 8
+STEP_ERR_ROWS, STEP_ERR_CAPACITY = 1, 2
+STAT_KEYS = ('hits', 'N', 'L', 'F', 'S', 'adm', 'ev', 'preempt', 'overflow', 'compactions', 'appends', 'barriers',
+             'steps')
+
+
+class PlanCtl(ctypes.Structure):
+    """elr_plan_ctl: the device-driven step's control state, descriptor and capacity bounds."""
+    _fields_ = [('state', c_vp), ('desc', c_vp), ('mat_cap', c_i64), ('log_cap', c_i64), ('triton', c_i64)]
 
 
 class PlanOut(ctypes.Structure):
@@ -161,7 +182,7 @@ class ExecOut(ctypes.Structure):
     _fields_ = [(n, c_i64) for n in EXEC_OUT_FIELDS]
 
 
-ABI_STRUCTS = (DirState, DirParams, PlanIn, PlanOut, AssembleArgs, SlotsArgs, UpdateArgs, ExecArgs, ExecOut)
+ABI_STRUCTS = (DirState, DirParams, PlanIn, PlanOut, AssembleArgs, SlotsArgs, UpdateArgs, ExecArgs, ExecOut, PlanCtl)
 
 
 def lib():

@@ -34,14 +34,15 @@ namespace elr {
 // Threads [0, nL*K) take one (row, k) entry each; threads [nL*K, nL*K + nh) take one hit slot each.  The two parts
 // touch disjoint arrays (ent/lstep are read; pstep/rj/rok are written), and hit slots are unique.
 __global__ __launch_bounds__(kDirBlock) void k_dir_lsteps_hits(elr_dir_state st, elr_dir_params p,
-                                                               const int64_t* __restrict__ hs, int64_t nh,
+                                                               const int64_t* __restrict__ hs, DevCount nh_,
                                                                const int64_t* __restrict__ L_row,
-                                                               const int32_t* __restrict__ L_cnt, int64_t nL,
+                                                               const int32_t* __restrict__ L_cnt, DevCount nL_,
                                                                int32_t s, int32_t* __restrict__ L_steps,
                                                                int32_t* __restrict__ L_ids,
                                                                int64_t* __restrict__ hrec_dyn,
                                                                int64_t* __restrict__ hrec_j) {
   const int64_t t = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
+  const int64_t nh = nh_.get(), nL = nL_.get();
   const int64_t K = p.K, nLK = nL * K;
   if (t < nLK) {
     const int64_t i = t / K, k = t - i * K;
@@ -102,7 +103,8 @@ inline bool params_ok(const elr_dir_state* st, const elr_dir_params* p) {
 
 DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
                             const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
-                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch) {
+                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch,
+                            const int64_t* desc) {
   char* base = (char*)scratch;
   DirHdr* hdr = (DirHdr*)base;
   const int64_t nblk = dir_nblocks(nev);
@@ -112,12 +114,13 @@ DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, con
   DirEvictPlan e;
   e.nblk = nblk;
   e.rel_nblk = rel_cnt ? 0 : nblk;
-  e.fused = nblk <= kFusedScanBlocks;
-  e.count = DirEvictCount{S, P, ev_slot, nev, ev_row_in, thr_in, ev_row_out, rep, ev_dyn, bsum, nblk, hdr,
+  e.fused = desc || nblk <= kFusedScanBlocks;   // device-driven: the apply kernel's live blocks sum the counts
+  const DevCount n = dcount(nev, desc, kDNev);
+  e.count = DirEvictCount{S, P, ev_slot, n, ev_row_in, thr_in, ev_row_out, rep, ev_dyn, bsum, nblk, hdr,
                           rel_cnt != nullptr};
-  e.apply = DirEvictApply{S, P, ev_slot, nev, rows, rep, ev_dyn, evl_ids, evf_slots, bsum, nblk, hdr, rel_rank,
+  e.apply = DirEvictApply{S, P, ev_slot, n, rows, rep, ev_dyn, evl_ids, evf_slots, bsum, nblk, hdr, rel_rank,
                           e.fused, rel_cnt};
-  e.release = DirEvictRelease{S, P, ev_slot, nev, rows, rep, rel_rank, hdr};
+  e.release = DirEvictRelease{S, P, ev_slot, n, rows, rep, rel_rank, hdr};
   return e;
 }
 
@@ -126,7 +129,8 @@ void dir_evict_scan(const DirEvictPlan& e, hipStream_t strm) {
 }
 
 DirBPlan dir_b_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* a_rows, const int64_t* a_k,
-                    int64_t na, const DirBItems& it, int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch) {
+                    int64_t na, const DirBItems& it, int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch,
+                    const int64_t* desc) {
   char* base = (char*)scratch;
   DirHdr* hdr = (DirHdr*)base;
   const int64_t nblk_c = dir_nblocks(it.nr + it.nc), nblk_a = dir_nblocks(na);
@@ -134,10 +138,12 @@ DirBPlan dir_b_plan(const elr_dir_state& S, const elr_dir_params& P, const int64
   DirBPlan e;
   e.na = na;
   e.nblk_c = nblk_c;
-  e.fused = nblk_c <= kFusedScanBlocks;
-  e.count = DirBCount{S, P, a_rows, a_k, na, it, (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr};
+  e.fused = desc || nblk_c <= kFusedScanBlocks;   // device-driven: the compaction kernel's live blocks sum the counts
+  DirBItems itd = it;
+  itd.desc = desc;
+  e.count = DirBCount{S, P, a_rows, a_k, na, itd, (int32_t)s, a_ids, bsum, nblk_c, nblk_a, hdr, desc};
   e.count_blocks = nblk_a + nblk_c;
-  e.compact = DirBCompact{S, P, it, c_slots, bsum, nblk_c, hdr, e.fused, na};
+  e.compact = DirBCompact{S, P, itd, c_slots, bsum, nblk_c, hdr, e.fused, na, desc};
   // fused: at least one block, which advances the counters also when there are only appends
   e.compact_blocks = e.fused ? (nblk_c ? nblk_c : 1) : nblk_c;
   return e;
@@ -161,11 +167,13 @@ int dir_a_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t*
 
 void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
                             const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s, int32_t* L_steps,
-                            int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm) {
+                            int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm,
+                            const int64_t* desc) {
   const int64_t n1 = nL * P.K + nh;
   if (n1) {
-    k_dir_lsteps_hits<<<(unsigned)dir_nblocks(n1), kDirBlock, 0, strm>>>(S, P, hs, nh, L_row, L_cnt, nL, (int32_t)s,
-                                                                         L_steps, L_ids, hrec_dyn, hrec_j);
+    k_dir_lsteps_hits<<<(unsigned)dir_nblocks(n1), kDirBlock, 0, strm>>>(
+        S, P, hs, dcount(nh, desc, kDNh), L_row, L_cnt, dcount(nL, desc, kDNL), (int32_t)s, L_steps, L_ids, hrec_dyn,
+        hrec_j);
   }
 }
 

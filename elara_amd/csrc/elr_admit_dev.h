@@ -2,6 +2,7 @@
 // pool-slot bookkeeping as a functor (elr_launch.h), which the step's executor launches beside call B's count kernel.
 #pragma once
 
+#include "elr_desc.h"
 #include "elr_launch.h"
 
 namespace elr {
@@ -42,7 +43,24 @@ struct PlanAdmitSlots {
   int8_t* rj;
   int8_t* rok;
   int32_t* pstep;
+  // device-driven step: sl.n_free, sl.nev, sl.nkeep, n_adm and lazy_n are upper bounds (the grid), and sl.keep and
+  // adm_rows the planner's slot partition (2 nkeep entries) and the rows in class-rank order (rows_bound of them),
+  // offset on the device
+  const int64_t* desc;
+  int64_t rows_bound;
   __device__ void operator()(int64_t blk, int64_t) const {
+    elr_slots_args sl = this->sl;
+    int64_t n_adm = this->n_adm, lazy_n = this->lazy_n;
+    const int64_t* adm_rows = this->adm_rows;
+    if (desc) {   // each within the bound the grid and the arrays were sized for
+      sl.n_free = clampi(desc[kDNFree], 0, sl.n_free);
+      sl.nev = clampi(desc[kDNev], 0, sl.nev);
+      sl.nkeep = clampi(desc[kDNKeep], 0, sl.nkeep);
+      sl.keep += clampi(desc[kDKeepOff], 0, 2 * this->sl.nkeep - sl.nkeep);
+      n_adm = clampi(desc[kDNAdm], 0, this->n_adm);
+      lazy_n = clampi(desc[kDLazy], 0, n_adm);
+      adm_rows += clampi(desc[kDW0], 0, rows_bound - n_adm);
+    }
     const int64_t i = blk * kFunctorBlock + threadIdx.x;
     const int64_t nf = sl.n_free + sl.nev, rest = nf - n_adm;
     if (i < n_adm) {

@@ -2,6 +2,7 @@
 // eviction copies as one functor (elr_launch.h).
 #pragma once
 
+#include "elr_desc.h"
 #include "elr_launch.h"
 #include "elr_rowio.h"
 
@@ -33,7 +34,8 @@ struct IxExpand {   // item i = r * K + k: row clamp(dyn[r], 0, nd - 1) * K + k
   }
 };
 
-// One row copy: n rows of W floats, dst row dix(i) = src row six(i).
+// One row copy: n rows of W floats, dst row dix(i) = src row six(i).  n_dev (a device-driven step): the row count
+// is n_dev[0] * n_mul, n its upper bound (the grid).
 template <class DI, class SI>
 struct CopyPart {
   float* dst;
@@ -43,6 +45,8 @@ struct CopyPart {
   int64_t src_rows;
   SI six;
   int64_t n, W;
+  const int64_t* n_dev;
+  int64_t n_mul;
 };
 
 // Rows wid, wid + wcount, ... of copy c by one wave.
@@ -50,7 +54,8 @@ template <bool V4, class DI, class SI>
 __device__ __forceinline__ void copy_part(const CopyPart<DI, SI>& c, int64_t wid, int64_t wcount) {
   const int lane = threadIdx.x & 63;
   const int64_t W = c.W;
-  for (int64_t i = wid; i < c.n; i += wcount) {
+  const int64_t n = c.n_dev ? clampi(*c.n_dev * c.n_mul, 0, c.n) : c.n;
+  for (int64_t i = wid; i < n; i += wcount) {
     const int64_t d = c.dix(i);
     const int64_t s = c.six(i);
     if (d < 0 || d >= c.dst_rows || s < 0 || s >= c.src_rows) continue;
@@ -99,12 +104,15 @@ struct EvictMove {
   bool v4;
 };
 
+// desc (a device-driven step): nev is an upper bound, the count comes from the descriptor.
 inline EvictMove evict_move_prep(float* mat, int64_t mat_rows, const int64_t* evf_slots, const float* pool,
                                  int64_t pool_rows, const int64_t* ev_slot, float* logs, int64_t log_rows,
                                  const int64_t* evl_ids, const float* glog, int64_t nd, int64_t K,
-                                 const int64_t* ev_dyn, int64_t nev, int64_t D) {
-  EvictMove m{{mat, mat_rows, IxList{evf_slots}, pool, pool_rows, IxList{ev_slot}, nev, 3 * D},
-              {logs, log_rows, IxList{evl_ids}, glog, nd * K, IxExpand{ev_dyn, K, nd}, nev * K, D}, 0, 0, false};
+                                 const int64_t* ev_dyn, int64_t nev, int64_t D, const int64_t* desc = nullptr) {
+  const int64_t* nv = desc ? desc + kDNev : nullptr;
+  EvictMove m{{mat, mat_rows, IxList{evf_slots}, pool, pool_rows, IxList{ev_slot}, nev, 3 * D, nv, 1},
+              {logs, log_rows, IxList{evl_ids}, glog, nd * K, IxExpand{ev_dyn, K, nd}, nev * K, D, nv, K}, 0, 0,
+              false};
   m.nb1 = copy_blocks(m.c1.n, kCopyMaxBlocks);
   m.nb2 = copy_blocks(m.c2.n, kCopyMaxBlocks);
   m.v4 = copy_v4(m.c1) && copy_v4(m.c2);

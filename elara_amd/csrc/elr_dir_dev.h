@@ -2,6 +2,7 @@
 // functors (elr_launch.h), so that the step's executor can launch them beside independent row kernels.
 #pragma once
 
+#include "elr_desc.h"
 #include "elr_launch.h"
 #include "elr_scan.h"
 
@@ -77,6 +78,46 @@ __device__ __forceinline__ void fused_offsets(int64_t blk, const int64_t* __rest
   __syncthreads();
 }
 
+// fused_offsets for a device-driven step, whose grid is sized from an upper bound: only the first nlive blocks hold
+// items (and wrote counts), any number of them; each thread sums the counts of every kDirBlock-th live block.
+template <int NCH>
+__device__ __forceinline__ void live_offsets(int64_t blk, const int64_t* __restrict__ bsum, int64_t nblk, int64_t nlive,
+                                             int64_t (&off)[NCH], int64_t (&tot)[NCH]) {
+  __shared__ int64_t sh[2][NCH][kDirBlock / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int64_t before[NCH], all[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) before[c] = all[c] = 0;
+  for (int64_t b = threadIdx.x; b < nlive; b += kDirBlock)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t x = bsum[c * nblk + b];
+      all[c] += x;
+      before[c] += b < blk ? x : 0;
+    }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t sb = wave_incl_scan<int64_t>(before[c]), sa = wave_incl_scan<int64_t>(all[c]);
+    if (lane == 63) {
+      sh[0][c][w] = sb;
+      sh[1][c][w] = sa;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    int64_t a = 0, t = 0;
+    for (int v = 0; v < kDirBlock / 64; ++v) {
+      a += sh[0][c][v];
+      t += sh[1][c][v];
+    }
+    off[c] = a;
+    tot[c] = t;
+  }
+  __syncthreads();
+}
+
 __device__ __forceinline__ bool in_range(int64_t x, int64_t hi) { return x >= 0 && x < hi; }
 
 // searchsorted(toff, row, right=True) - 1, with ATen's wrap of index -1 to T-1 (elara_dir.cpp:46-48, 75).
@@ -130,7 +171,7 @@ struct DirEvictCount {
   elr_dir_state st;
   elr_dir_params p;
   const int64_t* ev_slot;
-  int64_t nev;
+  DevCount nev;
   const int64_t* ev_row_in;
   const int8_t* thr_in;
   int64_t* ev_row;
@@ -143,8 +184,10 @@ struct DirEvictCount {
   __device__ void operator()(int64_t blk, int64_t) const {
     dir_snapshot(blk, st, hdr);
     const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
+    const int64_t n_ev = nev.get();
+    if (nev.p && blk * kDirBlock >= n_ev) return;   // device-driven: past the live blocks (nobody reads their counts)
     int v[3] = {0, 0, 0};
-    if (i < nev) {
+    if (i < n_ev) {
       const int64_t sl = ev_slot[i];
       const int64_t C = p.n0 + p.Cdyn;
       int64_t row = -1, c0 = -1, j = 0;
@@ -187,7 +230,7 @@ struct DirEvictApply {
   elr_dir_state st;
   elr_dir_params p;
   const int64_t* ev_slot;
-  int64_t nev;
+  DevCount nev;
   const int64_t* ev_row;
   const uint8_t* rep;
   const int64_t* ev_dyn;
@@ -202,9 +245,15 @@ struct DirEvictApply {
   __device__ void operator()(int64_t blk, int64_t) const {
     const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
     const int64_t K = p.K;
+    const int64_t nev = this->nev.get();
     const int64_t nf0 = hdr->nf0, top0 = hdr->top0, mt0 = hdr->mt0;
     int64_t off[3], gtot[3];
-    if (fused) {
+    if (this->nev.p) {   // device-driven: block 0 (which always runs) advances the counters, blocks past the items exit
+      const int64_t nlive = (nev + kDirBlock - 1) / kDirBlock;
+      if (blk > 0 && blk >= nlive) return;
+      live_offsets<3>(blk, boff, nblk, nlive, off, gtot);
+      if (blk == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, top0, mt0, gtot[0], gtot[1], gtot[2]);
+    } else if (fused) {
       fused_offsets<3>(blk, boff, nblk, off, gtot);
       if (blk == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, top0, mt0, gtot[0], gtot[1], gtot[2]);
     } else {
@@ -278,14 +327,14 @@ struct DirEvictRelease {
   elr_dir_state st;
   elr_dir_params p;
   const int64_t* ev_slot;
-  int64_t nev;
+  DevCount nev;
   const int64_t* ev_row;
   const uint8_t* rep;
   const int64_t* rel_rank;
   const DirHdr* hdr;
   __device__ void operator()(int64_t blk, int64_t) const {
     const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
-    if (i >= nev || rep[i]) return;
+    if (i >= nev.get() || rep[i]) return;
     const int64_t row = ev_row[i], sl = ev_slot[i];
     if (!in_range(row, p.R) || !in_range(sl, p.n0 + p.Cdyn)) return;
     const int64_t c0 = st.adm_c0[sl];
@@ -313,6 +362,20 @@ struct DirBItems {
   const int64_t* r_cnt;
   int64_t nr;
   bool c_release;
+  // device-driven step: nc, nr are upper bounds and c_rows, c_cnt the class-ordered rows and codes, to be offset by
+  // the compactions' first position; resolved() reads the descriptor
+  const int64_t* desc;
+  __device__ __forceinline__ DirBItems resolved() const {
+    if (!desc) return *this;
+    DirBItems r = *this;
+    const int64_t at = clampi(desc[kDB + ELR_RANK_NCMP], 0, nc);
+    r.c_rows = c_rows + at;
+    r.c_cnt = c_cnt + at;
+    r.nc = clampi(desc[kDNc], 0, nc - at);
+    r.nr = clampi(desc[kDNr], 0, nr);
+    r.desc = nullptr;
+    return r;
+  }
   __device__ __forceinline__ int64_t n() const { return nr + nc; }
   __device__ __forceinline__ bool is_rel(int64_t q) const { return q < nr; }
   __device__ __forceinline__ int64_t row(int64_t q) const { return q < nr ? r_rows[q] : c_rows[q - nr]; }
@@ -342,19 +405,23 @@ struct DirBCount {
   const int64_t* a_rows;
   const int64_t* a_k;
   int64_t na;
-  DirBItems it;
+  DirBItems it_in;
   int32_t s;
   int64_t* a_ids;
   int64_t* bsum;
   int64_t nblk_c;
   int64_t nblk_a;
   DirHdr* hdr;
+  const int64_t* desc;   // device-driven step: na is an upper bound, a_rows / a_k the class-ordered rows and codes
   __device__ void operator()(int64_t blk, int64_t) const {
     dir_snapshot(blk, st, hdr);
     const int64_t K = p.K;
     if ((int64_t)blk < nblk_a) {
       const int64_t i = (int64_t)blk * kDirBlock + threadIdx.x;
-      if (i >= na) return;
+      const int64_t at = desc ? clampi(desc[kDB + ELR_RANK_NAPP], 0, na) : 0;
+      const int64_t* a_rows = this->a_rows + at;
+      const int64_t* a_k = this->a_k + at;
+      if (i >= (desc ? clampi(desc[kDNa], 0, na - at) : na)) return;
       const int64_t id = log_id_of_rank(st.lfree, p.Lcap, *st.n_lfree, *st.log_top, i);
       a_ids[i] = id;
       const int64_t row = a_rows[i], k = a_k[i];
@@ -367,6 +434,8 @@ struct DirBCount {
     }
     const int64_t b = (int64_t)blk - nblk_a;
     const int64_t q = b * kDirBlock + threadIdx.x;
+    const DirBItems it = it_in.resolved();
+    if (desc && b * kDirBlock >= it.n()) return;   // device-driven: past the live blocks (nobody reads their counts)
     int v[2] = {0, 0};
     if (q < it.n()) {
       int64_t row, cnt, cur;
@@ -388,18 +457,27 @@ struct DirBCount {
 struct DirBCompact {
   elr_dir_state st;
   elr_dir_params p;
-  DirBItems it;
+  DirBItems it_in;
   int64_t* c_slots;
   const int64_t* boff;
   int64_t nblk;
   DirHdr* hdr;
   bool fused;
   int64_t na;
+  const int64_t* desc;   // device-driven step: the appends' count from the descriptor, live blocks only
   __device__ void operator()(int64_t blk, int64_t) const {
     const int64_t q = (int64_t)blk * kDirBlock + threadIdx.x;
     const int64_t mt0 = hdr->mt0;
+    const DirBItems it = it_in.resolved();
     int64_t off[2], gtot[2], nf1;
-    if (fused) {
+    if (desc) {   // block 0 (which always runs) advances the counters, blocks past the items exit
+      const int64_t nlive = (it.n() + kDirBlock - 1) / kDirBlock, na = clampi(desc[kDNa], 0, this->na);
+      if (blk > 0 && blk >= nlive) return;
+      live_offsets<2>(blk, boff, nblk, nlive, off, gtot);
+      const int64_t nf0 = hdr->nf0;
+      nf1 = nf_after_alloc(nf0, na);
+      if (blk == 0 && threadIdx.x == 0) hdr->nf1 = dir_advance(st, nf0, hdr->top0, mt0, na, gtot[0], gtot[1]);
+    } else if (fused) {
       fused_offsets<2>(blk, boff, nblk, off, gtot);
       const int64_t nf0 = hdr->nf0;
       nf1 = nf_after_alloc(nf0, na);
@@ -450,9 +528,11 @@ int dir_b_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t*
                 int64_t na, const int64_t* c_rows, const int64_t* c_cnt, int64_t nc, const int64_t* r_rows,
                 const int64_t* r_cnt, int64_t nr, int64_t* a_ids, int64_t* c_slots, void* scratch,
                 int64_t scratch_bytes);
+// desc (a device-driven step): nh and nL are upper bounds that size the grid, the counts come from the descriptor.
 void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
                             const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s, int32_t* L_steps,
-                            int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm);
+                            int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm,
+                            const int64_t* desc = nullptr);
 
 struct DirEvictPlan {
   DirEvictCount count;
@@ -464,9 +544,12 @@ struct DirEvictPlan {
 };
 // rel_cnt: NULL for the reference's default order (the release launch pushes the host logs of rows going to M);
 // otherwise those releases are deferred to call B and their counts written there (the release launch is empty).
+// desc (a device-driven step): nev is an upper bound (the grid), the count comes from the descriptor, and the
+// apply kernel sums the live blocks' counts itself (no scan launch).
 DirEvictPlan dir_evict_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* ev_slot, int64_t nev,
                             const int64_t* ev_row_in, const int8_t* thr_in, int64_t* ev_row_out, uint8_t* rep,
-                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch);
+                            int64_t* evl_ids, int64_t* evf_slots, int64_t* ev_dyn, int64_t* rel_cnt, void* scratch,
+                            const int64_t* desc = nullptr);
 void dir_evict_scan(const DirEvictPlan& e, hipStream_t strm);
 
 struct DirBPlan {
@@ -475,9 +558,12 @@ struct DirBPlan {
   int64_t count_blocks, compact_blocks, nblk_c, na;
   bool fused;
 };
-// Call B over its items (DirBItems: release items, then compactions).
+// Call B over its items (DirBItems: release items, then compactions).  desc (a device-driven step): na, it.nc and
+// it.nr are upper bounds, a_rows / a_k and it.c_rows / c_cnt the rows and codes in class-rank order (offset on the
+// device by the appends' and compactions' first positions), and no scan launch.
 DirBPlan dir_b_plan(const elr_dir_state& S, const elr_dir_params& P, const int64_t* a_rows, const int64_t* a_k,
-                    int64_t na, const DirBItems& it, int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch);
+                    int64_t na, const DirBItems& it, int64_t s, int64_t* a_ids, int64_t* c_slots, void* scratch,
+                    const int64_t* desc = nullptr);
 void dir_b_scan(const DirBPlan& e, hipStream_t strm);
 
 }  // namespace elr

@@ -5,6 +5,7 @@
 #include <initializer_list>
 
 #include "elr_copy_dev.h"
+#include "elr_desc.h"
 #include "elr_launch.h"
 #include "elr_rowio.h"
 
@@ -37,11 +38,66 @@ struct ExecAdam {
   const int64_t* rec_j;
   int64_t rec_off, n_rec;
   int copy;
+  // device-driven step: which of the update's parts this is (kExecHits ...), its counts and class-order offsets
+  // then come from the descriptor (n, na and n_rec hold upper bounds; n_rec 0: no records); g_rows: the rows of
+  // grad (and of the class-ordered slot arrays the tail and S parts index)
+  int kind;
+  const int64_t* desc;
+  int64_t g_rows;
 };
+
+enum : int { kExecPlain = 0, kExecHits, kExecAdm, kExecTail, kExecApp, kExecS };
+
+// The part's counts and offsets in a device-driven step (positions b[r] of the class order, executor.hip's update
+// order): the hits in place; the admitted rows from the work array into their pool slots with the N and L rows'
+// admission records; the compacted rows into their new MAT slots and the transient F rows into theirs (dst_b: the
+// class-ordered MAT slots, from b[FN]); the appended rows' gradients into their log ids; the S rows in place in
+// the MAT arena (dst_a: the class-ordered MAT slots, from b[S]).
+// Every value is kept within the part's bounds: in.n (its rows and its slot array), in.g_rows (the gradient rows)
+// and in.src_rows (the work rows).
+__device__ __forceinline__ ExecAdam exec_resolve(const ExecAdam& in) {
+  if (!in.desc) return in;
+  const int64_t* d = in.desc;
+  const int64_t gr = in.g_rows;
+  ExecAdam a = in;
+  switch (in.kind) {
+    case kExecHits:
+      a.g_base = clampi(d[kDB + ELR_RANK_HIT], 0, gr);
+      a.n = clampi(d[kDNh], 0, in.n < gr - a.g_base ? in.n : gr - a.g_base);
+      a.n_rec = in.n_rec ? a.n : 0;
+      break;
+    case kExecAdm:
+      a.g_base = clampi(d[kDW0], 0, gr);
+      a.n = clampi(d[kDNAdm], 0, in.n < gr - a.g_base ? in.n : gr - a.g_base);
+      a.n_rec = in.n_rec ? clampi(d[kDLazy], 0, a.n) : 0;
+      break;
+    case kExecTail: {
+      a.g_base = clampi(d[kDB + ELR_RANK_NCMP], 0, gr);
+      a.n = clampi(d[kDNTail], 0, in.n < gr - a.g_base ? in.n : gr - a.g_base);
+      a.na = clampi(d[kDNc], 0, a.n);
+      a.src_base = clampi(d[kDB + ELR_RANK_NCMP] - d[kDW0], 0, in.src_rows);
+      a.dst_b = in.dst_b + a.g_base + a.na;   // the transient rows' MAT slots follow the compacted rows'
+      break;
+    }
+    case kExecApp:
+      a.g_base = clampi(d[kDB + ELR_RANK_NAPP], 0, gr);
+      a.n = clampi(d[kDNa], 0, in.n < gr - a.g_base ? in.n : gr - a.g_base);
+      break;
+    case kExecS:
+      a.g_base = clampi(d[kDB + ELR_RANK_S], 0, gr);
+      a.n = clampi(d[kDNs], 0, in.n < gr - a.g_base ? in.n : gr - a.g_base);
+      a.dst_a = in.dst_a + a.g_base;
+      break;
+    default:
+      break;
+  }
+  if (a.na > a.n) a.na = a.n;
+  return a;
+}
 
 // Up to kExecParts parts in one launch: part q takes the blocks [bbeg[q], bbeg[q+1]) (a grid-stride loop over
 // its rows inside them).
-constexpr int kExecParts = 3;
+constexpr int kExecParts = 4;
 struct ExecMulti {
   ExecAdam part[kExecParts];
   int64_t bbeg[kExecParts + 1];
@@ -70,7 +126,7 @@ __device__ void AdamExec<VPL, U>::operator()(int64_t blk, int64_t) const {
   constexpr int64_t D = 64 * VPL;
   const int lane = threadIdx.x & 63;
   int64_t wid, wcount;
-  const ExecAdam& a = x.part[exec_part(x, blk, wid, wcount)];
+  const ExecAdam a = exec_resolve(x.part[exec_part(x, blk, wid, wcount)]);
   if (a.copy) {
     for (int64_t i = wid; i < a.n; i += wcount) {
       const int64_t d = a.dst_a[i];
@@ -130,7 +186,7 @@ struct AdamExecGen {
 __device__ inline void AdamExecGen::operator()(int64_t blk, int64_t) const {
   const int lane = threadIdx.x & 63;
   int64_t wid, wcount;
-  const ExecAdam& a = x.part[exec_part(x, blk, wid, wcount)];
+  const ExecAdam a = exec_resolve(x.part[exec_part(x, blk, wid, wcount)]);
   if (a.copy) {
     for (int64_t i = wid; i < a.n; i += wcount) {
       const int64_t d = a.dst_a[i];
@@ -205,7 +261,7 @@ struct UpdatePrep {
   float sc[8];
   AdamScalars s;
   bool dev_part, link_part;
-  ExecAdam hits, adm, tail, app;
+  ExecAdam hits, adm, tail, app, srows;   // srows: the S rows as an Adam part (device-driven step)
   EvictMove move;
   float* mat;
   const int64_t* s_slot;

@@ -22,6 +22,7 @@
 // the (ascending, unique) next batches: by binary search, or with one load from the ring of loaded batches
 // (next_bits) when the caller keeps one.
 #include "elr_admit_dev.h"
+#include "elr_desc.h"
 #include "elr_seg_dev.h"
 #include "elr_scan.h"
 
@@ -73,6 +74,18 @@ struct RowClass {
 };
 
 __device__ __forceinline__ bool row_ok(const elr_plan_in& p, int64_t r) { return p.R <= 0 || (r >= 0 && r < p.R); }
+
+// The batch's row count and the dynamic slot count: the arguments, or the device counts they bound.
+__device__ __forceinline__ int64_t rows_n(const elr_plan_in& p) {
+  if (!p.n_dev) return p.n;
+  const int64_t v = *p.n_dev;
+  return v < 0 ? 0 : (v < p.n ? v : p.n);
+}
+__device__ __forceinline__ int64_t dyn_n(const elr_plan_in& p) {
+  if (!p.nd_dev) return p.nd;
+  const int64_t v = *p.nd_dev;
+  return v < 0 ? 0 : (v < p.nd ? v : p.nd);
+}
 
 __device__ __forceinline__ RowClass classify_row(const elr_plan_in& p, int64_t r) {
   RowClass o;
@@ -161,7 +174,7 @@ __device__ void PlanCount::operator()(int64_t b, int64_t) const {
     const int64_t i = b * kPlanBlock + threadIdx.x;
     int k = -1;
     bool bad = false;
-    if (i < p.n) {
+    if (i < rows_n(p)) {
       const int64_t r = p.u[i];
       const RowClass rc = classify_row(p, r);
       bad = !row_ok(p, r);
@@ -181,7 +194,7 @@ __device__ void PlanCount::operator()(int64_t b, int64_t) const {
   } else {
     const int64_t bb = b - nbu;
     const int64_t j = bb * kPlanBlock + threadIdx.x;
-    const int k = j < p.nd ? dyn_class(p, p.dyn[j]) : -1;
+    const int k = j < dyn_n(p) ? dyn_class(p, p.dyn[j]) : -1;
     int tot[3];
     block_class_rank<3>(k, tot);
     if (threadIdx.x == 0) {
@@ -193,10 +206,201 @@ __device__ void PlanCount::operator()(int64_t b, int64_t) const {
   }
 }
 
-// Pass 2 (one block per channel): block offsets per class; class totals and the host counts.
+// ---- the device-driven step's resolution (elr_plan_step) ------------------------------------------------------
+constexpr int kRW = kScanBlock / 64;   // waves of the resolving block
+
+// The overflow path (srm2/elara.py:246-256) by the resolving block: the admitted rows are ordered as the reference's
+// stable sort of pri = (admitted and in the next batches: 0, admitted otherwise: 2) orders them, the last `need` of
+// them are not admitted after all and take the class they get without admission (their cls is rewritten), and the
+// class-rank block offsets and totals are recomputed into bu2 and tot2 (exclusive offsets per block of kPlanBlock
+// rows, as the scan launch makes them).  Returns, to thread 0, how many dropped rows appear in the next batches.
+__device__ int64_t plan_overflow(const elr_plan_in& p, const elr_plan_out& o, int64_t n, int64_t nbu, int64_t n_adm,
+                                 int64_t need, int64_t* __restrict__ bu2, int64_t* __restrict__ tot2) {
+  __shared__ int64_t a0_w[kRW];
+  __shared__ int wsum[kRW][3];
+  __shared__ int wcls[kRW][kNumCls];
+  __shared__ int64_t run[kNumCls + 3];   // class runs, then admitted rows in / not in the next batches, carry drops
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // admitted rows that appear in the next batches: they come first in the reference's priority order
+  int64_t a0 = 0;
+  for (int64_t i = threadIdx.x; i < n; i += kScanBlock) {
+    const int f = o.flags[i];
+    a0 += ((f & ELR_PLAN_ADMIT) && (f & ELR_PLAN_NEXT)) ? 1 : 0;
+  }
+  a0 = wave_incl_scan<int64_t>(a0);
+  if (lane == 63) a0_w[w] = a0;
+  if (threadIdx.x < kNumCls + 3) run[threadIdx.x] = 0;
+  __syncthreads();
+  int64_t A0 = 0;
+  for (int v = 0; v < kRW; ++v) A0 += a0_w[v];
+  const int64_t T = n_adm - need;   // admitted rows at priority rank T and beyond are dropped
+  for (int64_t c0 = 0; c0 < n; c0 += kScanBlock) {
+    const int64_t i = c0 + threadIdx.x;
+    const bool valid = i < n;
+    const int f = valid ? o.flags[i] : 0;
+    const bool adm = (f & ELR_PLAN_ADMIT) != 0, nx = (f & ELR_PLAN_NEXT) != 0;
+    const uint64_t m_nx = __builtin_amdgcn_ballot_w64(adm && nx), m_x = __builtin_amdgcn_ballot_w64(adm && !nx);
+    if (lane == 0) {
+      wsum[w][0] = __builtin_popcountll(m_nx);
+      wsum[w][1] = __builtin_popcountll(m_x);
+    }
+    __syncthreads();
+    int64_t bnx = run[kNumCls], bx = run[kNumCls + 1];
+    for (int v = 0; v < w; ++v) {
+      bnx += wsum[v][0];
+      bx += wsum[v][1];
+    }
+    const int64_t q_nx = bnx + __builtin_popcountll(m_nx & lanemask_lt());
+    const int64_t q_x = bx + __builtin_popcountll(m_x & lanemask_lt());
+    const bool drop = adm && (nx ? q_nx >= T : A0 + q_x >= T);
+    int k = valid ? (int)o.cls[i] : -1;
+    if (drop) {
+      k = (f & ELR_PLAN_N) ? ((f & ELR_PLAN_APP) ? kNApp : kNCmp)
+          : (f & ELR_PLAN_L) ? ((f & ELR_PLAN_APP) ? kLApp : kLCmp)
+          : (p.want_t ? kFNAdm : kS);
+      o.cls[i] = (int8_t)k;
+    }
+    const uint64_t m_cd = __builtin_amdgcn_ballot_w64(drop && nx);
+    const int rk = k >= 0 ? kRankOf[k] : -1;
+#pragma unroll
+    for (int q = 0; q < kNumCls; ++q) {
+      const uint64_t mq = __builtin_amdgcn_ballot_w64(rk == q);
+      if (lane == 0) wcls[w][q] = __builtin_popcountll(mq);
+    }
+    if (lane == 0) wsum[w][2] = __builtin_popcountll(m_cd);
+    __syncthreads();
+    if (threadIdx.x < kNumCls) {
+      const int q = threadIdx.x;
+      for (int sb = 0; sb < kScanBlock / kPlanBlock; ++sb) {
+        const int64_t blk = c0 / kPlanBlock + sb;
+        if (blk < nbu) bu2[(int64_t)q * nbu + blk] = run[q];
+        for (int v = sb * (kPlanBlock / 64); v < (sb + 1) * (kPlanBlock / 64); ++v) run[q] += wcls[v][q];
+      }
+    } else if (threadIdx.x < kNumCls + 3) {
+      const int q = threadIdx.x - kNumCls;
+      int64_t add = 0;
+      for (int v = 0; v < kRW; ++v) add += wsum[v][q];
+      run[threadIdx.x] += add;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x < kNumCls) tot2[threadIdx.x] = run[threadIdx.x];
+  __syncthreads();
+  return run[kNumCls + 2];
+}
+
+// The resolution of one step by the last block of the scan launch: everything the host planner decides from the
+// class counts (srm2/elara.py:234-267, 345-347; the capacity bound and the rows out of range of this build), written
+// into the step descriptor, with the dynamic pool's counters and the statistics advanced in the control state.
+__device__ void plan_resolve(const elr_plan_in& p, const elr_plan_out& o, const elr_plan_ctl& c, int64_t nbu,
+                             const int64_t* __restrict__ tot, int64_t* __restrict__ bu2,
+                             int64_t* __restrict__ tot2) {
+  __shared__ int64_t sh[4];
+  int64_t* S = c.state;
+  int64_t* Dd = c.desc;
+  const int64_t n = rows_n(p), nd = dyn_n(p);
+  if (threadIdx.x == 0) {
+    int64_t cnt[kNumCls];
+    for (int q = 0; q < kNumCls; ++q) cnt[kClsOfRank[q]] = tot[q];
+    const int64_t n_exp = tot[kNumCls], n_pre = tot[kNumCls + 1], n_free = S[kSNFree];
+    const int64_t n_adm = cnt[kNAdm] + cnt[kLAdm] + cnt[kFAdm];
+    int64_t need = n_adm - (n_free + n_exp);
+    const int64_t take = (need > 0 && nd > n_exp) ? (need < n_pre ? need : n_pre) : 0;
+    need -= take;
+    sh[0] = need > 0 ? need : 0;
+    sh[1] = take;
+    sh[2] = n_adm;
+  }
+  __syncthreads();
+  const int64_t need = sh[0];
+  const int64_t carry_drop = need > 0 ? plan_overflow(p, o, n, nbu, sh[2], need, bu2, tot2) : 0;
+  if (threadIdx.x != 0) return;
+  const int64_t take = sh[1];
+  if (need > 0)
+    for (int q = kNumCls; q < kNumCls + kDynCh + 1; ++q) tot2[q] = tot[q];
+  const int64_t* t = need > 0 ? tot2 : tot;   // by rank
+  int64_t b[kNumCls + 1];
+  b[0] = 0;
+  for (int q = 0; q < kNumCls; ++q) b[q + 1] = b[q] + t[q];
+  const int64_t nh = t[0], nNa = t[1], nLa = t[2], nFa = t[3], nNp = t[4], nLp = t[5], nNc = t[6], nLc = t[7],
+                nFn = t[8], nS = t[9];
+  const int64_t n_exp = tot[kNumCls], bad = tot[kNumCls + kDynCh], n_free = S[kSNFree];
+  const int64_t nev = n_exp + take;
+  const int64_t keep_off = take ? nev : nd + n_exp, nkeep = nd - (take ? nev : n_exp);
+  const int64_t n_adm = nNa + nLa + nFa;
+  const int64_t mat_top = p.mat_top ? *p.mat_top : 0, log_top = p.log_top ? *p.log_top : 0,
+                live = p.live ? *p.live : 0;
+  const int64_t K = p.K;
+  // the step's allocations at most: a MAT slot per eviction and compaction, a log entry per append and K per
+  // eviction, the latter from the free stack first (n_lfree = log_top - live)
+  const int64_t mt_hi = mat_top + nev + nNc + nLc;
+  int64_t lneed = nev * K + nNp + nLp - (log_top - live);
+  const int64_t lt_hi = log_top + (lneed > 0 ? lneed : 0);
+  const int64_t e = (bad > 0 ? ELR_STEP_ERR_ROWS : 0) | ((mt_hi > c.mat_cap || lt_hi > c.log_cap) ? ELR_STEP_ERR_CAPACITY : 0);
+  const int64_t err = S[kSErr];
+  if (!err && e) {
+    S[kSErr] = e;
+    S[kSErrStep] = p.s;
+    S[kSErrA] = bad;
+    S[kSErrB] = mt_hi;
+    S[kSErrC] = lt_hi;
+  }
+  const bool skip = (err | e) != 0;
+  for (int q = 0; q < kDWords; ++q) Dd[q] = 0;
+  Dd[kDOverflow] = need;   // the scatter launch takes bu2 / tot2 whenever the overflow path ran
+  Dd[kDNRows] = n;
+  Dd[kDNd] = nd;
+  Dd[kDMatHi] = mt_hi;
+  Dd[kDLogHi] = lt_hi;
+  if (skip) {
+    Dd[kDSkip] = 1;
+    return;
+  }
+  for (int q = 0; q <= kNumCls; ++q) Dd[kDB + q] = b[q];
+  Dd[kDNev] = nev;
+  Dd[kDKeepOff] = keep_off;
+  Dd[kDNKeep] = nkeep;
+  Dd[kDNFree] = n_free;
+  Dd[kDNAdm] = n_adm;
+  Dd[kDLazy] = nNa + nLa;
+  Dd[kDNL] = nLa + nLp + nLc;
+  Dd[kDNLa] = nLa;
+  Dd[kDNLp] = nLp;
+  Dd[kDNa] = nNp + nLp;
+  Dd[kDNc] = nNc + nLc;
+  Dd[kDNr] = c.triton ? nev : 0;
+  Dd[kDNh] = nh;
+  Dd[kDW0] = b[1];
+  Dd[kDNw] = b[kS] - b[1];
+  Dd[kDNs] = nS;
+  Dd[kDNTail] = b[9] - b[6];
+  Dd[kDTake] = take;
+  Dd[kDBarrier] = carry_drop > 0 ? 1 : 0;
+  S[kSNFree] = n_free + nev - n_adm;
+  S[kSNd] = nkeep + n_adm;
+  int64_t* st = S + kSStats;
+  st[kStHits] += nh;
+  st[kStN] += nNa + nNp + nNc;
+  st[kStL] += nLa + nLp + nLc;
+  st[kStF] += nFa + nFn;
+  st[kStS] += nS;
+  st[kStAdm] += n_adm;
+  st[kStEv] += nev;
+  st[kStPreempt] += take;
+  st[kStOverflow] += need;
+  st[kStCompactions] += nNc + nLc;
+  st[kStAppends] += nNp + nLp;
+  st[kStBarriers] += carry_drop > 0 ? 1 : 0;
+  st[kStSteps] += 1;
+}
+
+// Pass 2 (one block per channel): block offsets per class; class totals and the host counts.  With ctl.desc (the
+// device-driven step) the last block to finish resolves the step (plan_resolve).
 __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd,
-                                                          int64_t* __restrict__ bbad, int64_t* __restrict__ tot) {
+                                                          int64_t* __restrict__ bbad, int64_t* __restrict__ tot,
+                                                          elr_plan_ctl ctl, int64_t* __restrict__ bu2,
+                                                          int64_t* __restrict__ tot2) {
   // one block per channel: the kNumCls class channels, the kDynCh dynamic-slot channels, then the rows outside
   // [0, R), which the caller raises on instead of letting the step skip them
   const int c = blockIdx.x;
@@ -213,17 +417,39 @@ __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_pla
       o.counts[15] = p.live ? *p.live : 0;
     }
   }
+  if (!ctl.desc) return;
+  // the last block to arrive resolves the step: every block's totals are made visible device-wide before it
+  // arrives, and read after the arrival count says all are in (no block waits on another)
+  __shared__ int last;
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned long long prev = atomicAdd(reinterpret_cast<unsigned long long*>(ctl.state + kSArrive), 1ull);
+    last = prev == (unsigned long long)(gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  if (threadIdx.x == 0) ctl.state[kSArrive] = 0;   // ready for the next plan's arrivals
+  plan_resolve(p, o, ctl, nbu, tot, bu2, tot2);
 }
 
 // Pass 3: stable scatter by class.
 __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
-                                                             const int64_t* __restrict__ bu,
+                                                             const int64_t* __restrict__ bu_in,
                                                              const int64_t* __restrict__ bd,
-                                                             const int64_t* __restrict__ tot) {
+                                                             const int64_t* __restrict__ tot_in,
+                                                             const int64_t* __restrict__ desc,
+                                                             const int64_t* __restrict__ bu2,
+                                                             const int64_t* __restrict__ tot2) {
   const int64_t b = blockIdx.x;
+  // after the device-driven overflow path: its reclassified offsets and totals
+  const bool ovf = desc && desc[kDOverflow] > 0;
+  const int64_t* __restrict__ bu = ovf ? bu2 : bu_in;
+  const int64_t* __restrict__ tot = ovf ? tot2 : tot_in;
   if (b < nbu) {
     const int64_t i = b * kPlanBlock + threadIdx.x;
-    const int k = i < p.n ? kRankOf[(int)o.cls[i]] : -1;
+    const int k = i < rows_n(p) ? kRankOf[(int)o.cls[i]] : -1;
     int t[kNumCls];
     const int r = block_class_rank<kNumCls>(k, t);
     if (k >= 0) {
@@ -252,7 +478,10 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
   } else {
     const int64_t bb = b - nbu;
     const int64_t j = bb * kPlanBlock + threadIdx.x;
-    const int k = j < p.nd ? dyn_class(p, p.dyn[j]) : -1;
+    // the step's slot count: in the device-driven step from the descriptor, since the resolution has already
+    // advanced the control state's count to the one after this step
+    const int64_t nd = desc ? clampi(desc[kDNd], 0, p.nd) : dyn_n(p);
+    const int k = j < nd ? dyn_class(p, p.dyn[j]) : -1;
     int t3[3];
     const int r3 = block_class_rank<3>(k, t3);
     int t2[2];
@@ -263,7 +492,7 @@ __global__ __launch_bounds__(kPlanBlock) void k_plan_scatter(elr_plan_in p, elr_
       const int64_t d = p.dyn[j];
       o.dyn_out[base3 + bd[(int64_t)k * nbd + bb] + r3] = d;
       const int64_t pos2 = k == 0 ? bd[0 * nbd + bb] + r2 : dt[0] + bd[3 * nbd + bb] + r2;
-      o.dyn_out[p.nd + pos2] = d;
+      o.dyn_out[nd + pos2] = d;
     }
   }
 }
@@ -313,21 +542,31 @@ static int plan_classify_check(const elr_plan_in* in, const elr_plan_out* out, v
 }
 
 // The three launches of the classification; the count pass beside the segment sum's partial chunks when given
-// (blocks of the count pass first).
+// (blocks of the count pass first).  ctl (the device-driven step): the scan launch also resolves the step, with
+// the overflow path's offsets in the scratch after the plain layout.
 static int plan_classify_launch(const elr_plan_in& p, const elr_plan_out& o, void* scratch, hipStream_t st,
-                                const SegPartialsLaunch* seg) {
+                                const SegPartialsLaunch* seg, const elr_plan_ctl* ctl = nullptr) {
   const int64_t nbu = plan_blocks(p.n), nbd = plan_blocks(p.nd);
   int64_t* bu = (int64_t*)scratch;
   int64_t* bd = bu + kNumCls * nbu;
   int64_t* bbad = bd + kDynCh * nbd;
   int64_t* tot = bbad + nbu;
+  elr_plan_ctl c{};
+  int64_t* bu2 = nullptr;
+  int64_t* tot2 = nullptr;
+  if (ctl) {
+    c = *ctl;
+    bu2 = (int64_t*)((char*)scratch + elr_plan_scratch_bytes(p.n, p.nd));
+    tot2 = bu2 + kNumCls * nbu;
+  }
   const PlanCount count{p, o, nbu, nbd, bu, bd, bbad};
   if (seg && seg->blocks > 0)
     seg_partials_visit(*seg, [&](const auto& f, int64_t nb) { launch2(count, nbu + nbd, f, nb, st); });
   else
     launch1(count, nbu + nbd, st);
-  k_plan_scan<<<kNumCls + kDynCh + 1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot);
-  if (nbu + nbd > 0) k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot);
+  k_plan_scan<<<kNumCls + kDynCh + 1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot, c, bu2, tot2);
+  if (nbu + nbd > 0)
+    k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot, c.desc, bu2, tot2);
   return launch_status();
 }
 
@@ -350,6 +589,28 @@ extern "C" int elr_plan_classify_seg(const elr_plan_in* in, const elr_plan_out* 
   SegPartialsLaunch seg;
   if ((rc = seg_partials_prep(grad, n_occ, D, key_bits, dplan, dplan_bytes, seg))) return rc;
   return plan_classify_launch(*in, *out, scratch, (hipStream_t)stream, &seg);
+}
+
+extern "C" int64_t elr_plan_step_scratch_bytes(int64_t n, int64_t nd) {
+  using namespace elr;
+  const int64_t base = elr_plan_scratch_bytes(n, nd);
+  if (base < 0) return base;
+  return base + (((kNumCls * plan_blocks(n) + 16) * 8 + 255) & ~int64_t(255));
+}
+
+extern "C" int elr_plan_step(const elr_plan_in* in, const elr_plan_out* out, const elr_plan_ctl* ctl, void* scratch,
+                             int64_t scratch_bytes, const float* grad, int64_t n_occ, int64_t D, int key_bits,
+                             const void* dplan, int64_t dplan_bytes, void* stream) {
+  using namespace elr;
+  int rc = plan_classify_check(in, out, scratch, scratch_bytes);
+  if (rc) return rc;
+  if (!ctl || !ctl->state || !ctl->desc || ctl->mat_cap < 0 || ctl->log_cap < 0 || !in->nd_dev || !in->live ||
+      !in->mat_top || !in->log_top || in->n < 1 || (in->nd > 0 && !in->dyn))
+    return ELR_EINVAL;
+  if (scratch_bytes < elr_plan_step_scratch_bytes(in->n, in->nd)) return ELR_ECAPACITY;
+  SegPartialsLaunch seg{};
+  if (grad && (rc = seg_partials_prep(grad, n_occ, D, key_bits, dplan, dplan_bytes, seg))) return rc;
+  return plan_classify_launch(*in, *out, scratch, (hipStream_t)stream, grad ? &seg : nullptr, ctl);
 }
 
 extern "C" int elr_plan_admit(const int64_t* adm_rows, const int64_t* adm_slots, int64_t n_adm, int64_t lazy_n, int evl,

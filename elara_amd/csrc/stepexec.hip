@@ -249,12 +249,205 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   return update_s_rows(up, st);
 }
 
+// ---- the device-driven form (elr_step_exec_dev) ------------------------------------------------------------------
+// The same launches with every count and class-order offset read from the step descriptor that elr_plan_step wrote:
+// b[ELR_NRANK] of the arguments bounds the batch's rows, slots.nev the evictions (and the admissions and kept slots
+// with it), and the workspace is laid out for those bounds.  Row kernels run on grids capped at kDevRowBlocks blocks
+// whose waves loop over the rows; the directory kernels' grids cover the bounds and their blocks past the items exit
+// at once.  The S rows' Adam is the fourth part of the last launch.
+
+namespace {
+
+constexpr int64_t kDevRowBlocks = 4096;
+
+struct DevBounds {
+  int64_t n, nev, nadm, nkeep, nfree;
+};
+
+bool dev_bounds(const elr_exec_args& a, DevBounds& v) {
+  v.n = a.b[ELR_NRANK];
+  v.nev = a.slots.nev;
+  v.nkeep = a.slots.nkeep;
+  v.nfree = a.slots.n_free;
+  const int64_t C = a.pv.n0 + a.pv.Cdyn;
+  v.nadm = v.n < C ? v.n : C;
+  return v.n >= 1 && v.nev >= 0 && v.nkeep >= 0 && v.nfree >= 0 && v.nev <= a.pv.Cdyn && v.nkeep <= a.pv.Cdyn &&
+         v.nfree <= C && a.pv.K >= 1 && a.upd.D >= 1 && (a.dir_order == 0 || a.dir_order == 1);
+}
+
+// Byte layout of the device-driven workspace: every array at its bound.
+bool exec_layout_dev(const elr_exec_args& a, ExecLayout& L) {
+  DevBounds v;
+  if (!dev_bounds(a, v)) return false;
+  const int64_t K = a.pv.K, D = a.upd.D, n = v.n, nev = v.nev;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o += al256(bytes);
+    return at;
+  };
+  L.o.L_steps = take(n * K * 4);
+  L.o.L_ids = take(n * K * 4);
+  L.o.hrec_dyn = take(n * 8);
+  L.o.hrec_j = take(n * 8);
+  L.o.ev_row = take(nev * 8);
+  L.o.rep = take(nev);
+  L.o.evl_ids = take(nev * K * 8);
+  L.o.evf_slots = take(nev * 8);
+  L.o.ev_dyn = take(nev * 8);
+  L.o.adm_slots = take(v.nadm * 8);
+  L.o.a_ids = take(n * 8);
+  L.o.c_slots = take(n * 8);
+  L.o.work = take(n * 3 * D * 4);
+  const int64_t nr = a.dir_order ? nev : 0;
+  L.rel_cnt = take(nr * 8);
+  L.dir_a_scratch_bytes = elr_dir_scratch_bytes(nev, 0);
+  L.dir_b_scratch_bytes = elr_dir_scratch_bytes(0, n + nr);
+  if (L.dir_a_scratch_bytes < 0 || L.dir_b_scratch_bytes < 0) return false;
+  L.dir_a_scratch = take(L.dir_a_scratch_bytes > 0 ? L.dir_a_scratch_bytes : 1);
+  L.dir_b_scratch = take(L.dir_b_scratch_bytes > 0 ? L.dir_b_scratch_bytes : 1);
+  L.total = o;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int64_t elr_step_exec_dev_bytes(const elr_exec_args* args) {
+  if (!args) return ELR_EINVAL;
+  ExecLayout L;
+  if (!exec_layout_dev(*args, L)) return ELR_EINVAL;
+  return L.total;
+}
+
+extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes,
+                                 elr_exec_out* out, void* stream) {
+  using namespace elr;
+  if (!args || !out || !desc) return ELR_EINVAL;
+  const elr_exec_args& a = *args;
+  ExecLayout L;
+  DevBounds v;
+  if (!exec_layout_dev(a, L) || !dev_bounds(a, v)) return ELR_EINVAL;
+  if (!ws || ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255)) return ELR_ECAPACITY;
+  *out = L.o;
+  char* w = static_cast<char*>(ws);
+  auto at = [&](int64_t off) { return static_cast<void*>(w + off); };
+  const int64_t K = a.pv.K, D = a.upd.D, s = a.s, n = v.n, nev = v.nev;
+  const bool evl = a.pv.evl != 0;
+  const int64_t nr = a.dir_order ? nev : 0;
+  int64_t* rel_cnt = a.dir_order ? static_cast<int64_t*>(at(L.rel_cnt)) : nullptr;
+  int32_t* L_steps = static_cast<int32_t*>(at(L.o.L_steps));
+  int32_t* L_ids = static_cast<int32_t*>(at(L.o.L_ids));
+  int64_t* hrec_dyn = static_cast<int64_t*>(at(L.o.hrec_dyn));
+  int64_t* hrec_j = static_cast<int64_t*>(at(L.o.hrec_j));
+  int64_t* evl_ids = static_cast<int64_t*>(at(L.o.evl_ids));
+  int64_t* evf_slots = static_cast<int64_t*>(at(L.o.evf_slots));
+  int64_t* ev_dyn = static_cast<int64_t*>(at(L.o.ev_dyn));
+  int64_t* adm_slots = static_cast<int64_t*>(at(L.o.adm_slots));
+  int64_t* a_ids = static_cast<int64_t*>(at(L.o.a_ids));
+  int64_t* c_slots = static_cast<int64_t*>(at(L.o.c_slots));
+  float* work = static_cast<float*>(at(L.o.work));
+  int64_t* ev_row = static_cast<int64_t*>(at(L.o.ev_row));
+  uint8_t* rep = static_cast<uint8_t*>(at(L.o.rep));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc;
+  // the argument checks of the host-count form, at the bounds
+  if ((rc = dir_a_check(&a.dir, &a.pv, a.sl_ord, n, a.L_row, a.L_cnt, n, a.slots.ev_slot, nev, L_steps, L_ids,
+                        hrec_dyn, hrec_j, ev_row, rep, evl_ids, evf_slots, ev_dyn, at(L.dir_a_scratch),
+                        L.dir_a_scratch_bytes)))
+    return rc;
+  if ((rc = dir_b_check(&a.dir, &a.pv, a.u_ord, a.c_ord, n, a.u_ord, a.c_ord, n, ev_row, rel_cnt, nr, a_ids, c_slots,
+                        at(L.dir_b_scratch), L.dir_b_scratch_bytes)))
+    return rc;
+  const int64_t C = a.pv.n0 + a.pv.Cdyn;
+  elr_slots_args sl = a.slots;
+  sl.adm_slots = adm_slots;
+  if (!sl.free_stack || !sl.ev_slot || !sl.keep || !sl.dyn_out || !a.u_ord || !a.c_ord || !a.sl_ord || !a.loc_ord ||
+      !a.upd.grad || !a.upd.pool || !a.upd.mat || !a.upd.logs || !a.upd.glog || a.upd.glog_slots < 1)
+    return ELR_EINVAL;
+  const PlanAdmitSlots admit{sl, a.u_ord, v.nadm, v.nadm, evl ? 1 : 0, s, a.pv.n0, C, a.pv.R, (int)K,
+                             a.dir.code, a.dir.slot_of, a.dir.slot_row, a.dir.adm_c0, a.dir.rj, a.dir.rok,
+                             a.dir.pstep, desc, n};
+  // the assembly: the rows and the kind of each from the descriptor (one nominal segment for the host checks)
+  elr_assemble_args g{};
+  g.work = work;
+  g.rows = a.u_ord;
+  g.n = n;
+  g.D = D;
+  g.K = (int)K;
+  g.nseg = 1;
+  g.seg_end[0] = n;
+  g.seg_kind[0] = ELR_ASM_INIT;
+  g.seed = a.seed;
+  g.bound = a.bound;
+  g.L_ids = L_ids;
+  g.L_steps = L_steps;
+  g.L_cnt = a.L_cnt;
+  g.nL = n;
+  g.logs = a.upd.logs;
+  g.nlogs = a.upd.log_rows;
+  g.table = a.table;
+  g.recip = a.recip;
+  g.table_rows = a.table_rows;
+  g.mat = a.upd.mat;
+  g.mat_rows = a.upd.mat_rows;
+  g.loc = a.dir.loc;
+  g.R = a.pv.R;
+  if ((rc = assemble_check(g))) return rc;
+  // the update's parts at their bounds
+  const elr_update_args& U = a.upd;
+  float sc[8];
+  elr_adam_scalars(U.lr, U.b1, U.b2, U.eps, s, sc);
+  const AdamScalars scal = make_scalars(sc);
+  const float* G = U.grad;
+  const int64_t nd = U.glog_slots;
+  const bool al = aligned16(U.pool) && aligned16(U.mat) && aligned16(U.glog) && aligned16(work) && aligned16(G) &&
+                  aligned16(U.logs);
+  const int vpl = al ? wpr_vpl(D) : 0;
+  const ExecAdam hits{U.pool, U.pool_rows, a.sl_ord, n, nullptr, nullptr, 0, 0, G, 0, n, U.glog, nd, K, hrec_dyn,
+                      hrec_j, 0, evl ? n : 0, 0, kExecHits, desc, n};
+  const ExecAdam adm{U.pool, U.pool_rows, adm_slots, v.nadm, nullptr, work, n, 0, G, 0, v.nadm, U.glog, nd, K,
+                     nullptr, nullptr, a.pv.n0, evl ? v.nadm : 0, 0, kExecAdm, desc, n};
+  const ExecAdam tail{U.mat, U.mat_rows, c_slots, n, a.loc_ord, work, n, 0, G, 0, n, U.glog, nd, K, nullptr, nullptr,
+                      0, 0, 0, kExecTail, desc, n};
+  const ExecAdam app{U.logs, U.log_rows, a_ids, n, nullptr, nullptr, 0, 0, G, 0, n, nullptr, 0, K, nullptr, nullptr,
+                     0, 0, 1, kExecApp, desc, n};
+  const ExecAdam srows{U.mat, U.mat_rows, a.loc_ord, n, nullptr, nullptr, 0, 0, G, 0, n, nullptr, 0, K, nullptr,
+                       nullptr, 0, 0, 0, kExecS, desc, n};
+  ExecMulti hx, tx;
+  int64_t hblocks, tblocks;
+  if (!exec_multi({hits}, kDevRowBlocks, hx, hblocks) || !exec_multi({adm, tail, app, srows}, kDevRowBlocks, tx, tblocks))
+    return ELR_EINVAL;
+  const EvictMove move = evict_move_prep(U.mat, U.mat_rows, evf_slots, U.pool, U.pool_rows, a.slots.ev_slot, U.logs,
+                                         U.log_rows, evl_ids, U.glog, nd, K, ev_dyn, nev, D, desc);
+
+  // 1. call A's replay inputs and hit records
+  const elr_dir_state S = a.dir;
+  const elr_dir_params P = a.pv;
+  dir_lsteps_hits_launch(S, P, a.sl_ord, n, a.L_row, a.L_cnt, n, s, L_steps, L_ids, hrec_dyn, hrec_j, st, desc);
+  // 2-4. eviction counts + the hits; eviction apply + the assembly; eviction release + the eviction moves
+  const int64_t ev_blocks = dir_nblocks(nev > 0 ? nev : 1);
+  const DirEvictPlan ep = dir_evict_plan(S, P, a.slots.ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids,
+                                         evf_slots, ev_dyn, rel_cnt, at(L.dir_a_scratch), desc);
+  exec_visit(vpl, D, hx, hblocks, scal, [&](const auto& f, int64_t nb) { launch2(ep.count, ev_blocks, f, nb, st); });
+  assemble_visit(g, [&](const auto& f, int64_t nb) { launch2(ep.apply, ev_blocks, f, nb, st); }, desc,
+                 kDevRowBlocks);
+  evict_move_visit(move, [&](const auto& f, int64_t nb) { launch2(ep.release, ep.rel_nblk ? ev_blocks : 0, f, nb, st); });
+  // 5-6. admissions + call B's appends and counts; call B's compactions
+  const DirBItems it{a.u_ord, a.c_ord, n, ev_row, rel_cnt, nr, true};
+  const DirBPlan bp = dir_b_plan(S, P, a.u_ord, a.c_ord, n, it, s, a_ids, c_slots, at(L.dir_b_scratch), desc);
+  launch2(admit, admit_slots_blocks(sl, v.nadm), bp.count, bp.count_blocks, st);
+  launch1(bp.compact, bp.compact_blocks, st);
+  // 7. the admitted, compacted, transient, appended and S rows
+  exec_visit(vpl, D, tx, tblocks, scal, [&](const auto& f, int64_t nb) { launch1(f, nb, st); });
+  return launch_status();
+}
+
 extern "C" int elr_abi_sizes(int64_t* out, int n) {
   if (!out || n < 0) return ELR_EINVAL;
   const int64_t sz[] = {(int64_t)sizeof(elr_dir_state), (int64_t)sizeof(elr_dir_params), (int64_t)sizeof(elr_plan_in),
                         (int64_t)sizeof(elr_plan_out), (int64_t)sizeof(elr_assemble_args),
                         (int64_t)sizeof(elr_slots_args), (int64_t)sizeof(elr_update_args),
-                        (int64_t)sizeof(elr_exec_args), (int64_t)sizeof(elr_exec_out)};
+                        (int64_t)sizeof(elr_exec_args), (int64_t)sizeof(elr_exec_out), (int64_t)sizeof(elr_plan_ctl)};
   const int m = (int)(sizeof(sz) / sizeof(sz[0]));
   const int k = n < m ? n : m;
   for (int i = 0; i < k; ++i) out[i] = sz[i];

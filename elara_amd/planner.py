@@ -48,7 +48,8 @@ def _check_state(dev, named):
 
 
 def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_row, mat_top, log_top, s, K, want_t,
-                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None, counts_out=None, seg=None):
+                  loc=None, R=0, next_bits=None, next_mask=0, carry=False, live=None, counts_out=None, seg=None,
+                  n_dev=None, nd_dev=None, ctl=None):
     """Classify the unique rows u (int64, ascending) of logical step s and split the occupied dynamic slots dyn.
 
     u_nexts: up to 4 ascending int64 tensors (unique rows of the next batches).  State tensors as ElaraStep keeps
@@ -72,7 +73,12 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
 
     seg=(grad, dplan): also the partial chunks of the segment sum of grad [n_occ, D] over the batch's dedup plan
     (dedup.unique_plan), in the classification's first launch (elr_plan_classify_seg); complete the sum with
-    dedup.segment_sum_plan(grad, dplan, ..., partials_done=True)."""
+    dedup.segment_sum_plan(grad, dplan, ..., partials_done=True).
+
+    The device-driven step (elr_plan_step): n_dev / nd_dev (int64 [1] on the device) hold the row and dynamic slot
+    counts, u.numel() and dyn.numel() then bound them; ctl = (state, desc, mat_cap, log_cap, triton) with state
+    (int64 [CTL_WORDS]) the step's control state and desc (int64 [DESC_WORDS]) where the scan launch writes the
+    resolved step (preemption, overflow, class bounds, capacity check; see include/elara_amd.h)."""
     dev = u.device
     if dev.type != 'cuda':
         raise RuntimeError('plan_classify: tensors must be on a GPU')
@@ -90,7 +96,8 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
         raise RuntimeError(f'plan_classify: counts_out must be a contiguous {I64} tensor of {NCOUNTS} on {dev}')
     dyn = _dev_i64(dyn, dev)
     n, nd = u.numel(), dyn.numel()
-    nbytes = int(_lib.lib().elr_plan_scratch_bytes(n, nd))
+    nbytes = int(_lib.lib().elr_plan_step_scratch_bytes(n, nd) if ctl is not None
+                 else _lib.lib().elr_plan_scratch_bytes(n, nd))
     if nbytes < 0:
         _lib.check(nbytes, 'elr_plan_scratch_bytes')
     o64 = _lib.split_empty(dev, I64, (n, n, 2 * nd, 0 if counts_out is not None else NCOUNTS, n, n, n, n,
@@ -123,7 +130,33 @@ def plan_classify(u, u_nexts, slot_of, last_seen, code, kthr, toff, dyn, slot_ro
                 and next_bits.numel() >= R > 0):
             raise RuntimeError(f'plan_classify: next_bits must be a contiguous {I32} tensor of R rows on {dev}')
         pin.next_bits, pin.next_mask = next_bits.data_ptr(), int(next_mask) & 0xFFFFFFFF
+    for t, name in ((n_dev, 'n_dev'), (nd_dev, 'nd_dev')):
+        if t is not None and not (t.dtype == I64 and t.device == dev and t.numel() == 1):
+            raise RuntimeError(f'plan_classify: {name} must be an int64 tensor of one element on {dev}')
+    pin.n_dev = n_dev.data_ptr() if n_dev is not None else None
+    pin.nd_dev = nd_dev.data_ptr() if nd_dev is not None else None
     pout = _lib.PlanOut(*[t.data_ptr() if t is not None else None for t in out])
+    if ctl is not None:
+        state, desc, mat_cap, log_cap, triton = ctl
+        for t, m, name in ((state, _lib.CTL_WORDS, 'state'), (desc, _lib.DESC_WORDS, 'desc')):
+            if not (t.dtype == I64 and t.device == dev and t.is_contiguous() and t.numel() == m):
+                raise RuntimeError(f'plan_classify: ctl {name} must be a contiguous int64 tensor of {m} on {dev}')
+        if live is None or nd_dev is None:
+            raise RuntimeError('plan_classify: the device-driven step needs live and nd_dev')
+        c = _lib.PlanCtl(state.data_ptr(), desc.data_ptr(), int(mat_cap), int(log_cap), int(bool(triton)))
+        grad, dplan = seg if seg is not None else (None, None)
+        if grad is not None and not (grad.is_cuda and grad.device == dev and grad.dtype == torch.float32
+                                     and grad.is_contiguous() and grad.numel() == dplan.n * dplan.D):
+            raise RuntimeError(f'plan_classify: seg grad must be a contiguous float32 tensor of {dplan.n}x{dplan.D} '
+                               f'on {dev}')
+        with _lib.on_device(dev):
+            rc = _lib.lib().elr_plan_step(ctypes.byref(pin), ctypes.byref(pout), ctypes.byref(c), p(scratch), nbytes,
+                                          p(grad), dplan.n if grad is not None else 0,
+                                          dplan.D if grad is not None else 0, dplan.key_bits if grad is not None else 0,
+                                          p(dplan.buf) if grad is not None else None,
+                                          dplan.nbytes if grad is not None else 0, _lib.stream_of(u))
+        _lib.check(rc, 'elr_plan_step')
+        return out
     with _lib.on_device(dev):
         if seg is None:
             rc = _lib.lib().elr_plan_classify(ctypes.byref(pin), ctypes.byref(pout), p(scratch), nbytes,

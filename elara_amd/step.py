@@ -179,6 +179,48 @@ class HipBackend:
         _lib.check(rc, 'elr_step_exec')
         return ws, off
 
+    def step_exec_dev(self, es, p, pc, G):
+        """The device-driven form of step_exec (elr_step_exec_dev): the rest of the step with every count and
+        class-order offset read on the GPU from the plan's descriptor p._desc; bounds: the batch's rows (pc's length)
+        and the dynamic pool (evictions, admissions, kept slots)."""
+        from .elara_dir import _state
+        S, P, dev, _ = _state(es.state_list(), es.params())
+        pool, mat, logs, glog = self._arena_ptrs(es)
+        n = pc.u_ord.numel()
+        a = _lib.ExecArgs()
+        a.dir, a.pv, a.s = S, P, p.s
+        a.b[10] = n   # the rows' bound (b[ELR_NRANK]); the other bounds are read on the GPU
+        a.u_ord, a.c_ord, a.sl_ord, a.loc_ord = (pc.u_ord.data_ptr(), pc.c_ord.data_ptr(), pc.sl_ord.data_ptr(),
+                                                 pc.loc_ord.data_ptr())
+        a.L_row, a.L_cnt = pc.L_row.data_ptr(), pc.L_cnt.data_ptr()
+        if G.dtype != torch.float32 or not G.is_contiguous() or G.numel() != n * self.D:
+            raise RuntimeError(f'step_exec_dev: the gradients must be a contiguous float32 [{n}, {self.D}] tensor')
+        sl = a.slots
+        sl.free_stack, sl.n_free = es._free_buf.data_ptr(), es.C - es.n0
+        sl.ev_slot, sl.nev = pc.dyn_out.data_ptr(), es.Cdyn
+        sl.keep, sl.nkeep = pc.dyn_out.data_ptr(), es.Cdyn
+        sl.dyn_out = es._dyn_buf.data_ptr()
+        a.seed, a.bound = int(self.seed) & 0xFFFFFFFF, float(self.bound)
+        a.table, a.recip, a.table_rows = self.table.t.data_ptr(), self.table.r.data_ptr(), self.table.t.shape[0]
+        u = a.upd
+        u.D, u.K = self.D, es.K
+        u.pool, u.pool_rows, u.mat, u.mat_rows = pool, es.pool.shape[0], mat, es.mat.shape[0]
+        u.logs, u.log_rows, u.glog, u.glog_slots = logs, es.logs.shape[0], glog, es.glog.shape[0]
+        u.grad = G.data_ptr()
+        u.lr, u.b1, u.b2, u.eps = self.hp
+        a.dir_order = 1 if es.dir_impl == 'triton' else 0
+        L = _lib.lib()
+        nb = int(L.elr_step_exec_dev_bytes(ctypes.byref(a)))
+        _lib.check(min(nb, 0), 'elr_step_exec_dev_bytes')
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        off = _lib.ExecOut()
+        with _lib.on_device(dev):
+            rc = L.elr_step_exec_dev(ctypes.byref(a), ctypes.c_void_p(p._desc.data_ptr()),
+                                     ctypes.c_void_p(ws.data_ptr()), nb, ctypes.byref(off),
+                                     ctypes.c_void_p(_lib.raw_stream(dev)))
+        _lib.check(rc, 'elr_step_exec_dev')
+        return ws, off
+
     def step_update(self, es, p, G, part=0):
         """ElaraStep.update in one native call (elr_step_update): the same launches in the same order, issued from
         C++ with no per-launch Python work.  part: 0 all, 1 the device part, 2 the link part (ELR_UPDATE_*)."""
@@ -226,6 +268,9 @@ class Plan:
 
     def __getattr__(self, name):
         d = self.__dict__
+        if '_pc' in d and '_dims' not in d and not name.startswith('__'):
+            self._resolve_dev()   # a device-driven step's plan: its counts are read now (a synchronisation)
+            return getattr(self, name)
         if '_ws' not in d or name not in Plan._VIEWS and name not in ('FN_slot', 'S_slot', 'adm_rec_slot'):
             raise AttributeError(name)
         if name in ('FN_slot', 'S_slot'):
@@ -245,6 +290,33 @@ class Plan:
             v = d['_ws'][o:o + n * _lib.ESIZE[dt]].view(dt).view(*dims)
         setattr(self, name, v)
         return v
+
+    def _resolve_dev(self):
+        """The counts and arrays of a device-driven step's plan, from its descriptor (elr_plan_step) and the
+        planner's and executor's outputs: the same attributes a host-planned step has."""
+        d = self.__dict__
+        desc, pc, es = d['_desc'].tolist(), d['_pc'], d['_es']
+        b = desc[_lib.D_B:_lib.D_B + 11]
+        counts = [0] * 10
+        for r, cl in enumerate(RANK_CLASSES):
+            counts[cl] = b[r + 1] - b[r]
+        nNa, nNp, nNc, nLa, nLp, nLc = counts[1:7]
+        nev, n = desc[_lib.D_NEV], desc[_lib.D_NROWS]
+        self.b, self.counts, self.n = b, counts, n
+        self.nL = (nLa, nLp, nLc)
+        self.lazy_n = desc[_lib.D_LAZY]
+        self.skipped = bool(desc[_lib.D_SKIP])
+        self.overflowed = desc[_lib.D_OVERFLOW] > 0
+        self.barrier = bool(desc[_lib.D_BARRIER])
+        self.preempted = desc[_lib.D_TAKE]
+        self.order, self.rank, self.u_ord = pc.order[:n], pc.rank[:n], pc.u_ord[:n]
+        self.ev_slot = pc.dyn_out[:nev]
+        self.hit_slot = pc.sl_ord[:b[R_HIT + 1]]
+        nL = nLa + nLp + nLc
+        self.L_row, self.L_cnt = pc.L_row[:nL], pc.L_cnt[:nL]
+        d['_loc_ord'] = pc.loc_ord
+        d['_dims'] = dict(nL=nL, K=es.K, nh=b[R_HIT + 1], nev=nev, n_adm=desc[_lib.D_NADM], na=nNp + nLp,
+                          nc=nNc + nLc, nw=b[R_S] - b[R_NADM], D=es.D)
 
 
 class HostBudgetExceeded(RuntimeError):
@@ -280,7 +352,7 @@ class ElaraStep:
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
                  backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK,
-                 dir_impl='cpp'):
+                 dir_impl='cpp', sync_free=True):
         d = torch.device(device)
         if dir_impl not in ('cpp', 'ref', 'triton'):
             raise ValueError(f"dir_impl must be 'cpp', 'ref' or 'triton' (got {dir_impl!r})")
@@ -372,7 +444,7 @@ class ElaraStep:
                       else None)
         self._link_pending = []
         self.link_blocks = 32   # blocks per launch of the link part (measured best of 16-128 at C5 with host arenas)
-        self.stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
+        self._stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs', 'barriers')}
         self.wait_s = 0.0   # host time spent waiting for the GPU at the plans' synchronisations
         self._deferred = []
@@ -388,6 +460,33 @@ class ElaraStep:
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
+        # the device-driven step: the plan's counts stay on the GPU (elr_plan_step resolves the step there and
+        # elr_step_exec_dev reads the resolution), so the host never waits for a step.  Taken when the backend has
+        # it and nothing needs the host between the plan and the update: arenas in HBM, no host budget (its
+        # accounting reads the arenas' tops), the ring of loaded batches (the next batches are not needed as lists).
+        self.sync_free = bool(sync_free and getattr(self.be, 'step_exec_dev', None) is not None
+                              and self._slots_in_place and self._sync is not None and self.next_bits is not None
+                              and not self.host_arenas and self.host_budget == 0)
+        self._ctl_state = None
+        self._err_poll = None
+        if self.sync_free:
+            self._ctl_state = torch.zeros(_lib.CTL_WORDS, dtype=I64, device=d)
+            self._ctl_state[_lib.S_NFREE] = C - n0
+            self._err_pin = torch.zeros(1, dtype=I64, pin_memory=True)
+
+    @property
+    def stats(self):
+        """Per-run counts (srm2/elara.py's planner stats): admitted, evicted, hits, N, L, F, S rows, overflow,
+        preempted, compactions, appends, barriers, and 'syncs', the host synchronisations of the plans.  In the
+        device-driven step the row counts accumulate on the GPU: reading them is a synchronisation (not counted)."""
+        if self._ctl_state is None:
+            return self._stats
+        out = dict(self._stats)
+        vals = self._ctl_state[_lib.S_STATS:_lib.S_STATS + len(_lib.STAT_KEYS)].tolist()
+        for k, v in zip(_lib.STAT_KEYS, vals):
+            if k in out:
+                out[k] = v
+        return out
 
     # ---- helpers ----
     def state_list(self):
@@ -398,8 +497,40 @@ class ElaraStep:
     def params(self):
         return [self.R, self.K, self.log_cap, self.n0, self.Cdyn, self.MAT, self.mat_trash, int(self.evl)]
 
+    def check_errors(self):
+        """The device-driven step's errors, read from its control state (a host synchronisation): ValueError for a
+        batch with rows outside [0, R), RuntimeError for a step that could allocate past an arena.  The step that
+        hit the error and every later one did nothing.  Also brings the host's view of the free stack and the
+        dynamic slot list up to date."""
+        if self._ctl_state is None:
+            return
+        st = self._ctl_state.tolist()
+        nf, nd = st[_lib.S_NFREE], st[_lib.S_ND]
+        self.n_free, self.free = nf, self._free_buf[:nf]
+        self.dyn_slots = self._dyn_buf[:nd]
+        err, s_err = st[_lib.S_ERR], st[_lib.S_ERR_STEP]
+        if err & _lib.STEP_ERR_ROWS:
+            raise ValueError(f'step {s_err}: {st[_lib.S_ERR_A]} rows of the batch lie outside [0, {self.R})')
+        if err & _lib.STEP_ERR_CAPACITY:
+            raise RuntimeError(f'arena capacity: step {s_err} may allocate up to MAT row {st[_lib.S_ERR_B]} (capacity '
+                               f'{self.mat_cap - 1}) and log entry {st[_lib.S_ERR_C]} (capacity {self.log_cap})')
+
+    def _poll_errors(self):
+        """Raise a device-driven step's error as soon as the host sees it, without waiting: the error word is copied
+        to pinned memory behind the step's work and looked at only once that copy has completed."""
+        ev = self._err_poll
+        if ev is not None:
+            if not ev.query():
+                return
+            if int(self._err_pin[0]):
+                self.check_errors()
+        self._err_pin.copy_(self._ctl_state[_lib.S_ERR:_lib.S_ERR + 1], non_blocking=True)
+        self._err_poll = torch.cuda.Event()
+        self._err_poll.record()
+
     def check_capacity(self):
         """Raise if an allocation ran past the MAT or log arena (rows beyond capacity are not written)."""
+        self.check_errors()
         mt, lt = self._host(self.mat_top, self.log_top)
         if mt > self.mat_cap - 1 or lt > self.log_cap:
             raise RuntimeError(f'arena capacity exceeded (MAT {mt}/{self.mat_cap - 1}, logs {lt}/{self.log_cap})')
@@ -464,7 +595,7 @@ class ElaraStep:
         self._host_list(torch.zeros(0, dtype=I64, device=self.d))
 
     def _host(self, *ts):
-        self.stats['syncs'] += 1
+        self._stats['syncs'] += 1
         return torch.stack([t.reshape(()).to(I64) for t in ts]).tolist()
 
     def _host_list_async(self, t):
@@ -475,7 +606,7 @@ class ElaraStep:
         if not (t.is_cuda and self.d.type == 'cuda'):
             vals = self._host_list(t)
             return lambda: vals
-        self.stats['syncs'] += 1
+        self._stats['syncs'] += 1
         n = t.numel()
         sb = self._sync
         if sb is not None and t.data_ptr() == sb.data_ptr() and all(
@@ -509,7 +640,7 @@ class ElaraStep:
 
     def _host_list(self, t):
         """t.tolist() -- with any deferred device counts read in the same transfer (one synchronisation)."""
-        self.stats['syncs'] += 1
+        self._stats['syncs'] += 1
         if not self._deferred:
             return t.tolist()
         n = t.numel()
@@ -523,7 +654,12 @@ class ElaraStep:
     def plan(self, s, u, u_nexts, g_occ=None, dplan=None):
         """The step's plan.  With g_occ and dplan, the batch's per-row gradients (the segment sum in class-rank
         order) are queued right after the classification, before the host waits for the class counts, and kept
-        in p.G unless the overflow path reorders the rows."""
+        in p.G unless the overflow path reorders the rows.  In the device-driven step u is (rows, count on the
+        device) and the whole step is issued here (_plan_dev)."""
+        if isinstance(u, tuple):
+            if not self.sync_free:
+                raise RuntimeError('plan: a device count of rows needs the device-driven step')
+            return self._plan_dev(s, u[0], u[1], g_occ, dplan)
         d, K, C = self.d, self.K, self.C
         n = u.numel()
         # classes, class order, expired / preemptible / protected dynamic slots, counts (srm2/elara.py:214-267)
@@ -555,7 +691,7 @@ class ElaraStep:
         if (self.evl_mode == 2 and not self.evl and self.host_budget > 0
                 and (mat_top * 3 + live) * self.D * 4 >= self.evl_gate_frac * self.host_budget):
             self.evl = True
-            self.stats['evl_on_step'] = s
+            self._stats['evl_on_step'] = s
         sl, c, order = pc.sl, pc.c, pc.order
         n_adm = counts[C_NADM] + counts[C_LADM] + counts[C_FADM]
         nd = self.dyn_slots.numel()
@@ -565,7 +701,7 @@ class ElaraStep:
             ev_slot, keep_dyn = pc.dyn_out[:n_exp + take], pc.dyn_out[n_exp + take:nd]
             n_exp += take
             need -= take
-            self.stats['preempt'] += take
+            self._stats['preempt'] += take
         else:
             ev_slot, keep_dyn = pc.dyn_out[:n_exp], pc.dyn_out[nd + n_exp:]
         rank = pc.rank
@@ -579,7 +715,7 @@ class ElaraStep:
             oo = torch.argsort(pri, stable=True)
             drop = oo[n_adm - need:n_adm]
             admit[drop] = False
-            self.stats['overflow'] += need
+            self._stats['overflow'] += need
             n_adm -= need
             cls = classify_from_flags(pc.flags, admit, self.st_mode == 'T')
             # with the class counts: how many of the dropped rows recur in the next batches (carry rows) -- the
@@ -687,10 +823,36 @@ class ElaraStep:
             self.budget_account(*self._host(self.mat_top, self.log_top))
         return p
 
+    def _plan_dev(self, s, u, n_dev, g_occ, dplan):
+        """The device-driven step (srm2/elara.py:209-414 and 471-580 with no host read): the classification whose
+        scan launch resolves the step on the GPU (elr_plan_step), the segment sum in the resolved class order, and
+        the rest of the step (elr_step_exec_dev), every launch sized from upper bounds -- the batch's occurrence
+        count for its unique rows, the dynamic pool for evictions and admissions.  Returns a Plan whose counts and
+        arrays are read from the GPU only when something asks for them."""
+        if g_occ is None or dplan is None:
+            raise RuntimeError('the device-driven step takes the batch\'s occurrence gradients and dedup plan')
+        self._poll_errors()
+        K = self.K
+        g_occ = g_occ.contiguous()
+        desc = torch.empty(_lib.DESC_WORDS, dtype=I64, device=self.d)
+        ctl = (self._ctl_state, desc, self.mat_cap - 1, self.log_cap, self.dir_impl == 'triton')
+        pc = self.be.plan_classify(
+            u, [], self.slot_of, self.last_seen, self.code, self.kthr, self.toff, self._dyn_buf, self.slot_row,
+            self.mat_top, self.log_top, s, K, self.st_mode == 'T', self.loc, self.R, carry=self.dyn == 'carry',
+            live=self.live, next_bits=self.next_bits,
+            next_mask=sum(1 << ((s + k) % 32) for k in range(1, self.depth)), counts_out=self._sync[:NCOUNTS],
+            seg=(g_occ, dplan), n_dev=n_dev, nd_dev=self._ctl_state[_lib.S_ND:_lib.S_ND + 1], ctl=ctl)
+        G = self.be.segsum(g_occ, dplan, u.numel(), pc.rank, partials_done=True)
+        p = Plan()
+        p.s, p.u, p.evl, p._pc, p._desc, p._es = s, u, self.evl, pc, desc, self
+        p._ws, p._off = self.be.step_exec_dev(self, p, pc, G)
+        p.done = True
+        return p
+
     def _plan_stats(self, p, n_adm, nev, barrier):
         counts = p.counts
         nNa, nNp, nNc, nLa, nLp, nLc, nFa, nFn = counts[1:9]
-        st_ = self.stats
+        st_ = self._stats
         st_['adm'] += n_adm
         st_['ev'] += nev
         st_['hits'] += counts[C_HIT]
@@ -820,7 +982,7 @@ class ElaraStep:
         run() does (srm2/train.py:359-366); if batch s+1 was not, the next step waits for this step's writes into
         host arenas before it assembles."""
         p = self.plan(s, u, u_nexts, g_occ, dplan)
-        if getattr(p, 'done', False):   # the native executor has issued the assembly and the update
+        if p.__dict__.get('done', False):   # the native executor has issued the assembly and the update
             return p
         self.assemble(p)
         G = p.G if p.G is not None else self.be.segsum(g_occ, dplan, u.numel(), p.rank)
@@ -922,6 +1084,12 @@ def _run(step, batches, grads, steps, on_step):
         if ev is not None:
             torch.cuda.current_stream(dev).wait_event(ev)
         PLANS[j] = dplan
+        if step.sync_free:   # the device-driven step takes the rows with their count on the device, never read here
+            if nu is None:   # an empty batch
+                u, nu = torch.zeros(1, dtype=torch.int64, device=dev), torch.zeros(1, dtype=torch.int64, device=dev)
+            U[j] = (u, nu)
+            step.observe(j + 1, u, nu)
+            return
         if nu is None:
             U[j] = u
             step.observe(j + 1, u)
@@ -938,13 +1106,14 @@ def _run(step, batches, grads, steps, on_step):
         observe(j)
     if step.L + 1 < S:
         dedup(step.L + 1)
-    step.flush_deferred()
+    if not step.sync_free:
+        step.flush_deferred()
     for s in range(S):
         if s + step.L + 1 < S:
             observe(s + step.L + 1)
         if s + step.L + 2 < S:
             dedup(s + step.L + 2)
-        u_nexts = [U[s + k] for k in range(1, step.depth) if s + k < S]
+        u_nexts = [] if step.sync_free else [U[s + k] for k in range(1, step.depth) if s + k < S]
         g = grads(s) if callable(grads) else grads[s]
         p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
         if on_step is not None:

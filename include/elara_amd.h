@@ -330,6 +330,9 @@ typedef struct elr_plan_in {
                                  appears in one of the next batches, and every unprotected dynamic slot is expired;
                                  0: 'ttl' (admitted when last_seen > s; expired when last_seen of its row <= s) */
   const int64_t* live;        /* device counter copied into counts[15] (may be NULL) */
+  const int64_t* n_dev;       /* device int64 [1] or NULL: the row count is min(*n_dev, n), n then the upper bound
+                                 that sizes the grids (the batch's unique count, read on the device) */
+  const int64_t* nd_dev;      /* device int64 [1] or NULL: the dynamic slot count is min(*nd_dev, nd) */
 } elr_plan_in;
 
 typedef struct elr_plan_out {
@@ -365,6 +368,38 @@ int elr_plan_classify(const elr_plan_in* in, const elr_plan_out* out, void* scra
 int elr_plan_classify_seg(const elr_plan_in* in, const elr_plan_out* out, void* scratch, int64_t scratch_bytes,
                           const float* grad, int64_t n_occ, int64_t D, int key_bits, const void* dplan,
                           int64_t dplan_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * The device-driven step (no counterpart in the reference, whose planner reads the class counts and the host work
+ * lists on the host every step, srm2/elara.py:242, 406).  elr_plan_step is elr_plan_classify_seg whose scan launch
+ * also resolves the step on the device: the preemption and the overflow decisions (srm2/elara.py:234-258: the
+ * un-admitted rows are dropped in the reference's priority order and reclassified, and the carry barrier noted),
+ * the class-rank bounds, the evicted and kept slot ranges, the capacity bound of the step's allocations and the
+ * count of rows out of range.  It writes them into the step descriptor `desc` (ELR_DESC_WORDS int64, device), which
+ * elr_step_exec_dev reads, and keeps the dynamic pool's counters, sticky errors and accumulated statistics in
+ * `state` (ELR_CTL_WORDS int64, device, zero-initialised by the caller except the free-stack depth and the slot
+ * count).  A step that would run past an arena or holds rows outside [0, R) records the error in state and does
+ * nothing (every count of its descriptor is 0), nor does any later step: the caller raises when it next reads
+ * state.  No host synchronisation anywhere.
+ * ------------------------------------------------------------------------------------------------------- */
+#define ELR_DESC_WORDS 40
+#define ELR_CTL_WORDS 32
+#define ELR_STEP_ERR_ROWS 1        /* rows of the batch outside [0, R): state[4] holds how many */
+#define ELR_STEP_ERR_CAPACITY 2    /* the step could allocate past an arena: state[4], state[5] = MAT and log bounds */
+typedef struct elr_plan_ctl {
+  int64_t* state;             /* [ELR_CTL_WORDS] device: 0 free-stack depth, 1 dynamic slots held, 2 error bits,
+                                 3 step of the first error, 4-6 its figures (rows out of range, MAT bound, log
+                                 bound), 7 internal (0 between calls), 8-20 statistics (hits, N, L, F, S, admitted,
+                                 evicted, preempted, overflow, compactions, appends, barriers, steps) */
+  int64_t* desc;              /* [ELR_DESC_WORDS] device: the step descriptor */
+  int64_t mat_cap;            /* largest MAT row the step may allocate (capacity - 1: the last row is trash) */
+  int64_t log_cap;            /* largest log id */
+  int64_t triton;             /* 1: the Triton directory's order (the evictions' releases go to call B) */
+} elr_plan_ctl;
+int64_t elr_plan_step_scratch_bytes(int64_t n, int64_t nd);
+int elr_plan_step(const elr_plan_in* in, const elr_plan_out* out, const elr_plan_ctl* ctl, void* scratch,
+                  int64_t scratch_bytes, const float* grad, int64_t n_occ, int64_t D, int key_bits, const void* dplan,
+                  int64_t dplan_bytes, void* stream);
 
 /* Admissions of one step (srm2/elara.py:352-367): row adm_rows[i] takes dynamic pool slot adm_slots[i]
  * (slot_of, slot_row); the first lazy_n rows are N/L rows (adm_c0 = their code; with evl their resident history
@@ -566,9 +601,20 @@ typedef struct elr_exec_out {
 int64_t elr_step_exec_bytes(const elr_exec_args* args);
 int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_bytes, elr_exec_out* out, void* stream);
 
-/* sizeof of this header's structs, for a binding to check its layouts (no counterpart in the reference): out[0..8] =
+/* elr_step_exec for the device-driven step (no counterpart in the reference): every count and class-order offset
+ * comes from the descriptor `desc` that elr_plan_step wrote on the same stream, so the host issues the rest of the
+ * step without reading the GPU.  args as for elr_step_exec except: b[ELR_NRANK] bounds the batch's rows (the other
+ * bounds are ignored); u_ord, c_ord, sl_ord, loc_ord, L_row, L_cnt are elr_plan_step's outputs (class order, from
+ * position 0); slots.ev_slot and slots.keep are its dyn_out, slots.nev bounds the evictions and slots.nkeep the kept
+ * slots (both at most Cdyn), slots.n_free the free stack's depth.  The workspace (elr_step_exec_dev_bytes) holds
+ * every array at its bound; the arrays' valid prefixes have the descriptor's counts.  The S rows are updated too. */
+int64_t elr_step_exec_dev_bytes(const elr_exec_args* args);
+int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes, elr_exec_out* out,
+                      void* stream);
+
+/* sizeof of this header's structs, for a binding to check its layouts (no counterpart in the reference): out[0..9] =
  * elr_dir_state, elr_dir_params, elr_plan_in, elr_plan_out, elr_assemble_args, elr_slots_args, elr_update_args,
- * elr_exec_args, elr_exec_out (at most n of them); returns the number written. */
+ * elr_exec_args, elr_exec_out, elr_plan_ctl (at most n of them); returns the number written. */
 int elr_abi_sizes(int64_t* out, int n);
 
 /* ---------------------------------------------------------------------------------------------------------
