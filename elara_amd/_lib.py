@@ -88,6 +88,8 @@ SIGNATURES = {
                                      c_vp]),
     'elr_step_exec_dev_bytes': (c_i64, [c_vp]),
     'elr_step_exec_dev': (ctypes.c_int, [c_vp, c_vp, c_vp, c_i64, c_vp, c_vp]),
+    'elr_step_dev_bytes': (c_i64, [c_vp]),
+    'elr_step_dev': (ctypes.c_int, [c_vp, c_vp, c_i64, c_vp, c_vp]),
 }
 
 DIR_FIELDS = ('code', 'loc', 'ent', 'lstep', 'lfree', 'n_lfree', 'log_top', 'mat_top', 'live', 'adm_c0', 'rj',
@@ -182,7 +184,23 @@ class ExecOut(ctypes.Structure):
     _fields_ = [(n, c_i64) for n in EXEC_OUT_FIELDS]
 
 
-ABI_STRUCTS = (DirState, DirParams, PlanIn, PlanOut, AssembleArgs, SlotsArgs, UpdateArgs, ExecArgs, ExecOut, PlanCtl)
+class StepDevArgs(ctypes.Structure):
+    """elr_step_dev_args: a whole device-driven step in one call."""
+    _fields_ = [('plan', PlanIn), ('ctl', PlanCtl), ('grad', c_vp), ('n_occ', c_i64), ('key_bits', c_i64),
+                ('dplan', c_vp), ('dplan_bytes', c_i64), ('exec', ExecArgs)]
+
+
+STEP_DEV_OUT_FIELDS = ('cls', 'flags', 'sl', 'c', 'order', 'rank', 'dyn_out', 'counts', 'u_ord', 'c_ord', 'sl_ord',
+                       'L_row', 'L_cnt', 'loc_ord', 'grad_rows', 'exec_ws')
+
+
+class StepDevOut(ctypes.Structure):
+    """elr_step_dev_out: byte offsets in the step's workspace of the plan's outputs, G and the executor's arrays."""
+    _fields_ = [(n, c_i64) for n in STEP_DEV_OUT_FIELDS] + [('exec', ExecOut)]
+
+
+ABI_STRUCTS = (DirState, DirParams, PlanIn, PlanOut, AssembleArgs, SlotsArgs, UpdateArgs, ExecArgs, ExecOut, PlanCtl,
+               StepDevArgs, StepDevOut)
 
 
 def lib():

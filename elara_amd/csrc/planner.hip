@@ -292,6 +292,7 @@ __device__ int64_t plan_overflow(const elr_plan_in& p, const elr_plan_out& o, in
 // The resolution of one step by the last block of the scan launch: everything the host planner decides from the
 // class counts (srm2/elara.py:234-267, 345-347; the capacity bound and the rows out of range of this build), written
 // into the step descriptor, with the dynamic pool's counters and the statistics advanced in the control state.
+// One thread decides; it loads everything it reads at once (a single round trip) and the stores go out together.
 __device__ void plan_resolve(const elr_plan_in& p, const elr_plan_out& o, const elr_plan_ctl& c, int64_t nbu,
                              const int64_t* __restrict__ tot, int64_t* __restrict__ bu2,
                              int64_t* __restrict__ tot2) {
@@ -299,11 +300,20 @@ __device__ void plan_resolve(const elr_plan_in& p, const elr_plan_out& o, const 
   int64_t* S = c.state;
   int64_t* Dd = c.desc;
   const int64_t n = rows_n(p), nd = dyn_n(p);
+  constexpr int NT = kNumCls + kDynCh + 1;
+  int64_t t[NT], st[kNumStats], n_free = 0, err = 0, mat_top = 0, log_top = 0, live = 0;
   if (threadIdx.x == 0) {
-    int64_t cnt[kNumCls];
-    for (int q = 0; q < kNumCls; ++q) cnt[kClsOfRank[q]] = tot[q];
-    const int64_t n_exp = tot[kNumCls], n_pre = tot[kNumCls + 1], n_free = S[kSNFree];
-    const int64_t n_adm = cnt[kNAdm] + cnt[kLAdm] + cnt[kFAdm];
+#pragma unroll
+    for (int q = 0; q < NT; ++q) t[q] = tot[q];   // by rank, then expired, preemptible, protected, not, bad
+#pragma unroll
+    for (int q = 0; q < kNumStats; ++q) st[q] = S[kSStats + q];
+    n_free = S[kSNFree];
+    err = S[kSErr];
+    mat_top = p.mat_top ? *p.mat_top : 0;
+    log_top = p.log_top ? *p.log_top : 0;
+    live = p.live ? *p.live : 0;
+    const int64_t n_exp = t[kNumCls], n_pre = t[kNumCls + 1];
+    const int64_t n_adm = t[1] + t[2] + t[3];   // ranks NADM, LADM, FADM
     int64_t need = n_adm - (n_free + n_exp);
     const int64_t take = (need > 0 && nd > n_exp) ? (need < n_pre ? need : n_pre) : 0;
     need -= take;
@@ -316,28 +326,29 @@ __device__ void plan_resolve(const elr_plan_in& p, const elr_plan_out& o, const 
   const int64_t carry_drop = need > 0 ? plan_overflow(p, o, n, nbu, sh[2], need, bu2, tot2) : 0;
   if (threadIdx.x != 0) return;
   const int64_t take = sh[1];
-  if (need > 0)
-    for (int q = kNumCls; q < kNumCls + kDynCh + 1; ++q) tot2[q] = tot[q];
-  const int64_t* t = need > 0 ? tot2 : tot;   // by rank
+  if (need > 0) {   // the reclassified totals (the dynamic-slot ones stay), for the scatter launch too
+#pragma unroll
+    for (int q = 0; q < kNumCls; ++q) t[q] = tot2[q];
+#pragma unroll
+    for (int q = kNumCls; q < NT; ++q) tot2[q] = t[q];
+  }
   int64_t b[kNumCls + 1];
   b[0] = 0;
+#pragma unroll
   for (int q = 0; q < kNumCls; ++q) b[q + 1] = b[q] + t[q];
   const int64_t nh = t[0], nNa = t[1], nLa = t[2], nFa = t[3], nNp = t[4], nLp = t[5], nNc = t[6], nLc = t[7],
                 nFn = t[8], nS = t[9];
-  const int64_t n_exp = tot[kNumCls], bad = tot[kNumCls + kDynCh], n_free = S[kSNFree];
+  const int64_t n_exp = t[kNumCls], bad = t[kNumCls + kDynCh];
   const int64_t nev = n_exp + take;
   const int64_t keep_off = take ? nev : nd + n_exp, nkeep = nd - (take ? nev : n_exp);
   const int64_t n_adm = nNa + nLa + nFa;
-  const int64_t mat_top = p.mat_top ? *p.mat_top : 0, log_top = p.log_top ? *p.log_top : 0,
-                live = p.live ? *p.live : 0;
   const int64_t K = p.K;
   // the step's allocations at most: a MAT slot per eviction and compaction, a log entry per append and K per
   // eviction, the latter from the free stack first (n_lfree = log_top - live)
   const int64_t mt_hi = mat_top + nev + nNc + nLc;
-  int64_t lneed = nev * K + nNp + nLp - (log_top - live);
+  const int64_t lneed = nev * K + nNp + nLp - (log_top - live);
   const int64_t lt_hi = log_top + (lneed > 0 ? lneed : 0);
   const int64_t e = (bad > 0 ? ELR_STEP_ERR_ROWS : 0) | ((mt_hi > c.mat_cap || lt_hi > c.log_cap) ? ELR_STEP_ERR_CAPACITY : 0);
-  const int64_t err = S[kSErr];
   if (!err && e) {
     S[kSErr] = e;
     S[kSErrStep] = p.s;
@@ -346,52 +357,46 @@ __device__ void plan_resolve(const elr_plan_in& p, const elr_plan_out& o, const 
     S[kSErrC] = lt_hi;
   }
   const bool skip = (err | e) != 0;
-  for (int q = 0; q < kDWords; ++q) Dd[q] = 0;
-  Dd[kDOverflow] = need;   // the scatter launch takes bu2 / tot2 whenever the overflow path ran
-  Dd[kDNRows] = n;
-  Dd[kDNd] = nd;
-  Dd[kDMatHi] = mt_hi;
-  Dd[kDLogHi] = lt_hi;
-  if (skip) {
-    Dd[kDSkip] = 1;
-    return;
+  int64_t v[kDWords];
+#pragma unroll
+  for (int q = 0; q < kDWords; ++q) v[q] = 0;
+  v[kDOverflow] = need;   // the scatter launch takes bu2 / tot2 whenever the overflow path ran
+  v[kDNRows] = n;
+  v[kDNd] = nd;
+  v[kDMatHi] = mt_hi;
+  v[kDLogHi] = lt_hi;
+  v[kDSkip] = skip ? 1 : 0;
+  if (!skip) {
+#pragma unroll
+    for (int q = 0; q <= kNumCls; ++q) v[kDB + q] = b[q];
+    v[kDNev] = nev;
+    v[kDKeepOff] = keep_off;
+    v[kDNKeep] = nkeep;
+    v[kDNFree] = n_free;
+    v[kDNAdm] = n_adm;
+    v[kDLazy] = nNa + nLa;
+    v[kDNL] = nLa + nLp + nLc;
+    v[kDNLa] = nLa;
+    v[kDNLp] = nLp;
+    v[kDNa] = nNp + nLp;
+    v[kDNc] = nNc + nLc;
+    v[kDNr] = c.triton ? nev : 0;
+    v[kDNh] = nh;
+    v[kDW0] = b[1];
+    v[kDNw] = b[kNumCls - 1] - b[1];
+    v[kDNs] = nS;
+    v[kDNTail] = b[kNumCls - 1] - b[6];
+    v[kDTake] = take;
+    v[kDBarrier] = carry_drop > 0 ? 1 : 0;
+    S[kSNFree] = n_free + nev - n_adm;
+    S[kSNd] = nkeep + n_adm;
+    const int64_t add[kNumStats] = {nh, nNa + nNp + nNc, nLa + nLp + nLc, nFa + nFn, nS, n_adm, nev, take, need,
+                                    nNc + nLc, nNp + nLp, carry_drop > 0 ? 1 : 0, 1};
+#pragma unroll
+    for (int q = 0; q < kNumStats; ++q) S[kSStats + q] = st[q] + add[q];
   }
-  for (int q = 0; q <= kNumCls; ++q) Dd[kDB + q] = b[q];
-  Dd[kDNev] = nev;
-  Dd[kDKeepOff] = keep_off;
-  Dd[kDNKeep] = nkeep;
-  Dd[kDNFree] = n_free;
-  Dd[kDNAdm] = n_adm;
-  Dd[kDLazy] = nNa + nLa;
-  Dd[kDNL] = nLa + nLp + nLc;
-  Dd[kDNLa] = nLa;
-  Dd[kDNLp] = nLp;
-  Dd[kDNa] = nNp + nLp;
-  Dd[kDNc] = nNc + nLc;
-  Dd[kDNr] = c.triton ? nev : 0;
-  Dd[kDNh] = nh;
-  Dd[kDW0] = b[1];
-  Dd[kDNw] = b[kS] - b[1];
-  Dd[kDNs] = nS;
-  Dd[kDNTail] = b[9] - b[6];
-  Dd[kDTake] = take;
-  Dd[kDBarrier] = carry_drop > 0 ? 1 : 0;
-  S[kSNFree] = n_free + nev - n_adm;
-  S[kSNd] = nkeep + n_adm;
-  int64_t* st = S + kSStats;
-  st[kStHits] += nh;
-  st[kStN] += nNa + nNp + nNc;
-  st[kStL] += nLa + nLp + nLc;
-  st[kStF] += nFa + nFn;
-  st[kStS] += nS;
-  st[kStAdm] += n_adm;
-  st[kStEv] += nev;
-  st[kStPreempt] += take;
-  st[kStOverflow] += need;
-  st[kStCompactions] += nNc + nLc;
-  st[kStAppends] += nNp + nLp;
-  st[kStBarriers] += carry_drop > 0 ? 1 : 0;
-  st[kStSteps] += 1;
+#pragma unroll
+  for (int q = 0; q < kDWords; ++q) Dd[q] = v[q];
 }
 
 // Pass 2 (one block per channel): block offsets per class; class totals and the host counts.  With ctl.desc (the

@@ -259,6 +259,10 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
 namespace {
 
 constexpr int64_t kDevRowBlocks = 4096;
+// The assembly keeps one work row per wave for the rows of a large batch (C5: about 37k rows; 65k waves here): its
+// rows' loads are then all in flight at once, where a looping wave would wait for its stores before the next
+// row's loads.
+constexpr int64_t kDevAsmBlocks = 16384;
 
 struct DevBounds {
   int64_t n, nev, nadm, nkeep, nfree;
@@ -430,7 +434,7 @@ extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc,
                                          evf_slots, ev_dyn, rel_cnt, at(L.dir_a_scratch), desc);
   exec_visit(vpl, D, hx, hblocks, scal, [&](const auto& f, int64_t nb) { launch2(ep.count, ev_blocks, f, nb, st); });
   assemble_visit(g, [&](const auto& f, int64_t nb) { launch2(ep.apply, ev_blocks, f, nb, st); }, desc,
-                 kDevRowBlocks);
+                 kDevAsmBlocks);
   evict_move_visit(move, [&](const auto& f, int64_t nb) { launch2(ep.release, ep.rel_nblk ? ev_blocks : 0, f, nb, st); });
   // 5-6. admissions + call B's appends and counts; call B's compactions
   const DirBItems it{a.u_ord, a.c_ord, n, ev_row, rel_cnt, nr, true};
@@ -442,12 +446,117 @@ extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc,
   return launch_status();
 }
 
+// ---- the whole device-driven step (elr_step_dev) -------------------------------------------------------------------
+
+namespace {
+
+struct StepDevLayout {
+  elr_step_dev_out o;
+  int64_t plan_scratch, plan_scratch_bytes, exec_bytes, total;
+};
+
+// Workspace: the plan's outputs at their bounds (n rows, nd dynamic slots), its scratch, G [n, D], then the
+// executor's workspace.
+bool step_dev_layout(const elr_step_dev_args& a, StepDevLayout& L) {
+  const int64_t n = a.plan.n, nd = a.plan.nd, D = a.exec.upd.D;
+  if (n < 1 || nd < 0 || D < 1) return false;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = o;
+    o += al256(bytes);
+    return at;
+  };
+  L.o.cls = take(n);
+  L.o.flags = take(n);
+  L.o.sl = take(n * 4);
+  L.o.c = take(n);
+  L.o.order = take(n * 8);
+  L.o.rank = take(n * 8);
+  L.o.dyn_out = take(2 * nd * 8);
+  L.o.counts = take(17 * 8);
+  L.o.u_ord = take(n * 8);
+  L.o.c_ord = take(n * 8);
+  L.o.sl_ord = take(n * 8);
+  L.o.L_row = take(n * 8);
+  L.o.L_cnt = take(n * 4);
+  L.o.loc_ord = take(n * 8);
+  L.plan_scratch_bytes = elr_plan_step_scratch_bytes(n, nd);
+  if (L.plan_scratch_bytes < 0) return false;
+  L.plan_scratch = take(L.plan_scratch_bytes);
+  L.o.grad_rows = take(n * D * 4);
+  elr_exec_args e = a.exec;
+  e.b[ELR_NRANK] = n;
+  L.exec_bytes = elr_step_exec_dev_bytes(&e);
+  if (L.exec_bytes < 0) return false;
+  L.o.exec_ws = take(L.exec_bytes);
+  L.total = o;
+  return true;
+}
+
+}  // namespace
+
+extern "C" int64_t elr_step_dev_bytes(const elr_step_dev_args* args) {
+  if (!args) return ELR_EINVAL;
+  StepDevLayout L;
+  if (!step_dev_layout(*args, L)) return ELR_EINVAL;
+  return L.total;
+}
+
+extern "C" int elr_step_dev(const elr_step_dev_args* args, void* ws, int64_t ws_bytes, elr_step_dev_out* out,
+                            void* stream) {
+  if (!args || !out) return ELR_EINVAL;
+  const elr_step_dev_args& a = *args;
+  StepDevLayout L;
+  if (!step_dev_layout(a, L)) return ELR_EINVAL;
+  if (!ws || ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255)) return ELR_ECAPACITY;
+  char* w = static_cast<char*>(ws);
+  const int64_t n = a.plan.n, D = a.exec.upd.D;
+  elr_plan_out po;
+  po.cls = reinterpret_cast<int8_t*>(w + L.o.cls);
+  po.flags = reinterpret_cast<uint8_t*>(w + L.o.flags);
+  po.sl = reinterpret_cast<int32_t*>(w + L.o.sl);
+  po.c = reinterpret_cast<int8_t*>(w + L.o.c);
+  po.order = reinterpret_cast<int64_t*>(w + L.o.order);
+  po.rank = reinterpret_cast<int64_t*>(w + L.o.rank);
+  po.dyn_out = reinterpret_cast<int64_t*>(w + L.o.dyn_out);
+  po.counts = reinterpret_cast<int64_t*>(w + L.o.counts);
+  po.u_ord = reinterpret_cast<int64_t*>(w + L.o.u_ord);
+  po.c_ord = reinterpret_cast<int64_t*>(w + L.o.c_ord);
+  po.sl_ord = reinterpret_cast<int64_t*>(w + L.o.sl_ord);
+  po.L_row = reinterpret_cast<int64_t*>(w + L.o.L_row);
+  po.L_cnt = reinterpret_cast<int32_t*>(w + L.o.L_cnt);
+  po.loc_ord = reinterpret_cast<int64_t*>(w + L.o.loc_ord);
+  if (!a.plan.loc) return ELR_EINVAL;   // the executor needs the rows' MAT slots in class order
+  int rc = elr_plan_step(&a.plan, &po, &a.ctl, w + L.plan_scratch, L.plan_scratch_bytes, a.grad, a.n_occ, D,
+                         (int)a.key_bits, a.dplan, a.dplan_bytes, stream);
+  if (rc) return rc;
+  float* G = reinterpret_cast<float*>(w + L.o.grad_rows);
+  if (a.n_occ > 0 && (rc = elr_segment_sum_plan_final(a.grad, a.n_occ, D, (int)a.key_bits, a.dplan, a.dplan_bytes,
+                                                      po.rank, G, n, stream)))
+    return rc;
+  elr_exec_args e = a.exec;
+  e.b[ELR_NRANK] = n;
+  e.u_ord = po.u_ord;
+  e.c_ord = po.c_ord;
+  e.sl_ord = po.sl_ord;
+  e.loc_ord = po.loc_ord;
+  e.L_row = po.L_row;
+  e.L_cnt = po.L_cnt;
+  e.slots.ev_slot = po.dyn_out;
+  e.slots.keep = po.dyn_out;
+  e.upd.grad = G;
+  if ((rc = elr_step_exec_dev(&e, a.ctl.desc, w + L.o.exec_ws, L.exec_bytes, &L.o.exec, stream))) return rc;
+  *out = L.o;
+  return ELR_OK;
+}
+
 extern "C" int elr_abi_sizes(int64_t* out, int n) {
   if (!out || n < 0) return ELR_EINVAL;
   const int64_t sz[] = {(int64_t)sizeof(elr_dir_state), (int64_t)sizeof(elr_dir_params), (int64_t)sizeof(elr_plan_in),
                         (int64_t)sizeof(elr_plan_out), (int64_t)sizeof(elr_assemble_args),
                         (int64_t)sizeof(elr_slots_args), (int64_t)sizeof(elr_update_args),
-                        (int64_t)sizeof(elr_exec_args), (int64_t)sizeof(elr_exec_out), (int64_t)sizeof(elr_plan_ctl)};
+                        (int64_t)sizeof(elr_exec_args), (int64_t)sizeof(elr_exec_out), (int64_t)sizeof(elr_plan_ctl),
+                        (int64_t)sizeof(elr_step_dev_args), (int64_t)sizeof(elr_step_dev_out)};
   const int m = (int)(sizeof(sz) / sizeof(sz[0]));
   const int k = n < m ? n : m;
   for (int i = 0; i < k; ++i) out[i] = sz[i];

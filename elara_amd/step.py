@@ -69,6 +69,7 @@ class HipBackend:
         self.dx = dir_ext()
         self._arenas = None
         self._exec = None
+        self._dev = {}
 
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
@@ -179,47 +180,78 @@ class HipBackend:
         _lib.check(rc, 'elr_step_exec')
         return ws, off
 
-    def step_exec_dev(self, es, p, pc, G):
-        """The device-driven form of step_exec (elr_step_exec_dev): the rest of the step with every count and
-        class-order offset read on the GPU from the plan's descriptor p._desc; bounds: the batch's rows (pc's length)
-        and the dynamic pool (evictions, admissions, kept slots)."""
+    def step_dev(self, es, s, u, n_dev, g_occ, dplan):
+        """A whole device-driven step in one native call (elr_step_dev): the plan that resolves the step on the GPU,
+        the segment sum in its class order and the rest of the step, every count read on the GPU.  The call's
+        arguments are built once per ElaraStep and the workspace kept from step to step, so a step costs the host a
+        few field updates and one call.  Returns (workspace, offsets, sequence number)."""
+        st = self._dev.get(id(es))
+        if st is None or st['es'] is not es:
+            st = self._dev[id(es)] = self._dev_setup(es)
+        a, dev = st['args'], es.d
+        if not (u.dtype == torch.int64 and u.is_contiguous() and u.device == dev and n_dev.dtype == torch.int64
+                and n_dev.device == dev and n_dev.numel() == 1):
+            raise RuntimeError('step_dev: u must be a contiguous int64 tensor and n_dev an int64 [1] tensor on '
+                               f'{dev}')
+        n_occ = dplan.n
+        if n_occ and not (g_occ.dtype == torch.float32 and g_occ.is_contiguous() and g_occ.device == dev
+                          and g_occ.numel() == n_occ * self.D):
+            raise RuntimeError(f'step_dev: the gradients must be a contiguous float32 [{n_occ}, {self.D}] tensor')
+        a.plan.u, a.plan.n, a.plan.n_dev = u.data_ptr(), u.numel(), n_dev.data_ptr()
+        a.plan.s, a.exec.s = s, s
+        a.plan.next_mask = sum(1 << ((s + k) % 32) for k in range(1, es.depth)) & 0xFFFFFFFF
+        a.grad = g_occ.data_ptr() if n_occ else None
+        a.n_occ, a.key_bits = n_occ, dplan.key_bits
+        a.dplan, a.dplan_bytes = (dplan.buf.data_ptr(), dplan.nbytes) if n_occ else (None, 0)
+        L = _lib.lib()
+        nb = int(L.elr_step_dev_bytes(ctypes.byref(a)))
+        _lib.check(min(nb, 0), 'elr_step_dev_bytes')
+        if st['ws'] is None or st['ws'].numel() < nb:
+            st['ws'] = torch.empty(nb, dtype=torch.uint8, device=dev)
+        ws = st['ws']
+        out = _lib.StepDevOut()
+        with _lib.on_device(dev):
+            rc = L.elr_step_dev(ctypes.byref(a), ctypes.c_void_p(ws.data_ptr()), nb, ctypes.byref(out),
+                                ctypes.c_void_p(_lib.raw_stream(dev)))
+        _lib.check(rc, 'elr_step_dev')
+        st['seq'] += 1
+        return ws, out, st['seq']
+
+    def _dev_setup(self, es):
+        """The device-driven step's call arguments that stay fixed for an ElaraStep: the directory, the residency
+        state, the arenas and their bounds (elr_step_dev_args)."""
         from .elara_dir import _state
         S, P, dev, _ = _state(es.state_list(), es.params())
         pool, mat, logs, glog = self._arena_ptrs(es)
-        n = pc.u_ord.numel()
-        a = _lib.ExecArgs()
-        a.dir, a.pv, a.s = S, P, p.s
-        a.b[10] = n   # the rows' bound (b[ELR_NRANK]); the other bounds are read on the GPU
-        a.u_ord, a.c_ord, a.sl_ord, a.loc_ord = (pc.u_ord.data_ptr(), pc.c_ord.data_ptr(), pc.sl_ord.data_ptr(),
-                                                 pc.loc_ord.data_ptr())
-        a.L_row, a.L_cnt = pc.L_row.data_ptr(), pc.L_cnt.data_ptr()
-        if G.dtype != torch.float32 or not G.is_contiguous() or G.numel() != n * self.D:
-            raise RuntimeError(f'step_exec_dev: the gradients must be a contiguous float32 [{n}, {self.D}] tensor')
-        sl = a.slots
+        a = _lib.StepDevArgs()
+        pin = a.plan
+        pin.slot_of, pin.last_seen, pin.code = es.slot_of.data_ptr(), es.last_seen.data_ptr(), es.code.data_ptr()
+        pin.kthr, pin.toff, pin.T = es.kthr.data_ptr(), es.toff.data_ptr(), es.toff.numel()
+        pin.dyn, pin.nd, pin.slot_row = es._dyn_buf.data_ptr(), es._dyn_buf.numel(), es.slot_row.data_ptr()
+        pin.mat_top, pin.log_top, pin.live = es.mat_top.data_ptr(), es.log_top.data_ptr(), es.live.data_ptr()
+        pin.K, pin.want_t = es.K, int(es.st_mode == 'T')
+        pin.loc, pin.R = es.loc.data_ptr(), es.R
+        pin.next_bits = es.next_bits.data_ptr()
+        pin.carry = int(es.dyn == 'carry')
+        pin.nd_dev = es._ctl_state[_lib.S_ND:_lib.S_ND + 1].data_ptr()
+        c = a.ctl
+        c.state, c.desc = es._ctl_state.data_ptr(), es._desc.data_ptr()
+        c.mat_cap, c.log_cap, c.triton = es.mat_cap - 1, es.log_cap, int(es.dir_impl == 'triton')
+        e = a.exec
+        e.dir, e.pv = S, P
+        sl = e.slots
         sl.free_stack, sl.n_free = es._free_buf.data_ptr(), es.C - es.n0
-        sl.ev_slot, sl.nev = pc.dyn_out.data_ptr(), es.Cdyn
-        sl.keep, sl.nkeep = pc.dyn_out.data_ptr(), es.Cdyn
+        sl.nev, sl.nkeep = es.Cdyn, es.Cdyn
         sl.dyn_out = es._dyn_buf.data_ptr()
-        a.seed, a.bound = int(self.seed) & 0xFFFFFFFF, float(self.bound)
-        a.table, a.recip, a.table_rows = self.table.t.data_ptr(), self.table.r.data_ptr(), self.table.t.shape[0]
-        u = a.upd
-        u.D, u.K = self.D, es.K
-        u.pool, u.pool_rows, u.mat, u.mat_rows = pool, es.pool.shape[0], mat, es.mat.shape[0]
-        u.logs, u.log_rows, u.glog, u.glog_slots = logs, es.logs.shape[0], glog, es.glog.shape[0]
-        u.grad = G.data_ptr()
-        u.lr, u.b1, u.b2, u.eps = self.hp
-        a.dir_order = 1 if es.dir_impl == 'triton' else 0
-        L = _lib.lib()
-        nb = int(L.elr_step_exec_dev_bytes(ctypes.byref(a)))
-        _lib.check(min(nb, 0), 'elr_step_exec_dev_bytes')
-        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
-        off = _lib.ExecOut()
-        with _lib.on_device(dev):
-            rc = L.elr_step_exec_dev(ctypes.byref(a), ctypes.c_void_p(p._desc.data_ptr()),
-                                     ctypes.c_void_p(ws.data_ptr()), nb, ctypes.byref(off),
-                                     ctypes.c_void_p(_lib.raw_stream(dev)))
-        _lib.check(rc, 'elr_step_exec_dev')
-        return ws, off
+        e.seed, e.bound = int(self.seed) & 0xFFFFFFFF, float(self.bound)
+        e.table, e.recip, e.table_rows = self.table.t.data_ptr(), self.table.r.data_ptr(), self.table.t.shape[0]
+        up = e.upd
+        up.D, up.K = self.D, es.K
+        up.pool, up.pool_rows, up.mat, up.mat_rows = pool, es.pool.shape[0], mat, es.mat.shape[0]
+        up.logs, up.log_rows, up.glog, up.glog_slots = logs, es.logs.shape[0], glog, es.glog.shape[0]
+        up.lr, up.b1, up.b2, up.eps = self.hp
+        e.dir_order = 1 if es.dir_impl == 'triton' else 0
+        return {'es': es, 'args': a, 'ws': None, 'seq': 0}
 
     def step_update(self, es, p, G, part=0):
         """ElaraStep.update in one native call (elr_step_update): the same launches in the same order, issued from
@@ -268,7 +300,7 @@ class Plan:
 
     def __getattr__(self, name):
         d = self.__dict__
-        if '_pc' in d and '_dims' not in d and not name.startswith('__'):
+        if '_doff' in d and '_dims' not in d and not name.startswith('__'):
             self._resolve_dev()   # a device-driven step's plan: its counts are read now (a synchronisation)
             return getattr(self, name)
         if '_ws' not in d or name not in Plan._VIEWS and name not in ('FN_slot', 'S_slot', 'adm_rec_slot'):
@@ -292,16 +324,24 @@ class Plan:
         return v
 
     def _resolve_dev(self):
-        """The counts and arrays of a device-driven step's plan, from its descriptor (elr_plan_step) and the
-        planner's and executor's outputs: the same attributes a host-planned step has."""
+        """The counts and arrays of a device-driven step's plan, from its descriptor and the outputs the step left in
+        its workspace: the same attributes a host-planned step has (a host synchronisation)."""
         d = self.__dict__
-        desc, pc, es = d['_desc'].tolist(), d['_pc'], d['_es']
+        es, ws, off = d['_es'], d['_ws'], d['_doff']
+        if d['_seq'] != es.be._dev[id(es)]['seq']:
+            raise RuntimeError(f'the plan of step {d["s"]} is no longer readable: a later step has reused its '
+                               'workspace (read a device-driven plan before the next step)')
+        desc = es._desc.tolist()
         b = desc[_lib.D_B:_lib.D_B + 11]
         counts = [0] * 10
         for r, cl in enumerate(RANK_CLASSES):
             counts[cl] = b[r + 1] - b[r]
         nNa, nNp, nNc, nLa, nLp, nLc = counts[1:7]
         nev, n = desc[_lib.D_NEV], desc[_lib.D_NROWS]
+
+        def arr(field, dt, m):
+            o = getattr(off, field)
+            return ws[o:o + m * _lib.ESIZE[dt]].view(dt)
         self.b, self.counts, self.n = b, counts, n
         self.nL = (nLa, nLp, nLc)
         self.lazy_n = desc[_lib.D_LAZY]
@@ -309,12 +349,15 @@ class Plan:
         self.overflowed = desc[_lib.D_OVERFLOW] > 0
         self.barrier = bool(desc[_lib.D_BARRIER])
         self.preempted = desc[_lib.D_TAKE]
-        self.order, self.rank, self.u_ord = pc.order[:n], pc.rank[:n], pc.u_ord[:n]
-        self.ev_slot = pc.dyn_out[:nev]
-        self.hit_slot = pc.sl_ord[:b[R_HIT + 1]]
+        self.order, self.rank, self.u_ord = arr('order', I64, n), arr('rank', I64, n), arr('u_ord', I64, n)
+        self.ev_slot = arr('dyn_out', I64, nev)
+        self.hit_slot = arr('sl_ord', I64, b[R_HIT + 1])
         nL = nLa + nLp + nLc
-        self.L_row, self.L_cnt = pc.L_row[:nL], pc.L_cnt[:nL]
-        d['_loc_ord'] = pc.loc_ord
+        self.L_row, self.L_cnt = arr('L_row', I64, nL), arr('L_cnt', I32, nL)
+        self.G = arr('grad_rows', torch.float32, n * es.D).view(n, es.D)
+        d['_loc_ord'] = arr('loc_ord', I64, n)
+        eo = off.exec_ws
+        d['_off'] = _lib.ExecOut(*[getattr(off.exec, f) + eo for f in _lib.EXEC_OUT_FIELDS])
         d['_dims'] = dict(nL=nL, K=es.K, nh=b[R_HIT + 1], nev=nev, n_adm=desc[_lib.D_NADM], na=nNp + nLp,
                           nc=nNc + nLc, nw=b[R_S] - b[R_NADM], D=es.D)
 
@@ -460,18 +503,20 @@ class ElaraStep:
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
-        # the device-driven step: the plan's counts stay on the GPU (elr_plan_step resolves the step there and
-        # elr_step_exec_dev reads the resolution), so the host never waits for a step.  Taken when the backend has
+        # the device-driven step: the plan's counts stay on the GPU (elr_step_dev: the plan resolves the step there
+        # and the executor reads the resolution), so the host never waits for a step.  Taken when the backend has
         # it and nothing needs the host between the plan and the update: arenas in HBM, no host budget (its
         # accounting reads the arenas' tops), the ring of loaded batches (the next batches are not needed as lists).
-        self.sync_free = bool(sync_free and getattr(self.be, 'step_exec_dev', None) is not None
+        self.sync_free = bool(sync_free and getattr(self.be, 'step_dev', None) is not None
                               and self._slots_in_place and self._sync is not None and self.next_bits is not None
                               and not self.host_arenas and self.host_budget == 0)
         self._ctl_state = None
         self._err_poll = None
+        self._polls = 0
         if self.sync_free:
             self._ctl_state = torch.zeros(_lib.CTL_WORDS, dtype=I64, device=d)
             self._ctl_state[_lib.S_NFREE] = C - n0
+            self._desc = torch.zeros(_lib.DESC_WORDS, dtype=I64, device=d)
             self._err_pin = torch.zeros(1, dtype=I64, pin_memory=True)
 
     @property
@@ -515,9 +560,16 @@ class ElaraStep:
             raise RuntimeError(f'arena capacity: step {s_err} may allocate up to MAT row {st[_lib.S_ERR_B]} (capacity '
                                f'{self.mat_cap - 1}) and log entry {st[_lib.S_ERR_C]} (capacity {self.log_cap})')
 
+    POLL_EVERY = 16   # device-driven steps between two looks at the error word
+
     def _poll_errors(self):
-        """Raise a device-driven step's error as soon as the host sees it, without waiting: the error word is copied
-        to pinned memory behind the step's work and looked at only once that copy has completed."""
+        """Raise a device-driven step's error soon after the host can see it, without waiting: every POLL_EVERY
+        steps the error word is copied to pinned memory behind the step's work, and looked at once that copy has
+        completed.  (A step with an error and every later one do nothing on the GPU, so raising late changes no
+        state; the end of a run reads the word in any case.)"""
+        self._polls += 1
+        if self._polls % self.POLL_EVERY:
+            return
         ev = self._err_poll
         if ev is not None:
             if not ev.query():
@@ -824,28 +876,18 @@ class ElaraStep:
         return p
 
     def _plan_dev(self, s, u, n_dev, g_occ, dplan):
-        """The device-driven step (srm2/elara.py:209-414 and 471-580 with no host read): the classification whose
-        scan launch resolves the step on the GPU (elr_plan_step), the segment sum in the resolved class order, and
-        the rest of the step (elr_step_exec_dev), every launch sized from upper bounds -- the batch's occurrence
-        count for its unique rows, the dynamic pool for evictions and admissions.  Returns a Plan whose counts and
-        arrays are read from the GPU only when something asks for them."""
+        """The device-driven step (srm2/elara.py:209-414 and 471-580 with no host read): one native call
+        (elr_step_dev) issues the classification whose scan launch resolves the step on the GPU, the segment sum in
+        the resolved class order and the rest of the step, every launch sized from upper bounds -- the batch's
+        occurrence count for its unique rows, the dynamic pool for evictions and admissions.  Returns a Plan whose
+        counts and arrays are read from the GPU only when something asks for them, which must happen before the
+        next step is issued (the next step reuses the workspace)."""
         if g_occ is None or dplan is None:
             raise RuntimeError('the device-driven step takes the batch\'s occurrence gradients and dedup plan')
         self._poll_errors()
-        K = self.K
-        g_occ = g_occ.contiguous()
-        desc = torch.empty(_lib.DESC_WORDS, dtype=I64, device=self.d)
-        ctl = (self._ctl_state, desc, self.mat_cap - 1, self.log_cap, self.dir_impl == 'triton')
-        pc = self.be.plan_classify(
-            u, [], self.slot_of, self.last_seen, self.code, self.kthr, self.toff, self._dyn_buf, self.slot_row,
-            self.mat_top, self.log_top, s, K, self.st_mode == 'T', self.loc, self.R, carry=self.dyn == 'carry',
-            live=self.live, next_bits=self.next_bits,
-            next_mask=sum(1 << ((s + k) % 32) for k in range(1, self.depth)), counts_out=self._sync[:NCOUNTS],
-            seg=(g_occ, dplan), n_dev=n_dev, nd_dev=self._ctl_state[_lib.S_ND:_lib.S_ND + 1], ctl=ctl)
-        G = self.be.segsum(g_occ, dplan, u.numel(), pc.rank, partials_done=True)
         p = Plan()
-        p.s, p.u, p.evl, p._pc, p._desc, p._es = s, u, self.evl, pc, desc, self
-        p._ws, p._off = self.be.step_exec_dev(self, p, pc, G)
+        p.s, p.u, p.evl, p._es = s, u, self.evl, self
+        p._ws, p._doff, p._seq = self.be.step_dev(self, s, u, n_dev, g_occ.contiguous(), dplan)
         p.done = True
         return p
 
@@ -1059,7 +1101,11 @@ def _run(step, batches, grads, steps, on_step):
         (record_stream keeps the allocator from reusing them before that work is done)."""
         src = batches[j]
         ids = src.to(dev)
-        slot = step.count_slot()
+        # the host-planned step reads the unique count at its next synchronisation, from a slot of its sync buffer;
+        # the device-driven step never reads it, and the host runs steps ahead of the GPU, so each batch has a count
+        # tensor of its own (kept by the allocator until the main stream's work on it is done) rather than a slot
+        # the host could hand to a later batch before this one's plan has run
+        slot = None if step.sync_free else step.count_slot()
         kw = {} if slot is None else {'nu_out': slot}
         if side is None:
             AHEAD[j] = (*step.be.unique_async(ids, step.R, **kw), None)

@@ -612,9 +612,40 @@ int64_t elr_step_exec_dev_bytes(const elr_exec_args* args);
 int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes, elr_exec_out* out,
                       void* stream);
 
-/* sizeof of this header's structs, for a binding to check its layouts (no counterpart in the reference): out[0..9] =
+/* A whole device-driven step in one call (no counterpart in the reference): elr_plan_step, the rest of the batch's
+ * segment sum (elr_segment_sum_plan_final, in the class order the plan resolves) and elr_step_exec_dev, with every
+ * array in one workspace that the caller keeps from step to step (elr_step_dev_bytes, 256-byte aligned).
+ *   plan:  as for elr_plan_step; its u, n, n_dev, s and next_mask change per step, nd bounds the dynamic slots;
+ *          the output pointers are ignored (the call places them in ws).
+ *   ctl:   as for elr_plan_step (desc is where this step's descriptor goes).
+ *   grad [n_occ, D], key_bits, dplan, dplan_bytes: the batch's occurrence gradients and dedup plan (elr_dedup_plan).
+ *   exec:  as for elr_step_exec_dev; its class-ordered arrays and slot lists are taken from the plan's outputs in
+ *          ws, exec.b[ELR_NRANK] from plan.n and exec.upd.grad from the segment sum in ws.
+ * out receives the byte offsets in ws of the plan's outputs (elr_plan_out order), of the per-row gradients G and
+ * of the executor's outputs; they hold this step's values until the next call. */
+typedef struct elr_step_dev_args {
+  elr_plan_in plan;
+  elr_plan_ctl ctl;
+  const float* grad;
+  int64_t n_occ;
+  int64_t key_bits;
+  const void* dplan;
+  int64_t dplan_bytes;
+  elr_exec_args exec;
+} elr_step_dev_args;
+typedef struct elr_step_dev_out {
+  int64_t cls, flags, sl, c, order, rank, dyn_out, counts, u_ord, c_ord, sl_ord, L_row, L_cnt, loc_ord;
+  int64_t grad_rows;          /* G [plan.n, D]: the per-row gradients in class-rank order */
+  int64_t exec_ws;            /* the executor's workspace; out.exec's offsets are relative to it */
+  elr_exec_out exec;
+} elr_step_dev_out;
+int64_t elr_step_dev_bytes(const elr_step_dev_args* args);
+int elr_step_dev(const elr_step_dev_args* args, void* ws, int64_t ws_bytes, elr_step_dev_out* out, void* stream);
+
+/* sizeof of this header's structs, for a binding to check its layouts (no counterpart in the reference): out[0..11] =
  * elr_dir_state, elr_dir_params, elr_plan_in, elr_plan_out, elr_assemble_args, elr_slots_args, elr_update_args,
- * elr_exec_args, elr_exec_out, elr_plan_ctl (at most n of them); returns the number written. */
+ * elr_exec_args, elr_exec_out, elr_plan_ctl, elr_step_dev_args, elr_step_dev_out (at most n of them); returns the
+ * number written. */
 int elr_abi_sizes(int64_t* out, int n);
 
 /* ---------------------------------------------------------------------------------------------------------

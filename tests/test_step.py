@@ -145,7 +145,7 @@ def test_gpu_step_matches_oracle_step(dev, name):
     switched on by memory pressure part way through (the reference's default, srm2/train.py:128-130).  triton*: the
     Triton directory's allocation order (srm2/elara_kernels.py), through the native step executor and, with host
     arenas, through the call-by-call directory entry points.  Every configuration without host arenas, a host
-    budget or a look-ahead beyond the ring runs the device-driven step (elr_plan_step + elr_step_exec_dev: no host
+    budget or a look-ahead beyond the ring runs the device-driven step (elr_step_dev: one native call and no host
     synchronisation per step, overflow and preemption resolved on the GPU); *_hostsync run the step that reads its
     class counts on the host instead."""
     from elara_amd.step import run
@@ -230,7 +230,7 @@ def test_gpu_native_update_matches_python_update(dev, name):
     class CallByCall(HipBackend):
         step_update = None
         step_exec = None
-        step_exec_dev = None
+        step_dev = None
 
     print(f'[gpu-test] native update {name}', flush=True)
     kw = {'evl': {}, 'no_evl_S': {'evl': False, 'st': 'S'}, 'host_arenas': {'host': True}}[name]
