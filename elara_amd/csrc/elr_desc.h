@@ -50,7 +50,7 @@ enum : int {
   kSErrA = 4,      // its figures: rows out of range, the MAT bound, the log bound
   kSErrB = 5,
   kSErrC = 6,
-  kSArrive = 7,    // the planner scan launch's arrival count (back to 0 after each launch)
+  kSReserved = 7,  // unused
   kSStats = 8,     // [8, 8 + kNumStats): accumulated per-step statistics (the ElaraStep.stats keys below)
   kSWords = 32
 };

@@ -54,7 +54,9 @@ __device__ __forceinline__ bool sorted_has(const int64_t* __restrict__ a, int64_
 __device__ __forceinline__ bool in_next(const elr_plan_in& p, int64_t r) {
   if (p.next_bits) return (p.next_bits[r] & p.next_mask) != 0;
   bool f = false;
-  for (int k = 0; k < p.nnext; ++k) f = f || sorted_has(p.next[k], p.n_next[k], r);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)   // constant indices keep the lists' pointers in registers (nnext <= 4)
+    if (k < p.nnext) f = f || sorted_has(p.next[k], p.n_next[k], r);
   return f;
 }
 
@@ -357,86 +359,119 @@ __device__ void plan_resolve(const elr_plan_in& p, const elr_plan_out& o, const 
     S[kSErrC] = lt_hi;
   }
   const bool skip = (err | e) != 0;
-  int64_t v[kDWords];
+  // every descriptor word is written once (the words a skipped step leaves are zero)
+  Dd[kDOverflow] = need;   // the scatter launch takes bu2 / tot2 whenever the overflow path ran
+  Dd[kDNRows] = n;
+  Dd[kDNd] = nd;
+  Dd[kDMatHi] = mt_hi;
+  Dd[kDLogHi] = lt_hi;
+  Dd[kDSkip] = skip ? 1 : 0;
 #pragma unroll
-  for (int q = 0; q < kDWords; ++q) v[q] = 0;
-  v[kDOverflow] = need;   // the scatter launch takes bu2 / tot2 whenever the overflow path ran
-  v[kDNRows] = n;
-  v[kDNd] = nd;
-  v[kDMatHi] = mt_hi;
-  v[kDLogHi] = lt_hi;
-  v[kDSkip] = skip ? 1 : 0;
-  if (!skip) {
+  for (int q = 0; q <= kNumCls; ++q) Dd[kDB + q] = skip ? 0 : b[q];
+  const int64_t words[][2] = {{kDNev, nev},
+                              {kDKeepOff, keep_off},
+                              {kDNKeep, nkeep},
+                              {kDNFree, n_free},
+                              {kDNAdm, n_adm},
+                              {kDLazy, nNa + nLa},
+                              {kDNL, nLa + nLp + nLc},
+                              {kDNLa, nLa},
+                              {kDNLp, nLp},
+                              {kDNa, nNp + nLp},
+                              {kDNc, nNc + nLc},
+                              {kDNr, c.triton ? nev : 0},
+                              {kDNh, nh},
+                              {kDW0, b[1]},
+                              {kDNw, b[kNumCls - 1] - b[1]},
+                              {kDNs, nS},
+                              {kDNTail, b[kNumCls - 1] - b[6]},
+                              {kDTake, take},
+                              {kDBarrier, carry_drop > 0 ? 1 : 0}};
+  constexpr int kNamed = sizeof(words) / sizeof(words[0]);
+  static_assert(kDB + kNumCls + 1 + kNamed + 6 <= kDWords, "descriptor words");
 #pragma unroll
-    for (int q = 0; q <= kNumCls; ++q) v[kDB + q] = b[q];
-    v[kDNev] = nev;
-    v[kDKeepOff] = keep_off;
-    v[kDNKeep] = nkeep;
-    v[kDNFree] = n_free;
-    v[kDNAdm] = n_adm;
-    v[kDLazy] = nNa + nLa;
-    v[kDNL] = nLa + nLp + nLc;
-    v[kDNLa] = nLa;
-    v[kDNLp] = nLp;
-    v[kDNa] = nNp + nLp;
-    v[kDNc] = nNc + nLc;
-    v[kDNr] = c.triton ? nev : 0;
-    v[kDNh] = nh;
-    v[kDW0] = b[1];
-    v[kDNw] = b[kNumCls - 1] - b[1];
-    v[kDNs] = nS;
-    v[kDNTail] = b[kNumCls - 1] - b[6];
-    v[kDTake] = take;
-    v[kDBarrier] = carry_drop > 0 ? 1 : 0;
-    S[kSNFree] = n_free + nev - n_adm;
-    S[kSNd] = nkeep + n_adm;
-    const int64_t add[kNumStats] = {nh, nNa + nNp + nNc, nLa + nLp + nLc, nFa + nFn, nS, n_adm, nev, take, need,
-                                    nNc + nLc, nNp + nLp, carry_drop > 0 ? 1 : 0, 1};
+  for (int q = 0; q < kNamed; ++q) Dd[words[q][0]] = skip ? 0 : words[q][1];
+  if (skip) return;
+  S[kSNFree] = n_free + nev - n_adm;
+  S[kSNd] = nkeep + n_adm;
+  const int64_t add[kNumStats] = {nh, nNa + nNp + nNc, nLa + nLp + nLc, nFa + nFn, nS, n_adm, nev, take, need,
+                                  nNc + nLc, nNp + nLp, carry_drop > 0 ? 1 : 0, 1};
 #pragma unroll
-    for (int q = 0; q < kNumStats; ++q) S[kSStats + q] = st[q] + add[q];
-  }
-#pragma unroll
-  for (int q = 0; q < kDWords; ++q) Dd[q] = v[q];
+  for (int q = 0; q < kNumStats; ++q) S[kSStats + q] = st[q] + add[q];
 }
 
-// Pass 2 (one block per channel): block offsets per class; class totals and the host counts.  With ctl.desc (the
-// device-driven step) the last block to finish resolves the step (plan_resolve).
+// The host counts of pass 2 (class totals by class, the dynamic-slot totals, the rows outside [0, R) and the arena
+// tops at plan time), by the thread that holds channel c's total.
+__device__ __forceinline__ void plan_counts_out(const elr_plan_in& p, const elr_plan_out& o, int c, int64_t total) {
+  if (c < kNumCls) o.counts[kClsOfRank[c]] = total;
+  else if (c < kNumCls + 3) o.counts[c] = total;
+  else if (c == kNumCls + kDynCh) o.counts[16] = total;
+  if (c == 0) {
+    o.counts[13] = p.mat_top ? *p.mat_top : 0;
+    o.counts[14] = p.log_top ? *p.log_top : 0;
+    o.counts[15] = p.live ? *p.live : 0;
+  }
+}
+
+// Pass 2 (one block per channel): block offsets per class; class totals and the host counts.
 __global__ __launch_bounds__(kScanBlock) void k_plan_scan(elr_plan_in p, elr_plan_out o, int64_t nbu, int64_t nbd,
                                                           int64_t* __restrict__ bu, int64_t* __restrict__ bd,
-                                                          int64_t* __restrict__ bbad, int64_t* __restrict__ tot,
-                                                          elr_plan_ctl ctl, int64_t* __restrict__ bu2,
-                                                          int64_t* __restrict__ tot2) {
+                                                          int64_t* __restrict__ bbad, int64_t* __restrict__ tot) {
   // one block per channel: the kNumCls class channels, the kDynCh dynamic-slot channels, then the rows outside
   // [0, R), which the caller raises on instead of letting the step skip them
   const int c = blockIdx.x;
   if (c < kNumCls) scan_channels_block(bu + (int64_t)c * nbu, nbu, 1, tot + c);
   else if (c < kNumCls + kDynCh) scan_channels_block(bd + (int64_t)(c - kNumCls) * nbd, nbd, 1, tot + c);
   else scan_channels_block(bbad, nbu, 1, tot + c);
-  if (threadIdx.x == 0) {   // the thread that stored tot[c]
-    if (c < kNumCls) o.counts[kClsOfRank[c]] = tot[c];
-    else if (c < kNumCls + 3) o.counts[c] = tot[c];
-    else if (c == kNumCls + kDynCh) o.counts[16] = tot[c];
-    if (c == 0) {
-      o.counts[13] = p.mat_top ? *p.mat_top : 0;
-      o.counts[14] = p.log_top ? *p.log_top : 0;
-      o.counts[15] = p.live ? *p.live : 0;
+  if (threadIdx.x == 0) plan_counts_out(p, o, c, tot[c]);   // the thread that stored tot[c]
+}
+
+// Pass 2 of the device-driven step, in one block: wave c scans channel c (its loads kScanQ * 64 entries at a time,
+// all in flight together), then the same block resolves the step (plan_resolve) -- no block waits on another and
+// no device-wide fence is needed.  Only the blocks that hold live rows or slots are scanned (the scatter reads no
+// others).
+constexpr int kPlanCh = kNumCls + kDynCh + 1;
+constexpr int kScanQ = 8;
+static_assert(kPlanCh <= kScanBlock / 64, "one wave per channel");
+
+__global__ __launch_bounds__(kScanBlock) void k_plan_scan_dev(elr_plan_in p, elr_plan_out o, int64_t nbu,
+                                                              int64_t nbd, int64_t* __restrict__ bu,
+                                                              int64_t* __restrict__ bd, int64_t* __restrict__ bbad,
+                                                              int64_t* __restrict__ tot, elr_plan_ctl ctl,
+                                                              int64_t* __restrict__ bu2, int64_t* __restrict__ tot2) {
+  __shared__ int64_t stot[kPlanCh];
+  const int lane = threadIdx.x & 63, c = threadIdx.x >> 6;
+  if (c < kPlanCh) {
+    const bool rowch = c < kNumCls || c == kNumCls + kDynCh;
+    const int64_t live = ((rowch ? rows_n(p) : dyn_n(p)) + kPlanBlock - 1) / kPlanBlock, cap = rowch ? nbu : nbd;
+    const int64_t n = live < cap ? live : cap;
+    int64_t* __restrict__ ch = c < kNumCls             ? bu + (int64_t)c * nbu
+                               : c < kNumCls + kDynCh ? bd + (int64_t)(c - kNumCls) * nbd
+                                                      : bbad;
+    int64_t carry = 0;
+    for (int64_t b0 = 0; b0 < n; b0 += 64 * kScanQ) {
+      int x[kScanQ];   // a block's count is at most kPlanBlock
+#pragma unroll
+      for (int q = 0; q < kScanQ; ++q) {
+        const int64_t b = b0 + q * 64 + lane;
+        x[q] = b < n ? (int)ch[b] : 0;
+      }
+#pragma unroll
+      for (int q = 0; q < kScanQ; ++q) {
+        const int64_t b = b0 + q * 64 + lane;
+        const int inc = wave_incl_scan<int>(x[q]);
+        if (b < n) ch[b] = carry + inc - x[q];
+        carry += __shfl(inc, 63, 64);
+      }
+    }
+    if (lane == 0) {
+      tot[c] = carry;
+      stot[c] = carry;
+      plan_counts_out(p, o, c, carry);
     }
   }
-  if (!ctl.desc) return;
-  // the last block to arrive resolves the step: every block's totals are made visible device-wide before it
-  // arrives, and read after the arrival count says all are in (no block waits on another)
-  __shared__ int last;
-  __threadfence();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned long long prev = atomicAdd(reinterpret_cast<unsigned long long*>(ctl.state + kSArrive), 1ull);
-    last = prev == (unsigned long long)(gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  if (threadIdx.x == 0) ctl.state[kSArrive] = 0;   // ready for the next plan's arrivals
-  plan_resolve(p, o, ctl, nbu, tot, bu2, tot2);
+  plan_resolve(p, o, ctl, nbu, stot, bu2, tot2);
 }
 
 // Pass 3: stable scatter by class.
@@ -569,7 +604,8 @@ static int plan_classify_launch(const elr_plan_in& p, const elr_plan_out& o, voi
     seg_partials_visit(*seg, [&](const auto& f, int64_t nb) { launch2(count, nbu + nbd, f, nb, st); });
   else
     launch1(count, nbu + nbd, st);
-  k_plan_scan<<<kNumCls + kDynCh + 1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot, c, bu2, tot2);
+  if (ctl) k_plan_scan_dev<<<1, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot, c, bu2, tot2);
+  else k_plan_scan<<<kPlanCh, kScanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, bbad, tot);
   if (nbu + nbd > 0)
     k_plan_scatter<<<(unsigned)(nbu + nbd), kPlanBlock, 0, st>>>(p, o, nbu, nbd, bu, bd, tot, c.desc, bu2, tot2);
   return launch_status();

@@ -389,7 +389,7 @@ int elr_plan_classify_seg(const elr_plan_in* in, const elr_plan_out* out, void* 
 typedef struct elr_plan_ctl {
   int64_t* state;             /* [ELR_CTL_WORDS] device: 0 free-stack depth, 1 dynamic slots held, 2 error bits,
                                  3 step of the first error, 4-6 its figures (rows out of range, MAT bound, log
-                                 bound), 7 internal (0 between calls), 8-20 statistics (hits, N, L, F, S, admitted,
+                                 bound), 7 unused, 8-20 statistics (hits, N, L, F, S, admitted,
                                  evicted, preempted, overflow, compactions, appends, barriers, steps) */
   int64_t* desc;              /* [ELR_DESC_WORDS] device: the step descriptor */
   int64_t mat_cap;            /* largest MAT row the step may allocate (capacity - 1: the last row is trash) */
