@@ -24,6 +24,7 @@ gap, 134-140 us after 20 ms).  The --mode c1/c3/c4 lines warm up for at least 80
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode headline|copy] [--no-cpu]
 """
 import argparse
+import gc
 import json
 import os
 import sys
@@ -717,11 +718,36 @@ def mode_c4(args):
     return res
 
 
-def mode_c5(args):
-    """Config C5: the whole ELARA step (elara_amd.step) with HBM-resident arenas: 26 tables (vocab log-uniform in
-    [1e3, 4e7]), batch 16,384 x 26 Zipf(1.1), D = 128, pool 337,626 with 321,242 static hot rows, K = 3, evl on.
-    --warmup-c5 untimed steps (the pool fills, kernels load), then --steps-c5 timed steps.  Occurrence gradients:
-    8 resident buffers cycled."""
+def c5_bytes(s, steps, O, U, c_bar, D=128):
+    """Algorithmic bytes of one C5 step, by part, from the timed steps' class statistics s (sums over `steps`), the
+    batch's occurrences O, its unique rows per step U and the mean log entries c_bar an L row replays.  Each part is
+    what its kernels must read and write once, with R = 4 D bytes per vector (a gradient, a log entry) and 3 R per
+    row state (w, m, v):
+      segment sum   the occurrences' gradients and sorted positions read, the per-row sums G written;
+      hits          state read and written, G read, the history record written (glog, R + 8);
+      assembly      the work row written (3 R) per N, L and F row; an L row reads its c log entries, an F row its
+                    MAT record (3 R);
+      update        admitted, compacted and transient rows read work row and G and write their state (to the
+                    pool or the MAT arena); appended rows read G and write a log entry;
+      evictions     the evicted states read from the pool and written to the MAT arena.
+    The planner's and the directory's own arrays (ids, codes, slots, entry ids: a few MB) are left out."""
+    R = 4 * D
+    per = {k: s[k] / steps for k in s}
+    work = per['N'] + per['L'] + per['F']
+    fn = max(work - per['adm'] - per['appends'] - per['compactions'], 0.0)
+    parts = {
+        'segment_sum': O * (R + 4) + U * R,
+        'hits': per['hits'] * (8 * R + 8),
+        'assembly': work * 3 * R + per['L'] * c_bar * R + per['F'] * 3 * R,
+        'update': (per['adm'] + per['compactions'] + fn) * 7 * R + per['appends'] * 2 * R,
+        'evictions': per['ev'] * 6 * R,
+    }
+    return sum(parts.values()), {k: int(v) for k, v in parts.items()}
+
+
+def _c5_run(args, sync_free, sample=8):
+    """One C5 run (see mode_c5); returns the timed figures, the statistics over the timed steps, and the mean log
+    entries per replayed L row sampled over the last `sample` untimed steps (a host read of each sampled plan)."""
     import torch
     from elara_amd import synth
     from elara_amd.step import ElaraStep, run
@@ -741,12 +767,16 @@ def mode_c5(args):
     mat_cap = total * 20_000 + 1_000_000 if host else total * O // 2
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
                    seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=log_cap,
-                   mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl)
+                   mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl, sync_free=sync_free)
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
-    mark = {}
+    mark = {'c': 0, 'nL': 0}
 
     def on_step(s, p):
+        if W - sample < s <= W:   # untimed: the replayed entries of the L rows
+            nL = sum(p.nL)
+            mark['nL'] += nL
+            mark['c'] += int(p.L_cnt[:nL].clamp(min=0, max=3).sum()) if nL else 0
         if s == W:
             torch.cuda.synchronize()
             mark['stats'] = dict(st.stats)
@@ -761,27 +791,63 @@ def mode_c5(args):
     torch.cuda.synchronize()
     el = time.perf_counter() - mark['t0']
     s = {k: v - mark['stats'][k] for k, v in st.stats.items()}
-    uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
-    mt, lt = (int(x) for x in (st.mat_top, st.log_top))
-    where = 'pinned host arenas (capacity tier)' if host else 'HBM-resident arenas'
-    res = _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
-                 {'workload': 'C5 full ELARA step, %s: 26 tables (R=%d), batch 16,384 x 26 '
-                              'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, tabs.R),
-                  'arenas': 'host' if host else 'hbm', 'dir_impl': args.dir_impl, 'mat_top': mt, 'log_top': lt,
-                  'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
-                  'occurrences_per_step': O, 'unique_rows_per_step': uniq / steps, 'dim': D}, None,
-                 extra={'steps_per_s': steps / el, 'stats': s,
-                        'device_driven': st.sync_free,
-                        'syncs_per_step': s['syncs'] / steps,
-                        'host_wait_us_per_step': (st.wait_s - mark['wait']) / steps * 1e6,
-                        'note': 'device_driven: the step\'s counts stay on the GPU (elr_plan_step, '
-                                'elr_step_exec_dev) and the host issues every step without waiting; otherwise '
-                                'host_wait_us_per_step is the time the host waits at the plan\'s synchronisation'})
-    res['dir_check'] = st.dir_check()
-    if not args.no_cpu:
+    out = {'el': el, 'stats': s, 'steps': steps, 'warmup': W, 'O': O, 'D': D, 'R': tabs.R, 'host': host,
+           'c_bar': mark['c'] / mark['nL'] if mark['nL'] else 0.0, 'device_driven': st.sync_free,
+           'wait_us': (st.wait_s - mark['wait']) / steps * 1e6, 'mat_top': int(st.mat_top), 'log_top': int(st.log_top),
+           'dir_check': st.dir_check()}
+    if not args.no_cpu and sync_free:
         ncpu = min(total, 30)
-        res['cpu_baseline'] = cpu_c5_baseline(tabs, static, [b.cpu() for b in batches[:ncpu]], [g.cpu() for g in gs],
-                                              C, D, steps=ncpu - 10, warmup=10)
+        out['cpu_baseline'] = cpu_c5_baseline(tabs, static, [b.cpu() for b in batches[:ncpu]],
+                                              [g.cpu() for g in gs], C, D, steps=ncpu - 10, warmup=10)
+    del st, batches, gs, on_step
+    gc.collect()   # the step and its backend refer to each other
+    torch.cuda.empty_cache()
+    return out
+
+
+def mode_c5(args):
+    """Config C5: the whole ELARA step (elara_amd.step) with HBM-resident arenas: 26 tables (vocab log-uniform in
+    [1e3, 4e7]), batch 16,384 x 26 Zipf(1.1), D = 128, pool 337,626 with 321,242 static hot rows, K = 3, evl on.
+    --warmup-c5 untimed steps (the pool fills, kernels load), then --steps-c5 timed steps.  Occurrence gradients:
+    8 resident buffers cycled.  The line is the device-driven step (no host synchronisation per step); the same
+    workload on the host-planned step (one synchronisation per step, at the plan) is reported beside it."""
+    a = _c5_run(args, True)
+    steps, W, el, s = a['steps'], a['warmup'], a['el'], a['stats']
+    uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
+    byts, parts = c5_bytes(s, steps, a['O'], uniq / steps, a['c_bar'], a['D'])
+    where = 'pinned host arenas (capacity tier)' if a['host'] else 'HBM-resident arenas'
+    res = _line('C5 full ELARA GPU step: unique rows/s (d=128)', uniq / el, 'rows/s', args, steps, W, el,
+                {'workload': 'C5 full ELARA step, %s: 26 tables (R=%d), batch 16,384 x 26 '
+                             'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, a['R']),
+                 'arenas': 'host' if a['host'] else 'hbm', 'dir_impl': args.dir_impl, 'mat_top': a['mat_top'],
+                 'log_top': a['log_top'], 'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
+                 'occurrences_per_step': a['O'], 'unique_rows_per_step': uniq / steps, 'dim': a['D']},
+                byts / 1e9,
+                extra={'steps_per_s': steps / el, 'stats': s,
+                       'device_driven': a['device_driven'],
+                       'syncs_per_step': s['syncs'] / steps,
+                       'bytes_per_step': int(byts), 'bytes_by_part': parts,
+                       'replayed_entries_per_L_row': a['c_bar'],
+                       'note': 'device_driven: one native call per step (elr_step_dev); the plan resolves the step '
+                               'on the GPU and the host issues every step without waiting.  bytes_per_step: the '
+                               'parts\' algorithmic bytes (bench.c5_bytes) from the timed steps\' class counts'})
+    res['dir_check'] = a['dir_check']
+    if 'cpu_baseline' in a:
+        res['cpu_baseline'] = a['cpu_baseline']
+    if not args.host_arenas:
+        h = _c5_run(args, False)
+        hs = h['stats']
+        hu = hs['hits'] + hs['N'] + hs['L'] + hs['F'] + hs['S']
+        hb, _ = c5_bytes(hs, h['steps'], h['O'], hu / h['steps'], h['c_bar'], h['D'])
+        res['host_planned'] = {'ms_per_step': h['el'] / h['steps'] * 1e3, 'value': hu / h['el'],
+                               'syncs_per_step': hs['syncs'] / h['steps'],
+                               'host_wait_us_per_step': h['wait_us'],
+                               'step_GBps': hb * h['steps'] / h['el'] / 1e9,
+                               'step_frac_of_hbm_peak': hb * h['steps'] / h['el'] / 1e9 / HBM_PEAK_GBS,
+                               'dir_check_ok': h['dir_check']['ok'],
+                               'note': 'the same workload on the host-planned step: the host reads the class '
+                                       'counts once per step; the sort of the batch loaded ahead then runs on '
+                                       'its side stream while the host plans'}
     return res
 
 
