@@ -745,6 +745,19 @@ def c5_bytes(s, steps, O, U, c_bar, D=128):
     return sum(parts.values()), {k: int(v) for k, v in parts.items()}
 
 
+def c5_link_bytes(s, steps, c_bar, D=128):
+    """Bytes of one C5 step that cross the host link when the MAT and log arenas are in pinned host memory: the
+    assembly's reads (an L row's c log entries, an F row's MAT record), the update's writes (compacted and
+    transient rows' states into the MAT arena, appended log entries) and the evictions' (a MAT record, or at most
+    K = 3 history entries, per evicted row: 3 R)."""
+    R = 4 * D
+    per = {k: s[k] / steps for k in s}
+    work = per['N'] + per['L'] + per['F']
+    fn = max(work - per['adm'] - per['appends'] - per['compactions'], 0.0)
+    return int(per['L'] * c_bar * R + per['F'] * 3 * R + (per['compactions'] + fn) * 3 * R + per['appends'] * R
+               + per['ev'] * 3 * R)
+
+
 def _c5_run(args, sync_free, sample=8):
     """One C5 run (see mode_c5); returns the timed figures, the statistics over the timed steps, and the mean log
     entries per replayed L row sampled over the last `sample` untimed steps (a host read of each sampled plan)."""
@@ -767,7 +780,8 @@ def _c5_run(args, sync_free, sample=8):
     mat_cap = total * 20_000 + 1_000_000 if host else total * O // 2
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
                    seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=log_cap,
-                   mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl, sync_free=sync_free)
+                   mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl, sync_free=sync_free,
+                   link_stream=bool(host and args.link_stream))
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
     mark = {'c': 0, 'nL': 0}
@@ -811,6 +825,9 @@ def mode_c5(args):
     --warmup-c5 untimed steps (the pool fills, kernels load), then --steps-c5 timed steps.  Occurrence gradients:
     8 resident buffers cycled.  The line is the device-driven step (no host synchronisation per step); the same
     workload on the host-planned step (one synchronisation per step, at the plan) is reported beside it."""
+    # the host link's ceiling first, on streams made before the step's own (streams beyond the hardware queues share
+    # one, which would serialise the two directions)
+    ceil = link_ceiling() if args.host_arenas else None
     a = _c5_run(args, True)
     steps, W, el, s = a['steps'], a['warmup'], a['el'], a['stats']
     uniq = s['hits'] + s['N'] + s['L'] + s['F'] + s['S']
@@ -832,6 +849,15 @@ def mode_c5(args):
                                'on the GPU and the host issues every step without waiting.  bytes_per_step: the '
                                'parts\' algorithmic bytes (bench.c5_bytes) from the timed steps\' class counts'})
     res['dir_check'] = a['dir_check']
+    if a['host']:
+        lb = c5_link_bytes(s, steps, a['c_bar'])
+        gbs = lb * steps / el / 1e9
+        res['host_link'] = {'bytes_per_step': lb, 'GBps': gbs, 'ceiling_GBps': ceil['kernel_both'],
+                            'frac_of_ceiling': gbs / ceil['kernel_both'], 'ceiling': ceil,
+                            'link_stream': bool(args.link_stream),
+                            'note': 'bytes_per_step: bench.c5_link_bytes; ceiling: bench.link_ceiling on this box, '
+                                    'the row kernel reading and writing a pinned host arena in place, both '
+                                    'directions at once'}
     if 'cpu_baseline' in a:
         res['cpu_baseline'] = a['cpu_baseline']
     if not args.host_arenas:
@@ -849,6 +875,76 @@ def mode_c5(args):
                                        'counts once per step; the sort of the batch loaded ahead then runs on '
                                        'its side stream while the host plans'}
     return res
+
+
+def link_ceiling(reps=5):
+    """The host link's own bandwidth on this box, in GB/s: pinned-host <-> HBM copies (hipMemcpyAsync through torch)
+    one way and both ways at once, and the library's row kernel (elr_copy_rows) reading and writing rows of a
+    pinned host arena in place -- the way the capacity tier's kernels reach the arenas -- one way and both at once
+    (two streams of default priority).  Rows: 1536 bytes (a MAT record at d = 128), 2^19 of them at random positions
+    of a 2^20-row arena."""
+    import torch
+    from elara_amd.rows import copy_rows
+    dev = torch.device('cuda:0')
+    nbytes = 1 << 30
+    h = torch.empty(nbytes // 4, dtype=torch.float32, pin_memory=True)
+    h2 = torch.empty(nbytes // 4, dtype=torch.float32, pin_memory=True)
+    d = torch.ones(nbytes // 4, device=dev)
+    d2 = torch.ones(nbytes // 4, device=dev)
+    s1, s2 = torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    def both(f1, f2):
+        def go():
+            cur = torch.cuda.current_stream(dev)
+            s1.wait_stream(cur)
+            s2.wait_stream(cur)
+            with torch.cuda.stream(s1):
+                f1()
+            with torch.cuda.stream(s2):
+                f2()
+            cur.wait_stream(s1)
+            cur.wait_stream(s2)
+        return go
+    out = {}
+    out['copy_h2d'] = nbytes / timed(lambda: d.copy_(h, non_blocking=True)) / 1e9
+    out['copy_d2h'] = nbytes / timed(lambda: h.copy_(d, non_blocking=True)) / 1e9
+    out['copy_both'] = 2 * nbytes / timed(both(lambda: d.copy_(h, non_blocking=True),
+                                               lambda: h2.copy_(d2, non_blocking=True))) / 1e9
+    del h, h2, d, d2
+    D3, nrow, narena = 384, 1 << 19, 1 << 20
+    arena = torch.empty(narena, D3, dtype=torch.float32, pin_memory=True)
+    arena.zero_()
+    rows_in = torch.ones(nrow, D3, device=dev)
+    rows_out = torch.empty(nrow, D3, device=dev)
+    gen = torch.Generator(device='cpu').manual_seed(3)
+    ia = torch.randperm(narena, generator=gen)[:nrow].to(dev)
+    ib = torch.randperm(narena, generator=gen)[:nrow].to(dev)
+    rb = nrow * D3 * 4
+    out['kernel_read'] = rb / timed(lambda: copy_rows(rows_out, None, arena, ia)) / 1e9
+    out['kernel_write'] = rb / timed(lambda: copy_rows(arena, ib, rows_in, None)) / 1e9
+    out['kernel_both'] = 2 * rb / timed(both(lambda: copy_rows(rows_out, None, arena, ia),
+                                            lambda: copy_rows(arena, ib, rows_in, None))) / 1e9
+    del arena, rows_in, rows_out
+    torch.cuda.empty_cache()
+    return out
+
+
+def mode_link(args):
+    """The host link's bandwidth (link_ceiling): the ceiling the capacity-tier C5 line is measured against."""
+    c = link_ceiling()
+    return {'mode': 'link', 'unit': 'GB/s', **{k: round(v, 2) for k, v in c.items()},
+            'note': 'copy_*: hipMemcpyAsync between pinned host memory and HBM (1 GiB); kernel_*: elr_copy_rows '
+                    'reading / writing 1536-byte rows of a pinned host arena in place (2^19 random rows); *_both: '
+                    'the two directions at once on two streams'}
 
 
 def copy_calibration(args):
@@ -922,7 +1018,7 @@ def main():
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=200)
     ap.add_argument('--mode', default='headline',
-                    choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'rows', 'hostsync', 'all'])
+                    choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'rows', 'hostsync', 'link', 'all'])
     ap.add_argument('--rows-order', default='random', choices=['random', 'consecutive'],
                     help='--mode rows: the order of the updated rows')
     ap.add_argument('--steps-c3', type=int, default=100)
@@ -931,6 +1027,9 @@ def main():
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
+    ap.add_argument('--link-stream', action='store_true',
+                    help='C5 with host arenas: the update\'s host-arena writes on a second stream (the host-planned '
+                         'call-by-call step) instead of the one-call step')
     ap.add_argument('--dir-impl', default='cpp', choices=['cpp', 'ref', 'triton'],
                     help="C5's directory allocation order (the reference's --elara-dir-impl; cpp and ref are equal)")
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')
@@ -942,7 +1041,7 @@ def main():
               'an all-to-all of occurrence gradients; not implemented); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     fns = {'headline': headline, 'copy': copy_calibration, 'c1': mode_c1, 'c3': mode_c3, 'c4': mode_c4,
-           'c5': mode_c5, 'rows': mode_rows, 'hostsync': host_sync_costs}
+           'c5': mode_c5, 'rows': mode_rows, 'hostsync': host_sync_costs, 'link': mode_link}
     for m in (['headline', 'c1', 'c3', 'c4', 'c5'] if args.mode == 'all' else [args.mode]):
         res = fns[m](args)
         print(json.dumps(res, default=float), flush=True)

@@ -172,7 +172,8 @@ class ExecArgs(ctypes.Structure):
     _fields_ = [('dir', DirState), ('pv', DirParams), ('s', c_i64), ('b', c_i64 * 11), ('u_ord', c_vp), ('c_ord', c_vp),
                 ('sl_ord', c_vp), ('loc_ord', c_vp), ('L_row', c_vp), ('L_cnt', c_vp), ('slots', SlotsArgs),
                 ('seed', c_u32), ('bound', c_f32), ('table', c_vp), ('recip', c_vp), ('table_rows', c_i64),
-                ('upd', UpdateArgs), ('dir_order', c_i64)]
+                ('upd', UpdateArgs), ('dir_order', c_i64), ('link_stream', c_vp), ('link_start', c_vp),
+                ('link_done', c_vp), ('link_wait', c_vp)]
 
 
 EXEC_OUT_FIELDS = ('L_steps', 'L_ids', 'hrec_dyn', 'hrec_j', 'ev_row', 'rep', 'evl_ids', 'evf_slots', 'ev_dyn',

@@ -218,6 +218,8 @@ inline unsigned grid_for(int64_t units, int64_t per_block, int64_t cap_blocks = 
   return (unsigned)b;
 }
 
+inline int hip_rc(hipError_t e) { return e == hipSuccess ? ELR_OK : (int)e; }
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? ELR_OK : (int)e;

@@ -32,10 +32,12 @@ namespace {
 struct ExecLayout {
   elr_exec_out o;
   int64_t rel_cnt;  // the evictions' deferred release counts (Triton order only)
+  int64_t stage_mat, stage_log;  // with a link stream: the evicted states and histories staged in HBM
   int64_t dir_a_scratch, dir_a_scratch_bytes, dir_b_scratch, dir_b_scratch_bytes, total;
 };
 
 int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
+int64_t cap(int64_t blocks, int64_t lim) { return blocks < lim ? blocks : lim; }
 
 // Byte layout of the workspace for args; false when the bounds are inconsistent.
 bool exec_layout(const elr_exec_args& a, ExecLayout& L) {
@@ -76,6 +78,8 @@ bool exec_layout(const elr_exec_args& a, ExecLayout& L) {
   if (L.dir_a_scratch_bytes < 0 || L.dir_b_scratch_bytes < 0) return false;
   L.dir_a_scratch = take(L.dir_a_scratch_bytes > 0 ? L.dir_a_scratch_bytes : 1);
   L.dir_b_scratch = take(L.dir_b_scratch_bytes > 0 ? L.dir_b_scratch_bytes : 1);
+  L.stage_mat = take(a.link_stream ? nev * 3 * D * 4 : 0);
+  L.stage_log = take(a.link_stream ? nev * K * D * 4 : 0);
   L.total = o;
   return true;
 }
@@ -94,7 +98,7 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   if (!args || !out) return ELR_EINVAL;
   const elr_exec_args& a = *args;
   ExecLayout L;
-  if (!exec_layout(a, L)) return ELR_EINVAL;
+  if (!exec_layout(a, L) || (a.link_stream && (!a.link_start || !a.link_done))) return ELR_EINVAL;
   if (!ws || ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255)) return ELR_ECAPACITY;
   *out = L.o;
   char* w = static_cast<char*>(ws);
@@ -208,7 +212,7 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   u.fn_slot = a.loc_ord + b[ELR_RANK_FN];
   u.s_slot = a.loc_ord + b[ELR_RANK_S];
   u.part = ELR_UPDATE_ALL;
-  u.link_blocks = 0;
+  u.link_blocks = a.link_stream ? a.upd.link_blocks : 0;
   UpdatePrep up;
   if ((rc = update_prep(&u, up))) return rc;
   ExecMulti hx;
@@ -228,10 +232,23 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
                         rel_cnt, at(L.dir_a_scratch));
   exec_visit(up.vpl, D, hx, hblocks, up.s, [&](const auto& f, int64_t nb) { launch2(ep.count, ev_blocks, f, nb, st); });
   if (nev) dir_evict_scan(ep, st);
+  if (a.link_wait && (rc = hip_rc(hipStreamWaitEvent(st, static_cast<hipEvent_t>(a.link_wait), 0)))) return rc;
   if (nw > 0) assemble_visit(g, [&](const auto& f, int64_t nb) { launch2(ep.apply, ev_blocks, f, nb, st); });
   else launch1(ep.apply, ev_blocks, st);
+  hipStream_t lk = static_cast<hipStream_t>(a.link_stream);
+  // with a link stream, the evicted states and histories are staged in HBM here (before the admissions reuse their
+  // slots) and written to the host arenas on the link stream, with the update's other host-arena writes
+  float* stage_mat = lk ? static_cast<float*>(at(L.stage_mat)) : nullptr;
+  float* stage_log = lk ? static_cast<float*>(at(L.stage_log)) : nullptr;
+  const EvictMove& mv = up.move;
+  const EvictMove stage{{stage_mat, nev, IxList{nullptr}, mv.c1.src, mv.c1.src_rows, mv.c1.six, nev, 3 * D, nullptr,
+                         1},
+                        {stage_log, nev * K, IxList{nullptr}, mv.c2.src, mv.c2.src_rows, mv.c2.six, nev * K, D,
+                         nullptr, K},
+                        mv.nb1, mv.nb2, mv.v4 && aligned16(stage_mat) && aligned16(stage_log)};
   if (nev)
-    evict_move_visit(up.move, [&](const auto& f, int64_t nb) { launch2(ep.release, ep.rel_nblk, f, nb, st); });
+    evict_move_visit(lk ? stage : mv,
+                     [&](const auto& f, int64_t nb) { launch2(ep.release, ep.rel_nblk, f, nb, st); });
   // 5-6.
   const int64_t adm_blocks = admit_slots_blocks(sl, n_adm);
   if (na || nc || nr) {
@@ -245,8 +262,28 @@ extern "C" int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_byt
   }
   // 7-8.
   if ((rc = launch_status())) return rc;
-  if ((rc = adam_exec(up, {up.adm, up.tail, up.app}, st))) return rc;
-  return update_s_rows(up, st);
+  if (!lk) {
+    if ((rc = adam_exec(up, {up.adm, up.tail, up.app}, st))) return rc;
+    return update_s_rows(up, st);
+  }
+  // the host-arena writes on the link stream, after everything above
+  if ((rc = adam_exec(up, {up.adm}, st))) return rc;
+  if ((rc = hip_rc(hipEventRecord(static_cast<hipEvent_t>(a.link_start), st))) ||
+      (rc = hip_rc(hipStreamWaitEvent(lk, static_cast<hipEvent_t>(a.link_start), 0))))
+    return rc;
+  if (nev) {   // the staged evictions into the host arenas
+    const CopyPart<IxList, IxList> o1{mv.c1.dst, mv.c1.dst_rows, mv.c1.dix, stage_mat, nev, IxList{nullptr}, nev,
+                                      3 * D, nullptr, 1};
+    const CopyPart<IxList, IxList> o2{mv.c2.dst, mv.c2.dst_rows, mv.c2.dix, stage_log, nev * K, IxList{nullptr},
+                                      nev * K, D, nullptr, K};
+    const int64_t nb1 = cap(mv.nb1, up.lb), nb = nb1 + cap(mv.nb2, up.lb);
+    if (stage.v4) launch1(CopyRows2<true, IxList, IxList, IxList, IxList>{o1, o2, nb1}, nb, lk);
+    else launch1(CopyRows2<false, IxList, IxList, IxList, IxList>{o1, o2, nb1}, nb, lk);
+  }
+  if ((rc = adam_exec(up, {up.tail}, lk, up.lb)) || (rc = adam_exec(up, {up.app}, lk, up.lb)) ||
+      (rc = update_s_rows(up, lk)))
+    return rc;
+  return hip_rc(hipEventRecord(static_cast<hipEvent_t>(a.link_done), lk));
 }
 
 // ---- the device-driven form (elr_step_exec_dev) ------------------------------------------------------------------
@@ -330,7 +367,7 @@ extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc,
   const elr_exec_args& a = *args;
   ExecLayout L;
   DevBounds v;
-  if (!exec_layout_dev(a, L) || !dev_bounds(a, v)) return ELR_EINVAL;
+  if (!exec_layout_dev(a, L) || !dev_bounds(a, v) || a.link_stream || a.link_wait) return ELR_EINVAL;
   if (!ws || ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255)) return ELR_ECAPACITY;
   *out = L.o;
   char* w = static_cast<char*>(ws);

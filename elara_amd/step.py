@@ -137,10 +137,12 @@ class HipBackend:
                             _lib.dptr(es.glog).value)
         return self._arenas[1:]
 
-    def step_exec(self, es, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord):
+    def step_exec(self, es, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord, link=None):
         """ElaraStep's calls after the class-count synchronisation -- directory call A, the admissions with the slot
         bookkeeping, call B, the assembly and the update -- in one native call (elr_step_exec), in that order on the
-        current stream.  Returns the workspace and the offsets of the arrays written there."""
+        current stream.  link (host arenas): (stream, start event, done event, event to wait on before the assembly
+        or None) -- the update's host-arena writes go to that stream.  Returns the workspace and the offsets of the
+        arrays written there."""
         from .elara_dir import _state
         S, P, dev, _ = _state(es.state_list(), es.params())
         pool, mat, logs, glog = self._arena_ptrs(es)
@@ -169,6 +171,11 @@ class HipBackend:
         u.grad = G.data_ptr()
         u.lr, u.b1, u.b2, u.eps = self.hp
         a.dir_order = 1 if es.dir_impl == 'triton' else 0
+        if link is not None:
+            lk, start, done, wait = link
+            a.link_stream, a.link_start, a.link_done = lk.cuda_stream, start.cuda_event, done.cuda_event
+            a.link_wait = wait.cuda_event if wait is not None else None
+            u.link_blocks = int(es.link_blocks)
         L = _lib.lib()
         nb = int(L.elr_step_exec_bytes(ctypes.byref(a)))
         _lib.check(min(nb, 0), 'elr_step_exec_bytes')
@@ -395,7 +402,7 @@ class ElaraStep:
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
                  backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK,
-                 dir_impl='cpp', sync_free=True):
+                 dir_impl='cpp', sync_free=True, link_stream=False):
         d = torch.device(device)
         if dir_impl not in ('cpp', 'ref', 'triton'):
             raise ValueError(f"dir_impl must be 'cpp', 'ref' or 'triton' (got {dir_impl!r})")
@@ -477,16 +484,22 @@ class ElaraStep:
         self.host_arenas = bool(host_arenas and d.type == 'cuda')
         self.mat = torch.empty(self.mat_cap, 3, D, **ad)
         self.logs = torch.empty(self.log_cap + 1, D, **ad)
-        # with host arenas, the update's writes into them (compacted and transient rows into MAT, log appends, S
-        # rows) run on a second stream of default priority while the next step plans and assembles, so the host
-        # link carries both directions at once (update writes, assembly reads).  The next assembly that might read
-        # those rows waits for them: the one two steps later, or the next one if the step overflowed (an
+        # with host arenas and link_stream, the update's writes into them (compacted and transient rows into MAT,
+        # log appends, S rows) run on a second stream of default priority while the next step plans and assembles,
+        # so the host link carries both directions at once (update writes, assembly reads).  The next assembly that
+        # might read those rows waits for them: the one two steps later, or the next one if the step overflowed (an
         # un-admitted row of batch s can reappear in batch s + 1; otherwise a row of batch s + 1 is a hit or admitted
-        # in step s, and the rows the link part writes are neither).
-        self._link = (torch.cuda.Stream(device=d) if self.host_arenas and getattr(self.be, 'step_update', None)
-                      else None)
+        # in step s, and the rows the link part writes are neither)
+        # (link_stream=True; by default the host-arena step runs as the HBM one does, in one native call per step
+        # on one stream, and its kernels reach the host arenas in place)
+        self._link = (torch.cuda.Stream(device=d) if link_stream and self.host_arenas
+                      and getattr(self.be, 'step_update', None) else None)
         self._link_pending = []
-        self.link_blocks = 32   # blocks per launch of the link part (measured best of 16-128 at C5 with host arenas)
+        self._link_start = None
+        if self._link is not None:
+            self._link_start = torch.cuda.Event()
+            self._link_start.record(self._link)   # creates the event the native step records on its stream
+        self.link_blocks = 64   # blocks per launch of the link part (measured best of 32-128 at C5 with host arenas)
         self._stats = {k: 0 for k in ('adm', 'ev', 'hits', 'N', 'L', 'F', 'S', 'overflow', 'preempt',
                                      'compactions', 'appends', 'syncs', 'barriers')}
         self.wait_s = 0.0   # host time spent waiting for the GPU at the plans' synchronisations
@@ -505,11 +518,12 @@ class ElaraStep:
             self.code[self.static_rows] = self.MAT
         # the device-driven step: the plan's counts stay on the GPU (elr_step_dev: the plan resolves the step there
         # and the executor reads the resolution), so the host never waits for a step.  Taken when the backend has
-        # it and nothing needs the host between the plan and the update: arenas in HBM, no host budget (its
-        # accounting reads the arenas' tops), the ring of loaded batches (the next batches are not needed as lists).
+        # it and nothing needs the host between the plan and the update: no link stream (its ordering is kept by
+        # the host), no host budget (its accounting reads the arenas' tops), the ring of loaded batches (the next
+        # batches are not needed as lists).  Host arenas are reached by the same kernels in place.
         self.sync_free = bool(sync_free and getattr(self.be, 'step_dev', None) is not None
                               and self._slots_in_place and self._sync is not None and self.next_bits is not None
-                              and not self.host_arenas and self.host_budget == 0)
+                              and self._link is None and self.host_budget == 0)
         self._ctl_state = None
         self._err_poll = None
         self._polls = 0
@@ -598,6 +612,21 @@ class ElaraStep:
             else:
                 keep.append((s_ev, ev, nxt))
         self._link_pending = keep
+
+    def _link_args(self, p):
+        """The link-stream arguments of a native step with host arenas: the done event it records, and the event its
+        assembly waits for -- the latest pending link update the assembly may read (the rule of assemble), whose
+        predecessors on the link stream are then done too."""
+        wait, keep = None, []
+        for s_ev, ev, nxt in self._link_pending:
+            if s_ev <= p.s - 2 or (s_ev == p.s - 1 and nxt):
+                wait = ev
+            else:
+                keep.append((s_ev, ev, nxt))
+        self._link_pending = keep
+        done = torch.cuda.Event()
+        done.record(self._link)   # creates the event; the step records it again after its link launches
+        return self._link, self._link_start, done, wait
 
     def join_link(self):
         """Make the current stream wait for every pending link-stream update (before reading the arenas)."""
@@ -822,13 +851,19 @@ class ElaraStep:
         # the native executor takes the rest of the step in one call, unless the host must look at the arenas'
         # tops between the directory calls and the update (a host budget this step could reach) or the update's
         # host-arena writes go to the link stream
-        native = (getattr(self.be, 'step_exec', None) is not None and self._link is None and self._slots_in_place
+        native = (getattr(self.be, 'step_exec', None) is not None and self._slots_in_place
                   and g_occ is not None and not (self.host_budget and (mt_hi > self.faulted['mat']
                                                                        or lt_hi > self.faulted['log'])))
         if native:
             if G is None:
                 G = self.be.segsum(g_occ, dplan, n, rank, **sk)
-            p._ws, p._off = self.be.step_exec(self, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord)
+            link = self._link_args(p) if self._link is not None else None
+            p._ws, p._off = self.be.step_exec(self, p, G, ev_slot, keep_dyn, u_ord, c_ord, sl_ord, loc_ord,
+                                              link=link)
+            if link is not None:   # kept until the link stream has read them
+                for t in (p._ws, G, loc_ord):
+                    t.record_stream(self._link)
+                self._link_pending.append((p.s, link[2], p.link_next))
             p._dims = dict(nL=nLa + nLp + nLc, K=K, nh=counts[C_HIT], nev=nev, n_adm=n_adm, na=nNp + nLp,
                            nc=nNc + nLc, nw=b[R_S] - b[R_NADM], D=self.D)
             p._loc_ord = loc_ord

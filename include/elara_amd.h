@@ -589,6 +589,16 @@ typedef struct elr_exec_args {
   int64_t dir_order;          /* log-id allocation order: 0 = elara_dir.cpp's (the reference's default directory,
                                  equal to its torch path), 1 = its Triton path's (as elr_dir_a_deferred followed by
                                  elr_dir_b_release) */
+  void* link_stream;          /* elr_step_exec only (host arenas), or NULL: the update's host-arena writes -- the
+                                 compacted and transient rows into MAT, the log appends, the S rows -- go to this
+                                 hipStream_t, ordered after the rest by link_start (recorded on the call's stream,
+                                 waited on by link_stream), and link_done is recorded after them.  The caller keeps
+                                 the workspace and G until link_done. */
+  void* link_start;           /* hipEvent_t (with link_stream) */
+  void* link_done;            /* hipEvent_t (with link_stream) */
+  void* link_wait;            /* hipEvent_t or NULL: waited on by the call's stream just before the assembly (the
+                                 first launch that reads the arenas), e.g. the link_done of a step whose writes the
+                                 assembly may read */
 } elr_exec_args;
 
 /* Offsets (bytes from ws) of the arrays elr_step_exec writes: elr_dir_a's nine outputs (L_steps, L_ids, hrec_dyn,
@@ -607,7 +617,8 @@ int elr_step_exec(const elr_exec_args* args, void* ws, int64_t ws_bytes, elr_exe
  * bounds are ignored); u_ord, c_ord, sl_ord, loc_ord, L_row, L_cnt are elr_plan_step's outputs (class order, from
  * position 0); slots.ev_slot and slots.keep are its dyn_out, slots.nev bounds the evictions and slots.nkeep the kept
  * slots (both at most Cdyn), slots.n_free the free stack's depth.  The workspace (elr_step_exec_dev_bytes) holds
- * every array at its bound; the arrays' valid prefixes have the descriptor's counts.  The S rows are updated too. */
+ * every array at its bound; the arrays' valid prefixes have the descriptor's counts.  The S rows are updated too.
+ * link_stream and link_wait must be NULL (every launch on the call's stream). */
 int64_t elr_step_exec_dev_bytes(const elr_exec_args* args);
 int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes, elr_exec_out* out,
                       void* stream);
