@@ -781,7 +781,7 @@ def _c5_run(args, sync_free, sample=8):
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
                    seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=log_cap,
                    mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl, sync_free=sync_free,
-                   link_stream=bool(host and args.link_stream))
+                   link_stream=not args.one_stream if host else None)
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
     mark = {'c': 0, 'nL': 0}
@@ -854,7 +854,7 @@ def mode_c5(args):
         gbs = lb * steps / el / 1e9
         res['host_link'] = {'bytes_per_step': lb, 'GBps': gbs, 'ceiling_GBps': ceil['kernel_both'],
                             'frac_of_ceiling': gbs / ceil['kernel_both'], 'ceiling': ceil,
-                            'link_stream': bool(args.link_stream),
+                            'link_stream': not args.one_stream,
                             'note': 'bytes_per_step: bench.c5_link_bytes; ceiling: bench.link_ceiling on this box, '
                                     'the row kernel reading and writing a pinned host arena in place, both '
                                     'directions at once'}
@@ -1027,9 +1027,9 @@ def main():
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
-    ap.add_argument('--link-stream', action='store_true',
-                    help='C5 with host arenas: the update\'s host-arena writes on a second stream (the host-planned '
-                         'call-by-call step) instead of the one-call step')
+    ap.add_argument('--one-stream', action='store_true',
+                    help='C5 with host arenas: the whole step on one stream (device-driven) instead of the update\'s '
+                         'host-arena writes on a link stream beside the next step (host-planned)')
     ap.add_argument('--dir-impl', default='cpp', choices=['cpp', 'ref', 'triton'],
                     help="C5's directory allocation order (the reference's --elara-dir-impl; cpp and ref are equal)")
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')

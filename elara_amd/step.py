@@ -391,7 +391,9 @@ class ElaraStep:
     (srm2/train.py:366); st_mode 'T' (transient full-state updates on the GPU) or 'S' (materialised cold rows
     updated in the MAT arena); log_cap / mat_cap: arena capacities in rows (row log_cap of the log arena and row
     mat_cap - 1 of the MAT arena are trash rows); host_arenas: keep the MAT and log arenas in pinned host memory
-    (the capacity tier, srm2/elara.py:40-103); host_budget: bytes the arenas may hold, accounted as the
+    (the capacity tier, srm2/elara.py:40-103), whose writes go to a link stream unless link_stream is False;
+    sync_free: the device-driven step where it applies (no link stream, no host budget, the ring of loaded
+    batches); host_budget: bytes the arenas may hold, accounted as the
     reference's ArenaStore does (faulted in chunks of budget_chunk bytes up to each arena's top; 0: no budget),
     HostBudgetExceeded when a step would pass it (srm2/elara.py:63-81); dir_impl: the log-id allocation order of
     the reference directory it stands in for (srm2/elara.py:150-155, srm2/train.py:133): 'cpp' (the default) or
@@ -402,7 +404,7 @@ class ElaraStep:
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
                  backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK,
-                 dir_impl='cpp', sync_free=True, link_stream=False):
+                 dir_impl='cpp', sync_free=True, link_stream=None):
         d = torch.device(device)
         if dir_impl not in ('cpp', 'ref', 'triton'):
             raise ValueError(f"dir_impl must be 'cpp', 'ref' or 'triton' (got {dir_impl!r})")
@@ -490,8 +492,10 @@ class ElaraStep:
         # might read those rows waits for them: the one two steps later, or the next one if the step overflowed (an
         # un-admitted row of batch s can reappear in batch s + 1; otherwise a row of batch s + 1 is a hit or admitted
         # in step s, and the rows the link part writes are neither)
-        # (link_stream=True; by default the host-arena step runs as the HBM one does, in one native call per step
-        # on one stream, and its kernels reach the host arenas in place)
+        # (link_stream None: on with host arenas; False: the host-arena step runs as the HBM one does, on one
+        # stream -- device-driven when nothing else needs the host)
+        if link_stream is None:
+            link_stream = self.host_arenas
         self._link = (torch.cuda.Stream(device=d) if link_stream and self.host_arenas
                       and getattr(self.be, 'step_update', None) else None)
         self._link_pending = []

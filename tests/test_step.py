@@ -25,7 +25,7 @@ def make(cfg, device, backend=None):
                      log_cap=cfg['log_cap'], mat_cap=cfg['mat_cap'], device=device, backend=backend,
                      host_arenas=cfg.get('host', False), dyn=cfg.get('dyn', 'ttl'), host_budget=cfg.get('budget', 0),
                      budget_chunk=cfg.get('chunk', 64 << 20), dir_impl=cfg.get('dir_impl', 'cpp'),
-                     sync_free=cfg.get('sync_free', True), link_stream=cfg.get('link', False))
+                     sync_free=cfg.get('sync_free', True), link_stream=cfg.get('link'))
 
 
 def same_stats(a, b):
@@ -138,8 +138,9 @@ def test_step_raises_on_rows_out_of_range(where, request):
                                   'triton_hostsync', 'carry_overflow', 'triton_overflow_S', 'host_arenas_hostsync'])
 def test_gpu_step_matches_oracle_step(dev, name):
     """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
-    kernels over the host link -- by the device-driven step, by the native host-planned one (*_hostsync), or with
-    the update's host-arena writes on a link stream (host_arenas_overflow, carry_overflow_host, triton_host_S).  L40_no_ring: a look-ahead too long for the 32-bit ring of loaded batches, so the
+    kernels over the host link -- with the update's host-arena writes on a link stream (the default:
+    host_arenas_overflow, carry_overflow_host, triton_host_S), by the device-driven step on one stream (host_arenas,
+    host_arenas_S), or by the native host-planned step on one stream (host_arenas_hostsync).  L40_no_ring: a look-ahead too long for the 32-bit ring of loaded batches, so the
     planner searches the next batches' sorted rows instead.  D32_K8, D96, D200_K5_S: widths the wave-per-row
     kernels do not take (the generic assembly and update kernels, srm2/gpu_ops.py:97 takes any D) and up to K = 8
     log entries per row.  carry*: carry residency (srm2/train.py:43 elara_carry); evl_gate: the representation
@@ -152,15 +153,15 @@ def test_gpu_step_matches_oracle_step(dev, name):
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
     kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
-          'host_arenas': {'host': True}, 'host_arenas_S': {'host': True, 'st': 'S'},
-          'host_arenas_overflow': {'host': True, 'C': 2000, 'link': True},
-          'host_arenas_hostsync': {'host': True, 'sync_free': False},
+          'host_arenas': {'host': True, 'link': False}, 'host_arenas_S': {'host': True, 'st': 'S', 'link': False},
+          'host_arenas_overflow': {'host': True, 'C': 2000},
+          'host_arenas_hostsync': {'host': True, 'sync_free': False, 'link': False},
           'D64_K2': {'D': 64, 'K': 2, 'kthr': 2}, 'D256_K4': {'D': 256, 'K': 4, 'kthr': 3},
           'K1_kthr0': {'K': 1, 'kthr': 0}, 'L40_no_ring': {'L': 40}, 'D32_K8': {'D': 32, 'K': 8, 'kthr': 6},
           'D96': {'D': 96}, 'D200_K5_S': {'D': 200, 'K': 5, 'kthr': 4, 'st': 'S'}, 'carry': {'dyn': 'carry'},
-          'carry_overflow_host': {'dyn': 'carry', 'C': 1800, 'host': True, 'link': True},
+          'carry_overflow_host': {'dyn': 'carry', 'C': 1800, 'host': True},
           'evl_gate': {'evl': 2, 'budget': 14_000_000, 'chunk': 64 << 10}, 'triton': {'dir_impl': 'triton'},
-          'triton_host_S': {'dir_impl': 'triton', 'host': True, 'st': 'S', 'kthr': 2, 'link': True},
+          'triton_host_S': {'dir_impl': 'triton', 'host': True, 'st': 'S', 'kthr': 2},
           'small_overflow_hostsync': {'C': 2000, 'sync_free': False}, 'triton_hostsync': {'dir_impl': 'triton',
                                                                                           'sync_free': False},
           'carry_overflow': {'dyn': 'carry', 'C': 1800}, 'triton_overflow_S': {'dir_impl': 'triton', 'C': 2000,
@@ -177,9 +178,10 @@ def test_gpu_step_matches_oracle_step(dev, name):
     assert same_stats(g, c), (g.stats, c.stats)
     if g.sync_free:   # the device-driven step: no host synchronisation in the steps (one at the end of the run)
         assert g.stats['syncs'] <= 1, g.stats
-    assert g.sync_free == (not cfg.get('link') and not cfg.get('budget') and name != 'L40_no_ring'
+    link = cfg.get('host', False) if cfg.get('link') is None else cfg['link']   # the default: on with host arenas
+    assert (g._link is not None) == link, name
+    assert g.sync_free == (not link and not cfg.get('budget') and name != 'L40_no_ring'
                            and cfg.get('sync_free', True)), name
-    assert (g._link is not None) == bool(cfg.get('link')), name
     if name in ('host_arenas_overflow', 'carry_overflow_host'):
         assert g.stats['overflow'] > 0 and g._link is not None, g.stats
     if name == 'carry_overflow_host':
@@ -236,7 +238,7 @@ def test_gpu_native_update_matches_python_update(dev, name):
         step_dev = None
 
     print(f'[gpu-test] native update {name}', flush=True)
-    kw = {'evl': {}, 'no_evl_S': {'evl': False, 'st': 'S'}, 'host_arenas': {'host': True, 'link': True}}[name]
+    kw = {'evl': {}, 'no_evl_S': {'evl': False, 'st': 'S'}, 'host_arenas': {'host': True}}[name]
     cfg = config(T=6, lo=200, hi=20000, B=1000, steps=30, **{'C': 2500, 'n_static': 1500, **kw})
     a = make(cfg, dev)
     b = make(cfg, dev, CallByCall(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2, dev))
