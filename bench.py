@@ -437,8 +437,8 @@ def headline(args):
         'config': {'workload': 'C2 exact replay (262,144 rows x d=128, k~U{1,2,3}, gaps U{1..50}) + one '
                                'row-sparse Adam step on the materialised rows', 'rows_per_step': n, 'dim': D,
                    'kmax': K, 'log_entries': nlog, 'parallelism': 'single GPU'},
-        'roofline': {'bound': 'hbm', 'kernel': 'elr::k_replay_wpr<2, 3, 2>', 'achieved': rep_gbs, 'peak': HBM_PEAK_GBS,
-                     'unit': 'GB/s', 'frac': rep_gbs / HBM_PEAK_GBS, 'traffic': _traffic('elr::k_replay_wpr<2, 3, 2>'),
+        'roofline': {'bound': 'hbm', 'kernel': 'elr::k_replay_wpr<2, 3, 1>', 'achieved': rep_gbs, 'peak': HBM_PEAK_GBS,
+                     'unit': 'GB/s', 'frac': rep_gbs / HBM_PEAK_GBS, 'traffic': _traffic('elr::k_replay_wpr<2, 3, 1>'),
                      'algorithmic_bytes_per_launch': rb, 'mean_launch_ms': rep_ms,
                      'median_launch_ms': float(np.median(rep_all)), 'launches_timed': len(rep_all)},
         'kernels': {'replay': {'ms': rep_ms, 'GBps': rep_gbs, 'bytes': rb, 'ms_first': rep_all[0]},

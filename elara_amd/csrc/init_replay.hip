@@ -155,7 +155,9 @@ __global__ __launch_bounds__(256) void k_replay_scalar(float* __restrict__ out, 
 }
 
 // ---- wave-per-row kernels (D = 64*VPL) ------------------------------------------------------------------------------
-constexpr int kReplayRowsPerWave = 2;
+// Rows per wave of the replay: one (at C2, 262,144 x 128: 0.3-1% faster per launch than two, same box and run;
+// four is 4-5% slower).  Its loads are issued before its arithmetic either way.
+constexpr int kReplayRowsPerWave = 1;
 constexpr int kInitRowsPerWave = 2;
 
 template <int VPL, int U>
