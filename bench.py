@@ -860,7 +860,7 @@ def mode_c5(args):
                                     'directions at once'}
     if 'cpu_baseline' in a:
         res['cpu_baseline'] = a['cpu_baseline']
-    if not args.host_arenas:
+    if not args.host_arenas and args.c5_host_planned:
         h = _c5_run(args, False)
         hs = h['stats']
         hu = hs['hits'] + hs['N'] + hs['L'] + hs['F'] + hs['S']
@@ -1027,6 +1027,8 @@ def main():
     ap.add_argument('--steps-c5', type=int, default=200)
     ap.add_argument('--warmup-c5', type=int, default=100)
     ap.add_argument('--host-arenas', action='store_true', help='C5 with the MAT and log arenas in pinned host memory')
+    ap.add_argument('--c5-host-planned', action=argparse.BooleanOptionalAction, default=True,
+                    help='C5: also run the host-planned step on the same workload (reported under host_planned)')
     ap.add_argument('--one-stream', action='store_true',
                     help='C5 with host arenas: the whole step on one stream (device-driven) instead of the update\'s '
                          'host-arena writes on a link stream beside the next step (host-planned)')
