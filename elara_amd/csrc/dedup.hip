@@ -103,10 +103,12 @@ __device__ __forceinline__ void bins_excl_scan(const int (&x)[BPT], int (&ex)[BP
   total = tot[0];
 }
 
-// One block per digit: exclusive scan of that digit's per-tile counts (in place) and the digit's total.
-__global__ __launch_bounds__(kScanBlock) void k_radix_hist_scan(int64_t* __restrict__ hist, int64_t ntile,
-                                                                int64_t* __restrict__ dtot) {
-  scan_channels_block(hist + (int64_t)blockIdx.x * ntile, ntile, 1, dtot + blockIdx.x);
+// One block per digit: exclusive scan of that digit's per-tile counts (in place) and the digit's total.  Blocks of
+// kSortThreads: a few hundred tiles take one to four rounds, and the small blocks find room beside the other
+// stream's kernels, where 1024-thread blocks wait for a whole CU's wave slots.
+__global__ __launch_bounds__(kSortThreads) void k_radix_hist_scan(int64_t* __restrict__ hist, int64_t ntile,
+                                                                  int64_t* __restrict__ dtot) {
+  scan_channels_block<kSortThreads>(hist + (int64_t)blockIdx.x * ntile, ntile, 1, dtot + blockIdx.x);
 }
 
 // One block: exclusive scan of per-block counts in place, total to *tot (and to *tot2 when given).
@@ -782,12 +784,12 @@ static void radix_pass(const int64_t* ids, int64_t n, int p, int cur, int nxt, D
   Key* kb[2] = {(Key*)S.keys[0], (Key*)S.keys[1]};
   if (p == 0) {
     k_radix_hist<int64_t, Key, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
-    k_radix_hist_scan<<<1u << RB, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
+    k_radix_hist_scan<<<1u << RB, kSortThreads, 0, st>>>(S.hist, ntile, S.dtot);
     k_radix_scatter<int64_t, Key, true, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(
         ids, nullptr, n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
   } else {
     k_radix_hist<Key, Key, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
-    k_radix_hist_scan<<<1u << RB, kScanBlock, 0, st>>>(S.hist, ntile, S.dtot);
+    k_radix_hist_scan<<<1u << RB, kSortThreads, 0, st>>>(S.hist, ntile, S.dtot);
     k_radix_scatter<Key, Key, false, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(
         kb[cur], S.vals[cur], n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
   }

@@ -50,21 +50,22 @@ __device__ __forceinline__ void block_excl_scan(const int (&v)[NCH], int (&ex)[N
 }
 
 // In-place exclusive scan of `nch` channels of `n` int64 values each (channel c at bsum[c*n .. c*n+n)), by one
-// block of kScanBlock threads; channel totals to tot[c] (device memory) when tot is not null.
+// block of NT threads; channel totals to tot[c] (device memory) when tot is not null.
+template <int NT = kScanBlock>
 __device__ __forceinline__ void scan_channels_block(int64_t* __restrict__ bsum, int64_t n, int nch,
                                                     int64_t* __restrict__ tot) {
-  __shared__ int64_t wtot[kScanBlock / 64];
+  __shared__ int64_t wtot[NT / 64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int c = 0; c < nch; ++c) {
     int64_t carry = 0;
-    for (int64_t b0 = 0; b0 < n; b0 += kScanBlock) {
+    for (int64_t b0 = 0; b0 < n; b0 += NT) {
       const int64_t b = b0 + threadIdx.x;
       const int64_t x = b < n ? bsum[c * n + b] : 0;
       const int64_t inc = wave_incl_scan<int64_t>(x);
       if (lane == 63) wtot[w] = inc;
       __syncthreads();
       int64_t base = 0, all = 0;
-      for (int q = 0; q < kScanBlock / 64; ++q) {
+      for (int q = 0; q < NT / 64; ++q) {
         base += q < w ? wtot[q] : 0;
         all += wtot[q];
       }
