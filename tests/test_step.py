@@ -135,7 +135,8 @@ def test_step_raises_on_rows_out_of_range(where, request):
                                   'host_arenas_S', 'host_arenas_overflow', 'D64_K2', 'D256_K4', 'K1_kthr0',
                                   'L40_no_ring', 'D32_K8', 'D96', 'D200_K5_S', 'carry', 'carry_overflow_host',
                                   'evl_gate', 'triton', 'triton_host_S', 'small_overflow_hostsync',
-                                  'triton_hostsync', 'carry_overflow', 'triton_overflow_S', 'host_arenas_hostsync'])
+                                  'triton_hostsync', 'carry_overflow', 'triton_overflow_S', 'host_arenas_hostsync',
+                                  'hot_ids', 'small_batch'])
 def test_gpu_step_matches_oracle_step(dev, name):
     """host_arenas*: the MAT and log arenas in pinned host memory (the capacity tier), read and written by the
     kernels over the host link -- with the update's host-arena writes on a link stream (the default:
@@ -149,7 +150,9 @@ def test_gpu_step_matches_oracle_step(dev, name):
     arenas and a link stream, through the call-by-call directory entry points.  Every configuration without a link
     stream, a host budget or a look-ahead beyond the ring runs the device-driven step (elr_step_dev: one native call and no host
     synchronisation per step, overflow and preemption resolved on the GPU); *_hostsync run the step that reads its
-    class counts on the host instead."""
+    class counts on the host instead.  hot_ids: ids of more than 240 occurrences in a batch (the segment
+    sum's hot segments, summed from their partial chunks only); small_batch: 2,400 occurrences per batch (ATen's
+    windowed order, no partial chunks)."""
     from elara_amd.step import run
     print(f'[gpu-test] elara step {name}', flush=True)
     kw = {'small_evl': {}, 'small_no_evl': {'evl': False}, 'small_S': {'st': 'S'}, 'small_overflow': {'C': 2000},
@@ -165,8 +168,9 @@ def test_gpu_step_matches_oracle_step(dev, name):
           'small_overflow_hostsync': {'C': 2000, 'sync_free': False}, 'triton_hostsync': {'dir_impl': 'triton',
                                                                                           'sync_free': False},
           'carry_overflow': {'dyn': 'carry', 'C': 1800}, 'triton_overflow_S': {'dir_impl': 'triton', 'C': 2000,
-                                                                               'st': 'S', 'kthr': 2}}[name]
-    cfg = config(T=6, lo=200, hi=20000, B=1000, steps=40, **{'C': 2500, 'n_static': 1500, **kw})
+                                                                               'st': 'S', 'kthr': 2},
+          'hot_ids': {'lo': 30, 'B': 1500}, 'small_batch': {'B': 400}}[name]
+    cfg = config(**{'T': 6, 'lo': 200, 'hi': 20000, 'B': 1000, 'steps': 40, 'C': 2500, 'n_static': 1500, **kw})
     g = make(cfg, dev)
     assert (g.next_bits is None) == (name == 'L40_no_ring')
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
