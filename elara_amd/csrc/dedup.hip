@@ -5,14 +5,16 @@
 // aten.embedding_dense_backward (srm2/train.py:429), and gives config C3 its fused form (dedup, fixed-order
 // segment sum, Adam on each unique row).
 //
-// Sort.  Stable LSD radix sort of (id, occurrence index) pairs, 8-bit digits, ceil(key_bits / 8) passes, keys held
-// as uint32 when key_bits <= 32.  Each pass is three launches: per-tile digit histograms (tiles of 4096 keys, or
-// 1024 below 2^21 keys), one block per digit scanning that digit's per-tile counts, and a scatter in which each
-// key's rank among equal digits of its tile comes from wave ballots (peer mask of the 8 digit bits), a per-wave
-// running count in LDS and a scan over the tile's waves, so equal keys keep their occurrence order.
+// Sort.  Stable LSD radix sort of (id, occurrence index) pairs, 8-bit digits, ceil(key_bits / 8) passes (or one
+// pass fewer with 9- or 10-bit digits), keys held as uint32 when key_bits <= 32.  Tiles of 4096 keys, or 1024 below
+// 2^21 keys.  A pass is three launches: per-tile digit histograms, a wave per digit scanning that digit's per-tile
+// counts, and a scatter in which each key's rank among equal digits of its tile comes from wave ballots (peer mask
+// of the digit bits), a per-wave running count in LDS and a scan over the tile's waves, so equal keys keep their
+// occurrence order.
 //
-// Segments.  Sorted position i starts a segment when its key differs from position i-1; a scan of those heads
-// gives every position its unique index (the inverse) and every unique id its first position.
+// Segments.  Sorted position i starts a segment when its key differs from position i-1; per-block head counts,
+// then a launch in which each block adds up the counts of the blocks before it, gives every position its unique
+// index (the inverse) and every unique id its first position.  The extra-chunk plan is laid out the same way.
 //
 // Summation order: ATen's, as torch.ops.aten.embedding_dense_backward computes it on this GPU
 // (aten/src/ATen/native/cuda/Embedding.cu embedding_dense_backward_cuda and EmbeddingBackwardKernel.cu, PyTorch
@@ -103,19 +105,33 @@ __device__ __forceinline__ void bins_excl_scan(const int (&x)[BPT], int (&ex)[BP
   total = tot[0];
 }
 
-// One block per digit: exclusive scan of that digit's per-tile counts (in place) and the digit's total.  Blocks of
-// kSortThreads: a few hundred tiles take one to four rounds, and the small blocks find room beside the other
-// stream's kernels, where 1024-thread blocks wait for a whole CU's wave slots.
+// One wave per digit: exclusive scan of that digit's per-tile counts (in place) and the digit's total.  The wave
+// loads up to 512 counts (8 per lane) before it scans them, so a few hundred tiles cost one round of loads; no
+// block barrier.
 __global__ __launch_bounds__(kSortThreads) void k_radix_hist_scan(int64_t* __restrict__ hist, int64_t ntile,
-                                                                  int64_t* __restrict__ dtot) {
-  scan_channels_block<kSortThreads>(hist + (int64_t)blockIdx.x * ntile, ntile, 1, dtot + blockIdx.x);
-}
-
-// One block: exclusive scan of per-block counts in place, total to *tot (and to *tot2 when given).
-__global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict__ bsum, int64_t n,
-                                                            int64_t* __restrict__ tot, int64_t* __restrict__ tot2) {
-  scan_channels_block(bsum, n, 1, tot);
-  if (tot2 && threadIdx.x == 0) *tot2 = *tot;   // the thread that stored *tot
+                                                                  int nbins, int64_t* __restrict__ dtot) {
+  constexpr int kWaves = kSortThreads / 64, kPer = 8;
+  const int lane = threadIdx.x & 63;
+  const int d = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (d >= nbins) return;
+  int64_t* h = hist + (int64_t)d * ntile;
+  int64_t carry = 0;
+  for (int64_t g0 = 0; g0 < ntile; g0 += 64 * kPer) {
+    int64_t x[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int64_t b = g0 + k * 64 + lane;
+      x[k] = b < ntile ? h[b] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int64_t b = g0 + k * 64 + lane;
+      const int64_t inc = wave_incl_scan<int64_t>(x[k]);
+      if (b < ntile) h[b] = carry + inc - x[k];
+      carry += __shfl(inc, 63, 64);
+    }
+  }
+  if (lane == 0) dtot[d] = carry;
 }
 
 // Stable scatter of one pass.  FIRST: the source keys are the caller's int64 ids and the values are their
@@ -144,6 +160,17 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
   __shared__ Key lk[TILE];
   __shared__ int32_t lv[TILE];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int64_t tile0 = (int64_t)blockIdx.x * TILE, base = tile0 + (int64_t)w * (ITEMS * 64);
+  // the tile's items first, so that their loads overlap the digit bases' loads and scan
+  Key kk[ITEMS];
+  int32_t vv[ITEMS];
+#pragma unroll
+  for (int r = 0; r < ITEMS; ++r) {
+    const int64_t pos = base + (int64_t)r * 64 + lane;
+    const bool valid = pos < n;
+    kk[r] = valid ? (Key)src_keys[pos] : (Key)0;
+    vv[r] = valid ? (FIRST ? (int32_t)pos : src_vals[pos]) : 0;
+  }
   {
     // digit bases: exclusive scan of the digit totals (n < 2^31, so they fit in int)
     int x[BPT], ex[BPT], total;
@@ -158,18 +185,12 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_scatter(const Src* __res
 #pragma unroll
     for (int j = 0; j < BPT; ++j) wc[q][t * BPT + j] = 0;
   __syncthreads();
-  const int64_t tile0 = (int64_t)blockIdx.x * TILE, base = tile0 + (int64_t)w * (ITEMS * 64);
-  Key kk[ITEMS];
-  int32_t vv[ITEMS];
   int rk[ITEMS];
 #pragma unroll
   for (int r = 0; r < ITEMS; ++r) {
     const int64_t pos = base + (int64_t)r * 64 + lane;
     const bool valid = pos < n;
-    const Key k = valid ? (Key)src_keys[pos] : (Key)0;
-    kk[r] = k;
-    vv[r] = valid ? (FIRST ? (int32_t)pos : src_vals[pos]) : 0;
-    const uint32_t d = digit_of<RB>(k, shift);
+    const uint32_t d = digit_of<RB>(kk[r], shift);
     uint64_t m = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < RB; ++b) {
@@ -254,17 +275,35 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_count(const Key* __restrict__
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
 
-// Segment heads: unique ids, segment starts (seg_start[U] = n), each segment's first occurrence index and the
-// inverse.
+// Sum of cnt[0 .. b) over the whole block, returned to every thread: the offset of block b from the per-block
+// counts of the launch before, without a scan launch in between (b is at most a few thousand).
+__device__ __forceinline__ int64_t block_offset(const int64_t* __restrict__ cnt, int64_t b) {
+  __shared__ int64_t wpart[kSegBlock / 64];
+  int64_t x = 0;
+  for (int64_t i = threadIdx.x; i < b; i += kSegBlock) x += cnt[i];
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+  if ((threadIdx.x & 63) == 0) wpart[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int64_t t = 0;
+#pragma unroll
+  for (int q = 0; q < kSegBlock / 64; ++q) t += wpart[q];
+  __syncthreads();   // wpart is reused by the caller's next call
+  return t;
+}
+
+// Segment heads: unique ids, segment starts, each segment's first occurrence index and the inverse.  The block's
+// first segment index is the sum of the earlier blocks' head counts (k_seg_count); the last block stores U to d_U
+// (and n_unique) and seg_start[U] = n.
 template <typename Key, int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__ sk, const int32_t* __restrict__ sv,
-                                                         int64_t n, const int64_t* __restrict__ boff,
-                                                         const int64_t* __restrict__ d_U,
+                                                         int64_t n, const int64_t* __restrict__ bcnt,
+                                                         int64_t* __restrict__ d_U, int64_t* __restrict__ n_unique,
                                                          int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
                                                          int32_t* __restrict__ seg_occ0,
                                                          int64_t* __restrict__ inverse) {
   const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
-  int64_t before = boff[blockIdx.x];   // heads in earlier positions of the tile's earlier rounds
+  int64_t before = block_offset(bcnt, blockIdx.x);   // heads in earlier positions of the tile's earlier rounds
   for (int r = 0; r < ITEMS; ++r) {
     const int64_t i = base + (int64_t)r * kSegBlock;
     const int f = is_head(sk, i, n);
@@ -283,7 +322,11 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__
     before += tot[0];
     __syncthreads();   // block_excl_scan's LDS is reused by the next round
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0) seg_start[*d_U] = n;
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) {
+    *d_U = before;
+    if (n_unique) *n_unique = before;
+    seg_start[before] = n;
+  }
 }
 
 // Sort path.  A segment of more than kHotLen occurrences is hot: the partial-chunk kernel sums all of its runs (its
@@ -311,18 +354,19 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_count(const int64_t* __rest
 }
 
 // chunk_off[u] = first work item of segment u's partial chunks; chunk_seg[item] = u; hot segments are listed in
-// hot_list[0 .. *d_hot) (in no particular order: each is summed on its own).
+// hot_list[0 .. *d_hot) (in no particular order: each is summed on its own).  The block's first work item is the sum
+// of the earlier blocks' counts (k_chunk_count); the last block stores the number of work items to *d_E.
 template <int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __restrict__ seg_start,
                                                            const int64_t* __restrict__ d_U,
-                                                           const int64_t* __restrict__ boff,
+                                                           const int64_t* __restrict__ bcnt,
                                                            int32_t* __restrict__ chunk_off,
                                                            int32_t* __restrict__ chunk_seg,
                                                            int32_t* __restrict__ hot_list,
-                                                           int64_t* __restrict__ d_hot) {
+                                                           int64_t* __restrict__ d_hot, int64_t* __restrict__ d_E) {
   const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   const int64_t U = *d_U;
-  int64_t before = boff[blockIdx.x];
+  int64_t before = block_offset(bcnt, blockIdx.x);
   for (int r = 0; r < ITEMS; ++r) {
     const int64_t u = base + (int64_t)r * kSegBlock;
     const int e = extra_chunks(seg_start, u, U);
@@ -338,6 +382,7 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __rest
     before += tot[0];
     __syncthreads();
   }
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *d_E = before;
 }
 
 // Does occurrence k of a segment (occurrence index o, previous one prev) start a new group?  Sort path
@@ -720,7 +765,7 @@ inline int64_t al256(int64_t b) { return (b + 255) & ~int64_t(255); }
 struct DedupScratch {
   void* keys[2];
   int32_t* vals[2];
-  int64_t* hist;      // [256 * ntile], ntile = n / (kSortThreads * items_for(n)) rounded up
+  int64_t* hist;      // [kRadixMaxBins * ntile], ntile = n / (kSortThreads * items_for(n)) rounded up
   int64_t* dtot;      // [256] digit totals
   int64_t* bsum;      // [n / (kSegBlock * items_for(n)) + 1]
   int64_t* d_tot;     // [3]: U, E (partial chunks), hot segments
@@ -781,15 +826,17 @@ template <typename Key, int ITEMS, int RB>
 static void radix_pass(const int64_t* ids, int64_t n, int p, int cur, int nxt, DedupScratch& S, hipStream_t st) {
   const int64_t ntile = cdiv(n, kSortThreads * ITEMS);
   const int shift = RB * p;
+  constexpr int BINS = 1 << RB;
+  constexpr unsigned kScanGrid = (unsigned)(BINS / (kSortThreads / 64));   // a wave per digit
   Key* kb[2] = {(Key*)S.keys[0], (Key*)S.keys[1]};
   if (p == 0) {
     k_radix_hist<int64_t, Key, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(ids, n, shift, S.hist, ntile);
-    k_radix_hist_scan<<<1u << RB, kSortThreads, 0, st>>>(S.hist, ntile, S.dtot);
+    k_radix_hist_scan<<<kScanGrid, kSortThreads, 0, st>>>(S.hist, ntile, BINS, S.dtot);
     k_radix_scatter<int64_t, Key, true, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(
         ids, nullptr, n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
   } else {
     k_radix_hist<Key, Key, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(kb[cur], n, shift, S.hist, ntile);
-    k_radix_hist_scan<<<1u << RB, kSortThreads, 0, st>>>(S.hist, ntile, S.dtot);
+    k_radix_hist_scan<<<kScanGrid, kSortThreads, 0, st>>>(S.hist, ntile, BINS, S.dtot);
     k_radix_scatter<Key, Key, false, ITEMS, RB><<<(unsigned)ntile, kSortThreads, 0, st>>>(
         kb[cur], S.vals[cur], n, shift, S.hist, S.dtot, ntile, kb[nxt], S.vals[nxt]);
   }
@@ -827,9 +874,8 @@ static int dedup_core_items(const int64_t* ids, int64_t n, int key_bits, DedupSc
   const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
   int64_t* uniq = uniq_out ? uniq_out : S.uniq;
   k_seg_count<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
-  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot, n_unique);
-  k_seg_apply<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, uniq, S.seg_start,
-                                                                S.seg_occ0, inverse);
+  k_seg_apply<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, n_unique, uniq,
+                                                                S.seg_start, S.seg_occ0, inverse);
   return cur;
 }
 
@@ -848,9 +894,8 @@ template <int ITEMS>
 static void chunk_plan_items(int64_t n, DedupScratch& S, hipStream_t st) {
   const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
   k_chunk_count<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.d_tot + 2);
-  k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk, S.d_tot + 1, nullptr);
   k_chunk_apply<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.chunk_off,
-                                                             S.chunk_seg, S.hot_list, S.d_tot + 2);
+                                                             S.chunk_seg, S.hot_list, S.d_tot + 2, S.d_tot + 1);
 }
 
 static void chunk_plan(int64_t n, DedupScratch& S, hipStream_t st) {

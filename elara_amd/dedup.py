@@ -94,10 +94,21 @@ def unique_plan(ids, D, bound=None):
     return u, plan
 
 
-def unique_plan_async(ids, D, bound=None, nu_out=None):
+def plan_bytes(n, D):
+    """Bytes of the plan buffer of a batch of n ids for gradients of width D (elr_dedup_plan_bytes)."""
+    nbytes = int(_lib.lib().elr_dedup_plan_bytes(int(n), int(D)))
+    if nbytes < 0:
+        _lib.check(nbytes, 'elr_dedup_plan_bytes')
+    return nbytes
+
+
+def unique_plan_async(ids, D, bound=None, nu_out=None, out=None):
     """unique_plan without reading the unique count: returns (u_full, plan, nu) with u_full [n] whose first nu
     entries are the unique ids, nu the count on the device (None when n == 0).  Set plan.U once nu is known.
-    nu_out (int64 [1] on the device, optional): where the count goes, else a new tensor."""
+    nu_out (int64 [1] on the device, optional): where the count goes, else a new tensor.
+    out (optional): (buf, u, nu) to write into instead of new tensors -- uint8 buf of at least plan_bytes(n, D)
+    bytes, int64 u of at least n elements, int64 nu [1] (nu_out, if given, takes its place); the caller keeps them
+    from being reused before the GPU's work on the plan is done."""
     flat = _ids(ids)
     n = flat.numel()
     dev = flat.device
@@ -107,11 +118,20 @@ def unique_plan_async(ids, D, bound=None, nu_out=None):
     if n == 0:
         return torch.empty(0, dtype=I64, device=dev), plan, None
     plan.key_bits = _key_bits(flat, bound)
-    nbytes = int(_lib.lib().elr_dedup_plan_bytes(n, int(D)))
-    if nbytes < 0:
-        _lib.check(nbytes, 'elr_dedup_plan_bytes')
-    plan.buf, plan.nbytes = torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
-    u = torch.empty(n, dtype=I64, device=dev)
+    nbytes = plan_bytes(n, D)
+    if out is not None:
+        buf, u, nu0 = out
+        if not (buf.dtype == torch.uint8 and buf.device == dev and buf.numel() >= nbytes and buf.is_contiguous()
+                and u.dtype == I64 and u.device == dev and u.numel() >= n and u.is_contiguous()):
+            raise RuntimeError(f'out must hold a uint8 buffer of {nbytes} bytes and an int64 tensor of {n} '
+                               f'elements on {dev}')
+        plan.buf, plan.nbytes = buf, nbytes
+        u = u[:n]
+        if nu_out is None:
+            nu_out = nu0
+    else:
+        plan.buf, plan.nbytes = torch.empty(nbytes, dtype=torch.uint8, device=dev), nbytes
+        u = torch.empty(n, dtype=I64, device=dev)
     if nu_out is not None and not (nu_out.dtype == I64 and nu_out.device == dev and nu_out.numel() == 1):
         raise RuntimeError(f'nu_out must be an int64 tensor of one element on {dev}')
     nu = nu_out if nu_out is not None else torch.empty(1, dtype=I64, device=dev)

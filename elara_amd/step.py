@@ -32,7 +32,7 @@ import torch
 
 from . import _lib  # noqa: F401  (the library must be present)
 from .assemble import assemble_rows
-from .dedup import segment_sum_plan, unique_plan, unique_plan_async
+from .dedup import plan_bytes, segment_sum_plan, unique_plan, unique_plan_async
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
@@ -74,8 +74,11 @@ class HipBackend:
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
 
-    def unique_async(self, ids, bound=None, nu_out=None):
-        return unique_plan_async(ids, self.D, bound, nu_out)
+    def unique_async(self, ids, bound=None, nu_out=None, out=None):
+        return unique_plan_async(ids, self.D, bound, nu_out, out)
+
+    def plan_bytes(self, n):
+        return plan_bytes(n, self.D)
 
     sync_counts = True   # takes counts_out / nu_out: the plan's counts and the deferred counts in one device buffer
 
@@ -516,7 +519,9 @@ class ElaraStep:
         self._sync = torch.zeros(64, dtype=I64, device=d) if sync else None
         self._sync_next = NCOUNTS
         self.dedup_ahead = True   # run() sorts the batches loaded ahead on a second stream (dedup_stream)
+        self.dedup_lead = 1   # run() queues a batch's sort this many steps before the step that observes it
         self._side = None
+        self._plan_pool = None   # run()'s reusable dedup-plan buffers (PlanPool), made on first use
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
@@ -1128,38 +1133,108 @@ def run(step, batches, grads, steps=None, on_step=None, freeze_gc=True):
         gc.unfreeze()
 
 
+class PlanPool:
+    """Reusable dedup-plan buffers for run(): one entry (plan buffer, unique-id array, unique count, and the events
+    that order its reuse) per batch between its dedup and its step.  Without it each batch's plan would be new
+    allocations handed between streams with record_stream: the device-driven step's host, which runs steps ahead of
+    the GPU, would then find no freed block of that size and allocate anew on every batch (tens of microseconds of
+    host time per allocation, the host being the step's bottleneck).
+
+    An entry is taken for a batch's sort and given back once the batch's step has been issued; a reused entry's sort
+    first waits, on the GPU, for the event recorded on the main stream after that step (on one stream, stream order
+    alone suffices).  Entries are reused only while at least `spare` are free, so a sort waits for the step before
+    the one just issued and not for the last one."""
+
+    def __init__(self, dev, spare=2):
+        self.dev, self.spare = dev, spare
+        self.free = []   # entries given back, oldest first
+        self.made = 0
+
+    def take(self, n, nbytes, side):
+        if len(self.free) >= self.spare:
+            e = self.free.pop(0)
+            if side is not None and e['rel_set']:
+                side.wait_event(e['rel'])   # the main stream's work on its last batch comes first
+            if e['buf'].numel() >= nbytes and e['u'].numel() >= n:
+                return e
+            # too small for this batch: new buffers; the old ones go back to the allocator only after the main
+            # stream's work on them (they were made on the sort's stream)
+            if side is not None:
+                main = torch.cuda.current_stream(self.dev)
+                e['buf'].record_stream(main)
+                e['u'].record_stream(main)
+                e['nu'].record_stream(main)
+        else:
+            e = {'rel': torch.cuda.Event(), 'sorted': torch.cuda.Event(), 'rel_set': False}
+            self.made += 1
+        ctx = torch.cuda.stream(side) if side is not None else _nullctx()
+        with ctx:   # made on the stream that writes them first
+            e['buf'] = torch.empty(nbytes, dtype=torch.uint8, device=self.dev)
+            e['u'] = torch.empty(max(n, 1), dtype=I64, device=self.dev)
+            e['nu'] = torch.empty(1, dtype=I64, device=self.dev)
+        return e
+
+    def give(self, e, side):
+        if side is not None:
+            e['rel'].record(torch.cuda.current_stream(self.dev))
+            e['rel_set'] = True
+        self.free.append(e)
+
+
+class _nullctx:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False
+
+
 def _run(step, batches, grads, steps, on_step):
     S = len(batches) if steps is None else steps
-    U, PLANS, AHEAD = {}, {}, {}
+    U, PLANS, AHEAD, ENTRY = {}, {}, {}, {}
     dev = step.d
     side = step.dedup_stream()
+    pool = None
+    if dev.type == 'cuda' and getattr(step.be, 'plan_bytes', None) is not None:
+        if step._plan_pool is None:
+            step._plan_pool = PlanPool(dev)
+        pool = step._plan_pool
 
     def dedup(j):
         """Batch j's dedup plan.  With a side stream it is queued there one step before the batch is observed, so
-        that its sort runs beside the next step's kernels; the tensors it makes are used on the main stream later
-        (record_stream keeps the allocator from reusing them before that work is done)."""
+        that its sort runs beside the next step's kernels.  Its buffers come from the plan pool (given back after
+        batch j's step); without a pool, the tensors it makes are used on the main stream later (record_stream keeps
+        the allocator from reusing them before that work is done)."""
         src = batches[j]
         ids = src.to(dev)
         # the host-planned step reads the unique count at its next synchronisation, from a slot of its sync buffer;
         # the device-driven step never reads it, and the host runs steps ahead of the GPU, so each batch has a count
-        # tensor of its own (kept by the allocator until the main stream's work on it is done) rather than a slot
-        # the host could hand to a later batch before this one's plan has run
+        # tensor of its own (its pool entry's, or one kept by the allocator until the main stream's work on it is
+        # done) rather than a slot the host could hand to a later batch before this one's plan has run
         slot = None if step.sync_free else step.count_slot()
         kw = {} if slot is None else {'nu_out': slot}
+        n = ids.numel()
+        e = pool.take(n, step.be.plan_bytes(n), side) if pool is not None and n else None
+        if e is not None:
+            ENTRY[j] = e
+            kw['out'] = (e['buf'], e['u'], e['nu'])
         if side is None:
             AHEAD[j] = (*step.be.unique_async(ids, step.R, **kw), None)
             return
         main = torch.cuda.current_stream(dev)
-        if src.device != ids.device or src.data_ptr() != ids.data_ptr():
+        copied = src.device != ids.device or src.data_ptr() != ids.data_ptr()
+        if copied:
             side.wait_stream(main)   # the copy that made ids
         with torch.cuda.stream(side):
             u, dplan, nu = step.be.unique_async(ids, step.R, **kw)
-            ev = torch.cuda.Event()
+            ev = e['sorted'] if e is not None else torch.cuda.Event()
             ev.record()
-        ids.record_stream(side)
-        for t in (u, dplan.buf, nu if slot is None else None):
-            if t is not None:
-                t.record_stream(main)
+        if copied:
+            ids.record_stream(side)
+        if e is None:
+            for t in (u, dplan.buf, nu if slot is None else None):
+                if t is not None:
+                    t.record_stream(main)
         AHEAD[j] = (u, dplan, nu, ev)
 
     def observe(j):
@@ -1186,22 +1261,26 @@ def _run(step, batches, grads, steps, on_step):
         step.observe(j + 1, u, nu)
         step.defer_count(nu, resolve)
 
+    lead = max(int(step.dedup_lead), 1)
     for j in range(min(S, step.L + 1)):
         dedup(j)
         observe(j)
-    if step.L + 1 < S:
-        dedup(step.L + 1)
+    for j in range(step.L + 1, min(S, step.L + 1 + lead)):
+        dedup(j)
     if not step.sync_free:
         step.flush_deferred()
     for s in range(S):
         if s + step.L + 1 < S:
             observe(s + step.L + 1)
-        if s + step.L + 2 < S:
-            dedup(s + step.L + 2)
+        if s + step.L + 1 + lead < S:
+            dedup(s + step.L + 1 + lead)
         u_nexts = [] if step.sync_free else [U[s + k] for k in range(1, step.depth) if s + k < S]
         g = grads(s) if callable(grads) else grads[s]
         p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
         if on_step is not None:
             on_step(s + 1, p)
+        e = ENTRY.pop(s, None)
+        if e is not None:   # batch s's last use: its step (and the unique rows of the depth-1 plans before it)
+            pool.give(e, side)
     step.join_link()
     step.check_capacity()
