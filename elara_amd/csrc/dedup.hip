@@ -7,7 +7,7 @@
 //
 // Sort.  Stable LSD radix sort of (id, occurrence index) pairs, 8-bit digits, ceil(key_bits / 8) passes (or one
 // pass fewer with 9- or 10-bit digits), keys held as uint32 when key_bits <= 32.  Tiles of 4096 keys, or 1024 below
-// 2^21 keys.  A pass is three launches: per-tile digit histograms, a wave per digit scanning that digit's per-tile
+// 2^18 keys.  A pass is three launches: per-tile digit histograms, a wave per digit scanning that digit's per-tile
 // counts, and a scatter in which each key's rank among equal digits of its tile comes from wave ballots (peer mask
 // of the digit bits), a per-wave running count in LDS and a scan over the tile's waves, so equal keys keep their
 // occurrence order.
@@ -34,11 +34,16 @@
 namespace elr {
 
 constexpr int kSortThreads = 256;
-// Keys per thread of a sort tile and positions per thread of a segment tile: 16 for large batches (tiles of 4,096),
-// 4 below kBigBatch, so that a batch of a few hundred thousand ids still spreads over several hundred blocks.
+// Keys per thread of a sort tile and positions per thread of a segment tile: 16 (tiles of 4,096) from kBigBatch
+// keys, 4 below it, so that a small batch still spreads over a few hundred blocks.  The threshold is set for a batch
+// sorted beside other kernels, as the ELARA step sorts the batches it loads ahead: at config C5 (425,984 keys)
+// tiles of 4,096 make a sort alone 124 us against 81 us with tiles of 1,024, but its launches of a quarter as many
+// blocks take fewer CUs from the step's kernels beside them, and the step is faster (0.342 against 0.357 ms
+// device-driven, 0.279 against 0.297 ms host-planned; three alternations on one box; tiles of 2,048 in between,
+// 8,192 slower than both).
 constexpr int kItemsBig = 16;
 constexpr int kItemsSmall = 4;
-constexpr int64_t kBigBatch = int64_t(1) << 21;
+constexpr int64_t kBigBatch = int64_t(1) << 18;
 inline int items_for(int64_t n) { return n >= kBigBatch ? kItemsBig : kItemsSmall; }
 constexpr int kRadixBins = 256;      // bins of an 8-bit digit; passes take 8, 9 or 10 bits (sort_plan)
 constexpr int kRadixMaxBits = 10;

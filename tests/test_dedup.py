@@ -177,10 +177,10 @@ def test_gpu_unique_matches_torch(dev, case):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize('key_bits', [1, 8, 9, 12, 17, 20, 24, 27, 30, 32, 33, 40, 63])
-@pytest.mark.parametrize('n', [70001, (1 << 21) + 3])
+@pytest.mark.parametrize('n', [70001, (1 << 18) - 1, (1 << 18) + 3, (1 << 21) + 3])
 def test_gpu_unique_every_digit_width(dev, key_bits, n):
     """The sort takes 8-, 9- or 10-bit digits (fewer passes: 27-bit keys in 3 passes of 9 bits, 30-bit keys in 3 of
-    10); for each key width from the caller's bound, both tile sizes (below and above 2^21 ids) give torch.unique's
+    10); for each key width from the caller's bound, both tile sizes (either side of 2^18 ids) give torch.unique's
     rows and inverse.  Ids are spread over the whole width, with duplicates and the extreme keys 0 and 2^b - 1."""
     from elara_amd.dedup import unique
     rng = np.random.default_rng(key_bits * 7 + n % 5)
