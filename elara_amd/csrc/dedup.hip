@@ -12,9 +12,10 @@
 // of the digit bits), a per-wave running count in LDS and a scan over the tile's waves, so equal keys keep their
 // occurrence order.
 //
-// Segments.  Sorted position i starts a segment when its key differs from position i-1; per-block head counts,
-// then a launch in which each block adds up the counts of the blocks before it, gives every position its unique
-// index (the inverse) and every unique id its first position.  The extra-chunk plan is laid out the same way.
+// Segments.  Sorted position i starts a segment when its key differs from position i-1; per-block head counts, then
+// a launch in which each block adds up the counts of the blocks before it (or, above kFoldMaxBlocks blocks, a
+// one-block scan launch in between), gives every position its unique index (the inverse) and every unique id its
+// first position.  The extra-chunk plan is laid out the same way.
 //
 // Summation order: ATen's, as torch.ops.aten.embedding_dense_backward computes it on this GPU
 // (aten/src/ATen/native/cuda/Embedding.cu embedding_dense_backward_cuda and EmbeddingBackwardKernel.cu, PyTorch
@@ -137,6 +138,11 @@ __global__ __launch_bounds__(kSortThreads) void k_radix_hist_scan(int64_t* __res
     }
   }
   if (lane == 0) dtot[d] = carry;
+}
+
+// One block: exclusive scan of per-block counts in place (grids above kFoldMaxBlocks; see k_seg_apply).
+__global__ __launch_bounds__(kScanBlock) void k_scan_blocks(int64_t* __restrict__ bsum, int64_t n) {
+  scan_channels_block(bsum, n, 1, nullptr);
 }
 
 // Stable scatter of one pass.  FIRST: the source keys are the caller's int64 ids and the values are their
@@ -280,8 +286,13 @@ __global__ __launch_bounds__(kSegBlock) void k_seg_count(const Key* __restrict__
   if (threadIdx.x == 0) bsum[blockIdx.x] = tot[0];
 }
 
+// Grids of at most this many blocks take their block offsets by block_offset; larger ones from a one-block scan
+// launch (k_scan_blocks) between the count and apply launches.  At config C3 (830 blocks) the summing blocks made the
+// step 55 us slower where the sort runs beside the final segment kernel; at C5 (104 blocks) they save the launch.
+constexpr int64_t kFoldMaxBlocks = 256;
+
 // Sum of cnt[0 .. b) over the whole block, returned to every thread: the offset of block b from the per-block
-// counts of the launch before, without a scan launch in between (b is at most a few thousand).
+// counts of the launch before, without a scan launch in between.
 __device__ __forceinline__ int64_t block_offset(const int64_t* __restrict__ cnt, int64_t b) {
   __shared__ int64_t wpart[kSegBlock / 64];
   int64_t x = 0;
@@ -298,17 +309,18 @@ __device__ __forceinline__ int64_t block_offset(const int64_t* __restrict__ cnt,
 }
 
 // Segment heads: unique ids, segment starts, each segment's first occurrence index and the inverse.  The block's
-// first segment index is the sum of the earlier blocks' head counts (k_seg_count); the last block stores U to d_U
-// (and n_unique) and seg_start[U] = n.
+// first segment index: the sum of the earlier blocks' head counts (k_seg_count), or, with `scanned`, bcnt[block]
+// after k_scan_blocks.  The last block stores U to d_U (and n_unique) and seg_start[U] = n.
 template <typename Key, int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_seg_apply(const Key* __restrict__ sk, const int32_t* __restrict__ sv,
-                                                         int64_t n, const int64_t* __restrict__ bcnt,
+                                                         int64_t n, const int64_t* __restrict__ bcnt, int scanned,
                                                          int64_t* __restrict__ d_U, int64_t* __restrict__ n_unique,
                                                          int64_t* __restrict__ uniq, int64_t* __restrict__ seg_start,
                                                          int32_t* __restrict__ seg_occ0,
                                                          int64_t* __restrict__ inverse) {
   const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
-  int64_t before = block_offset(bcnt, blockIdx.x);   // heads in earlier positions of the tile's earlier rounds
+  // heads in earlier positions of the tile's earlier rounds
+  int64_t before = scanned ? bcnt[blockIdx.x] : block_offset(bcnt, blockIdx.x);
   for (int r = 0; r < ITEMS; ++r) {
     const int64_t i = base + (int64_t)r * kSegBlock;
     const int f = is_head(sk, i, n);
@@ -360,18 +372,19 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_count(const int64_t* __rest
 
 // chunk_off[u] = first work item of segment u's partial chunks; chunk_seg[item] = u; hot segments are listed in
 // hot_list[0 .. *d_hot) (in no particular order: each is summed on its own).  The block's first work item is the sum
-// of the earlier blocks' counts (k_chunk_count); the last block stores the number of work items to *d_E.
+// of the earlier blocks' counts (k_chunk_count), or bcnt[block] with `scanned`; the last block stores the number of
+// work items to *d_E.
 template <int ITEMS>
 __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __restrict__ seg_start,
                                                            const int64_t* __restrict__ d_U,
-                                                           const int64_t* __restrict__ bcnt,
+                                                           const int64_t* __restrict__ bcnt, int scanned,
                                                            int32_t* __restrict__ chunk_off,
                                                            int32_t* __restrict__ chunk_seg,
                                                            int32_t* __restrict__ hot_list,
                                                            int64_t* __restrict__ d_hot, int64_t* __restrict__ d_E) {
   const int64_t base = (int64_t)blockIdx.x * kSegBlock * ITEMS + threadIdx.x;
   const int64_t U = *d_U;
-  int64_t before = block_offset(bcnt, blockIdx.x);
+  int64_t before = scanned ? bcnt[blockIdx.x] : block_offset(bcnt, blockIdx.x);
   for (int r = 0; r < ITEMS; ++r) {
     const int64_t u = base + (int64_t)r * kSegBlock;
     const int e = extra_chunks(seg_start, u, U);
@@ -878,8 +891,10 @@ static int dedup_core_items(const int64_t* ids, int64_t n, int key_bits, DedupSc
   const int32_t* sv = S.vals[cur];
   const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
   int64_t* uniq = uniq_out ? uniq_out : S.uniq;
+  const int scanned = nblk > kFoldMaxBlocks;
   k_seg_count<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, n, S.bsum);
-  k_seg_apply<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, S.d_tot, n_unique, uniq,
+  if (scanned) k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk);
+  k_seg_apply<Key, ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(sk, sv, n, S.bsum, scanned, S.d_tot, n_unique, uniq,
                                                                 S.seg_start, S.seg_occ0, inverse);
   return cur;
 }
@@ -898,8 +913,10 @@ inline int win_shift_for(int64_t n) { return n <= kAtenSmall ? kAtenWinShift : 0
 template <int ITEMS>
 static void chunk_plan_items(int64_t n, DedupScratch& S, hipStream_t st) {
   const int64_t nblk = cdiv(n, kSegBlock * ITEMS);
+  const int scanned = nblk > kFoldMaxBlocks;
   k_chunk_count<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.d_tot + 2);
-  k_chunk_apply<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, S.chunk_off,
+  if (scanned) k_scan_blocks<<<1, kScanBlock, 0, st>>>(S.bsum, nblk);
+  k_chunk_apply<ITEMS><<<(unsigned)nblk, kSegBlock, 0, st>>>(S.seg_start, S.d_tot, S.bsum, scanned, S.chunk_off,
                                                              S.chunk_seg, S.hot_list, S.d_tot + 2, S.d_tot + 1);
 }
 

@@ -239,6 +239,26 @@ def test_gpu_embedding_backward_matches_aten(dev, n, U, D):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('n', [1 << 20, (1 << 20) + 1])
+def test_gpu_segment_block_offsets_both_ways(dev, n):
+    """The segment-head and chunk-plan launches take their block offsets by summing the earlier blocks' counts in
+    each block up to 256 blocks (2^20 ids in tiles of 4,096) and from a one-block scan launch above (one id more):
+    unique equals torch.unique and the sums equal ATen's embedding_dense_backward on both sides, with a hot id."""
+    from elara_amd.dedup import embedding_dense_backward, unique
+    U, D = 300_000, 64
+    print(f'[gpu-test] block offsets n={n}', flush=True)
+    ids, g = golden_module().case_inputs(n, U, D, 11, U - 1, 2)
+    gd, idd = torch.from_numpy(g).to(dev), torch.from_numpy(ids).to(dev)
+    u, inv = unique(idd, bound=U)
+    tu, tinv = torch.unique(idd, return_inverse=True)
+    assert torch.equal(u, tu) and torch.equal(inv, tinv)
+    want = torch.ops.aten.embedding_dense_backward(gd, idd, U, -1, False)
+    got = embedding_dense_backward(gd, idd, U)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got.cpu().numpy()), bits(want.cpu().numpy()))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize('D', [128, 64, 256, 512, 96])
 def test_gpu_segment_lengths_at_every_boundary(dev, D):
     """Ids whose occurrence counts sit on each boundary of the kernels' work split -- runs of 10, the first chunk
