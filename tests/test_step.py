@@ -283,6 +283,37 @@ def test_gpu_step_degenerate_batches(dev, name):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('sync_free,ahead', [(True, True), (False, True), (True, False)])
+def test_gpu_step_ragged_batches(dev, sync_free, ahead):
+    """Batches of changing sizes (a later batch larger than any before it, then smaller ones): run() takes each
+    batch's dedup-plan buffers from its pool, and a batch that outgrows every free entry gets new ones.  Device-
+    driven and host-planned, with the sorts on a second stream or on the step's own.  Equal to the oracle-driven
+    step."""
+    from elara_amd.step import run
+    print(f'[gpu-test] elara step ragged batches sync_free={sync_free} ahead={ahead}', flush=True)
+    sizes = [300, 100, 800, 200, 1600, 50, 1200, 400, 2400, 150, 700, 1000, 90, 3000, 500, 250]
+    tabs = synth.C5Tables(T=6, lo=200, hi=20000, alpha=1.1, seed=5)
+    rng = np.random.default_rng(12)
+    static = tabs.static_rows(rng, 1000, 1500, n_batches=10)
+    batches = [torch.from_numpy(tabs.batch(rng, b)) for b in sizes]
+    O = sum(b.numel() for b in batches)
+    cfg = dict(toff=tabs.toff, R=tabs.R, D=128, C=9000, static=static, steps=len(sizes), bound=synth.bound_for(128),
+               log_cap=O + 16, mat_cap=min(tabs.R + 1, O + 16), batches=batches, sync_free=sync_free)
+    g = make(cfg, dev)
+    g.dedup_ahead = ahead
+    c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
+    gf = grads_fn(cfg, None)
+    run(g, cfg['batches'], gf)
+    run(c, cfg['batches'], gf)
+    torch.cuda.synchronize()
+    assert compare(g, c, cfg) > 0
+    assert same_stats(g, c)
+    assert g.sync_free == sync_free
+    pool = g._plan_pool
+    assert pool is not None and pool.made >= 2, 'the dedup plans come from the pool'
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize('dir_impl,steps', [('cpp', 200), ('triton', 100)])
 def test_gpu_step_c5_full_shape(dev, dir_impl, steps):
     """Config C5 shapes: 26 tables (vocab log-uniform in [1e3, 4e7], ~75M rows), batch 16,384 x 26 Zipf(1.1),
