@@ -1261,26 +1261,33 @@ def _run(step, batches, grads, steps, on_step):
         step.observe(j + 1, u, nu)
         step.defer_count(nu, resolve)
 
-    lead = max(int(step.dedup_lead), 1)
-    for j in range(min(S, step.L + 1)):
-        dedup(j)
-        observe(j)
-    for j in range(step.L + 1, min(S, step.L + 1 + lead)):
-        dedup(j)
-    if not step.sync_free:
-        step.flush_deferred()
-    for s in range(S):
-        if s + step.L + 1 < S:
-            observe(s + step.L + 1)
-        if s + step.L + 1 + lead < S:
-            dedup(s + step.L + 1 + lead)
-        u_nexts = [] if step.sync_free else [U[s + k] for k in range(1, step.depth) if s + k < S]
-        g = grads(s) if callable(grads) else grads[s]
-        p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
-        if on_step is not None:
-            on_step(s + 1, p)
-        e = ENTRY.pop(s, None)
-        if e is not None:   # batch s's last use: its step (and the unique rows of the depth-1 plans before it)
+    try:
+        lead = max(int(step.dedup_lead), 1)
+        for j in range(min(S, step.L + 1)):
+            dedup(j)
+            observe(j)
+        for j in range(step.L + 1, min(S, step.L + 1 + lead)):
+            dedup(j)
+        if not step.sync_free:
+            step.flush_deferred()
+        for s in range(S):
+            if s + step.L + 1 < S:
+                observe(s + step.L + 1)
+            if s + step.L + 1 + lead < S:
+                dedup(s + step.L + 1 + lead)
+            u_nexts = [] if step.sync_free else [U[s + k] for k in range(1, step.depth) if s + k < S]
+            g = grads(s) if callable(grads) else grads[s]
+            p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
+            if on_step is not None:
+                on_step(s + 1, p)
+            e = ENTRY.pop(s, None)
+            if e is not None:   # batch s's last use: its step (and the unique rows of the depth-1 plans before it)
+                pool.give(e, side)
+        step.join_link()
+        step.check_capacity()
+    finally:
+        # entries still out (a step raised): back to the pool behind the main stream's work queued so far, so that
+        # no later sort writes into a plan that queued work may still read
+        for e in ENTRY.values():
             pool.give(e, side)
-    step.join_link()
-    step.check_capacity()
+        ENTRY.clear()
