@@ -24,6 +24,7 @@ plan synchronises with the host once (class counts, elara.py:242), plus once mor
 hot-path kernels come from a backend object (HipBackend: this library's HIP kernels), so the same step can be
 driven by another implementation of the kernels (the oracle's) for comparison.
 """
+import contextlib
 import ctypes
 import gc
 import time
@@ -519,7 +520,6 @@ class ElaraStep:
         self._sync = torch.zeros(64, dtype=I64, device=d) if sync else None
         self._sync_next = NCOUNTS
         self.dedup_ahead = True   # run() sorts the batches loaded ahead on a second stream (dedup_stream)
-        self.dedup_lead = 1   # run() queues a batch's sort this many steps before the step that observes it
         self._side = None
         self._plan_pool = None   # run()'s reusable dedup-plan buffers (PlanPool), made on first use
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
@@ -1153,8 +1153,11 @@ class PlanPool:
     def take(self, n, nbytes, side):
         if len(self.free) >= self.spare:
             e = self.free.pop(0)
-            if side is not None and e['rel_set']:
-                side.wait_event(e['rel'])   # the main stream's work on its last batch comes first
+            if side is not None:   # the main stream's work on its last batch comes first
+                if e['rel_set']:
+                    side.wait_event(e['rel'])
+                else:   # given back without an event (by a run on one stream): wait for all the main stream's work
+                    side.wait_stream(torch.cuda.current_stream(self.dev))
             if e['buf'].numel() >= nbytes and e['u'].numel() >= n:
                 return e
             # too small for this batch: new buffers; the old ones go back to the allocator only after the main
@@ -1167,7 +1170,7 @@ class PlanPool:
         else:
             e = {'rel': torch.cuda.Event(), 'sorted': torch.cuda.Event(), 'rel_set': False}
             self.made += 1
-        ctx = torch.cuda.stream(side) if side is not None else _nullctx()
+        ctx = torch.cuda.stream(side) if side is not None else contextlib.nullcontext()
         with ctx:   # made on the stream that writes them first
             e['buf'] = torch.empty(nbytes, dtype=torch.uint8, device=self.dev)
             e['u'] = torch.empty(max(n, 1), dtype=I64, device=self.dev)
@@ -1179,14 +1182,6 @@ class PlanPool:
             e['rel'].record(torch.cuda.current_stream(self.dev))
             e['rel_set'] = True
         self.free.append(e)
-
-
-class _nullctx:
-    def __enter__(self):
-        return self
-
-    def __exit__(self, *a):
-        return False
 
 
 def _run(step, batches, grads, steps, on_step):
@@ -1262,19 +1257,18 @@ def _run(step, batches, grads, steps, on_step):
         step.defer_count(nu, resolve)
 
     try:
-        lead = max(int(step.dedup_lead), 1)
         for j in range(min(S, step.L + 1)):
             dedup(j)
             observe(j)
-        for j in range(step.L + 1, min(S, step.L + 1 + lead)):
-            dedup(j)
+        if step.L + 1 < S:
+            dedup(step.L + 1)
         if not step.sync_free:
             step.flush_deferred()
         for s in range(S):
             if s + step.L + 1 < S:
                 observe(s + step.L + 1)
-            if s + step.L + 1 + lead < S:
-                dedup(s + step.L + 1 + lead)
+            if s + step.L + 2 < S:
+                dedup(s + step.L + 2)
             u_nexts = [] if step.sync_free else [U[s + k] for k in range(1, step.depth) if s + k < S]
             g = grads(s) if callable(grads) else grads[s]
             p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)
