@@ -29,6 +29,7 @@
 // only when both terms are), so starting a group from its first gradient gives the same bits.  Long (Zipf-hot)
 // segments are cut into chunks of 6 groups summed in parallel by different waves (partial sums per group, added in
 // order by the segment's own wave).
+#include "elr_dir_dev.h"
 #include "elr_scan.h"
 #include "elr_seg_dev.h"
 
@@ -578,14 +579,14 @@ __device__ __forceinline__ void seg_hot_block(const int64_t* __restrict__ seg_st
                                               const float* __restrict__ parts,
                                               const int32_t* __restrict__ hot_list, const int64_t* __restrict__ d_hot,
                                               int64_t hot_blocks, float* __restrict__ out, int64_t nrows,
-                                              const AdamScalars& s, float* __restrict__ relay) {
+                                              const AdamScalars& s, float* __restrict__ relay, int64_t block) {
   constexpr int64_t D = 64 * VPL;
   constexpr int PB = VPL <= 2 ? kSegParts : kSegParts / 2;
   constexpr int NWV = 4;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t nh = *d_hot;
-  for (int64_t h = blockIdx.x; h < nh; h += hot_blocks) {
+  for (int64_t h = block; h < nh; h += hot_blocks) {
     const int64_t u = hot_list[h];
     const int64_t L = seg_start[u + 1] - seg_start[u];
     const int64_t nr = (L + kAtenGroup - 1) / kAtenGroup;
@@ -630,28 +631,42 @@ __device__ __forceinline__ void seg_hot_block(const int64_t* __restrict__ seg_st
   }
 }
 
+// The final kernel as a functor (elr_launch.h): block `block` of the launch, the first hot_blocks of them on the hot
+// segments.  k_seg_final_wpr launches it on its own; the device-driven step also runs it beside the directory's
+// first launch of the executor (k_run2).
 template <int VPL, int MODE>
-__global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__ grad,
-                                                       const int32_t* __restrict__ sv,
-                                                       const int64_t* __restrict__ seg_start,
-                                                       const int32_t* __restrict__ seg_occ0,
-                                                       const int64_t* __restrict__ uniq,
-                                                       const int32_t* __restrict__ chunk_off,
-                                                       const float* __restrict__ parts,
-                                                       const int64_t* __restrict__ d_U, int64_t u_base,
-                                                       const int32_t* __restrict__ hot_list,
-                                                       const int64_t* __restrict__ d_hot, int64_t hot_blocks,
-                                                       float* __restrict__ out, int64_t nrows, AdamScalars s) {
+struct SegFinalWpr {
+  const float* grad;
+  const int32_t* sv;
+  const int64_t* seg_start;
+  const int32_t* seg_occ0;
+  const int64_t* uniq;
+  const int32_t* chunk_off;
+  const float* parts;
+  const int64_t* d_U;
+  int64_t u_base;
+  const int32_t* hot_list;
+  const int64_t* d_hot;
+  int64_t hot_blocks;
+  float* out;
+  int64_t nrows;
+  AdamScalars s;
+  __device__ void operator()(int64_t block, int64_t nblocks) const;
+};
+
+template <int VPL, int MODE>
+__device__ void SegFinalWpr<VPL, MODE>::operator()(int64_t block, int64_t) const {
   constexpr int64_t D = 64 * VPL;
   constexpr int SW = kSegPerWave;
   __shared__ float relay[D];
-  if ((int64_t)blockIdx.x < hot_blocks) {
-    seg_hot_block<VPL, MODE>(seg_start, uniq, chunk_off, parts, hot_list, d_hot, hot_blocks, out, nrows, s, relay);
+  if (block < hot_blocks) {
+    seg_hot_block<VPL, MODE>(seg_start, uniq, chunk_off, parts, hot_list, d_hot, hot_blocks, out, nrows, s, relay,
+                             block);
     return;
   }
   const int lane = threadIdx.x & 63;
   const int64_t U = *d_U;
-  const int64_t u0 = u_base + (((int64_t)blockIdx.x - hot_blocks) * 4 + (threadIdx.x >> 6)) * SW;
+  const int64_t u0 = u_base + ((block - hot_blocks) * 4 + (threadIdx.x >> 6)) * SW;
   if (u0 >= U) return;
   int64_t s0[SW], len[SW], row[SW], o0[SW];
   bool ok[SW];
@@ -774,6 +789,11 @@ __global__ __launch_bounds__(256) void k_seg_final_wpr(const float* __restrict__
       frag_store<VPL>(rec + 2 * D, v[q]);
     }
   }
+}
+
+template <int VPL, int MODE>
+__global__ __launch_bounds__(256) void k_seg_final_wpr(SegFinalWpr<VPL, MODE> f) {
+  f((int64_t)blockIdx.x, (int64_t)gridDim.x);
 }
 
 // ---- host side -------------------------------------------------------------------------------------------------
@@ -952,9 +972,9 @@ static void seg_reduce_wpr(const float* grad, const int32_t* sv, DedupScratch& S
   for (int64_t a = 0; a < n; a += per) {
     const int64_t m = n - a < per ? n - a : per;
     const int64_t hb = a == 0 ? n / kHotLen + 1 : 0;
-    k_seg_final_wpr<VPL, MODE><<<(unsigned)(hb + cdiv(m, 4 * kSegPerWave)), 256, 0, st>>>(
-        grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a, S.hot_list, S.d_tot + 2, hb, out,
-        nrows, s);
+    const SegFinalWpr<VPL, MODE> f{grad, sv, S.seg_start, S.seg_occ0, uniq, S.chunk_off, S.parts, S.d_tot, a,
+                                   S.hot_list, S.d_tot + 2, hb, out, nrows, s};
+    k_seg_final_wpr<VPL, MODE><<<(unsigned)(hb + cdiv(m, 4 * kSegPerWave)), 256, 0, st>>>(f);
   }
 }
 
@@ -1114,6 +1134,38 @@ static int segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bit
   const int rc = seg_reduce_d<0>(grad, D, S.vals[plan_result_buffer(key_bits)], S, perm, n, out, out_rows, none, st,
                                  partials);
   return rc != ELR_OK ? rc : launch_status();
+}
+
+template <int VPL>
+static void seg_final_with(const float* grad, const int32_t* sv, DedupScratch& S, const int64_t* perm, int64_t n,
+                           float* out, int64_t nrows, const DirLstepsHits& first, int64_t nb1, hipStream_t st) {
+  const int64_t hb = n / kHotLen + 1;
+  const SegFinalWpr<VPL, 0> f{grad, sv, S.seg_start, S.seg_occ0, perm, S.chunk_off, S.parts, S.d_tot, 0,
+                              S.hot_list, S.d_tot + 2, hb, out, nrows, AdamScalars{}};
+  launch2(first, nb1, f, hb + cdiv(n, 4 * kSegPerWave), st);
+}
+
+int segment_sum_plan_final_with(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                                int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows,
+                                const DirLstepsHits& first, int64_t nb1, void* stream) {
+  if (!dedup_sizes_ok(n) || D < 1 || key_bits < 1 || key_bits > 64 || out_rows < 0 || nb1 < 0) return ELR_EINVAL;
+  if (n == 0 || !grad || !plan || !out) return ELR_EUNSUPPORTED;
+  // the wave-per-row final kernel in one launch: aligned rows of 64, 128, 256 or 512, the sort path, at most one
+  // launch's worth of segments (seg_reduce_wpr)
+  if (!aligned16(grad) || !aligned16(out) || win_shift_for(n) || n > kOneShotBlocks * 4 * kSegPerWave)
+    return ELR_EUNSUPPORTED;
+  DedupScratch S;
+  if (plan_bytes < dedup_scratch_bytes(n, D, &S, const_cast<void*>(plan))) return ELR_ECAPACITY;
+  const int32_t* sv = S.vals[plan_result_buffer(key_bits)];
+  hipStream_t st = (hipStream_t)stream;
+  switch (D) {
+    case 64: seg_final_with<1>(grad, sv, S, perm, n, out, out_rows, first, nb1, st); break;
+    case 128: seg_final_with<2>(grad, sv, S, perm, n, out, out_rows, first, nb1, st); break;
+    case 256: seg_final_with<4>(grad, sv, S, perm, n, out, out_rows, first, nb1, st); break;
+    case 512: seg_final_with<8>(grad, sv, S, perm, n, out, out_rows, first, nb1, st); break;
+    default: return ELR_EUNSUPPORTED;
+  }
+  return launch_status();
 }
 
 }  // namespace elr

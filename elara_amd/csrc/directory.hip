@@ -29,51 +29,6 @@
 
 namespace elr {
 
-// ---------------------------------------------------------------------------------------------------------------
-// A1: replay inputs of L rows (elara_dir.cpp:56-59) and resident-history recording of hits (elara_dir.cpp:60-71).
-// Threads [0, nL*K) take one (row, k) entry each; threads [nL*K, nL*K + nh) take one hit slot each.  The two parts
-// touch disjoint arrays (ent/lstep are read; pstep/rj/rok are written), and hit slots are unique.
-__global__ __launch_bounds__(kDirBlock) void k_dir_lsteps_hits(elr_dir_state st, elr_dir_params p,
-                                                               const int64_t* __restrict__ hs, DevCount nh_,
-                                                               const int64_t* __restrict__ L_row,
-                                                               const int32_t* __restrict__ L_cnt, DevCount nL_,
-                                                               int32_t s, int32_t* __restrict__ L_steps,
-                                                               int32_t* __restrict__ L_ids,
-                                                               int64_t* __restrict__ hrec_dyn,
-                                                               int64_t* __restrict__ hrec_j) {
-  const int64_t t = (int64_t)blockIdx.x * kDirBlock + threadIdx.x;
-  const int64_t nh = nh_.get(), nL = nL_.get();
-  const int64_t K = p.K, nLK = nL * K;
-  if (t < nLK) {
-    const int64_t i = t / K, k = t - i * K;
-    const int64_t row = L_row[i];
-    int32_t e = -1;
-    if (in_range(row, p.R + 1)) e = st.ent[row * K + k];
-    L_steps[t] = (e >= 0 && e <= p.Lcap) ? st.lstep[e] : 0;
-    L_ids[t] = k < (int64_t)L_cnt[i] ? e : -1;
-    return;
-  }
-  const int64_t i = t - nLK;
-  if (i >= nh) return;
-  const int64_t sl = hs[i];
-  const int64_t C = p.n0 + p.Cdyn;
-  if (!in_range(sl, C)) {
-    hrec_dyn[i] = p.Cdyn;
-    hrec_j[i] = 0;
-    return;
-  }
-  const bool dyn = sl >= p.n0;
-  const int64_t c0 = st.adm_c0[sl], j = st.rj[sl];
-  const bool ok = st.rok[sl] != 0;
-  const bool rec = p.evl && dyn && ok && (c0 + j < K);
-  const int64_t hd = rec ? sl - p.n0 : p.Cdyn, hj = rec ? j : 0;
-  hrec_dyn[i] = hd;
-  hrec_j[i] = hj;
-  if (in_range(hj, K)) st.pstep[hd * K + hj] = s;  // non-recorded hits write the trash row (Cdyn, 0), as the reference
-  st.rj[sl] = (int8_t)(j + (rec ? 1 : 0));
-  st.rok[sl] = (int8_t)(ok && !(dyn && !rec));
-}
-
 // Grids of more than kFusedScanBlocks blocks: single-block exclusive scan of the per-block counts of `nch`
 // channels (in place) and the counter update, from the old counters that the count kernel kept in hdr.
 // Channel roles: mode 0 (call A): 0 = log allocations, 1 = MAT allocations, 2 = releases.
@@ -165,16 +120,24 @@ int dir_a_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t*
   return ELR_OK;
 }
 
+DirLstepsHits dir_lsteps_hits_prep(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
+                                   const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s,
+                                   int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j,
+                                   const int64_t* desc, int64_t& blocks) {
+  const int64_t n1 = nL * P.K + nh;
+  blocks = n1 ? dir_nblocks(n1) : 0;
+  return DirLstepsHits{S, P, hs, dcount(nh, desc, kDNh), L_row, L_cnt, dcount(nL, desc, kDNL), (int32_t)s, L_steps,
+                       L_ids, hrec_dyn, hrec_j};
+}
+
 void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
                             const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s, int32_t* L_steps,
                             int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm,
                             const int64_t* desc) {
-  const int64_t n1 = nL * P.K + nh;
-  if (n1) {
-    k_dir_lsteps_hits<<<(unsigned)dir_nblocks(n1), kDirBlock, 0, strm>>>(
-        S, P, hs, dcount(nh, desc, kDNh), L_row, L_cnt, dcount(nL, desc, kDNL), (int32_t)s, L_steps, L_ids, hrec_dyn,
-        hrec_j);
-  }
+  int64_t blocks;
+  const DirLstepsHits f = dir_lsteps_hits_prep(S, P, hs, nh, L_row, L_cnt, nL, s, L_steps, L_ids, hrec_dyn, hrec_j,
+                                               desc, blocks);
+  launch1(f, blocks, strm);
 }
 
 int dir_b_check(const elr_dir_state* st, const elr_dir_params* p, const int64_t* a_rows, const int64_t* a_k,

@@ -141,6 +141,58 @@ __device__ __forceinline__ int64_t log_id_of_rank(const int32_t* __restrict__ lf
   return top0 + rank - nf0;
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// A1: replay inputs of L rows (elara_dir.cpp:56-59) and resident-history recording of hits (elara_dir.cpp:60-71).
+// Threads [0, nL*K) take one (row, k) entry each; threads [nL*K, nL*K + nh) take one hit slot each.  The two parts
+// touch disjoint arrays (ent/lstep are read; pstep/rj/rok are written), and hit slots are unique.
+struct DirLstepsHits {
+  elr_dir_state st;
+  elr_dir_params p;
+  const int64_t* hs;
+  DevCount nh_;
+  const int64_t* L_row;
+  const int32_t* L_cnt;
+  DevCount nL_;
+  int32_t s;
+  int32_t* L_steps;
+  int32_t* L_ids;
+  int64_t* hrec_dyn;
+  int64_t* hrec_j;
+  __device__ void operator()(int64_t block, int64_t) const {
+    const int64_t t = block * kDirBlock + threadIdx.x;
+    const int64_t nh = nh_.get(), nL = nL_.get();
+    const int64_t K = p.K, nLK = nL * K;
+    if (t < nLK) {
+      const int64_t i = t / K, k = t - i * K;
+      const int64_t row = L_row[i];
+      int32_t e = -1;
+      if (in_range(row, p.R + 1)) e = st.ent[row * K + k];
+      L_steps[t] = (e >= 0 && e <= p.Lcap) ? st.lstep[e] : 0;
+      L_ids[t] = k < (int64_t)L_cnt[i] ? e : -1;
+      return;
+    }
+    const int64_t i = t - nLK;
+    if (i >= nh) return;
+    const int64_t sl = hs[i];
+    const int64_t C = p.n0 + p.Cdyn;
+    if (!in_range(sl, C)) {
+      hrec_dyn[i] = p.Cdyn;
+      hrec_j[i] = 0;
+      return;
+    }
+    const bool dyn = sl >= p.n0;
+    const int64_t c0 = st.adm_c0[sl], j = st.rj[sl];
+    const bool ok = st.rok[sl] != 0;
+    const bool rec = p.evl && dyn && ok && (c0 + j < K);
+    const int64_t hd = rec ? sl - p.n0 : p.Cdyn, hj = rec ? j : 0;
+    hrec_dyn[i] = hd;
+    hrec_j[i] = hj;
+    if (in_range(hj, K)) st.pstep[hd * K + hj] = s;  // non-recorded hits write the trash row (Cdyn, 0), as the reference
+    st.rj[sl] = (int8_t)(j + (rec ? 1 : 0));
+    st.rok[sl] = (int8_t)(ok && !(dyn && !rec));
+  }
+};
+
 // Per-item quantities of an eviction (elara_dir.cpp:73-77, 80, 89, 92).
 struct EvCounts {
   int nalloc;  // log ids for the resident history (rows going back to L): k < j
@@ -533,6 +585,12 @@ void dir_lsteps_hits_launch(const elr_dir_state& S, const elr_dir_params& P, con
                             const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s, int32_t* L_steps,
                             int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j, hipStream_t strm,
                             const int64_t* desc = nullptr);
+// The same as a functor and its block count, for a launch beside an independent body (the device-driven step pairs
+// it with the segment sum's final kernel).
+DirLstepsHits dir_lsteps_hits_prep(const elr_dir_state& S, const elr_dir_params& P, const int64_t* hs, int64_t nh,
+                                   const int64_t* L_row, const int32_t* L_cnt, int64_t nL, int64_t s,
+                                   int32_t* L_steps, int32_t* L_ids, int64_t* hrec_dyn, int64_t* hrec_j,
+                                   const int64_t* desc, int64_t& blocks);
 
 struct DirEvictPlan {
   DirEvictCount count;

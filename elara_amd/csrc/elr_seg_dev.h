@@ -120,6 +120,16 @@ struct SegPartialsLaunch {
 int seg_partials_prep(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan, int64_t plan_bytes,
                       SegPartialsLaunch& out);
 
+struct DirLstepsHits;   // elr_dir_dev.h
+
+// elr_segment_sum_plan_final's launch with `first` (nb1 blocks; the directory's replay inputs and hit records of the
+// device-driven step, which touch none of the sum's arrays) in the same launch, its blocks first.  ELR_EUNSUPPORTED,
+// with nothing launched, when the plan's final kernel is not the single wave-per-row launch (the caller then
+// launches the two on their own).
+int segment_sum_plan_final_with(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan,
+                                int64_t plan_bytes, const int64_t* perm, float* out, int64_t out_rows,
+                                const DirLstepsHits& first, int64_t nb1, void* stream);
+
 template <class Visit>
 inline void seg_partials_visit(const SegPartialsLaunch& L, Visit&& visit) {
   const SegPartials<1>& a = L.a;

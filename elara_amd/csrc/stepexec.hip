@@ -26,6 +26,7 @@
 #include "elr_asm_dev.h"
 #include "elr_dir_dev.h"
 #include "elr_exec_dev.h"
+#include "elr_seg_dev.h"
 
 namespace {
 
@@ -360,8 +361,10 @@ extern "C" int64_t elr_step_exec_dev_bytes(const elr_exec_args* args) {
   return L.total;
 }
 
-extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes,
-                                 elr_exec_out* out, void* stream) {
+// The device-driven executor; with lsteps_done its first launch (call A's replay inputs and hit records) was issued
+// by the caller already (elr_step_dev runs it beside the segment sum's final kernel).
+static int step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes,
+                         elr_exec_out* out, void* stream, bool lsteps_done) {
   using namespace elr;
   if (!args || !out || !desc) return ELR_EINVAL;
   const elr_exec_args& a = *args;
@@ -464,7 +467,8 @@ extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc,
   // 1. call A's replay inputs and hit records
   const elr_dir_state S = a.dir;
   const elr_dir_params P = a.pv;
-  dir_lsteps_hits_launch(S, P, a.sl_ord, n, a.L_row, a.L_cnt, n, s, L_steps, L_ids, hrec_dyn, hrec_j, st, desc);
+  if (!lsteps_done)
+    dir_lsteps_hits_launch(S, P, a.sl_ord, n, a.L_row, a.L_cnt, n, s, L_steps, L_ids, hrec_dyn, hrec_j, st, desc);
   // 2-4. eviction counts + the hits; eviction apply + the assembly; eviction release + the eviction moves
   const int64_t ev_blocks = dir_nblocks(nev > 0 ? nev : 1);
   const DirEvictPlan ep = dir_evict_plan(S, P, a.slots.ev_slot, nev, nullptr, nullptr, ev_row, rep, evl_ids,
@@ -491,6 +495,11 @@ struct StepDevLayout {
   elr_step_dev_out o;
   int64_t plan_scratch, plan_scratch_bytes, exec_bytes, total;
 };
+
+extern "C" int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes,
+                                 elr_exec_out* out, void* stream) {
+  return step_exec_dev(args, desc, ws, ws_bytes, out, stream, false);
+}
 
 // Workspace: the plan's outputs at their bounds (n rows, nd dynamic slots), its scratch, G [n, D], then the
 // executor's workspace.
@@ -568,9 +577,6 @@ extern "C" int elr_step_dev(const elr_step_dev_args* args, void* ws, int64_t ws_
                          (int)a.key_bits, a.dplan, a.dplan_bytes, stream);
   if (rc) return rc;
   float* G = reinterpret_cast<float*>(w + L.o.grad_rows);
-  if (a.n_occ > 0 && (rc = elr_segment_sum_plan_final(a.grad, a.n_occ, D, (int)a.key_bits, a.dplan, a.dplan_bytes,
-                                                      po.rank, G, n, stream)))
-    return rc;
   elr_exec_args e = a.exec;
   e.b[ELR_NRANK] = n;
   e.u_ord = po.u_ord;
@@ -582,7 +588,28 @@ extern "C" int elr_step_dev(const elr_step_dev_args* args, void* ws, int64_t ws_
   e.slots.ev_slot = po.dyn_out;
   e.slots.keep = po.dyn_out;
   e.upd.grad = G;
-  if ((rc = elr_step_exec_dev(&e, a.ctl.desc, w + L.o.exec_ws, L.exec_bytes, &L.o.exec, stream))) return rc;
+  // the segment sum's final kernel, with the executor's first launch (call A's replay inputs and hit records, which
+  // need the plan's scatter and nothing of the sum) beside it in one launch where the final kernel allows it
+  bool lsteps_done = false;
+  ExecLayout EL;
+  if (a.n_occ > 0 && exec_layout_dev(e, EL)) {
+    char* ew = w + L.o.exec_ws;
+    int64_t lblocks = 0;
+    const elr::DirLstepsHits lh = elr::dir_lsteps_hits_prep(
+        e.dir, e.pv, e.sl_ord, n, e.L_row, e.L_cnt, n, e.s, reinterpret_cast<int32_t*>(ew + EL.o.L_steps),
+        reinterpret_cast<int32_t*>(ew + EL.o.L_ids), reinterpret_cast<int64_t*>(ew + EL.o.hrec_dyn),
+        reinterpret_cast<int64_t*>(ew + EL.o.hrec_j), a.ctl.desc, lblocks);
+    rc = elr::segment_sum_plan_final_with(a.grad, a.n_occ, D, (int)a.key_bits, a.dplan, a.dplan_bytes, po.rank, G, n,
+                                          lh, lblocks, stream);
+    if (rc == ELR_OK) lsteps_done = true;
+    else if (rc != ELR_EUNSUPPORTED) return rc;
+  }
+  if (a.n_occ > 0 && !lsteps_done &&
+      (rc = elr_segment_sum_plan_final(a.grad, a.n_occ, D, (int)a.key_bits, a.dplan, a.dplan_bytes, po.rank, G, n,
+                                       stream)))
+    return rc;
+  if ((rc = step_exec_dev(&e, a.ctl.desc, w + L.o.exec_ws, L.exec_bytes, &L.o.exec, stream, lsteps_done)))
+    return rc;
   *out = L.o;
   return ELR_OK;
 }
