@@ -21,7 +21,10 @@
 // the same step); the moves read evf_slots and evl_ids of launch 3; the admissions write the slots the eviction
 // kernels of launches 2-4 read, and call B pops the log ids that launch 4 pushed.  (Pairing the apply kernel, the
 // largest of the eviction kernels in registers, with the assembly rather than the Adam pass keeps both pairs at the
-// occupancy of their row kernel.)
+// occupancy of their row kernel.)  In the device-driven step (elr_step_dev) launch 1 shares its launch with the
+// segment sum's final kernel: both read only the plan's scatter and the sum writes only the per-row gradients G,
+// which neither launch 1 nor the directory reads, while launch 1 writes the replay inputs, the hits' history records
+// and the directory's pstep / rj / rok, which the sum does not touch.
 #include "elr_admit_dev.h"
 #include "elr_asm_dev.h"
 #include "elr_dir_dev.h"

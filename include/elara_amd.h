@@ -625,7 +625,9 @@ int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, 
 
 /* A whole device-driven step in one call (no counterpart in the reference): elr_plan_step, the rest of the batch's
  * segment sum (elr_segment_sum_plan_final, in the class order the plan resolves) and elr_step_exec_dev, with every
- * array in one workspace that the caller keeps from step to step (elr_step_dev_bytes, 256-byte aligned).
+ * array in one workspace that the caller keeps from step to step (elr_step_dev_bytes, 256-byte aligned).  Where the
+ * sum's final kernel is the single wave-per-row launch (D = 64, 128, 256 or 512, 16-byte aligned rows, more than
+ * 3072 occurrences), the executor's first launch (call A's replay inputs and hit records) runs in the same launch. 
  *   plan:  as for elr_plan_step; its u, n, n_dev, s and next_mask change per step, nd bounds the dynamic slots;
  *          the output pointers are ignored (the call places them in ws).
  *   ctl:   as for elr_plan_step (desc is where this step's descriptor goes).
