@@ -781,7 +781,7 @@ def _c5_run(args, sync_free, sample=8):
     st = ElaraStep(tabs.toff, tabs.R, D, C, static_rows=static, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T',
                    seed=42, bound=synth.bound_for(D), hp=synth.ADAM, max_step=total + 2, log_cap=log_cap,
                    mat_cap=mat_cap, device=dev, host_arenas=host, dir_impl=args.dir_impl, sync_free=sync_free,
-                   link_stream=not args.one_stream if host else None)
+                   link_stream=not args.one_stream if host else None, field_layout=args.c5_field_sort)
     gen = torch.Generator(dev).manual_seed(5)
     gs = [torch.randn(O, D, device=dev, generator=gen) * 1e-3 for _ in range(8)]
     mark = {'c': 0, 'nL': 0}
@@ -838,6 +838,8 @@ def mode_c5(args):
                              'Zipf(1.1), pool 337,626 (321,242 static), K=3, evl on' % (where, a['R']),
                  'arenas': 'host' if a['host'] else 'hbm', 'dir_impl': args.dir_impl, 'mat_top': a['mat_top'],
                  'log_top': a['log_top'], 'host_gc': 'set-up objects frozen during the loop (step.run freeze_gc)',
+                 'dedup': ('sorted per table (elr_dedup_plan_fields)' if args.c5_field_sort
+                           else 'general radix sort (elr_dedup_plan)'),
                  'occurrences_per_step': a['O'], 'unique_rows_per_step': uniq / steps, 'dim': a['D']},
                 byts / 1e9,
                 extra={'steps_per_s': steps / el, 'stats': s,
@@ -1032,6 +1034,9 @@ def main():
     ap.add_argument('--one-stream', action='store_true',
                     help='C5 with host arenas: the whole step on one stream (device-driven) instead of the update\'s '
                          'host-arena writes on a link stream beside the next step (host-planned)')
+    ap.add_argument('--c5-field-sort', action=argparse.BooleanOptionalAction, default=True,
+                    help='C5: sort each batch per table (its layout, as the reference builds it) instead of the '
+                         'general radix sort')
     ap.add_argument('--dir-impl', default='cpp', choices=['cpp', 'ref', 'triton'],
                     help="C5's directory allocation order (the reference's --elara-dir-impl; cpp and ref are equal)")
     ap.add_argument('--no-cpu', action='store_true', help='skip the CPU baseline leg')

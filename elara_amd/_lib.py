@@ -75,6 +75,8 @@ SIGNATURES = {
     'elr_step_update': (ctypes.c_int, [c_vp, c_vp]),
     'elr_dedup_plan_bytes': (c_i64, [c_i64, c_i64]),
     'elr_dedup_plan': (ctypes.c_int, [c_vp, c_i64, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64, c_i64, c_vp]),
+    'elr_dedup_plan_fields': (ctypes.c_int, [c_vp, c_i64, c_i64, c_vp, ctypes.c_int, c_vp, c_vp, c_vp, c_vp, c_i64,
+                                             c_i64, c_vp]),
     'elr_segment_sum_plan': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64, c_vp]),
     'elr_segment_sum_plan_final': (ctypes.c_int, [c_vp, c_i64, c_i64, ctypes.c_int, c_vp, c_i64, c_vp, c_vp, c_i64,
                                                   c_vp]),

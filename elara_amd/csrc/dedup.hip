@@ -404,6 +404,282 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __rest
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 0) *d_E = before;
 }
 
+// ---- dedup plan of a batch laid out by field -------------------------------------------------------------------
+// A batch of nrows samples x nf fields in (sample, field) order, field c holding rows [lo[c], lo[c + 1]) of the
+// table with the bounds ascending: every id of field c is below every id of field c + 1, so the stable sort of the
+// whole batch is field 0's column sorted stably, then field 1's, and so on (within a column, sample order is
+// occurrence order).  One block per field sorts its column of at most kFieldRows ids in LDS: LSD passes of at most
+// kFieldDigit bits over the id's offset in its field, each key ranked as in k_radix_scatter (ballots, a running
+// count per wave, a scan over the waves), the column re-read from LDS after each pass.  The plan is then the
+// general path's, bit for bit, in two launches (k_field_sort, then k_field_apply, which adds the earlier fields'
+// segment and chunk counts) instead of three per radix pass and four for the segments and chunks.  An id outside
+// its field's rows takes the key R_c (the field's row count), sorts after the field's ids and comes out as -1 in
+// uniq: a row out of range for the caller.
+constexpr int kFieldThreads = 1024;
+constexpr int kFieldItems = 16;
+constexpr int64_t kFieldRows = (int64_t)kFieldThreads * kFieldItems;   // samples per batch: the row index is 16-bit
+constexpr int kFieldDigit = 9;
+constexpr int kFieldMax = 128;                      // fields per batch (the bounds travel as a kernel argument)
+constexpr int64_t kFieldSpanMax = (int64_t(1) << 31) - 2;   // rows per field: keys 0 .. R_c fit in 31 bits
+
+struct FieldBounds {
+  int64_t lo[kFieldMax + 1];
+};
+
+// Passes and digit width for keys in [0, span]: ceil(bits / kFieldDigit) passes of equal width.
+__device__ __forceinline__ void field_digits(int64_t span, int& passes, int& rb) {
+  int bits = 1;
+  while (bits < 31 && (int64_t(1) << bits) <= span) ++bits;
+  passes = (bits + kFieldDigit - 1) / kFieldDigit;
+  rb = (bits + passes - 1) / passes;
+}
+
+// Head flags of the sorted column in lk (bit r: this thread's item r, position w * kFieldItems * 64 + r * 64 +
+// lane) and this wave's head count.
+__device__ __forceinline__ uint32_t field_heads(const uint32_t* lk, int n, int& wcount) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint32_t hm = 0;
+  wcount = 0;
+#pragma unroll
+  for (int r = 0; r < kFieldItems; ++r) {
+    const int j = w * kFieldItems * 64 + r * 64 + lane;
+    const bool h = j < n && (j == 0 || lk[j - 1] != lk[j]);
+    hm |= h ? 1u << r : 0u;
+    wcount += __popcll(__ballot(h));
+  }
+  return hm;
+}
+
+// Positions of the column's segment heads, hpos[u] for u < U, and hpos[U] = n, from the head flags; returns U.
+// Synchronises the block before writing (hpos may share LDS with what the head test read) and after.
+__device__ __forceinline__ int field_head_positions(uint32_t hm, int wcount, int n, int* wtot, int* hpos) {
+  constexpr int NW = kFieldThreads / 64;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) wtot[w] = wcount;
+  __syncthreads();
+  int U = 0, run = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    U += wtot[q];
+    run += q < w ? wtot[q] : 0;
+  }
+#pragma unroll
+  for (int r = 0; r < kFieldItems; ++r) {
+    const bool h = (hm >> r) & 1u;
+    const uint64_t bal = __ballot(h);
+    if (h) hpos[run + __popcll(bal & lanemask_lt())] = w * kFieldItems * 64 + r * 64 + lane;
+    run += __popcll(bal);
+  }
+  if (threadIdx.x == 0) hpos[U] = n;
+  __syncthreads();
+  return U;
+}
+
+__global__ __launch_bounds__(kFieldThreads) void k_field_sort(const int64_t* __restrict__ ids, int64_t nrows, int nf,
+                                                              FieldBounds fb, uint32_t* __restrict__ skeys,
+                                                              int32_t* __restrict__ svals, int64_t* __restrict__ cnt,
+                                                              int64_t* __restrict__ d_hot) {
+  constexpr int NW = kFieldThreads / 64, WSPAN = kFieldItems * 64, BINS = 1 << kFieldDigit;
+  __shared__ uint32_t lk[kFieldRows + 1];   // the column by digit; at the end the head positions (U + 1 of them)
+  __shared__ uint16_t lv[2][kFieldRows];    // sample index of each key: pass p writes lv[p & 1]
+  __shared__ uint16_t wc[NW][BINS];         // per wave: running count of digit d, then the count in earlier waves
+  __shared__ int lbase[BINS];
+  __shared__ int wtot[NW];
+  const int c = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int n = (int)nrows;
+  const int64_t lo = fb.lo[c], hi = fb.lo[c + 1], R = hi - lo;
+  int passes, rb;
+  field_digits(R, passes, rb);
+  const int nbins = 1 << rb;
+  const uint32_t mask = (uint32_t)nbins - 1u;
+  if (c == 0 && t == 0) *d_hot = 0;
+  uint32_t kk[kFieldItems];
+#pragma unroll
+  for (int r = 0; r < kFieldItems; ++r) {
+    const int j = w * WSPAN + r * 64 + lane;
+    uint32_t key = 0;
+    if (j < n) {
+      const int64_t id = ids[(int64_t)j * nf + c];
+      key = id >= lo && id < hi ? (uint32_t)(id - lo) : (uint32_t)R;
+    }
+    kk[r] = key;
+  }
+  for (int p = 0; p < passes; ++p) {
+    const int shift = p * rb;
+    const uint16_t* vsrc = lv[(p + 1) & 1];
+    uint16_t* vdst = lv[p & 1];
+    if (t < nbins)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) wc[q][t] = 0;
+    __syncthreads();
+    int rk[kFieldItems];
+#pragma unroll
+    for (int r = 0; r < kFieldItems; ++r) {
+      const bool valid = w * WSPAN + r * 64 + lane < n;
+      const uint32_t d = (kk[r] >> shift) & mask;
+      uint64_t m = __ballot(valid);
+      for (int b = 0; b < rb; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t bal = __ballot(bit);
+        m &= bit ? bal : ~bal;
+      }
+      const int lr = __popcll(m & lanemask_lt());
+      // one wave's LDS accesses take effect in program order: every lane reads the count before the lowest lane of
+      // its digit group adds the group's size
+      const int before = valid ? (int)wc[w][d] : 0;
+      rk[r] = valid ? before + lr : -1;
+      if (valid && lr == 0) wc[w][d] = (uint16_t)(before + __popcll(m));
+    }
+    __syncthreads();
+    int run = 0;
+    if (t < nbins)
+#pragma unroll
+      for (int q = 0; q < NW; ++q) {
+        const int x = wc[q][t];
+        wc[q][t] = (uint16_t)run;
+        run += x;
+      }
+    {
+      int v[1] = {run}, ex[1], tot[1];
+      block_excl_scan<kFieldThreads, 1>(v, ex, tot);
+      if (t < nbins) lbase[t] = ex[0];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kFieldItems; ++r)
+      if (rk[r] >= 0) {
+        const int j = w * WSPAN + r * 64 + lane;
+        const uint32_t d = (kk[r] >> shift) & mask;
+        const int lp = lbase[d] + wc[w][d] + rk[r];
+        lk[lp] = kk[r];
+        vdst[lp] = p == 0 ? (uint16_t)j : vsrc[j];
+      }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kFieldItems; ++r) {
+      const int j = w * WSPAN + r * 64 + lane;
+      if (j < n) kk[r] = lk[j];
+    }
+  }
+  const uint16_t* vfin = lv[(passes - 1) & 1];
+  const int64_t out0 = (int64_t)c * nrows;
+#pragma unroll
+  for (int r = 0; r < kFieldItems; ++r) {
+    const int j = w * WSPAN + r * 64 + lane;
+    if (j < n) {
+      skeys[out0 + j] = kk[r];
+      svals[out0 + j] = (int32_t)vfin[j] * nf + c;
+    }
+  }
+  int wcount;
+  const uint32_t hm = field_heads(lk, n, wcount);
+  int* hpos = reinterpret_cast<int*>(lk);
+  const int U = field_head_positions(hm, wcount, n, wtot, hpos);
+  int e = 0;
+  for (int u = t; u < U; u += kFieldThreads) e += part_chunks(hpos[u + 1] - hpos[u]);
+  int v[1] = {e}, ex[1], tot[1];
+  block_excl_scan<kFieldThreads, 1>(v, ex, tot);
+  if (t == 0) {
+    cnt[2 * c] = U;
+    cnt[2 * c + 1] = tot[0];
+  }
+}
+
+// Field c's unique ids, segment starts, first occurrences, inverse and chunk plan, offset by the earlier fields'
+// segment and chunk counts (cnt, from k_field_sort).  The last field's block stores U, E and seg_start[U] = n.
+__global__ __launch_bounds__(kFieldThreads) void k_field_apply(const uint32_t* __restrict__ skeys,
+                                                               const int32_t* __restrict__ svals, int64_t nrows,
+                                                               int nf, FieldBounds fb, const int64_t* __restrict__ cnt,
+                                                               int64_t* __restrict__ d_tot,
+                                                               int64_t* __restrict__ n_unique,
+                                                               int64_t* __restrict__ uniq,
+                                                               int64_t* __restrict__ seg_start,
+                                                               int32_t* __restrict__ seg_occ0,
+                                                               int64_t* __restrict__ inverse,
+                                                               int32_t* __restrict__ chunk_off,
+                                                               int32_t* __restrict__ chunk_seg,
+                                                               int32_t* __restrict__ hot_list) {
+  constexpr int NW = kFieldThreads / 64, WSPAN = kFieldItems * 64;
+  __shared__ uint32_t lk[kFieldRows];
+  __shared__ int hpos[kFieldRows + 1];
+  __shared__ int wtot[NW];
+  __shared__ int64_t pre[2][NW];
+  const int c = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int n = (int)nrows;
+  const int64_t lo = fb.lo[c], R = fb.lo[c + 1] - lo, out0 = (int64_t)c * nrows;
+  {
+    // segments and chunks of the earlier fields (nf <= kFieldMax <= kFieldThreads)
+    int64_t a = t < c ? cnt[2 * t] : 0, b = t < c ? cnt[2 * t + 1] : 0;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      a += __shfl_xor(a, d, 64);
+      b += __shfl_xor(b, d, 64);
+    }
+    if (lane == 0) {
+      pre[0][w] = a;
+      pre[1][w] = b;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kFieldItems; ++r) {
+    const int j = w * WSPAN + r * 64 + lane;
+    if (j < n) lk[j] = skeys[out0 + j];
+  }
+  __syncthreads();
+  int64_t su = 0, se = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) {
+    su += pre[0][q];
+    se += pre[1][q];
+  }
+  int wcount;
+  const uint32_t hm = field_heads(lk, n, wcount);
+  const int U = field_head_positions(hm, wcount, n, wtot, hpos);
+  // every position's segment: the last head at or before it (a binary search of hpos, which the head positions'
+  // ballots would otherwise have to carry through the items)
+  for (int j = t; j < n; j += kFieldThreads) {
+    int a = 0, b = U - 1;   // hpos[a] <= j < hpos[b + 1]
+    while (a < b) {
+      const int m = (a + b + 1) >> 1;
+      if (hpos[m] <= j) a = m;
+      else b = m - 1;
+    }
+    const int64_t gu = su + a;
+    const int32_t o = svals[out0 + j];
+    if (hpos[a] == j) {
+      const uint32_t k = lk[j];
+      uniq[gu] = (int64_t)k == R ? -1 : lo + (int64_t)k;
+      seg_start[gu] = out0 + j;
+      seg_occ0[gu] = o;
+    }
+    if (inverse) inverse[o] = gu;
+  }
+  int64_t before = se;
+  for (int u0 = 0; u0 < U; u0 += kFieldThreads) {
+    const int u = u0 + t;
+    const int L = u < U ? hpos[u + 1] - hpos[u] : 0;
+    const int e = u < U ? part_chunks(L) : 0;
+    int v[1] = {e}, ex[1], tot[1];
+    block_excl_scan<kFieldThreads, 1>(v, ex, tot);
+    if (u < U) {
+      const int64_t off = before + ex[0];
+      const int32_t gu = (int32_t)(su + u);
+      chunk_off[gu] = (int32_t)off;
+      for (int k = 0; k < e; ++k) chunk_seg[off + k] = gu;
+      if (seg_hot(L)) hot_list[atomicAdd(reinterpret_cast<unsigned long long*>(d_tot + 2), 1ull)] = gu;
+    }
+    before += tot[0];
+    __syncthreads();   // block_excl_scan's LDS is reused by the next round
+  }
+  if (c == nf - 1 && t == 0) {
+    const int64_t Ut = su + U;
+    d_tot[0] = Ut;
+    if (n_unique) *n_unique = Ut;
+    seg_start[Ut] = out0 + n;
+    d_tot[1] = before;
+  }
+}
+
 // Does occurrence k of a segment (occurrence index o, previous one prev) start a new group?  Sort path
 // (win_shift == 0): every kAtenGroup occurrences; windowed path: when its index window differs from the previous
 // occurrence's.  Wave-uniform (all arguments are).
@@ -1099,6 +1375,39 @@ extern "C" int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64
                                  : dedup_core<uint64_t>(ids, n, key_bits, S, uniq, inverse, n_unique, st);
   if (cur != plan_result_buffer(key_bits)) return ELR_EINVAL;
   chunk_plan(n, S, st);
+  return launch_status();
+}
+
+extern "C" int elr_dedup_plan_fields(const int64_t* ids, int64_t nrows, int64_t nfields, const int64_t* field_lo,
+                                     int key_bits, int64_t* uniq, int64_t* inverse, int64_t* n_unique, void* plan,
+                                     int64_t plan_bytes, int64_t D, void* stream) {
+  using namespace elr;
+  if (nrows < 0 || nfields < 1 || !field_lo || key_bits < 1 || key_bits > 64 || D < 1) return ELR_EINVAL;
+  if (nrows > 0 && nfields > ((int64_t(1) << 31) - 1) / nrows) return ELR_EINVAL;
+  const int64_t n = nrows * nfields;
+  if (n == 0) return ELR_OK;
+  if (field_lo[0] < 0) return ELR_EINVAL;
+  for (int64_t c = 0; c < nfields; ++c)
+    if (field_lo[c + 1] < field_lo[c]) return ELR_EINVAL;
+  if (nrows > kFieldRows || nfields > kFieldMax || n <= kAtenSmall)
+    return elr_dedup_plan(ids, n, key_bits, uniq, inverse, n_unique, plan, plan_bytes, D, stream);
+  for (int64_t c = 0; c < nfields; ++c)
+    if (field_lo[c + 1] - field_lo[c] > kFieldSpanMax)
+      return elr_dedup_plan(ids, n, key_bits, uniq, inverse, n_unique, plan, plan_bytes, D, stream);
+  if (!ids || !uniq || !plan) return ELR_EINVAL;
+  DedupScratch S;
+  if (plan_bytes < dedup_scratch_bytes(n, D, &S, plan)) return ELR_ECAPACITY;
+  static_assert(2 * kFieldMax <= kRadixMaxBins, "the per-field counts fit in the first histogram's space");
+  FieldBounds fb;
+  for (int64_t c = 0; c <= nfields; ++c) fb.lo[c] = field_lo[c];
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* sv = S.vals[plan_result_buffer(key_bits)];
+  k_field_sort<<<(unsigned)nfields, kFieldThreads, 0, st>>>(ids, nrows, (int)nfields, fb, (uint32_t*)S.keys[0], sv,
+                                                            S.hist, S.d_tot + 2);
+  k_field_apply<<<(unsigned)nfields, kFieldThreads, 0, st>>>((const uint32_t*)S.keys[0], sv, nrows, (int)nfields, fb,
+                                                             S.hist, S.d_tot, n_unique, uniq, S.seg_start,
+                                                             S.seg_occ0, inverse, S.chunk_off, S.chunk_seg,
+                                                             S.hot_list);
   return launch_status();
 }
 

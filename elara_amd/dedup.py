@@ -84,10 +84,20 @@ class DedupPlan:
     __slots__ = ('buf', 'nbytes', 'n', 'D', 'key_bits', 'U')
 
 
-def unique_plan(ids, D, bound=None):
+def field_bounds(lo):
+    """Host int64 array of a batch's field bounds for unique_plan(fields=...): nfields + 1 ascending values, field
+    c's ids in [lo[c], lo[c + 1])."""
+    import numpy as np
+    a = np.ascontiguousarray(np.asarray(lo, dtype=np.int64))
+    if a.ndim != 1 or a.size < 2 or a[0] < 0 or bool((a[1:] < a[:-1]).any()):
+        raise RuntimeError('field bounds must be at least two ascending non-negative values')
+    return a
+
+
+def unique_plan(ids, D, bound=None, fields=None):
     """unique(ids) without the inverse, keeping the sort as a plan for segment_sum_plan over gradients of width D:
-    returns (u, plan)."""
-    u, plan, nu = unique_plan_async(ids, D, bound)
+    returns (u, plan).  fields: see unique_plan_async."""
+    u, plan, nu = unique_plan_async(ids, D, bound, fields=fields)
     if nu is not None:
         plan.U = int(nu)
         u = u[:plan.U]
@@ -102,13 +112,17 @@ def plan_bytes(n, D):
     return nbytes
 
 
-def unique_plan_async(ids, D, bound=None, nu_out=None, out=None):
+def unique_plan_async(ids, D, bound=None, nu_out=None, out=None, fields=None):
     """unique_plan without reading the unique count: returns (u_full, plan, nu) with u_full [n] whose first nu
     entries are the unique ids, nu the count on the device (None when n == 0).  Set plan.U once nu is known.
     nu_out (int64 [1] on the device, optional): where the count goes, else a new tensor.
     out (optional): (buf, u, nu) to write into instead of new tensors -- uint8 buf of at least plan_bytes(n, D)
     bytes, int64 u of at least n elements, int64 nu [1] (nu_out, if given, takes its place); the caller keeps them
-    from being reused before the GPU's work on the plan is done."""
+    from being reused before the GPU's work on the plan is done.
+    fields (optional, field_bounds(...)): the batch is laid out by field -- (sample, field) order, field c's ids in
+    [fields[c], fields[c + 1]) -- and is sorted per field (elr_dedup_plan_fields): the same plan, in two launches.
+    An id outside its field's rows comes out as -1 in u.  Batches whose size is not a multiple of the field count
+    take the general sort."""
     flat = _ids(ids)
     n = flat.numel()
     dev = flat.device
@@ -135,7 +149,14 @@ def unique_plan_async(ids, D, bound=None, nu_out=None, out=None):
     if nu_out is not None and not (nu_out.dtype == I64 and nu_out.device == dev and nu_out.numel() == 1):
         raise RuntimeError(f'nu_out must be an int64 tensor of one element on {dev}')
     nu = nu_out if nu_out is not None else torch.empty(1, dtype=I64, device=dev)
+    nf = 0 if fields is None else fields.size - 1
     with _lib.on_device(dev):
+        if nf > 0 and n % nf == 0:
+            rc = _lib.lib().elr_dedup_plan_fields(_lib.ptr(flat), n // nf, nf, fields.ctypes.data, plan.key_bits,
+                                                  _lib.ptr(u), None, _lib.ptr(nu), _lib.ptr(plan.buf), nbytes, int(D),
+                                                  _lib.stream_of(flat))
+            _lib.check(rc, 'elr_dedup_plan_fields')
+            return u, plan, nu
         rc = _lib.lib().elr_dedup_plan(_lib.ptr(flat), n, plan.key_bits, _lib.ptr(u), None, _lib.ptr(nu),
                                        _lib.ptr(plan.buf), nbytes, int(D), _lib.stream_of(flat))
     _lib.check(rc, 'elr_dedup_plan')

@@ -33,7 +33,7 @@ import torch
 
 from . import _lib  # noqa: F401  (the library must be present)
 from .assemble import assemble_rows
-from .dedup import plan_bytes, segment_sum_plan, unique_plan, unique_plan_async
+from .dedup import field_bounds, plan_bytes, segment_sum_plan, unique_plan, unique_plan_async
 from .elara_dir import dir_ext
 from .gpu_ops import ScalarTable, init_rows, replay_rows
 from .ops import adam_rows_dense, gpu_adam
@@ -75,8 +75,8 @@ class HipBackend:
     def unique(self, ids, bound=None):
         return unique_plan(ids, self.D, bound)
 
-    def unique_async(self, ids, bound=None, nu_out=None, out=None):
-        return unique_plan_async(ids, self.D, bound, nu_out, out)
+    def unique_async(self, ids, bound=None, nu_out=None, out=None, fields=None):
+        return unique_plan_async(ids, self.D, bound, nu_out, out, fields)
 
     def plan_bytes(self, n):
         return plan_bytes(n, self.D)
@@ -402,13 +402,17 @@ class ElaraStep:
     HostBudgetExceeded when a step would pass it (srm2/elara.py:63-81); dir_impl: the log-id allocation order of
     the reference directory it stands in for (srm2/elara.py:150-155, srm2/train.py:133): 'cpp' (the default) or
     'ref', equal, or 'triton', which allocates every log id of a step before any release (srm2/elara_kernels.py);
-    the other states are the same under all three.
+    the other states are the same under all three.  field_layout: every batch that run() loads is laid out by table,
+    as the reference's one-hot batches are (srm2/train.py:187-214): (sample, table) order, with table t's column
+    holding rows [toff[t], toff[t + 1]) (toff[T] = R); its dedup plan then sorts each table's column on its own
+    (dedup.unique_plan_async(fields=...)), the same plan in two launches.  A row outside its table's range is then
+    reported as a row outside [0, R).
     """
 
     def __init__(self, toff, R, D, C, static_rows=None, K=3, kthr=3, evl=True, L=8, depth=3, st_mode='T', seed=42,
                  bound=0.01, hp=(1e-3, 0.9, 0.999, 1e-8), max_step=1000, log_cap=None, mat_cap=None, device='cuda',
                  backend=None, host_arenas=False, dyn='ttl', evl_gate_frac=0.75, host_budget=0, budget_chunk=CHUNK,
-                 dir_impl='cpp', sync_free=True, link_stream=None):
+                 dir_impl='cpp', sync_free=True, link_stream=None, field_layout=False):
         d = torch.device(device)
         if dir_impl not in ('cpp', 'ref', 'triton'):
             raise ValueError(f"dir_impl must be 'cpp', 'ref' or 'triton' (got {dir_impl!r})")
@@ -432,6 +436,9 @@ class ElaraStep:
         self.be = backend or HipBackend(D, seed, bound, hp, max_step, d)
         self.toff = torch.as_tensor(toff, dtype=I64).to(d)
         T = self.toff.numel()
+        # batches laid out by table ((sample, table) order, table t's column holding its rows): sorted per table
+        self.field_bounds = (field_bounds(torch.cat([self.toff.cpu(), torch.tensor([R], dtype=I64)]).numpy())
+                             if field_layout else None)
         self.kthr = (torch.full((T,), int(kthr), dtype=I8) if isinstance(kthr, int)
                      else torch.as_tensor(kthr, dtype=I8)).to(d)
         self.log_cap = int(log_cap or 2 * R)
@@ -1209,6 +1216,8 @@ def _run(step, batches, grads, steps, on_step):
         slot = None if step.sync_free else step.count_slot()
         kw = {} if slot is None else {'nu_out': slot}
         n = ids.numel()
+        if pool is not None and step.field_bounds is not None:
+            kw['fields'] = step.field_bounds
         e = pool.take(n, step.be.plan_bytes(n), side) if pool is not None and n else None
         if e is not None:
             ENTRY[j] = e

@@ -263,6 +263,19 @@ int elr_adam_dedup_noalloc(float* state, int64_t C, const int64_t* ids, const fl
 int64_t elr_dedup_plan_bytes(int64_t n, int64_t D);
 int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, int64_t* inverse, int64_t* n_unique,
                    void* plan, int64_t plan_bytes, int64_t D, void* stream);
+/* elr_dedup_plan for a batch laid out by field, as the reference's one-hot batches are (srm2/train.py:187-214:
+ * global id = local id + the field's table offset, flattened in (sample, field) order): ids [nrows * nfields],
+ * field c of sample i at ids[i * nfields + c], and field c's ids in [field_lo[c], field_lo[c + 1]) (field_lo: host
+ * array of nfields + 1 ascending bounds, field_lo[0] >= 0).  The whole batch sorted is then each field's column
+ * sorted, one after the other, and one block per field sorts its column in LDS: two launches in place of
+ * elr_dedup_plan's three per radix pass and four more.  The plan, uniq, inverse and n_unique are bitwise
+ * elr_dedup_plan's (the order of the hot-segment list aside, which no result depends on).  An id outside its
+ * field's rows breaks that contract: it comes out as -1 in uniq, a row out of range for the caller.  Shapes the
+ * per-field sort does not take (nrows > 16,384, nfields > 128, nrows * nfields <= 3,072, a field of more than
+ * 2^31 - 2 rows) go to elr_dedup_plan with the same arguments.  ELR_EINVAL for bounds that are not ascending. */
+int elr_dedup_plan_fields(const int64_t* ids, int64_t nrows, int64_t nfields, const int64_t* field_lo, int key_bits,
+                          int64_t* uniq, int64_t* inverse, int64_t* n_unique, void* plan, int64_t plan_bytes,
+                          int64_t D, void* stream);
 int elr_segment_sum_plan(const float* grad, int64_t n, int64_t D, int key_bits, const void* plan, int64_t plan_bytes,
                          const int64_t* perm, float* out, int64_t out_rows, void* stream);
 /* elr_segment_sum_plan in two parts, for a caller that queues the first beside other work: the partial chunks of

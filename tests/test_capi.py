@@ -241,6 +241,23 @@ def test_planner_executor_dedup_argument_checks():
     assert L.elr_dedup_plan(None, 0, 20, None, None, None, None, 0, 8, None) == 0                   # n == 0
     assert L.elr_dedup_plan(fake, 10, 0, fake, None, fake, fake, 1 << 20, 8, None) == -1            # key bits
     assert L.elr_dedup_plan(fake, 10, 20, fake, None, fake, fake, 1, 8, None) == -3                 # plan too small
+    lo = (ctypes.c_int64 * 4)(0, 100, 200, 300)
+    F = L.elr_dedup_plan_fields
+    assert F(None, 0, 3, lo, 20, None, None, None, None, 0, 8, None) == 0                           # n == 0
+    assert F(fake, 2000, 0, lo, 20, fake, None, fake, fake, 1 << 30, 8, None) == -1                 # no fields
+    assert F(fake, 2000, 3, None, 20, fake, None, fake, fake, 1 << 30, 8, None) == -1               # no bounds
+    assert F(fake, 1 << 30, 3, lo, 20, fake, None, fake, fake, 1 << 30, 8, None) == -1              # n >= 2^31
+    assert F(fake, 2000, 3, (ctypes.c_int64 * 4)(0, 100, 50, 300), 20, fake, None, fake, fake, 1 << 30, 8,
+             None) == -1                                                                             # descending
+    assert F(fake, 2000, 3, (ctypes.c_int64 * 4)(-1, 100, 200, 300), 20, fake, None, fake, fake, 1 << 30, 8,
+             None) == -1                                                                             # negative
+    assert F(fake, 2000, 3, lo, 20, fake, None, fake, fake, 1, 8, None) == -3                       # plan too small
+    assert F(fake, 100, 3, lo, 20, fake, None, fake, fake, 1, 8, None) == -3     # general sort: same checks
+    from elara_amd.dedup import field_bounds
+    assert field_bounds([0, 5, 5, 9]).dtype == np.int64
+    for bad in ([3], [0, 5, 4], [-1, 2], [[0, 1], [2, 3]]):
+        with pytest.raises(RuntimeError, match='ascending'):
+            field_bounds(bad)
     assert L.elr_segment_sum_plan(fake, 10, 600, 20, fake, 1 << 30, None, fake, 10, None) == -2     # D > 512
     assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1, None, fake, 10, None) == -3             # plan too small
     assert L.elr_segment_sum_plan(fake, 10, 8, 20, fake, 1 << 20, None, fake, -1, None) == -1

@@ -345,6 +345,98 @@ def test_gpu_dedup_plan_matches_unique_and_backward(dev, D, case):
     assert np.array_equal(bits(big.cpu().numpy()), bits(want))
 
 
+def field_case(case, rng):
+    """(ids [nrows * nfields] in (sample, field) order, field bounds) of a batch laid out by field."""
+    if case == 'c5':
+        tabs = synth.C5Tables(T=26, lo=1e3, hi=4e7, alpha=1.1, seed=3)
+        return tabs.batch(rng, 16384), np.append(tabs.toff, tabs.R)
+    vocab = {'ragged': [1, 3, 511, 512, 513, 2**17, 70000],       # 5,000 rows: one hot id per tiny field
+             'one_field': [2**20],                                  # 16,384 rows, one block
+             'wide': [50] * 100,                                    # 100 rows x 100 fields
+             'big_span': [2**31 - 2, 5, 40000],                     # keys of 31 bits: 4 passes
+             'fallback_rows': [3000, 90000, 17],                    # 20,000 rows: the general sort
+             'fallback_small': [100] * 26}[case]                    # 2,600 ids: ATen's windowed order
+    nrows = {'ragged': 5000, 'one_field': 16384, 'wide': 100, 'big_span': 12000, 'fallback_rows': 20000,
+             'fallback_small': 100}[case]
+    z = synth.ZipfFields(vocab, 1.1, seed=int(rng.integers(1 << 30)))
+    return z.draw(rng, nrows), np.append(z.offsets, z.offsets[-1] + z.vocab[-1])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('case', ['c5', 'ragged', 'one_field', 'wide', 'big_span', 'fallback_rows', 'fallback_small'])
+def test_gpu_dedup_plan_fields_matches_general(dev, case):
+    """A batch laid out by field, sorted per field (elr_dedup_plan_fields): the unique ids, the inverse and the
+    segment sums over its plan are bitwise those of the general sort's plan and the oracle's; the unique count is
+    the same.  Covers both result buffers of the plan (27- and 18-bit bounds), fields of one row (a hot segment of
+    every occurrence), digit widths at 2^9 +- 1, 31-bit keys, a hundred fields of 100 rows, and the shapes that go to
+    the general sort."""
+    import ctypes
+    from elara_amd import _lib
+    from elara_amd.dedup import field_bounds, plan_bytes, segment_sum_plan, unique_plan_async
+    print(f'[gpu-test] dedup plan by field {case}', flush=True)
+    rng = np.random.default_rng(29)
+    ids, lo = field_case(case, rng)
+    D = 64 if case == 'wide' else 128
+    n, nf, bound = ids.size, lo.size - 1, int(lo[-1])
+    t = torch.from_numpy(ids).to(dev)
+    u1, p1, nu1 = unique_plan_async(t, D, bound)
+    u2, p2, nu2 = unique_plan_async(t, D, bound, fields=field_bounds(lo))
+    U = int(nu1)
+    assert int(nu2) == U
+    assert torch.equal(u1[:U], u2[:U])
+    g = rng.standard_normal((n, D)).astype(np.float32)
+    u_ref, s_ref, _ = O.segment_sum(ids, g)
+    assert np.array_equal(u2[:U].cpu().numpy(), u_ref)
+    p1.U = p2.U = U
+    gd = torch.from_numpy(g).to(dev)
+    s1, s2 = segment_sum_plan(gd, p1), segment_sum_plan(gd, p2)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(s2.cpu().numpy()), bits(s_ref))
+    assert np.array_equal(bits(s1.cpu().numpy()), bits(s2.cpu().numpy()))
+    # the inverse (not asked for by the step)
+    inv = torch.full((n,), -5, dtype=torch.int64, device=dev)
+    uu, nu = torch.empty(n, dtype=torch.int64, device=dev), torch.empty(1, dtype=torch.int64, device=dev)
+    buf = torch.empty(plan_bytes(n, D), dtype=torch.uint8, device=dev)
+    fb = field_bounds(lo)
+    rc = _lib.lib().elr_dedup_plan_fields(_lib.ptr(t), n // nf, nf, fb.ctypes.data, p2.key_bits, _lib.ptr(uu),
+                                          _lib.ptr(inv), _lib.ptr(nu), _lib.ptr(buf), buf.numel(), D,
+                                          ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert int(nu) == U
+    assert np.array_equal(u_ref[inv.cpu().numpy()], ids)
+
+
+@pytest.mark.gpu
+def test_gpu_dedup_plan_fields_flags_ids_outside_their_field(dev):
+    """An id that is a valid row of another field breaks the layout's contract: the per-field plan reports it as -1
+    (a row out of range for the caller) and keeps every other id and segment sum as the general plan gives them."""
+    from elara_amd.dedup import field_bounds, segment_sum_plan, unique_plan_async
+    print('[gpu-test] dedup plan by field, id outside its field', flush=True)
+    rng = np.random.default_rng(31)
+    ids, lo = field_case('ragged', rng)
+    nf = lo.size - 1
+    bad = 7 * nf + 2                                 # sample 7, field 2 ([4, 515)), given a row of field 5
+    ids[bad] = lo[5] + 11
+    t = torch.from_numpy(ids).to(dev)
+    u, plan, nu = unique_plan_async(t, 128, int(lo[-1]), fields=field_bounds(lo))
+    U = int(nu)
+    got = u[:U].cpu().numpy()
+    assert (got == -1).sum() == 1
+    good = np.delete(ids, bad)
+    keep = got >= 0
+    assert np.array_equal(got[keep], np.unique(good))
+    plan.U = U
+    g = rng.standard_normal((ids.size, 128)).astype(np.float32)
+    s = segment_sum_plan(torch.from_numpy(g).to(dev), plan).cpu().numpy()
+    # the sort path groups each id's occurrences from its own first one, so the batch without the flagged occurrence
+    # sums every other id the same way
+    u_ref, s_ref, _ = O.segment_sum(good, np.delete(g, bad, axis=0))
+    assert np.array_equal(got[keep], u_ref)
+    assert np.array_equal(bits(s[keep]), bits(s_ref))
+    assert np.array_equal(bits(s[~keep][0]), bits(g[bad]))
+
+
 @pytest.mark.gpu
 def test_gpu_segment_sum_very_long_segment(dev):
     """One id with 100,000 occurrences (1,563 chunks) next to short ones."""

@@ -25,7 +25,8 @@ def make(cfg, device, backend=None):
                      log_cap=cfg['log_cap'], mat_cap=cfg['mat_cap'], device=device, backend=backend,
                      host_arenas=cfg.get('host', False), dyn=cfg.get('dyn', 'ttl'), host_budget=cfg.get('budget', 0),
                      budget_chunk=cfg.get('chunk', 64 << 20), dir_impl=cfg.get('dir_impl', 'cpp'),
-                     sync_free=cfg.get('sync_free', True), link_stream=cfg.get('link'))
+                     sync_free=cfg.get('sync_free', True), link_stream=cfg.get('link'),
+                     field_layout=cfg.get('field', False))
 
 
 def same_stats(a, b):
@@ -126,6 +127,21 @@ def test_step_raises_on_rows_out_of_range(where, request):
     st = make(cfg, dev, OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2) if where == 'cpu' else None)
     batches = [b.clone() for b in cfg['batches']]
     batches[2][5] = cfg['R'] + 7
+    with pytest.raises(ValueError, match='outside'):
+        run(st, batches, grads_fn(cfg, None))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('sync_free', [True, False])
+def test_gpu_step_field_layout_raises_on_row_of_another_table(dev, sync_free):
+    """With field_layout, a batch row that belongs to another table than its column's breaks the declared layout:
+    the per-table sort reports it as a row outside [0, R), device-driven and host-planned, and the step raises."""
+    from elara_amd.step import run
+    print(f'[gpu-test] elara step field layout, row of another table, sync_free={sync_free}', flush=True)
+    cfg = config(T=4, lo=200, hi=2000, B=1000, steps=4, C=800, n_static=300, field=True, sync_free=sync_free)
+    st = make(cfg, dev)
+    batches = [b.clone() for b in cfg['batches']]
+    batches[2][5] = int(cfg['toff'][3]) + 1          # sample 1, table 1's column: a row of table 3
     with pytest.raises(ValueError, match='outside'):
         run(st, batches, grads_fn(cfg, None))
 
@@ -283,14 +299,15 @@ def test_gpu_step_degenerate_batches(dev, name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('sync_free,ahead', [(True, True), (False, True), (True, False)])
-def test_gpu_step_ragged_batches(dev, sync_free, ahead):
+@pytest.mark.parametrize('sync_free,ahead,field', [(True, True, False), (False, True, False), (True, False, False),
+                                                   (True, True, True), (False, True, True)])
+def test_gpu_step_ragged_batches(dev, sync_free, ahead, field):
     """Batches of changing sizes (a later batch larger than any before it, then smaller ones): run() takes each
     batch's dedup-plan buffers from its pool, and a batch that outgrows every free entry gets new ones.  Device-
-    driven and host-planned, with the sorts on a second stream or on the step's own.  Equal to the oracle-driven
-    step."""
+    driven and host-planned, with the sorts on a second stream or on the step's own, and sorted per table (the
+    smallest batches, of at most 3,072 ids, then take the general sort).  Equal to the oracle-driven step."""
     from elara_amd.step import run
-    print(f'[gpu-test] elara step ragged batches sync_free={sync_free} ahead={ahead}', flush=True)
+    print(f'[gpu-test] elara step ragged batches sync_free={sync_free} ahead={ahead} field={field}', flush=True)
     sizes = [300, 100, 800, 200, 1600, 50, 1200, 400, 2400, 150, 700, 1000, 90, 3000, 500, 250]
     tabs = synth.C5Tables(T=6, lo=200, hi=20000, alpha=1.1, seed=5)
     rng = np.random.default_rng(12)
@@ -298,7 +315,7 @@ def test_gpu_step_ragged_batches(dev, sync_free, ahead):
     batches = [torch.from_numpy(tabs.batch(rng, b)) for b in sizes]
     O = sum(b.numel() for b in batches)
     cfg = dict(toff=tabs.toff, R=tabs.R, D=128, C=9000, static=static, steps=len(sizes), bound=synth.bound_for(128),
-               log_cap=O + 16, mat_cap=min(tabs.R + 1, O + 16), batches=batches, sync_free=sync_free)
+               log_cap=O + 16, mat_cap=min(tabs.R + 1, O + 16), batches=batches, sync_free=sync_free, field=field)
     g = make(cfg, dev)
     g.dedup_ahead = ahead
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
@@ -314,18 +331,19 @@ def test_gpu_step_ragged_batches(dev, sync_free, ahead):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('dir_impl,steps', [('cpp', 200), ('triton', 100)])
-def test_gpu_step_c5_full_shape(dev, dir_impl, steps):
+@pytest.mark.parametrize('dir_impl,steps,field', [('cpp', 200, True), ('triton', 100, False)])
+def test_gpu_step_c5_full_shape(dev, dir_impl, steps, field):
     """Config C5 shapes: 26 tables (vocab log-uniform in [1e3, 4e7], ~75M rows), batch 16,384 x 26 Zipf(1.1),
     D = 128, pool 337,626 (321,242 static hot rows), K = 3, evl on; 200 steps (the pool's steady-state churn and
     m / v of hot rows over many steps), HIP vs oracle bitwise: directory, pool, histories, arenas and the
     eval-style weights of every touched row.  Arena capacities as measured at this shape (about 47k log entries
     and 7k MAT rows per step in steady state) with headroom; the plan's capacity check raises if they run out.
-    Also 100 steps in the Triton directory's allocation order."""
+    The 200 steps sort each batch per table (as bench.py's C5 line does), the 100 steps in the Triton directory's
+    allocation order with the general sort."""
     from elara_amd.step import run
-    print(f'[gpu-test] elara step C5 full shape, {steps} steps, {dir_impl} order', flush=True)
+    print(f'[gpu-test] elara step C5 full shape, {steps} steps, {dir_impl} order, field={field}', flush=True)
     cfg = config(T=26, lo=1e3, hi=4e7, B=16384, steps=steps, C=337_626, n_static=337_626 - 16_384,
-                 dir_impl=dir_impl)
+                 dir_impl=dir_impl, field=field)
     cfg['log_cap'] = 2_000_000 + steps * 60_000
     cfg['mat_cap'] = 1_000_000 + steps * 12_000
     g = make(cfg, dev)
