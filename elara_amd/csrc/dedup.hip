@@ -411,8 +411,9 @@ __global__ __launch_bounds__(kSegBlock) void k_chunk_apply(const int64_t* __rest
 // occurrence order).  One block per field sorts its column of at most kFieldRows ids in LDS: LSD passes of at most
 // kFieldDigit bits over the id's offset in its field, each key ranked as in k_radix_scatter (ballots, a running
 // count per wave, a scan over the waves), the column re-read from LDS after each pass.  The plan is then the
-// general path's, bit for bit, in two launches (k_field_sort, then k_field_apply, which adds the earlier fields'
-// segment and chunk counts) instead of three per radix pass and four for the segments and chunks.  An id outside
+// general path's, bit for bit, in three launches (k_field_keys, the columns' keys; k_field_sort; k_field_apply, which
+// adds the earlier fields' segment and chunk counts) instead of three per radix pass and four for the segments and
+// chunks.  An id outside
 // its field's rows takes the key R_c (the field's row count), sorts after the field's ids and comes out as -1 in
 // uniq: a row out of range for the caller.
 constexpr int kFieldThreads = 1024;
@@ -475,8 +476,27 @@ __device__ __forceinline__ int field_head_positions(uint32_t hm, int wcount, int
   return U;
 }
 
-__global__ __launch_bounds__(kFieldThreads) void k_field_sort(const int64_t* __restrict__ ids, int64_t nrows, int nf,
-                                                              FieldBounds fb, uint32_t* __restrict__ skeys,
+// Each field's ids as offsets in its field (the key R_c for an id outside it), field after field: keys[c * nrows + j].
+// One block per field and kFieldKeyRows samples, so that the gather of a column (each wave's 64 loads touch 64
+// different cache lines) is spread over the whole GPU instead of being done by the field's sorting block alone.
+constexpr int kFieldKeyRows = 1024;
+__global__ __launch_bounds__(256) void k_field_keys(const int64_t* __restrict__ ids, int64_t nrows, int nf,
+                                                    FieldBounds fb, uint32_t* __restrict__ keys) {
+  const int c = blockIdx.y;
+  const int64_t lo = fb.lo[c], hi = fb.lo[c + 1];
+  const int64_t j0 = (int64_t)blockIdx.x * kFieldKeyRows;
+#pragma unroll
+  for (int r = 0; r < kFieldKeyRows / 256; ++r) {
+    const int64_t j = j0 + r * 256 + threadIdx.x;
+    if (j < nrows) {
+      const int64_t id = ids[j * nf + c];
+      keys[(int64_t)c * nrows + j] = id >= lo && id < hi ? (uint32_t)(id - lo) : (uint32_t)(hi - lo);
+    }
+  }
+}
+
+__global__ __launch_bounds__(kFieldThreads) void k_field_sort(const uint32_t* __restrict__ keys, int64_t nrows,
+                                                              int nf, FieldBounds fb, uint32_t* __restrict__ skeys,
                                                               int32_t* __restrict__ svals, int64_t* __restrict__ cnt,
                                                               int64_t* __restrict__ d_hot) {
   constexpr int NW = kFieldThreads / 64, WSPAN = kFieldItems * 64, BINS = 1 << kFieldDigit;
@@ -487,7 +507,7 @@ __global__ __launch_bounds__(kFieldThreads) void k_field_sort(const int64_t* __r
   __shared__ int wtot[NW];
   const int c = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const int n = (int)nrows;
-  const int64_t lo = fb.lo[c], hi = fb.lo[c + 1], R = hi - lo;
+  const int64_t R = fb.lo[c + 1] - fb.lo[c];
   int passes, rb;
   field_digits(R, passes, rb);
   const int nbins = 1 << rb;
@@ -497,12 +517,7 @@ __global__ __launch_bounds__(kFieldThreads) void k_field_sort(const int64_t* __r
 #pragma unroll
   for (int r = 0; r < kFieldItems; ++r) {
     const int j = w * WSPAN + r * 64 + lane;
-    uint32_t key = 0;
-    if (j < n) {
-      const int64_t id = ids[(int64_t)j * nf + c];
-      key = id >= lo && id < hi ? (uint32_t)(id - lo) : (uint32_t)R;
-    }
-    kk[r] = key;
+    kk[r] = j < n ? keys[(int64_t)c * nrows + j] : 0u;
   }
   for (int p = 0; p < passes; ++p) {
     const int shift = p * rb;
@@ -635,24 +650,27 @@ __global__ __launch_bounds__(kFieldThreads) void k_field_apply(const uint32_t* _
   int wcount;
   const uint32_t hm = field_heads(lk, n, wcount);
   const int U = field_head_positions(hm, wcount, n, wtot, hpos);
-  // every position's segment: the last head at or before it (a binary search of hpos, which the head positions'
-  // ballots would otherwise have to carry through the items)
-  for (int j = t; j < n; j += kFieldThreads) {
-    int a = 0, b = U - 1;   // hpos[a] <= j < hpos[b + 1]
-    while (a < b) {
-      const int m = (a + b + 1) >> 1;
-      if (hpos[m] <= j) a = m;
-      else b = m - 1;
+  // every position's segment: heads at or before it, less one (this wave's earlier heads from the head flags)
+  int run = 0;
+#pragma unroll
+  for (int q = 0; q < NW; ++q) run += q < w ? wtot[q] : 0;
+#pragma unroll
+  for (int r = 0; r < kFieldItems; ++r) {
+    const int j = w * WSPAN + r * 64 + lane;
+    const bool h = (hm >> r) & 1u;
+    const uint64_t bal = __ballot(h);
+    if (j < n) {
+      const int64_t gu = su + run + __popcll(bal & lanemask_lt()) + (h ? 0 : -1);
+      const int32_t o = svals[out0 + j];
+      if (h) {
+        const uint32_t k = lk[j];
+        uniq[gu] = (int64_t)k == R ? -1 : lo + (int64_t)k;
+        seg_start[gu] = out0 + j;
+        seg_occ0[gu] = o;
+      }
+      if (inverse) inverse[o] = gu;
     }
-    const int64_t gu = su + a;
-    const int32_t o = svals[out0 + j];
-    if (hpos[a] == j) {
-      const uint32_t k = lk[j];
-      uniq[gu] = (int64_t)k == R ? -1 : lo + (int64_t)k;
-      seg_start[gu] = out0 + j;
-      seg_occ0[gu] = o;
-    }
-    if (inverse) inverse[o] = gu;
+    run += __popcll(bal);
   }
   int64_t before = se;
   for (int u0 = 0; u0 < U; u0 += kFieldThreads) {
@@ -1402,8 +1420,10 @@ extern "C" int elr_dedup_plan_fields(const int64_t* ids, int64_t nrows, int64_t 
   for (int64_t c = 0; c <= nfields; ++c) fb.lo[c] = field_lo[c];
   hipStream_t st = (hipStream_t)stream;
   int32_t* sv = S.vals[plan_result_buffer(key_bits)];
-  k_field_sort<<<(unsigned)nfields, kFieldThreads, 0, st>>>(ids, nrows, (int)nfields, fb, (uint32_t*)S.keys[0], sv,
-                                                            S.hist, S.d_tot + 2);
+  k_field_keys<<<dim3((unsigned)cdiv(nrows, kFieldKeyRows), (unsigned)nfields), 256, 0, st>>>(
+      ids, nrows, (int)nfields, fb, (uint32_t*)S.keys[1]);
+  k_field_sort<<<(unsigned)nfields, kFieldThreads, 0, st>>>((const uint32_t*)S.keys[1], nrows, (int)nfields, fb,
+                                                            (uint32_t*)S.keys[0], sv, S.hist, S.d_tot + 2);
   k_field_apply<<<(unsigned)nfields, kFieldThreads, 0, st>>>((const uint32_t*)S.keys[0], sv, nrows, (int)nfields, fb,
                                                              S.hist, S.d_tot, n_unique, uniq, S.seg_start,
                                                              S.seg_occ0, inverse, S.chunk_off, S.chunk_seg,

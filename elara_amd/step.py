@@ -548,6 +548,12 @@ class ElaraStep:
             self._ctl_state[_lib.S_NFREE] = C - n0
             self._desc = torch.zeros(_lib.DESC_WORDS, dtype=I64, device=d)
             self._err_pin = torch.zeros(1, dtype=I64, pin_memory=True)
+        if d.type == 'cuda':
+            # the end of every run() reads the arenas' tops (check_capacity, through torch's stack kernel); reading
+            # them once here loads that kernel, whose first load in a process (10-20 ms) would otherwise fall at
+            # the end of the first run's steps
+            self._host(self.mat_top, self.log_top)
+            self._stats['syncs'] -= 1
 
     @property
     def stats(self):
