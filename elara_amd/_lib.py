@@ -190,7 +190,8 @@ class ExecOut(ctypes.Structure):
 class StepDevArgs(ctypes.Structure):
     """elr_step_dev_args: a whole device-driven step in one call."""
     _fields_ = [('plan', PlanIn), ('ctl', PlanCtl), ('grad', c_vp), ('n_occ', c_i64), ('key_bits', c_i64),
-                ('dplan', c_vp), ('dplan_bytes', c_i64), ('exec', ExecArgs)]
+                ('dplan', c_vp), ('dplan_bytes', c_i64), ('exec', ExecArgs), ('mark_rows', c_vp), ('mark_n', c_vp),
+                ('mark_nmax', c_i64), ('mark_value', c_i64), ('mark_bit', c_i64), ('mark_event', c_vp)]
 
 
 STEP_DEV_OUT_FIELDS = ('cls', 'flags', 'sl', 'c', 'order', 'rank', 'dyn_out', 'counts', 'u_ord', 'c_ord', 'sl_ord',

@@ -8,6 +8,36 @@
 
 namespace elr {
 
+// out[rows[i]] = value for i < min(*n_dev, n_max) (a device-side count, e.g. the unique rows of a batch whose count
+// the host has not read): the TTL lookahead's record of when rows appear next (srm2/elara.py:160-161).  With bits,
+// also bits[r] |= bit (the planner's ring of loaded batches): the rows of one batch are distinct, so no two threads
+// write the same word.  Rows out of range are skipped.  Grid-stride over the blocks it is given.
+struct MarkRows {
+  const int64_t* rows;
+  const int64_t* n_dev;
+  int64_t n_max;
+  int32_t value;
+  int32_t* out;
+  int64_t out_rows;
+  uint32_t* bits;
+  uint32_t bit;
+  __device__ __forceinline__ void operator()(int64_t block, int64_t nblocks) const {
+    const int64_t v = *n_dev, n = v < 0 ? 0 : (v < n_max ? v : n_max);
+    for (int64_t i = block * kFunctorBlock + threadIdx.x; i < n; i += nblocks * kFunctorBlock) {
+      const int64_t r = rows[i];
+      if (r >= 0 && r < out_rows) {
+        out[r] = value;
+        if (bits) bits[r] |= bit;
+      }
+    }
+  }
+};
+// Blocks of a MarkRows launch of at most n_max rows: one row per thread, at most 512 blocks.
+inline int64_t mark_rows_blocks(int64_t n_max) {
+  const int64_t b = (n_max + kFunctorBlock - 1) / kFunctorBlock;
+  return b < 512 ? b : 512;
+}
+
 // Row index maps: the row of item i, or -1 to skip the item.
 struct IxList {   // idx[i] (NULL: i)
   const int64_t* idx;

@@ -65,31 +65,12 @@ extern "C" int elr_glog_take(float* logs, int64_t nlogs, const int64_t* ids, con
   return copy_rows_launch(logs, nlogs, IxList{ids}, glog, nd * K, IxExpand{dyn, K, nd}, n * K, W, stream);
 }
 
-// out[rows[i]] = value for i < *n_dev (a device-side count, e.g. the unique rows of a batch whose count the host has
-// not read yet): the TTL lookahead's record of when rows appear next (srm2/elara.py:160-161), without a
-// synchronisation.  Rows out of range are skipped.
-// With bits, also bits[r] |= bit (the planner's ring of loaded batches): the rows of one call are distinct, so no
-// two threads write the same word.
-__global__ __launch_bounds__(256) void k_mark_rows(const int64_t* __restrict__ rows, const int64_t* __restrict__ n_dev,
-                                                   int64_t n_max, int32_t value, int32_t* __restrict__ out,
-                                                   int64_t out_rows, uint32_t* __restrict__ bits, uint32_t bit) {
-  const int64_t n = *n_dev < n_max ? *n_dev : n_max;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const int64_t r = rows[i];
-  if (r >= 0 && r < out_rows) {
-    out[r] = value;
-    if (bits) bits[r] |= bit;
-  }
-}
-
 extern "C" int elr_mark_rows(const int64_t* rows, const int64_t* n_dev, int64_t n_max, int32_t value, int32_t* out,
                              int64_t out_rows, uint32_t* bits, uint32_t bit, void* stream) {
   if (n_max < 0 || out_rows < 0) return ELR_EINVAL;
   if (n_max == 0) return ELR_OK;
   if (!rows || !n_dev || !out) return ELR_EINVAL;
-  const int64_t blocks = (n_max + 255) / 256;
-  if (blocks >= (int64_t(1) << 31)) return ELR_EINVAL;
-  k_mark_rows<<<(unsigned)blocks, 256, 0, (hipStream_t)stream>>>(rows, n_dev, n_max, value, out, out_rows, bits, bit);
+  elr::launch1(elr::MarkRows{rows, n_dev, n_max, value, out, out_rows, bits, bit}, elr::mark_rows_blocks(n_max),
+               (hipStream_t)stream);
   return elr::launch_status();
 }

@@ -365,9 +365,11 @@ extern "C" int64_t elr_step_exec_dev_bytes(const elr_exec_args* args) {
 }
 
 // The device-driven executor; with lsteps_done its first launch (call A's replay inputs and hit records) was issued
-// by the caller already (elr_step_dev runs it beside the segment sum's final kernel).
+// by the caller already (elr_step_dev runs it beside the segment sum's final kernel).  With mark, the lookahead's
+// mark of a batch loaded ahead runs in the compaction's launch, after the stream waits for mark_event (if any).
 static int step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, int64_t ws_bytes,
-                         elr_exec_out* out, void* stream, bool lsteps_done) {
+                         elr_exec_out* out, void* stream, bool lsteps_done, const elr::MarkRows* mark = nullptr,
+                         hipEvent_t mark_event = nullptr) {
   using namespace elr;
   if (!args || !out || !desc) return ELR_EINVAL;
   const elr_exec_args& a = *args;
@@ -484,7 +486,13 @@ static int step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* w
   const DirBItems it{a.u_ord, a.c_ord, n, ev_row, rel_cnt, nr, true};
   const DirBPlan bp = dir_b_plan(S, P, a.u_ord, a.c_ord, n, it, s, a_ids, c_slots, at(L.dir_b_scratch), desc);
   launch2(admit, admit_slots_blocks(sl, v.nadm), bp.count, bp.count_blocks, st);
-  launch1(bp.compact, bp.compact_blocks, st);
+  if (mark) {
+    // no kernel after this step's plan reads last_seen or next_bits, and the next step's plan comes after this
+    if (mark_event && hipStreamWaitEvent(st, mark_event, 0) != hipSuccess) return ELR_EINVAL;
+    launch2(bp.compact, bp.compact_blocks, *mark, mark_rows_blocks(mark->n_max), st);
+  } else {
+    launch1(bp.compact, bp.compact_blocks, st);
+  }
   // 7. the admitted, compacted, transient, appended and S rows
   exec_visit(vpl, D, tx, tblocks, scal, [&](const auto& f, int64_t nb) { launch1(f, nb, st); });
   return launch_status();
@@ -555,6 +563,9 @@ extern "C" int elr_step_dev(const elr_step_dev_args* args, void* ws, int64_t ws_
                             void* stream) {
   if (!args || !out) return ELR_EINVAL;
   const elr_step_dev_args& a = *args;
+  if (a.mark_rows && (!a.mark_n || !a.plan.last_seen || a.mark_nmax < 0 || a.mark_value < INT32_MIN ||
+                      a.mark_value > INT32_MAX || a.mark_bit < 0 || a.mark_bit > (int64_t)UINT32_MAX))
+    return ELR_EINVAL;
   StepDevLayout L;
   if (!step_dev_layout(a, L)) return ELR_EINVAL;
   if (!ws || ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255)) return ELR_ECAPACITY;
@@ -611,7 +622,10 @@ extern "C" int elr_step_dev(const elr_step_dev_args* args, void* ws, int64_t ws_
       (rc = elr_segment_sum_plan_final(a.grad, a.n_occ, D, (int)a.key_bits, a.dplan, a.dplan_bytes, po.rank, G, n,
                                        stream)))
     return rc;
-  if ((rc = step_exec_dev(&e, a.ctl.desc, w + L.o.exec_ws, L.exec_bytes, &L.o.exec, stream, lsteps_done)))
+  elr::MarkRows mark{a.mark_rows, a.mark_n, a.mark_nmax, (int32_t)a.mark_value, const_cast<int32_t*>(a.plan.last_seen),
+                     a.plan.R, a.plan.next_bits, (uint32_t)a.mark_bit};
+  if ((rc = step_exec_dev(&e, a.ctl.desc, w + L.o.exec_ws, L.exec_bytes, &L.o.exec, stream, lsteps_done,
+                          a.mark_rows ? &mark : nullptr, (hipEvent_t)a.mark_event)))
     return rc;
   *out = L.o;
   return ELR_OK;

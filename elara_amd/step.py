@@ -191,11 +191,13 @@ class HipBackend:
         _lib.check(rc, 'elr_step_exec')
         return ws, off
 
-    def step_dev(self, es, s, u, n_dev, g_occ, dplan):
+    def step_dev(self, es, s, u, n_dev, g_occ, dplan, mark=None):
         """A whole device-driven step in one native call (elr_step_dev): the plan that resolves the step on the GPU,
         the segment sum in its class order and the rest of the step, every count read on the GPU.  The call's
         arguments are built once per ElaraStep and the workspace kept from step to step, so a step costs the host a
-        few field updates and one call.  Returns (workspace, offsets, sequence number)."""
+        few field updates and one call.  mark: (rows, count on the device, logical step, bit, event or None), the
+        lookahead's mark of a batch loaded ahead, done in the step's compaction launch after the stream waits for
+        the event.  Returns (workspace, offsets, sequence number)."""
         st = self._dev.get(id(es))
         if st is None or st['es'] is not es:
             st = self._dev[id(es)] = self._dev_setup(es)
@@ -214,6 +216,17 @@ class HipBackend:
         a.grad = g_occ.data_ptr() if n_occ else None
         a.n_occ, a.key_bits = n_occ, dplan.key_bits
         a.dplan, a.dplan_bytes = (dplan.buf.data_ptr(), dplan.nbytes) if n_occ else (None, 0)
+        if mark is None:
+            a.mark_rows, a.mark_n, a.mark_nmax, a.mark_value, a.mark_bit, a.mark_event = None, None, 0, 0, 0, None
+        else:
+            mu, mn, mval, mbit, mev = mark
+            if not (mu.dtype == torch.int64 and mu.is_contiguous() and mu.device == dev and mn.dtype == torch.int64
+                    and mn.device == dev and mn.numel() == 1):
+                raise RuntimeError(f'step_dev: the marked rows must be a contiguous int64 tensor with an int64 [1] '
+                                   f'count on {dev}')
+            a.mark_rows, a.mark_n, a.mark_nmax = mu.data_ptr(), mn.data_ptr(), mu.numel()
+            a.mark_value, a.mark_bit = int(mval), int(mbit)
+            a.mark_event = mev.cuda_event if mev is not None else None
         L = _lib.lib()
         nb = int(L.elr_step_dev_bytes(ctypes.byref(a)))
         _lib.check(min(nb, 0), 'elr_step_dev_bytes')
@@ -529,6 +542,10 @@ class ElaraStep:
         self.dedup_ahead = True   # run() sorts the batches loaded ahead on a second stream (dedup_stream)
         self._side = None
         self._plan_pool = None   # run()'s reusable dedup-plan buffers (PlanPool), made on first use
+        # run(), device-driven with the dedup on a second stream: each batch loaded ahead is marked (the lookahead) in
+        # the launch of the previous step's directory compaction instead of a launch of its own between the steps
+        self.fold_mark = True
+        self._pending_mark = None
         if self.static_rows is not None:   # srm2/elara.py:434-440 load_static: pinned rows' state lives in the pool
             self.pool[:n0] = self.be.init_rows(self.static_rows)
             self.code[self.static_rows] = self.MAT
@@ -669,6 +686,17 @@ class ElaraStep:
             self.be.mark_rows(u, n_dev, step, self.last_seen, self.next_bits, bit)
         else:
             self.be.mark_rows(u, n_dev, step, self.last_seen)
+
+    def observe_in_next_step(self, step, u, n_dev, event=None):
+        """observe(step, u, n_dev) done by the next device-driven step's native call, in the launch of its directory
+        compaction -- after that step's plan has read the lookahead and before the following step's plan -- once the
+        stream has waited for `event` (recorded after u's dedup plan on another stream)."""
+        if not self.sync_free or self.next_bits is None:
+            raise RuntimeError('observe_in_next_step needs the device-driven step')
+        if self._pending_mark is not None:
+            raise RuntimeError('a batch is already waiting to be marked by the next step')
+        self._observed = max(self._observed, int(step))
+        self._pending_mark = (u, n_dev, int(step), 1 << (step % 32), event)
 
     def defer_count(self, t, cb):
         """Read the device int64 scalar t at the next host synchronisation and pass it to cb."""
@@ -944,7 +972,8 @@ class ElaraStep:
         self._poll_errors()
         p = Plan()
         p.s, p.u, p.evl, p._es = s, u, self.evl, self
-        p._ws, p._doff, p._seq = self.be.step_dev(self, s, u, n_dev, g_occ.contiguous(), dplan)
+        mark, self._pending_mark = self._pending_mark, None
+        p._ws, p._doff, p._seq = self.be.step_dev(self, s, u, n_dev, g_occ.contiguous(), dplan, mark)
         p.done = True
         return p
 
@@ -1247,18 +1276,22 @@ def _run(step, batches, grads, steps, on_step):
                     t.record_stream(main)
         AHEAD[j] = (u, dplan, nu, ev)
 
-    def observe(j):
+    def observe(j, in_next_step=False):
         """Mark batch j's rows (the lookahead) on the main stream, its unique count read at the next host
-        synchronisation (the plan's)."""
+        synchronisation (the plan's).  in_next_step (device-driven, sorted on the side stream): marked by the next
+        step's native call instead, which waits for the sort there."""
         u, dplan, nu, ev = AHEAD.pop(j)
-        if ev is not None:
+        if ev is not None and not in_next_step:
             torch.cuda.current_stream(dev).wait_event(ev)
         PLANS[j] = dplan
         if step.sync_free:   # the device-driven step takes the rows with their count on the device, never read here
             if nu is None:   # an empty batch
                 u, nu = torch.zeros(1, dtype=torch.int64, device=dev), torch.zeros(1, dtype=torch.int64, device=dev)
             U[j] = (u, nu)
-            step.observe(j + 1, u, nu)
+            if in_next_step:
+                step.observe_in_next_step(j + 1, u, nu, ev)
+            else:
+                step.observe(j + 1, u, nu)
             return
         if nu is None:
             U[j] = u
@@ -1271,19 +1304,28 @@ def _run(step, batches, grads, steps, on_step):
         step.observe(j + 1, u, nu)
         step.defer_count(nu, resolve)
 
+    # device-driven with the sorts on the side stream: batch s + L + 2, sorted just before step s is issued, is marked
+    # by step s itself (after its plan, as observe() before step s + 1 would)
+    fold = bool(step.sync_free and side is not None and getattr(step, 'fold_mark', False))
+    if fold:
+        step._pending_mark = None
     try:
         for j in range(min(S, step.L + 1)):
             dedup(j)
             observe(j)
         if step.L + 1 < S:
             dedup(step.L + 1)
+            if fold:
+                observe(step.L + 1)
         if not step.sync_free:
             step.flush_deferred()
         for s in range(S):
-            if s + step.L + 1 < S:
+            if s + step.L + 1 < S and not fold:
                 observe(s + step.L + 1)
             if s + step.L + 2 < S:
                 dedup(s + step.L + 2)
+                if fold:
+                    observe(s + step.L + 2, in_next_step=True)
             u_nexts = [] if step.sync_free else [U[s + k] for k in range(1, step.depth) if s + k < S]
             g = grads(s) if callable(grads) else grads[s]
             p = step.step(s + 1, batches[s].to(dev), g.to(dev), U.pop(s), PLANS.pop(s), u_nexts)

@@ -647,6 +647,12 @@ int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, 
  *   grad [n_occ, D], key_bits, dplan, dplan_bytes: the batch's occurrence gradients and dedup plan (elr_dedup_plan).
  *   exec:  as for elr_step_exec_dev; its class-ordered arrays and slot lists are taken from the plan's outputs in
  *          ws, exec.b[ELR_NRANK] from plan.n and exec.upd.grad from the segment sum in ws.
+ *   mark_*: optional (mark_rows NULL: none): the TTL lookahead's mark of a batch loaded ahead, elr_mark_rows(
+ *          mark_rows, mark_n, mark_nmax, mark_value, plan.last_seen, plan.R, plan.next_bits, mark_bit), done in one
+ *          launch with the directory's compaction -- after this step's plan has read last_seen and next_bits and
+ *          before the next step's -- once the stream has waited for mark_event (a hipEvent_t recorded after the
+ *          batch's dedup plan on another stream, or NULL).  The mark does not depend on this step's results and
+ *          happens also when the step itself does nothing (an error).
  * out receives the byte offsets in ws of the plan's outputs (elr_plan_out order), of the per-row gradients G and
  * of the executor's outputs; they hold this step's values until the next call. */
 typedef struct elr_step_dev_args {
@@ -658,6 +664,12 @@ typedef struct elr_step_dev_args {
   const void* dplan;
   int64_t dplan_bytes;
   elr_exec_args exec;
+  const int64_t* mark_rows;
+  const int64_t* mark_n;
+  int64_t mark_nmax;
+  int64_t mark_value;
+  int64_t mark_bit;
+  void* mark_event;
 } elr_step_dev_args;
 typedef struct elr_step_dev_out {
   int64_t cls, flags, sl, c, order, rank, dyn_out, counts, u_ord, c_ord, sl_ord, L_row, L_cnt, loc_ord;

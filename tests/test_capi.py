@@ -57,6 +57,17 @@ def test_step_exec_checks_and_workspace_size():
     a.b[3] = 9
     assert L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(256), 10, ctypes.byref(o), None) == -3    # too small
     assert L.elr_step_exec(ctypes.byref(a), ctypes.c_void_p(272), 1 << 30, ctypes.byref(o), None) == -3  # unaligned
+    # the device-driven step's optional lookahead mark: its count, last_seen and a 32-bit bit are checked first
+    d, do = _lib.StepDevArgs(), _lib.StepDevOut()
+    d.mark_rows, d.mark_n, d.mark_nmax, d.mark_bit = 256, None, 10, 1 << 3
+    d.plan.last_seen = 256
+    assert L.elr_step_dev(ctypes.byref(d), ctypes.c_void_p(256), 1 << 30, ctypes.byref(do), None) == -1  # no count
+    d.mark_n, d.mark_bit = 256, 1 << 32
+    assert L.elr_step_dev(ctypes.byref(d), ctypes.c_void_p(256), 1 << 30, ctypes.byref(do), None) == -1  # bit > 32b
+    d.mark_bit, d.mark_value = 1 << 3, 1 << 31
+    assert L.elr_step_dev(ctypes.byref(d), ctypes.c_void_p(256), 1 << 30, ctypes.byref(do), None) == -1  # value
+    d.mark_value, d.plan.last_seen = 5, None
+    assert L.elr_step_dev(ctypes.byref(d), ctypes.c_void_p(256), 1 << 30, ctypes.byref(do), None) == -1  # last_seen
 
 
 def test_triton_order_argument_checks():

@@ -299,15 +299,18 @@ def test_gpu_step_degenerate_batches(dev, name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize('sync_free,ahead,field', [(True, True, False), (False, True, False), (True, False, False),
-                                                   (True, True, True), (False, True, True)])
-def test_gpu_step_ragged_batches(dev, sync_free, ahead, field):
+@pytest.mark.parametrize('sync_free,ahead,field,fold', [(True, True, False, True), (False, True, False, True),
+                                                        (True, False, False, True), (True, True, True, True),
+                                                        (False, True, True, True), (True, True, False, False)])
+def test_gpu_step_ragged_batches(dev, sync_free, ahead, field, fold):
     """Batches of changing sizes (a later batch larger than any before it, then smaller ones): run() takes each
     batch's dedup-plan buffers from its pool, and a batch that outgrows every free entry gets new ones.  Device-
-    driven and host-planned, with the sorts on a second stream or on the step's own, and sorted per table (the
-    smallest batches, of at most 3,072 ids, then take the general sort).  Equal to the oracle-driven step."""
+    driven and host-planned, with the sorts on a second stream or on the step's own, sorted per table (the smallest
+    batches, of at most 3,072 ids, then take the general sort), and device-driven with each batch loaded ahead
+    marked by the step before (the default) or by a launch of its own.  Equal to the oracle-driven step."""
     from elara_amd.step import run
-    print(f'[gpu-test] elara step ragged batches sync_free={sync_free} ahead={ahead} field={field}', flush=True)
+    print(f'[gpu-test] elara step ragged batches sync_free={sync_free} ahead={ahead} field={field} fold={fold}',
+          flush=True)
     sizes = [300, 100, 800, 200, 1600, 50, 1200, 400, 2400, 150, 700, 1000, 90, 3000, 500, 250]
     tabs = synth.C5Tables(T=6, lo=200, hi=20000, alpha=1.1, seed=5)
     rng = np.random.default_rng(12)
@@ -318,6 +321,7 @@ def test_gpu_step_ragged_batches(dev, sync_free, ahead, field):
                log_cap=O + 16, mat_cap=min(tabs.R + 1, O + 16), batches=batches, sync_free=sync_free, field=field)
     g = make(cfg, dev)
     g.dedup_ahead = ahead
+    g.fold_mark = fold
     c = make(cfg, 'cpu', OracleBackend(cfg['D'], 42, cfg['bound'], HP, cfg['steps'] + 2))
     gf = grads_fn(cfg, None)
     run(g, cfg['batches'], gf)
