@@ -949,6 +949,38 @@ def mode_link(args):
                     'the two directions at once on two streams'}
 
 
+def mode_c5plan(args):
+    """The dedup plan of one C5 batch alone (16,384 x 26 ids of 26 tables, D = 128), back to back on one stream:
+    the general radix sort (elr_dedup_plan) against the per-table sort (elr_dedup_plan_fields), --steps plans each
+    after 20 untimed ones, HIP events around the whole sequence (the plan's launches only; no host wait between
+    plans)."""
+    import torch
+    from elara_amd import synth
+    from elara_amd.dedup import field_bounds, plan_bytes, unique_plan_async
+    dev = torch.device('cuda:0')
+    tabs = synth.C5Tables(T=26, lo=1e3, hi=4e7, alpha=1.1, seed=0)
+    rng = np.random.default_rng(7)
+    bs = [torch.from_numpy(tabs.batch(rng, 16_384)).to(dev) for _ in range(8)]
+    fb = field_bounds(np.append(tabs.toff, tabs.R))
+    n = bs[0].numel()
+    out = (torch.empty(plan_bytes(n, 128), dtype=torch.uint8, device=dev),
+           torch.empty(n, dtype=torch.int64, device=dev), torch.empty(1, dtype=torch.int64, device=dev))
+    res = {'mode': 'c5plan', 'unit': 'us per plan', 'ids_per_plan': n, 'plans': args.steps}
+    for name, kw in (('general', {}), ('per_table', {'fields': fb})):
+        for i in range(20):
+            unique_plan_async(bs[i % 8], 128, tabs.R, out=out, **kw)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            unique_plan_async(bs[i % 8], 128, tabs.R, out=out, **kw)
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / args.steps * 1e3
+        res[name + '_unique'] = int(out[2])
+    return res
+
+
 def copy_calibration(args):
     """A plain device copy of known size: the PMC calibration of FETCH_SIZE / WRITE_SIZE, and the copy bandwidth
     (read + write bytes over the mean launch time, HIP events) as the practical ceiling of a streaming kernel."""
@@ -1020,7 +1052,8 @@ def main():
     ap.add_argument('--steps', type=int, default=200)
     ap.add_argument('--warmup', type=int, default=200)
     ap.add_argument('--mode', default='headline',
-                    choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'rows', 'hostsync', 'link', 'all'])
+                    choices=['headline', 'copy', 'c1', 'c3', 'c4', 'c5', 'c5plan', 'rows', 'hostsync', 'link',
+                             'all'])
     ap.add_argument('--rows-order', default='random', choices=['random', 'consecutive'],
                     help='--mode rows: the order of the updated rows')
     ap.add_argument('--steps-c3', type=int, default=100)
@@ -1048,7 +1081,7 @@ def main():
               'an all-to-all of occurrence gradients; not implemented); run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     fns = {'headline': headline, 'copy': copy_calibration, 'c1': mode_c1, 'c3': mode_c3, 'c4': mode_c4,
-           'c5': mode_c5, 'rows': mode_rows, 'hostsync': host_sync_costs, 'link': mode_link}
+           'c5': mode_c5, 'c5plan': mode_c5plan, 'rows': mode_rows, 'hostsync': host_sync_costs, 'link': mode_link}
     for m in (['headline', 'c1', 'c3', 'c4', 'c5'] if args.mode == 'all' else [args.mode]):
         res = fns[m](args)
         print(json.dumps(res, default=float), flush=True)
