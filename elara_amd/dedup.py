@@ -120,7 +120,7 @@ def unique_plan_async(ids, D, bound=None, nu_out=None, out=None, fields=None):
     bytes, int64 u of at least n elements, int64 nu [1] (nu_out, if given, takes its place); the caller keeps them
     from being reused before the GPU's work on the plan is done.
     fields (optional, field_bounds(...)): the batch is laid out by field -- (sample, field) order, field c's ids in
-    [fields[c], fields[c + 1]) -- and is sorted per field (elr_dedup_plan_fields): the same plan, in two launches.
+    [fields[c], fields[c + 1]) -- and is sorted per field (elr_dedup_plan_fields): the same plan, in three launches.
     An id outside its field's rows comes out as -1 in u.  Batches whose size is not a multiple of the field count
     take the general sort."""
     flat = _ids(ids)

@@ -418,7 +418,7 @@ class ElaraStep:
     the other states are the same under all three.  field_layout: every batch that run() loads is laid out by table,
     as the reference's one-hot batches are (srm2/train.py:187-214): (sample, table) order, with table t's column
     holding rows [toff[t], toff[t + 1]) (toff[T] = R); its dedup plan then sorts each table's column on its own
-    (dedup.unique_plan_async(fields=...)), the same plan in two launches.  A row outside its table's range is then
+    (dedup.unique_plan_async(fields=...)), the same plan in three launches.  A row outside its table's range is then
     reported as a row outside [0, R).
     """
 

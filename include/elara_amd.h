@@ -267,7 +267,7 @@ int elr_dedup_plan(const int64_t* ids, int64_t n, int key_bits, int64_t* uniq, i
  * global id = local id + the field's table offset, flattened in (sample, field) order): ids [nrows * nfields],
  * field c of sample i at ids[i * nfields + c], and field c's ids in [field_lo[c], field_lo[c + 1]) (field_lo: host
  * array of nfields + 1 ascending bounds, field_lo[0] >= 0).  The whole batch sorted is then each field's column
- * sorted, one after the other, and one block per field sorts its column in LDS: two launches in place of
+ * sorted, one after the other, and one block per field sorts its column in LDS: three launches in place of
  * elr_dedup_plan's three per radix pass and four more.  The plan, uniq, inverse and n_unique are bitwise
  * elr_dedup_plan's (the order of the hot-segment list aside, which no result depends on).  An id outside its
  * field's rows breaks that contract: it comes out as -1 in uniq, a row out of range for the caller.  Shapes the
