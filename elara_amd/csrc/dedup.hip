@@ -1412,7 +1412,7 @@ extern "C" int elr_dedup_plan_fields(const int64_t* ids, int64_t nrows, int64_t 
   for (int64_t c = 0; c < nfields; ++c)
     if (field_lo[c + 1] - field_lo[c] > kFieldSpanMax)
       return elr_dedup_plan(ids, n, key_bits, uniq, inverse, n_unique, plan, plan_bytes, D, stream);
-  if (!ids || !uniq || !plan) return ELR_EINVAL;
+  if (!ids || !uniq || !n_unique || !plan) return ELR_EINVAL;
   DedupScratch S;
   if (plan_bytes < dedup_scratch_bytes(n, D, &S, plan)) return ELR_ECAPACITY;
   static_assert(2 * kFieldMax <= kRadixMaxBins, "the per-field counts fit in the first histogram's space");

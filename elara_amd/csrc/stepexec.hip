@@ -486,15 +486,14 @@ static int step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* w
   const DirBItems it{a.u_ord, a.c_ord, n, ev_row, rel_cnt, nr, true};
   const DirBPlan bp = dir_b_plan(S, P, a.u_ord, a.c_ord, n, it, s, a_ids, c_slots, at(L.dir_b_scratch), desc);
   launch2(admit, admit_slots_blocks(sl, v.nadm), bp.count, bp.count_blocks, st);
-  if (mark) {
-    // no kernel after this step's plan reads last_seen or next_bits, and the next step's plan comes after this
-    if (mark_event && hipStreamWaitEvent(st, mark_event, 0) != hipSuccess) return ELR_EINVAL;
-    launch2(bp.compact, bp.compact_blocks, *mark, mark_rows_blocks(mark->n_max), st);
-  } else {
-    launch1(bp.compact, bp.compact_blocks, st);
-  }
+  // no kernel after this step's plan reads last_seen or next_bits, and the next step's plan comes after this; if the
+  // wait for the batch's sort cannot be queued, the step is still issued whole and the error returned at its end
+  const bool waited = mark && (!mark_event || hipStreamWaitEvent(st, mark_event, 0) == hipSuccess);
+  if (waited) launch2(bp.compact, bp.compact_blocks, *mark, mark_rows_blocks(mark->n_max), st);
+  else launch1(bp.compact, bp.compact_blocks, st);
   // 7. the admitted, compacted, transient, appended and S rows
   exec_visit(vpl, D, tx, tblocks, scal, [&](const auto& f, int64_t nb) { launch1(f, nb, st); });
+  if (mark && !waited) return ELR_EINVAL;
   return launch_status();
 }
 

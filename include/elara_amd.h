@@ -652,7 +652,8 @@ int elr_step_exec_dev(const elr_exec_args* args, const int64_t* desc, void* ws, 
  *          launch with the directory's compaction -- after this step's plan has read last_seen and next_bits and
  *          before the next step's -- once the stream has waited for mark_event (a hipEvent_t recorded after the
  *          batch's dedup plan on another stream, or NULL).  The mark does not depend on this step's results and
- *          happens also when the step itself does nothing (an error).
+ *          happens also when the step itself does nothing (an error).  If the wait cannot be queued, the step is
+ *          issued without the mark and the call returns ELR_EINVAL.
  * out receives the byte offsets in ws of the plan's outputs (elr_plan_out order), of the per-row gradients G and
  * of the executor's outputs; they hold this step's values until the next call. */
 typedef struct elr_step_dev_args {

@@ -263,6 +263,7 @@ def test_planner_executor_dedup_argument_checks():
     assert F(fake, 2000, 3, (ctypes.c_int64 * 4)(-1, 100, 200, 300), 20, fake, None, fake, fake, 1 << 30, 8,
              None) == -1                                                                             # negative
     assert F(fake, 2000, 3, lo, 20, fake, None, fake, fake, 1, 8, None) == -3                       # plan too small
+    assert F(fake, 2000, 3, lo, 20, fake, None, None, fake, 1 << 30, 8, None) == -1                # no count
     assert F(fake, 100, 3, lo, 20, fake, None, fake, fake, 1, 8, None) == -3     # general sort: same checks
     from elara_amd.dedup import field_bounds
     assert field_bounds([0, 5, 5, 9]).dtype == np.int64
